@@ -1,0 +1,566 @@
+// Chord attention (causal softmax with the gated geometric-decay bias) for gfx950.
+//
+// chord_fwd_kernel (prefill): flash-style online softmax on bf16 MFMA
+// (v_mfma_f32_32x32x16_bf16, fp32 accumulation).  A workgroup is 4 waves that
+// share one kv head: with GQA the waves take different query heads of the same
+// 32-row query block, otherwise consecutive query blocks of one head.  Scores
+// are computed transposed, S^T = K Q^T, so each lane owns one query row and the
+// row max / row sum stay in registers (one cross-half exchange); the output is
+// accumulated transposed too, O^T += V^T P^T, which lets P feed the second
+// MFMA straight from registers (keys of a 16-key step are permuted to match
+// the accumulator layout, and V^T is read from LDS in the same permutation).
+// K tiles are staged row-major and V tiles transposed in LDS, double-buffered,
+// one barrier per 64-key tile.  The GGD bias depends only on d = key - i_abs,
+// so each wave evaluates it once per tile for the 95 distinct distances of its
+// 32x64 tile into an LDS vector instead of once per score.
+//
+// chord_decode_kernel (decode / short queries over a long cache): split-K
+// flash-decoding.  A workgroup owns (split, kv head, batch row) and serves all
+// query rows of that kv head (GQA group x L <= 8), streaming K and V with fully
+// coalesced 16-byte loads (8 lanes per key row); dot products are finished
+// with 3 xor-shuffles.  Partials (m, l, acc) are merged across the 4 waves in
+// LDS and across splits by chord_merge_kernel.
+#include <algorithm>
+
+#include "capi_internal.h"
+#include "common.h"
+
+namespace motif {
+
+struct ChordArgs {
+  const bf16_t *q; int64_t q_sb, q_sh, q_st;
+  const bf16_t *k; int64_t k_sb, k_sh, k_st;
+  const bf16_t *v; int64_t v_sb, v_sh, v_st;
+  const float *alpha, *beta, *mu, *ssmax;
+  const float *log_n; int64_t ln_sb, ln_st;
+  bf16_t *out; int64_t o_sb, o_sh, o_st;
+  float *lse;
+  int B, H, Hkv, L, S, q_start;
+  float scale, eps;
+  const int32_t *cu;  // packed sequences (B == 1) or nullptr
+  // split-K partials
+  float *part;        // [B][Hkv][splits][R][D + 2]
+  int splits, rows;   // rows = group * L (decode kernel)
+};
+
+constexpr int kD = 64;        // head dim
+constexpr int kBN = 64;       // keys per tile
+constexpr int kKStride = 72;  // sK row stride (bf16): 144 B keeps 16 B reads conflict-free
+constexpr int kVStride = 68;  // sVt row stride (bf16): 136 B keeps 8 B reads conflict-free
+
+__device__ __forceinline__ float ggd_bias(float dist, float alpha, float beta, float mu, float eps) {
+  // -alpha * (|d - mu| + eps)^beta, the power through exp2(beta * log2(.)).
+  const float x = fabsf(dist - mu) + eps;
+  return -alpha * fast_exp2(beta * fast_log2(x));
+}
+
+__device__ __forceinline__ __bf16 to_bf(float f) {
+  const bf16_t b = f32_to_bf16(f);
+  return __builtin_bit_cast(__bf16, b);
+}
+
+// ------------------------------------------------------------------ prefill
+template <int HPW>  // query heads per workgroup (the rest of the 4 waves take query blocks)
+__global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
+  constexpr int QBPW = 4 / HPW;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int hl = lane & 31, hh = lane >> 5;
+  const int group = a.H / a.Hkv;
+  const int hg = blockIdx.y, sq = blockIdx.z;
+
+  // Sequence geometry (padded batch row, or one packed sequence).
+  int batch, tok0, Lq, Skv, q_start;
+  if (a.cu == nullptr) {
+    batch = sq; tok0 = 0; Lq = a.L; Skv = a.S; q_start = a.q_start;
+  } else {
+    batch = 0; tok0 = a.cu[sq]; Lq = a.cu[sq + 1] - tok0; Skv = Lq; q_start = 0;
+  }
+  const int nqbg = (Lq + 32 * QBPW - 1) / (32 * QBPW);
+  if (static_cast<int>(blockIdx.x) >= nqbg) return;
+  const int qbg = nqbg - 1 - blockIdx.x;  // heaviest (latest) query blocks first
+
+  const int head = hg * HPW + (w % HPW);
+  const int kvh = (hg * HPW) / group;
+  const int q0 = (qbg * QBPW + w / HPW) * 32;
+  const int my_q = q0 + hl;
+  const bool q_valid = my_q < Lq;
+  const int q_abs = q_start + my_q;
+
+  const int wg_q_last = min(Lq, (qbg + 1) * QBPW * 32) - 1;
+  const int kv_end = min(Skv, q_start + wg_q_last + 1);
+  const int ntiles = (kv_end + kBN - 1) / kBN;
+  const int wave_first_qabs = q_start + q0;
+  const int wave_kv_end = min(Skv, q_start + min(Lq, q0 + 32));
+
+  const bf16_t *qp = a.q + batch * a.q_sb + head * a.q_sh + int64_t(tok0) * a.q_st;
+  const bf16_t *kp = a.k + batch * a.k_sb + kvh * a.k_sh + int64_t(tok0) * a.k_st;
+  const bf16_t *vp = a.v + batch * a.v_sb + kvh * a.v_sh + int64_t(tok0) * a.v_st;
+
+  __shared__ __attribute__((aligned(16))) bf16_t sK[2][kBN][kKStride];
+  __shared__ __attribute__((aligned(16))) bf16_t sVt[2][kD][kVStride];
+  __shared__ float sBias[4][96];
+
+  // Q^T as the B operand: lane holds Q[my_q][16 ks + 8 hh .. +8].
+  bf16x8 qreg[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    if (q_valid) qreg[ks] = *reinterpret_cast<const bf16x8 *>(qp + int64_t(my_q) * a.q_st + ks * 16 + hh * 8);
+    else qreg[ks] = bf16x8{};
+  }
+  const float alpha_h = a.alpha[head], beta_h = a.beta[head], mu_h = a.mu[head];
+  const float mul = q_valid ? a.ssmax[head] * a.log_n[batch * a.ln_sb + int64_t(tok0 + my_q) * a.ln_st] : 0.f;
+  const float c_qk = mul * a.scale * kLog2e;
+  const float c_b = mul * kLog2e;
+
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x16 oacc[2];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) oacc[mt][j] = 0.f;
+
+  // Tile staging: K rows (2 x 16 B per thread), V transposed (2 keys x 8 d per thread).
+  uint4 kst[2], vst[2];
+  auto load_tile = [&](int t) {
+    const int n0 = t * kBN;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int c = tid + 256 * r;
+      const int key = n0 + (c >> 3), dc = (c & 7) * 8;
+      kst[r] = key < kv_end ? *reinterpret_cast<const uint4 *>(kp + int64_t(key) * a.k_st + dc) : uint4{0, 0, 0, 0};
+    }
+    const int key0 = n0 + 2 * (tid >> 3), dc = (tid & 7) * 8;
+    vst[0] = key0 < kv_end ? *reinterpret_cast<const uint4 *>(vp + int64_t(key0) * a.v_st + dc) : uint4{0, 0, 0, 0};
+    vst[1] = key0 + 1 < kv_end ? *reinterpret_cast<const uint4 *>(vp + int64_t(key0 + 1) * a.v_st + dc) : uint4{0, 0, 0, 0};
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int c = tid + 256 * r;
+      *reinterpret_cast<uint4 *>(&sK[buf][c >> 3][(c & 7) * 8]) = kst[r];
+    }
+    const int kk = 2 * (tid >> 3), dc = (tid & 7) * 8;
+    const uint32_t *v0 = reinterpret_cast<const uint32_t *>(&vst[0]);
+    const uint32_t *v1 = reinterpret_cast<const uint32_t *>(&vst[1]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lo = (v0[i] & 0xffffu) | (v1[i] << 16);      // d = dc + 2i
+      const uint32_t hi = (v0[i] >> 16) | (v1[i] & 0xffff0000u);  // d = dc + 2i + 1
+      *reinterpret_cast<uint32_t *>(&sVt[buf][dc + 2 * i][kk]) = lo;
+      *reinterpret_cast<uint32_t *>(&sVt[buf][dc + 2 * i + 1][kk]) = hi;
+    }
+  };
+
+  if (ntiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    const int n0 = t * kBN;
+    if (t + 1 < ntiles) load_tile(t + 1);
+
+    if (n0 < wave_kv_end) {
+      // Bias vector for distances n0 - (wave_first_qabs + 31) + e, e in [0, 95).
+      for (int e = lane; e < 95; e += 64)
+        sBias[w][e] = ggd_bias(static_cast<float>(n0 - wave_first_qabs - 31 + e), alpha_h, beta_h, mu_h, a.eps);
+
+      f32x16 sacc[2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) sacc[kt][j] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const bf16x8 kreg = *reinterpret_cast<const bf16x8 *>(&sK[buf][kt * 32 + hl][ks * 16 + hh * 8]);
+          sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kreg, qreg[ks], sacc[kt], 0, 0, 0);
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+
+      const bool need_mask = (n0 + kBN - 1 > wave_first_qabs) || (n0 + kBN > Skv);
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int koff = kt * 32 + 8 * (j >> 2) + 4 * hh + (j & 3);  // key - n0
+          const float bias = sBias[w][koff + 31 - hl];
+          float s = fmaf(sacc[kt][j], c_qk, c_b * bias);
+          if (need_mask && (n0 + koff > q_abs || n0 + koff >= Skv)) s = -INFINITY;
+          sacc[kt][j] = s;
+          mx = fmaxf(mx, s);
+        }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run, mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float resc = fast_exp2(m_run - m_use);
+      float rsum = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float p = fast_exp2(sacc[kt][j] - m_use);
+          sacc[kt][j] = p;
+          rsum += p;
+        }
+      rsum += __shfl_xor(rsum, 32, 64);
+      l_run = l_run * resc + rsum;
+      m_run = m_new;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) oacc[mt][j] *= resc;
+
+      // O^T += V^T P^T over 4 steps of 16 keys.
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          bf16x8 pb;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) pb[i] = to_bf(sacc[kt][8 * s + i]);
+          const int kb = kt * 32 + 16 * s + 4 * hh;
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt) {
+            const bf16_t *row = &sVt[buf][mt * 32 + hl][0];
+            const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(row + kb);
+            const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(row + kb + 8);
+            const bf16x8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            oacc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, oacc[mt], 0, 0, 0);
+          }
+        }
+      }
+    }
+
+    if (t + 1 < ntiles) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (q_valid) {
+    const float inv = 1.f / fmaxf(l_run, 1e-20f);
+    bf16_t *op = a.out + batch * a.o_sb + head * a.o_sh + int64_t(tok0 + my_q) * a.o_st;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d = mt * 32 + 8 * g4 + 4 * hh;
+        uint2 pk;
+        pk.x = static_cast<uint32_t>(f32_to_bf16(oacc[mt][4 * g4 + 0] * inv)) |
+               (static_cast<uint32_t>(f32_to_bf16(oacc[mt][4 * g4 + 1] * inv)) << 16);
+        pk.y = static_cast<uint32_t>(f32_to_bf16(oacc[mt][4 * g4 + 2] * inv)) |
+               (static_cast<uint32_t>(f32_to_bf16(oacc[mt][4 * g4 + 3] * inv)) << 16);
+        *reinterpret_cast<uint2 *>(op + d) = pk;
+      }
+    if (a.lse && hh == 0)
+      a.lse[(static_cast<size_t>(batch) * a.H + head) * a.L + tok0 + my_q] = m_run + fast_log2(l_run);
+  }
+}
+
+// ------------------------------------------------------------------ decode
+template <int R>  // query rows served per workgroup (GQA group x L)
+__global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int group = a.H / a.Hkv;
+  const int dc = (lane & 7) * 8;  // this lane's 8 feature columns
+  const int ksub = lane >> 3;     // key within an 8-key row group
+
+  const int kv_len = min(a.S, a.q_start + a.L);
+  const int per = ((kv_len + a.splits - 1) / a.splits + kBN - 1) / kBN * kBN;
+  const int k_lo = split * per, k_hi = min(kv_len, k_lo + per);
+
+  float q[R][8], c_qk[R], c_b[R], al[R], be[R], mu[R];
+  int qabs[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const bool ok = r < a.rows;
+    const int head = kvh * group + (ok ? r % group : 0);
+    const int i = ok ? r / group : 0;
+    const bf16_t *qp = a.q + b * a.q_sb + head * a.q_sh + int64_t(i) * a.q_st + dc;
+    const uint4 raw = *reinterpret_cast<const uint4 *>(qp);
+    const bf16_t *qb = reinterpret_cast<const bf16_t *>(&raw);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q[r][e] = ok ? bf16_to_f32(qb[e]) : 0.f;
+    const float mul = ok ? a.ssmax[head] * a.log_n[b * a.ln_sb + int64_t(i) * a.ln_st] : 0.f;
+    c_qk[r] = mul * a.scale * kLog2e;
+    c_b[r] = mul * kLog2e;
+    al[r] = a.alpha[head]; be[r] = a.beta[head]; mu[r] = a.mu[head];
+    qabs[r] = ok ? a.q_start + i : -1;
+  }
+
+  float m[R], l[R], acc[R][8];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    m[r] = -INFINITY; l[r] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[r][e] = 0.f;
+  }
+
+  const bf16_t *kp = a.k + b * a.k_sb + kvh * a.k_sh + dc;
+  const bf16_t *vp = a.v + b * a.v_sb + kvh * a.v_sh + dc;
+
+  for (int n0 = k_lo + w * kBN; n0 < k_hi; n0 += 4 * kBN) {
+    uint4 kr[8], vr[8];
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int key = n0 + 8 * it + ksub;
+      const bool ok = key < k_hi;
+      kr[it] = ok ? *reinterpret_cast<const uint4 *>(kp + int64_t(key) * a.k_st) : uint4{0, 0, 0, 0};
+      vr[it] = ok ? *reinterpret_cast<const uint4 *>(vp + int64_t(key) * a.v_st) : uint4{0, 0, 0, 0};
+    }
+    float s[R][8];
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const bf16_t *kb = reinterpret_cast<const bf16_t *>(&kr[it]);
+      float kf[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kf[e] = bf16_to_f32(kb[e]);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d = fmaf(q[r][e], kf[e], d);
+        d += __shfl_xor(d, 1, 64);
+        d += __shfl_xor(d, 2, 64);
+        d += __shfl_xor(d, 4, 64);
+        s[r][it] = d;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int key = n0 + 8 * it + ksub;
+        float x = -INFINITY;
+        if (key < k_hi && key <= qabs[r])
+          x = fmaf(s[r][it], c_qk[r], c_b[r] * ggd_bias(static_cast<float>(key - qabs[r]), al[r], be[r], mu[r], a.eps));
+        s[r][it] = x;
+        mx = fmaxf(mx, x);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m[r], mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float resc = fast_exp2(m[r] - m_use);
+      float ps = 0.f;
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const float p = fast_exp2(s[r][it] - m_use);
+        s[r][it] = p;
+        ps += p;
+      }
+      ps += __shfl_xor(ps, 8, 64);
+      ps += __shfl_xor(ps, 16, 64);
+      ps += __shfl_xor(ps, 32, 64);
+      l[r] = l[r] * resc + ps;
+      m[r] = m_new;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[r][e] *= resc;
+    }
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const bf16_t *vb = reinterpret_cast<const bf16_t *>(&vr[it]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float vf = bf16_to_f32(vb[e]);
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r][e] = fmaf(s[r][it], vf, acc[r][e]);
+      }
+    }
+  }
+
+  // Finish the per-wave accumulators (sum over the 8 key sub-rows).
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float x = acc[r][e];
+      x += __shfl_xor(x, 8, 64);
+      x += __shfl_xor(x, 16, 64);
+      x += __shfl_xor(x, 32, 64);
+      acc[r][e] = x;
+    }
+
+  // Merge the 4 waves in LDS.
+  __shared__ float sm[4][R], sl[4][R], sacc[4][R][kD];
+  if (lane < 8) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sacc[w][r][dc + e] = acc[r][e];
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) { sm[w][r] = m[r]; sl[w][r] = l[r]; }
+  }
+  __syncthreads();
+  for (int e = tid; e < R * kD; e += 256) {
+    const int r = e / kD, d = e % kD;
+    if (r >= a.rows) continue;
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, sm[ww][r]);
+    const float Mu = M == -INFINITY ? 0.f : M;
+    float o = 0.f, L = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      const float f = fast_exp2(sm[ww][r] - Mu);
+      o += sacc[ww][r][d] * f;
+      L += sl[ww][r] * f;
+    }
+    if (a.splits == 1) {
+      const int head = kvh * group + r % group, i = r / group;
+      a.out[b * a.o_sb + head * a.o_sh + int64_t(i) * a.o_st + d] = f32_to_bf16(o / fmaxf(L, 1e-20f));
+      if (a.lse && d == 0) a.lse[(static_cast<size_t>(b) * a.H + head) * a.L + i] = M + fast_log2(L);
+    } else {
+      float *pp = a.part + ((((static_cast<size_t>(b) * a.Hkv + kvh) * a.splits + split) * a.rows + r) * (kD + 2));
+      pp[d] = o;
+      if (d == 0) { pp[kD] = M; pp[kD + 1] = L; }
+    }
+  }
+}
+
+__global__ void __launch_bounds__(64) chord_merge_kernel(ChordArgs a) {
+  const int r = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, d = threadIdx.x;
+  const int group = a.H / a.Hkv;
+  const float *pp = a.part + (((static_cast<size_t>(b) * a.Hkv + kvh) * a.splits) * a.rows + r) * (kD + 2);
+  const size_t sstride = static_cast<size_t>(a.rows) * (kD + 2);
+  float M = -INFINITY;
+  for (int s = 0; s < a.splits; ++s) M = fmaxf(M, pp[s * sstride + kD]);
+  const float Mu = M == -INFINITY ? 0.f : M;
+  float o = 0.f, L = 0.f;
+  for (int s = 0; s < a.splits; ++s) {
+    const float f = fast_exp2(pp[s * sstride + kD] - Mu);
+    o += pp[s * sstride + d] * f;
+    L += pp[s * sstride + kD + 1] * f;
+  }
+  const int head = kvh * group + r % group, i = r / group;
+  a.out[b * a.o_sb + head * a.o_sh + int64_t(i) * a.o_st + d] = f32_to_bf16(o / fmaxf(L, 1e-20f));
+  if (a.lse && d == 0) a.lse[(static_cast<size_t>(b) * a.H + head) * a.L + i] = M + fast_log2(L);
+}
+
+// ------------------------------------------------------------------ planning
+static int device_cu_count() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+  return n;
+}
+
+constexpr int kDecodeMaxRows = 8;
+
+static bool use_decode(int H, int Hkv, int L, bool packed) {
+  return !packed && (H / Hkv) * L <= kDecodeMaxRows;
+}
+
+static int decode_splits(int B, int Hkv, int L, int S, int q_start_hint) {
+  (void)q_start_hint;
+  const int kv_len = std::max(1, S);
+  const int cus = device_cu_count();
+  const int base = std::max(1, B * Hkv);
+  int want = (2 * cus + base - 1) / base;                   // ~2 workgroups per CU
+  want = std::min(want, (kv_len + 4 * kBN - 1) / (4 * kBN));  // >= one 64-key tile per wave
+  (void)L;
+  return std::max(1, std::min(want, 32));
+}
+
+template <int R>
+static void launch_decode_r(const ChordArgs &a, hipStream_t s) {
+  chord_decode_kernel<R><<<dim3(a.splits, a.Hkv, a.B), dim3(256), 0, s>>>(a);
+}
+
+}  // namespace motif
+
+using namespace motif;
+
+extern "C" size_t motif_chord_workspace_bytes(int B, int H, int Hkv, int L, int S, int D, int *splits) {
+  int sp = 1;
+  if (B > 0 && H > 0 && Hkv > 0 && H % Hkv == 0 && L > 0 && use_decode(H, Hkv, L, false))
+    sp = decode_splits(B, Hkv, L, S, 0);
+  if (splits) *splits = sp;
+  if (sp <= 1) return 0;
+  const size_t rows = static_cast<size_t>(H / Hkv) * L;
+  return static_cast<size_t>(B) * Hkv * sp * rows * (D + 2) * sizeof(float);
+}
+
+extern "C" int motif_chord_fwd(
+    const void *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void *k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void *v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    const float *alpha, const float *beta, const float *mu, const float *ssmax,
+    const float *log_n, int64_t ln_sb, int64_t ln_st,
+    void *out, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    float *lse,
+    int B, int H, int Hkv, int L, int S, int D,
+    int q_start, float scale, float eps,
+    const int32_t *cu_seqlens, int nseq, int max_seqlen,
+    void *workspace, size_t workspace_bytes,
+    int dtype, void *stream) {
+  if (B < 0 || H <= 0 || Hkv <= 0 || L < 0 || S < 0 || q_start < 0)
+    return set_error(MOTIF_ERR_INVALID, "chord_fwd: bad size or negative q_start");
+  if (H % Hkv != 0) return set_error(MOTIF_ERR_INVALID, "chord_fwd: H must be a multiple of Hkv");
+  if (D != kD) return set_error(MOTIF_ERR_UNSUPPORTED, "chord_fwd: head_dim must be 64");
+  if (dtype != MOTIF_BF16) return set_error(MOTIF_ERR_UNSUPPORTED, "chord_fwd: only bf16 is implemented");
+  const bool packed = cu_seqlens != nullptr;
+  if (packed && (B != 1 || nseq <= 0 || L != S))
+    return set_error(MOTIF_ERR_INVALID, "chord_fwd: packed sequences need B == 1, nseq > 0 and L == S");
+  if (!packed && nseq != B) return set_error(MOTIF_ERR_INVALID, "chord_fwd: nseq must equal B");
+  if (B == 0 || L == 0) return MOTIF_OK;
+  if (!q || !k || !v || !alpha || !beta || !mu || !ssmax || !log_n || !out)
+    return set_error(MOTIF_ERR_INVALID, "chord_fwd: NULL pointer");
+  if (((q_st | k_st | v_st | o_st | q_sh | k_sh | v_sh | o_sh | q_sb | k_sb | v_sb | o_sb) & 7) != 0 ||
+      ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
+        reinterpret_cast<uintptr_t>(out)) & 15) != 0)
+    return set_error(MOTIF_ERR_UNSUPPORTED, "chord_fwd: q/k/v/out need 16-byte aligned rows (strides multiple of 8)");
+
+  ChordArgs a;
+  a.q = static_cast<const bf16_t *>(q); a.q_sb = q_sb; a.q_sh = q_sh; a.q_st = q_st;
+  a.k = static_cast<const bf16_t *>(k); a.k_sb = k_sb; a.k_sh = k_sh; a.k_st = k_st;
+  a.v = static_cast<const bf16_t *>(v); a.v_sb = v_sb; a.v_sh = v_sh; a.v_st = v_st;
+  a.alpha = alpha; a.beta = beta; a.mu = mu; a.ssmax = ssmax;
+  a.log_n = log_n; a.ln_sb = ln_sb; a.ln_st = ln_st;
+  a.out = static_cast<bf16_t *>(out); a.o_sb = o_sb; a.o_sh = o_sh; a.o_st = o_st;
+  a.lse = lse;
+  a.B = B; a.H = H; a.Hkv = Hkv; a.L = L; a.S = S; a.q_start = q_start;
+  a.scale = scale; a.eps = eps;
+  a.cu = cu_seqlens;
+  a.part = nullptr; a.splits = 1; a.rows = (H / Hkv) * L;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int group = H / Hkv;
+
+  if (use_decode(H, Hkv, L, packed)) {
+    if (S == 0) return set_error(MOTIF_ERR_INVALID, "chord_fwd: empty key cache");
+    a.splits = decode_splits(B, Hkv, L, S, q_start);
+    if (a.splits > 1) {
+      const size_t need = motif_chord_workspace_bytes(B, H, Hkv, L, S, D, nullptr);
+      if (!workspace || workspace_bytes < need)
+        return set_error(MOTIF_ERR_INVALID, "chord_fwd: workspace too small (need " + std::to_string(need) + " bytes)");
+      a.part = static_cast<float *>(workspace);
+    }
+    if (a.rows <= 1) launch_decode_r<1>(a, s);
+    else if (a.rows <= 2) launch_decode_r<2>(a, s);
+    else if (a.rows <= 4) launch_decode_r<4>(a, s);
+    else launch_decode_r<8>(a, s);
+    int rc = check_launch("chord_decode_kernel");
+    if (rc || a.splits == 1) return rc;
+    chord_merge_kernel<<<dim3(a.rows, Hkv, B), dim3(64), 0, s>>>(a);
+    return check_launch("chord_merge_kernel");
+  }
+
+  const int hpw = (group % 4 == 0) ? 4 : (group % 2 == 0) ? 2 : 1;
+  const int qbpw = 4 / hpw;
+  const int maxlen = packed ? max_seqlen : L;
+  if (maxlen <= 0) return MOTIF_OK;
+  dim3 grid((maxlen + 32 * qbpw - 1) / (32 * qbpw), H / hpw, packed ? nseq : B), block(256);
+  if (hpw == 4) chord_fwd_kernel<4><<<grid, block, 0, s>>>(a);
+  else if (hpw == 2) chord_fwd_kernel<2><<<grid, block, 0, s>>>(a);
+  else chord_fwd_kernel<1><<<grid, block, 0, s>>>(a);
+  return check_launch("chord_fwd_kernel");
+}

@@ -1,0 +1,108 @@
+'''ctypes binding of libmotif_hip.so (declared in include/motif_hip.h).
+
+The library is loaded after `torch` so that it binds to the HIP runtime torch
+already loaded (both are `libamdhip64.so.7`): one runtime per process, so the
+hipStream_t handles and device pointers torch hands out are valid for it.
+'''
+import ctypes
+import os
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), 'libmotif_hip.so')
+
+MOTIF_F32 = 0
+MOTIF_BF16 = 1
+
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int
+_P = ctypes.c_void_p
+_F32 = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+# Argument lists mirror include/motif_hip.h one for one.
+_T4 = [_P, _I64, _I64, _I64]
+_SIGNATURES = {
+    'motif_abi_version': ([], _I32),
+    'motif_last_error': ([], ctypes.c_char_p),
+    'motif_gdn_recurrent_fwd': (
+        _T4 * 5 + [_P, _P] + _T4 + [_I32] * 5 + [_I32, _I32, _P], _I32),
+    'motif_gdn_chunk_workspace_bytes': ([_I32] * 5, _SZ),
+    'motif_gdn_chunk_fwd': (
+        _T4 * 5 + [_P, _P] + _T4 + [_I32] * 6 + [_P, _P, _I32, _I32, _P, _SZ, _I32, _I32, _P], _I32),
+    'motif_short_conv_silu': (
+        [_P, _I64, _I64, _P, _P, _P, _P, _I64, _I64] + [_I32] * 4 + [_P, _I32, _I32, _I32, _P], _I32),
+    'motif_chord_workspace_bytes': ([_I32] * 6 + [ctypes.POINTER(_I32)], _SZ),
+    'motif_chord_fwd': (
+        _T4 * 3 + [_P, _P, _P, _P] + [_P, _I64, _I64] + _T4 + [_P] + [_I32] * 6
+        + [_I32, _F32, _F32] + [_P, _I32, _I32] + [_P, _SZ] + [_I32, _P], _I32),
+}
+
+EXPORTED = tuple(_SIGNATURES)
+
+_lib = None
+_load_error = None
+
+
+def _load():
+    global _lib, _load_error
+    if _lib is not None or _load_error is not None:
+        return
+    try:
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = lib
+    except (OSError, AttributeError) as exc:
+        _load_error = exc
+
+
+def available() -> bool:
+    '''True when the kernel library loaded and a ROCm device is visible.'''
+    _load()
+    return _lib is not None and torch.cuda.is_available()
+
+
+def lib():
+    '''The loaded library; raises RuntimeError when it cannot be loaded.'''
+    _load()
+    if _lib is None:
+        raise RuntimeError(
+            f'the motif HIP kernel library is not available ({LIB_PATH}): {_load_error}. '
+            'Build it with `python codon-motif_amd/csrc/build.py`.')
+    return _lib
+
+
+def check(rc: int, what: str):
+    '''Turn a non-zero motif_status into an exception (INVALID -> ValueError).'''
+    if rc == 0:
+        return
+    msg = lib().motif_last_error().decode(errors='replace')
+    if rc == 1:
+        raise ValueError(f'{what}: {msg}')
+    if rc == 2:
+        raise NotImplementedError(f'{what}: {msg}')
+    raise RuntimeError(f'{what}: {msg}')
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return MOTIF_F32
+    if dt == torch.bfloat16:
+        return MOTIF_BF16
+    raise NotImplementedError(f'unsupported dtype {dt} (float32 / bfloat16 only)')
+
+
+def stream_ptr(device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def t4(t):
+    '''(pointer, batch stride, head stride, time stride) of a [B, H, T, ...] tensor.'''
+    return [t.data_ptr(), t.stride(0), t.stride(1), t.stride(2)]

@@ -1,0 +1,180 @@
+'''Chord attention (GGD-biased causal softmax) on the gfx950 HIP kernels.
+
+`apply_chord_attention` keeps the reference signature, defaults, validation
+messages and exception types (motif/ops/chord_attention.py:1557-1625 with
+`_check_tensors` :966-1011 and `_check_params` :1448-1472).  The launcher
+picks the MFMA flash kernel for prefill shapes and the split-K decode kernel
+when a kv head serves at most 8 query rows (GQA group x L), which is the
+reference's long-KV / short-Q split path (:1128-1229).
+`apply_chord_attention_varlen` adds packed sequences (new).
+'''
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+HEAD_DIM = 64
+
+
+def _check_tensors(q, k, v, log_n):
+    for name, t in (('q', q), ('k', k), ('v', v)):
+        if not t.is_cuda:
+            raise ValueError(f'{name} must live on CUDA')
+        if t.dim() != 4:
+            raise ValueError(f'{name} must be 4-D [B, H, L, D], got {tuple(t.shape)}')
+        if t.stride(-1) != 1:
+            raise ValueError(f'{name} must be contiguous along the last dimension (stride(-1) == 1)')
+        if t.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            raise ValueError(f'{name} has unsupported dtype {t.dtype} (only fp16 / bf16 / fp32)')
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise ValueError('q / k / v must all have the same dtype')
+    if k.shape != v.shape:
+        raise ValueError(f'k / v must have the same shape, got {tuple(k.shape)} vs {tuple(v.shape)}')
+    B, H, L, D = q.shape
+    Bk, Hkv, S, Dk = k.shape
+    if B != Bk or D != Dk:
+        raise ValueError(f'q {tuple(q.shape)} and k {tuple(k.shape)} disagree on B / D')
+    if H % Hkv != 0:
+        raise ValueError(f'num_heads {H} must be divisible by num_kv_heads {Hkv}')
+    if D < 16:
+        raise ValueError(f'head_dim {D} is too small (>= 16 required)')
+    if log_n.shape != (B, L):
+        raise ValueError(f'log_n must be [B, q_len] = {(B, L)}, got {tuple(log_n.shape)}')
+    if log_n.dtype != torch.float32:
+        raise ValueError(f'log_n must be fp32, got {log_n.dtype}')
+    if log_n.stride(-1) != 1:
+        raise ValueError('log_n must be contiguous along the last dimension')
+    return B, H, L, D, Hkv, S
+
+
+def _check_params(alpha, beta, mu, ssmax, num_heads):
+    for name, t in (('alpha', alpha), ('beta', beta), ('mu', mu), ('ssmax', ssmax)):
+        if not t.is_cuda:
+            raise ValueError(f'{name} must live on CUDA')
+        if t.dtype != torch.float32:
+            raise ValueError(f'{name} must be fp32, got {t.dtype}')
+        if t.shape != (num_heads,):
+            raise ValueError(f'{name} must be [{num_heads}], got {tuple(t.shape)}')
+        if not t.is_contiguous():
+            raise ValueError(f'{name} must be contiguous')
+
+
+def _aligned(t):
+    '''Rows must start on 16-byte boundaries for the vector loads.'''
+    ok = t.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in t.stride()[:-1])
+    return t if ok else t.contiguous()
+
+
+def _launch(q, k, v, alpha, beta, mu, ssmax, log_n, q_start, scale, eps, out, lse=None,
+            cu_dev=None, nseq=None, max_seqlen=None):
+    B, H, L, D = q.shape
+    Hkv, S = k.shape[1], k.shape[2]
+    if q.dtype != torch.bfloat16:
+        raise NotImplementedError(
+            f'apply_chord_attention: the HIP kernel computes bf16 inputs; got {q.dtype}')
+    if D != HEAD_DIM:
+        raise NotImplementedError(f'apply_chord_attention: head_dim {D} unsupported (64 only)')
+    q, k, v = _aligned(q), _aligned(k), _aligned(v)
+    lib = _lib.lib()
+    if cu_dev is None:
+        nseq, max_seqlen = B, L
+        nbytes = lib.motif_chord_workspace_bytes(B, H, Hkv, L, S, D, None)
+    else:
+        nbytes = 0
+    ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=q.device)
+    rc = lib.motif_chord_fwd(
+        *_lib.t4(q), *_lib.t4(k), *_lib.t4(v),
+        alpha.data_ptr(), beta.data_ptr(), mu.data_ptr(), ssmax.data_ptr(),
+        log_n.data_ptr(), log_n.stride(0), log_n.stride(1),
+        *_lib.t4(out), _lib.ptr(lse),
+        B, H, Hkv, L, S, D, int(q_start), float(scale), float(eps),
+        _lib.ptr(cu_dev), int(nseq), int(max_seqlen),
+        ws.data_ptr(), ws.numel(), _lib.MOTIF_BF16, _lib.stream_ptr(q.device))
+    _lib.check(rc, 'motif_chord_fwd')
+    return out
+
+
+def apply_chord_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    alpha: torch.Tensor,
+    beta: torch.Tensor,
+    mu: torch.Tensor,
+    ssmax: torch.Tensor,
+    log_n: torch.Tensor,
+    q_start: Optional[int] = None,
+    softmax_scale: Optional[float] = None,
+    eps: float = 1e-5,
+) -> torch.Tensor:
+    '''Chord attention forward on the HIP kernels.
+
+    logits = (softmax_scale * q.k + bias) * ssmax_h * log_n[b, i] with the GGD
+    bias -alpha_h (|j - (q_start + i) - mu_h| + eps) ** beta_h, causal over
+    keys j <= q_start + i, softmax over keys, times v.
+
+    Args:
+        q: [B, H, L, D];  k, v: [B, H_kv, S, D] (bf16, D == 64).
+        alpha, beta, mu, ssmax: [H] fp32 contiguous.
+        log_n: [B, L] fp32.
+        q_start: absolute position of the first query; defaults to S - L.
+        softmax_scale: defaults to D ** -0.5.
+        eps: GGD epsilon.
+
+    Returns:
+        [B, H, L, D] in q's dtype.
+
+    Raises:
+        ValueError: on unsupported inputs or a negative q_start.
+        NotImplementedError: for inputs requiring grad, non-bf16 dtypes or D != 64.
+        RuntimeError: when the HIP library is unavailable or a launch fails.
+    '''
+    if not _lib.available():
+        raise RuntimeError('there is no usable HIP backend in the current environment')
+    B, H, L, D, Hkv, S = _check_tensors(q, k, v, log_n)
+    _check_params(alpha, beta, mu, ssmax, H)
+    if softmax_scale is None:
+        softmax_scale = D ** -0.5
+    if q_start is None:
+        q_start = S - L
+    q_start = int(q_start)
+    if q_start < 0:
+        raise ValueError(f'q_start must not be negative, got {q_start}')
+    needs_grad = torch.is_grad_enabled() and any(
+        t.requires_grad for t in (q, k, v, alpha, beta, mu, ssmax))
+    if needs_grad:
+        raise NotImplementedError('apply_chord_attention: backward is not implemented by the HIP kernels')
+    out = torch.empty((B, H, L, D), dtype=q.dtype, device=q.device)
+    if L == 0:
+        return out
+    return _launch(q, k, v, alpha, beta, mu, ssmax, log_n, q_start, softmax_scale, eps, out)
+
+
+def apply_chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, log_n, cu_seqlens,
+                                 softmax_scale=None, eps=1e-5):
+    '''Packed-sequence Chord attention (no reference counterpart).
+
+    B == 1; q [1, H, T, D], k/v [1, H_kv, T, D] hold the sequences back to back,
+    sequence i covering rows [cu_seqlens[i], cu_seqlens[i+1]).  Each sequence is
+    causal on its own with positions restarting at 0; log_n [1, T] is read at
+    the packed row (log(1 .. len_i) per sequence reproduces separate runs).
+    '''
+    if not _lib.available():
+        raise RuntimeError('there is no usable HIP backend in the current environment')
+    B, H, L, D, Hkv, S = _check_tensors(q, k, v, log_n)
+    _check_params(alpha, beta, mu, ssmax, H)
+    if B != 1 or S != L:
+        raise ValueError('apply_chord_attention_varlen: needs B == 1 and packed q / k of equal length')
+    cu_host = cu_seqlens.detach().to('cpu', torch.int64)
+    lens = cu_host[1:] - cu_host[:-1]
+    if int(cu_host[0]) != 0 or int(cu_host[-1]) != L or (lens < 0).any():
+        raise ValueError('cu_seqlens must start at 0, be non-decreasing and end at T')
+    if softmax_scale is None:
+        softmax_scale = D ** -0.5
+    out = torch.empty((B, H, L, D), dtype=q.dtype, device=q.device)
+    if L == 0:
+        return out
+    cu_dev = cu_host.to(device=q.device, dtype=torch.int32)
+    return _launch(q, k, v, alpha, beta, mu, ssmax, log_n, 0, softmax_scale, eps, out,
+                   cu_dev=cu_dev, nseq=int(lens.numel()), max_seqlen=int(lens.max()))

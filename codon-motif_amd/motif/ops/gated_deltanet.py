@@ -1,0 +1,216 @@
+'''Gated delta rule (GDN) ops on the gfx950 HIP kernels.
+
+Same public functions and argument meaning as the reference's
+motif/ops/gated_deltanet.py (`recurrent_gated_delta_rule` :26-59,
+`chunk_gated_delta_rule` :287-321, `chunk_gated_delta_rule_triton` :796-834),
+plus `chunk_gated_delta_rule_varlen` for packed sequences (new).
+
+Differences that do not change results beyond rounding:
+- the recurrent state is carried and returned in fp32 whatever the input dtype
+  (inputs may be fp32 or bf16; q/k/v/beta/g of mixed dtypes are computed in fp32);
+- `chunk_size` is rounded down to one of the kernel chunk lengths
+  {16, 32, 64} (values >= 64 use 64); the chunk length only changes the order
+  of floating-point operations, not the recurrence.
+Backward is not implemented: calling with inputs that require grad under
+autograd raises NotImplementedError.
+'''
+import torch
+
+from . import _lib
+
+__all__ = [
+    'recurrent_gated_delta_rule',
+    'chunk_gated_delta_rule',
+    'chunk_gated_delta_rule_triton',
+    'chunk_gated_delta_rule_varlen',
+]
+
+_KERNEL_CHUNKS = (64, 32, 16)
+
+
+def _kernel_chunk(chunk_size: int) -> int:
+    for c in _KERNEL_CHUNKS:
+        if chunk_size >= c:
+            return c
+    return 16
+
+
+def _prepare(q, k, v, beta, g, name):
+    '''Validate GDN inputs and return them in one kernel dtype.'''
+    for n, t in (('q', q), ('k', k), ('v', v)):
+        if t.dim() != 4:
+            raise ValueError(f'{name}: {n} must be 4-D [B, H, L, D], got {tuple(t.shape)}')
+    for n, t in (('beta', beta), ('g', g)):
+        if t.dim() != 3:
+            raise ValueError(f'{name}: {n} must be 3-D [B, H, L], got {tuple(t.shape)}')
+    B, H, L, Dk = q.shape
+    if k.shape != q.shape:
+        raise ValueError(f'{name}: k {tuple(k.shape)} must match q {tuple(q.shape)}')
+    if v.shape[:3] != (B, H, L):
+        raise ValueError(f'{name}: v {tuple(v.shape)} disagrees with q on [B, H, L]')
+    if beta.shape != (B, H, L) or g.shape != (B, H, L):
+        raise ValueError(f'{name}: beta / g must be [B, H, L] = {(B, H, L)}')
+    ts = (q, k, v, beta, g)
+    if not all(t.is_cuda for t in ts):
+        raise ValueError(f'{name}: inputs must live on the ROCm device (the HIP kernels have no CPU path)')
+    if len({t.device for t in ts}) != 1:
+        raise ValueError(f'{name}: inputs must share one device')
+    if any(t.requires_grad for t in ts) and torch.is_grad_enabled():
+        raise NotImplementedError(f'{name}: backward is not implemented by the HIP kernels')
+    dts = {t.dtype for t in ts}
+    if not dts <= {torch.float32, torch.bfloat16}:
+        raise NotImplementedError(f'{name}: dtypes {sorted(map(str, dts))} unsupported (float32 / bfloat16)')
+    cdt = torch.bfloat16 if dts == {torch.bfloat16} else torch.float32
+    out = []
+    for i, t in enumerate(ts):
+        t = t.to(cdt)
+        if i < 3 and t.stride(-1) != 1:  # feature axis of q / k / v must be unit-stride
+            t = t.contiguous()
+        out.append(t)
+    return out, cdt
+
+
+def _state_in(S, B, H, Dk, Dv, device, name):
+    if S is None:
+        return None
+    if S.shape != (B, H, Dk, Dv):
+        raise ValueError(f'{name}: S must be [B, H, Dk, Dv] = {(B, H, Dk, Dv)}, got {tuple(S.shape)}')
+    return S.to(device=device, dtype=torch.float32).contiguous()
+
+
+def recurrent_gated_delta_rule(q, k, v, beta, g, S=None):
+    '''Token-by-token gated delta rule on the HIP recurrence kernel.
+
+    Per step: S <- S * exp(g_t); S <- S + k_t (beta_t (v_t - k_t^T S))^T;
+    o_t = S^T q_t (reference motif/ops/gated_deltanet.py:26-59).
+
+    Args:
+        q, k: [B, H, L, Dk];  v: [B, H, L, Dv];  beta, g: [B, H, L].
+        S: optional [B, H, Dk, Dv] initial state (zeros when None).
+
+    Returns:
+        (o [B, H, L, Dv] in q's dtype, S [B, H, Dk, Dv] fp32)
+    '''
+    name = 'recurrent_gated_delta_rule'
+    (qc, kc, vc, bc, gc), cdt = _prepare(q, k, v, beta, g, name)
+    B, H, L, Dk = qc.shape
+    Dv = vc.shape[-1]
+    S_in = _state_in(S, B, H, Dk, Dv, qc.device, name)
+    o = torch.empty(B, H, L, Dv, dtype=cdt, device=qc.device)
+    S_out = torch.empty(B, H, Dk, Dv, dtype=torch.float32, device=qc.device)
+    gdn_recurrent_into(qc, kc, vc, bc, gc, S_in, S_out, o)
+    return o.to(q.dtype), S_out
+
+
+def gdn_recurrent_into(q, k, v, beta, g, S_in, S_out, o):
+    '''Launch the recurrence writing into preallocated `S_out` and `o`.
+
+    `S_out` may be `S_in` (in-place state update, used by the decode step);
+    no allocation happens here, so the launch can be captured in a hipGraph.
+    '''
+    B, H, L, Dk = q.shape
+    Dv = v.shape[-1]
+    code = _lib.dtype_code(q.dtype)
+    rc = _lib.lib().motif_gdn_recurrent_fwd(
+        *_lib.t4(q), *_lib.t4(k), *_lib.t4(v), *_lib.t4(beta), *_lib.t4(g),
+        _lib.ptr(S_in), S_out.data_ptr(), *_lib.t4(o),
+        B, H, L, Dk, Dv, code, _lib.dtype_code(o.dtype), _lib.stream_ptr(q.device))
+    _lib.check(rc, 'motif_gdn_recurrent_fwd')
+
+
+def _chunk_call(qc, kc, vc, bc, gc, S_in, C, cu=None, nseq=None):
+    B, H, L, Dk = qc.shape
+    Dv = vc.shape[-1]
+    dev = qc.device
+    if cu is None:
+        nseq = B
+        total = B * ((L + C - 1) // C)
+        cu_dev = coff_dev = None
+    else:
+        cu_host = cu.detach().to('cpu', torch.int64)
+        lens = cu_host[1:] - cu_host[:-1]
+        if (lens < 0).any() or int(cu_host[0]) != 0 or int(cu_host[-1]) != L:
+            raise ValueError('cu_seqlens must start at 0, be non-decreasing and end at L')
+        nch = (lens + C - 1) // C
+        coff = torch.zeros(nseq + 1, dtype=torch.int32)
+        coff[1:] = torch.cumsum(nch, 0).to(torch.int32)
+        total = int(coff[-1])
+        cu_dev = cu_host.to(device=dev, dtype=torch.int32)
+        coff_dev = coff.to(dev)
+    o = torch.empty(B, H, L, Dv, dtype=qc.dtype, device=dev)
+    S_out = torch.empty(nseq, H, Dk, Dv, dtype=torch.float32, device=dev)
+    nbytes = _lib.lib().motif_gdn_chunk_workspace_bytes(H, Dk, Dv, C, max(total, 1))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    code = _lib.dtype_code(qc.dtype)
+    rc = _lib.lib().motif_gdn_chunk_fwd(
+        *_lib.t4(qc), *_lib.t4(kc), *_lib.t4(vc), *_lib.t4(bc), *_lib.t4(gc),
+        _lib.ptr(S_in), S_out.data_ptr(), *_lib.t4(o),
+        B, H, L, Dk, Dv, C,
+        _lib.ptr(cu_dev), _lib.ptr(coff_dev), nseq, total,
+        ws.data_ptr(), ws.numel(), code, code, _lib.stream_ptr(dev))
+    _lib.check(rc, 'motif_gdn_chunk_fwd')
+    return o, S_out
+
+
+def chunk_gated_delta_rule(q, k, v, beta, g, S=None, chunk_size=64):
+    '''Chunked gated delta rule on the HIP chunk kernels.
+
+    Same result as the reference's pure-torch chunk loop
+    (motif/ops/gated_deltanet.py:287-321) up to rounding.
+
+    Args:
+        q, k: [B, H, L, Dk];  v: [B, H, L, Dv];  beta, g: [B, H, L].
+        S: optional [B, H, Dk, Dv] initial state (zeros when None).
+        chunk_size: chunk length (rounded down to 16, 32 or 64).
+
+    Returns:
+        (o [B, H, L, Dv] in q's dtype, S [B, H, Dk, Dv] fp32)
+    '''
+    name = 'chunk_gated_delta_rule'
+    (qc, kc, vc, bc, gc), _ = _prepare(q, k, v, beta, g, name)
+    B, H, L, Dk = qc.shape
+    S_in = _state_in(S, B, H, Dk, vc.shape[-1], qc.device, name)
+    o, S_out = _chunk_call(qc, kc, vc, bc, gc, S_in, _kernel_chunk(int(chunk_size)))
+    return o.to(q.dtype), S_out
+
+
+def chunk_gated_delta_rule_triton(q, k, v, beta, g, S=None, chunk_size=64):
+    '''The fast-backend entry of the reference (motif/ops/gated_deltanet.py:796-834).
+
+    Raises NotImplementedError when the HIP backend is unavailable or
+    `chunk_size < 16`, as the reference does for a missing Triton or a chunk
+    below the dot-product minimum; otherwise identical to
+    `chunk_gated_delta_rule`.
+    '''
+    if not _lib.available():
+        raise NotImplementedError('the HIP backend is not available for the GatedDeltaNet chunk scan.')
+    if int(chunk_size) < 16:
+        raise NotImplementedError('chunk_size must be >= 16')
+    return chunk_gated_delta_rule(q, k, v, beta, g, S, chunk_size)
+
+
+def chunk_gated_delta_rule_varlen(q, k, v, beta, g, cu_seqlens, S=None, chunk_size=64):
+    '''Packed-sequence chunked gated delta rule (no reference counterpart).
+
+    B must be 1; sequence i covers tokens [cu_seqlens[i], cu_seqlens[i+1]) and
+    runs independently from its own initial state S[i] (zeros when S is None).
+
+    Returns:
+        (o [1, H, L, Dv] in q's dtype, S [nseq, H, Dk, Dv] fp32)
+    '''
+    name = 'chunk_gated_delta_rule_varlen'
+    (qc, kc, vc, bc, gc), _ = _prepare(q, k, v, beta, g, name)
+    B, H, L, Dk = qc.shape
+    if B != 1:
+        raise ValueError(f'{name}: packed sequences need B == 1, got B={B}')
+    nseq = int(cu_seqlens.numel()) - 1
+    if nseq < 1:
+        raise ValueError(f'{name}: cu_seqlens needs at least two entries')
+    Dv = vc.shape[-1]
+    S_in = None
+    if S is not None:
+        if S.shape != (nseq, H, Dk, Dv):
+            raise ValueError(f'{name}: S must be [nseq, H, Dk, Dv] = {(nseq, H, Dk, Dv)}')
+        S_in = S.to(device=qc.device, dtype=torch.float32).contiguous()
+    o, S_out = _chunk_call(qc, kc, vc, bc, gc, S_in, _kernel_chunk(int(chunk_size)), cu_seqlens, nseq)
+    return o.to(q.dtype), S_out

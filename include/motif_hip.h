@@ -1,0 +1,156 @@
+/*
+ * motif_hip.h - C ABI of the MI355X (gfx950) kernels for Motif Chord's
+ * sequence-mixing hot path: the Gated DeltaNet (GDN) delta rule (token
+ * recurrence and chunked prefill), its short causal conv front end, and Chord
+ * GGD-biased softmax attention (prefill and split-K decode).
+ *
+ * Conventions
+ *  - Every entry point is `extern "C"`, takes raw device pointers, element
+ *    strides as int64 (the innermost/feature dimension must have stride 1),
+ *    sizes as int, and a hipStream_t passed as `void *stream` (NULL = default
+ *    stream).  Kernels are enqueued on that stream; nothing synchronises the
+ *    host, nothing allocates device memory (scratch comes in as `workspace`).
+ *  - Return value: MOTIF_OK (0) or a motif_status code; `motif_last_error()`
+ *    returns a message for the last failure on the calling thread.
+ *  - dtype codes: MOTIF_F32 = 0, MOTIF_BF16 = 1.
+ *  - Recurrent state is always fp32, row-major [.., dk, dv], contiguous.
+ */
+#ifndef MOTIF_HIP_H
+#define MOTIF_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum motif_status {
+  MOTIF_OK = 0,
+  MOTIF_ERR_INVALID = 1,     /* bad argument (shape, pointer, size) */
+  MOTIF_ERR_UNSUPPORTED = 2, /* valid but not implemented (head dim, dtype) */
+  MOTIF_ERR_HIP = 3          /* a HIP runtime call failed */
+};
+
+enum motif_dtype { MOTIF_F32 = 0, MOTIF_BF16 = 1 };
+
+/* Version of this ABI (bumped on any signature change). */
+int motif_abi_version(void);
+
+/* Message describing the last non-zero status returned on this thread. */
+const char *motif_last_error(void);
+
+/*
+ * Token-by-token gated delta rule.
+ * Replaces motif/ops/gated_deltanet.py:26-59 `recurrent_gated_delta_rule`
+ * (and the L == 1 decode dispatch at motif/block/attention/gdn_attn.py:198-199).
+ *   q, k [B,H,L,dk]; v [B,H,L,dv]; beta, g [B,H,L]   (all `in_dtype`)
+ *   state_in  [B,H,dk,dv] fp32 or NULL (zeros)
+ *   state_out [B,H,dk,dv] fp32; may alias state_in (in-place update)
+ *   o [B,H,L,dv] (`out_dtype`)
+ * Supported: dk in {16,32,64,128}, any dv >= 1.
+ */
+int motif_gdn_recurrent_fwd(
+    const void *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void *k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void *v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    const void *beta, int64_t b_sb, int64_t b_sh, int64_t b_st,
+    const void *g, int64_t g_sb, int64_t g_sh, int64_t g_st,
+    const float *state_in, float *state_out,
+    void *o, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    int B, int H, int L, int dk, int dv, int in_dtype, int out_dtype, void *stream);
+
+/*
+ * Workspace bytes needed by motif_gdn_chunk_fwd for `total_chunks` chunks
+ * (B * ceil(L / chunk) for padded batches, sum of ceil(len_i / chunk) for
+ * packed sequences).
+ */
+size_t motif_gdn_chunk_workspace_bytes(int H, int dk, int dv, int chunk, int total_chunks);
+
+/*
+ * Chunked gated delta rule (WY / UT form).
+ * Replaces motif/ops/gated_deltanet.py:287-321 `chunk_gated_delta_rule` and
+ * :796-834 `chunk_gated_delta_rule_triton` (with the chunk preparation of
+ * :118-177 and the inter-chunk scan of :326-422 / :614-641).
+ *   Layouts as motif_gdn_recurrent_fwd.
+ *   Padded batches: cu_seqlens = chunk_offsets = NULL, nseq = B.
+ *   Packed sequences (new capability): B == 1, cu_seqlens[nseq+1] and
+ *   chunk_offsets[nseq+1] (cumulative ceil(len_i / chunk)) are device int32;
+ *   state_in / state_out are then [nseq,H,dk,dv] and every sequence starts
+ *   from its own state (zeros when state_in is NULL).
+ *   chunk in {16, 32, 64}; dk in {32, 64, 128}; dv % 32 == 0, dv <= 256.
+ */
+int motif_gdn_chunk_fwd(
+    const void *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void *k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void *v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    const void *beta, int64_t b_sb, int64_t b_sh, int64_t b_st,
+    const void *g, int64_t g_sb, int64_t g_sh, int64_t g_st,
+    const float *state_in, float *state_out,
+    void *o, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    int B, int H, int L, int dk, int dv, int chunk,
+    const int32_t *cu_seqlens, const int32_t *chunk_offsets, int nseq, int total_chunks,
+    void *workspace, size_t workspace_bytes,
+    int in_dtype, int out_dtype, void *stream);
+
+/*
+ * Short causal depthwise conv (kernel K) followed by SiLU.
+ * Replaces motif/block/attention/gdn_attn.py:116-136 `GatedDeltaAttention._conv`.
+ *   x [B,L,D] (strides x_sb, x_st; channel stride 1), weight [D,K] contiguous,
+ *   tail_in [B,D,K-1] contiguous or NULL (zeros), tail_out [B,D,K-1] or NULL
+ *   (may alias tail_in), y [B,L,D].  All in `dtype`.
+ *   y[t] = SiLU(sum_r w[r] * xc[t+r]) with xc = [tail || x];
+ *   tail_out = last K-1 entries of xc (pre-activation inputs).
+ *   Packed sequences: B == 1, cu_seqlens[nseq+1] device int32, max_seqlen =
+ *   longest sequence; every sequence starts from a zero tail and tail_out is
+ *   then [nseq,D,K-1].  Padded batches pass cu_seqlens = NULL, nseq = B,
+ *   max_seqlen = L.  K in {2, 3, 4, 5}.
+ */
+int motif_short_conv_silu(
+    const void *x, int64_t x_sb, int64_t x_st,
+    const void *weight, const void *tail_in, void *tail_out,
+    void *y, int64_t y_sb, int64_t y_st,
+    int B, int L, int D, int K,
+    const int32_t *cu_seqlens, int nseq, int max_seqlen,
+    int dtype, void *stream);
+
+/*
+ * Workspace bytes needed by motif_chord_fwd (split-K partials); also returns
+ * the split count the launcher will use in *splits (may be NULL).
+ */
+size_t motif_chord_workspace_bytes(int B, int H, int Hkv, int L, int S, int D, int *splits);
+
+/*
+ * Chord attention forward: causal softmax attention with the per-head gated
+ * geometric-decay bias b = -alpha_h (|j - i_abs - mu_h| + eps)^beta_h, logits
+ * (scale q.k + b) * ssmax_h * log_n[b,i], i_abs = q_start + i, keys j <= i_abs.
+ * Replaces motif/ops/chord_attention.py:1557-1625 `apply_chord_attention`
+ * (forward, split-K and merge: :74-507, :1128-1299).
+ *   q [B,H,L,D]; k, v [B,Hkv,S,D]; out [B,H,L,D]   (dtype)
+ *   alpha, beta, mu, ssmax [H] fp32; log_n [B,L] fp32 (strides ln_sb, ln_st)
+ *   lse [B,H,L] fp32 (base-2 log-sum-exp) or NULL.
+ *   Packed sequences (new capability): B == 1, cu_seqlens[nseq+1] device int32,
+ *   max_seqlen = longest sequence; q/k/v packed on the sequence axis (L == S),
+ *   positions restart at 0 per sequence and log_n is indexed with the packed
+ *   row.  Padded batches pass cu_seqlens = NULL, nseq = B, max_seqlen = L.
+ *   D == 64; bf16 only.
+ */
+int motif_chord_fwd(
+    const void *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void *k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void *v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    const float *alpha, const float *beta, const float *mu, const float *ssmax,
+    const float *log_n, int64_t ln_sb, int64_t ln_st,
+    void *out, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    float *lse,
+    int B, int H, int Hkv, int L, int S, int D,
+    int q_start, float scale, float eps,
+    const int32_t *cu_seqlens, int nseq, int max_seqlen,
+    void *workspace, size_t workspace_bytes,
+    int dtype, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOTIF_HIP_H */

@@ -1,0 +1,124 @@
+'''GPU parity of apply_chord_attention (HIP kernels) against the fp64 CPU oracle.
+
+bf16 inputs; outputs within max-abs 2e-2 / mean-rel 5e-3 of the oracle.
+'''
+import pytest
+import torch
+
+from oracle import chord as ochord
+from support import assert_bf16_close, chord_inputs
+
+pytestmark = pytest.mark.gpu
+
+DEV = 'cuda'
+
+
+def _ops():
+    import motif.ops as ops
+    assert ops.HAS_TRITON, 'HIP library not loaded on a GPU box'
+    return ops
+
+
+def _run(ops, q, k, v, alpha, beta, mu, ssmax, log_n, q_start=None, scale=None):
+    dev = [t.to(DEV) for t in (q, k, v, alpha, beta, mu, ssmax, log_n)]
+    return ops.apply_chord_attention(*dev, q_start=q_start, softmax_scale=scale)
+
+
+def _log_n(B, L, q_start):
+    return ochord.log_n_table(q_start, L).float()[None].expand(B, L).contiguous()
+
+
+def _check_heads(out, q, k, v, alpha, beta, mu, ssmax, log_n, q_start, heads=None, what=''):
+    '''Compare selected heads (all by default) with the fp64 oracle.'''
+    H = q.shape[1]
+    Hkv = k.shape[1]
+    heads = range(H) if heads is None else heads
+    for h in heads:
+        kh = h // (H // Hkv)
+        ref = ochord.chord_attention(
+            q[:, h:h + 1], k[:, kh:kh + 1], v[:, kh:kh + 1], alpha[h:h + 1], beta[h:h + 1],
+            mu[h:h + 1], ssmax[h:h + 1], log_n, q_start)
+        assert_bf16_close(out[:, h:h + 1], ref, what=f'{what} head {h}')
+
+
+@pytest.mark.parametrize('Hkv', [12, 3])
+def test_prefill_config2_shape(Hkv):
+    '''Config 2 (B=2, H=12, T=2048, D=64, causal), checked on 3 heads against fp64.'''
+    ops = _ops()
+    B, H, L = 2, 12, 2048
+    q, k, v, alpha, beta, mu, ssmax = chord_inputs(B, H, Hkv, L, L, seed=0)
+    log_n = _log_n(B, L, 0)
+    out = _run(ops, q, k, v, alpha, beta, mu, ssmax, log_n, q_start=0)
+    assert out.dtype == torch.bfloat16 and out.shape == (B, H, L, 64)
+    _check_heads(out.cpu(), q, k, v, alpha, beta, mu, ssmax, log_n, 0, heads=[0, 5, 11], what='cfg2')
+
+
+@pytest.mark.parametrize('L', [1, 31, 77, 200])
+@pytest.mark.parametrize('Hkv', [4, 2, 1])
+def test_prefill_small_ragged(L, Hkv):
+    ops = _ops()
+    B, H = 2, 4
+    q, k, v, alpha, beta, mu, ssmax = chord_inputs(B, H, Hkv, L, L, seed=L + Hkv)
+    log_n = _log_n(B, L, 0)
+    out = _run(ops, q, k, v, alpha, beta, mu, ssmax, log_n, q_start=0)
+    _check_heads(out.cpu(), q, k, v, alpha, beta, mu, ssmax, log_n, 0, what=f'L={L}')
+
+
+def test_prefill_continuation_with_cache():
+    '''Chunked prefill: 100 new queries over a 300-key cache (q_start = 200 default).'''
+    ops = _ops()
+    B, H, Hkv, L, S = 1, 8, 2, 100, 300
+    q, k, v, alpha, beta, mu, ssmax = chord_inputs(B, H, Hkv, L, S, seed=3)
+    mu = torch.linspace(-2.0, 3.0, H)
+    ssmax = torch.linspace(0.5, 1.5, H)
+    log_n = _log_n(B, L, S - L)
+    out = _run(ops, q, k, v, alpha, beta, mu, ssmax, log_n)
+    _check_heads(out.cpu(), q, k, v, alpha, beta, mu, ssmax, log_n, S - L, what='cont')
+
+
+@pytest.mark.parametrize('B,S', [(4, 4097), (64, 1000), (2, 9)])
+def test_decode_split(B, S):
+    '''Decode: one query per sequence over an S-key cache, GQA 12:3 (split-K path).'''
+    ops = _ops()
+    H, Hkv = 12, 3
+    q, k, v, alpha, beta, mu, ssmax = chord_inputs(B, H, Hkv, 1, S, seed=S)
+    log_n = _log_n(B, 1, S - 1)
+    out = _run(ops, q, k, v, alpha, beta, mu, ssmax, log_n)
+    _check_heads(out.cpu(), q, k, v, alpha, beta, mu, ssmax, log_n, S - 1, what=f'decode B={B}')
+
+
+def test_decode_row_equals_last_prefill_row():
+    ops = _ops()
+    B, H, Hkv, S = 2, 12, 3, 700
+    q, k, v, alpha, beta, mu, ssmax = chord_inputs(B, H, Hkv, S, S, seed=8)
+    log_n = _log_n(B, S, 0)
+    full = _run(ops, q, k, v, alpha, beta, mu, ssmax, log_n, q_start=0)
+    last = _run(ops, q[:, :, -1:], k, v, alpha, beta, mu, ssmax, log_n[:, -1:].contiguous(), q_start=S - 1)
+    d = (full[:, :, -1:].float() - last.float()).abs().max().item()
+    assert d <= 2e-2, d
+
+
+def test_varlen_equals_independent_runs():
+    ops = _ops()
+    lens = [130, 1, 64, 257, 0, 40]
+    cu = torch.tensor([0] + list(torch.cumsum(torch.tensor(lens), 0)), dtype=torch.int32)
+    T = int(cu[-1])
+    H, Hkv = 12, 3
+    q, k, v, alpha, beta, mu, ssmax = chord_inputs(1, H, Hkv, T, T, seed=17)
+    log_n = torch.cat([ochord.log_n_table(0, n) for n in lens]).float()[None]
+    out = ops.apply_chord_attention_varlen(*(t.to(DEV) for t in (q, k, v, alpha, beta, mu, ssmax, log_n)), cu.to(DEV))
+    ref = ochord.chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, cu, softmax_scale=64 ** -0.5)
+    assert_bf16_close(out, ref, what='varlen')
+
+
+def test_validation_errors_match_reference_types():
+    ops = _ops()
+    q, k, v, alpha, beta, mu, ssmax = (t.to(DEV) for t in chord_inputs(1, 4, 2, 8, 8))
+    log_n = _log_n(1, 8, 0).to(DEV)
+    with pytest.raises(ValueError):
+        ops.apply_chord_attention(q, k, v, alpha, beta, mu, ssmax, log_n, q_start=-1)
+    with pytest.raises(ValueError):
+        ops.apply_chord_attention(q, k, v, alpha[:3], beta, mu, ssmax, log_n)
+    with pytest.raises(ValueError):
+        ops.apply_chord_attention(q, k[:, :1].expand(1, 3, 8, 64), v[:, :1].expand(1, 3, 8, 64),
+                                  alpha, beta, mu, ssmax, log_n)

@@ -1,0 +1,177 @@
+'''GPU parity of the GDN ops (HIP kernels through the C ABI) against the CPU oracle.
+
+Tolerances (from the measurement contract): fp32 inputs within 1e-4; bf16
+inputs within max-abs 2e-2 / mean-rel 5e-3 of the fp64 oracle; final
+recurrent state within relative error 1e-2 (bf16) or 1e-4 (fp32).
+'''
+import pytest
+import torch
+
+from oracle import gdn as ogdn
+from support import assert_bf16_close, assert_fp32_close, assert_state_close, gdn_inputs
+
+pytestmark = pytest.mark.gpu
+
+DEV = 'cuda'
+
+
+def _ops():
+    import motif.ops as ops
+    assert ops.HAS_TRITON, 'HIP library not loaded on a GPU box'
+    return ops
+
+
+def _oracle_rec(q, k, v, b, g, S=None):
+    return ogdn.recurrent(*(t.double() for t in (q, k, v, b, g)), None if S is None else S.double())
+
+
+def _oracle_chunk(q, k, v, b, g, S=None, C=64):
+    return ogdn.chunked(*(t.double() for t in (q, k, v, b, g)), None if S is None else S.double(), C)
+
+
+@pytest.mark.parametrize('dk,dv', [(64, 128), (64, 64), (32, 64), (128, 128)])
+def test_recurrent_fp32(dk, dv):
+    ops = _ops()
+    q, k, v, b, g = gdn_inputs(2, 3, 9, dk, dv, seed=1)
+    S0 = torch.randn(2, 3, dk, dv, generator=torch.Generator().manual_seed(5)) * 0.1
+    o, S = ops.recurrent_gated_delta_rule(*(t.to(DEV) for t in (q, k, v, b, g)), S0.to(DEV))
+    ro, rS = _oracle_rec(q, k, v, b, g, S0)
+    assert_fp32_close(o, ro, 1e-4, 'o')
+    assert_fp32_close(S, rS, 1e-4, 'S')
+
+
+def test_recurrent_bf16_decode_shape():
+    '''Config-4 GDN decode shape: one token, B=64, H=12, dk=64, dv=128, fp32 state.'''
+    ops = _ops()
+    q, k, v, b, g = gdn_inputs(64, 12, 1, 64, 128, seed=2, dtype=torch.bfloat16)
+    S0 = torch.randn(64, 12, 64, 128, generator=torch.Generator().manual_seed(3)) * 0.05
+    o, S = ops.recurrent_gated_delta_rule(*(t.to(DEV) for t in (q, k, v, b, g)), S0.to(DEV))
+    ro, rS = _oracle_rec(q, k, v, b, g, S0)
+    assert o.dtype == torch.bfloat16
+    assert_bf16_close(o, ro, what='o')
+    assert_state_close(S, rS, 1e-4, 'S')
+
+
+def test_recurrent_noncontiguous_layer_layout():
+    '''q/k/v as the layer produces them: [B, L, H, D] memory viewed as [B, H, L, D].'''
+    ops = _ops()
+    B, L, H, dk, dv = 2, 5, 4, 64, 128
+    gg = torch.Generator().manual_seed(7)
+    q = torch.nn.functional.normalize(torch.randn(B, L, H, dk, generator=gg), dim=-1).transpose(1, 2)
+    k = torch.nn.functional.normalize(torch.randn(B, L, H, dk, generator=gg), dim=-1).transpose(1, 2)
+    v = torch.randn(B, L, H, dv, generator=gg).transpose(1, 2)
+    b = torch.sigmoid(torch.randn(B, L, H, generator=gg)).transpose(1, 2)
+    g = torch.nn.functional.logsigmoid(torch.randn(B, L, H, generator=gg)).transpose(1, 2)
+    o, S = ops.recurrent_gated_delta_rule(*(t.to(DEV) for t in (q, k, v, b, g)))
+    ro, rS = _oracle_rec(q, k, v, b, g)
+    assert_fp32_close(o, ro, 1e-4, 'o')
+    assert_fp32_close(S, rS, 1e-4, 'S')
+
+
+@pytest.mark.parametrize('T', [256, 100, 1, 64, 130])
+def test_chunk_fp32_config1(T):
+    '''Config 1: B=1, H=4, dk=dv=64, chunk 64, fp32 (plus ragged lengths).'''
+    ops = _ops()
+    q, k, v, b, g = gdn_inputs(1, 4, T, 64, 64, seed=0)
+    o, S = ops.chunk_gated_delta_rule(*(t.to(DEV) for t in (q, k, v, b, g)), None, 64)
+    ro, rS = _oracle_chunk(q, k, v, b, g, None, 64)
+    assert_fp32_close(o, ro, 1e-4, 'o')
+    assert_fp32_close(S, rS, 1e-4, 'S')
+
+
+@pytest.mark.parametrize('C', [16, 32, 64])
+@pytest.mark.parametrize('dk,dv', [(64, 128), (128, 256), (32, 64)])
+def test_chunk_fp32_chunks_and_dims(C, dk, dv):
+    ops = _ops()
+    q, k, v, b, g = gdn_inputs(2, 2, 150, dk, dv, seed=C + dk)
+    S0 = torch.randn(2, 2, dk, dv, generator=torch.Generator().manual_seed(9)) * 0.1
+    o, S = ops.chunk_gated_delta_rule(*(t.to(DEV) for t in (q, k, v, b, g)), S0.to(DEV), C)
+    ro, rS = _oracle_rec(q, k, v, b, g, S0)
+    assert_fp32_close(o, ro, 1e-4, 'o')
+    assert_fp32_close(S, rS, 1e-4, 'S')
+
+
+def test_chunk_bf16_layer_shape():
+    '''bf16 inputs at the model's GDN shape (H=12, dk=64, dv=128), T=512.'''
+    ops = _ops()
+    q, k, v, b, g = gdn_inputs(1, 12, 512, 64, 128, seed=4, dtype=torch.bfloat16)
+    o, S = ops.chunk_gated_delta_rule(*(t.to(DEV) for t in (q, k, v, b, g)))
+    ro, rS = _oracle_chunk(q, k, v, b, g)
+    assert o.dtype == torch.bfloat16
+    assert_bf16_close(o, ro, what='o')
+    assert_state_close(S, rS, 1e-2, 'S')
+
+
+def test_chunk_triton_name_rejects_small_chunk():
+    ops = _ops()
+    q, k, v, b, g = (t.to(DEV) for t in gdn_inputs(1, 1, 8, 64, 64))
+    with pytest.raises(NotImplementedError):
+        ops.chunk_gated_delta_rule_triton(q, k, v, b, g, None, 8)
+
+
+def test_chunk_continuation_equals_full():
+    '''Running [0, t) then [t, T) from the carried state equals one run over [0, T).'''
+    ops = _ops()
+    q, k, v, b, g = (t.to(DEV) for t in gdn_inputs(1, 3, 300, 64, 128, seed=11))
+    o_full, S_full = ops.chunk_gated_delta_rule(q, k, v, b, g)
+    t = 173
+    o1, S1 = ops.chunk_gated_delta_rule(q[:, :, :t], k[:, :, :t], v[:, :, :t], b[:, :, :t], g[:, :, :t])
+    o2, S2 = ops.chunk_gated_delta_rule(q[:, :, t:], k[:, :, t:], v[:, :, t:], b[:, :, t:], g[:, :, t:], S1)
+    assert_fp32_close(torch.cat([o1, o2], 2), o_full, 1e-4, 'o')
+    assert_fp32_close(S2, S_full, 1e-4, 'S')
+
+
+def test_chunk_varlen_equals_independent_runs():
+    ops = _ops()
+    lens = [70, 1, 0, 200, 64, 33]
+    cu = torch.tensor([0] + list(torch.cumsum(torch.tensor(lens), 0)), dtype=torch.int32)
+    T = int(cu[-1])
+    q, k, v, b, g = gdn_inputs(1, 4, T, 64, 128, seed=13)
+    o, S = ops.chunk_gated_delta_rule_varlen(*(t.to(DEV) for t in (q, k, v, b, g)), cu.to(DEV))
+    ro, rS = ogdn.chunked_varlen(*(t.double() for t in (q, k, v, b, g)), cu)
+    assert_fp32_close(o, ro, 1e-4, 'o')
+    assert_fp32_close(S, rS, 1e-4, 'S')
+
+
+@pytest.mark.parametrize('cache', [False, True])
+@pytest.mark.parametrize('L', [1, 7, 200])
+def test_short_conv_silu(cache, L):
+    ops = _ops()
+    gg = torch.Generator().manual_seed(L)
+    B, D, K = 3, 96, 4
+    x = torch.randn(B, L, D, generator=gg)
+    w = torch.randn(D, 1, K, generator=gg) * 0.5
+    tail = torch.randn(B, D, K - 1, generator=gg) if cache else None
+    y, nt = ops.short_conv_silu(x.to(DEV), w.to(DEV), None if tail is None else tail.to(DEV))
+    ry, rt = ogdn.short_conv_silu(x.double(), w.double(), None if tail is None else tail.double())
+    assert_fp32_close(y, ry, 1e-5, 'y')
+    assert_fp32_close(nt, rt, 0.0, 'tail')
+
+
+def test_short_conv_silu_inplace_tail_bf16():
+    ops = _ops()
+    gg = torch.Generator().manual_seed(3)
+    B, D, K = 4, 1536, 4
+    x = torch.randn(B, 1, D, generator=gg).to(torch.bfloat16)
+    w = (torch.randn(D, 1, K, generator=gg) * 0.5).to(torch.bfloat16)
+    tail = torch.randn(B, D, K - 1, generator=gg).to(torch.bfloat16)
+    ry, rt = ogdn.short_conv_silu(x.double(), w.double(), tail.double())
+    tdev = tail.to(DEV)
+    y, nt = ops.short_conv_silu(x.to(DEV), w.to(DEV), tdev, new_cache=tdev)
+    assert nt.data_ptr() == tdev.data_ptr()
+    assert_bf16_close(y, ry, what='y')
+    assert torch.equal(nt.cpu().double(), rt)
+
+
+def test_short_conv_silu_varlen():
+    ops = _ops()
+    lens = [5, 0, 130, 2]
+    cu = torch.tensor([0] + list(torch.cumsum(torch.tensor(lens), 0)), dtype=torch.int32)
+    gg = torch.Generator().manual_seed(21)
+    D, K = 64, 4
+    x = torch.randn(1, int(cu[-1]), D, generator=gg)
+    w = torch.randn(D, 1, K, generator=gg)
+    y, tails = ops.short_conv_silu_varlen(x.to(DEV), w.to(DEV), cu.to(DEV))
+    ry, rt = ogdn.short_conv_silu_varlen(x.double(), w.double(), cu)
+    assert_fp32_close(y, ry, 1e-5, 'y')
+    assert_fp32_close(tails, rt, 0.0, 'tails')
