@@ -1,0 +1,324 @@
+'''Benchmark of Motif Chord's sequence-mixing hot path on one MI355X.
+
+Headline (value): config 3 -- full MotifChordModel forward at the 172M shape
+(d=768, 4 blocks x (3 GDN + 1 Chord), H=12, GDN dk=64 / dv=128, Chord D=64 /
+Hkv=3, SwiGLU 2048, vocab 32000), B=1, T=4096, bf16, random init
+(Linear / Embedding / Conv1d ~ N(0, 0.02), semantic parameters at their
+constructor values), uniform random token ids.  One step = one forward pass
+(logits included); value = tokens / s.
+
+Also reported in the same JSON line:
+- decode (config 4): one decode step at B=64 over a 4096-token context
+  (KV caches and recurrent states filled with random values; labelled), as a
+  captured hipGraph replayed K times;
+- per-kernel timings of the hot-path ops at the config-3/4 shapes with HIP
+  events on the launch stream, and the roofline of the dominant kernel;
+- cpu_baseline: this build's CPU restatement of the reference's PyTorch path
+  (oracle/, float32, torch threads) on one config-3 forward.
+
+Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu]
+'''
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, 'codon-motif_amd')):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = 'prefill tok/s @T=4096 + decode tok/s @B=64; % MFMA / HBM roofline (1 GPU)'
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def bench_config(vocab=32000):
+    from motif.model.config import MotifChordConfig
+    return MotifChordConfig(vocab_size=vocab, model_dim=768, num_heads=12, num_kv_heads=3,
+                            head_k_dim=64, block=('gdn', 'gdn', 'gdn', 'chord'), block_n=4)
+
+
+def init_model(model, std=0.02, seed=0):
+    import torch
+    import torch.nn as nn
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for m in model.modules():
+            if isinstance(m, (nn.Linear, nn.Embedding, nn.Conv1d)):
+                m.weight.copy_(torch.randn(m.weight.shape, generator=g) * std)
+    return model
+
+
+def cuda_time(fn, steps, warmup):
+    '''Average milliseconds of fn() over `steps` launches, HIP events on the current stream.'''
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def kernel_timings(dev):
+    '''Hot-path ops at the config-3 / config-4 shapes.'''
+    import torch
+    import torch.nn.functional as F
+
+    import motif.ops as ops
+    from motif.ops.gated_deltanet import gdn_recurrent_into
+    from oracle.chord import chord_prefill_flops
+    from oracle.gdn import gdn_prefill_flops
+
+    g = torch.Generator().manual_seed(0)
+    res = {}
+    B, H, T, dk, dv = 1, 12, 4096, 64, 128
+    q = F.normalize(torch.randn(B, T, H, dk, generator=g), dim=-1).transpose(1, 2).to(dev, torch.bfloat16)
+    k = F.normalize(torch.randn(B, T, H, dk, generator=g), dim=-1).transpose(1, 2).to(dev, torch.bfloat16)
+    v = torch.randn(B, T, H, dv, generator=g).transpose(1, 2).to(dev, torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g)).transpose(1, 2).to(dev, torch.bfloat16)
+    gg = F.logsigmoid(torch.randn(B, T, H, generator=g)).transpose(1, 2).to(dev, torch.bfloat16)
+    ms = cuda_time(lambda: ops.chunk_gated_delta_rule(q, k, v, beta, gg), 20, 3)
+    fl = gdn_prefill_flops(B, T, H, dk, dv)
+    res['gdn_chunk_prefill'] = dict(us=ms * 1e3, unit='TFLOP/s', achieved=fl / (ms * 1e-3) / 1e12,
+                                    peak=PEAK_BF16_TFLOPS, bound='mfma', work=fl,
+                                    shape='B=1 H=12 T=4096 dk=64 dv=128 bf16')
+
+    Hc, Hkv, D = 12, 3, 64
+    qc = (torch.randn(1, T, Hc, D, generator=g) * 0.5).transpose(1, 2).to(dev, torch.bfloat16)
+    kc = (torch.randn(1, T, Hkv, D, generator=g) * 0.5).transpose(1, 2).to(dev, torch.bfloat16)
+    vc = (torch.randn(1, T, Hkv, D, generator=g) * 0.5).transpose(1, 2).to(dev, torch.bfloat16)
+    al = (torch.randn(Hc, generator=g) * 0.1).to(dev)
+    be = (torch.randn(Hc, generator=g) * 0.1).to(dev)
+    mu = torch.zeros(Hc, device=dev)
+    ss = torch.ones(Hc, device=dev)
+    ln = torch.log(torch.arange(1, T + 1, dtype=torch.float32, device=dev))[None].contiguous()
+    ms = cuda_time(lambda: ops.apply_chord_attention(qc, kc, vc, al, be, mu, ss, ln, q_start=0), 20, 3)
+    fl = chord_prefill_flops(1, Hc, D, T)
+    res['chord_prefill'] = dict(us=ms * 1e3, unit='TFLOP/s', achieved=fl / (ms * 1e-3) / 1e12,
+                                peak=PEAK_BF16_TFLOPS, bound='mfma', work=fl,
+                                shape='B=1 H=12 Hkv=3 T=4096 D=64 bf16 causal')
+
+    Bd = 64
+    qd = F.normalize(torch.randn(Bd, H, 1, dk, generator=g), dim=-1).to(dev, torch.bfloat16)
+    kd = F.normalize(torch.randn(Bd, H, 1, dk, generator=g), dim=-1).to(dev, torch.bfloat16)
+    vd = torch.randn(Bd, H, 1, dv, generator=g).to(dev, torch.bfloat16)
+    bd = torch.sigmoid(torch.randn(Bd, H, 1, generator=g)).to(dev, torch.bfloat16)
+    gd = F.logsigmoid(torch.randn(Bd, H, 1, generator=g)).to(dev, torch.bfloat16)
+    S = (torch.randn(Bd, H, dk, dv, generator=g) * 0.05).to(dev)
+    od = torch.empty(Bd, H, 1, dv, device=dev, dtype=torch.bfloat16)
+    ms = cuda_time(lambda: gdn_recurrent_into(qd, kd, vd, bd, gd, S, S, od), 200, 10)
+    byts = Bd * H * dk * dv * 4 * 2 + Bd * H * (2 * dk + 2 * dv + 2) * 2
+    res['gdn_decode'] = dict(us=ms * 1e3, unit='GB/s', achieved=byts / (ms * 1e-3) / 1e9,
+                             peak=PEAK_HBM_GBS, bound='hbm', work=byts,
+                             shape='B=64 H=12 dk=64 dv=128 fp32 state, in place')
+
+    Sk = 4097
+    qk = (torch.randn(Bd, Hc, 1, D, generator=g) * 0.5).to(dev, torch.bfloat16)
+    kk = (torch.randn(Bd, Hkv, Sk, D, generator=g) * 0.5).to(dev, torch.bfloat16)
+    vk = (torch.randn(Bd, Hkv, Sk, D, generator=g) * 0.5).to(dev, torch.bfloat16)
+    lnd = torch.full((Bd, 1), float(torch.log(torch.tensor(float(Sk)))), device=dev)
+    ms = cuda_time(lambda: ops.apply_chord_attention(qk, kk, vk, al, be, mu, ss, lnd), 100, 5)
+    byts = 2 * Bd * Hkv * Sk * D * 2 + 2 * Bd * Hc * D * 2
+    res['chord_decode'] = dict(us=ms * 1e3, unit='GB/s', achieved=byts / (ms * 1e-3) / 1e9,
+                               peak=PEAK_HBM_GBS, bound='hbm', work=byts,
+                               shape='B=64 H=12 Hkv=3 S=4097 D=64 bf16 (split-K + merge)')
+    for r in res.values():
+        r['frac'] = r['achieved'] / r['peak']
+    return res
+
+
+def make_decode_cache(model, B, ctx, capacity, dev, dtype, seed=1):
+    '''Caches as after a ctx-token prefill, filled with random values (timing only).'''
+    import torch
+
+    from motif.model.cache import (DecoderBlockCache, GatedDeltaAttentionLayerCache, ModelCache,
+                                   StaticKVLayerCache)
+    g = torch.Generator().manual_seed(seed)
+    blocks = []
+    for block in model.blocks:
+        attn = []
+        for dec in block.features:
+            a = dec.attn
+            if dec.attn_type == 'chord':
+                c = StaticKVLayerCache().allocate(B, a.num_kv_heads, capacity, a.head_dim, dev, dtype)
+                c.k[:, :, :ctx].copy_((torch.randn(B, a.num_kv_heads, ctx, a.head_dim, generator=g) * 0.5).to(dtype))
+                c.v[:, :, :ctx].copy_((torch.randn(B, a.num_kv_heads, ctx, a.head_dim, generator=g) * 0.5).to(dtype))
+                c.length = ctx
+                c.length_dev.fill_(ctx)
+            else:
+                c = GatedDeltaAttentionLayerCache()
+                c.state = (torch.randn(B, a.num_heads, a.dk, a.dv, generator=g) * 0.05).to(dev)
+                c.conv_state = tuple((torch.randn(B, n, a.conv_size - 1, generator=g) * 0.5).to(dev, dtype)
+                                     for n in (a.num_heads * a.dk, a.num_heads * a.dk, a.num_heads * a.dv))
+                c.length = ctx
+            attn.append(c)
+        bc = DecoderBlockCache(attn=attn)
+        bc.attn_res.seq_len = ctx
+        bc.attn_res.blocks = [torch.zeros(B, 1, model.config.model_dim, device=dev, dtype=dtype)]
+        blocks.append(bc)
+    return ModelCache(blocks=blocks)
+
+
+def cpu_baseline(T=4096, seed=0):
+    '''One config-3 forward through the CPU oracle (float32), threads as configured.'''
+    import torch
+
+    from motif.model.motif import MotifChordModel
+    from oracle.model import OracleModel
+    cfg = bench_config()
+    model = init_model(MotifChordModel(cfg), seed=seed)
+    p = {k: v.detach().float() for k, v in model.state_dict().items()}
+    ocfg = dict(model_dim=cfg.model_dim, num_heads=cfg.num_heads, num_kv_heads=cfg.num_kv_heads,
+                head_k_dim=cfg.head_k_dim, block=cfg.block, block_n=cfg.block_n)
+    om = OracleModel(p, ocfg, dtype=torch.float32)
+    ids = torch.randint(0, cfg.vocab_size, (1, T), generator=torch.Generator().manual_seed(seed))
+    t0 = time.perf_counter()
+    with torch.no_grad():
+        om.forward(ids)
+    dt = time.perf_counter() - t0
+    cpu_model = ''
+    try:
+        with open('/proc/cpuinfo') as f:
+            for line in f:
+                if line.startswith('model name'):
+                    cpu_model = line.split(':', 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return dict(value=T / dt, unit='tok/s', cores=torch.get_num_threads(), kind='port',
+                sample=f'one config-3 forward (B=1, T={T}) through oracle/ (CPU restatement of the '
+                       f'reference torch path: chunk loop GDN, eager Chord), float32; {dt:.2f} s; '
+                       f'CPU: {cpu_model}')
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=10)
+    ap.add_argument('--warmup', type=int, default=3)
+    ap.add_argument('--no-cpu', action='store_true')
+    ap.add_argument('--seq', type=int, default=4096)
+    ap.add_argument('--decode-batch', type=int, default=64)
+    args = ap.parse_args()
+    world = int(os.environ.get('WORLD_SIZE', '1'))
+    if args.gpus != 1 or world != 1:
+        print(f'bench.py measures one GPU only (this build has no multi-GPU path); '
+              f'got --gpus {args.gpus}, WORLD_SIZE={world}', file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import motif.ops as ops
+    from motif.model.motif import MotifChordModel
+    if not ops.HAS_TRITON:
+        raise RuntimeError('HIP kernel library not loaded or no ROCm device visible')
+    dev = torch.device('cuda', 0)
+    torch.cuda.set_device(dev)
+    torch.backends.cuda.matmul.allow_tf32 = False
+
+    cfg = bench_config()
+    model = init_model(MotifChordModel(cfg)).to(dev, torch.bfloat16).eval()
+    T = args.seq
+    ids = torch.randint(0, cfg.vocab_size, (1, T), generator=torch.Generator().manual_seed(0)).to(dev)
+
+    log(f'[bench] prefill B=1 T={T}: warmup {args.warmup}, steps {args.steps}')
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            model(ids)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for _ in range(args.steps):
+            model(ids)
+        ev1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    ms_step = ev0.elapsed_time(ev1) / args.steps
+    prefill_tok_s = T / (ms_step * 1e-3)
+    log(f'[bench] prefill {ms_step:.2f} ms/step ({prefill_tok_s:.0f} tok/s, wall {wall:.2f} s)')
+
+    log('[bench] decode B=64 ctx=4096 (hipGraph)')
+    Bd, ctx = args.decode_batch, 4096
+    dec_model = model
+    cache = make_decode_cache(dec_model, Bd, ctx, ctx + 8, dev, torch.bfloat16)
+    tok = torch.randint(0, cfg.vocab_size, (Bd, 1), generator=torch.Generator().manual_seed(1)).to(dev)
+    lengths = [[c.length for c in b.attn] for b in cache.blocks]
+
+    def rewind():
+        for b, ls in zip(cache.blocks, lengths):
+            for c, n in zip(b.attn, ls):
+                c.length = n
+            b.attn_res.seq_len = ctx
+
+    with torch.no_grad():
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                rewind()
+                dec_model(tok, cache=cache)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        rewind()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = dec_model(tok, cache=cache)
+        rewind()
+        dec_ms = cuda_time(graph.replay, max(args.steps * 5, 20), 3)
+    decode_tok_s = Bd / (dec_ms * 1e-3)
+    log(f'[bench] decode {dec_ms:.3f} ms/step ({decode_tok_s:.0f} tok/s)')
+    del out, graph
+
+    log('[bench] kernel timings')
+    with torch.no_grad():
+        kern = kernel_timings(dev)
+    for name, r in kern.items():
+        log(f'[bench]   {name}: {r["us"]:.1f} us, {r["achieved"]:.1f} {r["unit"]} ({100 * r["frac"]:.1f}% of peak)')
+    # the dominant prefill kernel: the one that takes the most time per forward
+    per_fwd = {'gdn_chunk_prefill': kern['gdn_chunk_prefill']['us'] * 12,
+               'chord_prefill': kern['chord_prefill']['us'] * 4}
+    dom = max(per_fwd, key=per_fwd.get)
+    r = kern[dom]
+    roofline = dict(kernel=dom, bound=r['bound'], achieved=round(r['achieved'], 3), peak=r['peak'],
+                    unit=r['unit'], frac=round(r['frac'], 5), traffic=None, avg_us=round(r['us'], 2),
+                    work_per_launch=r['work'], shape=r['shape'])
+
+    cpu = None
+    if not args.no_cpu:
+        log('[bench] cpu baseline (oracle, float32, one T=4096 forward)')
+        cpu = cpu_baseline(T)
+        log(f'[bench] cpu {cpu["value"]:.1f} tok/s on {cpu["cores"]} threads')
+
+    line = {
+        'metric': METRIC, 'value': round(prefill_tok_s, 1), 'unit': 'tok/s', 'n_gpus': 1,
+        'steps': args.steps, 'warmup': args.warmup, 'ms_per_step': round(ms_step, 4),
+        'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16',
+        'data': 'synthetic (uniform random ids; random-init weights of the 172M-shape architecture)',
+        'config': {'workload': 'config 3: MotifChordModel forward, d=768, 4x(3 GDN + 1 Chord), H=12, '
+                               'GDN dk=64 dv=128, Chord D=64 Hkv=3, vocab 32000, B=1, T=4096, bf16',
+                   'global_batch': 1, 'seq_len': T, 'parallelism': 'single GPU'},
+        'decode': {'tok_s': round(decode_tok_s, 1), 'ms_per_step': round(dec_ms, 4), 'batch': Bd,
+                   'context': ctx, 'note': 'config 4: one hipGraph-captured decode step replayed; '
+                                           'caches random-filled to 4096 positions (timing only)'},
+        'roofline': roofline,
+        'kernels': {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                    for k, v in kern.items()},
+        'cpu_baseline': cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == '__main__':
+    main()

@@ -28,19 +28,20 @@
 namespace motif {
 
 struct ChordArgs {
-  const bf16_t *q; int64_t q_sb, q_sh, q_st;
-  const bf16_t *k; int64_t k_sb, k_sh, k_st;
-  const bf16_t *v; int64_t v_sb, v_sh, v_st;
+  const void *q; int64_t q_sb, q_sh, q_st;
+  const void *k; int64_t k_sb, k_sh, k_st;
+  const void *v; int64_t v_sb, v_sh, v_st;
   const float *alpha, *beta, *mu, *ssmax;
   const float *log_n; int64_t ln_sb, ln_st;
-  bf16_t *out; int64_t o_sb, o_sh, o_st;
+  void *out; int64_t o_sb, o_sh, o_st;
   float *lse;
   int B, H, Hkv, L, S, q_start;
   float scale, eps;
   const int32_t *cu;  // packed sequences (B == 1) or nullptr
   // split-K partials
-  float *part;        // [B][Hkv][splits][R][D + 2]
-  int splits, rows;   // rows = group * L (decode kernel)
+  float *part;        // [B][Hkv][splits][L * group][D + 2]
+  int splits;         // key-range splits (decode kernel)
+  int nqc;            // row chunks per (batch, kv head) (decode kernel)
 };
 
 constexpr int kD = 64;        // head dim
@@ -93,9 +94,9 @@ __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
   const int wave_first_qabs = q_start + q0;
   const int wave_kv_end = min(Skv, q_start + min(Lq, q0 + 32));
 
-  const bf16_t *qp = a.q + batch * a.q_sb + head * a.q_sh + int64_t(tok0) * a.q_st;
-  const bf16_t *kp = a.k + batch * a.k_sb + kvh * a.k_sh + int64_t(tok0) * a.k_st;
-  const bf16_t *vp = a.v + batch * a.v_sb + kvh * a.v_sh + int64_t(tok0) * a.v_st;
+  const bf16_t *qp = static_cast<const bf16_t *>(a.q) + batch * a.q_sb + head * a.q_sh + int64_t(tok0) * a.q_st;
+  const bf16_t *kp = static_cast<const bf16_t *>(a.k) + batch * a.k_sb + kvh * a.k_sh + int64_t(tok0) * a.k_st;
+  const bf16_t *vp = static_cast<const bf16_t *>(a.v) + batch * a.v_sb + kvh * a.v_sh + int64_t(tok0) * a.v_st;
 
   __shared__ __attribute__((aligned(16))) bf16_t sK[2][kBN][kKStride];
   __shared__ __attribute__((aligned(16))) bf16_t sVt[2][kD][kVStride];
@@ -243,7 +244,7 @@ __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
 
   if (q_valid) {
     const float inv = 1.f / fmaxf(l_run, 1e-20f);
-    bf16_t *op = a.out + batch * a.o_sb + head * a.o_sh + int64_t(tok0 + my_q) * a.o_st;
+    bf16_t *op = static_cast<bf16_t *>(a.out) + batch * a.o_sb + head * a.o_sh + int64_t(tok0 + my_q) * a.o_st;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -262,30 +263,79 @@ __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
 }
 
 // ------------------------------------------------------------------ decode
-template <int R>  // query rows served per workgroup (GQA group x L)
+// 8 consecutive features of one row as floats (16-byte loads).
+template <typename T> __device__ __forceinline__ void load8(const T *p, float out[8]);
+template <> __device__ __forceinline__ void load8<bf16_t>(const bf16_t *p, float out[8]) {
+  const uint4 raw = *reinterpret_cast<const uint4 *>(p);
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    out[2 * e] = __uint_as_float(w[e] << 16);
+    out[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+  }
+}
+template <> __device__ __forceinline__ void load8<float>(const float *p, float out[8]) {
+  const float4 x = *reinterpret_cast<const float4 *>(p), y = *reinterpret_cast<const float4 *>(p + 4);
+  out[0] = x.x; out[1] = x.y; out[2] = x.z; out[3] = x.w;
+  out[4] = y.x; out[5] = y.y; out[6] = y.z; out[7] = y.w;
+}
+
+// 8 raw features of one K / V row kept packed in registers until use.
+template <typename T> struct Row8;
+template <> struct Row8<bf16_t> {
+  uint4 r;
+  __device__ __forceinline__ void load(const bf16_t *p) { r = *reinterpret_cast<const uint4 *>(p); }
+  __device__ __forceinline__ void zero() { r = uint4{0, 0, 0, 0}; }
+  __device__ __forceinline__ float get(int e) const {
+    const uint32_t w = e < 2 ? r.x : e < 4 ? r.y : e < 6 ? r.z : r.w;
+    return (e & 1) ? __uint_as_float(w & 0xffff0000u) : __uint_as_float(w << 16);
+  }
+};
+template <> struct Row8<float> {
+  float4 x, y;
+  __device__ __forceinline__ void load(const float *p) {
+    x = *reinterpret_cast<const float4 *>(p);
+    y = *reinterpret_cast<const float4 *>(p + 4);
+  }
+  __device__ __forceinline__ void zero() { x = y = float4{0.f, 0.f, 0.f, 0.f}; }
+  __device__ __forceinline__ float get(int e) const {
+    const float4 &h = e < 4 ? x : y;
+    const int i = e & 3;
+    return i == 0 ? h.x : i == 1 ? h.y : i == 2 ? h.z : h.w;
+  }
+};
+
+// Rows of a workgroup: global row gr = qc * R + r over the L * group (query,
+// head) pairs of one kv head, query i = gr / group, head = kvh * group + gr % group.
+template <typename T, int R>
 __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int split = blockIdx.x, kvh = blockIdx.y;
+  const int b = blockIdx.z / a.nqc, qc = blockIdx.z % a.nqc;
   const int group = a.H / a.Hkv;
+  const int total_rows = a.L * group;
   const int dc = (lane & 7) * 8;  // this lane's 8 feature columns
   const int ksub = lane >> 3;     // key within an 8-key row group
+  const T *qg = static_cast<const T *>(a.q);
+  const T *kg = static_cast<const T *>(a.k);
+  const T *vg = static_cast<const T *>(a.v);
+  T *og = static_cast<T *>(a.out);
 
   const int kv_len = min(a.S, a.q_start + a.L);
   const int per = ((kv_len + a.splits - 1) / a.splits + kBN - 1) / kBN * kBN;
-  const int k_lo = split * per, k_hi = min(kv_len, k_lo + per);
+  const int i_last = min(a.L - 1, (qc * R + R - 1) / group);
+  const int k_lo = split * per;
+  const int k_hi = min(min(kv_len, k_lo + per), a.q_start + i_last + 1);
 
   float q[R][8], c_qk[R], c_b[R], al[R], be[R], mu[R];
   int qabs[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const bool ok = r < a.rows;
-    const int head = kvh * group + (ok ? r % group : 0);
-    const int i = ok ? r / group : 0;
-    const bf16_t *qp = a.q + b * a.q_sb + head * a.q_sh + int64_t(i) * a.q_st + dc;
-    const uint4 raw = *reinterpret_cast<const uint4 *>(qp);
-    const bf16_t *qb = reinterpret_cast<const bf16_t *>(&raw);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) q[r][e] = ok ? bf16_to_f32(qb[e]) : 0.f;
+    const int gr = qc * R + r;
+    const bool ok = gr < total_rows;
+    const int head = kvh * group + (ok ? gr % group : 0);
+    const int i = ok ? gr / group : 0;
+    load8(qg + b * a.q_sb + head * a.q_sh + int64_t(i) * a.q_st + dc, q[r]);
     const float mul = ok ? a.ssmax[head] * a.log_n[b * a.ln_sb + int64_t(i) * a.ln_st] : 0.f;
     c_qk[r] = mul * a.scale * kLog2e;
     c_b[r] = mul * kLog2e;
@@ -301,30 +351,30 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a) {
     for (int e = 0; e < 8; ++e) acc[r][e] = 0.f;
   }
 
-  const bf16_t *kp = a.k + b * a.k_sb + kvh * a.k_sh + dc;
-  const bf16_t *vp = a.v + b * a.v_sb + kvh * a.v_sh + dc;
+  const T *kp = kg + b * a.k_sb + kvh * a.k_sh + dc;
+  const T *vp = vg + b * a.v_sb + kvh * a.v_sh + dc;
 
   for (int n0 = k_lo + w * kBN; n0 < k_hi; n0 += 4 * kBN) {
-    uint4 kr[8], vr[8];
+    Row8<T> kf[8], vf[8];
 #pragma unroll
     for (int it = 0; it < 8; ++it) {
       const int key = n0 + 8 * it + ksub;
-      const bool ok = key < k_hi;
-      kr[it] = ok ? *reinterpret_cast<const uint4 *>(kp + int64_t(key) * a.k_st) : uint4{0, 0, 0, 0};
-      vr[it] = ok ? *reinterpret_cast<const uint4 *>(vp + int64_t(key) * a.v_st) : uint4{0, 0, 0, 0};
+      if (key < k_hi) {
+        kf[it].load(kp + int64_t(key) * a.k_st);
+        vf[it].load(vp + int64_t(key) * a.v_st);
+      } else {
+        kf[it].zero();
+        vf[it].zero();
+      }
     }
     float s[R][8];
 #pragma unroll
     for (int it = 0; it < 8; ++it) {
-      const bf16_t *kb = reinterpret_cast<const bf16_t *>(&kr[it]);
-      float kf[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) kf[e] = bf16_to_f32(kb[e]);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         float d = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) d = fmaf(q[r][e], kf[e], d);
+        for (int e = 0; e < 8; ++e) d = fmaf(q[r][e], kf[it].get(e), d);
         d += __shfl_xor(d, 1, 64);
         d += __shfl_xor(d, 2, 64);
         d += __shfl_xor(d, 4, 64);
@@ -365,15 +415,11 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a) {
       for (int e = 0; e < 8; ++e) acc[r][e] *= resc;
     }
 #pragma unroll
-    for (int it = 0; it < 8; ++it) {
-      const bf16_t *vb = reinterpret_cast<const bf16_t *>(&vr[it]);
+    for (int it = 0; it < 8; ++it)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float vf = bf16_to_f32(vb[e]);
+      for (int e = 0; e < 8; ++e)
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r][e] = fmaf(s[r][it], vf, acc[r][e]);
-      }
-    }
+        for (int r = 0; r < R; ++r) acc[r][e] = fmaf(s[r][it], vf[it].get(e), acc[r][e]);
   }
 
   // Finish the per-wave accumulators (sum over the 8 key sub-rows).
@@ -403,47 +449,50 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a) {
   __syncthreads();
   for (int e = tid; e < R * kD; e += 256) {
     const int r = e / kD, d = e % kD;
-    if (r >= a.rows) continue;
+    const int gr = qc * R + r;
+    if (gr >= total_rows) continue;
     float M = -INFINITY;
 #pragma unroll
     for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, sm[ww][r]);
     const float Mu = M == -INFINITY ? 0.f : M;
-    float o = 0.f, L = 0.f;
+    float o = 0.f, Ls = 0.f;
 #pragma unroll
     for (int ww = 0; ww < 4; ++ww) {
       const float f = fast_exp2(sm[ww][r] - Mu);
       o += sacc[ww][r][d] * f;
-      L += sl[ww][r] * f;
+      Ls += sl[ww][r] * f;
     }
     if (a.splits == 1) {
-      const int head = kvh * group + r % group, i = r / group;
-      a.out[b * a.o_sb + head * a.o_sh + int64_t(i) * a.o_st + d] = f32_to_bf16(o / fmaxf(L, 1e-20f));
-      if (a.lse && d == 0) a.lse[(static_cast<size_t>(b) * a.H + head) * a.L + i] = M + fast_log2(L);
+      const int head = kvh * group + gr % group, i = gr / group;
+      st(og + b * a.o_sb + head * a.o_sh + int64_t(i) * a.o_st + d, o / fmaxf(Ls, 1e-20f));
+      if (a.lse && d == 0) a.lse[(static_cast<size_t>(b) * a.H + head) * a.L + i] = M + fast_log2(Ls);
     } else {
-      float *pp = a.part + ((((static_cast<size_t>(b) * a.Hkv + kvh) * a.splits + split) * a.rows + r) * (kD + 2));
+      float *pp = a.part + ((((static_cast<size_t>(b) * a.Hkv + kvh) * a.splits + split) * total_rows + gr) * (kD + 2));
       pp[d] = o;
-      if (d == 0) { pp[kD] = M; pp[kD + 1] = L; }
+      if (d == 0) { pp[kD] = M; pp[kD + 1] = Ls; }
     }
   }
 }
 
+template <typename T>
 __global__ void __launch_bounds__(64) chord_merge_kernel(ChordArgs a) {
-  const int r = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, d = threadIdx.x;
+  const int gr = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, d = threadIdx.x;
   const int group = a.H / a.Hkv;
-  const float *pp = a.part + (((static_cast<size_t>(b) * a.Hkv + kvh) * a.splits) * a.rows + r) * (kD + 2);
-  const size_t sstride = static_cast<size_t>(a.rows) * (kD + 2);
+  const int total_rows = a.L * group;
+  const float *pp = a.part + (((static_cast<size_t>(b) * a.Hkv + kvh) * a.splits) * total_rows + gr) * (kD + 2);
+  const size_t sstride = static_cast<size_t>(total_rows) * (kD + 2);
   float M = -INFINITY;
   for (int s = 0; s < a.splits; ++s) M = fmaxf(M, pp[s * sstride + kD]);
   const float Mu = M == -INFINITY ? 0.f : M;
-  float o = 0.f, L = 0.f;
+  float o = 0.f, Ls = 0.f;
   for (int s = 0; s < a.splits; ++s) {
     const float f = fast_exp2(pp[s * sstride + kD] - Mu);
     o += pp[s * sstride + d] * f;
-    L += pp[s * sstride + kD + 1] * f;
+    Ls += pp[s * sstride + kD + 1] * f;
   }
-  const int head = kvh * group + r % group, i = r / group;
-  a.out[b * a.o_sb + head * a.o_sh + int64_t(i) * a.o_st + d] = f32_to_bf16(o / fmaxf(L, 1e-20f));
-  if (a.lse && d == 0) a.lse[(static_cast<size_t>(b) * a.H + head) * a.L + i] = M + fast_log2(L);
+  const int head = kvh * group + gr % group, i = gr / group;
+  st(static_cast<T *>(a.out) + b * a.o_sb + head * a.o_sh + int64_t(i) * a.o_st + d, o / fmaxf(Ls, 1e-20f));
+  if (a.lse && d == 0) a.lse[(static_cast<size_t>(b) * a.H + head) * a.L + i] = M + fast_log2(Ls);
 }
 
 // ------------------------------------------------------------------ planning
@@ -456,24 +505,26 @@ static int device_cu_count() {
 
 constexpr int kDecodeMaxRows = 8;
 
+// Short query blocks over a long cache take the split-K vector kernel.
 static bool use_decode(int H, int Hkv, int L, bool packed) {
   return !packed && (H / Hkv) * L <= kDecodeMaxRows;
 }
 
-static int decode_splits(int B, int Hkv, int L, int S, int q_start_hint) {
-  (void)q_start_hint;
+static int decode_splits(int B, int Hkv, int S) {
   const int kv_len = std::max(1, S);
-  const int cus = device_cu_count();
   const int base = std::max(1, B * Hkv);
-  int want = (2 * cus + base - 1) / base;                   // ~2 workgroups per CU
+  int want = (2 * device_cu_count() + base - 1) / base;       // ~2 workgroups per CU
   want = std::min(want, (kv_len + 4 * kBN - 1) / (4 * kBN));  // >= one 64-key tile per wave
-  (void)L;
   return std::max(1, std::min(want, 32));
 }
 
-template <int R>
-static void launch_decode_r(const ChordArgs &a, hipStream_t s) {
-  chord_decode_kernel<R><<<dim3(a.splits, a.Hkv, a.B), dim3(256), 0, s>>>(a);
+template <typename T>
+static void launch_decode(const ChordArgs &a, int R, hipStream_t s) {
+  const dim3 grid(a.splits, a.Hkv, a.B * a.nqc), block(256);
+  if (R <= 1) chord_decode_kernel<T, 1><<<grid, block, 0, s>>>(a);
+  else if (R <= 2) chord_decode_kernel<T, 2><<<grid, block, 0, s>>>(a);
+  else if (R <= 4) chord_decode_kernel<T, 4><<<grid, block, 0, s>>>(a);
+  else chord_decode_kernel<T, 8><<<grid, block, 0, s>>>(a);
 }
 
 }  // namespace motif
@@ -483,7 +534,7 @@ using namespace motif;
 extern "C" size_t motif_chord_workspace_bytes(int B, int H, int Hkv, int L, int S, int D, int *splits) {
   int sp = 1;
   if (B > 0 && H > 0 && Hkv > 0 && H % Hkv == 0 && L > 0 && use_decode(H, Hkv, L, false))
-    sp = decode_splits(B, Hkv, L, S, 0);
+    sp = decode_splits(B, Hkv, S);
   if (splits) *splits = sp;
   if (sp <= 1) return 0;
   const size_t rows = static_cast<size_t>(H / Hkv) * L;
@@ -507,50 +558,59 @@ extern "C" int motif_chord_fwd(
     return set_error(MOTIF_ERR_INVALID, "chord_fwd: bad size or negative q_start");
   if (H % Hkv != 0) return set_error(MOTIF_ERR_INVALID, "chord_fwd: H must be a multiple of Hkv");
   if (D != kD) return set_error(MOTIF_ERR_UNSUPPORTED, "chord_fwd: head_dim must be 64");
-  if (dtype != MOTIF_BF16) return set_error(MOTIF_ERR_UNSUPPORTED, "chord_fwd: only bf16 is implemented");
+  if (dtype != MOTIF_BF16 && dtype != MOTIF_F32)
+    return set_error(MOTIF_ERR_UNSUPPORTED, "chord_fwd: dtype must be bf16 or fp32");
   const bool packed = cu_seqlens != nullptr;
   if (packed && (B != 1 || nseq <= 0 || L != S))
     return set_error(MOTIF_ERR_INVALID, "chord_fwd: packed sequences need B == 1, nseq > 0 and L == S");
+  if (packed && dtype != MOTIF_BF16)
+    return set_error(MOTIF_ERR_UNSUPPORTED, "chord_fwd: packed sequences are implemented for bf16");
   if (!packed && nseq != B) return set_error(MOTIF_ERR_INVALID, "chord_fwd: nseq must equal B");
   if (B == 0 || L == 0) return MOTIF_OK;
   if (!q || !k || !v || !alpha || !beta || !mu || !ssmax || !log_n || !out)
     return set_error(MOTIF_ERR_INVALID, "chord_fwd: NULL pointer");
-  if (((q_st | k_st | v_st | o_st | q_sh | k_sh | v_sh | o_sh | q_sb | k_sb | v_sb | o_sb) & 7) != 0 ||
+  const int64_t vec = dtype == MOTIF_BF16 ? 8 : 4;  // elements per 16 bytes
+  if (((q_st | k_st | v_st | o_st | q_sh | k_sh | v_sh | o_sh | q_sb | k_sb | v_sb | o_sb) % vec) != 0 ||
       ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
         reinterpret_cast<uintptr_t>(out)) & 15) != 0)
-    return set_error(MOTIF_ERR_UNSUPPORTED, "chord_fwd: q/k/v/out need 16-byte aligned rows (strides multiple of 8)");
+    return set_error(MOTIF_ERR_UNSUPPORTED, "chord_fwd: q/k/v/out need 16-byte aligned rows");
 
   ChordArgs a;
-  a.q = static_cast<const bf16_t *>(q); a.q_sb = q_sb; a.q_sh = q_sh; a.q_st = q_st;
-  a.k = static_cast<const bf16_t *>(k); a.k_sb = k_sb; a.k_sh = k_sh; a.k_st = k_st;
-  a.v = static_cast<const bf16_t *>(v); a.v_sb = v_sb; a.v_sh = v_sh; a.v_st = v_st;
+  a.q = q; a.q_sb = q_sb; a.q_sh = q_sh; a.q_st = q_st;
+  a.k = k; a.k_sb = k_sb; a.k_sh = k_sh; a.k_st = k_st;
+  a.v = v; a.v_sb = v_sb; a.v_sh = v_sh; a.v_st = v_st;
   a.alpha = alpha; a.beta = beta; a.mu = mu; a.ssmax = ssmax;
   a.log_n = log_n; a.ln_sb = ln_sb; a.ln_st = ln_st;
-  a.out = static_cast<bf16_t *>(out); a.o_sb = o_sb; a.o_sh = o_sh; a.o_st = o_st;
+  a.out = out; a.o_sb = o_sb; a.o_sh = o_sh; a.o_st = o_st;
   a.lse = lse;
   a.B = B; a.H = H; a.Hkv = Hkv; a.L = L; a.S = S; a.q_start = q_start;
   a.scale = scale; a.eps = eps;
   a.cu = cu_seqlens;
-  a.part = nullptr; a.splits = 1; a.rows = (H / Hkv) * L;
+  a.part = nullptr; a.splits = 1; a.nqc = 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int group = H / Hkv;
+  const int rows = group * L;
 
-  if (use_decode(H, Hkv, L, packed)) {
+  if (dtype == MOTIF_F32 || use_decode(H, Hkv, L, packed)) {
     if (S == 0) return set_error(MOTIF_ERR_INVALID, "chord_fwd: empty key cache");
-    a.splits = decode_splits(B, Hkv, L, S, q_start);
+    int R = 8;
+    if (rows <= 8) {
+      R = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
+      a.splits = decode_splits(B, Hkv, S);
+    }
+    a.nqc = (rows + R - 1) / R;
     if (a.splits > 1) {
       const size_t need = motif_chord_workspace_bytes(B, H, Hkv, L, S, D, nullptr);
       if (!workspace || workspace_bytes < need)
         return set_error(MOTIF_ERR_INVALID, "chord_fwd: workspace too small (need " + std::to_string(need) + " bytes)");
       a.part = static_cast<float *>(workspace);
     }
-    if (a.rows <= 1) launch_decode_r<1>(a, s);
-    else if (a.rows <= 2) launch_decode_r<2>(a, s);
-    else if (a.rows <= 4) launch_decode_r<4>(a, s);
-    else launch_decode_r<8>(a, s);
+    if (dtype == MOTIF_BF16) launch_decode<bf16_t>(a, R, s);
+    else launch_decode<float>(a, R, s);
     int rc = check_launch("chord_decode_kernel");
     if (rc || a.splits == 1) return rc;
-    chord_merge_kernel<<<dim3(a.rows, Hkv, B), dim3(64), 0, s>>>(a);
+    if (dtype == MOTIF_BF16) chord_merge_kernel<bf16_t><<<dim3(rows, Hkv, B), dim3(64), 0, s>>>(a);
+    else chord_merge_kernel<float><<<dim3(rows, Hkv, B), dim3(64), 0, s>>>(a);
     return check_launch("chord_merge_kernel");
   }
 

@@ -1,0 +1,154 @@
+'''GatedDeltaAttention with the reference interface (motif/block/attention/gdn_attn.py:19-219).
+
+Same constructor arguments, parameter names / shapes / initialisation, cache
+type and forward contract.  The sequence mixing runs on the HIP kernels:
+short conv + SiLU (motif_short_conv_silu), then the delta rule
+(motif_gdn_recurrent_fwd for L == 1, motif_gdn_chunk_fwd otherwise).  The
+projections, L2 normalisation, gates, GatedRMSNorm and o_proj stay in
+PyTorch-ROCm.
+
+Precision: the reference casts q/k/v/beta/g to fp32 before the delta rule
+(:197).  Those tensors are produced in the activation dtype, so casting is
+exact; this layer hands them to the kernel in that dtype and the kernel
+computes in fp32 with an fp32 state, which yields the same inputs to the
+recurrence.  The returned state is fp32.
+'''
+import math
+from typing import Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from motif.block.attention.base import AttentionOutput, BasicAttention
+from motif.model.cache import GatedDeltaAttentionLayerCache
+from motif.ops import (
+    GatedRMSNorm,
+    HAS_TRITON,
+    chunk_gated_delta_rule,
+    recurrent_gated_delta_rule,
+    short_conv_silu,
+    short_conv_silu_varlen,
+    chunk_gated_delta_rule_varlen,
+)
+
+
+class GatedDeltaAttention(BasicAttention):
+    '''Gated delta-net attention (GDN) layer.'''
+
+    def __init__(
+        self,
+        hidden_size: int,
+        num_heads: int,
+        head_k_dim: Optional[int] = None,
+        expand_v: float = 2.0,
+        conv_size: int = 4,
+        chunk_size: int = 64,
+        bias: bool = False,
+        dropout: float = 0.0,
+        use_triton: bool = True,
+        **kwargs,
+    ):
+        super().__init__(hidden_size=hidden_size, num_heads=num_heads, num_kv_heads=num_heads)
+        self.dk = head_k_dim or self.head_dim
+        self.dv = int(self.dk * expand_v)
+        self.conv_size = conv_size
+        self.chunk_size = chunk_size
+        self.bias = bias
+        self.dropout = dropout
+        self.use_triton = bool(use_triton and HAS_TRITON)
+        dk_all = self.num_heads * self.dk
+        dv_all = self.num_heads * self.dv
+
+        self.q_proj = nn.Linear(hidden_size, dk_all, bias=bias)
+        self.k_proj = nn.Linear(hidden_size, dk_all, bias=bias)
+        self.v_proj = nn.Linear(hidden_size, dv_all, bias=bias)
+        self.a_proj = nn.Linear(hidden_size, self.num_heads, bias=bias)
+        self.b_proj = nn.Linear(hidden_size, self.num_heads, bias=bias)
+        self.g_proj = nn.Linear(hidden_size, dv_all, bias=bias)
+        self.o_proj = nn.Linear(dv_all, hidden_size, bias=bias)
+
+        self.q_conv = nn.Conv1d(dk_all, dk_all, conv_size, groups=dk_all, bias=False)
+        self.k_conv = nn.Conv1d(dk_all, dk_all, conv_size, groups=dk_all, bias=False)
+        self.v_conv = nn.Conv1d(dv_all, dv_all, conv_size, groups=dv_all, bias=False)
+
+        # A ~ U(1, 16); dt log-uniform in [1e-3, 1e-1] stored as softplus^-1(dt).
+        A = torch.empty(self.num_heads).uniform_(1, 16)
+        self.A_log = nn.Parameter(A.log())
+        dt = torch.exp(torch.rand(self.num_heads) * (math.log(0.1) - math.log(0.001)) + math.log(0.001))
+        self.dt_bias = nn.Parameter(dt + torch.log(-torch.expm1(-dt)))
+
+        self.o_norm = GatedRMSNorm(self.dv)
+
+    @classmethod
+    def cache_type(cls) -> type:
+        return GatedDeltaAttentionLayerCache
+
+    def _gates(self, hidden_states):
+        beta = torch.sigmoid(self.b_proj(hidden_states)).transpose(1, 2)
+        g = -self.A_log.exp() * F.softplus(self.a_proj(hidden_states) + self.dt_bias)
+        return beta, g.transpose(1, 2)
+
+    def _heads(self, q, k, v, B, L):
+        q = q.view(B, L, self.num_heads, self.dk).transpose(1, 2)
+        k = k.view(B, L, self.num_heads, self.dk).transpose(1, 2)
+        v = v.view(B, L, self.num_heads, self.dv).transpose(1, 2)
+        q = F.normalize(q, dim=-1) * (self.dk ** -0.5)
+        k = F.normalize(k, dim=-1)
+        return q, k, v
+
+    def _output(self, o, hidden_states, B, L):
+        o = o.to(hidden_states.dtype).transpose(1, 2)
+        gate = self.g_proj(hidden_states).view(B, L, self.num_heads, self.dv)
+        o = self.o_norm(torch.cat([o, gate.to(o.dtype)], dim=-1)).reshape(B, L, -1)
+        return self.o_proj(o)
+
+    def forward(self, hidden_states: torch.Tensor, past_key_value=None) -> AttentionOutput:
+        '''Run the layer over [B, L, hidden]; continue from / update `past_key_value`.'''
+        B, L, _ = hidden_states.shape
+        use_cache = past_key_value is not None
+        if use_cache:
+            if not isinstance(past_key_value, GatedDeltaAttentionLayerCache):
+                raise TypeError(f'GatedDeltaAttention requires GatedDeltaAttentionLayerCache, '
+                                f'got {type(past_key_value).__name__}')
+            tails = past_key_value.conv_state if past_key_value.conv_state is not None else (None, None, None)
+            S0 = past_key_value.state
+        else:
+            tails = (None, None, None)
+            S0 = None
+
+        q, cq = short_conv_silu(self.q_proj(hidden_states), self.q_conv.weight, tails[0])
+        k, ck = short_conv_silu(self.k_proj(hidden_states), self.k_conv.weight, tails[1])
+        v, cv = short_conv_silu(self.v_proj(hidden_states), self.v_conv.weight, tails[2])
+        q, k, v = self._heads(q, k, v, B, L)
+        beta, g = self._gates(hidden_states)
+
+        if L == 1:
+            o, S = recurrent_gated_delta_rule(q, k, v, beta, g, S0)
+        else:
+            o, S = chunk_gated_delta_rule(q, k, v, beta, g, S0, self.chunk_size)
+        output = self._output(o, hidden_states, B, L)
+
+        if use_cache:
+            past_key_value.update(S, (cq, ck, cv), steps=L)
+            return AttentionOutput(output=output, past_key_value=past_key_value)
+        payload = {'state': S.detach(), 'conv_state': tuple(c.detach() for c in (cq, ck, cv))}
+        return AttentionOutput(output=output, payload=payload)
+
+    def forward_varlen(self, hidden_states: torch.Tensor, cu_seqlens: torch.Tensor) -> AttentionOutput:
+        '''Packed sequences (B == 1): every sequence starts from zero state and zero
+        conv tails.  Returns the output and a payload with the per-sequence final
+        states [nseq, H, dk, dv] and conv tails [nseq, D, K-1].'''
+        B, L, _ = hidden_states.shape
+        if B != 1:
+            raise ValueError('forward_varlen expects packed sequences with B == 1')
+        lens = cu_seqlens.detach().cpu()
+        max_len = int((lens[1:] - lens[:-1]).max()) if lens.numel() > 1 else 0
+        q, cq = short_conv_silu_varlen(self.q_proj(hidden_states), self.q_conv.weight, cu_seqlens, max_len)
+        k, ck = short_conv_silu_varlen(self.k_proj(hidden_states), self.k_conv.weight, cu_seqlens, max_len)
+        v, cv = short_conv_silu_varlen(self.v_proj(hidden_states), self.v_conv.weight, cu_seqlens, max_len)
+        q, k, v = self._heads(q, k, v, B, L)
+        beta, g = self._gates(hidden_states)
+        o, S = chunk_gated_delta_rule_varlen(q, k, v, beta, g, cu_seqlens, None, self.chunk_size)
+        output = self._output(o, hidden_states, B, L)
+        return AttentionOutput(output=output, payload={'state': S, 'conv_state': (cq, ck, cv)})

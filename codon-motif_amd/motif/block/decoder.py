@@ -1,0 +1,93 @@
+'''Decoder / DecoderBlock with the reference interface (motif/block/decoder.py:44-222):
+pre-norm attention in parallel with a pre-norm SwiGLU MLP, and the intra-block
+attention-residual read in front of every decoder.'''
+from dataclasses import dataclass
+from typing import List, Literal, Optional, Union
+
+import torch
+import torch.nn as nn
+
+from motif.block.attention import AttentionOutput, ChordAttention, GatedDeltaAttention
+from motif.block.mlp import SwiGLU
+from motif.model.cache import DecoderBlockCache, GatedDeltaAttentionLayerCache, KVLayerCache
+from motif.model.config import MotifChordConfig
+from motif.ops import RMSNorm
+from motif.ops.attn_res import apply_block_attn_res
+
+
+@dataclass
+class DecoderBlockOutput:
+    hidden_states: torch.Tensor
+    cache: DecoderBlockCache
+
+    @property
+    def blocks(self) -> List[torch.Tensor]:
+        return self.cache.attn_res.blocks
+
+
+class Decoder(nn.Module):
+    def __init__(self, attn_type: Literal['gdn', 'chord'], config: MotifChordConfig):
+        super().__init__()
+        self.attn_type = attn_type.lower()
+        self.attn_norm = RMSNorm(config.model_dim)
+        if self.attn_type == 'chord':
+            self.attn = ChordAttention(hidden_size=config.model_dim, num_heads=config.num_heads,
+                                       num_kv_heads=config.num_kv_heads)
+        else:
+            self.attn = GatedDeltaAttention(hidden_size=config.model_dim, num_heads=config.num_heads,
+                                            head_k_dim=config.head_k_dim, expand_v=2.0, chunk_size=64,
+                                            bias=False)
+        self.mlp_norm = RMSNorm(config.model_dim)
+        self.mlp = SwiGLU(in_features=config.model_dim)
+
+    @property
+    def cache_type(self):
+        return KVLayerCache if self.attn_type == 'chord' else GatedDeltaAttentionLayerCache
+
+
+class DecoderBlock(nn.Module):
+    def __init__(self, config: MotifChordConfig):
+        super().__init__()
+        self.features = nn.ModuleList([Decoder(attn_type=t, config=config) for t in config.block])
+        self.pseudo_queries = nn.ParameterList([nn.Parameter(torch.zeros(config.model_dim)) for _ in self.features])
+        self.attn_res_norms = nn.ModuleList([RMSNorm(config.model_dim) for _ in self.features])
+
+    def forward(self, hidden_states: torch.Tensor, cache: Optional[DecoderBlockCache] = None,
+                mask: Optional[torch.Tensor] = None, position: Union[int, torch.Tensor] = 0,
+                cu_seqlens: Optional[torch.Tensor] = None) -> DecoderBlockOutput:
+        '''Run every decoder, threading the attention-residual state.
+
+        `cu_seqlens` (packed sequences, B == 1; no reference counterpart) runs
+        every layer in its varlen form and uses no layer caches.'''
+        if cache is None:
+            cache = DecoderBlockCache()
+        attn_res = cache.attn_res
+        attn_res.init_embedding(hidden_states)
+        if cu_seqlens is None:
+            if len(cache.attn) == 0:
+                if not self.training:
+                    cache.ensure_attn([d.cache_type for d in self.features])
+            elif len(cache.attn) != len(self.features):
+                raise ValueError(f'cache.attn has {len(cache.attn)} entries but the block has '
+                                 f'{len(self.features)} layers')
+        use_attn_cache = cu_seqlens is None and len(cache.attn) == len(self.features)
+
+        for i, decoder in enumerate(self.features):
+            h = apply_block_attn_res(attn_res, self.pseudo_queries[i], self.attn_res_norms[i])
+            x = decoder.attn_norm(h)
+            if cu_seqlens is not None:
+                attn_out = decoder.attn.forward_varlen(x, cu_seqlens)
+            elif isinstance(decoder.attn, ChordAttention):
+                attn_out = decoder.attn(hidden_states=x, past_key_value=cache.attn[i] if use_attn_cache else None,
+                                        attention_mask=mask, embedding_start=position)
+            else:
+                attn_out = decoder.attn(hidden_states=x, past_key_value=cache.attn[i] if use_attn_cache else None)
+            f_h = attn_out.output + decoder.mlp(decoder.mlp_norm(h))
+            if use_attn_cache:
+                cache.attn[i] = attn_out.past_key_value
+            attn_res.update_increment(f_h)
+
+        block_repr = attn_res.partial_block
+        if block_repr is None:
+            block_repr = hidden_states
+        return DecoderBlockOutput(hidden_states=block_repr, cache=cache)

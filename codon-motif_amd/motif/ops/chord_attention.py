@@ -3,9 +3,10 @@
 `apply_chord_attention` keeps the reference signature, defaults, validation
 messages and exception types (motif/ops/chord_attention.py:1557-1625 with
 `_check_tensors` :966-1011 and `_check_params` :1448-1472).  The launcher
-picks the MFMA flash kernel for prefill shapes and the split-K decode kernel
-when a kv head serves at most 8 query rows (GQA group x L), which is the
-reference's long-KV / short-Q split path (:1128-1229).
+picks the bf16 MFMA flash kernel for prefill shapes and the split-K vector
+kernel when a kv head serves at most 8 query rows (GQA group x L), which is
+the reference's long-KV / short-Q split path (:1128-1229).  fp32 inputs run on
+the vector kernel for every shape (fp32 FMA throughout, the accuracy mode).
 `apply_chord_attention_varlen` adds packed sequences (new).
 '''
 from typing import Optional
@@ -62,7 +63,8 @@ def _check_params(alpha, beta, mu, ssmax, num_heads):
 
 def _aligned(t):
     '''Rows must start on 16-byte boundaries for the vector loads.'''
-    ok = t.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in t.stride()[:-1])
+    per16 = 16 // t.element_size()
+    ok = t.data_ptr() % 16 == 0 and all(s % per16 == 0 for s in t.stride()[:-1])
     return t if ok else t.contiguous()
 
 
@@ -70,9 +72,11 @@ def _launch(q, k, v, alpha, beta, mu, ssmax, log_n, q_start, scale, eps, out, ls
             cu_dev=None, nseq=None, max_seqlen=None):
     B, H, L, D = q.shape
     Hkv, S = k.shape[1], k.shape[2]
-    if q.dtype != torch.bfloat16:
+    if q.dtype not in (torch.bfloat16, torch.float32):
         raise NotImplementedError(
-            f'apply_chord_attention: the HIP kernel computes bf16 inputs; got {q.dtype}')
+            f'apply_chord_attention: the HIP kernels take bf16 or fp32 inputs; got {q.dtype}')
+    if cu_dev is not None and q.dtype != torch.bfloat16:
+        raise NotImplementedError('apply_chord_attention_varlen: packed sequences are implemented for bf16')
     if D != HEAD_DIM:
         raise NotImplementedError(f'apply_chord_attention: head_dim {D} unsupported (64 only)')
     q, k, v = _aligned(q), _aligned(k), _aligned(v)
@@ -90,7 +94,7 @@ def _launch(q, k, v, alpha, beta, mu, ssmax, log_n, q_start, scale, eps, out, ls
         *_lib.t4(out), _lib.ptr(lse),
         B, H, Hkv, L, S, D, int(q_start), float(scale), float(eps),
         _lib.ptr(cu_dev), int(nseq), int(max_seqlen),
-        ws.data_ptr(), ws.numel(), _lib.MOTIF_BF16, _lib.stream_ptr(q.device))
+        ws.data_ptr(), ws.numel(), _lib.dtype_code(q.dtype), _lib.stream_ptr(q.device))
     _lib.check(rc, 'motif_chord_fwd')
     return out
 
@@ -115,7 +119,7 @@ def apply_chord_attention(
     keys j <= q_start + i, softmax over keys, times v.
 
     Args:
-        q: [B, H, L, D];  k, v: [B, H_kv, S, D] (bf16, D == 64).
+        q: [B, H, L, D];  k, v: [B, H_kv, S, D] (bf16 or fp32, D == 64).
         alpha, beta, mu, ssmax: [H] fp32 contiguous.
         log_n: [B, L] fp32.
         q_start: absolute position of the first query; defaults to S - L.
@@ -127,7 +131,7 @@ def apply_chord_attention(
 
     Raises:
         ValueError: on unsupported inputs or a negative q_start.
-        NotImplementedError: for inputs requiring grad, non-bf16 dtypes or D != 64.
+        NotImplementedError: for inputs requiring grad, fp16 inputs or D != 64.
         RuntimeError: when the HIP library is unavailable or a launch fails.
     '''
     if not _lib.available():

@@ -105,7 +105,7 @@ def log_n_table(q_start, q_len):
 
 
 def chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, cu_seqlens,
-                           softmax_scale=None, eps=GGD_EPS):
+                           softmax_scale=None, eps=GGD_EPS, compute_dtype=torch.float64):
     '''Packed-sequence Chord attention (B == 1): new capability.
 
     Defined as an independent causal run per sequence with positions restarting
@@ -118,7 +118,7 @@ def chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, cu_seqlens,
         qs, ks, vs = q[:, :, s:e], k[:, :, s:e], v[:, :, s:e]
         ln = log_n_table(0, e - s)[None]
         outs.append(chord_attention(qs, ks, vs, alpha, beta, mu, ssmax, ln, 0,
-                                    softmax_scale, eps))
+                                    softmax_scale, eps, compute_dtype))
     return torch.cat(outs, dim=2)
 
 
@@ -154,9 +154,10 @@ def chord_layer(hidden, p, num_heads, num_kv_heads, k_cache=None, v_cache=None,
     k = rms_norm(k, p['k_norm.weight'], eps_norm)
     alpha, beta, mu = ggd_parameters(p)
     ssmax = p['ssmax_s'].double()
+    cd = torch.float64 if hidden.dtype == torch.float64 else torch.float32
     if cu_seqlens is not None:
         out = chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, cu_seqlens,
-                                     softmax_scale=D ** -0.5)
+                                     softmax_scale=D ** -0.5, compute_dtype=cd)
         k_all, v_all = k, v
     else:
         if k_cache is not None and k_cache.shape[2] > 0:
@@ -168,7 +169,7 @@ def chord_layer(hidden, p, num_heads, num_kv_heads, k_cache=None, v_cache=None,
             k_all, v_all = k, v
         ln = log_n_table(q_start, L)[None].expand(B, L)
         out = chord_attention(q, k_all, v_all, alpha, beta, mu, ssmax, ln, q_start,
-                              softmax_scale=D ** -0.5)
+                              softmax_scale=D ** -0.5, compute_dtype=cd)
     out = out.to(hidden.dtype).transpose(1, 2).reshape(B, L, hid)
     return (out @ p['o_proj.weight'].t()) * G, k_all, v_all
 

@@ -122,3 +122,18 @@ def test_validation_errors_match_reference_types():
     with pytest.raises(ValueError):
         ops.apply_chord_attention(q, k[:, :1].expand(1, 3, 8, 64), v[:, :1].expand(1, 3, 8, 64),
                                   alpha, beta, mu, ssmax, log_n)
+
+
+@pytest.mark.parametrize('B,H,Hkv,L,S', [(2, 4, 2, 77, 77), (1, 12, 3, 300, 300), (2, 12, 3, 5, 900), (3, 4, 4, 1, 2000)])
+def test_fp32_mode(B, H, Hkv, L, S):
+    """fp32 inputs run the fp32 vector kernel: within 1e-4 of the fp64 oracle."""
+    ops = _ops()
+    q, k, v, alpha, beta, mu, ssmax = chord_inputs(B, H, Hkv, L, S, seed=L + S)
+    q, k, v = q.float(), k.float(), v.float()
+    mu = torch.linspace(-1.0, 1.0, H)
+    log_n = _log_n(B, L, S - L)
+    out = _run(ops, q, k, v, alpha, beta, mu, ssmax, log_n)
+    assert out.dtype == torch.float32
+    ref = ochord.chord_attention(q, k, v, alpha, beta, mu, ssmax, log_n, S - L)
+    err = (out.double().cpu() - ref).abs().max().item()
+    assert err <= 1e-4, err
