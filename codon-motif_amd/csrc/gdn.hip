@@ -12,34 +12,11 @@
 //   (value tile of 32 columns, head, sequence) carries S[:, tile] across the
 //   chunks and emits the chunk outputs O = (Q e^gamma) S + Attn X in the same
 //   pass (X = U - W S), so neither the prefix states nor X round-trip HBM.
-#include "capi_internal.h"
-#include "common.h"
+#include <algorithm>
+
+#include "gdn_internal.h"
 
 namespace motif {
-
-struct GdnArgs {
-  const void *q; int64_t q_sb, q_sh, q_st;
-  const void *k; int64_t k_sb, k_sh, k_st;
-  const void *v; int64_t v_sb, v_sh, v_st;
-  const void *beta; int64_t b_sb, b_sh, b_st;
-  const void *g; int64_t g_sb, g_sh, g_st;
-  const float *s_in;
-  float *s_out;
-  void *o; int64_t o_sb, o_sh, o_st;
-  int B, H, L, dk, dv;
-};
-
-struct ChunkArgs {
-  const int32_t *cu;    // packed-sequence boundaries or nullptr
-  const int32_t *coff;  // cumulative chunk counts or nullptr
-  int nseq;
-  int nper;             // chunks per batch row (padded batches)
-  int total_chunks;
-  float *gam;           // [H][TC][C]
-  float *W;             // [H][TC][C][DK]
-  float *U;             // [H][TC][C][DV]
-  float *attn;          // [H][TC][C][C]
-};
 
 // ------------------------------------------------------------------ recurrence
 template <typename TI, typename TO, int DK>
@@ -97,35 +74,6 @@ __global__ void __launch_bounds__(128) gdn_recurrent_kernel(GdnArgs a) {
 #pragma unroll
     for (int i = 0; i < DK; ++i) a.s_out[sbase + static_cast<size_t>(i) * a.dv + col] = S[i];
   }
-}
-
-// ------------------------------------------------------------------ chunk map
-struct ChunkInfo {
-  int batch, seq, t0, len;
-};
-
-__device__ __forceinline__ ChunkInfo resolve_chunk(int c, int C, int L, const ChunkArgs &ca) {
-  ChunkInfo ci;
-  int tok_end;
-  if (ca.cu == nullptr) {
-    ci.seq = c / ca.nper;
-    ci.batch = ci.seq;
-    ci.t0 = (c - ci.seq * ca.nper) * C;
-    tok_end = L;
-  } else {
-    int lo = 0, hi = ca.nseq - 1;  // largest s with coff[s] <= c (skips empty sequences)
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (ca.coff[mid] <= c) lo = mid;
-      else hi = mid - 1;
-    }
-    ci.seq = lo;
-    ci.batch = 0;
-    ci.t0 = ca.cu[lo] + (c - ca.coff[lo]) * C;
-    tok_end = ca.cu[lo + 1];
-  }
-  ci.len = min(C, tok_end - ci.t0);
-  return ci;
 }
 
 // ---------------------------------------------------------------- chunk prep
@@ -467,8 +415,10 @@ extern "C" int motif_gdn_recurrent_fwd(
 
 extern "C" size_t motif_gdn_chunk_workspace_bytes(int H, int dk, int dv, int chunk, int total_chunks) {
   if (H <= 0 || dk <= 0 || dv <= 0 || chunk <= 0 || total_chunks <= 0) return 0;
+  // bf16 inputs on the MFMA path need its layout; fp32 inputs use the fp32 kernels.
+  size_t mfma = chunk_mfma_supported(dk, dv, chunk) ? chunk_mfma_workspace_bytes(H, dk, dv, total_chunks) : 0;
   const size_t per = static_cast<size_t>(chunk) * (1 + dk + dv + chunk);
-  return per * H * total_chunks * sizeof(float);
+  return std::max(mfma, per * H * total_chunks * sizeof(float));
 }
 
 extern "C" int motif_gdn_chunk_fwd(
@@ -529,6 +479,12 @@ extern "C" int motif_gdn_chunk_fwd(
   ca.U = ca.W + tc * chunk * dk;
   ca.attn = ca.U + tc * chunk * dv;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (in_dtype != MOTIF_F32 && in_dtype != MOTIF_BF16)
+    return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_chunk: unsupported dtype");
+  // bf16 inputs take the MFMA path (3-pass bf16 products, ~16 mantissa bits);
+  // fp32 inputs keep fp32 FMA throughout (the 1e-4 accuracy mode).
+  if (in_dtype == MOTIF_BF16 && chunk_mfma_supported(dk, dv, chunk))
+    return launch_chunk_mfma(a, ca, workspace, in_dtype, s);
   if (in_dtype == MOTIF_F32) return launch_chunk<float>(a, ca, chunk, s);
   if (in_dtype == MOTIF_BF16) return launch_chunk<bf16_t>(a, ca, chunk, s);
   return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_chunk: unsupported dtype");
