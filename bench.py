@@ -17,6 +17,8 @@ Also reported in the same JSON line:
   (oracle/, float32, torch threads) on one config-3 forward.
 
 Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu]
+       python bench.py --kernels-only   # hot-path ops + a copy kernel of known size,
+                                        # the target of the rocprofv3 --pmc traffic runs
 '''
 import argparse
 import json
@@ -138,6 +140,40 @@ def kernel_timings(dev):
     return res
 
 
+def copy_calibration(dev, mib=256, reps=5):
+    '''A plain device copy of `mib` MiB (reads and writes exactly that many bytes):
+    the scale for the FETCH_SIZE / WRITE_SIZE counters of the --pmc runs.'''
+    import torch
+    src = torch.ones(mib * 2 ** 19, dtype=torch.bfloat16, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return mib * 1024  # KiB per direction
+
+
+# rocprofv3 --pmc summary (FETCH_SIZE / WRITE_SIZE, copy-calibrated) of bench.py --kernels-only
+TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'hot_path_ops_hbm_traffic.txt')
+OP_KERNELS = {'gdn_chunk_prefill': ('gdn_prep_mfma', 'gdn_scan_mfma'), 'chord_prefill': ('chord_fwd_kernel',),
+              'gdn_decode': ('gdn_recurrent_kernel',), 'chord_decode': ('chord_decode_kernel', 'chord_merge_kernel')}
+
+
+def measured_traffic(op):
+    '''HBM bytes per launch of `op` (all its kernels) from the committed --pmc summary, or None.'''
+    try:
+        with open(TRAFFIC_FILE) as f:
+            rows = [ln.split() for ln in f if ln[:1].isalpha() and '<' in ln.split()[0] and len(ln.split()) == 5]
+    except OSError:
+        return None
+    total, seen = 0.0, set()
+    for r in rows:
+        name = r[0].split('<')[0]
+        if name in OP_KERNELS.get(op, ()):
+            total += float(r[4]) * 1e6
+            seen.add(name)
+    return total if seen == set(OP_KERNELS.get(op, ())) else None
+
+
 def make_decode_cache(model, B, ctx, capacity, dev, dtype, seed=1):
     '''Caches as after a ctx-token prefill, filled with random values (timing only).'''
     import torch
@@ -208,6 +244,7 @@ def main():
     ap.add_argument('--steps', type=int, default=10)
     ap.add_argument('--warmup', type=int, default=3)
     ap.add_argument('--no-cpu', action='store_true')
+    ap.add_argument('--kernels-only', action='store_true')
     ap.add_argument('--seq', type=int, default=4096)
     ap.add_argument('--decode-batch', type=int, default=64)
     args = ap.parse_args()
@@ -226,6 +263,14 @@ def main():
     dev = torch.device('cuda', 0)
     torch.cuda.set_device(dev)
     torch.backends.cuda.matmul.allow_tf32 = False
+
+    if args.kernels_only:
+        with torch.no_grad():
+            kern = kernel_timings(dev)
+            copy_calibration(dev)
+        print(json.dumps({k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                          for k, v in kern.items()}), flush=True)
+        return
 
     cfg = bench_config()
     model = init_model(MotifChordModel(cfg)).to(dev, torch.bfloat16).eval()
@@ -292,7 +337,7 @@ def main():
     dom = max(per_fwd, key=per_fwd.get)
     r = kern[dom]
     roofline = dict(kernel=dom, bound=r['bound'], achieved=round(r['achieved'], 3), peak=r['peak'],
-                    unit=r['unit'], frac=round(r['frac'], 5), traffic=None, avg_us=round(r['us'], 2),
+                    unit=r['unit'], frac=round(r['frac'], 5), traffic=measured_traffic(dom), avg_us=round(r['us'], 2),
                     work_per_launch=r['work'], shape=r['shape'])
 
     cpu = None
