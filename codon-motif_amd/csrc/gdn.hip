@@ -483,8 +483,7 @@ extern "C" int motif_gdn_chunk_fwd(
     return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_chunk: unsupported dtype");
   // bf16 inputs take the MFMA path (3-pass bf16 products, ~16 mantissa bits);
   // fp32 inputs keep fp32 FMA throughout (the 1e-4 accuracy mode).
-  if (in_dtype == MOTIF_BF16 && chunk_mfma_supported(dk, dv, chunk))
-    return launch_chunk_mfma(a, ca, workspace, in_dtype, s);
+  if (chunk_mfma_eligible(a, chunk, in_dtype, out_dtype)) return launch_chunk_mfma(a, ca, workspace, s);
   if (in_dtype == MOTIF_F32) return launch_chunk<float>(a, ca, chunk, s);
   if (in_dtype == MOTIF_BF16) return launch_chunk<bf16_t>(a, ca, chunk, s);
   return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_chunk: unsupported dtype");

@@ -36,6 +36,12 @@ __device__ __forceinline__ f32x4 mma(const bf16x8 &a, const bf16x8 &b, f32x4 c) 
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// 16x16x16: A lane (m = l % 16) holds k = 4 (l / 16) .. +3, B lane (n = l % 16) the same k.
+__device__ __forceinline__ f32x4 mma16(const bf16x4 &a, const bf16x4 &b, f32x4 c) {
+  typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s16x4;
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+}
+
 // c += (ah + al)(bh + bl) without the lo.lo term; SA / SB: operand has a lo part.
 template <bool SA, bool SB>
 __device__ __forceinline__ f32x4 mma3(const bf16x8 &ah, const bf16x8 &al, const bf16x8 &bh,
@@ -74,23 +80,78 @@ struct WsLayout {
 };
 
 // ------------------------------------------------------------------ prep
+// LDS planes of [rows][64] bf16 (128-byte rows), 16-byte chunks XOR-swizzled by
+// row so that 16 rows read at one column hit distinct banks.  Element offset of
+// (row, col); col & 3 == 0 keeps 8-byte accesses aligned, col & 7 == 0 16-byte ones.
+__device__ __forceinline__ int swz(int row, int col) {
+  return row * 64 + ((((col >> 3) ^ (row & 7)) << 3) | (col & 7));
+}
+__device__ __forceinline__ bf16x8 rd8s(const __bf16 *p, int row, int col) {
+  return *reinterpret_cast<const bf16x8 *>(p + swz(row, col));
+}
+__device__ __forceinline__ bf16x4 rd4s(const __bf16 *p, int row, int col) {
+  return *reinterpret_cast<const bf16x4 *>(p + swz(row, col));
+}
+// 8 k-values [k0 + 4g, +4) and [k0 + 16 + 4g, +4) of a swizzled row: the A operand
+// that pairs with a B operand built from two 16x16 accumulator tiles.
+__device__ __forceinline__ bf16x8 rd_perm_s(const __bf16 *p, int row, int k0, int g) {
+  return __builtin_shufflevector(rd4s(p, row, k0 + 4 * g), rd4s(p, row, k0 + 16 + 4 * g), 0, 1, 2, 3, 4, 5, 6, 7);
+}
+__device__ __forceinline__ void split4(const float *x, bf16x4 &h, bf16x4 &l) {
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    h[t] = bf(x[t]);
+    l[t] = bf(x[t] - fl(h[t]));
+  }
+}
+__device__ __forceinline__ void split8(const float *x, bf16x8 &h, bf16x8 &l) {
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    h[t] = bf(x[t]);
+    l[t] = bf(x[t] - fl(h[t]));
+  }
+}
+__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
+  return static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+}
+__device__ __forceinline__ uint16_t bits(__bf16 x) { return __builtin_bit_cast(uint16_t, x); }
+
+// Byte offsets of the prep kernel's LDS.  Phase 7 (the operator products) keeps
+//   att hi/lo  [64][64]   Attn = (Q K^T) * D, rows i', columns i
+//   tt  hi/lo  [64][64]   T^T, rows j, columns i
+//   kt         [DK][64]   K^T (exact), vt [DV][64] V^T (exact), ktt hi/lo [DK][64] K~^T
+// Phases 1-5 use the kt.. region for K and Q rows (padded, row-major) and NT, one fp32
+// [64][68] array holding N = strict(beta K K^T * D) below the diagonal and T^T on and
+// above it; the level-2 product Y^T lives in the tt region until T^T is written there.
 template <int DK, int DV>
-struct PrepSmem {
-  __bf16 kh[kC][DK + kPad];                        // K rows (bf16 inputs are exact)
-  __bf16 qh[kC][DK + kPad];                        // Q rows
-  __bf16 kth[DK][kC + kPad], ktl[DK][kC + kPad];   // K~^T
-  __bf16 ath[kC][kC + kPad], atl[kC][kC + kPad];   // Attn
-  __bf16 wth[DK][kC + kPad], wtl[DK][kC + kPad];   // W^T
-  __bf16 uth[DV][kC + kPad], utl[DV][kC + kPad];   // U^T
-  float A[kC][kC + 4];                             // strictly lower A (16-byte rows)
-  float gam[kC], beta[kC], zk[kC], eg[kC];
+struct PrepLayout {
+  static constexpr int kPlane = 64 * 64 * 2;
+  static constexpr int att_h = 0, att_l = kPlane, tt_h = 2 * kPlane, tt_l = 3 * kPlane;
+  static constexpr int base = 4 * kPlane;
+  static constexpr int kt = base, vt = kt + DK * 128, ktt_h = vt + DV * 128, ktt_l = ktt_h + DK * 128;
+  static constexpr int end7 = ktt_l + DK * 128;
+  static constexpr int kRow = DK + kPad;  // K / Q rows (bf16 elements)
+  static constexpr int kh = base, qh = kh + 64 * kRow * 2, nt = qh + 64 * kRow * 2;
+  static constexpr int end1 = nt + 64 * 68 * 4;
+  static constexpr int yt = tt_h;  // [32][36] fp32
+  static constexpr int small = end7 > end1 ? end7 : end1;  // gam[64], beta[64]
+  static constexpr int bytes = small + 2 * 64 * 4;
 };
 
 template <int DK, int DV>
-__global__ void __launch_bounds__(256) gdn_prep_mfma(GdnArgs a, ChunkArgs ca, char *ws) {
+__global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca, char *ws) {
   using TI = bf16_t;
-  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
-  PrepSmem<DK, DV> &sm = *reinterpret_cast<PrepSmem<DK, DV> *>(smem_raw);
+  using PL = PrepLayout<DK, DV>;
+  constexpr int NTS = 68;  // NT row stride (floats)
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  __bf16 *att_h = reinterpret_cast<__bf16 *>(smem + PL::att_h), *att_l = reinterpret_cast<__bf16 *>(smem + PL::att_l);
+  __bf16 *tt_h = reinterpret_cast<__bf16 *>(smem + PL::tt_h), *tt_l = reinterpret_cast<__bf16 *>(smem + PL::tt_l);
+  __bf16 *kt = reinterpret_cast<__bf16 *>(smem + PL::kt), *vt = reinterpret_cast<__bf16 *>(smem + PL::vt);
+  __bf16 *ktt_h = reinterpret_cast<__bf16 *>(smem + PL::ktt_h), *ktt_l = reinterpret_cast<__bf16 *>(smem + PL::ktt_l);
+  __bf16 *kh = reinterpret_cast<__bf16 *>(smem + PL::kh), *qh = reinterpret_cast<__bf16 *>(smem + PL::qh);
+  float *nt = reinterpret_cast<float *>(smem + PL::nt);
+  float *yt = reinterpret_cast<float *>(smem + PL::yt);
+  float *gam = reinterpret_cast<float *>(smem + PL::small), *bet = gam + 64;
 
   const int chunk = blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -103,15 +164,33 @@ __global__ void __launch_bounds__(256) gdn_prep_mfma(GdnArgs a, ChunkArgs ca, ch
   const TI *bb = static_cast<const TI *>(a.beta) + ci.batch * a.b_sb + h * a.b_sh + int64_t(ci.t0) * a.b_st;
   const TI *gb = static_cast<const TI *>(a.g) + ci.batch * a.g_sb + h * a.g_sh + int64_t(ci.t0) * a.g_st;
 
-  // K, Q rows (zero past the chunk's valid length): 16-byte loads, all in flight together.
-  constexpr int PT = kC * DK / 8 / 256;  // 16-byte pieces per thread and matrix
-  uint4 kr[PT], qr[PT];
+  // ---- phase 1: rows 2p, 2p + 1 of one 8-column segment per thread (zero past len)
+  constexpr int KSEG = DK / 8, VSEG = DV / 8, VP = 32 * VSEG / 256;
+  const int kp = tid / KSEG, kseg = tid % KSEG;
+  const bool kval = kp < 32;
+  const uint4 z4 = {0, 0, 0, 0};
+  uint4 k0r = z4, k1r = z4, q0r = z4, q1r = z4;
+  if (kval) {
+    const int r0 = 2 * kp, r1 = r0 + 1;
+    if (r0 < ci.len) {
+      k0r = *reinterpret_cast<const uint4 *>(kb + int64_t(r0) * a.k_st + 8 * kseg);
+      q0r = *reinterpret_cast<const uint4 *>(qb + int64_t(r0) * a.q_st + 8 * kseg);
+    }
+    if (r1 < ci.len) {
+      k1r = *reinterpret_cast<const uint4 *>(kb + int64_t(r1) * a.k_st + 8 * kseg);
+      q1r = *reinterpret_cast<const uint4 *>(qb + int64_t(r1) * a.q_st + 8 * kseg);
+    }
+  }
+  uint4 v0r[VP], v1r[VP];
 #pragma unroll
-  for (int r = 0; r < PT; ++r) {
-    const int p = tid + 256 * r, i = p / (DK / 8), c8 = p % (DK / 8);
-    const bool ok = i < ci.len;
-    kr[r] = ok ? *reinterpret_cast<const uint4 *>(kb + int64_t(i) * a.k_st + 8 * c8) : uint4{0, 0, 0, 0};
-    qr[r] = ok ? *reinterpret_cast<const uint4 *>(qb + int64_t(i) * a.q_st + 8 * c8) : uint4{0, 0, 0, 0};
+  for (int r = 0; r < VP; ++r) {
+    const int p = tid + 256 * r, vp = p / VSEG, vs = p % VSEG;
+    v0r[r] = z4;
+    v1r[r] = z4;
+    if (vs < a.dv / 8) {
+      if (2 * vp < ci.len) v0r[r] = *reinterpret_cast<const uint4 *>(vb + int64_t(2 * vp) * a.v_st + 8 * vs);
+      if (2 * vp + 1 < ci.len) v1r[r] = *reinterpret_cast<const uint4 *>(vb + int64_t(2 * vp + 1) * a.v_st + 8 * vs);
+    }
   }
   if (w == 0) {  // gates and the inclusive prefix sum of g
     float gv = 0.f, bv = 0.f;
@@ -125,149 +204,302 @@ __global__ void __launch_bounds__(256) gdn_prep_mfma(GdnArgs a, ChunkArgs ca, ch
       const float y = __shfl_up(s, off, 64);
       if (lane >= off) s += y;
     }
-    sm.gam[lane] = s;
-    sm.beta[lane] = bv;
-    sm.eg[lane] = exp_f(s);
-    sm.zk[lane] = bv * exp_f(s);
+    gam[lane] = s;
+    bet[lane] = bv;
   }
-#pragma unroll
-  for (int r = 0; r < PT; ++r) {
-    const int p = tid + 256 * r, i = p / (DK / 8), c8 = p % (DK / 8);
-    *reinterpret_cast<uint4 *>(&sm.kh[i][8 * c8]) = kr[r];
-    *reinterpret_cast<uint4 *>(&sm.qh[i][8 * c8]) = qr[r];
+  if (kval) {
+    *reinterpret_cast<uint4 *>(kh + (2 * kp) * PL::kRow + 8 * kseg) = k0r;
+    *reinterpret_cast<uint4 *>(kh + (2 * kp + 1) * PL::kRow + 8 * kseg) = k1r;
+    *reinterpret_cast<uint4 *>(qh + (2 * kp) * PL::kRow + 8 * kseg) = q0r;
+    *reinterpret_cast<uint4 *>(qh + (2 * kp + 1) * PL::kRow + 8 * kseg) = q1r;
   }
   __syncthreads();
 
-  const float glast = sm.gam[kC - 1];
-  // K~^T = (K e^{gamma_C - gamma})^T, split.
-  for (int e = tid; e < kC * DK; e += 256) {
-    const int i = e / DK, d = e - i * DK;
-    const float x = fl(sm.kh[i][d]) * exp_f(glast - sm.gam[i]);
-    const __bf16 x1 = bf(x);
-    sm.kth[d][i] = x1;
-    sm.ktl[d][i] = bf(x - fl(x1));
-  }
-
-  // G = K K^T and QK = Q K^T: wave w owns row tile mt = w (rows 16w .. 16w+15).
-  {
-    const int mt = w;
+  // ---- phase 2: G = K K^T -> N, and K Q^T -> Attn, on 16x16 tiles (bi <= bj).
+  // Tile (bi, bj) of G holds G[16 bi + 4g + r][16 bj + ln] = G[16 bj + ln][16 bi + 4g + r]
+  // (symmetric), i.e. N row 16 bj + ln, columns 16 bi + 4g .. +3: one float4 per lane.
+  // Tile (bi, bj) of K Q^T holds (Q K^T)[16 bj + ln][16 bi + 4g + r]: Attn row 16 bj + ln.
+  for (int t = w; t < 26; t += 4) {
+    if (t < 16) {  // Attn block (row block bj, column block bi); zero above the diagonal
+      const int bj = t >> 2, bi = t & 3;
+      const int row = 16 * bj + ln, col = 16 * bi + 4 * g;
+      float x[4] = {0.f, 0.f, 0.f, 0.f};
+      if (bi <= bj) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int nt = 0; nt < kC / 16; ++nt) {
-      f32x4 gacc = {0.f, 0.f, 0.f, 0.f}, qacc = {0.f, 0.f, 0.f, 0.f};
+        for (int ks = 0; ks < DK / 32; ++ks) {
+          const int k0 = 32 * ks + 8 * g;
+          acc = mma(rd8(kh + (16 * bi + ln) * PL::kRow, k0), rd8(qh + (16 * bj + ln) * PL::kRow, k0), acc);
+        }
+        const float gi = gam[row];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          x[r] = (col + r <= row) ? acc[r] * exp_f(gi - gam[col + r]) : 0.f;
+      }
+      bf16x4 hv, lv;
+      split4(x, hv, lv);
+      *reinterpret_cast<bf16x4 *>(att_h + swz(row, col)) = hv;
+      *reinterpret_cast<bf16x4 *>(att_l + swz(row, col)) = lv;
+    } else {  // N block (row block bj, column block bi), bi <= bj
+      int u = t - 16, bj = 0;
+      while (u > bj) { u -= bj + 1; ++bj; }
+      const int bi = u;
+      const int row = 16 * bj + ln, col = 16 * bi + 4 * g;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < DK / 32; ++ks) {
         const int k0 = 32 * ks + 8 * g;
-        const bf16x8 bk = rd8(sm.kh[16 * nt + ln], k0);
-        gacc = mma(rd8(sm.kh[16 * mt + ln], k0), bk, gacc);
-        qacc = mma(rd8(sm.qh[16 * mt + ln], k0), bk, qacc);
+        acc = mma(rd8(kh + (16 * bi + ln) * PL::kRow, k0), rd8(kh + (16 * bj + ln) * PL::kRow, k0), acc);
       }
+      const float gi = gam[row], bi_ = bet[row];
+      f32x4 x;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[r] = (col + r < row) ? bi_ * acc[r] * exp_f(gi - gam[col + r]) : 0.f;
+      *reinterpret_cast<f32x4 *>(nt + row * NTS + col) = x;
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 3: diagonal 16x16 blocks of T = (I + N)^{-1} by forward substitution,
+  // wave w -> block w, lane c < 16 -> column c; T[16w + i][16w + c] goes to NT row 16w + c.
+  if (ln == lane) {
+    const int b = w, c = lane;
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float *nrow = nt + (16 * b + i) * NTS + 16 * b;
+      float s = (i == c) ? 1.f : 0.f;
+#pragma unroll
+      for (int j = 0; j < i; ++j) s = fmaf(-nrow[j], x[j], s);
+      x[i] = s;
+    }
+    float *trow = nt + (16 * b + c) * NTS + 16 * b;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (i >= c) trow[i] = x[i];
+  }
+  __syncthreads();
+
+  // ---- phase 4: 32x32 inverses: T_ab = -T_aa N_ab T_bb for (a, b) = (1, 0), (3, 2).
+  if (w < 2) {
+    const int a_ = 2 * w + 1, b_ = 2 * w;
+    // X = N_ab T_bb (16x16x16 products in three passes)
+    float av[4], bv[4];
+    {
+      const f32x4 n4 = *reinterpret_cast<const f32x4 *>(nt + (16 * a_ + ln) * NTS + 16 * b_ + 4 * g);
+      const f32x4 t4 = *reinterpret_cast<const f32x4 *>(nt + (16 * b_ + ln) * NTS + 16 * b_ + 4 * g);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int i = 16 * mt + 4 * g + r, j = 16 * nt + ln;
-        float av = 0.f, atv = 0.f;
-        if (j <= i) {
-          const float dec = exp_f(sm.gam[i] - sm.gam[j]);
-          atv = qacc[r] * dec;
-          if (j < i) av = -sm.beta[i] * dec * gacc[r];
-        }
-        sm.A[i][j] = av;
-        const __bf16 t1 = bf(atv);
-        sm.ath[i][j] = t1;
-        sm.atl[i][j] = bf(atv - fl(t1));
+        av[r] = n4[r];
+        bv[r] = (4 * g + r >= ln) ? t4[r] : 0.f;  // T_bb[4g + r][ln], lower triangular
       }
     }
-  }
-  __syncthreads();
-
-  // Forward substitution, one column of [W | U] per thread.
-  for (int col = tid; col < DK + a.dv; col += 256) {
-    float x[kC];
-    if (col < DK) {
-#pragma unroll
-      for (int i = 0; i < kC; ++i) x[i] = sm.zk[i] * fl(sm.kh[i][col]);
-    } else {
-      const int e = col - DK;
-#pragma unroll
-      for (int i = 0; i < kC; ++i) x[i] = (i < ci.len) ? sm.beta[i] * ldf(vb + int64_t(i) * a.v_st + e) : 0.f;
-    }
-#pragma unroll
-    for (int i = 1; i < kC; ++i) {
-      // four independent partial sums over j, A row read 4 floats at a time
-      float p0 = x[i], p1 = 0.f, p2 = 0.f, p3 = 0.f;
-#pragma unroll
-      for (int j0 = 0; j0 < i; j0 += 4) {
-        const float4 av = *reinterpret_cast<const float4 *>(&sm.A[i][j0]);
-        p0 = fmaf(av.x, x[j0], p0);
-        if (j0 + 1 < i) p1 = fmaf(av.y, x[j0 + 1], p1);
-        if (j0 + 2 < i) p2 = fmaf(av.z, x[j0 + 2], p2);
-        if (j0 + 3 < i) p3 = fmaf(av.w, x[j0 + 3], p3);
-      }
-      x[i] = (p0 + p1) + (p2 + p3);
-    }
-    __bf16 *rh = col < DK ? sm.wth[col] : sm.uth[col - DK];
-    __bf16 *rl = col < DK ? sm.wtl[col] : sm.utl[col - DK];
-#pragma unroll
-    for (int i0 = 0; i0 < kC; i0 += 8) {
-      bf16x8 vh, vl;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        vh[t] = bf(x[i0 + t]);
-        vl[t] = bf(x[i0 + t] - fl(vh[t]));
-      }
-      *reinterpret_cast<bf16x8 *>(rh + i0) = vh;
-      *reinterpret_cast<bf16x8 *>(rl + i0) = vl;
-    }
-  }
-  __syncthreads();
-
-  // Output operators.  Tiles: An (DK/16)^2, Hn (DK/16)(DV/16), Qp 4 (DK/16), Op 4 (DV/16).
-  const WsLayout L(DK, a.dv);
-  char *cell = ws + (static_cast<size_t>(h) * ca.total_chunks + chunk) * L.cell;
-  __bf16 *an_h = reinterpret_cast<__bf16 *>(cell + L.an), *an_l = an_h + DK * DK;
-  __bf16 *qp_h = reinterpret_cast<__bf16 *>(cell + L.qp), *qp_l = qp_h + kC * DK;
-  float *hn = reinterpret_cast<float *>(cell + L.hn);
-  float *op = reinterpret_cast<float *>(cell + L.op);
-  constexpr int TDK = DK / 16, TC = kC / 16;
-  const int tdv = a.dv / 16;
-  const int n_an = TDK * TDK, n_hn = TDK * tdv, n_qp = TC * TDK, n_op = TC * tdv;
-  const int ntiles = n_an + n_hn + n_qp + n_op;
-  const float eC = exp_f(glast);
-  for (int t = w; t < ntiles; t += 4) {
-    int kind, mt, nt;
-    if (t < n_an) { kind = 0; mt = t / TDK; nt = t % TDK; }
-    else if (t < n_an + n_hn) { kind = 1; mt = (t - n_an) / tdv; nt = (t - n_an) % tdv; }
-    else if (t < n_an + n_hn + n_qp) { kind = 2; mt = (t - n_an - n_hn) / TDK; nt = (t - n_an - n_hn) % TDK; }
-    else { kind = 3; mt = (t - n_an - n_hn - n_qp) / tdv; nt = (t - n_an - n_hn - n_qp) % tdv; }
-    // A rows: K~^T rows (kinds 0, 1) or Attn rows (kinds 2, 3); B rows: W^T (0, 2) or U^T (1, 3).
-    const __bf16 *arh = kind < 2 ? sm.kth[16 * mt + ln] : sm.ath[16 * mt + ln];
-    const __bf16 *arl = kind < 2 ? sm.ktl[16 * mt + ln] : sm.atl[16 * mt + ln];
-    const __bf16 *brh = (kind & 1) ? sm.uth[16 * nt + ln] : sm.wth[16 * nt + ln];
-    const __bf16 *brl = (kind & 1) ? sm.utl[16 * nt + ln] : sm.wtl[16 * nt + ln];
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < kC / 32; ++ks) {
-      const int k0 = 32 * ks + 8 * g;
-      acc = mma3<true, true>(rd8(arh, k0), rd8(arl, k0), rd8(brh, k0), rd8(brl, k0), acc);
-    }
+    bf16x4 ah, al, bh, bl;
+    split4(av, ah, al);
+    split4(bv, bh, bl);
+    f32x4 x = {0.f, 0.f, 0.f, 0.f};
+    x = mma16(al, bh, x);
+    x = mma16(ah, bl, x);
+    x = mma16(ah, bh, x);
+    // T_ab = -T_aa X: A = T_aa[ln][4g + r] (stored at NT[16a + 4g + r][16a + ln]), B = X.
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = 16 * mt + 4 * g + r, col = 16 * nt + ln;
-      if (kind == 0) {
-        const float x = (row == col ? eC : 0.f) - acc[r];
-        const __bf16 x1 = bf(x);
-        an_h[row * DK + col] = x1;
-        an_l[row * DK + col] = bf(x - fl(x1));
-      } else if (kind == 1) {
-        hn[row * a.dv + col] = acc[r];
-      } else if (kind == 2) {
-        const float qv = fl(sm.qh[row][col]) * sm.eg[row];
-        const float x = qv - acc[r];
-        const __bf16 x1 = bf(x);
-        qp_h[row * DK + col] = x1;
-        qp_l[row * DK + col] = bf(x - fl(x1));
-      } else {
-        op[row * a.dv + col] = acc[r];
+      const int k = 4 * g + r;
+      av[r] = (k <= ln) ? nt[(16 * a_ + k) * NTS + 16 * a_ + ln] : 0.f;
+      bv[r] = x[r];
+    }
+    split4(av, ah, al);
+    split4(bv, bh, bl);
+    f32x4 y = {0.f, 0.f, 0.f, 0.f};
+    y = mma16(al, bh, y);
+    y = mma16(ah, bl, y);
+    y = mma16(ah, bh, y);
+    // y[r] = (T_aa X)[4g + r][ln] -> T[16a + 4g + r][16b + ln] at NT[16b + ln][16a + 4g + r]
+    *reinterpret_cast<f32x4 *>(nt + (16 * b_ + ln) * NTS + 16 * a_ + 4 * g) = -y;
+  }
+  __syncthreads();
+
+  // ---- phase 5: the 64x64 inverse: T[32:, :32] = -T[32:, 32:] N[32:, :32] T[:32, :32].
+  {
+    const int ti = w >> 1, tj = w & 1;
+    // Y = N[32:, :32] T[:32, :32], tile (ti, tj), K = 32.
+    float av[8], bv[8];
+    {
+      const float *nrow = nt + (32 + 16 * ti + ln) * NTS + 8 * g;
+      const float *trow = nt + (16 * tj + ln) * NTS + 8 * g;  // T[8g + t][16 tj + ln]
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        av[t] = nrow[t];
+        bv[t] = (8 * g + t >= 16 * tj + ln) ? trow[t] : 0.f;
       }
+    }
+    bf16x8 ah, al, bh, bl;
+    split8(av, ah, al);
+    split8(bv, bh, bl);
+    f32x4 y = {0.f, 0.f, 0.f, 0.f};
+    y = mma3<true, true>(ah, al, bh, bl, y);
+    *reinterpret_cast<f32x4 *>(yt + (16 * tj + ln) * 36 + 16 * ti + 4 * g) = y;  // Y^T
+    __syncthreads();
+    // T[32 + 16 ti + m][16 tj + n] = -sum_k T[32 + 16 ti + m][32 + k] Y[k][16 tj + n]
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int k = 8 * g + t;
+      av[t] = (k <= 16 * ti + ln) ? nt[(32 + k) * NTS + 32 + 16 * ti + ln] : 0.f;
+      bv[t] = yt[(16 * tj + ln) * 36 + k];
+    }
+    split8(av, ah, al);
+    split8(bv, bh, bl);
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+    o = mma3<true, true>(ah, al, bh, bl, o);
+    *reinterpret_cast<f32x4 *>(nt + (16 * tj + ln) * NTS + 32 + 16 * ti + 4 * g) = -o;
+  }
+  __syncthreads();
+
+  // ---- phase 6: T^T (bf16 hi/lo), then the transposed K, K~ and V planes.
+  {
+    const int j = tid >> 2, i0 = 16 * (tid & 3);
+    float x[16];
+#pragma unroll
+    for (int t = 0; t < 16; ++t) x[t] = (i0 + t >= j) ? nt[j * NTS + i0 + t] : 0.f;
+    bf16x8 h0, l0, h1, l1;
+    split8(x, h0, l0);
+    split8(x + 8, h1, l1);
+    *reinterpret_cast<bf16x8 *>(tt_h + swz(j, i0)) = h0;
+    *reinterpret_cast<bf16x8 *>(tt_l + swz(j, i0)) = l0;
+    *reinterpret_cast<bf16x8 *>(tt_h + swz(j, i0 + 8)) = h1;
+    *reinterpret_cast<bf16x8 *>(tt_l + swz(j, i0 + 8)) = l1;
+  }
+  const float glast = gam[kC - 1];
+  __syncthreads();  // NT and the K / Q rows are dead from here on
+  if (kval) {
+    const int j = 2 * kp;
+    const float f0 = exp_f(glast - gam[j]), f1 = exp_f(glast - gam[j + 1]);
+    const bf16x8 ka = __builtin_bit_cast(bf16x8, k0r), kb_ = __builtin_bit_cast(bf16x8, k1r);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int d = 8 * kseg + t;
+      *reinterpret_cast<uint32_t *>(kt + swz(d, j)) = pack2(bits(ka[t]), bits(kb_[t]));
+      const float x0 = fl(ka[t]) * f0, x1 = fl(kb_[t]) * f1;
+      const __bf16 h0 = bf(x0), h1 = bf(x1);
+      *reinterpret_cast<uint32_t *>(ktt_h + swz(d, j)) = pack2(bits(h0), bits(h1));
+      *reinterpret_cast<uint32_t *>(ktt_l + swz(d, j)) = pack2(bits(bf(x0 - fl(h0))), bits(bf(x1 - fl(h1))));
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < VP; ++r) {
+    const int p = tid + 256 * r, vp = p / VSEG, vs = p % VSEG;
+    if (vs < a.dv / 8) {
+      const bf16x8 va = __builtin_bit_cast(bf16x8, v0r[r]), vb_ = __builtin_bit_cast(bf16x8, v1r[r]);
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        *reinterpret_cast<uint32_t *>(vt + swz(8 * vs + t, 2 * vp)) = pack2(bits(va[t]), bits(vb_[t]));
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 7: M = [K~^T ; Attn] T, computed as M^T tiles (rows j, columns m) and fed
+  // straight from the accumulators into  Z^T = K^T (diag(beta e^gamma) M^T)  and
+  // Y^T = V^T (diag(beta) M^T).  m-tiles 0 .. DK/16-1 give A_n and H_n, the rest Q' and O'.
+  const WsLayout Lw(DK, a.dv);
+  char *cell = ws + (static_cast<size_t>(h) * ca.total_chunks + chunk) * Lw.cell;
+  __bf16 *an_h = reinterpret_cast<__bf16 *>(cell + Lw.an), *an_l = an_h + DK * DK;
+  __bf16 *qp_h = reinterpret_cast<__bf16 *>(cell + Lw.qp), *qp_l = qp_h + kC * DK;
+  float *hn = reinterpret_cast<float *>(cell + Lw.hn);
+  float *op = reinterpret_cast<float *>(cell + Lw.op);
+  const float eC = exp_f(glast);
+  float sk[4][4], sv[4][4];  // per-row scales of M^T for rows j = 16 jt + 4g + r
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int j = 16 * jt + 4 * g + r;
+      sv[jt][r] = bet[j];
+      sk[jt][r] = bet[j] * exp_f(gam[j]);
+    }
+  constexpr int NMT = DK / 16 + kC / 16;
+  for (int mt = w; mt < NMT; mt += 4) {
+    const bool top = mt < DK / 16;
+    const int lrow = top ? 16 * mt + ln : 16 * (mt - DK / 16) + ln;
+    const __bf16 *Lh = top ? ktt_h : att_h, *Ll = top ? ktt_l : att_l;
+    bf16x8 lh[2], ll[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      lh[ks] = rd8s(Lh, lrow, 32 * ks + 8 * g);
+      ll[ks] = rd8s(Ll, lrow, 32 * ks + 8 * g);
+    }
+    bf16x4 mkh[4], mkl[4], mvh[4], mvl[4];
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        if (ks == 0 && jt >= 2) continue;  // T^T rows j >= 32 vanish on columns i < 32
+        acc = mma3<true, true>(rd8s(tt_h, 16 * jt + ln, 32 * ks + 8 * g), rd8s(tt_l, 16 * jt + ln, 32 * ks + 8 * g),
+                               lh[ks], ll[ks], acc);
+      }
+      float xk[4], xv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        xk[r] = acc[r] * sk[jt][r];
+        xv[r] = acc[r] * sv[jt][r];
+      }
+      split4(xk, mkh[jt], mkl[jt]);
+      split4(xv, mvh[jt], mvl[jt]);
+    }
+    bf16x8 bkh[2], bkl[2], bvh[2], bvl[2];
+#pragma unroll
+    for (int jp = 0; jp < 2; ++jp) {
+      bkh[jp] = __builtin_shufflevector(mkh[2 * jp], mkh[2 * jp + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+      bkl[jp] = __builtin_shufflevector(mkl[2 * jp], mkl[2 * jp + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+      bvh[jp] = __builtin_shufflevector(mvh[2 * jp], mvh[2 * jp + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+      bvl[jp] = __builtin_shufflevector(mvl[2 * jp], mvl[2 * jp + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+    const int mrow = 16 * (top ? mt : mt - DK / 16) + ln;  // d' (top) or i' (bottom)
+#pragma unroll
+    for (int dt = 0; dt < DK / 16; ++dt) {
+      f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int jp = 0; jp < 2; ++jp) {
+        const bf16x8 ak = rd_perm_s(kt, 16 * dt + ln, 32 * jp, g);
+        z = mma(ak, bkl[jp], z);
+        z = mma(ak, bkh[jp], z);
+      }
+      // z[r] = Z^T[16 dt + 4g + r][m]:  (M_k K)[m][d]
+      const int col = 16 * dt + 4 * g;
+      float x[4];
+      if (top) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[r] = (col + r == mrow ? eC : 0.f) - z[r];
+        bf16x4 hv, lv;
+        split4(x, hv, lv);
+        *reinterpret_cast<bf16x4 *>(an_h + mrow * DK + col) = hv;
+        *reinterpret_cast<bf16x4 *>(an_l + mrow * DK + col) = lv;
+      } else {
+        float qv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (mrow < ci.len) {
+          const bf16x4 q4 = *reinterpret_cast<const bf16x4 *>(qb + int64_t(mrow) * a.q_st + col);
+          const float e = exp_f(gam[mrow]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) qv[r] = fl(q4[r]) * e;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[r] = qv[r] - z[r];
+        bf16x4 hv, lv;
+        split4(x, hv, lv);
+        *reinterpret_cast<bf16x4 *>(qp_h + mrow * DK + col) = hv;
+        *reinterpret_cast<bf16x4 *>(qp_l + mrow * DK + col) = lv;
+      }
+    }
+    float *orow = (top ? hn : op) + static_cast<size_t>(mrow) * a.dv;
+    for (int et = 0; et < a.dv / 16; ++et) {
+      f32x4 y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int jp = 0; jp < 2; ++jp) {
+        const bf16x8 avv = rd_perm_s(vt, 16 * et + ln, 32 * jp, g);
+        y = mma(avv, bvl[jp], y);
+        y = mma(avv, bvh[jp], y);
+      }
+      *reinterpret_cast<f32x4 *>(orow + 16 * et + 4 * g) = y;
     }
   }
 }
@@ -474,7 +706,7 @@ __global__ void __launch_bounds__(256) gdn_scan_mfma(GdnArgs a, ChunkArgs ca, co
 
 template <int DK, int DV>
 int launch_prep(const GdnArgs &a, const ChunkArgs &ca, char *ws, hipStream_t s) {
-  const size_t smem = sizeof(PrepSmem<DK, DV>);
+  const size_t smem = PrepLayout<DK, DV>::bytes;
   auto kern = gdn_prep_mfma<DK, DV>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
@@ -514,12 +746,15 @@ size_t chunk_mfma_workspace_bytes(int H, int dk, int dv, int total_chunks) {
   return WsLayout(dk, dv).cell * static_cast<size_t>(H) * total_chunks;
 }
 
-int launch_chunk_mfma(const GdnArgs &a, const ChunkArgs &ca, void *workspace, int in_dtype, hipStream_t s) {
-  if (in_dtype != MOTIF_BF16) return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_chunk MFMA path takes bf16 inputs");
-  // 16-byte row loads of q / k
-  const int64_t st = a.q_sb | a.q_sh | a.q_st | a.k_sb | a.k_sh | a.k_st;
-  if ((st & 7) || ((reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.k)) & 15))
-    return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_chunk MFMA path needs 16-byte aligned q / k rows");
+bool chunk_mfma_eligible(const GdnArgs &a, int chunk, int in_dtype, int out_dtype) {
+  if (in_dtype != MOTIF_BF16 || out_dtype != MOTIF_BF16 || !chunk_mfma_supported(a.dk, a.dv, chunk)) return false;
+  // 16-byte row loads of q / k / v
+  const int64_t st = a.q_sb | a.q_sh | a.q_st | a.k_sb | a.k_sh | a.k_st | a.v_sb | a.v_sh | a.v_st;
+  const uintptr_t p = reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.k) | reinterpret_cast<uintptr_t>(a.v);
+  return (st & 7) == 0 && (p & 15) == 0;
+}
+
+int launch_chunk_mfma(const GdnArgs &a, const ChunkArgs &ca, void *workspace, hipStream_t s) {
   char *ws = static_cast<char *>(workspace);
   return a.dk == 32 ? launch_dk<32>(a, ca, ws, s) : launch_dk<64>(a, ca, ws, s);
 }

@@ -62,6 +62,8 @@ __device__ __forceinline__ ChunkInfo resolve_chunk(int c, int C, int L, const Ch
 // MFMA chunk path (gdn_chunk.hip): chunk 64, dk in {32, 64}, dv % 16 == 0, dv <= 128.
 bool chunk_mfma_supported(int dk, int dv, int chunk);
 size_t chunk_mfma_workspace_bytes(int H, int dk, int dv, int total_chunks);
-int launch_chunk_mfma(const GdnArgs &a, const ChunkArgs &ca, void *workspace, int in_dtype, hipStream_t s);
+// bf16 in and out, supported shape, 16-byte aligned q / k / v rows.
+bool chunk_mfma_eligible(const GdnArgs &a, int chunk, int in_dtype, int out_dtype);
+int launch_chunk_mfma(const GdnArgs &a, const ChunkArgs &ca, void *workspace, hipStream_t s);
 
 }  // namespace motif
