@@ -1,25 +1,29 @@
 // GDN chunked prefill on bf16 MFMA (gfx950), chunk length 64.
 //
-// Two kernels.  gdn_prep_mfma runs one workgroup per (chunk, head) and does all
+// Three kernels.  gdn_prep_mfma runs one workgroup per (chunk, head) and does all
 // the work that does not depend on the carried state: gamma = cumsum(g),
-// G = K K^T and Q K^T on MFMA, A = -strict(beta G * D), W and U by forward
-// substitution (I - A) [W | U] = [beta e^gamma K | beta V], and then the chunk
-// transition and output operators on MFMA:
+// N = strict(beta K K^T * D) and Attn = (Q K^T) * D on MFMA, T = (I + N)^{-1} by a
+// blocked inverse (16x16 diagonal blocks by substitution, then 32 and 64 by
+// T_ab = -T_aa N_ab T_bb products), and the chunk transition and output operators
 //   A_n = e^{gamma_C} I - K~^T W      (dk x dk)      K~ = K e^{gamma_C - gamma}
-//   H_n = K~^T U                      (dk x dv)
-//   Q'  = Q e^{gamma} - Attn W        (C x dk)       Attn = (Q K^T) * D
+//   H_n = K~^T U                      (dk x dv)      W = T beta e^gamma K, U = T beta V
+//   Q'  = Q e^{gamma} - Attn W        (C x dk)
 //   O'  = Attn U                      (C x dv)
 // so that for the state S_n entering chunk n
 //   S_{n+1} = A_n S_n + H_n,   O_n = O' + Q' S_n.
-// gdn_scan_mfma then carries S across the chunks: one workgroup per (64-column
-// value tile, head, sequence), one wave per 16 columns, S held in MFMA
-// accumulator layout in registers; each chunk is one A_n S and one Q' S product
-// (next chunk's operators prefetched into LDS while the current one computes).
+// gdn_state_scan carries S across the chunks, one wavefront per (16 state columns,
+// head, sequence) with S in accumulator registers and a three-chunk-deep register
+// prefetch of A_n / H_n; it writes every S_n as MFMA operands.  gdn_chunk_out then
+// forms O_n = O' + Q' S_n for all chunks in parallel.
 //
-// Inputs are bf16 (exact as MFMA operands).  fp32-derived operands (T-solved W
-// and U, Attn, K~, A_n, Q', the state) are split into bf16 hi + lo and products
-// take three MFMA passes (hi.hi + hi.lo + lo.hi, fp32 accumulation): about 16
-// mantissa bits per product, fp32 accumulation everywhere.
+// The workspace holds A_n, Q', H_n, O' and S_n in the order the consuming kernel's
+// lanes read them (one 16-byte piece per lane per operand tile), so every load of
+// the two scan kernels is a coalesced 1 KB wavefront access with no LDS staging.
+//
+// Inputs are bf16 (exact as MFMA operands).  fp32-derived operands (T, N, Attn, K~,
+// M, A_n, Q', the state) are split into bf16 hi + lo and their products take three
+// MFMA passes (hi.hi + hi.lo + lo.hi, fp32 accumulation), products with an exact
+// bf16 operand two: about 16 mantissa bits per product, fp32 accumulation throughout.
 #include "gdn_internal.h"
 
 namespace motif {
@@ -66,16 +70,23 @@ __device__ __forceinline__ bf16x8 rd_perm(const __bf16 *row, int k0, int g) {
 
 template <typename T> __device__ __forceinline__ float ldf(const T *p) { return ld(p); }
 
-// Workspace layout per (head, chunk) cell: An hi/lo [dk][dk] bf16, Qp hi/lo
-// [C][dk] bf16, Hn [dk][dv] fp32, Op [C][dv] fp32.
+// Workspace per (head, chunk) cell, every piece 16 bytes per lane of a 64-lane tile:
+//   an [2 planes][DK/16 mt][DK/32 ks][64]  bf16x8  A_n rows 16 mt + (l % 16), k slots
+//                                                  32 ks + 4 (l / 16) + {0..3, 16..19}
+//   qp [2][4][DK/32][64]                   bf16x8  Q' in the same operand order
+//   hn [dv/16 cg][DK/16 mt][64]            f32x4   H_n[16 mt + 4 (l / 16) + r][16 cg + l % 16]
+//   op [dv/16 cg][4 mt][64]                f32x4   O'[16 mt + l % 16][16 cg + 4 (l / 16) + r]
+//   sn [dv/16 cg][DK/32 ks][2 planes][64]  bf16x8  S_n rows 32 ks + 4 (l / 16) + {0..3, 16..19},
+//                                                  column 16 cg + l % 16
 struct WsLayout {
-  size_t an, qp, hn, op, cell;
+  size_t an, qp, hn, op, sn, cell;
   __host__ __device__ WsLayout(int dk, int dv) {
     an = 0;
     qp = an + 2ull * dk * dk * 2;
     hn = qp + 2ull * kC * dk * 2;
     op = hn + 4ull * dk * dv;
-    cell = op + 4ull * kC * dv;
+    sn = op + 4ull * kC * dv;
+    cell = sn + 4ull * dk * dv;
   }
 };
 
@@ -399,11 +410,9 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
 
   // ---- phase 7: M = [K~^T ; Attn] T, computed as M^T tiles (rows j, columns m) and fed
   // straight from the accumulators into  Z^T = K^T (diag(beta e^gamma) M^T)  and
-  // Y^T = V^T (diag(beta) M^T).  m-tiles 0 .. DK/16-1 give A_n and H_n, the rest Q' and O'.
+  // Y = (M diag(beta)) V  (or Y^T).  m-tiles 0 .. DK/16-1 give A_n and H_n, the rest Q' and O'.
   const WsLayout Lw(DK, a.dv);
   char *cell = ws + (static_cast<size_t>(h) * ca.total_chunks + chunk) * Lw.cell;
-  __bf16 *an_h = reinterpret_cast<__bf16 *>(cell + Lw.an), *an_l = an_h + DK * DK;
-  __bf16 *qp_h = reinterpret_cast<__bf16 *>(cell + Lw.qp), *qp_l = qp_h + kC * DK;
   float *hn = reinterpret_cast<float *>(cell + Lw.hn);
   float *op = reinterpret_cast<float *>(cell + Lw.op);
   const float eC = exp_f(glast);
@@ -455,6 +464,7 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
       bvl[jp] = __builtin_shufflevector(mvl[2 * jp], mvl[2 * jp + 1], 0, 1, 2, 3, 4, 5, 6, 7);
     }
     const int mrow = 16 * (top ? mt : mt - DK / 16) + ln;  // d' (top) or i' (bottom)
+    const int mti = top ? mt : mt - DK / 16;                 // row tile inside A_n / Q'
 #pragma unroll
     for (int dt = 0; dt < DK / 16; ++dt) {
       f32x4 z = {0.f, 0.f, 0.f, 0.f};
@@ -464,16 +474,12 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
         z = mma(ak, bkl[jp], z);
         z = mma(ak, bkh[jp], z);
       }
-      // z[r] = Z^T[16 dt + 4g + r][m]:  (M_k K)[m][d]
+      // z[r] = Z^T[16 dt + 4g + r][m] = (M_k K)[m][16 dt + 4g + r]
       const int col = 16 * dt + 4 * g;
       float x[4];
       if (top) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) x[r] = (col + r == mrow ? eC : 0.f) - z[r];
-        bf16x4 hv, lv;
-        split4(x, hv, lv);
-        *reinterpret_cast<bf16x4 *>(an_h + mrow * DK + col) = hv;
-        *reinterpret_cast<bf16x4 *>(an_l + mrow * DK + col) = lv;
       } else {
         float qv[4] = {0.f, 0.f, 0.f, 0.f};
         if (mrow < ci.len) {
@@ -484,223 +490,207 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) x[r] = qv[r] - z[r];
-        bf16x4 hv, lv;
-        split4(x, hv, lv);
-        *reinterpret_cast<bf16x4 *>(qp_h + mrow * DK + col) = hv;
-        *reinterpret_cast<bf16x4 *>(qp_l + mrow * DK + col) = lv;
       }
+      bf16x4 hv, lv;
+      split4(x, hv, lv);
+      // operand order: tile (plane, mti, ks = dt / 2), lane, half dt % 2
+      char *base = cell + (top ? Lw.an : Lw.qp);
+      const int ntile = top ? DK / 16 : kC / 16;
+      const size_t o_h = ((static_cast<size_t>(0 * ntile + mti) * (DK / 32) + dt / 2) * 64 + lane) * 16 + 8 * (dt & 1);
+      const size_t o_l = ((static_cast<size_t>(1 * ntile + mti) * (DK / 32) + dt / 2) * 64 + lane) * 16 + 8 * (dt & 1);
+      *reinterpret_cast<bf16x4 *>(base + o_h) = hv;
+      *reinterpret_cast<bf16x4 *>(base + o_l) = lv;
     }
-    float *orow = (top ? hn : op) + static_cast<size_t>(mrow) * a.dv;
+    // H_n as Y = M_v V (accumulator layout of the state), O' as Y^T (layout of O^T).
     for (int et = 0; et < a.dv / 16; ++et) {
       f32x4 y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int jp = 0; jp < 2; ++jp) {
         const bf16x8 avv = rd_perm_s(vt, 16 * et + ln, 32 * jp, g);
-        y = mma(avv, bvl[jp], y);
-        y = mma(avv, bvh[jp], y);
+        if (top) {
+          y = mma(bvl[jp], avv, y);
+          y = mma(bvh[jp], avv, y);
+        } else {
+          y = mma(avv, bvl[jp], y);
+          y = mma(avv, bvh[jp], y);
+        }
       }
-      *reinterpret_cast<f32x4 *>(orow + 16 * et + 4 * g) = y;
+      float *dst = top ? hn + (static_cast<size_t>(et) * (DK / 16) + mti) * 256
+                       : op + (static_cast<size_t>(et) * (kC / 16) + mti) * 256;
+      *reinterpret_cast<f32x4 *>(dst + 4 * lane) = y;
     }
   }
 }
 
-// ------------------------------------------------------------------ scan
+// ------------------------------------------------------------------ state scan
 template <int DK>
-struct ScanSmem {
-  __bf16 anh[2][DK][DK + kPad], anl[2][DK][DK + kPad];  // A_n hi / lo
-  __bf16 qph[2][kC][DK + kPad], qpl[2][kC][DK + kPad];  // Q' hi / lo
-  float hn[2][DK][64 + 4];                              // H_n, this workgroup's 64 columns
-  float op[2][kC][64 + 4];                              // O', this workgroup's 64 columns
+struct ScanStage {
+  uint4 an[2][DK / 16][DK / 32];  // A_n hi / lo operands
+  f32x4 hn[DK / 16];              // H_n, accumulator layout
 };
 
-template <typename TO, int DK>
-__global__ void __launch_bounds__(256) gdn_scan_mfma(GdnArgs a, ChunkArgs ca, const char *ws) {
-  constexpr int TDK = DK / 16;  // state row tiles
-  constexpr int KS = DK / 32;   // k-steps over the state rows
-  constexpr int N_AN = DK * DK / 8, N_QP = kC * DK / 8;  // 16-byte pieces per bf16 plane
-  constexpr int N_HN = DK * 16, N_OP = kC * 16;          // 16-byte pieces of the fp32 tiles
-  constexpr int PIECES = 2 * N_AN + 2 * N_QP + N_HN + N_OP;
-  constexpr int PER_T = (PIECES + 255) / 256;
-  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
-  ScanSmem<DK> &sm = *reinterpret_cast<ScanSmem<DK> *>(smem_raw);
+template <int DK>
+__device__ __forceinline__ void scan_load(ScanStage<DK> &st, const char *cell, const WsLayout &Lw, int cg, int lane) {
+  const uint4 *an = reinterpret_cast<const uint4 *>(cell + Lw.an) + lane;
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int mt = 0; mt < DK / 16; ++mt)
+#pragma unroll
+      for (int ks = 0; ks < DK / 32; ++ks) st.an[p][mt][ks] = an[((p * (DK / 16) + mt) * (DK / 32) + ks) * 64];
+  const f32x4 *hn = reinterpret_cast<const f32x4 *>(cell + Lw.hn) + static_cast<size_t>(cg) * (DK / 16) * 64 + lane;
+#pragma unroll
+  for (int mt = 0; mt < DK / 16; ++mt) st.hn[mt] = hn[mt * 64];
+}
 
-  const int tile = blockIdx.x, h = blockIdx.y, sq = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int ln = lane & 15, g = lane >> 4;
-  const int c_base = tile * 64;
-  const int col = c_base + 16 * w + ln;
-  const bool active = c_base + 16 * w < a.dv;  // wave-uniform
+// One wavefront per (16 state columns, head, sequence).  S[mt][r] = S[16 mt + 4g + r][16 cg + l % 16].
+template <int DK>
+__global__ void __launch_bounds__(64) gdn_state_scan(GdnArgs a, ChunkArgs ca, char *ws) {
+  constexpr int TDK = DK / 16, KS = DK / 32;
+  const int cg = blockIdx.x, h = blockIdx.y, sq = blockIdx.z;
+  const int lane = threadIdx.x, ln = lane & 15, g = lane >> 4;
+  const int col = 16 * cg + ln;
 
-  int first, count, batch, t_begin, t_end;
+  int first, count;
   if (ca.cu == nullptr) {
-    batch = sq; first = sq * ca.nper; count = ca.nper; t_begin = 0; t_end = a.L;
+    first = sq * ca.nper;
+    count = ca.nper;
   } else {
-    batch = 0; first = ca.coff[sq]; count = ca.coff[sq + 1] - first; t_begin = ca.cu[sq]; t_end = ca.cu[sq + 1];
+    first = ca.coff[sq];
+    count = ca.coff[sq + 1] - first;
   }
   const WsLayout Lw(DK, a.dv);
-  const char *cell0 = ws + (static_cast<size_t>(h) * ca.total_chunks + first) * Lw.cell;
+  char *cell0 = ws + (static_cast<size_t>(h) * ca.total_chunks + first) * Lw.cell;
 
-  // Each thread's staging pieces: byte offset inside a workspace cell and inside one
-  // LDS buffer (both fixed across chunks); pieces of columns past dv are skipped.
-  constexpr size_t BUF = sizeof(ScanSmem<DK>) / 2;  // the buffers interleave per array; offsets below
-  uint32_t src_off[PER_T], dst_off[PER_T];
-  uint32_t valid = 0;
-#pragma unroll
-  for (int r = 0; r < PER_T; ++r) {
-    int p = tid + 256 * r;
-    uint32_t so = 0, dof = 0;
-    bool ok = p < PIECES;
-    if (p < 2 * N_AN) {
-      const int plane = p / N_AN, q = p % N_AN;
-      so = Lw.an + p * 16;
-      dof = static_cast<uint32_t>(reinterpret_cast<char *>((plane ? sm.anl[0] : sm.anh[0])[q / (DK / 8)] + 8 * (q % (DK / 8))) - smem_raw);
-    } else if ((p -= 2 * N_AN) < 2 * N_QP) {
-      const int plane = p / N_QP, q = p % N_QP;
-      so = Lw.qp + p * 16;
-      dof = static_cast<uint32_t>(reinterpret_cast<char *>((plane ? sm.qpl[0] : sm.qph[0])[q / (DK / 8)] + 8 * (q % (DK / 8))) - smem_raw);
-    } else if ((p -= 2 * N_QP) < N_HN) {
-      const int row = p / 16, c4 = p % 16;
-      ok = ok && c_base + 4 * c4 < a.dv;
-      so = Lw.hn + (static_cast<uint32_t>(row) * a.dv + c_base + 4 * c4) * 4;
-      dof = static_cast<uint32_t>(reinterpret_cast<char *>(&sm.hn[0][row][4 * c4]) - smem_raw);
-    } else if ((p -= N_HN) < N_OP) {
-      const int row = p / 16, c4 = p % 16;
-      ok = ok && c_base + 4 * c4 < a.dv;
-      so = Lw.op + (static_cast<uint32_t>(row) * a.dv + c_base + 4 * c4) * 4;
-      dof = static_cast<uint32_t>(reinterpret_cast<char *>(&sm.op[0][row][4 * c4]) - smem_raw);
-    }
-    src_off[r] = so;
-    dst_off[r] = dof;
-    valid |= ok ? (1u << r) : 0u;
-  }
-  // Byte distance between buffer 0 and buffer 1 of each array (identical for all arrays
-  // only if laid out [2][...]; computed per array class below).
-  const uint32_t d_an = static_cast<uint32_t>(reinterpret_cast<char *>(sm.anh[1]) - reinterpret_cast<char *>(sm.anh[0]));
-  const uint32_t d_qp = static_cast<uint32_t>(reinterpret_cast<char *>(sm.qph[1]) - reinterpret_cast<char *>(sm.qph[0]));
-  const uint32_t d_hn = static_cast<uint32_t>(reinterpret_cast<char *>(sm.hn[1]) - reinterpret_cast<char *>(sm.hn[0]));
-  const uint32_t d_op = static_cast<uint32_t>(reinterpret_cast<char *>(sm.op[1]) - reinterpret_cast<char *>(sm.op[0]));
-  uint32_t dbuf[PER_T];
-#pragma unroll
-  for (int r = 0; r < PER_T; ++r) {
-    const int p = tid + 256 * r;
-    dbuf[r] = p < 2 * N_AN ? d_an : p < 2 * N_AN + 2 * N_QP ? d_qp : p < 2 * N_AN + 2 * N_QP + N_HN ? d_hn : d_op;
-  }
-  (void)BUF;
-
-  uint4 stg[PER_T];
-  auto stage_load = [&](int n) {
-    const char *c = cell0 + static_cast<size_t>(n) * Lw.cell;
-#pragma unroll
-    for (int r = 0; r < PER_T; ++r)
-      stg[r] = (valid >> r) & 1 ? *reinterpret_cast<const uint4 *>(c + src_off[r]) : uint4{0, 0, 0, 0};
-  };
-  auto stage_store = [&](int buf) {
-#pragma unroll
-    for (int r = 0; r < PER_T; ++r)
-      if (tid + 256 * r < PIECES)
-        *reinterpret_cast<uint4 *>(smem_raw + dst_off[r] + (buf ? dbuf[r] : 0)) = stg[r];
-  };
-
-  // State S[:, col] in accumulator layout: S[mt][r] = S[16 mt + 4 g + r][col].
   f32x4 S[TDK];
   const size_t sbase = (static_cast<size_t>(sq) * a.H + h) * DK * a.dv;
 #pragma unroll
   for (int mt = 0; mt < TDK; ++mt)
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      S[mt][r] = (active && a.s_in) ? a.s_in[sbase + static_cast<size_t>(16 * mt + 4 * g + r) * a.dv + col] : 0.f;
+      S[mt][r] = a.s_in ? a.s_in[sbase + static_cast<size_t>(16 * mt + 4 * g + r) * a.dv + col] : 0.f;
 
-  TO *ob = static_cast<TO *>(a.o) + batch * a.o_sb + h * a.o_sh;
-  const int lc = 16 * w + ln;  // column inside the workgroup tile
-
+  ScanStage<DK> s0, s1, s2;
   if (count > 0) {
-    stage_load(0);
-    stage_store(0);
+    scan_load<DK>(s0, cell0, Lw, cg, lane);
+    scan_load<DK>(s1, cell0 + static_cast<size_t>(min(1, count - 1)) * Lw.cell, Lw, cg, lane);
+    scan_load<DK>(s2, cell0 + static_cast<size_t>(min(2, count - 1)) * Lw.cell, Lw, cg, lane);
   }
-  __syncthreads();
 
-  for (int n = 0; n < count; ++n) {
-    const int buf = n & 1;
-    const bool more = n + 1 < count;
-    if (more) stage_load(n + 1);
-    if (active) {
-      // Operands first (LDS reads in flight together), then the MFMA passes
-      // interleaved over independent tiles.
-      bf16x8 anh[TDK][KS], anl[TDK][KS], qph[kC / 16][KS], qpl[kC / 16][KS];
+  // S_n as hi / lo operands (stored for the output kernel), then S_{n+1} = A_n S_n + H_n;
+  // the stage is then refilled with chunk min(n + 3, count - 1) (a repeat load of the
+  // last chunk near the end keeps the main loop free of branches, so the loads of the
+  // two other stages stay in flight across it).
+  auto step = [&](ScanStage<DK> &st, int n) {
+    char *cell = cell0 + static_cast<size_t>(n) * Lw.cell;
+    bf16x8 sh[KS], sl[KS];
 #pragma unroll
-      for (int mt = 0; mt < TDK; ++mt)
+    for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          anh[mt][ks] = rd_perm(sm.anh[buf][16 * mt + ln], 32 * ks, g);
-          anl[mt][ks] = rd_perm(sm.anl[buf][16 * mt + ln], 32 * ks, g);
-        }
-      f32x4 sacc[TDK], oacc[kC / 16];
-#pragma unroll
-      for (int mt = 0; mt < TDK; ++mt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sacc[mt][r] = sm.hn[buf][16 * mt + 4 * g + r][lc];
-#pragma unroll
-      for (int mt = 0; mt < kC / 16; ++mt)
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          qph[mt][ks] = rd_perm(sm.qph[buf][16 * mt + ln], 32 * ks, g);
-          qpl[mt][ks] = rd_perm(sm.qpl[buf][16 * mt + ln], 32 * ks, g);
-        }
-#pragma unroll
-      for (int mt = 0; mt < kC / 16; ++mt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) oacc[mt][r] = sm.op[buf][16 * mt + 4 * g + r][lc];
-      // B operands from S: k-step ks covers state rows 32 ks .. 32 ks + 31.
-      bf16x8 sh[KS], sl[KS];
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float x = S[2 * ks + i / 4][i % 4];
-          sh[ks][i] = bf(x);
-          sl[ks][i] = bf(x - fl(sh[ks][i]));
-        }
-      // S_{n+1} = H_n + A_n S_n ; O_n = O' + Q' S_n   (small passes first)
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-        for (int mt = 0; mt < TDK; ++mt) sacc[mt] = mma(anl[mt][ks], sh[ks], sacc[mt]);
-#pragma unroll
-        for (int mt = 0; mt < TDK; ++mt) sacc[mt] = mma(anh[mt][ks], sl[ks], sacc[mt]);
-#pragma unroll
-        for (int mt = 0; mt < TDK; ++mt) sacc[mt] = mma(anh[mt][ks], sh[ks], sacc[mt]);
+      for (int i = 0; i < 8; ++i) {
+        const float x = S[2 * ks + i / 4][i % 4];
+        sh[ks][i] = bf(x);
+        sl[ks][i] = bf(x - fl(sh[ks][i]));
       }
+    uint4 *sn = reinterpret_cast<uint4 *>(cell + Lw.sn) + static_cast<size_t>(cg) * KS * 2 * 64 + lane;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-        for (int mt = 0; mt < kC / 16; ++mt) oacc[mt] = mma(qpl[mt][ks], sh[ks], oacc[mt]);
-#pragma unroll
-        for (int mt = 0; mt < kC / 16; ++mt) oacc[mt] = mma(qph[mt][ks], sl[ks], oacc[mt]);
-#pragma unroll
-        for (int mt = 0; mt < kC / 16; ++mt) oacc[mt] = mma(qph[mt][ks], sh[ks], oacc[mt]);
-      }
-#pragma unroll
-      for (int mt = 0; mt < TDK; ++mt) S[mt] = sacc[mt];
-      const int t0 = t_begin + n * kC;
-      const int len = min(kC, t_end - t0);
-#pragma unroll
-      for (int mt = 0; mt < kC / 16; ++mt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = 16 * mt + 4 * g + r;
-          if (i < len) st(ob + int64_t(t0 + i) * a.o_st + col, oacc[mt][r]);
-        }
+    for (int ks = 0; ks < KS; ++ks) {
+      sn[(2 * ks) * 64] = __builtin_bit_cast(uint4, sh[ks]);
+      sn[(2 * ks + 1) * 64] = __builtin_bit_cast(uint4, sl[ks]);
     }
-    if (more) stage_store(buf ^ 1);
-    __syncthreads();
+    f32x4 acc[TDK];
+#pragma unroll
+    for (int mt = 0; mt < TDK; ++mt) acc[mt] = st.hn[mt];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+      for (int mt = 0; mt < TDK; ++mt) acc[mt] = mma(__builtin_bit_cast(bf16x8, st.an[1][mt][ks]), sh[ks], acc[mt]);
+#pragma unroll
+      for (int mt = 0; mt < TDK; ++mt) acc[mt] = mma(__builtin_bit_cast(bf16x8, st.an[0][mt][ks]), sl[ks], acc[mt]);
+#pragma unroll
+      for (int mt = 0; mt < TDK; ++mt) acc[mt] = mma(__builtin_bit_cast(bf16x8, st.an[0][mt][ks]), sh[ks], acc[mt]);
+    }
+#pragma unroll
+    for (int mt = 0; mt < TDK; ++mt) S[mt] = acc[mt];
+    scan_load<DK>(st, cell0 + static_cast<size_t>(min(n + 3, count - 1)) * Lw.cell, Lw, cg, lane);
+  };
+  int n = 0;
+  for (; n + 3 <= count; n += 3) {
+    step(s0, n);
+    step(s1, n + 1);
+    step(s2, n + 2);
   }
+  if (n < count) step(s0, n);
+  if (n + 1 < count) step(s1, n + 1);
 
-  if (active) {
 #pragma unroll
-    for (int mt = 0; mt < TDK; ++mt)
+  for (int mt = 0; mt < TDK; ++mt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        a.s_out[sbase + static_cast<size_t>(16 * mt + 4 * g + r) * a.dv + col] = S[mt][r];
+    for (int r = 0; r < 4; ++r)
+      a.s_out[sbase + static_cast<size_t>(16 * mt + 4 * g + r) * a.dv + col] = S[mt][r];
+}
+
+// ------------------------------------------------------------------ chunk output
+// O_n = O' + Q' S_n for every chunk in parallel, computed transposed so that each lane
+// ends with four consecutive columns of one row: O^T = S_n^T Q'^T, accumulator
+// lane l holding O[16 mt + l % 16][16 cg + 4 (l / 16) + r].
+template <typename TO, int DK>
+__global__ void __launch_bounds__(256) gdn_chunk_out(GdnArgs a, ChunkArgs ca, const char *ws, int vec_store) {
+  constexpr int KS = DK / 32;
+  const int chunk = blockIdx.x, h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int ln = lane & 15, g = lane >> 4;
+  const ChunkInfo ci = resolve_chunk(chunk, kC, a.L, ca);
+  const WsLayout Lw(DK, a.dv);
+  const char *cell = ws + (static_cast<size_t>(h) * ca.total_chunks + chunk) * Lw.cell;
+
+  bf16x8 qh[4][KS], ql[4][KS];
+  const uint4 *qp = reinterpret_cast<const uint4 *>(cell + Lw.qp) + lane;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qh[mt][ks] = __builtin_bit_cast(bf16x8, qp[((0 * 4 + mt) * KS + ks) * 64]);
+      ql[mt][ks] = __builtin_bit_cast(bf16x8, qp[((1 * 4 + mt) * KS + ks) * 64]);
+    }
+  TO *ob = static_cast<TO *>(a.o) + ci.batch * a.o_sb + h * a.o_sh + int64_t(ci.t0) * a.o_st;
+  for (int cg = w; cg < a.dv / 16; cg += 4) {
+    const uint4 *sn = reinterpret_cast<const uint4 *>(cell + Lw.sn) + static_cast<size_t>(cg) * KS * 2 * 64 + lane;
+    const f32x4 *op = reinterpret_cast<const f32x4 *>(cell + Lw.op) + static_cast<size_t>(cg) * 4 * 64 + lane;
+    bf16x8 sh[KS], sl[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      sh[ks] = __builtin_bit_cast(bf16x8, sn[(2 * ks) * 64]);
+      sl[ks] = __builtin_bit_cast(bf16x8, sn[(2 * ks + 1) * 64]);
+    }
+    f32x4 acc[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) acc[mt] = op[mt * 64];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) acc[mt] = mma(sl[ks], qh[mt][ks], acc[mt]);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) acc[mt] = mma(sh[ks], ql[mt][ks], acc[mt]);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) acc[mt] = mma(sh[ks], qh[mt][ks], acc[mt]);
+    }
+    const int c0 = 16 * cg + 4 * g;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int row = 16 * mt + ln;
+      if (row >= ci.len) continue;
+      TO *dst = ob + int64_t(row) * a.o_st + c0;
+      if (vec_store) {
+        bf16x4 v;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = bf(acc[mt][r]);
+        *reinterpret_cast<bf16x4 *>(dst) = v;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) st(dst + r, acc[mt][r]);
+      }
+    }
   }
 }
 
@@ -715,25 +705,19 @@ int launch_prep(const GdnArgs &a, const ChunkArgs &ca, char *ws, hipStream_t s) 
   return check_launch("gdn_prep_mfma");
 }
 
-template <typename TO, int DK>
-int launch_scan(const GdnArgs &a, const ChunkArgs &ca, const char *ws, hipStream_t s) {
-  const size_t smem = sizeof(ScanSmem<DK>);
-  auto kern = gdn_scan_mfma<TO, DK>;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
-  if (e != hipSuccess) return set_error(MOTIF_ERR_HIP, std::string("gdn_scan_mfma smem: ") + hipGetErrorString(e));
-  kern<<<dim3((a.dv + 63) / 64, a.H, ca.nseq), dim3(256), smem, s>>>(a, ca, ws);
-  return check_launch("gdn_scan_mfma");
-}
-
 template <int DK>
 int launch_dk(const GdnArgs &a, const ChunkArgs &ca, char *ws, hipStream_t s) {
   int rc;
-  // the prep's U^T plane is sized for the padded dv bound of its template
+  // the prep's V^T plane is sized for the padded dv bound of its template
   if (a.dv <= 64) rc = launch_prep<DK, 64>(a, ca, ws, s);
   else rc = launch_prep<DK, 128>(a, ca, ws, s);
   if (rc) return rc;
-  return launch_scan<bf16_t, DK>(a, ca, ws, s);
+  gdn_state_scan<DK><<<dim3(a.dv / 16, a.H, ca.nseq), dim3(64), 0, s>>>(a, ca, ws);
+  if ((rc = check_launch("gdn_state_scan"))) return rc;
+  // 8-byte output stores when every row start is 8-byte aligned
+  const int vec = ((a.o_sb | a.o_sh | a.o_st) & 3) == 0 && (reinterpret_cast<uintptr_t>(a.o) & 7) == 0;
+  gdn_chunk_out<bf16_t, DK><<<dim3(ca.total_chunks, a.H), dim3(256), 0, s>>>(a, ca, ws, vec);
+  return check_launch("gdn_chunk_out");
 }
 
 }  // namespace
