@@ -46,6 +46,10 @@ __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_lo
 // exp(x) through the hardware exp2 with the argument pre-scaled.
 __device__ __forceinline__ float exp_f(float x) { return exp2f(x * kLog2e); }
 
+// exp(x) as one v_exp_f32 (1 ulp, no denormal range handling: results below
+// 2^-126 may flush to zero) -- for decay factors e^{gamma_i - gamma_j} <= 1.
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);

@@ -70,6 +70,8 @@ __device__ __forceinline__ bf16x8 rd_perm(const __bf16 *row, int k0, int g) {
 
 template <typename T> __device__ __forceinline__ float ldf(const T *p) { return ld(p); }
 
+template <bool B> struct BoolC { static constexpr bool value = B; };
+
 // Workspace per (head, chunk) cell, every piece 16 bytes per lane of a 64-lane tile:
 //   an [2 planes][DK/16 mt][DK/32 ks][64]  bf16x8  A_n rows 16 mt + (l % 16), k slots
 //                                                  32 ks + 4 (l / 16) + {0..3, 16..19}
@@ -175,10 +177,12 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
   const TI *bb = static_cast<const TI *>(a.beta) + ci.batch * a.b_sb + h * a.b_sh + int64_t(ci.t0) * a.b_st;
   const TI *gb = static_cast<const TI *>(a.g) + ci.batch * a.g_sb + h * a.g_sh + int64_t(ci.t0) * a.g_st;
 
-  // ---- phase 1: rows 2p, 2p + 1 of one 8-column segment per thread (zero past len)
+  // ---- phase 1: rows 2p, 2p + 1 of one 8-column segment per thread (zero past len);
+  // p = tid % 32, so the 4-byte transposed writes of a wavefront cover 32 distinct
+  // column pairs of one LDS row (distinct banks).
   constexpr int KSEG = DK / 8, VSEG = DV / 8, VP = 32 * VSEG / 256;
-  const int kp = tid / KSEG, kseg = tid % KSEG;
-  const bool kval = kp < 32;
+  const int kp = tid & 31, kseg = tid >> 5;
+  const bool kval = kseg < KSEG;
   const uint4 z4 = {0, 0, 0, 0};
   uint4 k0r = z4, k1r = z4, q0r = z4, q1r = z4;
   if (kval) {
@@ -195,13 +199,20 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
   uint4 v0r[VP], v1r[VP];
 #pragma unroll
   for (int r = 0; r < VP; ++r) {
-    const int p = tid + 256 * r, vp = p / VSEG, vs = p % VSEG;
+    const int vp = tid & 31, vs = (tid >> 5) + 8 * r;
     v0r[r] = z4;
     v1r[r] = z4;
     if (vs < a.dv / 8) {
       if (2 * vp < ci.len) v0r[r] = *reinterpret_cast<const uint4 *>(vb + int64_t(2 * vp) * a.v_st + 8 * vs);
       if (2 * vp + 1 < ci.len) v1r[r] = *reinterpret_cast<const uint4 *>(vb + int64_t(2 * vp + 1) * a.v_st + 8 * vs);
     }
+  }
+  // Q rows of this wavefront's Q' row tile (tile w): Q[16 w + ln][16 dt + 4g .. +3].
+  bf16x4 qe[DK / 16];
+#pragma unroll
+  for (int dt = 0; dt < DK / 16; ++dt) {
+    qe[dt] = bf16x4{};
+    if (16 * w + ln < ci.len) qe[dt] = *reinterpret_cast<const bf16x4 *>(qb + int64_t(16 * w + ln) * a.q_st + 16 * dt + 4 * g);
   }
   if (w == 0) {  // gates and the inclusive prefix sum of g
     float gv = 0.f, bv = 0.f;
@@ -230,43 +241,47 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
   // Tile (bi, bj) of G holds G[16 bi + 4g + r][16 bj + ln] = G[16 bj + ln][16 bi + 4g + r]
   // (symmetric), i.e. N row 16 bj + ln, columns 16 bi + 4g .. +3: one float4 per lane.
   // Tile (bi, bj) of K Q^T holds (Q K^T)[16 bj + ln][16 bi + 4g + r]: Attn row 16 bj + ln.
-  for (int t = w; t < 26; t += 4) {
-    if (t < 16) {  // Attn block (row block bj, column block bi); zero above the diagonal
-      const int bj = t >> 2, bi = t & 3;
-      const int row = 16 * bj + ln, col = 16 * bi + 4 * g;
-      float x[4] = {0.f, 0.f, 0.f, 0.f};
-      if (bi <= bj) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  // Wave w takes Attn row block w and N row block 3 - w (all four column blocks, the
+  // ones above the diagonal masked to zero); operand reads are issued before the products.
+  {
+    const int ba = w, bn = 3 - w;
+    bf16x8 kop[4][DK / 32], qop[DK / 32], nop[DK / 32];
 #pragma unroll
-        for (int ks = 0; ks < DK / 32; ++ks) {
-          const int k0 = 32 * ks + 8 * g;
-          acc = mma(rd8(kh + (16 * bi + ln) * PL::kRow, k0), rd8(qh + (16 * bj + ln) * PL::kRow, k0), acc);
-        }
-        const float gi = gam[row];
+    for (int ks = 0; ks < DK / 32; ++ks) {
+      const int k0 = 32 * ks + 8 * g;
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          x[r] = (col + r <= row) ? acc[r] * exp_f(gi - gam[col + r]) : 0.f;
+      for (int bi = 0; bi < 4; ++bi) kop[bi][ks] = rd8(kh + (16 * bi + ln) * PL::kRow, k0);
+      qop[ks] = rd8(qh + (16 * ba + ln) * PL::kRow, k0);
+      nop[ks] = rd8(kh + (16 * bn + ln) * PL::kRow, k0);
+    }
+    f32x4 at[4], nt4[4];
+#pragma unroll
+    for (int bi = 0; bi < 4; ++bi) {
+      at[bi] = f32x4{0.f, 0.f, 0.f, 0.f};
+      nt4[bi] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < DK / 32; ++ks) {  // tiles above the diagonal are masked below
+        at[bi] = mma(kop[bi][ks], qop[ks], at[bi]);
+        nt4[bi] = mma(kop[bi][ks], nop[ks], nt4[bi]);
       }
+    }
+    const int rowa = 16 * ba + ln, rown = 16 * bn + ln;
+    const float ga = gam[rowa], gn = gam[rown], bn_ = bet[rown];
+#pragma unroll
+    for (int bi = 0; bi < 4; ++bi) {
+      const int col = 16 * bi + 4 * g;
+      float x[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[r] = (col + r <= rowa) ? at[bi][r] * exp_fast(ga - gam[col + r]) : 0.f;
       bf16x4 hv, lv;
       split4(x, hv, lv);
-      *reinterpret_cast<bf16x4 *>(att_h + swz(row, col)) = hv;
-      *reinterpret_cast<bf16x4 *>(att_l + swz(row, col)) = lv;
-    } else {  // N block (row block bj, column block bi), bi <= bj
-      int u = t - 16, bj = 0;
-      while (u > bj) { u -= bj + 1; ++bj; }
-      const int bi = u;
-      const int row = 16 * bj + ln, col = 16 * bi + 4 * g;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      *reinterpret_cast<bf16x4 *>(att_h + swz(rowa, col)) = hv;
+      *reinterpret_cast<bf16x4 *>(att_l + swz(rowa, col)) = lv;
+      // (the zeros written above the diagonal land where T is written later)
+      f32x4 y;
 #pragma unroll
-      for (int ks = 0; ks < DK / 32; ++ks) {
-        const int k0 = 32 * ks + 8 * g;
-        acc = mma(rd8(kh + (16 * bi + ln) * PL::kRow, k0), rd8(kh + (16 * bj + ln) * PL::kRow, k0), acc);
-      }
-      const float gi = gam[row], bi_ = bet[row];
-      f32x4 x;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) x[r] = (col + r < row) ? bi_ * acc[r] * exp_f(gi - gam[col + r]) : 0.f;
-      *reinterpret_cast<f32x4 *>(nt + row * NTS + col) = x;
+      for (int r = 0; r < 4; ++r) y[r] = (col + r < rown) ? bn_ * nt4[bi][r] * exp_fast(gn - gam[col + r]) : 0.f;
+      *reinterpret_cast<f32x4 *>(nt + rown * NTS + col) = y;
     }
   }
   __syncthreads();
@@ -384,7 +399,7 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
   __syncthreads();  // NT and the K / Q rows are dead from here on
   if (kval) {
     const int j = 2 * kp;
-    const float f0 = exp_f(glast - gam[j]), f1 = exp_f(glast - gam[j + 1]);
+    const float f0 = exp_fast(glast - gam[j]), f1 = exp_fast(glast - gam[j + 1]);
     const bf16x8 ka = __builtin_bit_cast(bf16x8, k0r), kb_ = __builtin_bit_cast(bf16x8, k1r);
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
@@ -398,7 +413,7 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
   }
 #pragma unroll
   for (int r = 0; r < VP; ++r) {
-    const int p = tid + 256 * r, vp = p / VSEG, vs = p % VSEG;
+    const int vp = tid & 31, vs = (tid >> 5) + 8 * r;
     if (vs < a.dv / 8) {
       const bf16x8 va = __builtin_bit_cast(bf16x8, v0r[r]), vb_ = __builtin_bit_cast(bf16x8, v1r[r]);
 #pragma unroll
@@ -415,7 +430,7 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
   char *cell = ws + (static_cast<size_t>(h) * ca.total_chunks + chunk) * Lw.cell;
   float *hn = reinterpret_cast<float *>(cell + Lw.hn);
   float *op = reinterpret_cast<float *>(cell + Lw.op);
-  const float eC = exp_f(glast);
+  const float eC = exp_fast(glast);
   float sk[4][4], sv[4][4];  // per-row scales of M^T for rows j = 16 jt + 4g + r
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt)
@@ -423,18 +438,18 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
     for (int r = 0; r < 4; ++r) {
       const int j = 16 * jt + 4 * g + r;
       sv[jt][r] = bet[j];
-      sk[jt][r] = bet[j] * exp_f(gam[j]);
+      sk[jt][r] = bet[j] * exp_fast(gam[j]);
     }
-  constexpr int NMT = DK / 16 + kC / 16;
-  for (int mt = w; mt < NMT; mt += 4) {
-    const bool top = mt < DK / 16;
-    const int lrow = top ? 16 * mt + ln : 16 * (mt - DK / 16) + ln;
+  // One m-tile: TOP -> rows d' = 16 mti + ln of A_n / H_n, else rows i' of Q' / O'.
+  auto mtile = [&](auto top_c, int mti, const bf16x4 *qrow) {
+    constexpr bool top = decltype(top_c)::value;
+    const int mrow = 16 * mti + ln;  // d' (top) or i' (bottom)
     const __bf16 *Lh = top ? ktt_h : att_h, *Ll = top ? ktt_l : att_l;
     bf16x8 lh[2], ll[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      lh[ks] = rd8s(Lh, lrow, 32 * ks + 8 * g);
-      ll[ks] = rd8s(Ll, lrow, 32 * ks + 8 * g);
+      lh[ks] = rd8s(Lh, mrow, 32 * ks + 8 * g);
+      ll[ks] = rd8s(Ll, mrow, 32 * ks + 8 * g);
     }
     bf16x4 mkh[4], mkl[4], mvh[4], mvl[4];
 #pragma unroll
@@ -463,8 +478,9 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
       bvh[jp] = __builtin_shufflevector(mvh[2 * jp], mvh[2 * jp + 1], 0, 1, 2, 3, 4, 5, 6, 7);
       bvl[jp] = __builtin_shufflevector(mvl[2 * jp], mvl[2 * jp + 1], 0, 1, 2, 3, 4, 5, 6, 7);
     }
-    const int mrow = 16 * (top ? mt : mt - DK / 16) + ln;  // d' (top) or i' (bottom)
-    const int mti = top ? mt : mt - DK / 16;                 // row tile inside A_n / Q'
+    const float eq = top ? eC : exp_fast(gam[mrow]);
+    char *base = cell + (top ? Lw.an : Lw.qp);
+    constexpr int ntile = top ? DK / 16 : kC / 16;
 #pragma unroll
     for (int dt = 0; dt < DK / 16; ++dt) {
       f32x4 z = {0.f, 0.f, 0.f, 0.f};
@@ -477,49 +493,41 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
       // z[r] = Z^T[16 dt + 4g + r][m] = (M_k K)[m][16 dt + 4g + r]
       const int col = 16 * dt + 4 * g;
       float x[4];
-      if (top) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) x[r] = (col + r == mrow ? eC : 0.f) - z[r];
-      } else {
-        float qv[4] = {0.f, 0.f, 0.f, 0.f};
-        if (mrow < ci.len) {
-          const bf16x4 q4 = *reinterpret_cast<const bf16x4 *>(qb + int64_t(mrow) * a.q_st + col);
-          const float e = exp_f(gam[mrow]);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) qv[r] = fl(q4[r]) * e;
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) x[r] = qv[r] - z[r];
-      }
+      for (int r = 0; r < 4; ++r)
+        x[r] = (top ? (col + r == mrow ? eq : 0.f) : fl(qrow[dt][r]) * eq) - z[r];
       bf16x4 hv, lv;
       split4(x, hv, lv);
       // operand order: tile (plane, mti, ks = dt / 2), lane, half dt % 2
-      char *base = cell + (top ? Lw.an : Lw.qp);
-      const int ntile = top ? DK / 16 : kC / 16;
       const size_t o_h = ((static_cast<size_t>(0 * ntile + mti) * (DK / 32) + dt / 2) * 64 + lane) * 16 + 8 * (dt & 1);
       const size_t o_l = ((static_cast<size_t>(1 * ntile + mti) * (DK / 32) + dt / 2) * 64 + lane) * 16 + 8 * (dt & 1);
       *reinterpret_cast<bf16x4 *>(base + o_h) = hv;
       *reinterpret_cast<bf16x4 *>(base + o_l) = lv;
     }
     // H_n as Y = M_v V (accumulator layout of the state), O' as Y^T (layout of O^T).
-    for (int et = 0; et < a.dv / 16; ++et) {
-      f32x4 y = {0.f, 0.f, 0.f, 0.f};
+    float *dst0 = top ? hn + mti * 256 : op + mti * 256;
 #pragma unroll
-      for (int jp = 0; jp < 2; ++jp) {
-        const bf16x8 avv = rd_perm_s(vt, 16 * et + ln, 32 * jp, g);
-        if (top) {
-          y = mma(bvl[jp], avv, y);
-          y = mma(bvh[jp], avv, y);
-        } else {
-          y = mma(avv, bvl[jp], y);
-          y = mma(avv, bvh[jp], y);
+    for (int et = 0; et < DV / 16; ++et) {
+      if (et < a.dv / 16) {
+        f32x4 y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int jp = 0; jp < 2; ++jp) {
+          const bf16x8 avv = rd_perm_s(vt, 16 * et + ln, 32 * jp, g);
+          if (top) {
+            y = mma(bvl[jp], avv, y);
+            y = mma(bvh[jp], avv, y);
+          } else {
+            y = mma(avv, bvl[jp], y);
+            y = mma(avv, bvh[jp], y);
+          }
         }
+        *reinterpret_cast<f32x4 *>(dst0 + static_cast<size_t>(et) * ntile * 256 + 4 * lane) = y;
       }
-      float *dst = top ? hn + (static_cast<size_t>(et) * (DK / 16) + mti) * 256
-                       : op + (static_cast<size_t>(et) * (kC / 16) + mti) * 256;
-      *reinterpret_cast<f32x4 *>(dst + 4 * lane) = y;
     }
-  }
+  };
+  // wave w: A_n / H_n row tile w (when w < DK/16) and Q' / O' row tile w
+  if (w < DK / 16) mtile(BoolC<true>{}, w, nullptr);
+  mtile(BoolC<false>{}, w, qe);
 }
 
 // ------------------------------------------------------------------ state scan
