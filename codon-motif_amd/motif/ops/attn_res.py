@@ -1,18 +1,61 @@
-'''Intra-block attention-residual read (adjacent to the hot path; PyTorch-ROCm).
+'''Intra-block attention-residual read (adjacent to the hot path).
 
-Softmax over the block's sources of <query, RMSNorm(source)>, then the
-weighted sum of the raw sources; same math as the reference's eager read
-(motif/ops/attn_res.py:588-593) and `apply_block_attn_res` (:596-622).
+Softmax over the block's sources of <query, RMSNorm(source)>, then the weighted
+sum of the raw sources: the reference's fused read (motif/ops/attn_res.py:22-55,
+:94-186) and eager read (:588-593), and `apply_block_attn_res` (:596-622).  On
+CUDA tensors it runs as one HIP kernel (`motif_attn_res_read`, fp32 arithmetic,
+every source read once); CPU tensors take the eager torch formula.
 '''
+import ctypes
+
 import torch
 
+from . import _lib
 
-def attn_res_read(sources, query, norm):
+MAX_SRC = 8
+
+
+def _eager(sources, query, norm):
     V = torch.stack(list(sources), dim=0)
     K = norm(V)
     logits = torch.einsum('d,nbtd->nbt', query.to(K.dtype), K)
     alpha = logits.softmax(dim=0)
     return torch.einsum('nbt,nbtd->btd', alpha, V)
+
+
+def attn_res_read(sources, query, norm):
+    '''h = sum_n softmax_n(<query, norm(x_n)>) x_n over sources x_n [B, T, D].'''
+    sources = list(sources)
+    x0 = sources[0]
+    if not x0.is_cuda:
+        return _eager(sources, query, norm)
+    if not _lib.available():
+        raise RuntimeError('attn_res_read: the HIP kernel library is not loaded')
+    if len(sources) > MAX_SRC:
+        raise NotImplementedError(f'attn_res_read: at most {MAX_SRC} sources, got {len(sources)}')
+    B, T, D = x0.shape
+    dt = x0.dtype
+    if dt not in (torch.bfloat16, torch.float32):
+        raise NotImplementedError(f'attn_res_read: dtype {dt}')
+    srcs = [s if s.stride(-1) == 1 else s.contiguous() for s in sources]
+    for s in srcs:
+        if s.shape != x0.shape or s.dtype != dt:
+            raise ValueError('attn_res_read: sources must share shape and dtype')
+    weight = norm.weight
+    if weight is None:
+        weight = torch.ones(D, dtype=dt, device=x0.device)
+    q = query.to(dt).contiguous()
+    w = weight.to(dt).contiguous()
+    out = torch.empty(B, T, D, dtype=dt, device=x0.device)
+    n = len(srcs)
+    ptrs = (ctypes.c_void_p * n)(*[s.data_ptr() for s in srcs])
+    sb = (ctypes.c_int64 * n)(*[s.stride(0) for s in srcs])
+    st = (ctypes.c_int64 * n)(*[s.stride(1) for s in srcs])
+    rc = _lib.lib().motif_attn_res_read(ptrs, sb, st, n, q.data_ptr(), w.data_ptr(), float(norm.eps),
+                                        out.data_ptr(), out.stride(0), out.stride(1), B, T, D,
+                                        _lib.dtype_code(dt), _lib.stream_ptr(x0.device))
+    _lib.check(rc, 'attn_res_read')
+    return out
 
 
 def apply_block_attn_res(cache, query, norm):

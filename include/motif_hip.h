@@ -149,6 +149,21 @@ int motif_chord_fwd(
     void *workspace, size_t workspace_bytes,
     int dtype, void *stream);
 
+/*
+ * Intra-block attention-residual read (one fused pass):
+ *   r_n = 1/sqrt(mean(x_n^2) + eps), s_n = sum_d query_d * weight_d * x_nd * r_n,
+ *   alpha = softmax_n(s), out = sum_n alpha_n * x_n      (fp32 arithmetic)
+ * Replaces motif/ops/attn_res.py:588-593 (the eager read of `_read_sources`) and
+ * the fused Triton read it falls back from (motif/ops/attn_res.py:94-186).
+ *   sources: host array of nsrc (1..8) device pointers, each [B,T,D] with strides
+ *   src_sb[n], src_st[n] (host arrays); query, norm_weight [D]; out [B,T,D].
+ *   All tensors in `dtype`; rows 16-byte aligned, D a multiple of 16 bytes and at
+ *   most 4096 bytes (D <= 2048 bf16 / 1024 fp32).
+ */
+int motif_attn_res_read(const void *const *sources, const int64_t *src_sb, const int64_t *src_st,
+                        int nsrc, const void *query, const void *norm_weight, float eps, void *out,
+                        int64_t out_sb, int64_t out_st, int B, int T, int D, int dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

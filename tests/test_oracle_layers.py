@@ -125,3 +125,30 @@ def test_parameter_count_of_published_shape():
 def test_fixtures_are_small_and_safe(name):
     path = os.path.join(GOLD, f'{name}.safetensors')
     assert os.path.getsize(path) < 1_000_000
+
+
+def test_attn_res_read_bruteforce():
+    '''oracle.model.attn_res_read against scalar loops of its definition
+    (softmax over sources of q . (w * x / rms(x)), then the weighted sum).'''
+    import math
+    from oracle.model import attn_res_read
+    g = torch.Generator().manual_seed(3)
+    N, B, T, D, eps = 3, 2, 4, 8, 1e-6
+    srcs = [torch.randn(B, T, D, generator=g, dtype=torch.float64) for _ in range(N)]
+    q = torch.randn(D, generator=g, dtype=torch.float64)
+    w = torch.randn(D, generator=g, dtype=torch.float64)
+    out = attn_res_read(srcs, q, w, eps)
+    for b in range(B):
+        for t in range(T):
+            s = []
+            for n in range(N):
+                x = [float(srcs[n][b, t, d]) for d in range(D)]
+                r = 1.0 / math.sqrt(sum(v * v for v in x) / D + eps)
+                s.append(sum(float(q[d]) * float(w[d]) * x[d] * r for d in range(D)))
+            m = max(s)
+            e = [math.exp(v - m) for v in s]
+            a = [v / sum(e) for v in e]
+            for d in range(D):
+                h = sum(a[n] * float(srcs[n][b, t, d]) for n in range(N))
+                assert abs(h - float(out[b, t, d])) < 1e-12
+    assert attn_res_read(srcs[:1], q, w, eps) is srcs[0]
