@@ -89,13 +89,32 @@ class GatedDeltaAttention(BasicAttention):
         g = -self.A_log.exp() * F.softplus(self.a_proj(hidden_states) + self.dt_bias)
         return beta, g.transpose(1, 2)
 
-    def _heads(self, q, k, v, B, L):
+    def _heads(self, q, k, v, B, L, normalized=False):
         q = q.view(B, L, self.num_heads, self.dk).transpose(1, 2)
         k = k.view(B, L, self.num_heads, self.dk).transpose(1, 2)
         v = v.view(B, L, self.num_heads, self.dv).transpose(1, 2)
-        q = F.normalize(q, dim=-1) * (self.dk ** -0.5)
-        k = F.normalize(k, dim=-1)
+        if not normalized:
+            q = F.normalize(q, dim=-1) * (self.dk ** -0.5)
+            k = F.normalize(k, dim=-1)
         return q, k, v
+
+    def _qkv(self, hidden_states, tails, B, L, cu_seqlens=None, max_len=None):
+        '''q / k / v projections through conv + SiLU; q and k then L2-normalised per
+        head (q also scaled by dk^-1/2), inside the conv kernel when dk <= 64.'''
+        fused = self.dk in (16, 32, 64)
+        hd = self.dk if fused else None
+        xs = (self.q_proj(hidden_states), self.k_proj(hidden_states), self.v_proj(hidden_states))
+        ws = (self.q_conv.weight, self.k_conv.weight, self.v_conv.weight)
+        opts = ((hd, self.dk ** -0.5), (hd, 1.0), (None, 1.0))
+        outs = []
+        for i in range(3):
+            if cu_seqlens is None:
+                outs.append(short_conv_silu(xs[i], ws[i], tails[i], head_dim=opts[i][0], scale=opts[i][1]))
+            else:
+                outs.append(short_conv_silu_varlen(xs[i], ws[i], cu_seqlens, max_len,
+                                                   head_dim=opts[i][0], scale=opts[i][1]))
+        q, k, v = self._heads(outs[0][0], outs[1][0], outs[2][0], B, L, normalized=fused)
+        return q, k, v, tuple(o[1] for o in outs)
 
     def _output(self, o, hidden_states, B, L):
         o = o.to(hidden_states.dtype).transpose(1, 2)
@@ -117,10 +136,7 @@ class GatedDeltaAttention(BasicAttention):
             tails = (None, None, None)
             S0 = None
 
-        q, cq = short_conv_silu(self.q_proj(hidden_states), self.q_conv.weight, tails[0])
-        k, ck = short_conv_silu(self.k_proj(hidden_states), self.k_conv.weight, tails[1])
-        v, cv = short_conv_silu(self.v_proj(hidden_states), self.v_conv.weight, tails[2])
-        q, k, v = self._heads(q, k, v, B, L)
+        q, k, v, (cq, ck, cv) = self._qkv(hidden_states, tails, B, L)
         beta, g = self._gates(hidden_states)
 
         if L == 1:
@@ -144,10 +160,7 @@ class GatedDeltaAttention(BasicAttention):
             raise ValueError('forward_varlen expects packed sequences with B == 1')
         lens = cu_seqlens.detach().cpu()
         max_len = int((lens[1:] - lens[:-1]).max()) if lens.numel() > 1 else 0
-        q, cq = short_conv_silu_varlen(self.q_proj(hidden_states), self.q_conv.weight, cu_seqlens, max_len)
-        k, ck = short_conv_silu_varlen(self.k_proj(hidden_states), self.k_conv.weight, cu_seqlens, max_len)
-        v, cv = short_conv_silu_varlen(self.v_proj(hidden_states), self.v_conv.weight, cu_seqlens, max_len)
-        q, k, v = self._heads(q, k, v, B, L)
+        q, k, v, (cq, ck, cv) = self._qkv(hidden_states, (None, None, None), B, L, cu_seqlens, max_len)
         beta, g = self._gates(hidden_states)
         o, S = chunk_gated_delta_rule_varlen(q, k, v, beta, g, cu_seqlens, None, self.chunk_size)
         output = self._output(o, hidden_states, B, L)

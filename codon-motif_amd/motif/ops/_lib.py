@@ -34,6 +34,8 @@ _SIGNATURES = {
         [_P, _I64, _I64, _P, _P, _P, _P, _I64, _I64] + [_I32] * 4 + [_P, _I32, _I32, _I32, _P], _I32),
     'motif_attn_res_read': (
         [_P, _P, _P, _I32, _P, _P, _F32, _P, _I64, _I64] + [_I32] * 4 + [_P], _I32),
+    'motif_short_conv_silu_l2norm': (
+        [_P, _I64, _I64, _P, _P, _P, _P, _I64, _I64] + [_I32] * 4 + [_P, _I32, _I32, _I32, _F32, _I32, _P], _I32),
     'motif_chord_workspace_bytes': ([_I32] * 6 + [ctypes.POINTER(_I32)], _SZ),
     'motif_chord_fwd': (
         _T4 * 3 + [_P, _P, _P, _P] + [_P, _I64, _I64] + _T4 + [_P] + [_I32] * 6

@@ -11,7 +11,21 @@ import torch
 from . import _lib
 
 
-def short_conv_silu(x, weight, cache=None, y=None, new_cache=None):
+def _conv_call(x, w, cache, new_cache, y, cu, nseq, max_len, head_dim, scale):
+    B, L, D = x.shape
+    K = w.shape[-1]
+    L_ = _lib.lib()
+    args = (x.data_ptr(), x.stride(0), x.stride(1), w.data_ptr(), _lib.ptr(cache), _lib.ptr(new_cache),
+            y.data_ptr(), y.stride(0), y.stride(1), B, L, D, K, _lib.ptr(cu), nseq, max_len)
+    if head_dim:
+        rc = L_.motif_short_conv_silu_l2norm(*args, int(head_dim), float(scale), _lib.dtype_code(x.dtype),
+                                             _lib.stream_ptr(x.device))
+    else:
+        rc = L_.motif_short_conv_silu(*args, _lib.dtype_code(x.dtype), _lib.stream_ptr(x.device))
+    _lib.check(rc, 'motif_short_conv_silu')
+
+
+def short_conv_silu(x, weight, cache=None, y=None, new_cache=None, head_dim=None, scale=1.0):
     '''Causal depthwise conv + SiLU.
 
     Args:
@@ -21,6 +35,9 @@ def short_conv_silu(x, weight, cache=None, y=None, new_cache=None):
         y: optional preallocated [B, L, D] output.
         new_cache: optional preallocated [B, D, K-1] tail output; may be `cache`
             itself (in-place update).
+        head_dim: if set (16, 32 or 64), every head_dim channels of each timestep
+            are then L2-normalised (F.normalize, eps 1e-12) and multiplied by
+            `scale` -- the GDN q / k front end (gdn_attn.py:190-191).
 
     Returns:
         (y [B, L, D], new_cache [B, D, K-1])
@@ -43,15 +60,11 @@ def short_conv_silu(x, weight, cache=None, y=None, new_cache=None):
         y = torch.empty(B, L, D, dtype=x.dtype, device=x.device)
     if new_cache is None:
         new_cache = torch.empty(B, D, K - 1, dtype=x.dtype, device=x.device)
-    rc = _lib.lib().motif_short_conv_silu(
-        x.data_ptr(), x.stride(0), x.stride(1), w.data_ptr(), _lib.ptr(cache), new_cache.data_ptr(),
-        y.data_ptr(), y.stride(0), y.stride(1), B, L, D, K, None, B, L,
-        _lib.dtype_code(x.dtype), _lib.stream_ptr(x.device))
-    _lib.check(rc, 'motif_short_conv_silu')
+    _conv_call(x, w, cache, new_cache, y, None, B, L, head_dim, scale)
     return y, new_cache
 
 
-def short_conv_silu_varlen(x, weight, cu_seqlens, max_seqlen=None):
+def short_conv_silu_varlen(x, weight, cu_seqlens, max_seqlen=None, head_dim=None, scale=1.0):
     '''Packed-sequence conv (B == 1): every sequence starts from a zero tail.
 
     Returns:
@@ -74,9 +87,5 @@ def short_conv_silu_varlen(x, weight, cu_seqlens, max_seqlen=None):
     cu_dev = cu_host.to(device=x.device, dtype=torch.int32)
     y = torch.empty(B, L, D, dtype=x.dtype, device=x.device)
     tails = torch.empty(nseq, D, K - 1, dtype=x.dtype, device=x.device)
-    rc = _lib.lib().motif_short_conv_silu(
-        x.data_ptr(), x.stride(0), x.stride(1), w.data_ptr(), None, tails.data_ptr(),
-        y.data_ptr(), y.stride(0), y.stride(1), B, L, D, K, cu_dev.data_ptr(), nseq, int(max_seqlen),
-        _lib.dtype_code(x.dtype), _lib.stream_ptr(x.device))
-    _lib.check(rc, 'motif_short_conv_silu')
+    _conv_call(x, w, None, tails, y, cu_dev, nseq, int(max_seqlen), head_dim, scale)
     return y, tails

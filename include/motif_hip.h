@@ -115,6 +115,21 @@ int motif_short_conv_silu(
     int dtype, void *stream);
 
 /*
+ * motif_short_conv_silu followed by the per-head L2 normalisation of the GDN
+ * q / k inputs: every group of head_dim consecutive channels of each timestep is
+ * divided by max(||y||_2, 1e-12) (F.normalize) and multiplied by `scale`
+ * (dk^-1/2 for q, 1 for k).  Replaces the conv + `F.normalize(..) * scale` pair of
+ * motif/block/attention/gdn_attn.py:120-121, :190-191.  head_dim in {16, 32, 64}.
+ */
+int motif_short_conv_silu_l2norm(
+    const void *x, int64_t x_sb, int64_t x_st,
+    const void *weight, const void *tail_in, void *tail_out,
+    void *y, int64_t y_sb, int64_t y_st,
+    int B, int L, int D, int K,
+    const int32_t *cu_seqlens, int nseq, int max_seqlen,
+    int head_dim, float scale, int dtype, void *stream);
+
+/*
  * Workspace bytes needed by motif_chord_fwd (split-K partials); also returns
  * the split count the launcher will use in *splits (may be NULL).
  */

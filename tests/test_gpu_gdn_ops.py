@@ -175,3 +175,38 @@ def test_short_conv_silu_varlen():
     ry, rt = ogdn.short_conv_silu_varlen(x.double(), w.double(), cu)
     assert_fp32_close(y, ry, 1e-5, 'y')
     assert_fp32_close(tails, rt, 0.0, 'tails')
+
+
+@pytest.mark.parametrize('hd,D', [(64, 768), (32, 96), (16, 48)])
+@pytest.mark.parametrize('dtype', [torch.float32, torch.bfloat16])
+def test_short_conv_silu_l2norm(hd, D, dtype):
+    '''conv + SiLU, then every hd channels L2-normalised (F.normalize) and scaled.'''
+    ops = _ops()
+    gg = torch.Generator().manual_seed(D + hd)
+    B, L, K, scale = 2, 37, 4, hd ** -0.5
+    x = torch.randn(B, L, D, generator=gg).to(dtype)
+    w = (torch.randn(D, 1, K, generator=gg) * 0.5).to(dtype)
+    tail = torch.randn(B, D, K - 1, generator=gg).to(dtype)
+    y, nt = ops.short_conv_silu(x.to(DEV), w.to(DEV), tail.to(DEV), head_dim=hd, scale=scale)
+    ry, rt = ogdn.short_conv_silu(x.double(), w.double(), tail.double())
+    ry = torch.nn.functional.normalize(ry.view(B, L, D // hd, hd), dim=-1).view(B, L, D) * scale
+    if dtype == torch.float32:
+        assert_fp32_close(y, ry, 1e-5, 'y')
+    else:
+        assert_bf16_close(y, ry, what='y')
+    assert torch.equal(nt.cpu().double(), rt)
+
+
+def test_short_conv_silu_l2norm_varlen():
+    ops = _ops()
+    lens = [5, 0, 130, 2]
+    cu = torch.tensor([0] + list(torch.cumsum(torch.tensor(lens), 0)), dtype=torch.int32)
+    gg = torch.Generator().manual_seed(22)
+    D, K = 128, 4
+    x = torch.randn(1, int(cu[-1]), D, generator=gg)
+    w = torch.randn(D, 1, K, generator=gg)
+    y, tails = ops.short_conv_silu_varlen(x.to(DEV), w.to(DEV), cu.to(DEV), head_dim=64, scale=0.125)
+    ry, rt = ogdn.short_conv_silu_varlen(x.double(), w.double(), cu)
+    ry = torch.nn.functional.normalize(ry.view(1, -1, 2, 64), dim=-1).view(1, -1, D) * 0.125
+    assert_fp32_close(y, ry, 1e-5, 'y')
+    assert_fp32_close(tails, rt, 0.0, 'tails')
