@@ -19,12 +19,10 @@ __device__ __forceinline__ float bf16_to_f32(bf16_t x) {
   return __uint_as_float(static_cast<uint32_t>(x) << 16);
 }
 
-// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN).
+// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN): the gfx950 conversion
+// instruction (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16_t>((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<bf16_t>(u >> 16);
+  return __builtin_bit_cast(bf16_t, static_cast<__bf16>(f));
 }
 
 template <typename T> struct Elem;
@@ -46,9 +44,39 @@ __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_lo
 // exp(x) through the hardware exp2 with the argument pre-scaled.
 __device__ __forceinline__ float exp_f(float x) { return exp2f(x * kLog2e); }
 
+// 1 / x as one v_rcp_f32 (1 ulp).
+__device__ __forceinline__ float rcp_fast(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// x * sigmoid(x) with the single-instruction exp and reciprocal.
+__device__ __forceinline__ float silu_fast(float x) {
+  return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * kLog2e));
+}
+
 // exp(x) as one v_exp_f32 (1 ulp, no denormal range handling: results below
 // 2^-126 may flush to zero) -- for decay factors e^{gamma_i - gamma_j} <= 1.
 __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+
+// Raw buffer over [base, base + bytes) (uniform base and size): a load whose byte
+// offset falls outside returns zeros by the hardware range check, so bounded tile
+// loads need no branches (a load under a lane-varying branch is followed by a wait,
+// which serialises a batch of loads).  Negative offsets wrap to large unsigned ones.
+typedef __amdgpu_buffer_rsrc_t buf_t;
+__device__ __forceinline__ buf_t make_buf(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_ld16(buf_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ uint2 buf_ld8(buf_t r, uint32_t off) {
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
+template <typename T> __device__ __forceinline__ float buf_ld(buf_t r, uint32_t elem);
+template <> __device__ __forceinline__ float buf_ld<float>(buf_t r, uint32_t elem) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, elem * 4, 0, 0));
+}
+template <> __device__ __forceinline__ float buf_ld<bf16_t>(buf_t r, uint32_t elem) {
+  return bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(r, elem * 2, 0, 0));
+}
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -25,7 +25,8 @@ struct ConvArgs {
   float scale;
 };
 
-constexpr int kConvStep = 16;
+constexpr int kConvStep = 16;  // timesteps per batch of loads (scalar kernel)
+constexpr int kVecStep = 8;    // timesteps per thread (vector kernel)
 
 template <typename T, int K, int HD>
 __global__ void __launch_bounds__(256) short_conv_silu_kernel(ConvArgs a) {
@@ -48,52 +49,69 @@ __global__ void __launch_bounds__(256) short_conv_silu_kernel(ConvArgs a) {
   const int t_hi = min(len, t_lo + a.tch);
   const int dc = active ? d : 0;
 
-  const T *x = static_cast<const T *>(a.x) + batch * a.x_sb + int64_t(t_begin) * a.x_st + dc;
+  const T *x = static_cast<const T *>(a.x) + batch * a.x_sb + int64_t(t_begin) * a.x_st;
   T *y = static_cast<T *>(a.y) + batch * a.y_sb + int64_t(t_begin) * a.y_st + dc;
   const T *w = static_cast<const T *>(a.w) + dc * K;
-  // Padded batches continue from tail_in; packed sequences start from zeros.
-  const T *tail = (a.cu == nullptr && a.tail_in)
-                      ? static_cast<const T *>(a.tail_in) + (static_cast<size_t>(batch) * a.D + dc) * (K - 1)
-                      : nullptr;
+  // Range-checked buffers over this sequence's rows and this batch row's tail_in:
+  // positions before the start or past the end read as zeros (packed sequences and
+  // a NULL tail_in get zero-sized tail buffers), so every load is unconditional.
+  const buf_t xbuf = make_buf(x, len > 0 ? static_cast<uint32_t>(((len - 1) * a.x_st + a.D) * sizeof(T)) : 0u);
+  const bool has_tail = a.cu == nullptr && a.tail_in;
+  const buf_t tbuf = make_buf(has_tail ? static_cast<const T *>(a.tail_in) + static_cast<size_t>(batch) * a.D * (K - 1)
+                                       : static_cast<const T *>(a.x),
+                              has_tail ? static_cast<uint32_t>(a.D * (K - 1) * sizeof(T)) : 0u);
+  auto xat = [&](int pos) { return buf_ld<T>(xbuf, static_cast<uint32_t>(pos * a.x_st + dc)); };
 
-  float wr[K];
+  // Issue everything the first block needs at once: weights, tail, window, 16 inputs.
+  float wr[K], tv[K - 1], xw[K - 1], xs[kConvStep];
 #pragma unroll
-  for (int r = 0; r < K; ++r) wr[r] = active ? ld(w + r) : 0.f;
+  for (int r = 0; r < K; ++r) wr[r] = ld(w + r);
+#pragma unroll
+  for (int u = 0; u < K - 1; ++u) tv[u] = buf_ld<T>(tbuf, dc * (K - 1) + u);
+#pragma unroll
+  for (int r = 0; r < K - 1; ++r) xw[r] = xat(t_lo - (K - 1) + r);
+#pragma unroll
+  for (int i = 0; i < kConvStep; ++i) xs[i] = xat(t_lo + i);
+  __builtin_amdgcn_sched_barrier(0);  // keep the loads above as one batch
 
-  // Window = inputs at sequence positions t_lo-K+1 .. t_lo-1 (negative -> tail).
-  float win[K - 1];
+  // Window = inputs at positions t_lo-K+1 .. t_lo-1 (before the start: tail entries);
+  // tail_keep = the entries of the last K-1 positions that come from tail_in (taken
+  // before anything is written, as tail_out may alias tail_in).
+  float win[K - 1], tail_keep[K - 1];
+  const bool last_run = t_hi == len;
 #pragma unroll
   for (int r = 0; r < K - 1; ++r) {
-    const int pos = t_lo - (K - 1) + r;
-    win[r] = !active ? 0.f : pos >= 0 ? ld(x + int64_t(pos) * a.x_st) : (tail ? ld(tail + pos + (K - 1)) : 0.f);
-  }
-  // Tail out needs the last K-1 entries of [tail || x]; capture the ones that
-  // come from tail_in before anything is written (tail_out may alias tail_in).
-  float tail_keep[K - 1];
-  const bool last_run = t_hi == len;
-  if (last_run) {
+    const int pos = t_lo - (K - 1) + r, pk = len - (K - 1) + r;
+    float tw = 0.f, tk = 0.f;
 #pragma unroll
-    for (int r = 0; r < K - 1; ++r) {
-      const int pos = len - (K - 1) + r;
-      tail_keep[r] = (pos >= 0 || !active) ? 0.f : (tail ? ld(tail + pos + (K - 1)) : 0.f);
+    for (int u = 0; u < K - 1; ++u) {  // tail entry pos + K - 1 (static register index)
+      tw = (pos + K - 1 == u) ? tv[u] : tw;
+      tk = (pk + K - 1 == u) ? tv[u] : tk;
     }
+    win[r] = active ? (pos >= 0 ? xw[r] : tw) : 0.f;
+    tail_keep[r] = (active && pk < 0) ? tk : 0.f;
   }
+#pragma unroll
+  for (int r = 0; r < K; ++r) wr[r] = active ? wr[r] : 0.f;
 
   for (int t0 = t_lo; t0 < t_hi; t0 += kConvStep) {
-    float xs[kConvStep];
+    if (t0 != t_lo) {
 #pragma unroll
-    for (int i = 0; i < kConvStep; ++i) xs[i] = (active && t0 + i < t_hi) ? ld(x + int64_t(t0 + i) * a.x_st) : 0.f;
+      for (int i = 0; i < kConvStep; ++i) xs[i] = xat(t0 + i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int i = 0; i < kConvStep; ++i) {
+      if (!active) xs[i] = 0.f;
       float acc = wr[K - 1] * xs[i];
 #pragma unroll
       for (int r = 0; r < K - 1; ++r) acc = fmaf(wr[r], win[r], acc);
-      float v = acc / (1.f + exp_fast(-acc));
+      float v = silu_fast(acc);
       if (HD > 0) {
         float ss = v * v;
 #pragma unroll
         for (int off = 1; off < HD; off <<= 1) ss += __shfl_xor(ss, off, 64);
-        v *= a.scale / fmaxf(sqrtf(ss), 1e-12f);
+        v *= a.scale * rcp_fast(fmaxf(sqrtf(ss), 1e-12f));
       }
       if (active && t0 + i < t_hi) st(y + int64_t(t0 + i) * a.y_st, v);
 #pragma unroll
@@ -107,9 +125,171 @@ __global__ void __launch_bounds__(256) short_conv_silu_kernel(ConvArgs a) {
 #pragma unroll
     for (int r = 0; r < K - 1; ++r) {
       const int pos = len - (K - 1) + r;
-      st(to + r, pos >= 0 ? ld(x + int64_t(pos) * a.x_st) : tail_keep[r]);
+      const float xv = xat(pos);
+      st(to + r, pos >= 0 ? xv : tail_keep[r]);
     }
   }
+}
+
+// Vector form for row-contiguous 16-byte-aligned channels: one thread owns E = 16 /
+// sizeof(T) consecutive channels over 8 timesteps (16-byte loads and stores).  With
+// HD > 0 a head is HD / E consecutive lanes.  Same arithmetic as the scalar kernel.
+template <typename T> struct Vec16;
+template <> struct Vec16<bf16_t> {
+  static constexpr int E = 8;
+  __device__ static void unpack(const uint4 &u, float *x) {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = __uint_as_float(w[i] << 16);
+      x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+  __device__ static uint4 pack(const float *x) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = static_cast<uint32_t>(f32_to_bf16(x[2 * i])) | (static_cast<uint32_t>(f32_to_bf16(x[2 * i + 1])) << 16);
+    return uint4{w[0], w[1], w[2], w[3]};
+  }
+};
+template <> struct Vec16<float> {
+  static constexpr int E = 4;
+  __device__ static void unpack(const uint4 &u, float *x) {
+    x[0] = __uint_as_float(u.x); x[1] = __uint_as_float(u.y); x[2] = __uint_as_float(u.z); x[3] = __uint_as_float(u.w);
+  }
+  __device__ static uint4 pack(const float *x) {
+    return uint4{__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3])};
+  }
+};
+
+template <typename T, int K, int HD>
+__global__ void __launch_bounds__(256) short_conv_silu_vec_kernel(ConvArgs a) {
+  constexpr int E = Vec16<T>::E;
+  constexpr int G = HD / E;  // lanes per head (HD > 0)
+  const int nc = a.D / E;
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  const int sq = blockIdx.y;
+  const int c = idx % nc, tb = idx / nc;
+  int batch, t_begin, len;
+  if (a.cu == nullptr) {
+    batch = sq;
+    t_begin = 0;
+    len = a.L;
+  } else {
+    batch = 0;
+    t_begin = a.cu[sq];
+    len = a.cu[sq + 1] - t_begin;
+  }
+  const int t_lo = tb * kVecStep;
+  // Head groups share tb, so a whole group is in or out together.
+  if (t_lo >= len && !(tb == 0 && len == 0)) return;
+  const int t_hi = min(len, t_lo + kVecStep);
+  const int d0 = c * E;
+
+  const T *x = static_cast<const T *>(a.x) + batch * a.x_sb + int64_t(t_begin) * a.x_st;
+  T *y = static_cast<T *>(a.y) + batch * a.y_sb + int64_t(t_begin) * a.y_st + d0;
+  const buf_t xbuf = make_buf(x, len > 0 ? static_cast<uint32_t>(((len - 1) * a.x_st + a.D) * sizeof(T)) : 0u);
+  const bool has_tail = a.cu == nullptr && a.tail_in;
+  const T *tail0 = has_tail ? static_cast<const T *>(a.tail_in) + (static_cast<size_t>(batch) * a.D + d0) * (K - 1)
+                            : nullptr;
+
+  uint4 raw[K - 1 + kVecStep];
+#pragma unroll
+  for (int i = 0; i < K - 1 + kVecStep; ++i)
+    raw[i] = buf_ld16(xbuf, static_cast<uint32_t>(((t_lo - (K - 1) + i) * a.x_st + d0) * sizeof(T)));
+  float wr[E][K], tv[E][K - 1];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+#pragma unroll
+    for (int r = 0; r < K; ++r) wr[e][r] = ld(static_cast<const T *>(a.w) + (d0 + e) * K + r);
+#pragma unroll
+    for (int u = 0; u < K - 1; ++u) tv[e][u] = has_tail ? ld(tail0 + e * (K - 1) + u) : 0.f;
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep the loads above as one batch
+
+  // window: positions t_lo-K+1 .. t_lo-1; before the sequence start -> tail entries
+  float win[K - 1][E];
+#pragma unroll
+  for (int r = 0; r < K - 1; ++r) {
+    const int pos = t_lo - (K - 1) + r;
+    float xv[E];
+    Vec16<T>::unpack(raw[r], xv);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      float tw = 0.f;
+#pragma unroll
+      for (int u = 0; u < K - 1; ++u) tw = (pos + K - 1 == u) ? tv[e][u] : tw;
+      win[r][e] = pos >= 0 ? xv[e] : tw;
+    }
+  }
+  const bool last_run = t_hi == len;
+  // entries of the last K-1 positions that come from tail_in (before any write)
+  float tail_keep[K - 1][E];
+#pragma unroll
+  for (int r = 0; r < K - 1; ++r) {
+    const int pk = len - (K - 1) + r;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      float tk = 0.f;
+#pragma unroll
+      for (int u = 0; u < K - 1; ++u) tk = (pk + K - 1 == u) ? tv[e][u] : tk;
+      tail_keep[r][e] = pk < 0 ? tk : 0.f;
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < kVecStep; ++i) {
+    float xt[E], v[E];
+    Vec16<T>::unpack(raw[K - 1 + i], xt);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      float acc = wr[e][K - 1] * xt[e];
+#pragma unroll
+      for (int r = 0; r < K - 1; ++r) acc = fmaf(wr[e][r], win[r][e], acc);
+      v[e] = silu_fast(acc);
+      ss = fmaf(v[e], v[e], ss);
+#pragma unroll
+      for (int r = 0; r < K - 2; ++r) win[r][e] = win[r + 1][e];
+      win[K - 2][e] = xt[e];
+    }
+    if (HD > 0) {
+#pragma unroll
+      for (int off = 1; off < G; off <<= 1) ss += __shfl_xor(ss, off, 64);
+      const float f = a.scale * rcp_fast(fmaxf(sqrtf(ss), 1e-12f));
+#pragma unroll
+      for (int e = 0; e < E; ++e) v[e] *= f;
+    }
+    if (t_lo + i < t_hi) *reinterpret_cast<uint4 *>(y + int64_t(t_lo + i) * a.y_st) = Vec16<T>::pack(v);
+  }
+
+  if (last_run && a.tail_out) {
+    T *to = static_cast<T *>(a.tail_out) + (static_cast<size_t>(sq) * a.D + d0) * (K - 1);
+#pragma unroll
+    for (int r = 0; r < K - 1; ++r) {
+      const int pos = len - (K - 1) + r;
+      float xv[E];
+      Vec16<T>::unpack(buf_ld16(xbuf, static_cast<uint32_t>((pos * a.x_st + d0) * sizeof(T))), xv);
+#pragma unroll
+      for (int e = 0; e < E; ++e) st(to + e * (K - 1) + r, pos >= 0 ? xv[e] : tail_keep[r][e]);
+    }
+  }
+}
+
+template <typename T, int HD>
+static int launch_conv_vec(const ConvArgs &a, int K, int nseq, int max_len, hipStream_t s) {
+  const int nc = a.D / Vec16<T>::E;
+  const int ntb = max(1, (max_len + kVecStep - 1) / kVecStep);
+  const dim3 grid(static_cast<unsigned>((static_cast<int64_t>(nc) * ntb + 255) / 256), nseq), block(256);
+  switch (K) {
+    case 2: short_conv_silu_vec_kernel<T, 2, HD><<<grid, block, 0, s>>>(a); break;
+    case 3: short_conv_silu_vec_kernel<T, 3, HD><<<grid, block, 0, s>>>(a); break;
+    case 4: short_conv_silu_vec_kernel<T, 4, HD><<<grid, block, 0, s>>>(a); break;
+    case 5: short_conv_silu_vec_kernel<T, 5, HD><<<grid, block, 0, s>>>(a); break;
+    default: return set_error(MOTIF_ERR_UNSUPPORTED, "short_conv_silu: K must be in {2, 3, 4, 5}");
+  }
+  return check_launch("short_conv_silu_vec_kernel");
 }
 
 template <typename T, int HD>
@@ -127,6 +307,19 @@ static int launch_conv_hd(const ConvArgs &a, int K, dim3 grid, hipStream_t s) {
 
 template <typename T>
 static int launch_conv(const ConvArgs &a, int K, int nseq, int max_len, int head_dim, hipStream_t s) {
+  constexpr int E = Vec16<T>::E;
+  const bool aliased = a.tail_out != nullptr && a.tail_out == a.tail_in;
+  const bool vec = !aliased && a.D % E == 0 && ((a.x_sb | a.x_st | a.y_sb | a.y_st) % E) == 0 &&
+                   ((reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.y)) & 15) == 0 &&
+                   head_dim % E == 0;
+  if (vec) {
+    switch (head_dim) {
+      case 0: return launch_conv_vec<T, 0>(a, K, nseq, max_len, s);
+      case 16: return launch_conv_vec<T, 16>(a, K, nseq, max_len, s);
+      case 32: return launch_conv_vec<T, 32>(a, K, nseq, max_len, s);
+      case 64: return launch_conv_vec<T, 64>(a, K, nseq, max_len, s);
+    }
+  }
   const dim3 grid((a.D + 255) / 256, nseq, max(1, (max_len + a.tch - 1) / a.tch));
   switch (head_dim) {
     case 0: return launch_conv_hd<T, 0>(a, K, grid, s);

@@ -24,6 +24,9 @@
 // M, A_n, Q', the state) are split into bf16 hi + lo and their products take three
 // MFMA passes (hi.hi + hi.lo + lo.hi, fp32 accumulation), products with an exact
 // bf16 operand two: about 16 mantissa bits per product, fp32 accumulation throughout.
+#include <algorithm>
+#include <cstdlib>
+
 #include "gdn_internal.h"
 
 namespace motif {
@@ -183,43 +186,31 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
   constexpr int KSEG = DK / 8, VSEG = DV / 8, VP = 32 * VSEG / 256;
   const int kp = tid & 31, kseg = tid >> 5;
   const bool kval = kseg < KSEG;
-  const uint4 z4 = {0, 0, 0, 0};
-  uint4 k0r = z4, k1r = z4, q0r = z4, q1r = z4;
-  if (kval) {
-    const int r0 = 2 * kp, r1 = r0 + 1;
-    if (r0 < ci.len) {
-      k0r = *reinterpret_cast<const uint4 *>(kb + int64_t(r0) * a.k_st + 8 * kseg);
-      q0r = *reinterpret_cast<const uint4 *>(qb + int64_t(r0) * a.q_st + 8 * kseg);
-    }
-    if (r1 < ci.len) {
-      k1r = *reinterpret_cast<const uint4 *>(kb + int64_t(r1) * a.k_st + 8 * kseg);
-      q1r = *reinterpret_cast<const uint4 *>(qb + int64_t(r1) * a.q_st + 8 * kseg);
-    }
-  }
+  // Loads go through range-checked buffers over the chunk's valid rows: rows past
+  // len read as zeros with no branches (so every load of the phase is in flight at once).
+  const int last = ci.len - 1;
+  const buf_t kbuf = make_buf(kb, (last * a.k_st + DK) * 2), qbuf = make_buf(qb, (last * a.q_st + DK) * 2);
+  const buf_t vbuf = make_buf(vb, (last * a.v_st + a.dv) * 2);
+  const buf_t gbuf = make_buf(gb, (last * a.g_st + 1) * 2), bbuf = make_buf(bb, (last * a.b_st + 1) * 2);
+  // gates (every wavefront loads them; wavefront 0 takes the prefix sum)
+  const float gv = buf_ld<TI>(gbuf, lane * a.g_st), bv = buf_ld<TI>(bbuf, lane * a.b_st);
+  const int kc = 8 * min(kseg, KSEG - 1);
+  const uint4 k0r = buf_ld16(kbuf, ((2 * kp) * a.k_st + kc) * 2), k1r = buf_ld16(kbuf, ((2 * kp + 1) * a.k_st + kc) * 2);
+  const uint4 q0r = buf_ld16(qbuf, ((2 * kp) * a.q_st + kc) * 2), q1r = buf_ld16(qbuf, ((2 * kp + 1) * a.q_st + kc) * 2);
   uint4 v0r[VP], v1r[VP];
 #pragma unroll
   for (int r = 0; r < VP; ++r) {
     const int vp = tid & 31, vs = (tid >> 5) + 8 * r;
-    v0r[r] = z4;
-    v1r[r] = z4;
-    if (vs < a.dv / 8) {
-      if (2 * vp < ci.len) v0r[r] = *reinterpret_cast<const uint4 *>(vb + int64_t(2 * vp) * a.v_st + 8 * vs);
-      if (2 * vp + 1 < ci.len) v1r[r] = *reinterpret_cast<const uint4 *>(vb + int64_t(2 * vp + 1) * a.v_st + 8 * vs);
-    }
+    const int vc = 8 * min(vs, a.dv / 8 - 1);
+    v0r[r] = buf_ld16(vbuf, ((2 * vp) * a.v_st + vc) * 2);
+    v1r[r] = buf_ld16(vbuf, ((2 * vp + 1) * a.v_st + vc) * 2);
   }
   // Q rows of this wavefront's Q' row tile (tile w): Q[16 w + ln][16 dt + 4g .. +3].
   bf16x4 qe[DK / 16];
 #pragma unroll
-  for (int dt = 0; dt < DK / 16; ++dt) {
-    qe[dt] = bf16x4{};
-    if (16 * w + ln < ci.len) qe[dt] = *reinterpret_cast<const bf16x4 *>(qb + int64_t(16 * w + ln) * a.q_st + 16 * dt + 4 * g);
-  }
-  if (w == 0) {  // gates and the inclusive prefix sum of g
-    float gv = 0.f, bv = 0.f;
-    if (lane < ci.len) {
-      gv = ldf(gb + int64_t(lane) * a.g_st);
-      bv = ldf(bb + int64_t(lane) * a.b_st);
-    }
+  for (int dt = 0; dt < DK / 16; ++dt)
+    qe[dt] = __builtin_bit_cast(bf16x4, buf_ld8(qbuf, ((16 * w + ln) * a.q_st + 16 * dt + 4 * g) * 2));
+  if (w == 0) {  // the inclusive prefix sum of g
     float s = gv;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -743,7 +734,9 @@ bool chunk_mfma_eligible(const GdnArgs &a, int chunk, int in_dtype, int out_dtyp
   // 16-byte row loads of q / k / v
   const int64_t st = a.q_sb | a.q_sh | a.q_st | a.k_sb | a.k_sh | a.k_st | a.v_sb | a.v_sh | a.v_st;
   const uintptr_t p = reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.k) | reinterpret_cast<uintptr_t>(a.v);
-  return (st & 7) == 0 && (p & 15) == 0;
+  // chunk-relative byte offsets of the range-checked buffer loads stay below 2^31
+  const int64_t tmax = std::max({std::abs(a.q_st), std::abs(a.k_st), std::abs(a.v_st), std::abs(a.b_st), std::abs(a.g_st)});
+  return (st & 7) == 0 && (p & 15) == 0 && tmax * kC * 2 < (int64_t(1) << 30);
 }
 
 int launch_chunk_mfma(const GdnArgs &a, const ChunkArgs &ca, void *workspace, hipStream_t s) {
