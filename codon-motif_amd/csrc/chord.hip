@@ -1,18 +1,18 @@
 // Chord attention (causal softmax with the gated geometric-decay bias) for gfx950.
 //
 // chord_fwd_kernel (prefill): flash-style online softmax on bf16 MFMA
-// (v_mfma_f32_32x32x16_bf16, fp32 accumulation).  A workgroup is 4 waves that
-// share one kv head: with GQA the waves take different query heads of the same
-// 32-row query block, otherwise consecutive query blocks of one head.  Scores
-// are computed transposed, S^T = K Q^T, so each lane owns one query row and the
-// row max / row sum stay in registers (one cross-half exchange); the output is
-// accumulated transposed too, O^T += V^T P^T, which lets P feed the second
-// MFMA straight from registers (keys of a 16-key step are permuted to match
-// the accumulator layout, and V^T is read from LDS in the same permutation).
-// K tiles are staged row-major and V tiles transposed in LDS, double-buffered,
-// one barrier per 64-key tile.  The GGD bias depends only on d = key - i_abs,
-// so each wave evaluates it once per tile for the 95 distinct distances of its
-// 32x64 tile into an LDS vector instead of once per score.
+// (v_mfma_f32_16x16x32_bf16, fp32 accumulation), 16 query rows per wave.  A
+// workgroup is 4 waves that share one kv head: with GQA the waves take different
+// query heads of the same 16-row query block, otherwise consecutive query blocks
+// of one head.  Scores are computed transposed, S^T = K Q^T, so each lane owns one
+// query row (spread over the 4 lane groups of 16) and the row max needs two lane
+// swaps; the output is accumulated transposed too, O^T += V^T P^T, with P^T fed
+// from the score accumulators (two 16-key tiles per 32-key MFMA step) and V^T
+// staged in LDS in the matching key order.  K / V tiles are double-buffered in
+// LDS, loaded through range-checked buffers, one barrier per 64-key tile.  The
+// GGD bias depends only on d = key - i_abs: each wave evaluates it once per tile
+// for the 79 distances of its 16x64 tile into 4 shifted LDS copies, so every
+// lane reads its 4 consecutive distances with one aligned 16-byte load.
 //
 // chord_decode_kernel (decode / short queries over a long cache): split-K
 // flash-decoding.  A workgroup owns (split, kv head, batch row) and serves all
@@ -61,12 +61,40 @@ __device__ __forceinline__ __bf16 to_bf(float f) {
 }
 
 // ------------------------------------------------------------------ prefill
+__device__ __forceinline__ f32x4 mma16(const bf16x8 &a, const bf16x8 &b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Position of key k (0..63) in a V^T row: inside each 32-key group the keys
+// 4g..4g+3 and 16+4g..16+4g+3 are stored together at 8g, so one 16-byte read is the
+// MFMA A operand that pairs with P^T taken from two 16-key accumulator tiles.
+__device__ __forceinline__ int vperm(int k) {
+  return (k & 32) | ((k & 12) << 1) | ((k & 16) >> 2) | (k & 3);
+}
+
+// Max of x over the four 16-lane groups (lanes l, l^16, l^32, l^48) via the gfx950
+// lane-swap instructions: each returned pair holds x of both partners.
+__device__ __forceinline__ float max_lane_groups(float x) {
+  const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
+  const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(s16[0]), __uint_as_float(s16[1]));
+}
+__device__ __forceinline__ float sum_lane_groups(float x) {
+  const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
+  const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
+}
+
+constexpr int kRow = 72;  // LDS row stride (bf16) of the K and V^T tiles: 144 B rows
+
 template <int HPW>  // query heads per workgroup (the rest of the 4 waves take query blocks)
 __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
   constexpr int QBPW = 4 / HPW;
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
-  const int hl = lane & 31, hh = lane >> 5;
+  const int ln = lane & 15, g = lane >> 4;
   const int group = a.H / a.Hkv;
   const int hg = blockIdx.y, sq = blockIdx.z;
 
@@ -77,63 +105,65 @@ __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
   } else {
     batch = 0; tok0 = a.cu[sq]; Lq = a.cu[sq + 1] - tok0; Skv = Lq; q_start = 0;
   }
-  const int nqbg = (Lq + 32 * QBPW - 1) / (32 * QBPW);
+  const int nqbg = (Lq + 16 * QBPW - 1) / (16 * QBPW);
   if (static_cast<int>(blockIdx.x) >= nqbg) return;
   const int qbg = nqbg - 1 - blockIdx.x;  // heaviest (latest) query blocks first
 
   const int head = hg * HPW + (w % HPW);
   const int kvh = (hg * HPW) / group;
-  const int q0 = (qbg * QBPW + w / HPW) * 32;
-  const int my_q = q0 + hl;
+  const int q0 = (qbg * QBPW + w / HPW) * 16;
+  const int my_q = q0 + ln;  // this lane's query row (shared by its 4 lane groups)
   const bool q_valid = my_q < Lq;
   const int q_abs = q_start + my_q;
 
-  const int wg_q_last = min(Lq, (qbg + 1) * QBPW * 32) - 1;
+  const int wg_q_last = min(Lq, (qbg + 1) * QBPW * 16) - 1;
   const int kv_end = min(Skv, q_start + wg_q_last + 1);
   const int ntiles = (kv_end + kBN - 1) / kBN;
   const int wave_first_qabs = q_start + q0;
-  const int wave_kv_end = min(Skv, q_start + min(Lq, q0 + 32));
+  const int wave_kv_end = min(Skv, q_start + min(Lq, q0 + 16));
 
   const bf16_t *qp = static_cast<const bf16_t *>(a.q) + batch * a.q_sb + head * a.q_sh + int64_t(tok0) * a.q_st;
   const bf16_t *kp = static_cast<const bf16_t *>(a.k) + batch * a.k_sb + kvh * a.k_sh + int64_t(tok0) * a.k_st;
   const bf16_t *vp = static_cast<const bf16_t *>(a.v) + batch * a.v_sb + kvh * a.v_sh + int64_t(tok0) * a.v_st;
 
-  __shared__ __attribute__((aligned(16))) bf16_t sK[2][kBN][kKStride];
-  __shared__ __attribute__((aligned(16))) bf16_t sVt[2][kD][kVStride];
-  __shared__ float sBias[4][96];
+  __shared__ __attribute__((aligned(16))) bf16_t sK[2][kBN][kRow];   // K rows
+  __shared__ __attribute__((aligned(16))) bf16_t sV[2][kD][kRow];    // V^T rows, keys in vperm order
+  __shared__ __attribute__((aligned(16))) float sTab[4][4][80];      // per wave: 4 shifted bias tables
 
-  // Q^T as the B operand: lane holds Q[my_q][16 ks + 8 hh .. +8].
-  bf16x8 qreg[4];
+  // Range-checked buffers over the kv head's visible keys (rows past kv_end read 0).
+  const buf_t kbuf = make_buf(kp, kv_end > 0 ? static_cast<uint32_t>(((kv_end - 1) * a.k_st + kD) * 2) : 0u);
+  const buf_t vbuf = make_buf(vp, kv_end > 0 ? static_cast<uint32_t>(((kv_end - 1) * a.v_st + kD) * 2) : 0u);
+  const buf_t qbuf = make_buf(qp, Lq > 0 ? static_cast<uint32_t>(((Lq - 1) * a.q_st + kD) * 2) : 0u);
+
+  // Q^T as the B operand: lane holds Q[my_q][32 ks + 8g .. +8].
+  bf16x8 qreg[2];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    if (q_valid) qreg[ks] = *reinterpret_cast<const bf16x8 *>(qp + int64_t(my_q) * a.q_st + ks * 16 + hh * 8);
-    else qreg[ks] = bf16x8{};
-  }
+  for (int ks = 0; ks < 2; ++ks)
+    qreg[ks] = __builtin_bit_cast(bf16x8, buf_ld16(qbuf, (my_q * a.q_st + 32 * ks + 8 * g) * 2));
   const float alpha_h = a.alpha[head], beta_h = a.beta[head], mu_h = a.mu[head];
-  const float mul = q_valid ? a.ssmax[head] * a.log_n[batch * a.ln_sb + int64_t(tok0 + my_q) * a.ln_st] : 0.f;
+  const float lnv = a.log_n[batch * a.ln_sb + int64_t(tok0 + min(my_q, Lq - 1)) * a.ln_st];
+  const float mul = q_valid ? a.ssmax[head] * lnv : 0.f;
   const float c_qk = mul * a.scale * kLog2e;
   const float c_b = mul * kLog2e;
 
-  float m_run = -INFINITY, l_run = 0.f;
-  f32x16 oacc[2];
+  float m_run = -INFINITY, l_part = 0.f;  // l_part: this lane's share of the row sum
+  f32x4 oacc[4];
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) oacc[mt][j] = 0.f;
+  for (int mt = 0; mt < 4; ++mt) oacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Tile staging: K rows (2 x 16 B per thread), V transposed (2 keys x 8 d per thread).
+  // Tile staging: K rows (2 x 16 B per thread); V as key pairs (2 keys x 8 d).
   uint4 kst[2], vst[2];
+  const int vpair = tid & 31, vseg = tid >> 5;
   auto load_tile = [&](int t) {
     const int n0 = t * kBN;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      const int c = tid + 256 * r;
-      const int key = n0 + (c >> 3), dc = (c & 7) * 8;
-      kst[r] = key < kv_end ? *reinterpret_cast<const uint4 *>(kp + int64_t(key) * a.k_st + dc) : uint4{0, 0, 0, 0};
+      const int c = tid + 256 * r, key = n0 + (c >> 3), dc = (c & 7) * 8;
+      kst[r] = buf_ld16(kbuf, (key * a.k_st + dc) * 2);
     }
-    const int key0 = n0 + 2 * (tid >> 3), dc = (tid & 7) * 8;
-    vst[0] = key0 < kv_end ? *reinterpret_cast<const uint4 *>(vp + int64_t(key0) * a.v_st + dc) : uint4{0, 0, 0, 0};
-    vst[1] = key0 + 1 < kv_end ? *reinterpret_cast<const uint4 *>(vp + int64_t(key0 + 1) * a.v_st + dc) : uint4{0, 0, 0, 0};
+    const int key0 = n0 + 2 * vpair;
+    vst[0] = buf_ld16(vbuf, (key0 * a.v_st + 8 * vseg) * 2);
+    vst[1] = buf_ld16(vbuf, ((key0 + 1) * a.v_st + 8 * vseg) * 2);
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
@@ -141,15 +171,15 @@ __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
       const int c = tid + 256 * r;
       *reinterpret_cast<uint4 *>(&sK[buf][c >> 3][(c & 7) * 8]) = kst[r];
     }
-    const int kk = 2 * (tid >> 3), dc = (tid & 7) * 8;
     const uint32_t *v0 = reinterpret_cast<const uint32_t *>(&vst[0]);
     const uint32_t *v1 = reinterpret_cast<const uint32_t *>(&vst[1]);
+    const int col = vperm(2 * vpair);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t lo = (v0[i] & 0xffffu) | (v1[i] << 16);      // d = dc + 2i
-      const uint32_t hi = (v0[i] >> 16) | (v1[i] & 0xffff0000u);  // d = dc + 2i + 1
-      *reinterpret_cast<uint32_t *>(&sVt[buf][dc + 2 * i][kk]) = lo;
-      *reinterpret_cast<uint32_t *>(&sVt[buf][dc + 2 * i + 1][kk]) = hi;
+      const uint32_t lo = (v0[i] & 0xffffu) | (v1[i] << 16);      // d = 8 vseg + 2i
+      const uint32_t hi = (v0[i] >> 16) | (v1[i] & 0xffff0000u);  // d = 8 vseg + 2i + 1
+      *reinterpret_cast<uint32_t *>(&sV[buf][8 * vseg + 2 * i][col]) = lo;
+      *reinterpret_cast<uint32_t *>(&sV[buf][8 * vseg + 2 * i + 1][col]) = hi;
     }
   };
 
@@ -165,75 +195,80 @@ __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
     if (t + 1 < ntiles) load_tile(t + 1);
 
     if (n0 < wave_kv_end) {
-      // Bias vector for distances n0 - (wave_first_qabs + 31) + e, e in [0, 95).
-      for (int e = lane; e < 95; e += 64)
-        sBias[w][e] = ggd_bias(static_cast<float>(n0 - wave_first_qabs - 31 + e), alpha_h, beta_h, mu_h, a.eps);
-
-      f32x16 sacc[2];
+      // Bias (log2 units) for distances n0 - wave_first_qabs - 15 + e, e in [0, 79),
+      // stored in 4 copies shifted by c so that every lane's 4 consecutive entries
+      // are one aligned 16-byte read: copy c holds entry e at index e - c.
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
+      for (int i = 0; i < 2; ++i) {
+        const int e = lane + 64 * i;
+        if (e < 79) {
+          const float bv = ggd_bias(static_cast<float>(n0 - wave_first_qabs - 15 + e), alpha_h, beta_h, mu_h, a.eps);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) sacc[kt][j] = 0.f;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const bf16x8 kreg = *reinterpret_cast<const bf16x8 *>(&sK[buf][kt * 32 + hl][ks * 16 + hh * 8]);
-          sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kreg, qreg[ks], sacc[kt], 0, 0, 0);
+          for (int c = 0; c < 4; ++c)
+            if (e >= c) sTab[w][c][e - c] = bv;
         }
       }
-      __builtin_amdgcn_wave_barrier();
+      // S^T = K Q^T: tile kt holds S^T[16 kt + 4g + r][ln] (key n0 + 16 kt + 4g + r).
+      f32x4 sacc[4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        sacc[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const bf16x8 kreg = *reinterpret_cast<const bf16x8 *>(&sK[buf][16 * kt + ln][32 * ks + 8 * g]);
+          sacc[kt] = mma16(kreg, qreg[ks], sacc[kt]);
+        }
+      }
+      __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // bias table visible to the wave
 
       const bool need_mask = (n0 + kBN - 1 > wave_first_qabs) || (n0 + kBN > Skv);
       float mx = -INFINITY;
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
+      for (int kt = 0; kt < 4; ++kt) {
+        const int e0 = 16 * kt + 4 * g - ln + 15, c = e0 & 3;
+        const f32x4 b4 = *reinterpret_cast<const f32x4 *>(&sTab[w][c][e0 - c]);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int koff = kt * 32 + 8 * (j >> 2) + 4 * hh + (j & 3);  // key - n0
-          const float bias = sBias[w][koff + 31 - hl];
-          float s = fmaf(sacc[kt][j], c_qk, c_b * bias);
-          if (need_mask && (n0 + koff > q_abs || n0 + koff >= Skv)) s = -INFINITY;
-          sacc[kt][j] = s;
-          mx = fmaxf(mx, s);
+        for (int r = 0; r < 4; ++r) {
+          const int koff = 16 * kt + 4 * g + r;  // key - n0
+          float sv = fmaf(sacc[kt][r], c_qk, c_b * b4[r]);
+          if (need_mask && (n0 + koff > q_abs || n0 + koff >= Skv)) sv = -INFINITY;
+          sacc[kt][r] = sv;
+          mx = fmaxf(mx, sv);
         }
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = max_lane_groups(mx);
       const float m_new = fmaxf(m_run, mx);
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
       const float resc = fast_exp2(m_run - m_use);
       float rsum = 0.f;
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const float p = fast_exp2(sacc[kt][j] - m_use);
-          sacc[kt][j] = p;
-          rsum += p;
+        for (int r = 0; r < 4; ++r) {
+          const float pv = fast_exp2(sacc[kt][r] - m_use);
+          sacc[kt][r] = pv;
+          rsum += pv;
         }
-      rsum += __shfl_xor(rsum, 32, 64);
-      l_run = l_run * resc + rsum;
+      l_part = l_part * resc + rsum;
       m_run = m_new;
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) oacc[mt][j] *= resc;
+        for (int r = 0; r < 4; ++r) oacc[mt][r] *= resc;
 
-      // O^T += V^T P^T over 4 steps of 16 keys.
+      // O^T += V^T P^T: P^T from two accumulator tiles per 32-key step.
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
+      for (int kp2 = 0; kp2 < 2; ++kp2) {
+        bf16x8 pb;
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          bf16x8 pb;
+        for (int r = 0; r < 4; ++r) {
+          pb[r] = to_bf(sacc[2 * kp2][r]);
+          pb[4 + r] = to_bf(sacc[2 * kp2 + 1][r]);
+        }
 #pragma unroll
-          for (int i = 0; i < 8; ++i) pb[i] = to_bf(sacc[kt][8 * s + i]);
-          const int kb = kt * 32 + 16 * s + 4 * hh;
-#pragma unroll
-          for (int mt = 0; mt < 2; ++mt) {
-            const bf16_t *row = &sVt[buf][mt * 32 + hl][0];
-            const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(row + kb);
-            const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(row + kb + 8);
-            const bf16x8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-            oacc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, oacc[mt], 0, 0, 0);
-          }
+        for (int mt = 0; mt < 4; ++mt) {
+          const bf16x8 va = *reinterpret_cast<const bf16x8 *>(&sV[buf][16 * mt + ln][32 * kp2 + 8 * g]);
+          oacc[mt] = mma16(va, pb, oacc[mt]);
         }
       }
     }
@@ -242,22 +277,19 @@ __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
     __syncthreads();
   }
 
+  const float l_run = sum_lane_groups(l_part);
   if (q_valid) {
     const float inv = 1.f / fmaxf(l_run, 1e-20f);
     bf16_t *op = static_cast<bf16_t *>(a.out) + batch * a.o_sb + head * a.o_sh + int64_t(tok0 + my_q) * a.o_st;
+    // lane holds O[my_q][16 mt + 4g + r]
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int d = mt * 32 + 8 * g4 + 4 * hh;
-        uint2 pk;
-        pk.x = static_cast<uint32_t>(f32_to_bf16(oacc[mt][4 * g4 + 0] * inv)) |
-               (static_cast<uint32_t>(f32_to_bf16(oacc[mt][4 * g4 + 1] * inv)) << 16);
-        pk.y = static_cast<uint32_t>(f32_to_bf16(oacc[mt][4 * g4 + 2] * inv)) |
-               (static_cast<uint32_t>(f32_to_bf16(oacc[mt][4 * g4 + 3] * inv)) << 16);
-        *reinterpret_cast<uint2 *>(op + d) = pk;
-      }
-    if (a.lse && hh == 0)
+    for (int mt = 0; mt < 4; ++mt) {
+      uint2 pk;
+      pk.x = static_cast<uint32_t>(f32_to_bf16(oacc[mt][0] * inv)) | (static_cast<uint32_t>(f32_to_bf16(oacc[mt][1] * inv)) << 16);
+      pk.y = static_cast<uint32_t>(f32_to_bf16(oacc[mt][2] * inv)) | (static_cast<uint32_t>(f32_to_bf16(oacc[mt][3] * inv)) << 16);
+      *reinterpret_cast<uint2 *>(op + 16 * mt + 4 * g) = pk;
+    }
+    if (a.lse && g == 0)
       a.lse[(static_cast<size_t>(batch) * a.H + head) * a.L + tok0 + my_q] = m_run + fast_log2(l_run);
   }
 }
@@ -618,7 +650,7 @@ extern "C" int motif_chord_fwd(
   const int qbpw = 4 / hpw;
   const int maxlen = packed ? max_seqlen : L;
   if (maxlen <= 0) return MOTIF_OK;
-  dim3 grid((maxlen + 32 * qbpw - 1) / (32 * qbpw), H / hpw, packed ? nseq : B), block(256);
+  dim3 grid((maxlen + 16 * qbpw - 1) / (16 * qbpw), H / hpw, packed ? nseq : B), block(256);
   if (hpw == 4) chord_fwd_kernel<4><<<grid, block, 0, s>>>(a);
   else if (hpw == 2) chord_fwd_kernel<2><<<grid, block, 0, s>>>(a);
   else chord_fwd_kernel<1><<<grid, block, 0, s>>>(a);
