@@ -140,13 +140,19 @@ __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks)
     qreg[ks] = __builtin_bit_cast(bf16x8, buf_ld16(qbuf, (my_q * a.q_st + 32 * ks + 8 * g) * 2));
+  // logit = mul * (scale * q.k + bias), mul = ssmax[head] * log_n[row].  With
+  // sg = sign(ssmax[head]) (uniform per wave, log_n >= 0) the kernel works with
+  // u = sg * log2e * (scale * q.k + bias): the row max of the logits is |mul| times
+  // the row max of u, and p = exp2(|mul| * (u - m_u)).
   const float alpha_h = a.alpha[head], beta_h = a.beta[head], mu_h = a.mu[head];
+  const float ssm = a.ssmax[head];
+  const float sg = ssm < 0.f ? -1.f : 1.f;
   const float lnv = a.log_n[batch * a.ln_sb + int64_t(tok0 + min(my_q, Lq - 1)) * a.ln_st];
-  const float mul = q_valid ? a.ssmax[head] * lnv : 0.f;
-  const float c_qk = mul * a.scale * kLog2e;
-  const float c_b = mul * kLog2e;
+  const float amul = q_valid ? fabsf(ssm * lnv) : 0.f;  // |mul| >= 0
+  const float c_u = sg * a.scale * kLog2e;               // u = fma(q.k, c_u, table)
+  const float c_t = sg * kLog2e;                         // table entries: c_t * bias
 
-  float m_run = -INFINITY, l_part = 0.f;  // l_part: this lane's share of the row sum
+  float m_run = -INFINITY, l_part = 0.f;  // m_run in u units; l_part: this lane's share of the row sum
   f32x4 oacc[4];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) oacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -202,7 +208,7 @@ __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
       for (int i = 0; i < 2; ++i) {
         const int e = lane + 64 * i;
         if (e < 79) {
-          const float bv = ggd_bias(static_cast<float>(n0 - wave_first_qabs - 15 + e), alpha_h, beta_h, mu_h, a.eps);
+          const float bv = c_t * ggd_bias(static_cast<float>(n0 - wave_first_qabs - 15 + e), alpha_h, beta_h, mu_h, a.eps);
 #pragma unroll
           for (int c = 0; c < 4; ++c)
             if (e >= c) sTab[w][c][e - c] = bv;
@@ -221,6 +227,7 @@ __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
       }
       __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // bias table visible to the wave
 
+      // u = c_u q.k + table; masked keys (diagonal / cache-end tiles only) are -inf.
       const bool need_mask = (n0 + kBN - 1 > wave_first_qabs) || (n0 + kBN > Skv);
       float mx = -INFINITY;
 #pragma unroll
@@ -228,33 +235,49 @@ __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
         const int e0 = 16 * kt + 4 * g - ln + 15, c = e0 & 3;
         const f32x4 b4 = *reinterpret_cast<const f32x4 *>(&sTab[w][c][e0 - c]);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int koff = 16 * kt + 4 * g + r;  // key - n0
-          float sv = fmaf(sacc[kt][r], c_qk, c_b * b4[r]);
-          if (need_mask && (n0 + koff > q_abs || n0 + koff >= Skv)) sv = -INFINITY;
-          sacc[kt][r] = sv;
-          mx = fmaxf(mx, sv);
-        }
+        for (int r = 0; r < 4; ++r) sacc[kt][r] = fmaf(sacc[kt][r], c_u, b4[r]);
       }
+      if (need_mask) {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = n0 + 16 * kt + 4 * g + r;
+            if (key > q_abs || key >= Skv) sacc[kt][r] = -INFINITY;
+          }
+      }
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sacc[kt][r]);
       mx = max_lane_groups(mx);
-      const float m_new = fmaxf(m_run, mx);
+      // Lazy rescaling: the running max moves only when the tile exceeds it by more
+      // than 8 (log2 units of the logits), so p <= 2^8 and most tiles skip the
+      // rescale of the output accumulators.
+      const bool grow = amul * (mx - m_run) > 8.f || m_run == -INFINITY;
+      const float m_new = grow ? mx : m_run;
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float resc = fast_exp2(m_run - m_use);
+      const float resc = m_run == -INFINITY ? 0.f : fast_exp2(amul * (m_run - m_use));
+      const float nb = -amul * m_use;
       float rsum = 0.f;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float pv = fast_exp2(sacc[kt][r] - m_use);
+          const float u = sacc[kt][r];
+          const float pv = u == -INFINITY ? 0.f : fast_exp2(fmaf(u, amul, nb));
           sacc[kt][r] = pv;
           rsum += pv;
         }
-      l_part = l_part * resc + rsum;
+      if (__builtin_amdgcn_read_exec() & __ballot(grow)) {
+        l_part *= resc;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) oacc[mt][r] *= resc;
+      }
+      l_part += rsum;
       m_run = m_new;
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) oacc[mt][r] *= resc;
 
       // O^T += V^T P^T: P^T from two accumulator tiles per 32-key step.
 #pragma unroll
@@ -290,7 +313,7 @@ __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
       *reinterpret_cast<uint2 *>(op + 16 * mt + 4 * g) = pk;
     }
     if (a.lse && g == 0)
-      a.lse[(static_cast<size_t>(batch) * a.H + head) * a.L + tok0 + my_q] = m_run + fast_log2(l_run);
+      a.lse[(static_cast<size_t>(batch) * a.H + head) * a.L + tok0 + my_q] = amul * m_run + fast_log2(l_run);
   }
 }
 

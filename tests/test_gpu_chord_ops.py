@@ -137,3 +137,16 @@ def test_fp32_mode(B, H, Hkv, L, S):
     ref = ochord.chord_attention(q, k, v, alpha, beta, mu, ssmax, log_n, S - L)
     err = (out.double().cpu() - ref).abs().max().item()
     assert err <= 1e-4, err
+
+
+@pytest.mark.parametrize('L,S', [(200, 200), (77, 300)])
+def test_prefill_signed_ssmax_and_mu(L, S):
+    '''Negative, zero-crossing and positive ssmax with a nonzero mu (bf16 prefill).'''
+    ops = _ops()
+    B, H, Hkv = 2, 8, 2
+    q, k, v, alpha, beta, mu, ssmax = chord_inputs(B, H, Hkv, L, S, seed=L * 7 + S)
+    ssmax = torch.linspace(-1.5, 1.5, H)
+    mu = torch.linspace(-3.0, 2.0, H)
+    log_n = _log_n(B, L, S - L)
+    out = _run(ops, q, k, v, alpha, beta, mu, ssmax, log_n)
+    _check_heads(out.cpu(), q, k, v, alpha, beta, mu, ssmax, log_n, S - L, what=f'signed ssmax L={L}')
