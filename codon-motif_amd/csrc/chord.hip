@@ -80,12 +80,6 @@ __device__ __forceinline__ float max_lane_groups(float x) {
   const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(s16[0]), __uint_as_float(s16[1]));
 }
-__device__ __forceinline__ float sum_lane_groups(float x) {
-  const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
-  const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
-}
 
 constexpr int kRow = 72;  // LDS row stride (bf16) of the K and V^T tiles: 144 B rows
 
@@ -152,10 +146,16 @@ __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
   const float c_u = sg * a.scale * kLog2e;               // u = fma(q.k, c_u, table)
   const float c_t = sg * kLog2e;                         // table entries: c_t * bias
 
-  float m_run = -INFINITY, l_part = 0.f;  // m_run in u units; l_part: this lane's share of the row sum
-  f32x4 oacc[4];
+  float m_run = -INFINITY;  // in u units
+  // O^T accumulators (tiles 0..3) and a fifth tile that multiplies P by ones: its
+  // entries are the row sums of P (bf16-rounded, as used in the output), so the
+  // normaliser follows the rescales of the output for free.
+  f32x4 oacc[5];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) oacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int mt = 0; mt < 5; ++mt) oacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  bf16x8 ones;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ones[i] = static_cast<__bf16>(1.f);
 
   // Tile staging: K rows (2 x 16 B per thread); V as key pairs (2 keys x 8 d).
   uint4 kst[2], vst[2];
@@ -259,24 +259,27 @@ __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
       const float resc = m_run == -INFINITY ? 0.f : fast_exp2(amul * (m_run - m_use));
       const float nb = -amul * m_use;
-      float rsum = 0.f;
+      // p = exp2(|mul| (u - m)); masked keys give exactly 0 (also when |mul| = 0).
+      if (need_mask) {
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+        for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float u = sacc[kt][r];
-          const float pv = u == -INFINITY ? 0.f : fast_exp2(fmaf(u, amul, nb));
-          sacc[kt][r] = pv;
-          rsum += pv;
-        }
+          for (int r = 0; r < 4; ++r) {
+            const float u = sacc[kt][r];
+            sacc[kt][r] = u == -INFINITY ? 0.f : fast_exp2(fmaf(u, amul, nb));
+          }
+      } else {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sacc[kt][r] = fast_exp2(fmaf(sacc[kt][r], amul, nb));
+      }
       if (__builtin_amdgcn_read_exec() & __ballot(grow)) {
-        l_part *= resc;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < 5; ++mt)
 #pragma unroll
           for (int r = 0; r < 4; ++r) oacc[mt][r] *= resc;
       }
-      l_part += rsum;
       m_run = m_new;
 
       // O^T += V^T P^T: P^T from two accumulator tiles per 32-key step.
@@ -293,6 +296,7 @@ __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
           const bf16x8 va = *reinterpret_cast<const bf16x8 *>(&sV[buf][16 * mt + ln][32 * kp2 + 8 * g]);
           oacc[mt] = mma16(va, pb, oacc[mt]);
         }
+        oacc[4] = mma16(ones, pb, oacc[4]);  // every row of tile 4: the row sum of P
       }
     }
 
@@ -300,7 +304,7 @@ __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
     __syncthreads();
   }
 
-  const float l_run = sum_lane_groups(l_part);
+  const float l_run = oacc[4][0];
   if (q_valid) {
     const float inv = 1.f / fmaxf(l_run, 1e-20f);
     bf16_t *op = static_cast<bf16_t *>(a.out) + batch * a.o_sb + head * a.o_sh + int64_t(tok0 + my_q) * a.o_st;

@@ -150,3 +150,17 @@ def test_prefill_signed_ssmax_and_mu(L, S):
     log_n = _log_n(B, L, S - L)
     out = _run(ops, q, k, v, alpha, beta, mu, ssmax, log_n)
     _check_heads(out.cpu(), q, k, v, alpha, beta, mu, ssmax, log_n, S - L, what=f'signed ssmax L={L}')
+
+
+def test_varlen_long_sequences_split_keys():
+    '''Packed sequences longer than one key-range split (1024 keys) of the prefill.'''
+    ops = _ops()
+    lens = [1200, 5, 1500]
+    cu = torch.tensor([0] + list(torch.cumsum(torch.tensor(lens), 0)), dtype=torch.int32)
+    T = int(cu[-1])
+    H, Hkv = 4, 1
+    q, k, v, alpha, beta, mu, ssmax = chord_inputs(1, H, Hkv, T, T, seed=29)
+    log_n = torch.cat([ochord.log_n_table(0, n) for n in lens]).float()[None]
+    out = ops.apply_chord_attention_varlen(*(t.to(DEV) for t in (q, k, v, alpha, beta, mu, ssmax, log_n)), cu.to(DEV))
+    ref = ochord.chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, cu, softmax_scale=64 ** -0.5)
+    assert_bf16_close(out, ref, what='varlen long')
