@@ -28,6 +28,10 @@ FLAGS = [
     '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
     '-I', os.path.join(os.path.dirname(os.path.dirname(HERE)), 'include'),
 ]
+# Per-source extras.  chord.hip: MFMA accumulators in ordinary VGPRs, so the softmax
+# and rescale code reads them without accumulator-register copies (the GDN kernels
+# keep the default: their register budgets rely on the accumulator file).
+EXTRA = {'chord.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form']}
 
 
 def _run(cmd, verbose):
@@ -52,7 +56,8 @@ def build(jobs=None, verbose=False):
     objs = [os.path.join(BUILD_DIR, os.path.basename(s)[:-4] + '.o') for s in srcs]
     jobs = jobs or min(len(srcs), os.cpu_count() or 1, 8)
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        futs = [ex.submit(_run, [HIPCC, *FLAGS, '-c', s, '-o', o], verbose) for s, o in zip(srcs, objs)]
+        futs = [ex.submit(_run, [HIPCC, *FLAGS, *EXTRA.get(os.path.basename(s), []), '-c', s, '-o', o], verbose)
+                for s, o in zip(srcs, objs)]
         for f in futs:
             f.result()
     tmp = OUT + '.tmp'
