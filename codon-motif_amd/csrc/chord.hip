@@ -364,20 +364,60 @@ template <> struct Row8<float> {
   }
 };
 
+// GGD bias table per head in log2 units: entry j holds delta = j - kTabPad (delta =
+// i_abs - key; the kTabPad leading entries, delta < 0, belong to masked keys and only
+// keep every 32-byte read that contains a visible key inside the table):
+// tab[h][j] = log2e * (-alpha_h (|-delta - mu_h| + eps)^beta_h).
+constexpr int kTabPad = 8;
+__global__ void __launch_bounds__(256) chord_bias_table_kernel(ChordArgs a, float *tab, int n) {
+  const int h = blockIdx.y, j = blockIdx.x * 256 + threadIdx.x;
+  if (j < n)
+    tab[static_cast<size_t>(h) * n + j] =
+        kLog2e * ggd_bias(static_cast<float>(kTabPad - j), a.alpha[h], a.beta[h], a.mu[h], a.eps);
+}
+
+// Sum over the 8 lanes of an aligned 8-lane group (DPP: quad swaps, then half-row mirror).
+__device__ __forceinline__ float sum8(float x) {
+  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x141, 0xF, 0xF, false));  // row_half_mirror
+  return x;
+}
+
+// 8 features of one K / V row as floats from a range-checked buffer (0 past the end).
+template <typename T> __device__ __forceinline__ void buf_row8(buf_t r, uint32_t off, float x[8]);
+template <> __device__ __forceinline__ void buf_row8<bf16_t>(buf_t r, uint32_t off, float x[8]) {
+  const uint4 u = buf_ld16(r, off);
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x[2 * e] = __uint_as_float(w[e] << 16);
+    x[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+  }
+}
+template <> __device__ __forceinline__ void buf_row8<float>(buf_t r, uint32_t off, float x[8]) {
+  const uint4 u = buf_ld16(r, off), v = buf_ld16(r, off + 16);
+  x[0] = __uint_as_float(u.x); x[1] = __uint_as_float(u.y); x[2] = __uint_as_float(u.z); x[3] = __uint_as_float(u.w);
+  x[4] = __uint_as_float(v.x); x[5] = __uint_as_float(v.y); x[6] = __uint_as_float(v.z); x[7] = __uint_as_float(v.w);
+}
+
 // Rows of a workgroup: global row gr = qc * R + r over the L * group (query,
 // head) pairs of one kv head, query i = gr / group, head = kvh * group + gr % group.
+// A wave takes 64 consecutive keys per step: lane (ksub = lane / 8, 8 features
+// from column 8 (lane % 8)) owns keys n0 + 8 ksub + it, it < 8, whose 8 bias
+// entries are 2 contiguous 16-byte reads of the head's table.  Each 8-lane group
+// keeps its own running max / sum / output (merged at the end), so the step has
+// no cross-lane traffic besides the 8-lane dot-product sums.
 template <typename T, int R>
-__global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a) {
+__global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a, const float *tab, int tab_n) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int split = blockIdx.x, kvh = blockIdx.y;
   const int b = blockIdx.z / a.nqc, qc = blockIdx.z % a.nqc;
   const int group = a.H / a.Hkv;
   const int total_rows = a.L * group;
   const int dc = (lane & 7) * 8;  // this lane's 8 feature columns
-  const int ksub = lane >> 3;     // key within an 8-key row group
+  const int ksub = lane >> 3;     // key group of this lane
   const T *qg = static_cast<const T *>(a.q);
-  const T *kg = static_cast<const T *>(a.k);
-  const T *vg = static_cast<const T *>(a.v);
   T *og = static_cast<T *>(a.out);
 
   const int kv_len = min(a.S, a.q_start + a.L);
@@ -386,8 +426,9 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a) {
   const int k_lo = split * per;
   const int k_hi = min(min(kv_len, k_lo + per), a.q_start + i_last + 1);
 
-  float q[R][8], c_qk[R], c_b[R], al[R], be[R], mu[R];
+  float q[R][8], c_qk[R], c_b[R];
   int qabs[R];
+  buf_t tb[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int gr = qc * R + r;
@@ -397,9 +438,9 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a) {
     load8(qg + b * a.q_sb + head * a.q_sh + int64_t(i) * a.q_st + dc, q[r]);
     const float mul = ok ? a.ssmax[head] * a.log_n[b * a.ln_sb + int64_t(i) * a.ln_st] : 0.f;
     c_qk[r] = mul * a.scale * kLog2e;
-    c_b[r] = mul * kLog2e;
-    al[r] = a.alpha[head]; be[r] = a.beta[head]; mu[r] = a.mu[head];
+    c_b[r] = mul;  // the table is in log2 units already
     qabs[r] = ok ? a.q_start + i : -1;
+    tb[r] = make_buf(tab + static_cast<size_t>(head) * tab_n, static_cast<uint32_t>(tab_n) * 4u);
   }
 
   float m[R], l[R], acc[R][8];
@@ -410,88 +451,85 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a) {
     for (int e = 0; e < 8; ++e) acc[r][e] = 0.f;
   }
 
-  const T *kp = kg + b * a.k_sb + kvh * a.k_sh + dc;
-  const T *vp = vg + b * a.v_sb + kvh * a.v_sh + dc;
+  const T *kp = static_cast<const T *>(a.k) + b * a.k_sb + kvh * a.k_sh;
+  const T *vp = static_cast<const T *>(a.v) + b * a.v_sb + kvh * a.v_sh;
+  const buf_t kbuf = make_buf(kp, k_hi > 0 ? static_cast<uint32_t>(((k_hi - 1) * a.k_st + kD) * sizeof(T)) : 0u);
+  const buf_t vbuf = make_buf(vp, k_hi > 0 ? static_cast<uint32_t>(((k_hi - 1) * a.v_st + kD) * sizeof(T)) : 0u);
 
   for (int n0 = k_lo + w * kBN; n0 < k_hi; n0 += 4 * kBN) {
-    Row8<T> kf[8], vf[8];
+    const int kb = n0 + 8 * ksub;  // this lane group's first key
+    float kf[8][8], vf[8][8], bt[R][8];
 #pragma unroll
     for (int it = 0; it < 8; ++it) {
-      const int key = n0 + 8 * it + ksub;
-      if (key < k_hi) {
-        kf[it].load(kp + int64_t(key) * a.k_st);
-        vf[it].load(vp + int64_t(key) * a.v_st);
-      } else {
-        kf[it].zero();
-        vf[it].zero();
-      }
+      buf_row8<T>(kbuf, static_cast<uint32_t>(((kb + it) * a.k_st + dc) * sizeof(T)), kf[it]);
+      buf_row8<T>(vbuf, static_cast<uint32_t>(((kb + it) * a.v_st + dc) * sizeof(T)), vf[it]);
     }
-    float s[R][8];
 #pragma unroll
-    for (int it = 0; it < 8; ++it) {
+    for (int r = 0; r < R; ++r) {  // entries delta = qabs - kb - 7 .. qabs - kb (it = 7 .. 0)
+      const uint32_t off = static_cast<uint32_t>(qabs[r] - kb - 7 + kTabPad) * 4u;
+      const uint4 lo = buf_ld16(tb[r], off), hi = buf_ld16(tb[r], off + 16);
+      const uint32_t wv[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        float d = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) d = fmaf(q[r][e], kf[it].get(e), d);
-        d += __shfl_xor(d, 1, 64);
-        d += __shfl_xor(d, 2, 64);
-        d += __shfl_xor(d, 4, 64);
-        s[r][it] = d;
-      }
+      for (int it = 0; it < 8; ++it) bt[r][it] = __uint_as_float(wv[7 - it]);
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      float mx = -INFINITY;
+      float sv[8], mx = -INFINITY;
 #pragma unroll
       for (int it = 0; it < 8; ++it) {
-        const int key = n0 + 8 * it + ksub;
-        float x = -INFINITY;
-        if (key < k_hi && key <= qabs[r])
-          x = fmaf(s[r][it], c_qk[r], c_b[r] * ggd_bias(static_cast<float>(key - qabs[r]), al[r], be[r], mu[r], a.eps));
-        s[r][it] = x;
-        mx = fmaxf(mx, x);
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d = fmaf(q[r][e], kf[it][e], d);
+        d = sum8(d);
+        const int key = kb + it;
+        const bool ok = key < k_hi && key <= qabs[r];
+        sv[it] = ok ? fmaf(d, c_qk[r], c_b[r] * bt[r][it]) : -INFINITY;
+        mx = fmaxf(mx, sv[it]);
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
       const float m_new = fmaxf(m[r], mx);
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float resc = fast_exp2(m[r] - m_use);
+      const float resc = m[r] == -INFINITY ? 0.f : fast_exp2(m[r] - m_use);
       float ps = 0.f;
 #pragma unroll
       for (int it = 0; it < 8; ++it) {
-        const float p = fast_exp2(s[r][it] - m_use);
-        s[r][it] = p;
-        ps += p;
+        sv[it] = sv[it] == -INFINITY ? 0.f : fast_exp2(sv[it] - m_use);
+        ps += sv[it];
       }
-      ps += __shfl_xor(ps, 8, 64);
-      ps += __shfl_xor(ps, 16, 64);
-      ps += __shfl_xor(ps, 32, 64);
       l[r] = l[r] * resc + ps;
       m[r] = m_new;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[r][e] *= resc;
+      for (int e = 0; e < 8; ++e) {
+        float x = acc[r][e] * resc;
+#pragma unroll
+        for (int it = 0; it < 8; ++it) x = fmaf(sv[it], vf[it][e], x);
+        acc[r][e] = x;
+      }
     }
-#pragma unroll
-    for (int it = 0; it < 8; ++it)
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-#pragma unroll
-        for (int r = 0; r < R; ++r) acc[r][e] = fmaf(s[r][it], vf[it].get(e), acc[r][e]);
   }
 
-  // Finish the per-wave accumulators (sum over the 8 key sub-rows).
+  // Merge the 8 key groups of the wave (lanes l, l^8, l^16, l^32 share features).
 #pragma unroll
-  for (int r = 0; r < R; ++r)
+  for (int r = 0; r < R; ++r) {
+    float M = m[r];
+    M = fmaxf(M, __shfl_xor(M, 8, 64));
+    M = fmaxf(M, __shfl_xor(M, 16, 64));
+    M = fmaxf(M, __shfl_xor(M, 32, 64));
+    const float f = m[r] == -INFINITY ? 0.f : fast_exp2(m[r] - (M == -INFINITY ? 0.f : M));
+    float lx = l[r] * f;
+    lx += __shfl_xor(lx, 8, 64);
+    lx += __shfl_xor(lx, 16, 64);
+    lx += __shfl_xor(lx, 32, 64);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      float x = acc[r][e];
+      float x = acc[r][e] * f;
       x += __shfl_xor(x, 8, 64);
       x += __shfl_xor(x, 16, 64);
       x += __shfl_xor(x, 32, 64);
       acc[r][e] = x;
     }
+    m[r] = M;
+    l[r] = lx;
+  }
 
   // Merge the 4 waves in LDS.
   __shared__ float sm[4][R], sl[4][R], sacc[4][R][kD];
@@ -578,12 +616,19 @@ static int decode_splits(int B, int Hkv, int S) {
 }
 
 template <typename T>
-static void launch_decode(const ChordArgs &a, int R, hipStream_t s) {
+static void launch_decode(const ChordArgs &a, int R, const float *tab, int tab_n, hipStream_t s) {
   const dim3 grid(a.splits, a.Hkv, a.B * a.nqc), block(256);
-  if (R <= 1) chord_decode_kernel<T, 1><<<grid, block, 0, s>>>(a);
-  else if (R <= 2) chord_decode_kernel<T, 2><<<grid, block, 0, s>>>(a);
-  else if (R <= 4) chord_decode_kernel<T, 4><<<grid, block, 0, s>>>(a);
-  else chord_decode_kernel<T, 8><<<grid, block, 0, s>>>(a);
+  if (R <= 1) chord_decode_kernel<T, 1><<<grid, block, 0, s>>>(a, tab, tab_n);
+  else if (R <= 2) chord_decode_kernel<T, 2><<<grid, block, 0, s>>>(a, tab, tab_n);
+  else if (R <= 4) chord_decode_kernel<T, 4><<<grid, block, 0, s>>>(a, tab, tab_n);
+  else chord_decode_kernel<T, 8><<<grid, block, 0, s>>>(a, tab, tab_n);
+}
+
+// Workspace of the vector (decode / fp32) path: the bias table [H][S] fp32, then the
+// split partials [B][Hkv][splits][rows][D + 2] fp32.
+static int table_len(int S) { return std::max(S, 1) + kTabPad; }
+static size_t table_bytes(int H, int S) {
+  return (static_cast<size_t>(H) * table_len(S) * sizeof(float) + 255) / 256 * 256;
 }
 
 }  // namespace motif
@@ -595,9 +640,12 @@ extern "C" size_t motif_chord_workspace_bytes(int B, int H, int Hkv, int L, int 
   if (B > 0 && H > 0 && Hkv > 0 && H % Hkv == 0 && L > 0 && use_decode(H, Hkv, L, false))
     sp = decode_splits(B, Hkv, S);
   if (splits) *splits = sp;
-  if (sp <= 1) return 0;
-  const size_t rows = static_cast<size_t>(H / Hkv) * L;
-  return static_cast<size_t>(B) * Hkv * sp * rows * (D + 2) * sizeof(float);
+  if (B <= 0 || H <= 0 || Hkv <= 0 || L <= 0) return 0;
+  // the table is needed by every call that takes the vector kernel (decode shapes
+  // and fp32 inputs); it is small, so it is always included
+  size_t n = table_bytes(H, S);
+  if (sp > 1) n += static_cast<size_t>(B) * Hkv * sp * (static_cast<size_t>(H / Hkv) * L) * (D + 2) * sizeof(float);
+  return n;
 }
 
 extern "C" int motif_chord_fwd(
@@ -658,15 +706,19 @@ extern "C" int motif_chord_fwd(
       a.splits = decode_splits(B, Hkv, S);
     }
     a.nqc = (rows + R - 1) / R;
-    if (a.splits > 1) {
-      const size_t need = motif_chord_workspace_bytes(B, H, Hkv, L, S, D, nullptr);
-      if (!workspace || workspace_bytes < need)
-        return set_error(MOTIF_ERR_INVALID, "chord_fwd: workspace too small (need " + std::to_string(need) + " bytes)");
-      a.part = static_cast<float *>(workspace);
-    }
-    if (dtype == MOTIF_BF16) launch_decode<bf16_t>(a, R, s);
-    else launch_decode<float>(a, R, s);
-    int rc = check_launch("chord_decode_kernel");
+    const size_t tb = table_bytes(H, S);
+    const size_t need = tb + (a.splits > 1 ? static_cast<size_t>(B) * Hkv * a.splits * rows * (D + 2) * sizeof(float) : 0);
+    if (!workspace || workspace_bytes < need)
+      return set_error(MOTIF_ERR_INVALID, "chord_fwd: workspace too small (need " + std::to_string(need) + " bytes)");
+    float *tab = static_cast<float *>(workspace);
+    if (a.splits > 1) a.part = reinterpret_cast<float *>(static_cast<char *>(workspace) + tb);
+    const int tn = table_len(S);
+    chord_bias_table_kernel<<<dim3((tn + 255) / 256, H), dim3(256), 0, s>>>(a, tab, tn);
+    int rc = check_launch("chord_bias_table_kernel");
+    if (rc) return rc;
+    if (dtype == MOTIF_BF16) launch_decode<bf16_t>(a, R, tab, tn, s);
+    else launch_decode<float>(a, R, tab, tn, s);
+    rc = check_launch("chord_decode_kernel");
     if (rc || a.splits == 1) return rc;
     if (dtype == MOTIF_BF16) chord_merge_kernel<bf16_t><<<dim3(rows, Hkv, B), dim3(64), 0, s>>>(a);
     else chord_merge_kernel<float><<<dim3(rows, Hkv, B), dim3(64), 0, s>>>(a);
