@@ -1,11 +1,15 @@
 '''GatedDeltaAttention with the reference interface (motif/block/attention/gdn_attn.py:19-219).
 
 Same constructor arguments, parameter names / shapes / initialisation, cache
-type and forward contract.  The sequence mixing runs on the HIP kernels:
-short conv + SiLU (motif_short_conv_silu), then the delta rule
-(motif_gdn_recurrent_fwd for L == 1, motif_gdn_chunk_fwd otherwise).  The
-projections, L2 normalisation, gates, GatedRMSNorm and o_proj stay in
-PyTorch-ROCm.
+type and forward contract.  The six input projections (q, k, v, gate, a, b) run
+as one GEMM against their concatenated weights.  The sequence mixing runs on the
+HIP kernels:
+  * prefill (L > 1): short conv + SiLU with the q / k L2 norm fused in
+    (motif_short_conv_silu_l2norm), then the chunked delta rule (motif_gdn_chunk_fwd);
+  * decode (L == 1 with a cache): one fused kernel from the projections to the
+    GatedRMSNorm output (motif_gdn_decode_fused), updating the cache's recurrent
+    state and conv tails in place.
+GatedRMSNorm (prefill) and o_proj stay in PyTorch-ROCm.
 
 Precision: the reference casts q/k/v/beta/g to fp32 before the delta rule
 (:197).  Those tensors are produced in the activation dtype, so casting is
@@ -26,6 +30,7 @@ from motif.ops import (
     GatedRMSNorm,
     HAS_TRITON,
     chunk_gated_delta_rule,
+    gdn_decode_fused,
     recurrent_gated_delta_rule,
     short_conv_silu,
     short_conv_silu_varlen,
@@ -84,9 +89,41 @@ class GatedDeltaAttention(BasicAttention):
     def cache_type(cls) -> type:
         return GatedDeltaAttentionLayerCache
 
-    def _gates(self, hidden_states):
-        beta = torch.sigmoid(self.b_proj(hidden_states)).transpose(1, 2)
-        g = -self.A_log.exp() * F.softplus(self.a_proj(hidden_states) + self.dt_bias)
+    def _proj_weight(self):
+        '''[q | k | v | gate | a | b] projection weight and bias as one matrix.  Cached
+        (rebuilt when a weight is replaced or updated in place); rebuilt per call while
+        autograd records, so gradients reach the six nn.Linear parameters.'''
+        mods = (self.q_proj, self.k_proj, self.v_proj, self.g_proj, self.a_proj, self.b_proj)
+        params = [m.weight for m in mods] + ([m.bias for m in mods] if self.bias else [])
+        if torch.is_grad_enabled() and any(p.requires_grad for p in params):
+            w = torch.cat([m.weight for m in mods])
+            return w, (torch.cat([m.bias for m in mods]) if self.bias else None)
+        key = tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in params)
+        cached = self.__dict__.get('_proj_cat')
+        if cached is None or cached[0] != key:
+            with torch.no_grad():
+                w = torch.cat([m.weight for m in mods])
+                b = torch.cat([m.bias for m in mods]) if self.bias else None
+            cached = (key, w, b)
+            self.__dict__['_proj_cat'] = cached
+        return cached[1], cached[2]
+
+    def _proj_offsets(self):
+        '''Column offsets of q, k, v, gate, a, b in the fused projection.'''
+        hk, hv, H = self.num_heads * self.dk, self.num_heads * self.dv, self.num_heads
+        return (0, hk, 2 * hk, 2 * hk + hv, 2 * hk + 2 * hv, 2 * hk + 2 * hv + H)
+
+    def _project(self, hidden_states):
+        '''All six projections -> (q, k, v, gate, a, b) views of one [B, L, ncols] result.'''
+        w, b = self._proj_weight()
+        proj = F.linear(hidden_states, w, b)
+        offs = self._proj_offsets()
+        ends = offs[1:] + (proj.shape[-1],)
+        return proj, tuple(proj[..., s:e] for s, e in zip(offs, ends))
+
+    def _gates(self, a, b):
+        beta = torch.sigmoid(b).transpose(1, 2)
+        g = -self.A_log.exp() * F.softplus(a + self.dt_bias)
         return beta, g.transpose(1, 2)
 
     def _heads(self, q, k, v, B, L, normalized=False):
@@ -98,12 +135,11 @@ class GatedDeltaAttention(BasicAttention):
             k = F.normalize(k, dim=-1)
         return q, k, v
 
-    def _qkv(self, hidden_states, tails, B, L, cu_seqlens=None, max_len=None):
-        '''q / k / v projections through conv + SiLU; q and k then L2-normalised per
+    def _qkv(self, xs, tails, B, L, cu_seqlens=None, max_len=None):
+        '''q / k / v projections `xs` through conv + SiLU; q and k then L2-normalised per
         head (q also scaled by dk^-1/2), inside the conv kernel when dk <= 64.'''
         fused = self.dk in (16, 32, 64)
         hd = self.dk if fused else None
-        xs = (self.q_proj(hidden_states), self.k_proj(hidden_states), self.v_proj(hidden_states))
         ws = (self.q_conv.weight, self.k_conv.weight, self.v_conv.weight)
         opts = ((hd, self.dk ** -0.5), (hd, 1.0), (None, 1.0))
         outs = []
@@ -116,11 +152,52 @@ class GatedDeltaAttention(BasicAttention):
         q, k, v = self._heads(outs[0][0], outs[1][0], outs[2][0], B, L, normalized=fused)
         return q, k, v, tuple(o[1] for o in outs)
 
-    def _output(self, o, hidden_states, B, L):
-        o = o.to(hidden_states.dtype).transpose(1, 2)
-        gate = self.g_proj(hidden_states).view(B, L, self.num_heads, self.dv)
-        o = self.o_norm(torch.cat([o, gate.to(o.dtype)], dim=-1)).reshape(B, L, -1)
+    def _output(self, o, gate, B, L):
+        o = o.to(gate.dtype).transpose(1, 2)
+        gate = gate.reshape(B, L, self.num_heads, self.dv)
+        o = self.o_norm(torch.cat([o, gate], dim=-1)).reshape(B, L, -1)
         return self.o_proj(o)
+
+    def _decode_fusable(self, hidden_states, cache):
+        '''True when one decode step can run as the fused kernel: one token, a cache whose
+        state / tails (if present) are in the kernel's layout, inference only.'''
+        B, L, _ = hidden_states.shape
+        if L != 1 or not hidden_states.is_cuda or hidden_states.dtype not in (torch.float32, torch.bfloat16):
+            return False
+        if self.dk not in (16, 32, 64) or self.dv > 128 or not 2 <= self.conv_size <= 5:
+            return False
+        if self.o_norm.weight is None or (torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters())):
+            return False
+        S = cache.state
+        if S is not None and (S.dtype != torch.float32 or not S.is_contiguous() or not S.is_cuda
+                              or tuple(S.shape) != (B, self.num_heads, self.dk, self.dv)):
+            return False
+        if cache.conv_state is not None:
+            chans = (self.num_heads * self.dk, self.num_heads * self.dk, self.num_heads * self.dv)
+            for t, c in zip(cache.conv_state, chans):
+                if (t is None or t.dtype != hidden_states.dtype or not t.is_contiguous() or not t.is_cuda
+                        or tuple(t.shape) != (B, c, self.conv_size - 1)):
+                    return False
+        return True
+
+    def _decode_step(self, hidden_states, cache):
+        '''One token through the fused decode kernel; the cache's state and conv tails are
+        updated in place (allocated as zeros on the first step).'''
+        B = hidden_states.shape[0]
+        dev, dt = hidden_states.device, hidden_states.dtype
+        H, K = self.num_heads, self.conv_size
+        if cache.state is None:
+            cache.state = torch.zeros(B, H, self.dk, self.dv, dtype=torch.float32, device=dev)
+        if cache.conv_state is None:
+            cache.conv_state = tuple(torch.zeros(B, c, K - 1, dtype=dt, device=dev)
+                                     for c in (H * self.dk, H * self.dk, H * self.dv))
+        w, b = self._proj_weight()
+        proj = F.linear(hidden_states.view(B, -1), w, b)
+        y = gdn_decode_fused(proj, self._proj_offsets(), (self.q_conv.weight, self.k_conv.weight, self.v_conv.weight),
+                             cache.conv_state, self.A_log, self.dt_bias, self.o_norm.weight, self.o_norm.eps,
+                             cache.state, H, self.dk, self.dv)
+        cache.update(cache.state, cache.conv_state, steps=1)
+        return self.o_proj(y.view(B, 1, -1))
 
     def forward(self, hidden_states: torch.Tensor, past_key_value=None) -> AttentionOutput:
         '''Run the layer over [B, L, hidden]; continue from / update `past_key_value`.'''
@@ -136,14 +213,19 @@ class GatedDeltaAttention(BasicAttention):
             tails = (None, None, None)
             S0 = None
 
-        q, k, v, (cq, ck, cv) = self._qkv(hidden_states, tails, B, L)
-        beta, g = self._gates(hidden_states)
+        if use_cache and self._decode_fusable(hidden_states, past_key_value):
+            output = self._decode_step(hidden_states, past_key_value)
+            return AttentionOutput(output=output, past_key_value=past_key_value)
+
+        _, (xq, xk, xv, gate, xa, xb) = self._project(hidden_states)
+        q, k, v, (cq, ck, cv) = self._qkv((xq, xk, xv), tails, B, L)
+        beta, g = self._gates(xa, xb)
 
         if L == 1:
             o, S = recurrent_gated_delta_rule(q, k, v, beta, g, S0)
         else:
             o, S = chunk_gated_delta_rule(q, k, v, beta, g, S0, self.chunk_size)
-        output = self._output(o, hidden_states, B, L)
+        output = self._output(o, gate, B, L)
 
         if use_cache:
             past_key_value.update(S, (cq, ck, cv), steps=L)
@@ -160,8 +242,9 @@ class GatedDeltaAttention(BasicAttention):
             raise ValueError('forward_varlen expects packed sequences with B == 1')
         lens = cu_seqlens.detach().cpu()
         max_len = int((lens[1:] - lens[:-1]).max()) if lens.numel() > 1 else 0
-        q, k, v, (cq, ck, cv) = self._qkv(hidden_states, (None, None, None), B, L, cu_seqlens, max_len)
-        beta, g = self._gates(hidden_states)
+        _, (xq, xk, xv, gate, xa, xb) = self._project(hidden_states)
+        q, k, v, (cq, ck, cv) = self._qkv((xq, xk, xv), (None, None, None), B, L, cu_seqlens, max_len)
+        beta, g = self._gates(xa, xb)
         o, S = chunk_gated_delta_rule_varlen(q, k, v, beta, g, cu_seqlens, None, self.chunk_size)
-        output = self._output(o, hidden_states, B, L)
+        output = self._output(o, gate, B, L)
         return AttentionOutput(output=output, payload={'state': S, 'conv_state': (cq, ck, cv)})

@@ -165,6 +165,26 @@ int motif_chord_fwd(
     int dtype, void *stream);
 
 /*
+ * One decode step of a GatedDeltaAttention layer after its input projections, fused:
+ * conv + SiLU of the new token (q, k, v; conv tails shifted in place), q / k L2
+ * normalisation (q * dk^-1/2), gates beta = sigmoid(b), g = -exp(A_log) softplus(a +
+ * dt_bias), the delta-rule update of the fp32 state (in place) and the GatedRMSNorm
+ * of the head outputs.  Replaces the L == 1 path of
+ * motif/block/attention/gdn_attn.py:183-209 (conv :116-136, recurrent_gated_delta_rule
+ * motif/ops/gated_deltanet.py:26-59, GatedRMSNorm motif/ops/rms_norm.py:530-553).
+ *   proj [B, ncols] (row stride proj_sb) holds the projections at column offsets
+ *   q_off (H*dk), k_off (H*dk), v_off (H*dv), g_off (H*dv, the norm gate), a_off (H),
+ *   b_off (H); wq, wk [H*dk, K], wv [H*dv, K] conv weights; tail_q/k/v [B, C, K-1];
+ *   a_log, dt_bias [H]; norm_weight [dv]; state [B, H, dk, dv] fp32; y [B, H*dv]
+ *   (row stride y_sb).  All but the state in `dtype`.  dk in {16, 32, 64}, dv <= 128.
+ */
+int motif_gdn_decode_fused(
+    const void *proj, int64_t proj_sb, int q_off, int k_off, int v_off, int g_off, int a_off, int b_off,
+    const void *wq, const void *wk, const void *wv, void *tail_q, void *tail_k, void *tail_v,
+    const void *a_log, const void *dt_bias, const void *norm_weight, float norm_eps,
+    float *state, void *y, int64_t y_sb, int B, int H, int dk, int dv, int K, int dtype, void *stream);
+
+/*
  * Intra-block attention-residual read (one fused pass):
  *   r_n = 1/sqrt(mean(x_n^2) + eps), s_n = sum_d query_d * weight_d * x_nd * r_n,
  *   alpha = softmax_n(s), out = sum_n alpha_n * x_n      (fp32 arithmetic)

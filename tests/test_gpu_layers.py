@@ -181,9 +181,36 @@ def test_tiny_model_decode_after_prefill_matches_full_forward():
 
 
 @torch.no_grad()
+def test_gdn_layer_varlen_equals_independent_runs():
+    """Packed GDN layer (conv, chunked rule, GatedRMSNorm) vs separate runs of each
+    sequence, including a one-token sequence (the recurrence path): exact up to fp32
+    rounding in fp32, and the bf16 bar in bf16 (measured bit-identical)."""
+    cfg, t = _fixture('gdn_layer')
+    cu = torch.tensor([0, 30, 31, 80], dtype=torch.int32, device=DEV)
+    for dt in (torch.float32, torch.bfloat16):
+        layer = _gdn_layer(cfg, dt)
+        x = t['x'][:1, :80].to(DEV, dt)
+        packed = layer.forward_varlen(x, cu).output
+        s = 0
+        for n in (30, 1, 49):
+            single = layer(x[:, s:s + n]).output
+            if dt == torch.float32:
+                assert_fp32_close(packed[:, s:s + n], single, 1e-5, f'fp32 seq len {n}')
+            else:
+                assert_bf16_close(packed[:, s:s + n], single, 2e-2, 5e-3, f'bf16 seq len {n}')
+            s += n
+
+
+@torch.no_grad()
 def test_tiny_model_varlen_equals_independent_runs():
     """Packed sequences vs separate runs of each sequence (both bf16 HIP paths;
-    they differ only in GEMM shapes and hence bf16 rounding)."""
+    they differ only in GEMM shapes and hence bf16 rounding).
+
+    The one-token sequence runs every GEMM with M = 1, which rounds differently
+    from the packed M = 80 GEMMs; this tiny random model amplifies that: the first
+    position of a 1-token and of a 2-token run (no packing involved) differ by the
+    same 1.0e-1 max-abs / 6.1e-2 mean-rel.  In fp32 those two agree to 1e-4, which
+    pins the L == 1 composition; the packed GDN layer alone is exact (above)."""
     cfg, t, model = _tiny_model(torch.bfloat16)
     lens = [30, 1, 49]
     ids = t['ids'][0, :80].to(DEV)
@@ -192,5 +219,10 @@ def test_tiny_model_varlen_equals_independent_runs():
     s = 0
     for n in lens:
         single = model(ids[None, s:s + n]).logits.float()
-        assert_bf16_close(packed[:, s:s + n], single, 0.2, 2e-2, f'seq len {n}')
+        bound = (0.2, 2e-2) if n > 1 else (0.2, 0.1)
+        assert_bf16_close(packed[:, s:s + n], single, *bound, f'seq len {n}')
         s += n
+    _, _, m32 = _tiny_model(torch.float32)
+    one = m32(ids[None, 30:31]).logits
+    two = m32(ids[None, 30:32]).logits[:, :1]
+    assert_fp32_close(one, two, 1e-4, 'fp32 L=1 vs first position of L=2')
