@@ -37,8 +37,30 @@ __global__ void __launch_bounds__(128) gdn_decode_kernel(GdnDecodeArgs a) {
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   __shared__ float sq[DK], sk[DK], sred[2];
+  const bool active = tid < a.dv;
 
+  // The state column, the gate and the norm weight do not depend on the conv: issue
+  // their loads first so their latency overlaps the conv / normalisation below.  The
+  // state block of (b, h) is one buffer; row i sits at the uniform offset i * dv * 4.
+  const buf_t sbuf = make_buf(a.state + (static_cast<size_t>(b) * a.H + h) * DK * a.dv,
+                              static_cast<uint32_t>(DK * a.dv * 4));
+  const uint32_t col = static_cast<uint32_t>(tid) * 4, row = static_cast<uint32_t>(a.dv) * 4;
+  float S[DK];
+  if (active) {
+#pragma unroll
+    for (int i = 0; i < DK; ++i)
+      S[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sbuf, col, i * row, 0));
+  }
   const T *pr = static_cast<const T *>(a.proj) + b * a.p_sb;
+  float gt = 0.f, nw = 0.f, xv = 0.f;
+  if (active) {
+    gt = ld(pr + a.g_off + h * a.dv + tid);
+    nw = ld(static_cast<const T *>(a.norm_w) + tid);
+    xv = ld(pr + a.v_off + h * a.dv + tid);
+  }
+  const float av = ld(pr + a.a_off + h), bv = ld(pr + a.b_off + h);
+  const float dtb = ld(static_cast<const T *>(a.dt_bias) + h), alog = ld(static_cast<const T *>(a.a_log) + h);
+
   auto conv = [&](const void *wgt, void *tails, int C, int ch, float xnew) {
     const T *wr = static_cast<const T *>(wgt) + static_cast<size_t>(ch) * K;
     T *tl = static_cast<T *>(tails) + (static_cast<size_t>(b) * C + ch) * (K - 1);
@@ -69,28 +91,18 @@ __global__ void __launch_bounds__(128) gdn_decode_kernel(GdnDecodeArgs a) {
     if (isq) sq[c] = y * (rsqrtf(static_cast<float>(DK)) / nrm);
     else sk[c] = y / nrm;
   }
-  const bool active = tid < a.dv;
   float vcol = 0.f;
-  if (active) {
-    const int ch = h * a.dv + tid;
-    vcol = conv(a.wv, a.tv, a.H * a.dv, ch, ld(pr + a.v_off + ch));
-  }
+  if (active) vcol = conv(a.wv, a.tv, a.H * a.dv, h * a.dv + tid, xv);
   // 3. gates (uniform)
-  const float av = ld(pr + a.a_off + h), bv = ld(pr + a.b_off + h);
   const float beta = 1.f / (1.f + exp_f(-bv));
-  const float xa = av + ld(static_cast<const T *>(a.dt_bias) + h);
+  const float xa = av + dtb;
   const float sp = xa > 20.f ? xa : log1pf(exp_f(xa));  // softplus, threshold 20
-  const float gate_g = -exp_f(ld(static_cast<const T *>(a.a_log) + h)) * sp;
-  const float decay = exp_f(gate_g);
+  const float decay = exp_f(-exp_f(alog) * sp);
   __syncthreads();
 
   // 4. delta rule on column e
   float o = 0.f;
-  const size_t sbase = (static_cast<size_t>(b) * a.H + h) * DK * a.dv;
   if (active) {
-    float S[DK];
-#pragma unroll
-    for (int i = 0; i < DK; ++i) S[i] = a.state[sbase + static_cast<size_t>(i) * a.dv + tid];
     float vold = 0.f;
 #pragma unroll
     for (int i = 0; i < DK; ++i) {
@@ -104,7 +116,8 @@ __global__ void __launch_bounds__(128) gdn_decode_kernel(GdnDecodeArgs a) {
       o = fmaf(sq[i], S[i], o);
     }
 #pragma unroll
-    for (int i = 0; i < DK; ++i) a.state[sbase + static_cast<size_t>(i) * a.dv + tid] = S[i];
+    for (int i = 0; i < DK; ++i)
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, S[i]), sbuf, col, i * row, 0);
   }
 
   // 5. GatedRMSNorm over the head's dv outputs (two waves: partial sums in LDS)
@@ -113,8 +126,7 @@ __global__ void __launch_bounds__(128) gdn_decode_kernel(GdnDecodeArgs a) {
   __syncthreads();
   const float ms = (sred[0] + (blockDim.x > 64 ? sred[1] : 0.f)) / static_cast<float>(a.dv);
   if (active) {
-    const float gt = ld(pr + a.g_off + h * a.dv + tid);
-    const float yv = o * rsqrtf(ms + a.norm_eps) * ld(static_cast<const T *>(a.norm_w) + tid) * silu_fast(gt);
+    const float yv = o * rsqrtf(ms + a.norm_eps) * nw * silu_fast(gt);
     st(static_cast<T *>(a.y) + b * a.y_sb + h * a.dv + tid, yv);
   }
 }

@@ -1,0 +1,248 @@
+// y = x W^T for a few activation rows (M <= 64 per launch row-block): the
+// projections of a decode step (nn.Linear with the weight W [N, K] row-major, bf16,
+// fp32 accumulation), with the elementwise op that follows each of them fused in:
+//   EPI_NONE    y = x W^T
+//   EPI_GATE    y = (x W^T) * sigmoid(aux)          Chord: o_proj(out) * sigmoid(g_proj h)
+//                                                   (motif/block/attention/chord_attn.py:117, :312)
+//   EPI_RESID   y = (x W^T) + aux, y2 = aux2 + y    decoder: f_h = attn + mlp, then the block's
+//                                                   running sum (motif/block/decoder.py:205-210,
+//                                                   motif/model/cache.py:264-266 in this package)
+//   EPI_SWIGLU  y = (x W_a^T) * SiLU(x W_b^T)       SwiGLU MLP (motif/block/mlp.py:42-63 with
+//                                                   motif/ops/swiglu.py:252-253), W = [W_a; W_b]
+// Every intermediate is rounded to bf16 where the reference's separate ops round
+// (GEMM output, sigmoid / SiLU output, product / sum).
+//
+// At M = 64 the weight is the only large operand: N * K * 2 bytes streamed once from
+// HBM.  A workgroup computes an (16 MT) x (16 NT) output tile over the whole of K; its
+// 8 waves split K, and each wave issues the loads of its whole share (up to 8 k-steps
+// of 32) at once, so a launch costs one memory round trip rather than one per k-step.
+// The v_mfma_f32_16x16x32_bf16 partial sums meet in LDS for the epilogue.  What bounds
+// a workgroup is the bytes through its CU, (16 MT + 16 NT) * K * 2, so the host picks
+// the largest tile that still gives about 256 workgroups; the workgroups that share a
+// weight tile are placed on one XCD (workgroups go to XCDs round-robin), so the tile
+// comes from HBM once and from that XCD's L2 after.
+#include "capi_internal.h"
+#include "common.h"
+
+namespace motif {
+
+namespace {
+
+enum { EPI_NONE = 0, EPI_GATE = 1, EPI_RESID = 2, EPI_SWIGLU = 3 };
+
+struct LinArgs {
+  const bf16_t *x; int64_t x_rs;     // [M, K]
+  const bf16_t *w; int64_t w_rs;     // [N, K]
+  bf16_t *y; int64_t y_rs;           // [M, Nout]
+  const bf16_t *aux; int64_t aux_rs; // GATE: gate pre-activation; RESID: residual  [M, Nout]
+  const bf16_t *aux2; int64_t aux2_rs;
+  bf16_t *y2; int64_t y2_rs;         // RESID: y2 = aux2 + y (skipped when y2 is NULL)
+  int M, N, K;                       // N = rows of W (SWIGLU: 2 * Nout)
+  int mblocks, ntiles;               // output tiles along M and along the columns
+};
+
+constexpr int kWaves = 8;
+constexpr int kMaxSteps = 8;  // k-steps (of 32) per wave per round trip
+constexpr int kXcds = 8;
+
+__device__ __forceinline__ f32x4 mma(const bf16x8 &a, const bf16x8 &b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 ld8(buf_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+__device__ __forceinline__ float rb(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+// Output column of W tile t, column c of a workgroup whose first output column is n0.
+// SWIGLU pairs value tile t with gate tile t (W rows nout + ...), so a workgroup of NT
+// W tiles covers 16 NT / 2 output columns there.
+template <int NT, int EPI>
+__device__ __forceinline__ int w_row(int n0, int t, int c, int nout) {
+  if (EPI == EPI_SWIGLU) return (t < NT / 2 ? 0 : nout) + n0 + 16 * (t % (NT / 2)) + c;
+  return n0 + 16 * t + c;
+}
+
+template <int MT, int NT, int KS, int EPI>
+__global__ void __launch_bounds__(512) linear_rows_kernel(LinArgs a) {
+  // The wave index in an SGPR: the k-range below is then wave-uniform to the compiler
+  // (scalar branches, step offsets in the loads' scalar offset operand).
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, kq = lane >> 4;
+  constexpr int kCols = EPI == EPI_SWIGLU ? 8 * NT : 16 * NT;  // output columns per tile
+  const int nout = EPI == EPI_SWIGLU ? a.N / 2 : a.N;
+
+  // XCD-aware tile order: the mblocks workgroups of one column tile sit kXcds ids apart.
+  const int id = blockIdx.x;
+  const int group = id / (kXcds * a.mblocks), r = id % (kXcds * a.mblocks);
+  const int nt = group * kXcds + r % kXcds, mb = r / kXcds;
+  if (nt >= a.ntiles) return;
+  const int n0 = nt * kCols, m0 = mb * 16 * MT;
+  const int rows = min(a.M - m0, 16 * MT);
+
+  // Output row r depends only on x row r and output column c only on W row c, so
+  // tiles past M or N read a clamped (valid) row and their outputs are not stored.
+  const bf16_t *xbase = a.x + static_cast<int64_t>(m0) * a.x_rs;
+  const buf_t xb = make_buf(xbase, static_cast<uint32_t>(((rows - 1) * a.x_rs + a.K) * 2));
+  const buf_t wb = make_buf(a.w, static_cast<uint32_t>(((a.N - 1) * a.w_rs + a.K) * 2));
+  uint32_t xo[MT], wo[NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+    xo[mt] = static_cast<uint32_t>((min(mt * 16 + r16, rows - 1) * a.x_rs + kq * 8) * 2);
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+    wo[t] = static_cast<uint32_t>((min(w_row<NT, EPI>(n0, t, r16, nout), a.N - 1) * a.w_rs + kq * 8) * 2);
+
+  const int nsteps = a.K / 32;
+  const int s0 = wv * nsteps / kWaves, s1 = (wv + 1) * nsteps / kWaves;
+
+  f32x4 acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // KS k-steps per round trip (K > 8 * 8 * 32 loops).  Steps past the wave's range
+  // read at an offset of 2^31 or more, which the range check turns into zeros (every
+  // operand offset is below 2^31), so every MFMA runs unconditionally: a guard around
+  // the MFMAs would let the compiler sink each step's loads into it and pay one
+  // memory round trip per step.
+  for (int s = s0; s < s1; s += KS) {
+    bf16x8 A[KS][MT], B[KS][NT];
+#pragma unroll
+    for (int c = 0; c < KS; ++c) {
+      const uint32_t soff = s + c < s1 ? static_cast<uint32_t>(s + c) * 64u : 0x80000000u;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) A[c][mt] = ld8(xb, xo[mt], soff);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) B[c][t] = ld8(wb, wo[t], soff);
+    }
+    // keep the whole batch of loads ahead of the MFMAs (the scheduler would otherwise
+    // interleave them to save registers, serialising the round trips)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < KS; ++c)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[mt][t] = mma(A[c][mt], B[c][t], acc[mt][t]);
+  }
+
+  // Cross-wave sum in LDS: red[wave][tile][lane] (16 bytes per lane).
+  __shared__ f32x4 red[kWaves][MT * NT][64];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) red[wv][mt * NT + t][lane] = acc[mt][t];
+  __syncthreads();
+
+  // Thread p finishes (row tile mt, value tile tv, lane l): one C tile (two for SWIGLU,
+  // the value tile and its gate tile).
+  constexpr int kOut = EPI == EPI_SWIGLU ? NT / 2 : NT;  // output tiles per row tile
+  const int p = threadIdx.x;
+  if (p >= MT * kOut * 64) return;
+  const int l = p & 63, tv = (p >> 6) % kOut, mt = (p >> 6) / kOut;
+  f32x4 v = red[0][mt * NT + tv][l], g = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (EPI == EPI_SWIGLU) g = red[0][mt * NT + tv + kOut][l];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) {
+    v += red[w][mt * NT + tv][l];
+    if (EPI == EPI_SWIGLU) g += red[w][mt * NT + tv + kOut][l];
+  }
+  const int col = n0 + 16 * tv + (l & 15);
+  if (col >= nout) return;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int rr = mt * 16 + 4 * (l >> 4) + j;
+    if (rr >= rows) continue;
+    const int64_t m = m0 + rr;
+    float val = rb(v[j]);
+    if (EPI == EPI_SWIGLU) {
+      val = val * rb(silu_fast(rb(g[j])));
+    } else if (EPI == EPI_GATE) {
+      const float gp = bf16_to_f32(a.aux[m * a.aux_rs + col]);
+      val = val * rb(rcp_fast(1.f + __builtin_amdgcn_exp2f(-gp * kLog2e)));
+    } else if (EPI == EPI_RESID) {
+      val = rb(val + bf16_to_f32(a.aux[m * a.aux_rs + col]));
+      if (a.y2) a.y2[m * a.y2_rs + col] = f32_to_bf16(bf16_to_f32(a.aux2[m * a.aux2_rs + col]) + val);
+    }
+    a.y[m * a.y_rs + col] = f32_to_bf16(val);
+  }
+}
+
+template <int MT, int NT, int EPI>
+int launch_tile(LinArgs a, hipStream_t s) {
+  constexpr int kCols = EPI == EPI_SWIGLU ? 8 * NT : 16 * NT;
+  const int nout = EPI == EPI_SWIGLU ? a.N / 2 : a.N;
+  a.ntiles = (nout + kCols - 1) / kCols;
+  a.mblocks = (a.M + 16 * MT - 1) / (16 * MT);
+  const int groups = (a.ntiles + kXcds - 1) / kXcds;
+  const dim3 grid(groups * kXcds * a.mblocks), block(64 * kWaves);
+  const int per_wave = (a.K / 32 + kWaves - 1) / kWaves;
+  if (per_wave <= 1) linear_rows_kernel<MT, NT, 1, EPI><<<grid, block, 0, s>>>(a);
+  else if (per_wave <= 2) linear_rows_kernel<MT, NT, 2, EPI><<<grid, block, 0, s>>>(a);
+  else if (per_wave <= 4) linear_rows_kernel<MT, NT, 4, EPI><<<grid, block, 0, s>>>(a);
+  else if (per_wave <= 6) linear_rows_kernel<MT, NT, 6, EPI><<<grid, block, 0, s>>>(a);
+  else linear_rows_kernel<MT, NT, kMaxSteps, EPI><<<grid, block, 0, s>>>(a);
+  return check_launch("linear_rows_kernel");
+}
+
+// Tile choice: rows per tile 16 MT (MT = 4, 2, 1) and W tiles NT (2, or 1 when the
+// epilogue allows it), the largest tile whose grid still has about 256 workgroups.
+template <int EPI>
+int launch_epi(const LinArgs &a, hipStream_t s) {
+  const int nout = EPI == EPI_SWIGLU ? a.N / 2 : a.N;
+  const int cols2 = EPI == EPI_SWIGLU ? 16 : 32;  // output columns of an NT = 2 tile
+  auto wgs = [&](int mt, int cols) { return ((a.M + 16 * mt - 1) / (16 * mt)) * ((nout + cols - 1) / cols); };
+  const int mtmax = a.M > 32 ? 4 : (a.M > 16 ? 2 : 1);
+  if (mtmax >= 4 && wgs(4, cols2) >= 200) return launch_tile<4, 2, EPI>(a, s);
+  if (mtmax >= 2 && wgs(2, cols2) >= 200) return launch_tile<2, 2, EPI>(a, s);
+  if constexpr (EPI == EPI_SWIGLU) {
+    return launch_tile<1, 2, EPI>(a, s);  // a value tile and its gate tile
+  } else {
+    if (wgs(1, cols2) >= 200) return launch_tile<1, 2, EPI>(a, s);
+    return launch_tile<1, 1, EPI>(a, s);
+  }
+}
+
+}  // namespace
+
+}  // namespace motif
+
+extern "C" int motif_linear_rows(const void *x, int64_t x_rs, const void *w, int64_t w_rs, void *y, int64_t y_rs,
+                                 int M, int N, int K, int epilogue, const void *aux, int64_t aux_rs,
+                                 const void *aux2, int64_t aux2_rs, void *y2, int64_t y2_rs, void *stream) {
+  using namespace motif;
+  if (M < 0 || N <= 0 || K <= 0) return set_error(MOTIF_ERR_INVALID, "linear_rows: bad size");
+  if (!x || !w || !y) return set_error(MOTIF_ERR_INVALID, "linear_rows: NULL pointer");
+  if (epilogue < EPI_NONE || epilogue > EPI_SWIGLU) return set_error(MOTIF_ERR_INVALID, "linear_rows: epilogue");
+  if ((epilogue == EPI_GATE || epilogue == EPI_RESID) && !aux)
+    return set_error(MOTIF_ERR_INVALID, "linear_rows: epilogue needs aux");
+  if (epilogue == EPI_RESID && y2 && !aux2) return set_error(MOTIF_ERR_INVALID, "linear_rows: y2 needs aux2");
+  if (epilogue == EPI_SWIGLU && (N & 1)) return set_error(MOTIF_ERR_INVALID, "linear_rows: SwiGLU needs even N");
+  if (K % 32) return set_error(MOTIF_ERR_UNSUPPORTED, "linear_rows: K must be a multiple of 32");
+  if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15) || (x_rs % 8) || (w_rs % 8))
+    return set_error(MOTIF_ERR_UNSUPPORTED, "linear_rows: x / W rows must be 16-byte aligned");
+  if (x_rs < K || w_rs < K) return set_error(MOTIF_ERR_INVALID, "linear_rows: row stride below K");
+  if ((static_cast<int64_t>(N - 1) * w_rs + K) * 2 >= (int64_t(1) << 31) ||
+      (static_cast<int64_t>(63) * x_rs + K) * 2 >= (int64_t(1) << 31))
+    return set_error(MOTIF_ERR_UNSUPPORTED, "linear_rows: operand above 2 GiB");
+  if (M == 0) return MOTIF_OK;
+  LinArgs a;
+  a.x = static_cast<const bf16_t *>(x); a.x_rs = x_rs;
+  a.w = static_cast<const bf16_t *>(w); a.w_rs = w_rs;
+  a.y = static_cast<bf16_t *>(y); a.y_rs = y_rs;
+  a.aux = static_cast<const bf16_t *>(aux); a.aux_rs = aux_rs;
+  a.aux2 = static_cast<const bf16_t *>(aux2); a.aux2_rs = aux2_rs;
+  a.y2 = static_cast<bf16_t *>(y2); a.y2_rs = y2_rs;
+  a.M = M; a.N = N; a.K = K;
+  a.mblocks = a.ntiles = 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (epilogue) {
+    case EPI_GATE: return launch_epi<EPI_GATE>(a, s);
+    case EPI_RESID: return launch_epi<EPI_RESID>(a, s);
+    case EPI_SWIGLU: return launch_epi<EPI_SWIGLU>(a, s);
+    default: return launch_epi<EPI_NONE>(a, s);
+  }
+}

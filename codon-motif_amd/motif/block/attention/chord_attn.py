@@ -16,6 +16,7 @@ import torch.nn as nn
 from motif.block.attention.base import AttentionOutput, BasicAttention
 from motif.model.cache import KVLayerCache, StaticKVLayerCache
 from motif.ops import RMSNorm, apply_chord_attention, apply_chord_attention_varlen
+from motif.ops.linear_rows import cat_weights, linear_rows, project, rows_eligible
 
 _HALF_DTYPES = (torch.float16, torch.bfloat16)
 _GGD_EPS = 1e-5
@@ -114,10 +115,10 @@ class ChordAttention(BasicAttention):
         batch_size, q_len, _ = hidden_states.shape
         kv_len_input = kv_states.shape[1]
 
-        G = torch.sigmoid(self.g_proj(hidden_states))
-        q = self.q_norm(self.reshape_q(self.q_proj(hidden_states), q_len, batch_size))
-        k = self.k_norm(self.reshape_kv(self.k_proj(kv_states), kv_len_input, batch_size))
-        v = self.reshape_kv(self.v_proj(kv_states), kv_len_input, batch_size)
+        xq, xk, xv, xg = self._project(hidden_states, kv_states)
+        q = self.q_norm(self.reshape_q(xq, q_len, batch_size))
+        k = self.k_norm(self.reshape_kv(xk, kv_len_input, batch_size))
+        v = self.reshape_kv(xv, kv_len_input, batch_size)
 
         use_cache = isinstance(past_key_value, KVLayerCache)
         q_start = embedding_start
@@ -139,10 +140,30 @@ class ChordAttention(BasicAttention):
                 (log_n if log_n.dim() == 2 else log_n.expand(batch_size, q_len)).contiguous(),
                 q_start=start, softmax_scale=self.head_dim ** -0.5, eps=_GGD_EPS)
             out = out.transpose(1, 2).reshape(batch_size, q_len, self.hidden_size)
-            return AttentionOutput(output=self.o_proj(out) * G, past_key_value=current_key_value)
+            return AttentionOutput(output=self._gated_output(out, xg), past_key_value=current_key_value)
 
-        return self._eager(q, k, v, G, q_start, q_len, kv_len, batch_size, log_n,
+        return self._eager(q, k, v, torch.sigmoid(xg), q_start, q_len, kv_len, batch_size, log_n,
                            attention_mask, output_attentions, current_key_value)
+
+    def _project(self, hidden_states, kv_states):
+        '''q, k, v and the gate pre-activation g (G = sigmoid(g)).  Self-attention runs the
+        four projections as one GEMM against their concatenated weights (the results are
+        column views of it); cross-attention projects k, v from kv_states.'''
+        if kv_states is hidden_states:
+            w, b = cat_weights(self, '_proj_cat', (self.q_proj, self.k_proj, self.v_proj, self.g_proj))
+            proj = project(hidden_states, w, b)
+            hs, kd = self.hidden_size, self.kv_dim
+            return (proj[..., :hs], proj[..., hs:hs + kd], proj[..., hs + kd:hs + 2 * kd],
+                    proj[..., hs + 2 * kd:])
+        return (self.q_proj(hidden_states), self.k_proj(kv_states), self.v_proj(kv_states),
+                self.g_proj(hidden_states))
+
+    def _gated_output(self, out, g_pre):
+        '''o_proj(out) * sigmoid(g_pre); one decode kernel (gate in the epilogue) for
+        decode-sized bf16 inputs.'''
+        if self.o_proj.bias is None and rows_eligible(out, self.o_proj.weight):
+            return linear_rows(out, self.o_proj.weight, 'gate', aux=g_pre)
+        return self.o_proj(out) * torch.sigmoid(g_pre)
 
     def forward_varlen(self, hidden_states: torch.Tensor, cu_seqlens: torch.Tensor) -> AttentionOutput:
         '''Packed sequences (B == 1): each sequence attends causally within itself
@@ -151,10 +172,10 @@ class ChordAttention(BasicAttention):
         batch_size, T, _ = hidden_states.shape
         if batch_size != 1:
             raise ValueError('forward_varlen expects packed sequences with B == 1')
-        G = torch.sigmoid(self.g_proj(hidden_states))
-        q = self.q_norm(self.reshape_q(self.q_proj(hidden_states), T, 1))
-        k = self.k_norm(self.reshape_kv(self.k_proj(hidden_states), T, 1))
-        v = self.reshape_kv(self.v_proj(hidden_states), T, 1)
+        xq, xk, xv, xg = self._project(hidden_states, hidden_states)
+        q = self.q_norm(self.reshape_q(xq, T, 1))
+        k = self.k_norm(self.reshape_kv(xk, T, 1))
+        v = self.reshape_kv(xv, T, 1)
         cu = cu_seqlens.detach().to('cpu', torch.int64)
         pos = torch.arange(T) - torch.repeat_interleave(cu[:-1], cu[1:] - cu[:-1])
         log_n = torch.log(pos.to(torch.float32) + 1).to(hidden_states.device)[None]
@@ -164,7 +185,7 @@ class ChordAttention(BasicAttention):
             _promote(self.ssmax_s).contiguous(), log_n, cu_seqlens,
             softmax_scale=self.head_dim ** -0.5, eps=_GGD_EPS)
         out = out.transpose(1, 2).reshape(1, T, self.hidden_size)
-        return AttentionOutput(output=self.o_proj(out) * G, payload={'k': k, 'v': v})
+        return AttentionOutput(output=self._gated_output(out, xg), payload={'k': k, 'v': v})
 
     def _eager(self, q, k, v, G, q_start, q_len, kv_len, batch_size, log_n,
                attention_mask, output_attentions, current_key_value):

@@ -28,6 +28,8 @@ from motif.block.attention.base import AttentionOutput, BasicAttention
 from motif.model.cache import GatedDeltaAttentionLayerCache
 from motif.ops import (
     GatedRMSNorm,
+    cat_weights,
+    project,
     HAS_TRITON,
     chunk_gated_delta_rule,
     gdn_decode_fused,
@@ -90,23 +92,9 @@ class GatedDeltaAttention(BasicAttention):
         return GatedDeltaAttentionLayerCache
 
     def _proj_weight(self):
-        '''[q | k | v | gate | a | b] projection weight and bias as one matrix.  Cached
-        (rebuilt when a weight is replaced or updated in place); rebuilt per call while
-        autograd records, so gradients reach the six nn.Linear parameters.'''
-        mods = (self.q_proj, self.k_proj, self.v_proj, self.g_proj, self.a_proj, self.b_proj)
-        params = [m.weight for m in mods] + ([m.bias for m in mods] if self.bias else [])
-        if torch.is_grad_enabled() and any(p.requires_grad for p in params):
-            w = torch.cat([m.weight for m in mods])
-            return w, (torch.cat([m.bias for m in mods]) if self.bias else None)
-        key = tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in params)
-        cached = self.__dict__.get('_proj_cat')
-        if cached is None or cached[0] != key:
-            with torch.no_grad():
-                w = torch.cat([m.weight for m in mods])
-                b = torch.cat([m.bias for m in mods]) if self.bias else None
-            cached = (key, w, b)
-            self.__dict__['_proj_cat'] = cached
-        return cached[1], cached[2]
+        '''[q | k | v | gate | a | b] projection weight and bias as one matrix.'''
+        return cat_weights(self, '_proj_cat', (self.q_proj, self.k_proj, self.v_proj, self.g_proj,
+                                                self.a_proj, self.b_proj))
 
     def _proj_offsets(self):
         '''Column offsets of q, k, v, gate, a, b in the fused projection.'''
@@ -116,7 +104,7 @@ class GatedDeltaAttention(BasicAttention):
     def _project(self, hidden_states):
         '''All six projections -> (q, k, v, gate, a, b) views of one [B, L, ncols] result.'''
         w, b = self._proj_weight()
-        proj = F.linear(hidden_states, w, b)
+        proj = project(hidden_states, w, b)
         offs = self._proj_offsets()
         ends = offs[1:] + (proj.shape[-1],)
         return proj, tuple(proj[..., s:e] for s, e in zip(offs, ends))
@@ -156,7 +144,7 @@ class GatedDeltaAttention(BasicAttention):
         o = o.to(gate.dtype).transpose(1, 2)
         gate = gate.reshape(B, L, self.num_heads, self.dv)
         o = self.o_norm(torch.cat([o, gate], dim=-1)).reshape(B, L, -1)
-        return self.o_proj(o)
+        return project(o, self.o_proj.weight, self.o_proj.bias)
 
     def _decode_fusable(self, hidden_states, cache):
         '''True when one decode step can run as the fused kernel: one token, a cache whose
@@ -192,12 +180,12 @@ class GatedDeltaAttention(BasicAttention):
             cache.conv_state = tuple(torch.zeros(B, c, K - 1, dtype=dt, device=dev)
                                      for c in (H * self.dk, H * self.dk, H * self.dv))
         w, b = self._proj_weight()
-        proj = F.linear(hidden_states.view(B, -1), w, b)
+        proj = project(hidden_states.view(B, -1), w, b)
         y = gdn_decode_fused(proj, self._proj_offsets(), (self.q_conv.weight, self.k_conv.weight, self.v_conv.weight),
                              cache.conv_state, self.A_log, self.dt_bias, self.o_norm.weight, self.o_norm.eps,
                              cache.state, H, self.dk, self.dv)
         cache.update(cache.state, cache.conv_state, steps=1)
-        return self.o_proj(y.view(B, 1, -1))
+        return project(y.view(B, 1, -1), self.o_proj.weight, self.o_proj.bias)
 
     def forward(self, hidden_states: torch.Tensor, past_key_value=None) -> AttentionOutput:
         '''Run the layer over [B, L, hidden]; continue from / update `past_key_value`.'''

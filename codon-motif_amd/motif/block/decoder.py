@@ -82,10 +82,13 @@ class DecoderBlock(nn.Module):
                                         attention_mask=mask, embedding_start=position)
             else:
                 attn_out = decoder.attn(hidden_states=x, past_key_value=cache.attn[i] if use_attn_cache else None)
-            f_h = attn_out.output + decoder.mlp(decoder.mlp_norm(h))
+            prev = attn_res.partial_block
+            f_h, partial = decoder.mlp.forward_residual(
+                decoder.mlp_norm(h), attn_out.output,
+                prev if prev is not None and prev.shape == attn_out.output.shape else None)
             if use_attn_cache:
                 cache.attn[i] = attn_out.past_key_value
-            attn_res.update_increment(f_h)
+            attn_res.update_increment(f_h, partial)
 
         block_repr = attn_res.partial_block
         if block_repr is None:

@@ -4,6 +4,7 @@ up to a multiple of 128.'''
 import torch.nn as nn
 
 from motif.ops import SwiGLU as SwiGLUOp
+from motif.ops.linear_rows import linear_rows, rows_eligible
 
 
 class SwiGLU(nn.Module):
@@ -18,5 +19,26 @@ class SwiGLU(nn.Module):
         self.down_proj = nn.Linear(hidden_features, out_features, bias=bias)
         self.act = SwiGLUOp(dim=-1)
 
+    def _fused(self, x):
+        '''Decode-sized bf16 input: SwiGLU fused into the gate/up projection kernel.'''
+        return (self.gate_up_proj.bias is None and self.down_proj.bias is None
+                and rows_eligible(x, self.gate_up_proj.weight) and x.shape[-1] == self.gate_up_proj.in_features)
+
     def forward(self, x):
+        if self._fused(x):
+            return linear_rows(linear_rows(x, self.gate_up_proj.weight, 'swiglu'), self.down_proj.weight)
         return self.down_proj(self.act(self.gate_up_proj(x)))
+
+    def forward_residual(self, x, residual, partial=None):
+        '''(f, p) with f = residual + forward(x) and p = partial + f (None when `partial`
+        is None).  For decode-sized inputs both adds run in the down projection's
+        epilogue; otherwise p is None and the caller folds f itself.'''
+        if (self._fused(x) and residual.dtype == x.dtype and residual.shape[:-1] == x.shape[:-1]
+                and residual.stride(-1) == 1
+                and (partial is None or (partial.shape == residual.shape and partial.dtype == x.dtype
+                                         and partial.stride(-1) == 1))):
+            h = linear_rows(x, self.gate_up_proj.weight, 'swiglu')
+            if partial is None:
+                return linear_rows(h, self.down_proj.weight, 'resid', aux=residual), None
+            return linear_rows(h, self.down_proj.weight, 'resid', aux=residual, aux2=partial)
+        return residual + self.forward(x), None

@@ -261,9 +261,15 @@ class AttnResCache:
         self.blocks = [hidden_states]
         self.chunk_len = q_len
 
-    def update_increment(self, f_h: torch.Tensor):
+    def update_increment(self, f_h: torch.Tensor, partial: Optional[torch.Tensor] = None):
+        '''Append one decoder's increment and fold it into the running block sum.
+        `partial` (optional, new): that sum already computed by the caller (the decode
+        projection kernel folds it in its epilogue); it must equal partial_block + f_h.'''
         self.blocks.append(f_h)
-        self.partial_block = f_h if self.partial_block is None else self._cat_or_add(self.partial_block, f_h)
+        if partial is not None:
+            self.partial_block = partial
+        else:
+            self.partial_block = f_h if self.partial_block is None else self._cat_or_add(self.partial_block, f_h)
         self.seq_len = max(self.seq_len, f_h.shape[1])
 
     def reset(self):

@@ -17,6 +17,7 @@ from .gated_deltanet import (
 from .short_conv import short_conv_silu, short_conv_silu_varlen
 from .attn_res import apply_block_attn_res, attn_res_read
 from .gdn_decode import gdn_decode_fused
+from .linear_rows import cat_weights, linear_rows, project, rows_eligible
 
 HAS_TRITON = _lib.available()
 HAS_HIP = HAS_TRITON
@@ -28,5 +29,6 @@ __all__ = [
     'chunk_gated_delta_rule_triton', 'chunk_gated_delta_rule_varlen',
     'short_conv_silu', 'short_conv_silu_varlen',
     'apply_block_attn_res', 'attn_res_read', 'gdn_decode_fused',
+    'cat_weights', 'linear_rows', 'project', 'rows_eligible',
     'HAS_TRITON', 'HAS_HIP',
 ]

@@ -199,6 +199,26 @@ int motif_attn_res_read(const void *const *sources, const int64_t *src_sb, const
                         int nsrc, const void *query, const void *norm_weight, float eps, void *out,
                         int64_t out_sb, int64_t out_st, int B, int T, int D, int dtype, void *stream);
 
+/*
+ * y = x W^T for a few activation rows (the projections of a decode step), bf16 with
+ * fp32 accumulation, with the elementwise op that follows the projection fused in.
+ * Replaces nn.Linear (cuBLAS / hipBLASLt) at decode sizes plus, per epilogue:
+ *   0 none
+ *   1 gate    y = (x W^T) * sigmoid(aux)      motif/block/attention/chord_attn.py:254, :313
+ *   2 resid   y = (x W^T) + aux; y2 = aux2 + y (when y2 != NULL)
+ *                                             motif/block/decoder.py:208 (f_h = attn + mlp),
+ *                                             motif/model/cache.py:514-526 (partial block fold)
+ *   3 swiglu  y = (x W[:N/2]^T) * SiLU(x W[N/2:]^T)
+ *                                             motif/block/mlp.py:53-63, motif/ops/swiglu.py:252-253
+ * Intermediates are rounded to bf16 where the reference's separate ops round.
+ *   x [M, K] (row stride x_rs), W [N, K] (row stride w_rs), y / aux / aux2 / y2
+ *   [M, Nout] with their row strides; Nout = N (N/2 for swiglu).  K a multiple of 32;
+ *   x and W rows 16-byte aligned; any M.
+ */
+int motif_linear_rows(const void *x, int64_t x_rs, const void *w, int64_t w_rs, void *y, int64_t y_rs,
+                      int M, int N, int K, int epilogue, const void *aux, int64_t aux_rs,
+                      const void *aux2, int64_t aux2_rs, void *y2, int64_t y2_rs, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
