@@ -21,18 +21,25 @@ struct AttnResArgs {
   const void *src[kMaxSrc];
   int64_t sb[kMaxSrc], st[kMaxSrc];
   const void *query, *weight;
-  void *out;
+  void *out;                 // h (may be NULL when the norms are requested)
   int64_t ob, ot;
   int nsrc, B, T, D;
   float eps;
+  // optional RMSNorms of h (the decoder's attn_norm / mlp_norm): nout[i] =
+  // RMSNorm(h; nw[i], neps) for i < nnorm
+  int nnorm;
+  const void *nw[2];
+  void *nout[2];
+  int64_t nb[2], nt[2];
+  float neps;
 };
 
 // 16-byte piece <-> 8 (bf16) or 4 (fp32) floats
 template <typename T> struct Piece;
 template <> struct Piece<bf16_t> {
   static constexpr int N = 8;
-  __device__ static void load(const bf16_t *p, float *x) {
-    const uint4 u = *reinterpret_cast<const uint4 *>(p);
+  __device__ static void load(const bf16_t *p, float *x) { unpack(*reinterpret_cast<const uint4 *>(p), x); }
+  __device__ static void unpack(const uint4 u, float *x) {
     const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -50,14 +57,19 @@ template <> struct Piece<bf16_t> {
 };
 template <> struct Piece<float> {
   static constexpr int N = 4;
-  __device__ static void load(const float *p, float *x) {
-    const float4 u = *reinterpret_cast<const float4 *>(p);
-    x[0] = u.x; x[1] = u.y; x[2] = u.z; x[3] = u.w;
+  __device__ static void load(const float *p, float *x) { unpack(*reinterpret_cast<const uint4 *>(p), x); }
+  __device__ static void unpack(const uint4 u, float *x) {
+    x[0] = __uint_as_float(u.x); x[1] = __uint_as_float(u.y);
+    x[2] = __uint_as_float(u.z); x[3] = __uint_as_float(u.w);
   }
   __device__ static void store(float *p, const float *x) {
     *reinterpret_cast<float4 *>(p) = float4{x[0], x[1], x[2], x[3]};
   }
 };
+
+template <typename T> __device__ __forceinline__ float round_to(float v);
+template <> __device__ __forceinline__ float round_to<float>(float v) { return v; }
+template <> __device__ __forceinline__ float round_to<bf16_t>(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
 // PPL: 16-byte pieces per lane (D <= 64 * PPL * Piece::N).
 template <typename T, int PPL>
@@ -69,45 +81,43 @@ __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
   const int b = tok / a.T, t = tok - b * a.T;
   const int np = a.D / E;
 
+  const uint32_t dbytes = static_cast<uint32_t>(a.D * sizeof(T));
+  const buf_t qb = make_buf(a.query, dbytes), wb = make_buf(a.weight, dbytes);
   float qw[PPL][E];
 #pragma unroll
   for (int i = 0; i < PPL; ++i) {
-    const int p = lane + 64 * i;
     float qv[E], wv[E];
-    if (p < np) {
-      Piece<T>::load(static_cast<const T *>(a.query) + p * E, qv);
-      Piece<T>::load(static_cast<const T *>(a.weight) + p * E, wv);
-    } else {
-#pragma unroll
-      for (int e = 0; e < E; ++e) qv[e] = wv[e] = 0.f;
-    }
+    Piece<T>::unpack(buf_ld16(qb, (lane + 64 * i) * 16), qv);
+    Piece<T>::unpack(buf_ld16(wb, (lane + 64 * i) * 16), wv);
 #pragma unroll
     for (int e = 0; e < E; ++e) qw[i][e] = qv[e] * wv[e];
   }
 
+  // every source row is loaded before any reduction, so the loads overlap
   float x[kMaxSrc][PPL][E];
+#pragma unroll
+  for (int n = 0; n < kMaxSrc; ++n) {
+    if (n >= a.nsrc) break;
+    // range-checked buffer over the row: pieces past D read as zeros, no branch
+    const buf_t row = make_buf(static_cast<const T *>(a.src[n]) + b * a.sb[n] + int64_t(t) * a.st[n],
+                               dbytes);
+#pragma unroll
+    for (int i = 0; i < PPL; ++i) Piece<T>::unpack(buf_ld16(row, (lane + 64 * i) * 16), x[n][i]);
+  }
   float logit[kMaxSrc];
   float mx = -INFINITY;
 #pragma unroll
   for (int n = 0; n < kMaxSrc; ++n) {
     logit[n] = -INFINITY;
     if (n < a.nsrc) {
-      const T *row = static_cast<const T *>(a.src[n]) + b * a.sb[n] + int64_t(t) * a.st[n];
       float ss = 0.f, dot = 0.f;
 #pragma unroll
-      for (int i = 0; i < PPL; ++i) {
-        const int p = lane + 64 * i;
-        if (p < np) Piece<T>::load(row + p * E, x[n][i]);
-        else {
-#pragma unroll
-          for (int e = 0; e < E; ++e) x[n][i][e] = 0.f;
-        }
+      for (int i = 0; i < PPL; ++i)
 #pragma unroll
         for (int e = 0; e < E; ++e) {
           ss = fmaf(x[n][i][e], x[n][i][e], ss);
           dot = fmaf(x[n][i][e], qw[i][e], dot);
         }
-      }
       ss = wave_sum(ss);
       dot = wave_sum(dot);
       logit[n] = dot * rsqrtf(ss / a.D + a.eps);
@@ -121,21 +131,54 @@ __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
     den += alpha[n];
   }
   const float inv = 1.f / den;
-  T *orow = static_cast<T *>(a.out) + b * a.ob + int64_t(t) * a.ot;
+  float h[PPL][E];
 #pragma unroll
   for (int i = 0; i < PPL; ++i) {
     const int p = lane + 64 * i;
-    if (p >= np) continue;
-    float h[E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) h[e] = 0.f;
+    for (int e = 0; e < E; ++e) h[i][e] = 0.f;
+    if (p >= np) continue;
 #pragma unroll
     for (int n = 0; n < kMaxSrc; ++n)
       if (n < a.nsrc) {
 #pragma unroll
-        for (int e = 0; e < E; ++e) h[e] = fmaf(alpha[n] * inv, x[n][i][e], h[e]);
+        for (int e = 0; e < E; ++e) h[i][e] = fmaf(alpha[n] * inv, x[n][i][e], h[i][e]);
       }
-    Piece<T>::store(orow + p * E, h);
+  }
+  if (a.out) {
+    T *orow = static_cast<T *>(a.out) + b * a.ob + int64_t(t) * a.ot;
+#pragma unroll
+    for (int i = 0; i < PPL; ++i) {
+      const int p = lane + 64 * i;
+      if (p < np) Piece<T>::store(orow + p * E, h[i]);
+    }
+  }
+  if (a.nnorm == 0) return;
+  // RMSNorm of h as the reference computes it on the stored h (rms_norm.py:481-486):
+  // y = T(h * rsqrt(mean(h^2) + eps)) * weight, the product rounded to T.
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < PPL; ++i)
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      h[i][e] = round_to<T>(h[i][e]);
+      ss = fmaf(h[i][e], h[i][e], ss);
+    }
+  const float r = rsqrtf(wave_sum(ss) / a.D + a.neps);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    if (k >= a.nnorm) break;
+    T *nrow = static_cast<T *>(a.nout[k]) + b * a.nb[k] + int64_t(t) * a.nt[k];
+#pragma unroll
+    for (int i = 0; i < PPL; ++i) {
+      const int p = lane + 64 * i;
+      if (p >= np) continue;
+      float w[E], y[E];
+      Piece<T>::unpack(buf_ld16(make_buf(a.nw[k], dbytes), p * 16), w);
+#pragma unroll
+      for (int e = 0; e < E; ++e) y[e] = round_to<T>(h[i][e] * r) * w[e];
+      Piece<T>::store(nrow + p * E, y);
+    }
   }
 }
 
@@ -155,13 +198,16 @@ int launch(const AttnResArgs &a, hipStream_t s) {
 
 }  // namespace motif
 
-extern "C" int motif_attn_res_read(const void *const *sources, const int64_t *src_sb, const int64_t *src_st,
-                                   int nsrc, const void *query, const void *norm_weight, float eps, void *out,
-                                   int64_t out_sb, int64_t out_st, int B, int T, int D, int dtype, void *stream) {
-  using namespace motif;
+namespace motif {
+namespace {
+
+int attn_res_entry(const void *const *sources, const int64_t *src_sb, const int64_t *src_st, int nsrc,
+                   const void *query, const void *norm_weight, float eps, void *out, int64_t out_sb,
+                   int64_t out_st, int nnorm, const void *const *nw, void *const *nout, const int64_t *nsb,
+                   const int64_t *nst, float neps, int B, int T, int D, int dtype, void *stream) {
   if (nsrc < 1 || nsrc > kMaxSrc)
     return set_error(MOTIF_ERR_UNSUPPORTED, "attn_res_read: 1 to 8 sources");
-  if (B < 0 || T < 0 || D <= 0 || !sources || !src_sb || !src_st || !query || !norm_weight || !out)
+  if (B < 0 || T < 0 || D <= 0 || !sources || !src_sb || !src_st || !query || !norm_weight || (!out && nnorm == 0))
     return set_error(MOTIF_ERR_INVALID, "attn_res_read: bad argument");
   if (dtype != MOTIF_F32 && dtype != MOTIF_BF16) return set_error(MOTIF_ERR_UNSUPPORTED, "attn_res_read: dtype");
   const int esz = dtype == MOTIF_BF16 ? 2 : 4, vec = 16 / esz;
@@ -169,7 +215,7 @@ extern "C" int motif_attn_res_read(const void *const *sources, const int64_t *sr
   AttnResArgs a{};
   uintptr_t align = reinterpret_cast<uintptr_t>(query) | reinterpret_cast<uintptr_t>(norm_weight) |
                     reinterpret_cast<uintptr_t>(out);
-  int64_t strides = out_sb | out_st;
+  int64_t strides = out ? (out_sb | out_st) : 0;
   for (int n = 0; n < nsrc; ++n) {
     if (!sources[n]) return set_error(MOTIF_ERR_INVALID, "attn_res_read: NULL source");
     a.src[n] = sources[n];
@@ -177,6 +223,15 @@ extern "C" int motif_attn_res_read(const void *const *sources, const int64_t *sr
     a.st[n] = src_st[n];
     align |= reinterpret_cast<uintptr_t>(sources[n]);
     strides |= src_sb[n] | src_st[n];
+  }
+  for (int k = 0; k < nnorm; ++k) {
+    if (!nw[k] || !nout[k]) return set_error(MOTIF_ERR_INVALID, "attn_res_read: NULL norm operand");
+    a.nw[k] = nw[k];
+    a.nout[k] = nout[k];
+    a.nb[k] = nsb[k];
+    a.nt[k] = nst[k];
+    align |= reinterpret_cast<uintptr_t>(nw[k]) | reinterpret_cast<uintptr_t>(nout[k]);
+    strides |= nsb[k] | nst[k];
   }
   if ((align & 15) || (strides % vec))
     return set_error(MOTIF_ERR_UNSUPPORTED, "attn_res_read: rows must be 16-byte aligned");
@@ -191,6 +246,29 @@ extern "C" int motif_attn_res_read(const void *const *sources, const int64_t *sr
   a.T = T;
   a.D = D;
   a.eps = eps;
+  a.nnorm = nnorm;
+  a.neps = neps;
   hipStream_t s = static_cast<hipStream_t>(stream);
   return dtype == MOTIF_BF16 ? launch<bf16_t>(a, s) : launch<float>(a, s);
+}
+
+}  // namespace
+}  // namespace motif
+
+extern "C" int motif_attn_res_read(const void *const *sources, const int64_t *src_sb, const int64_t *src_st,
+                                   int nsrc, const void *query, const void *norm_weight, float eps, void *out,
+                                   int64_t out_sb, int64_t out_st, int B, int T, int D, int dtype, void *stream) {
+  return motif::attn_res_entry(sources, src_sb, src_st, nsrc, query, norm_weight, eps, out, out_sb, out_st, 0,
+                               nullptr, nullptr, nullptr, nullptr, 0.f, B, T, D, dtype, stream);
+}
+
+extern "C" int motif_attn_res_read_norms(const void *const *sources, const int64_t *src_sb,
+                                         const int64_t *src_st, int nsrc, const void *query,
+                                         const void *norm_weight, float eps, void *out, int64_t out_sb,
+                                         int64_t out_st, int nnorm, const void *const *norm_weights,
+                                         void *const *norm_outs, const int64_t *norm_sb, const int64_t *norm_st,
+                                         float norm_eps, int B, int T, int D, int dtype, void *stream) {
+  if (nnorm < 0 || nnorm > 2) return motif::set_error(MOTIF_ERR_INVALID, "attn_res_read: 0 to 2 norms");
+  return motif::attn_res_entry(sources, src_sb, src_st, nsrc, query, norm_weight, eps, out, out_sb, out_st, nnorm,
+                               norm_weights, norm_outs, norm_sb, norm_st, norm_eps, B, T, D, dtype, stream);
 }

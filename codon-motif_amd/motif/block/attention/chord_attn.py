@@ -16,6 +16,7 @@ import torch.nn as nn
 from motif.block.attention.base import AttentionOutput, BasicAttention
 from motif.model.cache import KVLayerCache, StaticKVLayerCache
 from motif.ops import RMSNorm, apply_chord_attention, apply_chord_attention_varlen
+from motif.ops import _lib
 from motif.ops.linear_rows import cat_weights, linear_rows, project, rows_eligible
 
 _HALF_DTYPES = (torch.float16, torch.bfloat16)
@@ -114,6 +115,9 @@ class ChordAttention(BasicAttention):
             kv_states = hidden_states
         batch_size, q_len, _ = hidden_states.shape
         kv_len_input = kv_states.shape[1]
+        if (kv_states is hidden_states and attention_mask is None and not output_attentions
+                and self._static_fusable(hidden_states, past_key_value)):
+            return self._forward_static(hidden_states, past_key_value, embedding_start, section_log_len)
 
         xq, xk, xv, xg = self._project(hidden_states, kv_states)
         q = self.q_norm(self.reshape_q(xq, q_len, batch_size))
@@ -132,18 +136,85 @@ class ChordAttention(BasicAttention):
         log_n = self._log_n(q_start, q_len, batch_size, hidden_states.device, section_log_len)
 
         if attention_mask is None and not output_attentions:
-            alpha, beta, mu = self._ggd_parameters()
+            alpha, beta, mu, ssmax = self._ggd_cached()
             start = int(q_start.reshape(-1)[0]) if isinstance(q_start, torch.Tensor) else int(q_start)
             out = apply_chord_attention(
-                q, k, v, alpha.contiguous(), beta.contiguous(), mu.contiguous(),
-                _promote(self.ssmax_s).contiguous(),
-                (log_n if log_n.dim() == 2 else log_n.expand(batch_size, q_len)).contiguous(),
+                q, k, v, alpha, beta, mu, ssmax,
+                log_n if log_n.dim() == 2 else log_n.expand(batch_size, q_len),
                 q_start=start, softmax_scale=self.head_dim ** -0.5, eps=_GGD_EPS)
             out = out.transpose(1, 2).reshape(batch_size, q_len, self.hidden_size)
             return AttentionOutput(output=self._gated_output(out, xg), past_key_value=current_key_value)
 
         return self._eager(q, k, v, torch.sigmoid(xg), q_start, q_len, kv_len, batch_size, log_n,
                            attention_mask, output_attentions, current_key_value)
+
+    def _ggd_cached(self):
+        '''(alpha, beta, mu, ssmax) as contiguous fp32, cached until a parameter changes.'''
+        params = (self.theta_alpha, self.theta_beta, self.theta_mu, self.ssmax_s)
+        if torch.is_grad_enabled() and any(p.requires_grad for p in params):
+            alpha, beta, mu = self._ggd_parameters()
+            return tuple(t.contiguous() for t in (alpha, beta, mu, _promote(self.ssmax_s)))
+        key = tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in params)
+        cached = self.__dict__.get('_ggd_cat')
+        if cached is None or cached[0] != key:
+            with torch.no_grad():
+                alpha, beta, mu = self._ggd_parameters()
+                vals = tuple(t.contiguous() for t in (alpha, beta, mu, _promote(self.ssmax_s)))
+            cached = (key, vals)
+            self.__dict__['_ggd_cat'] = cached
+        return cached[1]
+
+    def _static_fusable(self, x, cache):
+        '''Inference into a preallocated KV cache with the fused input kernel.'''
+        if not isinstance(cache, StaticKVLayerCache) or cache.k is None or not x.is_cuda:
+            return False
+        if x.dtype not in (torch.bfloat16, torch.float32) or cache.k.dtype != x.dtype:
+            return False
+        if (self.head_dim * x.element_size()) % 16 or self.head_dim * x.element_size() > 512:
+            return False
+        if self.q_norm.weight is None or self.k_norm.weight is None or self.q_norm.eps != self.k_norm.eps:
+            return False
+        if torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()):
+            return False
+        return cache.length + x.shape[1] <= cache.capacity
+
+    def _forward_static(self, hidden_states, cache, embedding_start, section_log_len):
+        '''Projection GEMM, then one kernel for the q / k RMSNorms and the cache append
+        (motif_chord_qkv_prep), the Chord kernel over the cache prefix and the gated
+        o_proj -- the same results as the general path.'''
+        B, L, _ = hidden_states.shape
+        H, Hkv, D, hs, kd = self.num_heads, self.num_kv_heads, self.head_dim, self.hidden_size, self.kv_dim
+        w, b = cat_weights(self, '_proj_cat', (self.q_proj, self.k_proj, self.v_proj, self.g_proj))
+        proj = project(hidden_states, w, b)
+        if proj.stride(-1) != 1:
+            proj = proj.contiguous()
+        q_start = embedding_start
+        if isinstance(q_start, int) and q_start == 0 and cache.length > 0:
+            q_start = cache.length
+        pos = cache.reserve(L)
+        q = torch.empty(B, H, L, D, dtype=hidden_states.dtype, device=hidden_states.device)
+        dt = hidden_states.dtype
+        qw = self.q_norm.weight.to(dt).contiguous()
+        kw = self.k_norm.weight.to(dt).contiguous()
+        kc, vc = cache.k, cache.v
+        rc = _lib.lib().motif_chord_qkv_prep(
+            proj.data_ptr(), proj.stride(0), proj.stride(1), 0, hs, hs + kd,
+            qw.data_ptr(), kw.data_ptr(), float(self.q_norm.eps),
+            q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
+            kc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2),
+            vc.data_ptr(), vc.stride(0), vc.stride(1), vc.stride(2),
+            _lib.ptr(cache.length_dev), pos, B, L, H, Hkv, D, _lib.dtype_code(dt),
+            _lib.stream_ptr(hidden_states.device))
+        _lib.check(rc, 'motif_chord_qkv_prep')
+        k, v = kc[:, :, :cache.length], vc[:, :, :cache.length]
+        log_n = self._log_n(q_start, L, B, hidden_states.device, section_log_len)
+        alpha, beta, mu, ssmax = self._ggd_cached()
+        start = int(q_start.reshape(-1)[0]) if isinstance(q_start, torch.Tensor) else int(q_start)
+        out = apply_chord_attention(q, k, v, alpha, beta, mu, ssmax,
+                                    log_n if log_n.dim() == 2 else log_n.expand(B, L),
+                                    q_start=start, softmax_scale=D ** -0.5, eps=_GGD_EPS)
+        out = out.transpose(1, 2).reshape(B, L, hs)
+        return AttentionOutput(output=self._gated_output(out, proj[..., hs + 2 * kd:]), past_key_value=cache)
 
     def _project(self, hidden_states, kv_states):
         '''q, k, v and the gate pre-activation g (G = sigmoid(g)).  Self-attention runs the

@@ -12,7 +12,7 @@ from motif.block.mlp import SwiGLU
 from motif.model.cache import DecoderBlockCache, GatedDeltaAttentionLayerCache, KVLayerCache
 from motif.model.config import MotifChordConfig
 from motif.ops import RMSNorm
-from motif.ops.attn_res import apply_block_attn_res
+from motif.ops.attn_res import apply_block_attn_res, attn_res_read_norms
 
 
 @dataclass
@@ -52,6 +52,20 @@ class DecoderBlock(nn.Module):
         self.pseudo_queries = nn.ParameterList([nn.Parameter(torch.zeros(config.model_dim)) for _ in self.features])
         self.attn_res_norms = nn.ModuleList([RMSNorm(config.model_dim) for _ in self.features])
 
+    def _read(self, attn_res, i, decoder):
+        '''(attn_norm(h), mlp_norm(h)) for h, the attention-residual read of decoder i.
+        ROCm tensors: one kernel (read and both norms, h never stored).'''
+        sources = attn_res.aligned_values()
+        an, mn = decoder.attn_norm, decoder.mlp_norm
+        x0 = sources[0]
+        if (x0.is_cuda and len(sources) <= 8 and an.weight is not None and mn.weight is not None
+                and x0.shape[-1] * x0.element_size() <= 4096 and (x0.shape[-1] * x0.element_size()) % 16 == 0
+                and an.eps == mn.eps and sources[0].dtype in (torch.bfloat16, torch.float32)
+                and not (torch.is_grad_enabled() and any(s.requires_grad for s in sources))):
+            return attn_res_read_norms(sources, self.pseudo_queries[i], self.attn_res_norms[i], an, mn)
+        h = apply_block_attn_res(attn_res, self.pseudo_queries[i], self.attn_res_norms[i])
+        return an(h), mn(h)
+
     def forward(self, hidden_states: torch.Tensor, cache: Optional[DecoderBlockCache] = None,
                 mask: Optional[torch.Tensor] = None, position: Union[int, torch.Tensor] = 0,
                 cu_seqlens: Optional[torch.Tensor] = None) -> DecoderBlockOutput:
@@ -73,8 +87,7 @@ class DecoderBlock(nn.Module):
         use_attn_cache = cu_seqlens is None and len(cache.attn) == len(self.features)
 
         for i, decoder in enumerate(self.features):
-            h = apply_block_attn_res(attn_res, self.pseudo_queries[i], self.attn_res_norms[i])
-            x = decoder.attn_norm(h)
+            x, m = self._read(attn_res, i, decoder)
             if cu_seqlens is not None:
                 attn_out = decoder.attn.forward_varlen(x, cu_seqlens)
             elif isinstance(decoder.attn, ChordAttention):
@@ -84,7 +97,7 @@ class DecoderBlock(nn.Module):
                 attn_out = decoder.attn(hidden_states=x, past_key_value=cache.attn[i] if use_attn_cache else None)
             prev = attn_res.partial_block
             f_h, partial = decoder.mlp.forward_residual(
-                decoder.mlp_norm(h), attn_out.output,
+                m, attn_out.output,
                 prev if prev is not None and prev.shape == attn_out.output.shape else None)
             if use_attn_cache:
                 cache.attn[i] = attn_out.past_key_value

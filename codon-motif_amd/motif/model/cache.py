@@ -177,6 +177,17 @@ class StaticKVLayerCache(KVLayerCache):
         self.length_dev.fill_(self.length)
         return self.k[:, :, :self.length], self.v[:, :, :self.length]
 
+    def reserve(self, n: int) -> int:
+        '''Claim the next n positions for a caller that writes them itself (the fused
+        Chord input kernel, which also sets length_dev); returns the first position.'''
+        if self.k is None:
+            raise RuntimeError('StaticKVLayerCache.reserve before allocate()')
+        if self.length + n > self.capacity:
+            raise RuntimeError(f'StaticKVLayerCache capacity {self.capacity} exceeded ({self.length} + {n})')
+        pos = self.length
+        self.length += n
+        return pos
+
     def reset(self):
         self.length = 0
         if self.length_dev is not None:

@@ -15,7 +15,7 @@ from .gated_deltanet import (
     chunk_gated_delta_rule_varlen,
 )
 from .short_conv import short_conv_silu, short_conv_silu_varlen
-from .attn_res import apply_block_attn_res, attn_res_read
+from .attn_res import apply_block_attn_res, attn_res_read, attn_res_read_norms
 from .gdn_decode import gdn_decode_fused
 from .linear_rows import cat_weights, linear_rows, project, rows_eligible
 
@@ -28,7 +28,7 @@ __all__ = [
     'recurrent_gated_delta_rule', 'chunk_gated_delta_rule',
     'chunk_gated_delta_rule_triton', 'chunk_gated_delta_rule_varlen',
     'short_conv_silu', 'short_conv_silu_varlen',
-    'apply_block_attn_res', 'attn_res_read', 'gdn_decode_fused',
+    'apply_block_attn_res', 'attn_res_read', 'attn_res_read_norms', 'gdn_decode_fused',
     'cat_weights', 'linear_rows', 'project', 'rows_eligible',
     'HAS_TRITON', 'HAS_HIP',
 ]

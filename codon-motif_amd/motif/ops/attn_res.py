@@ -58,6 +58,47 @@ def attn_res_read(sources, query, norm):
     return out
 
 
+def attn_res_read_norms(sources, query, norm, norm_a, norm_b):
+    '''(norm_a(h), norm_b(h)) for h = attn_res_read(sources, query, norm), in one HIP
+    kernel that never writes h: the decoder's attn_norm / mlp_norm inputs.  RMSNorm
+    as the reference computes it on the stored h: T(h * rsqrt(mean(h^2) + eps)) * w.
+    Needs ROCm tensors, both norms with weights and one eps.'''
+    sources = list(sources)
+    x0 = sources[0]
+    if len(sources) > MAX_SRC:
+        raise NotImplementedError(f'attn_res_read_norms: at most {MAX_SRC} sources, got {len(sources)}')
+    B, T, D = x0.shape
+    dt = x0.dtype
+    if dt not in (torch.bfloat16, torch.float32):
+        raise NotImplementedError(f'attn_res_read_norms: dtype {dt}')
+    if norm_a.weight is None or norm_b.weight is None or norm_a.eps != norm_b.eps:
+        raise NotImplementedError('attn_res_read_norms: needs weighted norms with one eps')
+    srcs = [s if s.stride(-1) == 1 else s.contiguous() for s in sources]
+    for s in srcs:
+        if s.shape != x0.shape or s.dtype != dt:
+            raise ValueError('attn_res_read_norms: sources must share shape and dtype')
+    dev = x0.device
+    weight = norm.weight if norm.weight is not None else torch.ones(D, dtype=dt, device=dev)
+    q = query.to(dt).contiguous()
+    w = weight.to(dt).contiguous()
+    wa, wb = norm_a.weight.to(dt).contiguous(), norm_b.weight.to(dt).contiguous()
+    ya = torch.empty(B, T, D, dtype=dt, device=dev)
+    yb = torch.empty(B, T, D, dtype=dt, device=dev)
+    n = len(srcs)
+    ptrs = (ctypes.c_void_p * n)(*[s.data_ptr() for s in srcs])
+    sb = (ctypes.c_int64 * n)(*[s.stride(0) for s in srcs])
+    st = (ctypes.c_int64 * n)(*[s.stride(1) for s in srcs])
+    nw = (ctypes.c_void_p * 2)(wa.data_ptr(), wb.data_ptr())
+    no = (ctypes.c_void_p * 2)(ya.data_ptr(), yb.data_ptr())
+    nsb = (ctypes.c_int64 * 2)(ya.stride(0), yb.stride(0))
+    nst = (ctypes.c_int64 * 2)(ya.stride(1), yb.stride(1))
+    rc = _lib.lib().motif_attn_res_read_norms(ptrs, sb, st, n, q.data_ptr(), w.data_ptr(), float(norm.eps),
+                                              None, 0, 0, 2, nw, no, nsb, nst, float(norm_a.eps),
+                                              B, T, D, _lib.dtype_code(dt), _lib.stream_ptr(dev))
+    _lib.check(rc, 'attn_res_read_norms')
+    return ya, yb
+
+
 def apply_block_attn_res(cache, query, norm):
     sources = cache.aligned_values()
     if len(sources) == 1:

@@ -185,6 +185,26 @@ int motif_gdn_decode_fused(
     float *state, void *y, int64_t y_sb, int B, int H, int dk, int dv, int K, int dtype, void *stream);
 
 /*
+ * ChordAttention input stage for a preallocated KV cache: from the fused q | k | v
+ * projection rows proj [B, L, ncols] (strides p_sb, p_st; head h of q at column
+ * q_off + h*D, of k at k_off + g*D, of v at v_off + g*D), per head
+ *   q[b, h, t]               = RMSNorm(q_h; q_norm_weight)
+ *   k_cache[b, g, pos + t]   = RMSNorm(k_g; k_norm_weight)
+ *   v_cache[b, g, pos + t]   = v_g
+ * RMSNorm as motif/ops/rms_norm.py:481-486 (T(x * rsqrt(mean(x^2) + eps)) * w).
+ * Replaces motif/block/attention/chord_attn.py:255-265 and the KV append
+ * (motif/model/cache.py:170-215).  length_dev (optional) is set to pos + L.
+ * All row starts 16-byte aligned; D * sizeof(T) in {64, 128, 256, 512} bytes.
+ */
+int motif_chord_qkv_prep(const void *proj, int64_t p_sb, int64_t p_st, int q_off, int k_off, int v_off,
+                         const void *q_norm_weight, const void *k_norm_weight, float eps,
+                         void *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                         void *k_cache, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                         void *v_cache, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                         int *length_dev, int pos, int B, int L, int H, int Hkv, int D, int dtype,
+                         void *stream);
+
+/*
  * Intra-block attention-residual read (one fused pass):
  *   r_n = 1/sqrt(mean(x_n^2) + eps), s_n = sum_d query_d * weight_d * x_nd * r_n,
  *   alpha = softmax_n(s), out = sum_n alpha_n * x_n      (fp32 arithmetic)
@@ -198,6 +218,21 @@ int motif_gdn_decode_fused(
 int motif_attn_res_read(const void *const *sources, const int64_t *src_sb, const int64_t *src_st,
                         int nsrc, const void *query, const void *norm_weight, float eps, void *out,
                         int64_t out_sb, int64_t out_st, int B, int T, int D, int dtype, void *stream);
+
+/*
+ * The attention-residual read above followed by up to two RMSNorms of its result h
+ * (the decoder's attn_norm and mlp_norm), in the same pass: norm_outs[i] =
+ * T(h * rsqrt(mean(h^2) + norm_eps)) * norm_weights[i], h first rounded to T as the
+ * reference stores it.  Replaces motif/block/decoder.py:195-206 (apply_block_attn_res,
+ * then attn_norm / mlp_norm; RMSNorm motif/ops/rms_norm.py:461-486).
+ *   out may be NULL (h not stored); nnorm in 0..2; norm_weights[i] [D],
+ *   norm_outs[i] [B,T,D] with strides norm_sb[i], norm_st[i] (host arrays).
+ */
+int motif_attn_res_read_norms(const void *const *sources, const int64_t *src_sb, const int64_t *src_st,
+                              int nsrc, const void *query, const void *norm_weight, float eps, void *out,
+                              int64_t out_sb, int64_t out_st, int nnorm, const void *const *norm_weights,
+                              void *const *norm_outs, const int64_t *norm_sb, const int64_t *norm_st,
+                              float norm_eps, int B, int T, int D, int dtype, void *stream);
 
 /*
  * y = x W^T for a few activation rows (the projections of a decode step), bf16 with

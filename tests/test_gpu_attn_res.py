@@ -54,3 +54,31 @@ def test_strided_sources_and_limits():
     assert ((out.double().cpu() - ref).abs().max() / ref.abs().max()).item() <= 1e-5
     with pytest.raises(NotImplementedError):
         attn_res_read([views[0]] * 9, q.to(DEV), _Norm(w.to(DEV)))
+
+
+@pytest.mark.parametrize('dtype', [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize('nsrc,B,T,D', [(1, 4, 3, 768), (3, 2, 17, 768), (6, 64, 1, 768), (2, 1, 9, 256)])
+def test_read_with_norms_matches_oracle(dtype, nsrc, B, T, D):
+    '''Read + the decoder's two RMSNorms in one kernel: norm_i(h) for the stored h.
+    bf16: against the oracle's norms of the kernel's own h (the same bf16 h the
+    reference would normalise), so the bar covers the norms only; fp32: 1e-5.'''
+    from motif.ops.attn_res import attn_res_read, attn_res_read_norms
+    from oracle.gdn import rms_norm
+    srcs, q, w = _case(nsrc, B, T, D, nsrc * 10 + B, dtype)
+    g = torch.Generator().manual_seed(5)
+    wa = (1.0 + 0.1 * torch.randn(D, generator=g)).to(dtype)
+    wb = (1.0 + 0.1 * torch.randn(D, generator=g)).to(dtype)
+    ds = [s.to(DEV) for s in srcs]
+    ya, yb = attn_res_read_norms(ds, q.to(DEV), _Norm(w.to(DEV)), _Norm(wa.to(DEV)), _Norm(wb.to(DEV)))
+    h = attn_res_read(ds, q.to(DEV), _Norm(w.to(DEV))) if nsrc > 1 else ds[0]
+    if dtype == torch.float32:
+        href = oracle_read([s.double() for s in srcs], q.double(), w.double(), 1e-6)
+        for y, wt in ((ya, wa), (yb, wb)):
+            ref = rms_norm(href, wt.double(), 1e-6)
+            err = ((y.double().cpu() - ref).abs().max() / ref.abs().max()).item()
+            assert err <= 1e-5, err
+    else:
+        hc = h.cpu()
+        for y, wt in ((ya, wa), (yb, wb)):
+            ref = rms_norm(hc, wt, 1e-6)   # bf16 eager norm of the same h
+            assert_bf16_close(y, ref.float(), 2e-2, 5e-3, f'norm n={nsrc}')
