@@ -322,47 +322,6 @@ __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
 }
 
 // ------------------------------------------------------------------ decode
-// 8 consecutive features of one row as floats (16-byte loads).
-template <typename T> __device__ __forceinline__ void load8(const T *p, float out[8]);
-template <> __device__ __forceinline__ void load8<bf16_t>(const bf16_t *p, float out[8]) {
-  const uint4 raw = *reinterpret_cast<const uint4 *>(p);
-  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    out[2 * e] = __uint_as_float(w[e] << 16);
-    out[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
-  }
-}
-template <> __device__ __forceinline__ void load8<float>(const float *p, float out[8]) {
-  const float4 x = *reinterpret_cast<const float4 *>(p), y = *reinterpret_cast<const float4 *>(p + 4);
-  out[0] = x.x; out[1] = x.y; out[2] = x.z; out[3] = x.w;
-  out[4] = y.x; out[5] = y.y; out[6] = y.z; out[7] = y.w;
-}
-
-// 8 raw features of one K / V row kept packed in registers until use.
-template <typename T> struct Row8;
-template <> struct Row8<bf16_t> {
-  uint4 r;
-  __device__ __forceinline__ void load(const bf16_t *p) { r = *reinterpret_cast<const uint4 *>(p); }
-  __device__ __forceinline__ void zero() { r = uint4{0, 0, 0, 0}; }
-  __device__ __forceinline__ float get(int e) const {
-    const uint32_t w = e < 2 ? r.x : e < 4 ? r.y : e < 6 ? r.z : r.w;
-    return (e & 1) ? __uint_as_float(w & 0xffff0000u) : __uint_as_float(w << 16);
-  }
-};
-template <> struct Row8<float> {
-  float4 x, y;
-  __device__ __forceinline__ void load(const float *p) {
-    x = *reinterpret_cast<const float4 *>(p);
-    y = *reinterpret_cast<const float4 *>(p + 4);
-  }
-  __device__ __forceinline__ void zero() { x = y = float4{0.f, 0.f, 0.f, 0.f}; }
-  __device__ __forceinline__ float get(int e) const {
-    const float4 &h = e < 4 ? x : y;
-    const int i = e & 3;
-    return i == 0 ? h.x : i == 1 ? h.y : i == 2 ? h.z : h.w;
-  }
-};
 
 // GGD bias table per head in log2 units: entry j holds delta = j - kTabPad (delta =
 // i_abs - key; the kTabPad leading entries, delta < 0, belong to masked keys and only
@@ -384,30 +343,64 @@ __device__ __forceinline__ float sum8(float x) {
   return x;
 }
 
-// 8 features of one K / V row as floats from a range-checked buffer (0 past the end).
-template <typename T> __device__ __forceinline__ void buf_row8(buf_t r, uint32_t off, float x[8]);
-template <> __device__ __forceinline__ void buf_row8<bf16_t>(buf_t r, uint32_t off, float x[8]) {
-  const uint4 u = buf_ld16(r, off);
-  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    x[2 * e] = __uint_as_float(w[e] << 16);
-    x[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+
+// 8 features of one K / V / q row kept packed as loaded: bf16 dots use v_dot2_f32_bf16
+// on the packed pairs (the products are exact in fp32), fp32 rows take two loads.
+template <typename T> struct Row8;
+template <> struct Row8<bf16_t> {
+  uint4 u;
+  __device__ __forceinline__ void load(buf_t r, uint32_t off) { u = buf_ld16(r, off); }
+  __device__ __forceinline__ void load(const bf16_t *p) { u = *reinterpret_cast<const uint4 *>(p); }
+  __device__ __forceinline__ float dot(const Row8 &o, float acc) const {
+    typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf2;
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, u.x), __builtin_bit_cast(bf2, o.u.x), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, u.y), __builtin_bit_cast(bf2, o.u.y), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, u.z), __builtin_bit_cast(bf2, o.u.z), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, u.w), __builtin_bit_cast(bf2, o.u.w), acc, false);
+    return acc;
   }
-}
-template <> __device__ __forceinline__ void buf_row8<float>(buf_t r, uint32_t off, float x[8]) {
-  const uint4 u = buf_ld16(r, off), v = buf_ld16(r, off + 16);
-  x[0] = __uint_as_float(u.x); x[1] = __uint_as_float(u.y); x[2] = __uint_as_float(u.z); x[3] = __uint_as_float(u.w);
-  x[4] = __uint_as_float(v.x); x[5] = __uint_as_float(v.y); x[6] = __uint_as_float(v.z); x[7] = __uint_as_float(v.w);
-}
+  __device__ __forceinline__ void unpack(float x[8]) const {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = __uint_as_float(w[e] << 16);
+      x[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+    }
+  }
+};
+template <> struct Row8<float> {
+  uint4 u, v;
+  __device__ __forceinline__ void load(buf_t r, uint32_t off) { u = buf_ld16(r, off); v = buf_ld16(r, off + 16); }
+  __device__ __forceinline__ void load(const float *p) {
+    u = *reinterpret_cast<const uint4 *>(p);
+    v = *reinterpret_cast<const uint4 *>(p + 4);
+  }
+  __device__ __forceinline__ float dot(const Row8 &o, float acc) const {
+    float x[8], y[8];
+    unpack(x);
+    o.unpack(y);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = fmaf(x[e], y[e], acc);
+    return acc;
+  }
+  __device__ __forceinline__ void unpack(float x[8]) const {
+    x[0] = __uint_as_float(u.x); x[1] = __uint_as_float(u.y); x[2] = __uint_as_float(u.z); x[3] = __uint_as_float(u.w);
+    x[4] = __uint_as_float(v.x); x[5] = __uint_as_float(v.y); x[6] = __uint_as_float(v.z); x[7] = __uint_as_float(v.w);
+  }
+};
+
+constexpr int kDecKeys = 4;                 // keys per 8-lane group per step
+constexpr int kDecStep = 8 * kDecKeys;      // keys per wave per step
 
 // Rows of a workgroup: global row gr = qc * R + r over the L * group (query,
 // head) pairs of one kv head, query i = gr / group, head = kvh * group + gr % group.
-// A wave takes 64 consecutive keys per step: lane (ksub = lane / 8, 8 features
-// from column 8 (lane % 8)) owns keys n0 + 8 ksub + it, it < 8, whose 8 bias
-// entries are 2 contiguous 16-byte reads of the head's table.  Each 8-lane group
-// keeps its own running max / sum / output (merged at the end), so the step has
-// no cross-lane traffic besides the 8-lane dot-product sums.
+// A wave takes kDecStep consecutive keys per step: lane (ksub = lane / 8, 8 features
+// from column 8 (lane % 8)) owns keys n0 + 4 ksub + it, it < 4, whose 4 bias entries
+// are one 16-byte read of the head's table.  The next step's K / V rows and bias
+// entries are loaded before the current step is computed (two register stages), so a
+// wave keeps a step of loads in flight.  Each 8-lane group keeps its own running
+// max / sum / output (merged at the end): the step has no cross-lane traffic besides
+// the 8-lane dot-product sums.
 template <typename T, int R>
 __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a, const float *tab, int tab_n) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -426,7 +419,8 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a, const fl
   const int k_lo = split * per;
   const int k_hi = min(min(kv_len, k_lo + per), a.q_start + i_last + 1);
 
-  float q[R][8], c_qk[R], c_b[R];
+  Row8<T> q[R];
+  float c_qk[R], c_b[R];
   int qabs[R];
   buf_t tb[R];
 #pragma unroll
@@ -435,7 +429,7 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a, const fl
     const bool ok = gr < total_rows;
     const int head = kvh * group + (ok ? gr % group : 0);
     const int i = ok ? gr / group : 0;
-    load8(qg + b * a.q_sb + head * a.q_sh + int64_t(i) * a.q_st + dc, q[r]);
+    q[r].load(qg + b * a.q_sb + head * a.q_sh + int64_t(i) * a.q_st + dc);
     const float mul = ok ? a.ssmax[head] * a.log_n[b * a.ln_sb + int64_t(i) * a.ln_st] : 0.f;
     c_qk[r] = mul * a.scale * kLog2e;
     c_b[r] = mul;  // the table is in log2 units already
@@ -453,37 +447,49 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a, const fl
 
   const T *kp = static_cast<const T *>(a.k) + b * a.k_sb + kvh * a.k_sh;
   const T *vp = static_cast<const T *>(a.v) + b * a.v_sb + kvh * a.v_sh;
+  // rows past k_hi (the prefetch past the range) read as zeros
   const buf_t kbuf = make_buf(kp, k_hi > 0 ? static_cast<uint32_t>(((k_hi - 1) * a.k_st + kD) * sizeof(T)) : 0u);
   const buf_t vbuf = make_buf(vp, k_hi > 0 ? static_cast<uint32_t>(((k_hi - 1) * a.v_st + kD) * sizeof(T)) : 0u);
 
-  for (int n0 = k_lo + w * kBN; n0 < k_hi; n0 += 4 * kBN) {
-    const int kb = n0 + 8 * ksub;  // this lane group's first key
-    float kf[8][8], vf[8][8], bt[R][8];
+  struct Stage {
+    Row8<T> k[kDecKeys], v[kDecKeys];
+    uint4 bias[R];  // entries delta = qabs - kb - 3 .. qabs - kb (it = 3 .. 0)
+  };
+  auto load_stage = [&](int n0, Stage &st) {
+    const int kb = n0 + kDecKeys * ksub;
 #pragma unroll
-    for (int it = 0; it < 8; ++it) {
-      buf_row8<T>(kbuf, static_cast<uint32_t>(((kb + it) * a.k_st + dc) * sizeof(T)), kf[it]);
-      buf_row8<T>(vbuf, static_cast<uint32_t>(((kb + it) * a.v_st + dc) * sizeof(T)), vf[it]);
+    for (int it = 0; it < kDecKeys; ++it) {
+      st.k[it].load(kbuf, static_cast<uint32_t>(((kb + it) * a.k_st + dc) * sizeof(T)));
+      st.v[it].load(vbuf, static_cast<uint32_t>(((kb + it) * a.v_st + dc) * sizeof(T)));
     }
 #pragma unroll
-    for (int r = 0; r < R; ++r) {  // entries delta = qabs - kb - 7 .. qabs - kb (it = 7 .. 0)
-      const uint32_t off = static_cast<uint32_t>(qabs[r] - kb - 7 + kTabPad) * 4u;
-      const uint4 lo = buf_ld16(tb[r], off), hi = buf_ld16(tb[r], off + 16);
-      const uint32_t wv[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    for (int r = 0; r < R; ++r)
+      st.bias[r] = buf_ld16(tb[r], static_cast<uint32_t>(qabs[r] - kb - (kDecKeys - 1) + kTabPad) * 4u);
+  };
+
+  int n0 = k_lo + w * kDecStep;
+  Stage cur;
+  if (n0 < k_hi) load_stage(n0, cur);
+  for (; n0 < k_hi; n0 += 4 * kDecStep) {
+    Stage nxt;
+    load_stage(n0 + 4 * kDecStep, nxt);
+    // the next stage's loads stay ahead of this step's arithmetic
+    __builtin_amdgcn_sched_barrier(0);
+    const int kb = n0 + kDecKeys * ksub;
+    float vf[kDecKeys][8];
 #pragma unroll
-      for (int it = 0; it < 8; ++it) bt[r][it] = __uint_as_float(wv[7 - it]);
-    }
+    for (int it = 0; it < kDecKeys; ++it) cur.v[it].unpack(vf[it]);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      float sv[8], mx = -INFINITY;
+      const float bt[4] = {__uint_as_float(cur.bias[r].w), __uint_as_float(cur.bias[r].z),
+                           __uint_as_float(cur.bias[r].y), __uint_as_float(cur.bias[r].x)};
+      float sv[kDecKeys], mx = -INFINITY;
 #pragma unroll
-      for (int it = 0; it < 8; ++it) {
-        float d = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) d = fmaf(q[r][e], kf[it][e], d);
-        d = sum8(d);
+      for (int it = 0; it < kDecKeys; ++it) {
+        const float d = sum8(cur.k[it].dot(q[r], 0.f));
         const int key = kb + it;
         const bool ok = key < k_hi && key <= qabs[r];
-        sv[it] = ok ? fmaf(d, c_qk[r], c_b[r] * bt[r][it]) : -INFINITY;
+        sv[it] = ok ? fmaf(d, c_qk[r], c_b[r] * bt[it]) : -INFINITY;
         mx = fmaxf(mx, sv[it]);
       }
       const float m_new = fmaxf(m[r], mx);
@@ -491,7 +497,7 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a, const fl
       const float resc = m[r] == -INFINITY ? 0.f : fast_exp2(m[r] - m_use);
       float ps = 0.f;
 #pragma unroll
-      for (int it = 0; it < 8; ++it) {
+      for (int it = 0; it < kDecKeys; ++it) {
         sv[it] = sv[it] == -INFINITY ? 0.f : fast_exp2(sv[it] - m_use);
         ps += sv[it];
       }
@@ -501,10 +507,11 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a, const fl
       for (int e = 0; e < 8; ++e) {
         float x = acc[r][e] * resc;
 #pragma unroll
-        for (int it = 0; it < 8; ++it) x = fmaf(sv[it], vf[it][e], x);
+        for (int it = 0; it < kDecKeys; ++it) x = fmaf(sv[it], vf[it][e], x);
         acc[r][e] = x;
       }
     }
+    cur = nxt;
   }
 
   // Merge the 8 key groups of the wave (lanes l, l^8, l^16, l^32 share features).
