@@ -72,6 +72,34 @@ def cuda_time(fn, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
+def op_time(fn, launches, replays=5):
+    '''Average device milliseconds of one fn() launch: `launches` calls captured in one
+    hipGraph, replayed `replays` times between HIP events on the capturing stream, so
+    host launch overhead does not enter the figure (it matches the rocprofv3 kernel
+    durations of the same op).'''
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(launches):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (replays * launches)
+
+
 def kernel_timings(dev):
     '''Hot-path ops at the config-3 / config-4 shapes.'''
     import torch
@@ -90,7 +118,7 @@ def kernel_timings(dev):
     v = torch.randn(B, T, H, dv, generator=g).transpose(1, 2).to(dev, torch.bfloat16)
     beta = torch.sigmoid(torch.randn(B, T, H, generator=g)).transpose(1, 2).to(dev, torch.bfloat16)
     gg = F.logsigmoid(torch.randn(B, T, H, generator=g)).transpose(1, 2).to(dev, torch.bfloat16)
-    ms = cuda_time(lambda: ops.chunk_gated_delta_rule(q, k, v, beta, gg), 20, 3)
+    ms = op_time(lambda: ops.chunk_gated_delta_rule(q, k, v, beta, gg), 20)
     fl = gdn_prefill_flops(B, T, H, dk, dv)
     res['gdn_chunk_prefill'] = dict(us=ms * 1e3, unit='TFLOP/s', achieved=fl / (ms * 1e-3) / 1e12,
                                     peak=PEAK_BF16_TFLOPS, bound='mfma', work=fl,
@@ -105,32 +133,40 @@ def kernel_timings(dev):
     mu = torch.zeros(Hc, device=dev)
     ss = torch.ones(Hc, device=dev)
     ln = torch.log(torch.arange(1, T + 1, dtype=torch.float32, device=dev))[None].contiguous()
-    ms = cuda_time(lambda: ops.apply_chord_attention(qc, kc, vc, al, be, mu, ss, ln, q_start=0), 20, 3)
+    ms = op_time(lambda: ops.apply_chord_attention(qc, kc, vc, al, be, mu, ss, ln, q_start=0), 20)
     fl = chord_prefill_flops(1, Hc, D, T)
     res['chord_prefill'] = dict(us=ms * 1e3, unit='TFLOP/s', achieved=fl / (ms * 1e-3) / 1e12,
                                 peak=PEAK_BF16_TFLOPS, bound='mfma', work=fl,
                                 shape='B=1 H=12 Hkv=3 T=4096 D=64 bf16 causal')
 
-    Bd = 64
-    qd = F.normalize(torch.randn(Bd, H, 1, dk, generator=g), dim=-1).to(dev, torch.bfloat16)
-    kd = F.normalize(torch.randn(Bd, H, 1, dk, generator=g), dim=-1).to(dev, torch.bfloat16)
-    vd = torch.randn(Bd, H, 1, dv, generator=g).to(dev, torch.bfloat16)
-    bd = torch.sigmoid(torch.randn(Bd, H, 1, generator=g)).to(dev, torch.bfloat16)
-    gd = F.logsigmoid(torch.randn(Bd, H, 1, generator=g)).to(dev, torch.bfloat16)
+    # fused single-token GDN layer step (conv + norms + gates + delta rule + GatedRMSNorm),
+    # from the fused projection row to the o_proj input, state and conv tails in place
+    Bd, K = 64, 4
+    hk, hv = H * dk, H * dv
+    ncols = 2 * hk + 2 * hv + 2 * H
+    offs = (0, hk, 2 * hk, 2 * hk + hv, 2 * hk + 2 * hv, 2 * hk + 2 * hv + H)
+    proj = (torch.randn(Bd, ncols, generator=g) * 0.5).to(dev, torch.bfloat16)
+    cw = [(torch.randn(c, 1, K, generator=g) * 0.3).to(dev, torch.bfloat16) for c in (hk, hk, hv)]
+    tails = [(torch.randn(Bd, c, K - 1, generator=g) * 0.5).to(dev, torch.bfloat16) for c in (hk, hk, hv)]
+    a_log = torch.empty(H).uniform_(1, 16, generator=g).log().to(dev, torch.bfloat16)
+    dt_bias = (torch.rand(H, generator=g) * 0.1).to(dev, torch.bfloat16)
+    nw = torch.ones(dv, device=dev, dtype=torch.bfloat16)
     S = (torch.randn(Bd, H, dk, dv, generator=g) * 0.05).to(dev)
-    od = torch.empty(Bd, H, 1, dv, device=dev, dtype=torch.bfloat16)
-    ms = cuda_time(lambda: gdn_recurrent_into(qd, kd, vd, bd, gd, S, S, od), 200, 10)
-    byts = Bd * H * dk * dv * 4 * 2 + Bd * H * (2 * dk + 2 * dv + 2) * 2
+    ms = op_time(lambda: ops.gdn_decode_fused(proj, offs, cw, tails, a_log, dt_bias, nw, 1e-6, S, H, dk, dv), 50)
+    byts = (Bd * H * dk * dv * 4 * 2                      # state read + write
+            + Bd * (2 * hk + hv) * (K - 1) * 2 * 2        # conv tails read + write
+            + Bd * ncols * 2 + (2 * hk + hv) * K * 2      # projections, conv weights
+            + Bd * hv * 2)                                # output
     res['gdn_decode'] = dict(us=ms * 1e3, unit='GB/s', achieved=byts / (ms * 1e-3) / 1e9,
                              peak=PEAK_HBM_GBS, bound='hbm', work=byts,
-                             shape='B=64 H=12 dk=64 dv=128 fp32 state, in place')
+                             shape='B=64 H=12 dk=64 dv=128 K=4, fused layer step, fp32 state in place')
 
     Sk = 4097
     qk = (torch.randn(Bd, Hc, 1, D, generator=g) * 0.5).to(dev, torch.bfloat16)
     kk = (torch.randn(Bd, Hkv, Sk, D, generator=g) * 0.5).to(dev, torch.bfloat16)
     vk = (torch.randn(Bd, Hkv, Sk, D, generator=g) * 0.5).to(dev, torch.bfloat16)
     lnd = torch.full((Bd, 1), float(torch.log(torch.tensor(float(Sk)))), device=dev)
-    ms = cuda_time(lambda: ops.apply_chord_attention(qk, kk, vk, al, be, mu, ss, lnd), 100, 5)
+    ms = op_time(lambda: ops.apply_chord_attention(qk, kk, vk, al, be, mu, ss, lnd), 20)
     byts = 2 * Bd * Hkv * Sk * D * 2 + 2 * Bd * Hc * D * 2
     res['chord_decode'] = dict(us=ms * 1e3, unit='GB/s', achieved=byts / (ms * 1e-3) / 1e9,
                                peak=PEAK_HBM_GBS, bound='hbm', work=byts,
@@ -154,15 +190,18 @@ def copy_calibration(dev, mib=256, reps=5):
 
 # rocprofv3 --pmc summary (FETCH_SIZE / WRITE_SIZE, copy-calibrated) of bench.py --kernels-only
 TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'hot_path_ops_hbm_traffic.txt')
-OP_KERNELS = {'gdn_chunk_prefill': ('gdn_prep_mfma', 'gdn_scan_mfma'), 'chord_prefill': ('chord_fwd_kernel',),
-              'gdn_decode': ('gdn_recurrent_kernel',), 'chord_decode': ('chord_decode_kernel', 'chord_merge_kernel')}
+OP_KERNELS = {'gdn_chunk_prefill': ('gdn_prep_mfma', 'gdn_state_scan', 'gdn_chunk_out'),
+              'chord_prefill': ('chord_fwd_kernel',),
+              'gdn_decode': ('gdn_decode_kernel',),
+              'chord_decode': ('chord_bias_table_kernel', 'chord_decode_kernel', 'chord_merge_kernel')}
 
 
 def measured_traffic(op):
     '''HBM bytes per launch of `op` (all its kernels) from the committed --pmc summary, or None.'''
     try:
         with open(TRAFFIC_FILE) as f:
-            rows = [ln.split() for ln in f if ln[:1].isalpha() and '<' in ln.split()[0] and len(ln.split()) == 5]
+            rows = [ln.split() for ln in f
+                    if ln[:1].isalpha() and len(ln.split()) == 5 and ln.split()[1].isdigit()]
     except OSError:
         return None
     total, seen = 0.0, set()

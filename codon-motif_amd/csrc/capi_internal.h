@@ -11,6 +11,9 @@ namespace motif {
 
 int set_error(int code, const std::string &msg);
 
+// Zero n bytes at p on stream s with a kernel (safe inside a captured graph).
+int zero_async(void *p, size_t n, hipStream_t s);
+
 inline int check_launch(const char *what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)

@@ -351,8 +351,8 @@ static int conv_entry(
   if (nseq == 0 || (!packed && L == 0)) {
     if (!packed && tail_out && tail_out != tail_in && B > 0) {
       const size_t n = static_cast<size_t>(B) * D * (K - 1) * (dtype == MOTIF_F32 ? 4 : 2);
-      hipError_t e = tail_in ? hipMemcpyAsync(tail_out, tail_in, n, hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream))
-                             : hipMemsetAsync(tail_out, 0, n, static_cast<hipStream_t>(stream));
+      if (!tail_in) return zero_async(tail_out, n, static_cast<hipStream_t>(stream));
+      hipError_t e = hipMemcpyAsync(tail_out, tail_in, n, hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream));
       if (e != hipSuccess) return set_error(MOTIF_ERR_HIP, hipGetErrorString(e));
     }
     return MOTIF_OK;

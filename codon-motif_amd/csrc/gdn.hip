@@ -452,9 +452,8 @@ extern "C" int motif_gdn_chunk_fwd(
   if (total_chunks == 0) {
     // No tokens: the final state is the initial one.
     const size_t n = static_cast<size_t>(nseq) * H * dk * dv * sizeof(float);
-    hipError_t e = state_in ? hipMemcpyAsync(state_out, state_in, n, hipMemcpyDeviceToDevice,
-                                             static_cast<hipStream_t>(stream))
-                            : hipMemsetAsync(state_out, 0, n, static_cast<hipStream_t>(stream));
+    if (!state_in) return zero_async(state_out, n, static_cast<hipStream_t>(stream));
+    hipError_t e = hipMemcpyAsync(state_out, state_in, n, hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? MOTIF_OK : set_error(MOTIF_ERR_HIP, hipGetErrorString(e));
   }
   if (!q || !k || !v || !beta || !g || !o)
