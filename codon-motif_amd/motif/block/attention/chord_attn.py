@@ -115,22 +115,21 @@ class ChordAttention(BasicAttention):
             kv_states = hidden_states
         batch_size, q_len, _ = hidden_states.shape
         kv_len_input = kv_states.shape[1]
-        if (kv_states is hidden_states and attention_mask is None and not output_attentions
-                and self._static_fusable(hidden_states, past_key_value)):
-            return self._forward_static(hidden_states, past_key_value, embedding_start, section_log_len)
-
-        xq, xk, xv, xg = self._project(hidden_states, kv_states)
-        q = self.q_norm(self.reshape_q(xq, q_len, batch_size))
-        k = self.k_norm(self.reshape_kv(xk, kv_len_input, batch_size))
-        v = self.reshape_kv(xv, kv_len_input, batch_size)
-
         use_cache = isinstance(past_key_value, KVLayerCache)
         q_start = embedding_start
         if use_cache:
             cached = past_key_value.seq_length
             if isinstance(q_start, int) and q_start == 0 and cached > 0:
                 q_start = cached
-            k, v = past_key_value.update(k, v, dim=2)
+        if kv_states is hidden_states and self._prep_fusable(hidden_states):
+            q, k, v, xg = self._fused_inputs(hidden_states, past_key_value if use_cache else None)
+        else:
+            xq, xk, xv, xg = self._project(hidden_states, kv_states)
+            q = self.q_norm(self.reshape_q(xq, q_len, batch_size))
+            k = self.k_norm(self.reshape_kv(xk, kv_len_input, batch_size))
+            v = self.reshape_kv(xv, kv_len_input, batch_size)
+            if use_cache:
+                k, v = past_key_value.update(k, v, dim=2)
         current_key_value = past_key_value if use_cache else None
         kv_len = k.shape[2]
         log_n = self._log_n(q_start, q_len, batch_size, hidden_states.device, section_log_len)
@@ -164,57 +163,56 @@ class ChordAttention(BasicAttention):
             self.__dict__['_ggd_cat'] = cached
         return cached[1]
 
-    def _static_fusable(self, x, cache):
-        '''Inference into a preallocated KV cache with the fused input kernel.'''
-        if not isinstance(cache, StaticKVLayerCache) or cache.k is None or not x.is_cuda:
-            return False
-        if x.dtype not in (torch.bfloat16, torch.float32) or cache.k.dtype != x.dtype:
+    def _prep_fusable(self, x):
+        '''Self-attention inputs the fused input kernel (motif_chord_qkv_prep) serves.'''
+        if not x.is_cuda or x.dtype not in (torch.bfloat16, torch.float32):
             return False
         if (self.head_dim * x.element_size()) % 16 or self.head_dim * x.element_size() > 512:
             return False
         if self.q_norm.weight is None or self.k_norm.weight is None or self.q_norm.eps != self.k_norm.eps:
             return False
-        if torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()):
-            return False
-        return cache.length + x.shape[1] <= cache.capacity
+        return not (torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()))
 
-    def _forward_static(self, hidden_states, cache, embedding_start, section_log_len):
-        '''Projection GEMM, then one kernel for the q / k RMSNorms and the cache append
-        (motif_chord_qkv_prep), the Chord kernel over the cache prefix and the gated
-        o_proj -- the same results as the general path.'''
+    def _fused_inputs(self, hidden_states, cache):
+        '''(q, k, v, g) from one projection GEMM and one kernel for the q / k RMSNorms and
+        the placement of k / v: straight into a preallocated cache (StaticKVLayerCache with
+        room), else into new tensors that the cache (if any) appends.  k, v are the cache
+        views the attention reads; g is the gate pre-activation (G = sigmoid(g)).'''
         B, L, _ = hidden_states.shape
         H, Hkv, D, hs, kd = self.num_heads, self.num_kv_heads, self.head_dim, self.hidden_size, self.kv_dim
+        dev, dt = hidden_states.device, hidden_states.dtype
         w, b = cat_weights(self, '_proj_cat', (self.q_proj, self.k_proj, self.v_proj, self.g_proj))
         proj = project(hidden_states, w, b)
         if proj.stride(-1) != 1:
             proj = proj.contiguous()
-        q_start = embedding_start
-        if isinstance(q_start, int) and q_start == 0 and cache.length > 0:
-            q_start = cache.length
-        pos = cache.reserve(L)
-        q = torch.empty(B, H, L, D, dtype=hidden_states.dtype, device=hidden_states.device)
-        dt = hidden_states.dtype
+        static = (isinstance(cache, StaticKVLayerCache) and cache.k is not None and cache.k.dtype == dt
+                  and cache.length + L <= cache.capacity)
+        if static:
+            pos = cache.reserve(L)
+            kd_t, vd_t, len_dev = cache.k, cache.v, cache.length_dev
+        else:
+            pos = 0
+            kd_t = torch.empty(B, Hkv, L, D, dtype=dt, device=dev)
+            vd_t = torch.empty(B, Hkv, L, D, dtype=dt, device=dev)
+            len_dev = None
+        q = torch.empty(B, H, L, D, dtype=dt, device=dev)
         qw = self.q_norm.weight.to(dt).contiguous()
         kw = self.k_norm.weight.to(dt).contiguous()
-        kc, vc = cache.k, cache.v
         rc = _lib.lib().motif_chord_qkv_prep(
             proj.data_ptr(), proj.stride(0), proj.stride(1), 0, hs, hs + kd,
             qw.data_ptr(), kw.data_ptr(), float(self.q_norm.eps),
             q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
-            kc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2),
-            vc.data_ptr(), vc.stride(0), vc.stride(1), vc.stride(2),
-            _lib.ptr(cache.length_dev), pos, B, L, H, Hkv, D, _lib.dtype_code(dt),
-            _lib.stream_ptr(hidden_states.device))
+            kd_t.data_ptr(), kd_t.stride(0), kd_t.stride(1), kd_t.stride(2),
+            vd_t.data_ptr(), vd_t.stride(0), vd_t.stride(1), vd_t.stride(2),
+            _lib.ptr(len_dev), pos, B, L, H, Hkv, D, _lib.dtype_code(dt), _lib.stream_ptr(dev))
         _lib.check(rc, 'motif_chord_qkv_prep')
-        k, v = kc[:, :, :cache.length], vc[:, :, :cache.length]
-        log_n = self._log_n(q_start, L, B, hidden_states.device, section_log_len)
-        alpha, beta, mu, ssmax = self._ggd_cached()
-        start = int(q_start.reshape(-1)[0]) if isinstance(q_start, torch.Tensor) else int(q_start)
-        out = apply_chord_attention(q, k, v, alpha, beta, mu, ssmax,
-                                    log_n if log_n.dim() == 2 else log_n.expand(B, L),
-                                    q_start=start, softmax_scale=D ** -0.5, eps=_GGD_EPS)
-        out = out.transpose(1, 2).reshape(B, L, hs)
-        return AttentionOutput(output=self._gated_output(out, proj[..., hs + 2 * kd:]), past_key_value=cache)
+        if static:
+            k, v = cache.k[:, :, :cache.length], cache.v[:, :, :cache.length]
+        elif cache is not None:
+            k, v = cache.update(kd_t, vd_t, dim=2)
+        else:
+            k, v = kd_t, vd_t
+        return q, k, v, proj[..., hs + 2 * kd:]
 
     def _project(self, hidden_states, kv_states):
         '''q, k, v and the gate pre-activation g (G = sigmoid(g)).  Self-attention runs the
@@ -243,10 +241,13 @@ class ChordAttention(BasicAttention):
         batch_size, T, _ = hidden_states.shape
         if batch_size != 1:
             raise ValueError('forward_varlen expects packed sequences with B == 1')
-        xq, xk, xv, xg = self._project(hidden_states, hidden_states)
-        q = self.q_norm(self.reshape_q(xq, T, 1))
-        k = self.k_norm(self.reshape_kv(xk, T, 1))
-        v = self.reshape_kv(xv, T, 1)
+        if self._prep_fusable(hidden_states):
+            q, k, v, xg = self._fused_inputs(hidden_states, None)
+        else:
+            xq, xk, xv, xg = self._project(hidden_states, hidden_states)
+            q = self.q_norm(self.reshape_q(xq, T, 1))
+            k = self.k_norm(self.reshape_kv(xk, T, 1))
+            v = self.reshape_kv(xv, T, 1)
         cu = cu_seqlens.detach().to('cpu', torch.int64)
         pos = torch.arange(T) - torch.repeat_interleave(cu[:-1], cu[1:] - cu[:-1])
         log_n = torch.log(pos.to(torch.float32) + 1).to(hidden_states.device)[None]

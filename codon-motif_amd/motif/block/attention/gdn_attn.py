@@ -26,6 +26,7 @@ import torch.nn.functional as F
 
 from motif.block.attention.base import AttentionOutput, BasicAttention
 from motif.model.cache import GatedDeltaAttentionLayerCache
+from motif.ops.epilogue import gated_rms_norm_heads, usable
 from motif.ops import (
     GatedRMSNorm,
     cat_weights,
@@ -141,7 +142,13 @@ class GatedDeltaAttention(BasicAttention):
         return q, k, v, tuple(o[1] for o in outs)
 
     def _output(self, o, gate, B, L):
-        o = o.to(gate.dtype).transpose(1, 2)
+        '''GatedRMSNorm of [o || gate] per head, then o_proj.  One HIP pass over o and the
+        gate (no concatenation) when the kernel serves the tensors.'''
+        o = o.to(gate.dtype)
+        if self.o_norm.weight is not None and usable(o, gate):
+            y = gated_rms_norm_heads(o, gate, self.o_norm.weight, self.o_norm.eps)
+            return project(y, self.o_proj.weight, self.o_proj.bias)
+        o = o.transpose(1, 2)
         gate = gate.reshape(B, L, self.num_heads, self.dv)
         o = self.o_norm(torch.cat([o, gate], dim=-1)).reshape(B, L, -1)
         return project(o, self.o_proj.weight, self.o_proj.bias)

@@ -4,6 +4,7 @@ up to a multiple of 128.'''
 import torch.nn as nn
 
 from motif.ops import SwiGLU as SwiGLUOp
+from motif.ops.epilogue import add_fold, usable
 from motif.ops.linear_rows import linear_rows, rows_eligible
 
 
@@ -31,8 +32,9 @@ class SwiGLU(nn.Module):
 
     def forward_residual(self, x, residual, partial=None):
         '''(f, p) with f = residual + forward(x) and p = partial + f (None when `partial`
-        is None).  For decode-sized inputs both adds run in the down projection's
-        epilogue; otherwise p is None and the caller folds f itself.'''
+        is None, or when the adds took the torch fallback: the caller then folds f
+        itself).  Decode-sized inputs run both adds in the down projection's epilogue,
+        larger ones in one elementwise kernel.'''
         if (self._fused(x) and residual.dtype == x.dtype and residual.shape[:-1] == x.shape[:-1]
                 and residual.stride(-1) == 1
                 and (partial is None or (partial.shape == residual.shape and partial.dtype == x.dtype
@@ -41,4 +43,8 @@ class SwiGLU(nn.Module):
             if partial is None:
                 return linear_rows(h, self.down_proj.weight, 'resid', aux=residual), None
             return linear_rows(h, self.down_proj.weight, 'resid', aux=residual, aux2=partial)
-        return residual + self.forward(x), None
+        out = self.forward(x)
+        if residual.shape == out.shape and usable(residual, out) and (
+                partial is None or (partial.shape == out.shape and usable(partial))):
+            return add_fold(residual, out, partial)
+        return residual + out, None

@@ -1,0 +1,78 @@
+'''Prefill-size elementwise stages on HIP kernels (csrc/epilogue.hip), each one pass
+over HBM, rounding to the activation dtype where the reference's separate ops round:
+
+- `gated_rms_norm_heads`: GatedRMSNorm of the GDN layer output per head, from o and
+  the gate directly (the reference concatenates [o || gate] first;
+  motif/block/attention/gdn_attn.py:206-209, motif/ops/rms_norm.py:530-553).
+- `swiglu`: out * SiLU(gate) of the fused gate/up projection (motif/ops/swiglu.py:252-253).
+- `add_fold`: f = a + b and p' = p + f, the decoder's f_h and the block's running sum
+  (motif/block/decoder.py:208-213).
+
+`usable(*tensors)` says whether the kernels serve a call (ROCm, bf16/fp32, 16-byte
+aligned rows, no autograd); callers keep the torch formula otherwise.
+'''
+import torch
+
+from . import _lib
+
+
+def usable(*ts):
+    t0 = ts[0]
+    if not t0.is_cuda or t0.dtype not in (torch.bfloat16, torch.float32):
+        return False
+    if torch.is_grad_enabled() and any(t.requires_grad for t in ts):
+        return False
+    vec = 16 // t0.element_size()
+    for t in ts:
+        if t.dtype != t0.dtype or t.stride(-1) != 1 or t.data_ptr() % 16:
+            return False
+        if any(s % vec for s in t.stride()[:-1]) or t.shape[-1] % vec:
+            return False
+    return True
+
+
+def gated_rms_norm_heads(o, gate, weight, eps):
+    '''y [B, L, H*dv] = GatedRMSNorm over the head rows o[b, h, t, :] with the gate
+    gate[b, t, h*dv:(h+1)*dv] (o: [B, H, L, dv] any strides with unit feature stride;
+    gate: [B, L, H*dv]).'''
+    B, H, L, dv = o.shape
+    dt = o.dtype
+    w = weight.detach().to(dt).contiguous()
+    y = torch.empty(B, L, H * dv, dtype=dt, device=o.device)
+    rc = _lib.lib().motif_gated_rms_norm(
+        o.data_ptr(), o.stride(0), o.stride(1), o.stride(2), gate.data_ptr(), gate.stride(0), gate.stride(1),
+        w.data_ptr(), float(eps), y.data_ptr(), y.stride(0), y.stride(1), B, L, H, dv,
+        _lib.dtype_code(dt), _lib.stream_ptr(o.device))
+    _lib.check(rc, 'motif_gated_rms_norm')
+    return y
+
+
+def swiglu(x):
+    '''x [..., 2I] -> x[..., :I] * SiLU(x[..., I:]).'''
+    x2 = x.reshape(-1, x.shape[-1])
+    M, I = x2.shape[0], x.shape[-1] // 2
+    y = torch.empty(*x.shape[:-1], I, dtype=x.dtype, device=x.device)
+    rc = _lib.lib().motif_swiglu(x2.data_ptr(), x2.stride(0), y.data_ptr(), I, M, I, _lib.dtype_code(x.dtype),
+                                 _lib.stream_ptr(x.device))
+    _lib.check(rc, 'motif_swiglu')
+    return y
+
+
+def add_fold(a, b, p=None):
+    '''(f, p') with f = a + b and p' = p + f (p' is None when p is None); a, b, p of one
+    shape [..., N].'''
+    N = a.shape[-1]
+    a2, b2 = a.reshape(-1, N), b.reshape(-1, N)
+    f = torch.empty_like(a, memory_format=torch.contiguous_format)
+    f2 = f.view(-1, N)
+    p2 = po = po2 = None
+    if p is not None:
+        p2 = p.reshape(-1, N)
+        po = torch.empty_like(f)
+        po2 = po.view(-1, N)
+    rc = _lib.lib().motif_add_fold(a2.data_ptr(), a2.stride(0), b2.data_ptr(), b2.stride(0), _lib.ptr(p2),
+                                   0 if p2 is None else p2.stride(0), f2.data_ptr(), N, _lib.ptr(po2),
+                                   0 if po2 is None else N, a2.shape[0], N, _lib.dtype_code(a.dtype),
+                                   _lib.stream_ptr(a.device))
+    _lib.check(rc, 'motif_add_fold')
+    return f, po

@@ -1,7 +1,8 @@
-'''SwiGLU activation module (adjacent to the hot path; PyTorch-ROCm).
+'''SwiGLU activation module (adjacent to the hot path).
 
 values * SiLU(gate) over the two halves of the split dimension, as the
-reference's motif/ops/swiglu.py:184-253.
+reference's motif/ops/swiglu.py:184-253.  On ROCm tensors (last dimension, no
+autograd) it is one HIP pass (`motif_swiglu`); otherwise the torch formula.
 '''
 import torch
 import torch.nn as nn
@@ -15,5 +16,9 @@ class SwiGLU(nn.Module):
         self.use_triton = False
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.dim in (-1, x.dim() - 1) and x.shape[-1] % 2 == 0:
+            from .epilogue import swiglu, usable
+            if usable(x):
+                return swiglu(x)
         out, gate = torch.split(x, x.size(self.dim) // 2, dim=self.dim)
         return out * F.silu(gate)

@@ -254,6 +254,31 @@ int motif_linear_rows(const void *x, int64_t x_rs, const void *w, int64_t w_rs, 
                       int M, int N, int K, int epilogue, const void *aux, int64_t aux_rs,
                       const void *aux2, int64_t aux2_rs, void *y2, int64_t y2_rs, void *stream);
 
+/*
+ * GatedRMSNorm of the GDN layer output per head without the concatenation:
+ *   y[b, t, h*dv + e] = T(T(T(o * rsqrt(mean_e o^2 + eps)) * weight[e]) * T(SiLU(gate[b, t, h*dv + e])))
+ * for o = o[b, h, t, :].  Replaces motif/block/attention/gdn_attn.py:206-209 (cat + o_norm,
+ * motif/ops/rms_norm.py:530-553).  o [B, H, L, dv] (strides o_sb, o_sh, o_st), gate / y
+ * [B, L, H*dv] (strides g_sb, g_st / y_sb, y_st), weight [dv]; rows 16-byte aligned.
+ */
+int motif_gated_rms_norm(const void *o, int64_t o_sb, int64_t o_sh, int64_t o_st, const void *gate,
+                         int64_t g_sb, int64_t g_st, const void *weight, float eps, void *y,
+                         int64_t y_sb, int64_t y_st, int B, int L, int H, int dv, int dtype, void *stream);
+
+/*
+ * y[m, :] = x[m, :I] * SiLU(x[m, I:]) (SiLU rounded to T first) -- the SwiGLU activation
+ * (motif/ops/swiglu.py:252-253).  x [M, 2I] (row stride x_rs), y [M, I].
+ */
+int motif_swiglu(const void *x, int64_t x_rs, void *y, int64_t y_rs, int M, int I, int dtype, void *stream);
+
+/*
+ * f = a + b and p_out = p + f (p may be NULL), all [M, N] row-major with their row
+ * strides: the decoder's f_h = attn + mlp and the block's running sum
+ * (motif/block/decoder.py:208-213, motif/model/cache.py:514-526).
+ */
+int motif_add_fold(const void *a, int64_t a_rs, const void *b, int64_t b_rs, const void *p, int64_t p_rs,
+                   void *f, int64_t f_rs, void *p_out, int64_t po_rs, int M, int N, int dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

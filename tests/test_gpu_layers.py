@@ -226,3 +226,33 @@ def test_tiny_model_varlen_equals_independent_runs():
     one = m32(ids[None, 30:31]).logits
     two = m32(ids[None, 30:32]).logits[:, :1]
     assert_fp32_close(one, two, 1e-4, 'fp32 L=1 vs first position of L=2')
+
+
+@torch.no_grad()
+def test_elementwise_stage_kernels_match_torch():
+    """GatedRMSNorm of the GDN output (from o and the gate, no concatenation), SwiGLU and
+    the residual add-fold, against the torch formulas they replace (same roundings:
+    bit-identical expected up to the SiLU approximation, 1 bf16 ulp)."""
+    import torch.nn.functional as F
+    from motif.ops.epilogue import add_fold, gated_rms_norm_heads, swiglu
+    from motif.ops.rms_norm import GatedRMSNorm
+    g = torch.Generator().manual_seed(3)
+    for dt in (torch.float32, torch.bfloat16):
+        B, H, L, dv = 2, 3, 37, 128
+        o = torch.randn(B, L, H, dv, generator=g).to(DEV, dt).transpose(1, 2)   # [B,H,L,dv] view
+        big = torch.randn(B, L, 5 * H * dv, generator=g).to(DEV, dt)
+        gate = big[..., 2 * H * dv:3 * H * dv]                                 # strided column view
+        norm = GatedRMSNorm(dv).to(DEV, dt)
+        norm.weight.copy_((1 + 0.1 * torch.randn(dv, generator=g)).to(dt))
+        y = gated_rms_norm_heads(o, gate, norm.weight, norm.eps)
+        ref = norm(torch.cat([o.transpose(1, 2), gate.reshape(B, L, H, dv)], -1)).reshape(B, L, -1)
+        tol = 1e-5 if dt == torch.float32 else 2e-2
+        assert (y.float() - ref.float()).abs().max().item() <= tol * max(1.0, ref.abs().max().item())
+        x = torch.randn(5, 7, 2 * 256, generator=g).to(DEV, dt)
+        ref = x[..., :256] * F.silu(x[..., 256:])
+        assert (swiglu(x).float() - ref.float()).abs().max().item() <= tol * max(1.0, ref.abs().max().item())
+        a, b, p = (torch.randn(3, 9, 768, generator=g).to(DEV, dt) for _ in range(3))
+        f, p2 = add_fold(a, b, p)
+        assert torch.equal(f, a + b) and torch.equal(p2, p + (a + b))
+        f1, none = add_fold(a, b)
+        assert torch.equal(f1, a + b) and none is None
