@@ -9,6 +9,11 @@
 //   swiglu_kernel          y = T(x[:, :I] * T(SiLU(x[:, I:])))   (motif/ops/swiglu.py:252-253)
 //   add_fold_kernel        f = T(a + b); p_out = T(p + f)        (decoder f_h = attn + mlp and the
 //                          block's running sum, motif/block/decoder.py:208-213)
+//   gdn_gates_kernel       beta = T(sigmoid(b)), g = T(-T(exp(A_log)) * T(softplus(T(a + dt_bias))))
+//                          per (token, head), written as [B, H, L] (motif/block/attention/
+//                          gdn_attn.py:193-195; softplus threshold 20)
+//   mul_sigmoid_kernel     y = T(x * T(sigmoid(g)))             (Chord output gate,
+//                          motif/block/attention/chord_attn.py:254, :313)
 #include "capi_internal.h"
 #include "common.h"
 
@@ -159,6 +164,49 @@ __global__ void __launch_bounds__(256) add_fold_kernel(EwArgs a) {
   }
 }
 
+template <typename T> __device__ __forceinline__ float rnd(float v) { return v; }
+template <> __device__ __forceinline__ float rnd<bf16_t>(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+struct GateArgs {
+  const void *a, *b; int64_t a_sb, a_st, b_sb, b_st;   // [B, L, H] columns (unit head stride)
+  const void *a_log, *dt_bias;                         // [H]
+  void *beta, *g; int64_t o_sb, o_sh, o_st;            // [B, H, L]
+  int B, L, H;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(256) gdn_gates_kernel(GateArgs p) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= static_cast<int64_t>(p.B) * p.L * p.H) return;
+  const int h = static_cast<int>(i % p.H);
+  const int64_t bt = i / p.H;
+  const int t = static_cast<int>(bt % p.L), b = static_cast<int>(bt / p.L);
+  const float av = ld(static_cast<const T *>(p.a) + b * p.a_sb + int64_t(t) * p.a_st + h);
+  const float bv = ld(static_cast<const T *>(p.b) + b * p.b_sb + int64_t(t) * p.b_st + h);
+  const float x = rnd<T>(av + ld(static_cast<const T *>(p.dt_bias) + h));
+  const float sp = rnd<T>(x > 20.f ? x : log1pf(expf(x)));
+  const float A = rnd<T>(expf(ld(static_cast<const T *>(p.a_log) + h)));
+  const int64_t o = b * p.o_sb + h * p.o_sh + int64_t(t) * p.o_st;
+  st(static_cast<T *>(p.beta) + o, 1.f / (1.f + expf(-bv)));
+  st(static_cast<T *>(p.g) + o, -A * sp);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) mul_sigmoid_kernel(EwArgs a) {
+  constexpr int E = V16<T>::N;
+  const int cpr = a.N / E;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= static_cast<int64_t>(a.M) * cpr) return;
+  const int64_t m = i / cpr;
+  const int c = static_cast<int>(i - m * cpr) * E;
+  float x[E], g[E];
+  V16<T>::unpack(ld16(static_cast<const T *>(a.x) + m * a.x_rs + c), x);
+  V16<T>::unpack(ld16(static_cast<const T *>(a.x2) + m * a.x2_rs + c), g);
+#pragma unroll
+  for (int e = 0; e < E; ++e) x[e] = x[e] * V16<T>::round(1.f / (1.f + expf(-g[e])));
+  st16(static_cast<T *>(a.y) + m * a.y_rs + c, V16<T>::pack(x));
+}
+
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
@@ -221,4 +269,41 @@ extern "C" int motif_add_fold(const void *a_, int64_t a_rs, const void *b_, int6
   if (dtype == MOTIF_BF16) add_fold_kernel<bf16_t><<<grid, block, 0, s>>>(a);
   else add_fold_kernel<float><<<grid, block, 0, s>>>(a);
   return check_launch("add_fold_kernel");
+}
+
+extern "C" int motif_gdn_gates(const void *a, int64_t a_sb, int64_t a_st, const void *b, int64_t b_sb,
+                               int64_t b_st, const void *a_log, const void *dt_bias, void *beta, void *g,
+                               int64_t o_sb, int64_t o_sh, int64_t o_st, int B, int L, int H, int dtype,
+                               void *stream) {
+  using namespace motif;
+  if (B < 0 || L < 0 || H <= 0) return set_error(MOTIF_ERR_INVALID, "gdn_gates: bad size");
+  if (!a || !b || !a_log || !dt_bias || !beta || !g) return set_error(MOTIF_ERR_INVALID, "gdn_gates: NULL pointer");
+  if (dtype != MOTIF_F32 && dtype != MOTIF_BF16) return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_gates: dtype");
+  if (B == 0 || L == 0) return MOTIF_OK;
+  GateArgs p{a, b, a_sb, a_st, b_sb, b_st, a_log, dt_bias, beta, g, o_sb, o_sh, o_st, B, L, H};
+  const int64_t n = static_cast<int64_t>(B) * L * H;
+  const dim3 grid(static_cast<unsigned>((n + 255) / 256)), block(256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == MOTIF_BF16) gdn_gates_kernel<bf16_t><<<grid, block, 0, s>>>(p);
+  else gdn_gates_kernel<float><<<grid, block, 0, s>>>(p);
+  return check_launch("gdn_gates_kernel");
+}
+
+extern "C" int motif_mul_sigmoid(const void *x, int64_t x_rs, const void *g, int64_t g_rs, void *y, int64_t y_rs,
+                                 int M, int N, int dtype, void *stream) {
+  using namespace motif;
+  if (M < 0 || N <= 0) return set_error(MOTIF_ERR_INVALID, "mul_sigmoid: bad size");
+  if (!x || !g || !y) return set_error(MOTIF_ERR_INVALID, "mul_sigmoid: NULL pointer");
+  if (dtype != MOTIF_F32 && dtype != MOTIF_BF16) return set_error(MOTIF_ERR_UNSUPPORTED, "mul_sigmoid: dtype");
+  const int vec = dtype == MOTIF_BF16 ? 8 : 4;
+  if (!aligned16(x) || !aligned16(g) || !aligned16(y) || ((x_rs | g_rs | y_rs | N) % vec))
+    return set_error(MOTIF_ERR_UNSUPPORTED, "mul_sigmoid: rows must be 16-byte aligned");
+  if (M == 0) return MOTIF_OK;
+  EwArgs a{x, x_rs, g, g_rs, nullptr, 0, y, y_rs, nullptr, 0, M, N};
+  const int64_t n = static_cast<int64_t>(M) * (N / vec);
+  const dim3 grid(static_cast<unsigned>((n + 255) / 256)), block(256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == MOTIF_BF16) mul_sigmoid_kernel<bf16_t><<<grid, block, 0, s>>>(a);
+  else mul_sigmoid_kernel<float><<<grid, block, 0, s>>>(a);
+  return check_launch("mul_sigmoid_kernel");
 }

@@ -17,6 +17,7 @@ from motif.block.attention.base import AttentionOutput, BasicAttention
 from motif.model.cache import KVLayerCache, StaticKVLayerCache
 from motif.ops import RMSNorm, apply_chord_attention, apply_chord_attention_varlen
 from motif.ops import _lib
+from motif.ops.epilogue import mul_sigmoid, usable
 from motif.ops.linear_rows import cat_weights, linear_rows, project, rows_eligible
 
 _HALF_DTYPES = (torch.float16, torch.bfloat16)
@@ -232,7 +233,10 @@ class ChordAttention(BasicAttention):
         decode-sized bf16 inputs.'''
         if self.o_proj.bias is None and rows_eligible(out, self.o_proj.weight):
             return linear_rows(out, self.o_proj.weight, 'gate', aux=g_pre)
-        return self.o_proj(out) * torch.sigmoid(g_pre)
+        o = self.o_proj(out)
+        if o.shape == g_pre.shape and usable(o, g_pre):
+            return mul_sigmoid(o, g_pre)
+        return o * torch.sigmoid(g_pre)
 
     def forward_varlen(self, hidden_states: torch.Tensor, cu_seqlens: torch.Tensor) -> AttentionOutput:
         '''Packed sequences (B == 1): each sequence attends causally within itself

@@ -26,7 +26,7 @@ import torch.nn.functional as F
 
 from motif.block.attention.base import AttentionOutput, BasicAttention
 from motif.model.cache import GatedDeltaAttentionLayerCache
-from motif.ops.epilogue import gated_rms_norm_heads, usable
+from motif.ops.epilogue import gated_rms_norm_heads, gdn_gates, usable
 from motif.ops import (
     GatedRMSNorm,
     cat_weights,
@@ -111,6 +111,9 @@ class GatedDeltaAttention(BasicAttention):
         return proj, tuple(proj[..., s:e] for s, e in zip(offs, ends))
 
     def _gates(self, a, b):
+        if a.is_cuda and a.dtype in (torch.bfloat16, torch.float32) and b.dtype == a.dtype and not (
+                torch.is_grad_enabled() and (self.A_log.requires_grad or a.requires_grad)):
+            return gdn_gates(a, b, self.A_log, self.dt_bias)
         beta = torch.sigmoid(b).transpose(1, 2)
         g = -self.A_log.exp() * F.softplus(a + self.dt_bias)
         return beta, g.transpose(1, 2)

@@ -41,6 +41,9 @@ _SIGNATURES = {
         _I32),
     'motif_gated_rms_norm': (
         [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _F32, _P, _I64, _I64] + [_I32] * 5 + [_P], _I32),
+    'motif_gdn_gates': (
+        [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _P, _I64, _I64, _I64] + [_I32] * 4 + [_P], _I32),
+    'motif_mul_sigmoid': ([_P, _I64, _P, _I64, _P, _I64, _I32, _I32, _I32, _P], _I32),
     'motif_swiglu': ([_P, _I64, _P, _I64, _I32, _I32, _I32, _P], _I32),
     'motif_add_fold': ([_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I32, _I32, _I32, _P], _I32),
     'motif_attn_res_read_norms': (

@@ -76,3 +76,32 @@ def add_fold(a, b, p=None):
                                    _lib.stream_ptr(a.device))
     _lib.check(rc, 'motif_add_fold')
     return f, po
+
+
+def gdn_gates(a, b, a_log, dt_bias):
+    '''(beta, g) [B, H, L] from the a / b projections [B, L, H] (column views allowed):
+    beta = sigmoid(b), g = -exp(A_log) * softplus(a + dt_bias) -- one kernel instead of
+    the reference's six elementwise ops (motif/block/attention/gdn_attn.py:193-195).'''
+    B, L, H = a.shape
+    dt = a.dtype
+    al = a_log.detach().to(dt).contiguous()
+    db = dt_bias.detach().to(dt).contiguous()
+    beta = torch.empty(B, H, L, dtype=dt, device=a.device)
+    g = torch.empty(B, H, L, dtype=dt, device=a.device)
+    rc = _lib.lib().motif_gdn_gates(a.data_ptr(), a.stride(0), a.stride(1), b.data_ptr(), b.stride(0), b.stride(1),
+                                    al.data_ptr(), db.data_ptr(), beta.data_ptr(), g.data_ptr(),
+                                    beta.stride(0), beta.stride(1), beta.stride(2), B, L, H,
+                                    _lib.dtype_code(dt), _lib.stream_ptr(a.device))
+    _lib.check(rc, 'motif_gdn_gates')
+    return beta, g
+
+
+def mul_sigmoid(x, g):
+    '''x * sigmoid(g) (both [..., N], row-major views).'''
+    N = x.shape[-1]
+    x2, g2 = x.reshape(-1, N), g.reshape(-1, N)
+    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    rc = _lib.lib().motif_mul_sigmoid(x2.data_ptr(), x2.stride(0), g2.data_ptr(), g2.stride(0), y.data_ptr(), N,
+                                      x2.shape[0], N, _lib.dtype_code(x.dtype), _lib.stream_ptr(x.device))
+    _lib.check(rc, 'motif_mul_sigmoid')
+    return y

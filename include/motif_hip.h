@@ -279,6 +279,24 @@ int motif_swiglu(const void *x, int64_t x_rs, void *y, int64_t y_rs, int M, int 
 int motif_add_fold(const void *a, int64_t a_rs, const void *b, int64_t b_rs, const void *p, int64_t p_rs,
                    void *f, int64_t f_rs, void *p_out, int64_t po_rs, int M, int N, int dtype, void *stream);
 
+/*
+ * GDN gates in one pass: beta = sigmoid(b), g = -exp(A_log) * softplus(a + dt_bias)
+ * (softplus threshold 20), each step rounded to T as the reference's separate ops
+ * round (motif/block/attention/gdn_attn.py:193-195).  a, b [B, L, H] (strides a_sb,
+ * a_st / b_sb, b_st; unit head stride); a_log, dt_bias [H]; beta, g [B, H, L] with
+ * strides o_sb, o_sh, o_st.
+ */
+int motif_gdn_gates(const void *a, int64_t a_sb, int64_t a_st, const void *b, int64_t b_sb, int64_t b_st,
+                    const void *a_log, const void *dt_bias, void *beta, void *g, int64_t o_sb, int64_t o_sh,
+                    int64_t o_st, int B, int L, int H, int dtype, void *stream);
+
+/*
+ * y = x * sigmoid(g) (sigmoid rounded to T), [M, N] row-major: the Chord output gate
+ * o_proj(out) * G (motif/block/attention/chord_attn.py:254, :313).
+ */
+int motif_mul_sigmoid(const void *x, int64_t x_rs, const void *g, int64_t g_rs, void *y, int64_t y_rs,
+                      int M, int N, int dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

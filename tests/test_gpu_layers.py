@@ -256,3 +256,28 @@ def test_elementwise_stage_kernels_match_torch():
         assert torch.equal(f, a + b) and torch.equal(p2, p + (a + b))
         f1, none = add_fold(a, b)
         assert torch.equal(f1, a + b) and none is None
+
+
+@torch.no_grad()
+def test_gate_kernels_match_torch():
+    """GDN gates and the Chord sigmoid gate against the torch formulas (same roundings)."""
+    import torch.nn.functional as F
+    from motif.ops.epilogue import gdn_gates, mul_sigmoid
+    g = torch.Generator().manual_seed(4)
+    for dt in (torch.float32, torch.bfloat16):
+        B, L, H = 2, 33, 12
+        proj = (torch.randn(B, L, 40, generator=g) * 2).to(DEV, dt)
+        a, b = proj[..., 3:3 + H], proj[..., 20:20 + H]
+        A_log = torch.empty(H).uniform_(1, 16, generator=g).log().to(DEV, dt)
+        dt_bias = (torch.rand(H, generator=g) * 4 - 2).to(DEV, dt)
+        a[0, 0, 0] = 30.0   # softplus threshold branch
+        beta, gg = gdn_gates(a, b, A_log, dt_bias)
+        ref_b = torch.sigmoid(b).transpose(1, 2)
+        ref_g = (-A_log.exp() * F.softplus(a + dt_bias)).transpose(1, 2)
+        tol = 1e-5 if dt == torch.float32 else 1e-2
+        assert (beta.float() - ref_b.float()).abs().max().item() <= tol
+        assert (gg.float() - ref_g.float()).abs().max().item() <= tol * max(1.0, ref_g.abs().max().item())
+        x = torch.randn(3, 5, 64, generator=g).to(DEV, dt)
+        gp = torch.randn(3, 5, 64, generator=g).to(DEV, dt)
+        ref = x * torch.sigmoid(gp)
+        assert (mul_sigmoid(x, gp).float() - ref.float()).abs().max().item() <= tol * 4
