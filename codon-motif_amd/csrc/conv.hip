@@ -26,7 +26,7 @@ struct ConvArgs {
 };
 
 constexpr int kConvStep = 16;  // timesteps per batch of loads (scalar kernel)
-constexpr int kVecStep = 8;    // timesteps per thread (vector kernel)
+constexpr int kVecStep = 4;    // timesteps per thread (vector kernel)
 
 template <typename T, int K, int HD>
 __global__ void __launch_bounds__(256) short_conv_silu_kernel(ConvArgs a) {
@@ -132,7 +132,8 @@ __global__ void __launch_bounds__(256) short_conv_silu_kernel(ConvArgs a) {
 }
 
 // Vector form for row-contiguous 16-byte-aligned channels: one thread owns E = 16 /
-// sizeof(T) consecutive channels over 8 timesteps (16-byte loads and stores).  With
+// sizeof(T) consecutive channels over kVecStep timesteps (16-byte loads and stores;
+// few timesteps per thread keep enough waves in flight to cover the load latency).  With
 // HD > 0 a head is HD / E consecutive lanes.  Same arithmetic as the scalar kernel.
 template <typename T> struct Vec16;
 template <> struct Vec16<bf16_t> {
@@ -198,13 +199,31 @@ __global__ void __launch_bounds__(256) short_conv_silu_vec_kernel(ConvArgs a) {
 #pragma unroll
   for (int i = 0; i < K - 1 + kVecStep; ++i)
     raw[i] = buf_ld16(xbuf, static_cast<uint32_t>(((t_lo - (K - 1) + i) * a.x_st + d0) * sizeof(T)));
+  // The E channels' taps (E * K contiguous values = K 16-byte pieces) and their
+  // cached tails (K - 1 pieces), as 16-byte loads.
   float wr[E][K], tv[E][K - 1];
+  {
+    const T *wp = static_cast<const T *>(a.w) + d0 * K;
+    float wf[E * K];
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
+    for (int j = 0; j < K; ++j) Vec16<T>::unpack(*reinterpret_cast<const uint4 *>(wp + j * E), wf + j * E);
 #pragma unroll
-    for (int r = 0; r < K; ++r) wr[e][r] = ld(static_cast<const T *>(a.w) + (d0 + e) * K + r);
+    for (int e = 0; e < E; ++e)
 #pragma unroll
-    for (int u = 0; u < K - 1; ++u) tv[e][u] = has_tail ? ld(tail0 + e * (K - 1) + u) : 0.f;
+      for (int r = 0; r < K; ++r) wr[e][r] = wf[e * K + r];
+    float tf[E * (K - 1)];
+#pragma unroll
+    for (int j = 0; j < K - 1; ++j) {
+      if (has_tail) Vec16<T>::unpack(*reinterpret_cast<const uint4 *>(tail0 + j * E), tf + j * E);
+      else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) tf[j * E + e] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+#pragma unroll
+      for (int u = 0; u < K - 1; ++u) tv[e][u] = tf[e * (K - 1) + u];
   }
   __builtin_amdgcn_sched_barrier(0);  // keep the loads above as one batch
 
@@ -310,7 +329,8 @@ static int launch_conv(const ConvArgs &a, int K, int nseq, int max_len, int head
   constexpr int E = Vec16<T>::E;
   const bool aliased = a.tail_out != nullptr && a.tail_out == a.tail_in;
   const bool vec = !aliased && a.D % E == 0 && ((a.x_sb | a.x_st | a.y_sb | a.y_st) % E) == 0 &&
-                   ((reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.y)) & 15) == 0 &&
+                   ((reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.y) |
+                     reinterpret_cast<uintptr_t>(a.w) | reinterpret_cast<uintptr_t>(a.tail_in)) & 15) == 0 &&
                    head_dim % E == 0;
   if (vec) {
     switch (head_dim) {
