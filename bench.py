@@ -304,6 +304,9 @@ def main():
     dev = torch.device('cuda', 0)
     torch.cuda.set_device(dev)
     torch.backends.cuda.matmul.allow_tf32 = False
+    from motif import tuning
+    tuned = tuning.enable()
+    log(f'[bench] library GEMM tuning results loaded: {tuned}')
 
     if args.kernels_only:
         with torch.no_grad():
