@@ -64,7 +64,13 @@ __device__ __forceinline__ int w_row(int n0, int t, int c, int nout) {
   return n0 + 16 * t + c;
 }
 
-template <int MT, int NT, int KS, int EPI>
+// Per k-step a lane holds P 16-byte pieces of its row: P = 2 covers 64 k per step with
+// the lane's two pieces adjacent (k = 16 kq .. 16 kq + 15 of the step), so one load
+// instruction spans whole 128-byte lines (every 32-byte sector of a row's line) and the
+// L1 asks L2 for full lines -- half the requests of P = 1 (16 rows x 64 bytes per
+// instruction).  MFMA j of the step sums k = 16 kq + 8 j .. +7 over the lane groups
+// kq, the same set in A and B, so the products are unchanged.
+template <int MT, int NT, int KS, int EPI, int P>
 __global__ void __launch_bounds__(512) linear_rows_kernel(LinArgs a) {
   // The wave index in an SGPR: the k-range below is then wave-uniform to the compiler
   // (scalar branches, step offsets in the loads' scalar offset operand).
@@ -89,12 +95,12 @@ __global__ void __launch_bounds__(512) linear_rows_kernel(LinArgs a) {
   uint32_t xo[MT], wo[NT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
-    xo[mt] = static_cast<uint32_t>((min(mt * 16 + r16, rows - 1) * a.x_rs + kq * 8) * 2);
+    xo[mt] = static_cast<uint32_t>((min(mt * 16 + r16, rows - 1) * a.x_rs + kq * 8 * P) * 2);
 #pragma unroll
   for (int t = 0; t < NT; ++t)
-    wo[t] = static_cast<uint32_t>((min(w_row<NT, EPI>(n0, t, r16, nout), a.N - 1) * a.w_rs + kq * 8) * 2);
+    wo[t] = static_cast<uint32_t>((min(w_row<NT, EPI>(n0, t, r16, nout), a.N - 1) * a.w_rs + kq * 8 * P) * 2);
 
-  const int nsteps = a.K / 32;
+  const int nsteps = a.K / (32 * P);
   const int s0 = wv * nsteps / kWaves, s1 = (wv + 1) * nsteps / kWaves;
 
   f32x4 acc[MT][NT];
@@ -103,20 +109,23 @@ __global__ void __launch_bounds__(512) linear_rows_kernel(LinArgs a) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // KS k-steps per round trip (K > 8 * 8 * 32 loops).  Steps past the wave's range
+  // KS k-steps per round trip (longer K loops).  Steps past the wave's range
   // read at an offset of 2^31 or more, which the range check turns into zeros (every
   // operand offset is below 2^31), so every MFMA runs unconditionally: a guard around
   // the MFMAs would let the compiler sink each step's loads into it and pay one
   // memory round trip per step.
   for (int s = s0; s < s1; s += KS) {
-    bf16x8 A[KS][MT], B[KS][NT];
+    bf16x8 A[KS][P][MT], B[KS][P][NT];
 #pragma unroll
     for (int c = 0; c < KS; ++c) {
-      const uint32_t soff = s + c < s1 ? static_cast<uint32_t>(s + c) * 64u : 0x80000000u;
+      const uint32_t soff = s + c < s1 ? static_cast<uint32_t>(s + c) * (64u * P) : 0x80000000u;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) A[c][mt] = ld8(xb, xo[mt], soff);
+      for (int j = 0; j < P; ++j) {
 #pragma unroll
-      for (int t = 0; t < NT; ++t) B[c][t] = ld8(wb, wo[t], soff);
+        for (int mt = 0; mt < MT; ++mt) A[c][j][mt] = ld8(xb, xo[mt] + 16 * j, soff);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) B[c][j][t] = ld8(wb, wo[t] + 16 * j, soff);
+      }
     }
     // keep the whole batch of loads ahead of the MFMAs (the scheduler would otherwise
     // interleave them to save registers, serialising the round trips)
@@ -124,9 +133,11 @@ __global__ void __launch_bounds__(512) linear_rows_kernel(LinArgs a) {
 #pragma unroll
     for (int c = 0; c < KS; ++c)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      for (int j = 0; j < P; ++j)
 #pragma unroll
-        for (int t = 0; t < NT; ++t) acc[mt][t] = mma(A[c][mt], B[c][t], acc[mt][t]);
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int t = 0; t < NT; ++t) acc[mt][t] = mma(A[c][j][mt], B[c][j][t], acc[mt][t]);
   }
 
   // Cross-wave sum in LDS: red[wave][tile][lane] (16 bytes per lane).
@@ -171,6 +182,22 @@ __global__ void __launch_bounds__(512) linear_rows_kernel(LinArgs a) {
   }
 }
 
+template <int MT, int NT, int EPI, int P>
+int launch_tile_p(const LinArgs &a, const dim3 &grid, hipStream_t s) {
+  const dim3 block(64 * kWaves);
+  const int per_wave = (a.K / (32 * P) + kWaves - 1) / kWaves;
+  if (per_wave <= 1) linear_rows_kernel<MT, NT, 1, EPI, P><<<grid, block, 0, s>>>(a);
+  else if (per_wave <= 2) linear_rows_kernel<MT, NT, 2, EPI, P><<<grid, block, 0, s>>>(a);
+  else if constexpr (P == 2) {
+    linear_rows_kernel<MT, NT, 4, EPI, P><<<grid, block, 0, s>>>(a);  // 64-k steps: 4 per round trip
+  } else {
+    if (per_wave <= 4) linear_rows_kernel<MT, NT, 4, EPI, P><<<grid, block, 0, s>>>(a);
+    else if (per_wave <= 6) linear_rows_kernel<MT, NT, 6, EPI, P><<<grid, block, 0, s>>>(a);
+    else linear_rows_kernel<MT, NT, kMaxSteps, EPI, P><<<grid, block, 0, s>>>(a);
+  }
+  return check_launch("linear_rows_kernel");
+}
+
 template <int MT, int NT, int EPI>
 int launch_tile(LinArgs a, hipStream_t s) {
   constexpr int kCols = EPI == EPI_SWIGLU ? 8 * NT : 16 * NT;
@@ -178,14 +205,9 @@ int launch_tile(LinArgs a, hipStream_t s) {
   a.ntiles = (nout + kCols - 1) / kCols;
   a.mblocks = (a.M + 16 * MT - 1) / (16 * MT);
   const int groups = (a.ntiles + kXcds - 1) / kXcds;
-  const dim3 grid(groups * kXcds * a.mblocks), block(64 * kWaves);
-  const int per_wave = (a.K / 32 + kWaves - 1) / kWaves;
-  if (per_wave <= 1) linear_rows_kernel<MT, NT, 1, EPI><<<grid, block, 0, s>>>(a);
-  else if (per_wave <= 2) linear_rows_kernel<MT, NT, 2, EPI><<<grid, block, 0, s>>>(a);
-  else if (per_wave <= 4) linear_rows_kernel<MT, NT, 4, EPI><<<grid, block, 0, s>>>(a);
-  else if (per_wave <= 6) linear_rows_kernel<MT, NT, 6, EPI><<<grid, block, 0, s>>>(a);
-  else linear_rows_kernel<MT, NT, kMaxSteps, EPI><<<grid, block, 0, s>>>(a);
-  return check_launch("linear_rows_kernel");
+  const dim3 grid(groups * kXcds * a.mblocks);
+  // 64-k steps with full-line loads when K allows it
+  return a.K % 64 == 0 ? launch_tile_p<MT, NT, EPI, 2>(a, grid, s) : launch_tile_p<MT, NT, EPI, 1>(a, grid, s);
 }
 
 // Tile choice: rows per tile 16 MT (MT = 4, 2, 1) and W tiles NT (2, or 1 when the
