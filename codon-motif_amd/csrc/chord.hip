@@ -578,6 +578,204 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a, const fl
   }
 }
 
+// bf16 decode on MFMA (up to 16 (query, head) rows of one kv head per workgroup).
+// Per wave step of 32 keys (two 16-key tiles):
+//   S^T = K Q^T on v_mfma_f32_16x16x32_bf16 -- A = K (lane: key l % 16, features
+//   16 g + {0..7} then + {8..15} for the two k-steps, g = l / 16: two adjacent 16-byte
+//   loads covering each key row's 128-byte line), B = Q^T (lane: query row l % 16, the
+//   same features).  The accumulator gives lane l the scores of row l % 16 for keys
+//   4 g + i, so the softmax statistics of a row live in the 4 lanes l % 16 + 16 g.
+//   O^T += V^T P^T -- B = P^T straight from the scores (slots 0..3: tile 0 keys 4 g + i,
+//   slots 4..7: tile 1 keys 16 + 4 g + i), A = V^T with the same key slots, gathered
+//   from the wave's V tile in LDS (V rows are loaded with 16-byte coalesced reads and
+//   written row-major).  O^T's accumulator gives lane l features 16 ft + 4 g + i of
+//   row l % 16, so no cross-lane sum is needed for O.
+// The next step's K / V / bias loads are issued before the current step's arithmetic.
+constexpr int kMfmaRows = 16;
+constexpr int kVRow = 72;  // LDS V row stride (bf16): 144 bytes, conflict-free gathers
+
+__global__ void __launch_bounds__(256) chord_decode_mfma_kernel(ChordArgs a, const float *tab, int tab_n) {
+  // wave index in an SGPR: the key loop below is then scalar (MFMAs must not sit
+  // under a lane-mask branch, as they ignore EXEC)
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c16 = lane & 15, g = lane >> 4;
+  const int split = blockIdx.x, kvh = blockIdx.y;
+  const int b = blockIdx.z / a.nqc, qc = blockIdx.z % a.nqc;
+  const int group = a.H / a.Hkv;
+  const int total_rows = a.L * group;
+  const bf16_t *qg = static_cast<const bf16_t *>(a.q);
+
+  // this lane's query row (column of the B / C operands)
+  const int gr = qc * kMfmaRows + c16;
+  const bool row_ok = gr < total_rows;
+  const int head = kvh * group + (row_ok ? gr % group : 0);
+  const int qi = row_ok ? gr / group : 0;
+  bf16x8 qb[2];
+  {
+    const bf16_t *qr = qg + b * a.q_sb + head * a.q_sh + int64_t(qi) * a.q_st + 16 * g;
+    const uint4 u0 = *reinterpret_cast<const uint4 *>(qr), u1 = *reinterpret_cast<const uint4 *>(qr + 8);
+    const uint4 z{0, 0, 0, 0};
+    qb[0] = __builtin_bit_cast(bf16x8, row_ok ? u0 : z);
+    qb[1] = __builtin_bit_cast(bf16x8, row_ok ? u1 : z);
+  }
+  const float mul = row_ok ? a.ssmax[head] * a.log_n[b * a.ln_sb + int64_t(qi) * a.ln_st] : 0.f;
+  const float c_qk = mul * a.scale * kLog2e, c_b = mul;
+  const int qabs = row_ok ? a.q_start + qi : -1;
+  const buf_t tb = make_buf(tab + static_cast<size_t>(head) * tab_n, static_cast<uint32_t>(tab_n) * 4u);
+
+  const int kv_len = min(a.S, a.q_start + a.L);
+  const int per = ((kv_len + a.splits - 1) / a.splits + kBN - 1) / kBN * kBN;
+  const int i_last = min(a.L - 1, (qc * kMfmaRows + kMfmaRows - 1) / group);
+  const int k_lo = split * per;
+  const int k_hi = min(min(kv_len, k_lo + per), a.q_start + i_last + 1);
+
+  const bf16_t *kp = static_cast<const bf16_t *>(a.k) + b * a.k_sb + kvh * a.k_sh;
+  const bf16_t *vp = static_cast<const bf16_t *>(a.v) + b * a.v_sb + kvh * a.v_sh;
+  // rows past k_hi read as zeros
+  const buf_t kbuf = make_buf(kp, k_hi > 0 ? static_cast<uint32_t>(((k_hi - 1) * a.k_st + kD) * 2) : 0u);
+  const buf_t vbuf = make_buf(vp, k_hi > 0 ? static_cast<uint32_t>(((k_hi - 1) * a.v_st + kD) * 2) : 0u);
+
+  __shared__ __attribute__((aligned(16))) bf16_t sV[4][32 * kVRow];
+  bf16_t *myV = sV[w];
+
+  struct Stage {
+    uint4 k[2][2];   // [tile][piece]
+    uint4 v[4];      // V rows 8 r + lane / 8, features 8 (lane % 8)
+    uint4 bias[2];   // [tile] entries delta = qabs - kb - 3 .. qabs - kb
+  };
+  auto load_stage = [&](int n0, Stage &st) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const uint32_t off = static_cast<uint32_t>(((n0 + 16 * t + c16) * a.k_st + 16 * g) * 2);
+      st.k[t][0] = buf_ld16(kbuf, off);
+      st.k[t][1] = buf_ld16(kbuf, off + 16);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      st.v[r] = buf_ld16(vbuf, static_cast<uint32_t>(((n0 + 8 * r + (lane >> 3)) * a.v_st + 8 * (lane & 7)) * 2));
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      st.bias[t] = buf_ld16(tb, static_cast<uint32_t>(qabs - (n0 + 16 * t + 4 * g) - 3 + kTabPad) * 4u);
+  };
+
+  float m = -INFINITY, lsum = 0.f;
+  f32x4 o[4];
+#pragma unroll
+  for (int ft = 0; ft < 4; ++ft) o[ft] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  int n0 = k_lo + w * 32;
+  Stage cur;
+  if (n0 < k_hi) load_stage(n0, cur);
+  for (; n0 < k_hi; n0 += 4 * 32) {
+    Stage nxt;
+    load_stage(n0 + 4 * 32, nxt);
+    __builtin_amdgcn_sched_barrier(0);
+    // V rows of this step into the wave's LDS tile (row-major, padded rows)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      *reinterpret_cast<uint4 *>(myV + (8 * r + (lane >> 3)) * kVRow + 8 * (lane & 7)) = cur.v[r];
+    // scores
+    float sc[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+      sacc = mma16(__builtin_bit_cast(bf16x8, cur.k[t][0]), qb[0], sacc);
+      sacc = mma16(__builtin_bit_cast(bf16x8, cur.k[t][1]), qb[1], sacc);
+      const float bt[4] = {__uint_as_float(cur.bias[t].w), __uint_as_float(cur.bias[t].z),
+                           __uint_as_float(cur.bias[t].y), __uint_as_float(cur.bias[t].x)};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = n0 + 16 * t + 4 * g + i;
+        const bool ok = key < k_hi && key <= qabs;
+        sc[t][i] = ok ? fmaf(sacc[i], c_qk, c_b * bt[i]) : -INFINITY;
+      }
+    }
+    // row max over the 32 keys (4 lanes share a row)
+    float mx = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                     fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float resc = m == -INFINITY ? 0.f : fast_exp2(m - m_use);
+    m = m_new;
+    float ps = 0.f;
+    bf16_t pb[8];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float pv = sc[t][i] == -INFINITY ? 0.f : fast_exp2(sc[t][i] - m_use);
+        ps += pv;
+        pb[4 * t + i] = f32_to_bf16(pv);
+      }
+    lsum = lsum * resc + ps;
+    bf16x8 pB;
+    {
+      uint4 u;
+      u.x = pb[0] | (static_cast<uint32_t>(pb[1]) << 16);
+      u.y = pb[2] | (static_cast<uint32_t>(pb[3]) << 16);
+      u.z = pb[4] | (static_cast<uint32_t>(pb[5]) << 16);
+      u.w = pb[6] | (static_cast<uint32_t>(pb[7]) << 16);
+      pB = __builtin_bit_cast(bf16x8, u);
+    }
+    // O^T += V^T P^T per 16-feature tile
+#pragma unroll
+    for (int ft = 0; ft < 4; ++ft) {
+      const int e = 16 * ft + c16;
+      uint32_t wv[4];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const bf16_t *col = myV + (16 * h + 4 * g) * kVRow + e;
+        wv[2 * h] = col[0] | (static_cast<uint32_t>(col[kVRow]) << 16);
+        wv[2 * h + 1] = col[2 * kVRow] | (static_cast<uint32_t>(col[3 * kVRow]) << 16);
+      }
+      const bf16x8 vA = __builtin_bit_cast(bf16x8, uint4{wv[0], wv[1], wv[2], wv[3]});
+      o[ft] *= resc;
+      o[ft] = mma16(vA, pB, o[ft]);
+    }
+    cur = nxt;
+  }
+
+  // row sum over the 4 lanes of a row
+  lsum += __shfl_xor(lsum, 16, 64);
+  lsum += __shfl_xor(lsum, 32, 64);
+
+  // merge the 4 waves through LDS (reusing the V tiles' space is not needed: small)
+  __shared__ float sm[4][kMfmaRows], sl[4][kMfmaRows], so[4][kMfmaRows][kD + 1];
+  if (g == 0) { sm[w][c16] = m; sl[w][c16] = lsum; }
+#pragma unroll
+  for (int ft = 0; ft < 4; ++ft)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) so[w][c16][16 * ft + 4 * g + i] = o[ft][i];
+  __syncthreads();
+  for (int e = tid; e < kMfmaRows * kD; e += 256) {
+    const int r = e / kD, d = e % kD;
+    const int grr = qc * kMfmaRows + r;
+    if (grr >= total_rows) continue;
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, sm[ww][r]);
+    const float Mu = M == -INFINITY ? 0.f : M;
+    float ov = 0.f, Ls = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      const float f = fast_exp2(sm[ww][r] - Mu);
+      ov += so[ww][r][d] * f;
+      Ls += sl[ww][r] * f;
+    }
+    if (a.splits == 1) {
+      const int hh = kvh * group + grr % group, ii = grr / group;
+      st(static_cast<bf16_t *>(a.out) + b * a.o_sb + hh * a.o_sh + int64_t(ii) * a.o_st + d, ov / fmaxf(Ls, 1e-20f));
+      if (a.lse && d == 0) a.lse[(static_cast<size_t>(b) * a.H + hh) * a.L + ii] = M + fast_log2(Ls);
+    } else {
+      float *pp = a.part + ((((static_cast<size_t>(b) * a.Hkv + kvh) * a.splits + split) * total_rows + grr) * (kD + 2));
+      pp[d] = ov;
+      if (d == 0) { pp[kD] = M; pp[kD + 1] = Ls; }
+    }
+  }
+}
+
 template <typename T>
 __global__ void __launch_bounds__(64) chord_merge_kernel(ChordArgs a) {
   const int gr = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, d = threadIdx.x;
@@ -707,11 +905,13 @@ extern "C" int motif_chord_fwd(
 
   if (dtype == MOTIF_F32 || use_decode(H, Hkv, L, packed)) {
     if (S == 0) return set_error(MOTIF_ERR_INVALID, "chord_fwd: empty key cache");
+    const bool mfma = dtype == MOTIF_BF16;  // bf16 decode shapes: the MFMA kernel
     int R = 8;
     if (rows <= 8) {
       R = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
       a.splits = decode_splits(B, Hkv, S);
     }
+    if (mfma) R = kMfmaRows;
     a.nqc = (rows + R - 1) / R;
     const size_t tb = table_bytes(H, S);
     const size_t need = tb + (a.splits > 1 ? static_cast<size_t>(B) * Hkv * a.splits * rows * (D + 2) * sizeof(float) : 0);
@@ -723,7 +923,7 @@ extern "C" int motif_chord_fwd(
     chord_bias_table_kernel<<<dim3((tn + 255) / 256, H), dim3(256), 0, s>>>(a, tab, tn);
     int rc = check_launch("chord_bias_table_kernel");
     if (rc) return rc;
-    if (dtype == MOTIF_BF16) launch_decode<bf16_t>(a, R, tab, tn, s);
+    if (mfma) chord_decode_mfma_kernel<<<dim3(a.splits, Hkv, B * a.nqc), dim3(256), 0, s>>>(a, tab, tn);
     else launch_decode<float>(a, R, tab, tn, s);
     rc = check_launch("chord_decode_kernel");
     if (rc || a.splits == 1) return rc;
