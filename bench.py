@@ -195,7 +195,7 @@ TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'hot_path_ops_hbm_traffic.txt')
 OP_KERNELS = {'gdn_chunk_prefill': ('gdn_prep_mfma', 'gdn_state_scan', 'gdn_chunk_out'),
               'chord_prefill': ('chord_fwd_kernel',),
               'gdn_decode': ('gdn_decode_kernel',),
-              'chord_decode': ('chord_bias_table_kernel', 'chord_decode_kernel', 'chord_merge_kernel')}
+              'chord_decode': ('chord_decode_mfma_kernel', 'chord_merge_kernel')}
 
 
 def measured_traffic(op):

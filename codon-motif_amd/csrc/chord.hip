@@ -590,11 +590,13 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a, const fl
 //   from the wave's V tile in LDS (V rows are loaded with 16-byte coalesced reads and
 //   written row-major).  O^T's accumulator gives lane l features 16 ft + 4 g + i of
 //   row l % 16, so no cross-lane sum is needed for O.
-// The next step's K / V / bias loads are issued before the current step's arithmetic.
+// The GGD bias of each (row, key) is evaluated in registers (one exp2 / log2 pair), so
+// this kernel needs no bias table.  The next step's K / V loads are issued before the
+// current step's arithmetic.
 constexpr int kMfmaRows = 16;
 constexpr int kVRow = 72;  // LDS V row stride (bf16): 144 bytes, conflict-free gathers
 
-__global__ void __launch_bounds__(256) chord_decode_mfma_kernel(ChordArgs a, const float *tab, int tab_n) {
+__global__ void __launch_bounds__(256) chord_decode_mfma_kernel(ChordArgs a) {
   // wave index in an SGPR: the key loop below is then scalar (MFMAs must not sit
   // under a lane-mask branch, as they ignore EXEC)
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -621,7 +623,9 @@ __global__ void __launch_bounds__(256) chord_decode_mfma_kernel(ChordArgs a, con
   const float mul = row_ok ? a.ssmax[head] * a.log_n[b * a.ln_sb + int64_t(qi) * a.ln_st] : 0.f;
   const float c_qk = mul * a.scale * kLog2e, c_b = mul;
   const int qabs = row_ok ? a.q_start + qi : -1;
-  const buf_t tb = make_buf(tab + static_cast<size_t>(head) * tab_n, static_cast<uint32_t>(tab_n) * 4u);
+  // GGD bias of (row, key) evaluated in registers, log2 units (the same function the
+  // bias table holds): no table pass, no bias loads
+  const float g_alpha = a.alpha[head] * kLog2e, g_beta = a.beta[head], g_mu = a.mu[head];
 
   const int kv_len = min(a.S, a.q_start + a.L);
   const int per = ((kv_len + a.splits - 1) / a.splits + kBN - 1) / kBN * kBN;
@@ -641,7 +645,6 @@ __global__ void __launch_bounds__(256) chord_decode_mfma_kernel(ChordArgs a, con
   struct Stage {
     uint4 k[2][2];   // [tile][piece]
     uint4 v[4];      // V rows 8 r + lane / 8, features 8 (lane % 8)
-    uint4 bias[2];   // [tile] entries delta = qabs - kb - 3 .. qabs - kb
   };
   auto load_stage = [&](int n0, Stage &st) {
 #pragma unroll
@@ -653,9 +656,6 @@ __global__ void __launch_bounds__(256) chord_decode_mfma_kernel(ChordArgs a, con
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       st.v[r] = buf_ld16(vbuf, static_cast<uint32_t>(((n0 + 8 * r + (lane >> 3)) * a.v_st + 8 * (lane & 7)) * 2));
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-      st.bias[t] = buf_ld16(tb, static_cast<uint32_t>(qabs - (n0 + 16 * t + 4 * g) - 3 + kTabPad) * 4u);
   };
 
   float m = -INFINITY, lsum = 0.f;
@@ -681,13 +681,12 @@ __global__ void __launch_bounds__(256) chord_decode_mfma_kernel(ChordArgs a, con
       f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
       sacc = mma16(__builtin_bit_cast(bf16x8, cur.k[t][0]), qb[0], sacc);
       sacc = mma16(__builtin_bit_cast(bf16x8, cur.k[t][1]), qb[1], sacc);
-      const float bt[4] = {__uint_as_float(cur.bias[t].w), __uint_as_float(cur.bias[t].z),
-                           __uint_as_float(cur.bias[t].y), __uint_as_float(cur.bias[t].x)};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int key = n0 + 16 * t + 4 * g + i;
         const bool ok = key < k_hi && key <= qabs;
-        sc[t][i] = ok ? fmaf(sacc[i], c_qk, c_b * bt[i]) : -INFINITY;
+        const float bt = ggd_bias(static_cast<float>(key - qabs), g_alpha, g_beta, g_mu, a.eps);
+        sc[t][i] = ok ? fmaf(sacc[i], c_qk, c_b * bt) : -INFINITY;
       }
     }
     // row max over the 32 keys (4 lanes share a row)
@@ -829,7 +828,8 @@ static void launch_decode(const ChordArgs &a, int R, const float *tab, int tab_n
   else chord_decode_kernel<T, 8><<<grid, block, 0, s>>>(a, tab, tab_n);
 }
 
-// Workspace of the vector (decode / fp32) path: the bias table [H][S] fp32, then the
+// Workspace of the decode / fp32 paths: the bias table [H][S + 8] fp32 (read by the
+// fp32 vector kernel; the bf16 MFMA kernel evaluates the bias in registers), then the
 // split partials [B][Hkv][splits][rows][D + 2] fp32.
 static int table_len(int S) { return std::max(S, 1) + kTabPad; }
 static size_t table_bytes(int H, int S) {
@@ -920,10 +920,13 @@ extern "C" int motif_chord_fwd(
     float *tab = static_cast<float *>(workspace);
     if (a.splits > 1) a.part = reinterpret_cast<float *>(static_cast<char *>(workspace) + tb);
     const int tn = table_len(S);
-    chord_bias_table_kernel<<<dim3((tn + 255) / 256, H), dim3(256), 0, s>>>(a, tab, tn);
-    int rc = check_launch("chord_bias_table_kernel");
-    if (rc) return rc;
-    if (mfma) chord_decode_mfma_kernel<<<dim3(a.splits, Hkv, B * a.nqc), dim3(256), 0, s>>>(a, tab, tn);
+    int rc = MOTIF_OK;
+    if (!mfma) {  // the vector kernel reads the bias from a per-head table
+      chord_bias_table_kernel<<<dim3((tn + 255) / 256, H), dim3(256), 0, s>>>(a, tab, tn);
+      rc = check_launch("chord_bias_table_kernel");
+      if (rc) return rc;
+    }
+    if (mfma) chord_decode_mfma_kernel<<<dim3(a.splits, Hkv, B * a.nqc), dim3(256), 0, s>>>(a);
     else launch_decode<float>(a, R, tab, tn, s);
     rc = check_launch("chord_decode_kernel");
     if (rc || a.splits == 1) return rc;
