@@ -11,9 +11,10 @@
 //   O'  = Attn U                      (C x dv)
 // so that for the state S_n entering chunk n
 //   S_{n+1} = A_n S_n + H_n,   O_n = O' + Q' S_n.
-// gdn_state_scan carries S across the chunks, one wavefront per (16 state columns,
-// head, sequence) with S in accumulator registers and a three-chunk-deep register
-// prefetch of A_n / H_n; it writes every S_n as MFMA operands.  gdn_chunk_out then
+// gdn_state_scan carries S across the chunks, one workgroup per (16 state columns,
+// head, sequence) with one wave per 16-row tile of S in accumulator registers (the
+// tiles meet in LDS once per chunk) and a six-chunk-deep register prefetch of
+// A_n / H_n; it writes every S_n as MFMA operands.  gdn_chunk_out then
 // forms O_n = O' + Q' S_n for all chunks in parallel.
 //
 // The workspace holds A_n, Q', H_n, O' and S_n in the order the consuming kernel's
@@ -522,33 +523,40 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
 }
 
 // ------------------------------------------------------------------ state scan
+// One wave per 16-row tile of S.
 template <int DK>
 struct ScanStage {
-  uint4 an[2][DK / 16][DK / 32];  // A_n hi / lo operands
-  f32x4 hn[DK / 16];              // H_n, accumulator layout
+  uint4 an[2][DK / 32];  // A_n hi / lo operand rows of this wave's tile
+  f32x4 hn;              // H_n tile, accumulator layout
 };
 
 template <int DK>
-__device__ __forceinline__ void scan_load(ScanStage<DK> &st, const char *cell, const WsLayout &Lw, int cg, int lane) {
+__device__ __forceinline__ void scan_load(ScanStage<DK> &st, const char *cell, const WsLayout &Lw, int cg, int mt,
+                                          int lane) {
+  constexpr int TDK = DK / 16, KS = DK / 32;
   const uint4 *an = reinterpret_cast<const uint4 *>(cell + Lw.an) + lane;
 #pragma unroll
   for (int p = 0; p < 2; ++p)
 #pragma unroll
-    for (int mt = 0; mt < DK / 16; ++mt)
-#pragma unroll
-      for (int ks = 0; ks < DK / 32; ++ks) st.an[p][mt][ks] = an[((p * (DK / 16) + mt) * (DK / 32) + ks) * 64];
-  const f32x4 *hn = reinterpret_cast<const f32x4 *>(cell + Lw.hn) + static_cast<size_t>(cg) * (DK / 16) * 64 + lane;
-#pragma unroll
-  for (int mt = 0; mt < DK / 16; ++mt) st.hn[mt] = hn[mt * 64];
+    for (int ks = 0; ks < KS; ++ks) st.an[p][ks] = an[((p * TDK + mt) * KS + ks) * 64];
+  st.hn = reinterpret_cast<const f32x4 *>(cell + Lw.hn)[(static_cast<size_t>(cg) * TDK + mt) * 64 + lane];
 }
 
-// One wavefront per (16 state columns, head, sequence).  S[mt][r] = S[16 mt + 4g + r][16 cg + l % 16].
+// One workgroup per (16 state columns, head, sequence), one wave per 16-row tile mt of
+// S: S[r] = S[16 mt + 4g + r][16 cg + l % 16].  Per chunk every wave turns its tile
+// into hi / lo bf16 halves of the B operand (slots 0..3 of a 32-row k-step come from
+// tile 2 ks, slots 4..7 from tile 2 ks + 1), exchanges them through LDS (double
+// buffered: one barrier per chunk) and forms its tile of S_{n+1} = A_n S_n + H_n: a
+// chain of 3 (DK / 32) MFMAs per wave instead of 3 DK^2 / 512 for one wave per column
+// group.
 template <int DK>
-__global__ void __launch_bounds__(64) gdn_state_scan(GdnArgs a, ChunkArgs ca, char *ws) {
+__global__ void __launch_bounds__(64 * (DK / 16)) gdn_state_scan(GdnArgs a, ChunkArgs ca, char *ws) {
   constexpr int TDK = DK / 16, KS = DK / 32;
   const int cg = blockIdx.x, h = blockIdx.y, sq = blockIdx.z;
-  const int lane = threadIdx.x, ln = lane & 15, g = lane >> 4;
+  const int lane = threadIdx.x & 63, mt = threadIdx.x >> 6;
+  const int ln = lane & 15, g = lane >> 4;
   const int col = 16 * cg + ln;
+  const int ks_own = mt >> 1, half = mt & 1;  // where this tile sits in the B operand
 
   int first, count;
   if (ca.cu == nullptr) {
@@ -561,72 +569,74 @@ __global__ void __launch_bounds__(64) gdn_state_scan(GdnArgs a, ChunkArgs ca, ch
   const WsLayout Lw(DK, a.dv);
   char *cell0 = ws + (static_cast<size_t>(h) * ca.total_chunks + first) * Lw.cell;
 
-  f32x4 S[TDK];
+  f32x4 S;
   const size_t sbase = (static_cast<size_t>(sq) * a.H + h) * DK * a.dv;
 #pragma unroll
-  for (int mt = 0; mt < TDK; ++mt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      S[mt][r] = a.s_in ? a.s_in[sbase + static_cast<size_t>(16 * mt + 4 * g + r) * a.dv + col] : 0.f;
+  for (int r = 0; r < 4; ++r)
+    S[r] = a.s_in ? a.s_in[sbase + static_cast<size_t>(16 * mt + 4 * g + r) * a.dv + col] : 0.f;
 
-  ScanStage<DK> s0, s1, s2;
+  // [buffer][plane][ks][lane] bf16x8 B operands of S
+  __shared__ __attribute__((aligned(16))) uint4 sB[2][2][KS][64];
+
+  // kScanDepth stages of A_n / H_n in flight (chunk n + kScanDepth is requested while
+  // chunk n is computed)
+  constexpr int kScanDepth = 6;
+  ScanStage<DK> st[kScanDepth];
   if (count > 0) {
-    scan_load<DK>(s0, cell0, Lw, cg, lane);
-    scan_load<DK>(s1, cell0 + static_cast<size_t>(min(1, count - 1)) * Lw.cell, Lw, cg, lane);
-    scan_load<DK>(s2, cell0 + static_cast<size_t>(min(2, count - 1)) * Lw.cell, Lw, cg, lane);
+#pragma unroll
+    for (int j = 0; j < kScanDepth; ++j)
+      scan_load<DK>(st[j], cell0 + static_cast<size_t>(min(j, count - 1)) * Lw.cell, Lw, cg, mt, lane);
   }
 
-  // S_n as hi / lo operands (stored for the output kernel), then S_{n+1} = A_n S_n + H_n;
-  // the stage is then refilled with chunk min(n + 3, count - 1) (a repeat load of the
-  // last chunk near the end keeps the main loop free of branches, so the loads of the
-  // two other stages stay in flight across it).
-  auto step = [&](ScanStage<DK> &st, int n) {
+  // S_n as hi / lo operands (shared, and stored for the output kernel), then this
+  // wave's tile of S_{n+1}; the stage is then refilled with chunk
+  // min(n + kScanDepth, count - 1) (a repeat load of the last chunk near the end keeps
+  // the loop free of branches).
+  auto step = [&](ScanStage<DK> &stg, int n) {
     char *cell = cell0 + static_cast<size_t>(n) * Lw.cell;
-    bf16x8 sh[KS], sl[KS];
+    const int buf = n & 1;
+    uint2 hv, lv;
+    {
+      bf16_t hb[4], lb[4];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float x = S[2 * ks + i / 4][i % 4];
-        sh[ks][i] = bf(x);
-        sl[ks][i] = bf(x - fl(sh[ks][i]));
+      for (int r = 0; r < 4; ++r) {
+        const __bf16 hh = bf(S[r]);
+        hb[r] = __builtin_bit_cast(bf16_t, hh);
+        lb[r] = __builtin_bit_cast(bf16_t, bf(S[r] - fl(hh)));
       }
-    uint4 *sn = reinterpret_cast<uint4 *>(cell + Lw.sn) + static_cast<size_t>(cg) * KS * 2 * 64 + lane;
+      hv = uint2{hb[0] | (static_cast<uint32_t>(hb[1]) << 16), hb[2] | (static_cast<uint32_t>(hb[3]) << 16)};
+      lv = uint2{lb[0] | (static_cast<uint32_t>(lb[1]) << 16), lb[2] | (static_cast<uint32_t>(lb[3]) << 16)};
+    }
+    reinterpret_cast<uint2 *>(&sB[buf][0][ks_own][lane])[half] = hv;
+    reinterpret_cast<uint2 *>(&sB[buf][1][ks_own][lane])[half] = lv;
+    __syncthreads();
+    // S_n for the output kernel: the 2 KS = TDK operand arrays, one full 1 KB array per
+    // wave (array mt = plane mt % 2 of k-step mt / 2)
+    reinterpret_cast<uint4 *>(cell + Lw.sn)[(static_cast<size_t>(cg) * KS * 2 + mt) * 64 + lane] =
+        sB[buf][mt & 1][mt >> 1][lane];
+    f32x4 acc = stg.hn;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      sn[(2 * ks) * 64] = __builtin_bit_cast(uint4, sh[ks]);
-      sn[(2 * ks + 1) * 64] = __builtin_bit_cast(uint4, sl[ks]);
+      const bf16x8 sh = __builtin_bit_cast(bf16x8, sB[buf][0][ks][lane]);
+      const bf16x8 sl = __builtin_bit_cast(bf16x8, sB[buf][1][ks][lane]);
+      acc = mma(__builtin_bit_cast(bf16x8, stg.an[1][ks]), sh, acc);
+      acc = mma(__builtin_bit_cast(bf16x8, stg.an[0][ks]), sl, acc);
+      acc = mma(__builtin_bit_cast(bf16x8, stg.an[0][ks]), sh, acc);
     }
-    f32x4 acc[TDK];
-#pragma unroll
-    for (int mt = 0; mt < TDK; ++mt) acc[mt] = st.hn[mt];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-      for (int mt = 0; mt < TDK; ++mt) acc[mt] = mma(__builtin_bit_cast(bf16x8, st.an[1][mt][ks]), sh[ks], acc[mt]);
-#pragma unroll
-      for (int mt = 0; mt < TDK; ++mt) acc[mt] = mma(__builtin_bit_cast(bf16x8, st.an[0][mt][ks]), sl[ks], acc[mt]);
-#pragma unroll
-      for (int mt = 0; mt < TDK; ++mt) acc[mt] = mma(__builtin_bit_cast(bf16x8, st.an[0][mt][ks]), sh[ks], acc[mt]);
-    }
-#pragma unroll
-    for (int mt = 0; mt < TDK; ++mt) S[mt] = acc[mt];
-    scan_load<DK>(st, cell0 + static_cast<size_t>(min(n + 3, count - 1)) * Lw.cell, Lw, cg, lane);
+    S = acc;
+    scan_load<DK>(stg, cell0 + static_cast<size_t>(min(n + kScanDepth, count - 1)) * Lw.cell, Lw, cg, mt, lane);
   };
   int n = 0;
-  for (; n + 3 <= count; n += 3) {
-    step(s0, n);
-    step(s1, n + 1);
-    step(s2, n + 2);
+  for (; n + kScanDepth <= count; n += kScanDepth) {
+#pragma unroll
+    for (int j = 0; j < kScanDepth; ++j) step(st[j], n + j);
   }
-  if (n < count) step(s0, n);
-  if (n + 1 < count) step(s1, n + 1);
+#pragma unroll
+  for (int j = 0; j < kScanDepth - 1; ++j)
+    if (n + j < count) step(st[j], n + j);
 
 #pragma unroll
-  for (int mt = 0; mt < TDK; ++mt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      a.s_out[sbase + static_cast<size_t>(16 * mt + 4 * g + r) * a.dv + col] = S[mt][r];
+  for (int r = 0; r < 4; ++r) a.s_out[sbase + static_cast<size_t>(16 * mt + 4 * g + r) * a.dv + col] = S[r];
 }
 
 // ------------------------------------------------------------------ chunk output
@@ -711,7 +721,7 @@ int launch_dk(const GdnArgs &a, const ChunkArgs &ca, char *ws, hipStream_t s) {
   if (a.dv <= 64) rc = launch_prep<DK, 64>(a, ca, ws, s);
   else rc = launch_prep<DK, 128>(a, ca, ws, s);
   if (rc) return rc;
-  gdn_state_scan<DK><<<dim3(a.dv / 16, a.H, ca.nseq), dim3(64), 0, s>>>(a, ca, ws);
+  gdn_state_scan<DK><<<dim3(a.dv / 16, a.H, ca.nseq), dim3(64 * (DK / 16)), 0, s>>>(a, ca, ws);
   if ((rc = check_launch("gdn_state_scan"))) return rc;
   // 8-byte output stores when every row start is 8-byte aligned
   const int vec = ((a.o_sb | a.o_sh | a.o_st) & 3) == 0 && (reinterpret_cast<uintptr_t>(a.o) & 7) == 0;
