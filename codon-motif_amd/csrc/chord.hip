@@ -21,6 +21,7 @@
 // with 3 xor-shuffles.  Partials (m, l, acc) are merged across the 4 waves in
 // LDS and across splits by chord_merge_kernel.
 #include <algorithm>
+#include <type_traits>
 
 #include "capi_internal.h"
 #include "common.h"
@@ -83,11 +84,54 @@ __device__ __forceinline__ float max_lane_groups(float x) {
 
 constexpr int kRow = 72;  // LDS row stride (bf16) of the K and V^T tiles: 144 B rows
 
-template <int HPW>  // query heads per workgroup (the rest of the 4 waves take query blocks)
-__global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
+// Per-head bias rows of the prefill kernel: tab[h][e] with e = key - q_abs + e0 holds
+// kappa_h * GGD(key - q_abs) for key <= q_abs and -inf for key > q_abs (the causal
+// mask), kappa_h = sign(ssmax_h) / |scale| (sign(ssmax_h) when scale == 0).  With q
+// multiplied by rho_h = sign(ssmax_h * scale) (0 when scale == 0) the MFMA that starts
+// from these entries yields acc = rho_h (q.k + bias / scale), and the logit is
+// |ssmax_h log_n[i] scale| acc (|ssmax_h log_n[i]| acc when scale == 0).
+__global__ void __launch_bounds__(256) chord_prefill_table_kernel(ChordArgs a, float *tab, int len, int e0) {
+  const int h = blockIdx.y, e = blockIdx.x * 256 + threadIdx.x;
+  if (e >= len) return;
+  const int dist = e - e0;
+  float v = -INFINITY;
+  if (dist <= 0) {
+    const float sg = a.ssmax[h] < 0.f ? -1.f : 1.f;
+    const float kappa = a.scale != 0.f ? sg / fabsf(a.scale) : sg;
+    v = kappa * ggd_bias(static_cast<float>(dist), a.alpha[h], a.beta[h], a.mu[h], a.eps);
+  }
+  tab[static_cast<size_t>(h) * len + e] = v;
+}
+
+// Bias-row length for the largest q_abs e0: entries up to e0 + 78 are read (keys of a
+// 64-key tile reach 63 past the wave's last row, which is 15 past its first), the
+// 16-byte reads 3 more.
+__host__ __device__ constexpr int prefill_table_len(int e0) { return (e0 + 82 + 3) / 4 * 4; }
+
+// LDS tile rows of 64 bf16 (128 B) hold their eight 16-byte pieces in the order
+// piece ^ (row & 7): the row-per-lane 16-byte reads of the MFMA operands and the
+// staging stores are then free of bank conflicts (measured with SQ_LDS_BANK_CONFLICT).
+__device__ __forceinline__ int swz(int row, int col) { return row * 64 + ((((col >> 3) ^ row) & 7) << 3) + (col & 7); }
+
+// Each workgroup is two halves of 4 waves over the same query rows and heads: half 0
+// takes the first ceil(n / 2) of the rows' n key tiles, half 1 the rest, each with
+// its own double-buffered K / V tiles, and the two partial softmaxes are merged
+// through LDS at the end.  Splitting the keys halves the longest chain of tiles and
+// gives 8 waves per workgroup (two workgroups fill a CU's LDS: 4 waves per SIMD).
+//
+// Per 64-key step a wave reads its tile's bias entries from a 79-entry window of
+// its head's bias row kept in LDS as 4 copies shifted by 0..3 (every lane's four
+// consecutive entries are one aligned 16-byte read); the window is fetched with two
+// dword loads per lane.  Tile data and windows are fetched two steps ahead: the
+// loads issued in step i are written to LDS at the end of step i + 1.
+template <int HPW>  // query heads per half (the rest of a half's 4 waves take query blocks)
+__global__ void __launch_bounds__(512) chord_fwd_kernel(ChordArgs a, const float *tab, int tab_len, int e0) {
   constexpr int QBPW = 4 / HPW;
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = wv >> 2, w = wv & 3;
+  const int htid = tid & 255;  // thread index inside the half
   const int ln = lane & 15, g = lane >> 4;
   const int group = a.H / a.Hkv;
   const int hg = blockIdx.y, sq = blockIdx.z;
@@ -108,45 +152,123 @@ __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
   const int q0 = (qbg * QBPW + w / HPW) * 16;
   const int my_q = q0 + ln;  // this lane's query row (shared by its 4 lane groups)
   const bool q_valid = my_q < Lq;
-  const int q_abs = q_start + my_q;
 
   const int wg_q_last = min(Lq, (qbg + 1) * QBPW * 16) - 1;
   const int kv_end = min(Skv, q_start + wg_q_last + 1);
   const int ntiles = (kv_end + kBN - 1) / kBN;
-  const int wave_first_qabs = q_start + q0;
+  const int nsteps = (ntiles + 1) / 2;                   // tiles of half 0
+  const int t_first = half ? nsteps : 0;
+  const int t_count = half ? ntiles - nsteps : nsteps;   // half 1 may have one fewer
   const int wave_kv_end = min(Skv, q_start + min(Lq, q0 + 16));
+  // Keys past the cache end are masked by the table unless a query sits past it.
+  const bool kmask = q_start + min(Lq, q0 + 16) > Skv;
 
   const bf16_t *qp = static_cast<const bf16_t *>(a.q) + batch * a.q_sb + head * a.q_sh + int64_t(tok0) * a.q_st;
   const bf16_t *kp = static_cast<const bf16_t *>(a.k) + batch * a.k_sb + kvh * a.k_sh + int64_t(tok0) * a.k_st;
   const bf16_t *vp = static_cast<const bf16_t *>(a.v) + batch * a.v_sb + kvh * a.v_sh + int64_t(tok0) * a.v_st;
-
-  __shared__ __attribute__((aligned(16))) bf16_t sK[2][kBN][kRow];   // K rows
-  __shared__ __attribute__((aligned(16))) bf16_t sV[2][kD][kRow];    // V^T rows, keys in vperm order
-  __shared__ __attribute__((aligned(16))) float sTab[4][4][80];      // per wave: 4 shifted bias tables
-
-  // Range-checked buffers over the kv head's visible keys (rows past kv_end read 0).
+  // Range-checked buffers over the visible keys (rows past kv_end read 0).
+  const buf_t qbuf = make_buf(qp, Lq > 0 ? static_cast<uint32_t>(((Lq - 1) * a.q_st + kD) * 2) : 0u);
   const buf_t kbuf = make_buf(kp, kv_end > 0 ? static_cast<uint32_t>(((kv_end - 1) * a.k_st + kD) * 2) : 0u);
   const buf_t vbuf = make_buf(vp, kv_end > 0 ? static_cast<uint32_t>(((kv_end - 1) * a.v_st + kD) * 2) : 0u);
-  const buf_t qbuf = make_buf(qp, Lq > 0 ? static_cast<uint32_t>(((Lq - 1) * a.q_st + kD) * 2) : 0u);
+  const buf_t tbuf = make_buf(tab + static_cast<size_t>(head) * tab_len, static_cast<uint32_t>(tab_len) * 4u);
 
-  // Q^T as the B operand: lane holds Q[my_q][32 ks + 8g .. +8].
-  bf16x8 qreg[2];
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks)
-    qreg[ks] = __builtin_bit_cast(bf16x8, buf_ld16(qbuf, (my_q * a.q_st + 32 * ks + 8 * g) * 2));
-  // logit = mul * (scale * q.k + bias), mul = ssmax[head] * log_n[row].  With
-  // sg = sign(ssmax[head]) (uniform per wave, log_n >= 0) the kernel works with
-  // u = sg * log2e * (scale * q.k + bias): the row max of the logits is |mul| times
-  // the row max of u, and p = exp2(|mul| * (u - m_u)).
-  const float alpha_h = a.alpha[head], beta_h = a.beta[head], mu_h = a.mu[head];
+  // logit = a_row * acc (see chord_prefill_table_kernel), a_row = |ssmax log_n scale|;
+  // the kernel works in log2 units, p = exp2(A (acc - m)) with A = log2e a_row.
   const float ssm = a.ssmax[head];
   const float sg = ssm < 0.f ? -1.f : 1.f;
+  const float rho = a.scale > 0.f ? sg : a.scale < 0.f ? -sg : 0.f;
+  const float a_head = fabsf(ssm) * (a.scale != 0.f ? fabsf(a.scale) : 1.f) * kLog2e;
   const float lnv = a.log_n[batch * a.ln_sb + int64_t(tok0 + min(my_q, Lq - 1)) * a.ln_st];
-  const float amul = q_valid ? fabsf(ssm * lnv) : 0.f;  // |mul| >= 0
-  const float c_u = sg * a.scale * kLog2e;               // u = fma(q.k, c_u, table)
-  const float c_t = sg * kLog2e;                         // table entries: c_t * bias
+  // A > 0 keeps masked keys at exactly 0 (exp2(-inf)); a row with a_row = 0 has
+  // finite logits A * acc that round to 0 against the max, as the exact 0 logits do.
+  const float A = q_valid ? fmaxf(a_head * lnv, 1e-30f) : 1.f;
 
-  float m_run = -INFINITY;  // in u units
+  // rho Q^T as the B operand: lane holds rho Q[my_q][32 ks + 8g .. +8] (exact: rho in {-1, 0, 1}).
+  bf16x8 qreg[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    uint4 u = buf_ld16(qbuf, (my_q * a.q_st + 32 * ks + 8 * g) * 2);
+    if (rho < 0.f) { u.x ^= 0x80008000u; u.y ^= 0x80008000u; u.z ^= 0x80008000u; u.w ^= 0x80008000u; }
+    else if (rho == 0.f) u = uint4{0u, 0u, 0u, 0u};
+    qreg[ks] = __builtin_bit_cast(bf16x8, u);
+  }
+
+  __shared__ __attribute__((aligned(16))) bf16_t sK[2][2][kBN * kD];   // [half][buffer] K rows (swizzled)
+  __shared__ __attribute__((aligned(16))) bf16_t sV[2][2][kD * kBN];   // V^T rows, keys in vperm order (swizzled)
+  __shared__ __attribute__((aligned(16))) float sB[8][4 * 80];         // per wave: 4 shifted bias windows
+
+  // Bias window of tile t: entries wbase(t) + j, j = 0..78, of the head's row, where
+  // entry j serves key n0 + 16 kt + 4 g + r of row ln with j = 16 kt + 4 g + r + 15 - ln
+  // (table index key - q_abs + e0).  Lane l fetches entries l and 64 + l; an offset
+  // below the row start wraps past its end and reads 0 (only invalid rows read it).
+  const uint32_t woff = 4u * static_cast<uint32_t>(-q_start - q0 + e0 - 15 + lane);
+  float bwin[2];
+  auto load_window = [&](int t) {
+    const uint32_t o = woff + 4u * static_cast<uint32_t>(t * kBN);
+    bwin[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(tbuf, o, 0, 0));
+    bwin[1] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(tbuf, o + 256u, 0, 0));
+  };
+  // Copy c (80 floats; a stride of 20 16-byte units keeps the reads free of bank
+  // conflicts) holds entry j at position j - c.  Reads stay at positions <= 75; the
+  // stores of entries no lane reads (lane < c, lane 15) land at positions >= 76 of
+  // the previous copy or this one.
+  float *bw = &sB[wv][0];
+  auto store_window = [&]() {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) bw[79 * c + lane] = bwin[0];
+    if (lane < 16) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) bw[79 * c + 64 + lane] = bwin[1];
+    }
+  };
+  // this lane's bias entries of tile kt: bwr[16 kt .. +3]
+  const float *bwr = bw + 79 * ((15 - ln) & 3) + 4 * g + 15 - ln;
+
+  // Tile staging by the half's 256 threads: K rows (2 x 16 B per thread); V as key
+  // pairs (2 keys x 8 d).  The per-lane offsets are fixed; step t moves the buffer
+  // base to its first key (the range shrinks with it, so keys past kv_end read 0).
+  uint4 kst[2], vst[2];
+  const int vpair = htid & 31, vseg = htid >> 5;
+  const uint32_t koff = static_cast<uint32_t>(((htid >> 3) * a.k_st + (htid & 7) * 8) * 2);
+  const uint32_t koff2 = koff + static_cast<uint32_t>(32 * a.k_st * 2);
+  const uint32_t voff = static_cast<uint32_t>((2 * vpair * a.v_st + 8 * vseg) * 2);
+  const uint32_t voff2 = voff + static_cast<uint32_t>(a.v_st * 2);
+  const int64_t kbytes = kv_end > 0 ? ((kv_end - 1) * a.k_st + kD) * 2 : 0;
+  const int64_t vbytes = kv_end > 0 ? ((kv_end - 1) * a.v_st + kD) * 2 : 0;
+  auto load_tile = [&](int t) {
+    const int64_t kskip = int64_t(t) * kBN * a.k_st, vskip = int64_t(t) * kBN * a.v_st;
+    const int64_t krem = kbytes - 2 * kskip, vrem = vbytes - 2 * vskip;
+    const buf_t kr = make_buf(kp + kskip, krem > 0 ? static_cast<uint32_t>(krem) : 0u);
+    const buf_t vr = make_buf(vp + vskip, vrem > 0 ? static_cast<uint32_t>(vrem) : 0u);
+    kst[0] = buf_ld16(kr, koff);
+    kst[1] = buf_ld16(kr, koff2);
+    vst[0] = buf_ld16(vr, voff);
+    vst[1] = buf_ld16(vr, voff2);
+  };
+  // K rows (c >> 3) and (c >> 3) + 32 of this thread, V^T rows 8 vseg + m (m = 0..7)
+  const int ks_off = swz(htid >> 3, (htid & 7) * 8);
+  const int vcol = vperm(2 * vpair);
+  int vs_off[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) vs_off[m] = swz(8 * vseg + m, vcol);
+  auto store_tile = [&](auto bufc) {
+    constexpr int buf = decltype(bufc)::value;
+    *reinterpret_cast<uint4 *>(&sK[half][buf][ks_off]) = kst[0];
+    *reinterpret_cast<uint4 *>(&sK[half][buf][ks_off + 32 * 64]) = kst[1];
+    const uint32_t *v0 = reinterpret_cast<const uint32_t *>(&vst[0]);
+    const uint32_t *v1 = reinterpret_cast<const uint32_t *>(&vst[1]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lo = (v0[i] & 0xffffu) | (v1[i] << 16);      // d = 8 vseg + 2i
+      const uint32_t hi = (v0[i] >> 16) | (v1[i] & 0xffff0000u);  // d = 8 vseg + 2i + 1
+      *reinterpret_cast<uint32_t *>(&sV[half][buf][vs_off[2 * i]]) = lo;
+      *reinterpret_cast<uint32_t *>(&sV[half][buf][vs_off[2 * i + 1]]) = hi;
+    }
+  };
+  // operand reads: rows 16 kt + ln (K) / 16 mt + ln (V^T), 16-byte pieces g and 4 + g
+  const int rd0 = swz(ln, 8 * g), rd1 = swz(ln, 32 + 8 * g);
+
+  float m_run = -INFINITY;  // in acc units
   // O^T accumulators (tiles 0..3) and a fifth tile that multiplies P by ones: its
   // entries are the row sums of P (bf16-rounded, as used in the output), so the
   // normaliser follows the rescales of the output for free.
@@ -157,95 +279,40 @@ __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) ones[i] = static_cast<__bf16>(1.f);
 
-  // Tile staging: K rows (2 x 16 B per thread); V as key pairs (2 keys x 8 d).
-  uint4 kst[2], vst[2];
-  const int vpair = tid & 31, vseg = tid >> 5;
-  auto load_tile = [&](int t) {
-    const int n0 = t * kBN;
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int c = tid + 256 * r, key = n0 + (c >> 3), dc = (c & 7) * 8;
-      kst[r] = buf_ld16(kbuf, (key * a.k_st + dc) * 2);
-    }
-    const int key0 = n0 + 2 * vpair;
-    vst[0] = buf_ld16(vbuf, (key0 * a.v_st + 8 * vseg) * 2);
-    vst[1] = buf_ld16(vbuf, ((key0 + 1) * a.v_st + 8 * vseg) * 2);
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int c = tid + 256 * r;
-      *reinterpret_cast<uint4 *>(&sK[buf][c >> 3][(c & 7) * 8]) = kst[r];
-    }
-    const uint32_t *v0 = reinterpret_cast<const uint32_t *>(&vst[0]);
-    const uint32_t *v1 = reinterpret_cast<const uint32_t *>(&vst[1]);
-    const int col = vperm(2 * vpair);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t lo = (v0[i] & 0xffffu) | (v1[i] << 16);      // d = 8 vseg + 2i
-      const uint32_t hi = (v0[i] >> 16) | (v1[i] & 0xffff0000u);  // d = 8 vseg + 2i + 1
-      *reinterpret_cast<uint32_t *>(&sV[buf][8 * vseg + 2 * i][col]) = lo;
-      *reinterpret_cast<uint32_t *>(&sV[buf][8 * vseg + 2 * i + 1][col]) = hi;
-    }
-  };
-
-  if (ntiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
+  // Prologue: tile and window of the first step in LDS, the second step's in flight.
+  // Every load and store of the loop is unconditional (tiles and entries past the end
+  // read zeros through the range checks), so the wait counts are path independent.
+  load_window(t_first);
+  load_tile(t_first);
+  store_tile(std::integral_constant<int, 0>());
+  store_window();
+  load_window(t_first + 1);
+  load_tile(t_first + 1);
   __syncthreads();
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    const int n0 = t * kBN;
-    if (t + 1 < ntiles) load_tile(t + 1);
-
-    if (n0 < wave_kv_end) {
-      // Bias (log2 units) for distances n0 - wave_first_qabs - 15 + e, e in [0, 79),
-      // stored in 4 copies shifted by c so that every lane's 4 consecutive entries
-      // are one aligned 16-byte read: copy c holds entry e at index e - c.
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int e = lane + 64 * i;
-        if (e < 79) {
-          const float bv = c_t * ggd_bias(static_cast<float>(n0 - wave_first_qabs - 15 + e), alpha_h, beta_h, mu_h, a.eps);
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            if (e >= c) sTab[w][c][e - c] = bv;
-        }
-      }
-      // S^T = K Q^T: tile kt holds S^T[16 kt + 4g + r][ln] (key n0 + 16 kt + 4g + r).
+  // One step: tile t_first + i from LDS buffer BUF (a constant, so every LDS address
+  // is a fixed register plus an immediate).
+  auto step = [&](int i, auto bufc) {
+    constexpr int buf = decltype(bufc)::value;
+    const int n0 = (t_first + i) * kBN;
+    if (i < t_count && n0 < wave_kv_end) {
+      // acc^T = bias + rho K Q^T: tile kt holds key n0 + 16 kt + 4g + r of row ln.
       f32x4 sacc[4];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
-        sacc[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const bf16x8 kreg = *reinterpret_cast<const bf16x8 *>(&sK[buf][16 * kt + ln][32 * ks + 8 * g]);
-          sacc[kt] = mma16(kreg, qreg[ks], sacc[kt]);
-        }
+        const f32x4 bias = *reinterpret_cast<const f32x4 *>(bwr + 16 * kt);
+        const bf16x8 k0 = *reinterpret_cast<const bf16x8 *>(&sK[half][buf][rd0 + 1024 * kt]);
+        const bf16x8 k1 = *reinterpret_cast<const bf16x8 *>(&sK[half][buf][rd1 + 1024 * kt]);
+        sacc[kt] = mma16(k1, qreg[1], mma16(k0, qreg[0], bias));
       }
-      __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // bias table visible to the wave
-
-      // u = c_u q.k + table; masked keys (diagonal / cache-end tiles only) are -inf.
-      const bool need_mask = (n0 + kBN - 1 > wave_first_qabs) || (n0 + kBN > Skv);
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        const int e0 = 16 * kt + 4 * g - ln + 15, c = e0 & 3;
-        const f32x4 b4 = *reinterpret_cast<const f32x4 *>(&sTab[w][c][e0 - c]);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sacc[kt][r] = fmaf(sacc[kt][r], c_u, b4[r]);
-      }
-      if (need_mask) {
+      if (kmask && n0 + kBN > Skv) {
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int key = n0 + 16 * kt + 4 * g + r;
-            if (key > q_abs || key >= Skv) sacc[kt][r] = -INFINITY;
-          }
+          for (int r = 0; r < 4; ++r)
+            if (n0 + 16 * kt + 4 * g + r >= Skv) sacc[kt][r] = -INFINITY;
       }
+      float mx = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
@@ -254,26 +321,16 @@ __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
       // Lazy rescaling: the running max moves only when the tile exceeds it by more
       // than 8 (log2 units of the logits), so p <= 2^8 and most tiles skip the
       // rescale of the output accumulators.
-      const bool grow = amul * (mx - m_run) > 8.f || m_run == -INFINITY;
+      const bool grow = A * (mx - m_run) > 8.f || m_run == -INFINITY;
       const float m_new = grow ? mx : m_run;
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float resc = m_run == -INFINITY ? 0.f : fast_exp2(amul * (m_run - m_use));
-      const float nb = -amul * m_use;
-      // p = exp2(|mul| (u - m)); masked keys give exactly 0 (also when |mul| = 0).
-      if (need_mask) {
+      const float resc = m_run == -INFINITY ? 0.f : fast_exp2(A * (m_run - m_use));
+      const float nb = -A * m_use;
+      // p = exp2(A (acc - m)); masked keys (acc = -inf) give exactly 0.
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float u = sacc[kt][r];
-            sacc[kt][r] = u == -INFINITY ? 0.f : fast_exp2(fmaf(u, amul, nb));
-          }
-      } else {
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) sacc[kt][r] = fast_exp2(fmaf(sacc[kt][r], amul, nb));
-      }
+        for (int r = 0; r < 4; ++r) sacc[kt][r] = fast_exp2(fmaf(sacc[kt][r], A, nb));
       if (__builtin_amdgcn_read_exec() & __ballot(grow)) {
 #pragma unroll
         for (int mt = 0; mt < 5; ++mt)
@@ -293,31 +350,61 @@ __global__ void __launch_bounds__(256) chord_fwd_kernel(ChordArgs a) {
         }
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
-          const bf16x8 va = *reinterpret_cast<const bf16x8 *>(&sV[buf][16 * mt + ln][32 * kp2 + 8 * g]);
+          const bf16x8 va = *reinterpret_cast<const bf16x8 *>(&sV[half][buf][(kp2 ? rd1 : rd0) + 1024 * mt]);
           oacc[mt] = mma16(va, pb, oacc[mt]);
         }
         oacc[4] = mma16(ones, pb, oacc[4]);  // every row of tile 4: the row sum of P
       }
     }
 
-    if (t + 1 < ntiles) store_tile(buf ^ 1);
+    // The next step's window and tile (fetched one step ago) into LDS, the one after
+    // into flight.  The window region is this wave's own (its reads above come first
+    // in program order); the tile buffer was last read before the previous barrier.
+    store_window();
+    load_window(t_first + i + 2);
+    store_tile(std::integral_constant<int, buf ^ 1>());
+    load_tile(t_first + i + 2);
     __syncthreads();
+  };
+  int i = 0;
+  for (; i + 1 < nsteps; i += 2) {
+    step(i, std::integral_constant<int, 0>());
+    step(i + 1, std::integral_constant<int, 1>());
   }
+  if (i < nsteps) step(i, std::integral_constant<int, 0>());
 
-  const float l_run = oacc[4][0];
-  if (q_valid) {
-    const float inv = 1.f / fmaxf(l_run, 1e-20f);
+  // Merge: half 1 leaves O in its K buffers (4 waves x 16 x 64 floats = sK[1]) and
+  // (l, m) in its window region; half 0 combines them with its own and writes the rows.
+  float *mo = reinterpret_cast<float *>(&sK[1][0][0]) + w * 16 * 64 + lane;
+  float *mlm = &sB[4 + w][lane];
+  if (half == 1) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) mo[j * 64] = oacc[j >> 2][j & 3];
+    mlm[0] = oacc[4][0];
+    mlm[64] = m_run;
+  }
+  __syncthreads();
+  if (half == 0 && q_valid) {
+    const float lB = mlm[0], mB = mlm[64];
+    const float m = fmaxf(m_run, mB);
+    const float fA = m_run == -INFINITY ? 0.f : fast_exp2(A * (m_run - m));
+    const float fB = mB == -INFINITY ? 0.f : fast_exp2(A * (mB - m));
+    const float l = oacc[4][0] * fA + lB * fB;
+    const float inv = 1.f / fmaxf(l, 1e-20f);
     bf16_t *op = static_cast<bf16_t *>(a.out) + batch * a.o_sb + head * a.o_sh + int64_t(tok0 + my_q) * a.o_st;
     // lane holds O[my_q][16 mt + 4g + r]
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
+      float o[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[r] = (oacc[mt][r] * fA + mo[(4 * mt + r) * 64] * fB) * inv;
       uint2 pk;
-      pk.x = static_cast<uint32_t>(f32_to_bf16(oacc[mt][0] * inv)) | (static_cast<uint32_t>(f32_to_bf16(oacc[mt][1] * inv)) << 16);
-      pk.y = static_cast<uint32_t>(f32_to_bf16(oacc[mt][2] * inv)) | (static_cast<uint32_t>(f32_to_bf16(oacc[mt][3] * inv)) << 16);
+      pk.x = static_cast<uint32_t>(f32_to_bf16(o[0])) | (static_cast<uint32_t>(f32_to_bf16(o[1])) << 16);
+      pk.y = static_cast<uint32_t>(f32_to_bf16(o[2])) | (static_cast<uint32_t>(f32_to_bf16(o[3])) << 16);
       *reinterpret_cast<uint2 *>(op + 16 * mt + 4 * g) = pk;
     }
     if (a.lse && g == 0)
-      a.lse[(static_cast<size_t>(batch) * a.H + head) * a.L + tok0 + my_q] = amul * m_run + fast_log2(l_run);
+      a.lse[(static_cast<size_t>(batch) * a.H + head) * a.L + tok0 + my_q] = A * (m == -INFINITY ? 0.f : m) + fast_log2(l);
   }
 }
 
@@ -836,6 +923,10 @@ static size_t table_bytes(int H, int S) {
   return (static_cast<size_t>(H) * table_len(S) * sizeof(float) + 255) / 256 * 256;
 }
 
+static size_t prefill_table_bytes(int H, int e0) {
+  return (static_cast<size_t>(H) * prefill_table_len(e0) * sizeof(float) + 255) / 256 * 256;
+}
+
 }  // namespace motif
 
 using namespace motif;
@@ -846,9 +937,10 @@ extern "C" size_t motif_chord_workspace_bytes(int B, int H, int Hkv, int L, int 
     sp = decode_splits(B, Hkv, S);
   if (splits) *splits = sp;
   if (B <= 0 || H <= 0 || Hkv <= 0 || L <= 0) return 0;
-  // the table is needed by every call that takes the vector kernel (decode shapes
-  // and fp32 inputs); it is small, so it is always included
-  size_t n = table_bytes(H, S);
+  // the distance table of the vector kernel (decode shapes and fp32 inputs), or the
+  // bias rows of the bf16 prefill kernel sized for any q_start <= S (largest q_abs
+  // S + L - 1); both are small, so the larger is always included
+  size_t n = std::max(table_bytes(H, S), prefill_table_bytes(H, S + L - 1));
   if (sp > 1) n += static_cast<size_t>(B) * Hkv * sp * (static_cast<size_t>(H / Hkv) * L) * (D + 2) * sizeof(float);
   return n;
 }
@@ -939,9 +1031,21 @@ extern "C" int motif_chord_fwd(
   const int qbpw = 4 / hpw;
   const int maxlen = packed ? max_seqlen : L;
   if (maxlen <= 0) return MOTIF_OK;
-  dim3 grid((maxlen + 16 * qbpw - 1) / (16 * qbpw), H / hpw, packed ? nseq : B), block(256);
-  if (hpw == 4) chord_fwd_kernel<4><<<grid, block, 0, s>>>(a);
-  else if (hpw == 2) chord_fwd_kernel<2><<<grid, block, 0, s>>>(a);
-  else chord_fwd_kernel<1><<<grid, block, 0, s>>>(a);
+  // bias rows up to the largest query position (packed: positions restart per sequence)
+  const int64_t e0l = packed ? static_cast<int64_t>(max_seqlen) - 1 : std::max<int64_t>(S, int64_t(q_start) + L) - 1;
+  if (e0l > (int64_t(1) << 28)) return set_error(MOTIF_ERR_UNSUPPORTED, "chord_fwd: sequence too long");
+  const int e0 = static_cast<int>(e0l), tl = prefill_table_len(e0);
+  const size_t need = prefill_table_bytes(H, e0);
+  if (!workspace || workspace_bytes < need)
+    return set_error(MOTIF_ERR_INVALID, "chord_fwd: workspace too small (need " + std::to_string(need) + " bytes)");
+  float *tab = static_cast<float *>(workspace);
+  chord_prefill_table_kernel<<<dim3((tl + 255) / 256, H), dim3(256), 0, s>>>(a, tab, tl, e0);
+  const int rc = check_launch("chord_prefill_table_kernel");
+  if (rc) return rc;
+  const int nqbg = (maxlen + 16 * qbpw - 1) / (16 * qbpw);
+  dim3 grid(nqbg, H / hpw, packed ? nseq : B), block(512);
+  if (hpw == 4) chord_fwd_kernel<4><<<grid, block, 0, s>>>(a, tab, tl, e0);
+  else if (hpw == 2) chord_fwd_kernel<2><<<grid, block, 0, s>>>(a, tab, tl, e0);
+  else chord_fwd_kernel<1><<<grid, block, 0, s>>>(a, tab, tl, e0);
   return check_launch("chord_fwd_kernel");
 }

@@ -83,9 +83,7 @@ def _launch(q, k, v, alpha, beta, mu, ssmax, log_n, q_start, scale, eps, out, ls
     lib = _lib.lib()
     if cu_dev is None:
         nseq, max_seqlen = B, L
-        nbytes = lib.motif_chord_workspace_bytes(B, H, Hkv, L, S, D, None)
-    else:
-        nbytes = 0
+    nbytes = lib.motif_chord_workspace_bytes(B, H, Hkv, L, S, D, None)
     ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=q.device)
     rc = lib.motif_chord_fwd(
         *_lib.t4(q), *_lib.t4(k), *_lib.t4(v),
