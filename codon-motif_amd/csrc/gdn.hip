@@ -339,6 +339,9 @@ static GdnArgs make_args(const void *q, int64_t q_sb, int64_t q_sh, int64_t q_st
   a.s_in = state_in; a.s_out = state_out;
   a.o = o; a.o_sb = o_sb; a.o_sh = o_sh; a.o_st = o_st;
   a.B = B; a.H = H; a.L = L; a.dk = dk; a.dv = dv;
+  a.gate = nullptr; a.gt_sb = a.gt_st = 0;
+  a.nw = nullptr; a.neps = 0.f;
+  a.y = nullptr; a.y_sb = a.y_st = 0;
   return a;
 }
 
@@ -421,7 +424,7 @@ extern "C" size_t motif_gdn_chunk_workspace_bytes(int H, int dk, int dv, int chu
   return std::max(mfma, per * H * total_chunks * sizeof(float));
 }
 
-extern "C" int motif_gdn_chunk_fwd(
+static int chunk_fwd_impl(
     const void *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
     const void *k, int64_t k_sb, int64_t k_sh, int64_t k_st,
     const void *v, int64_t v_sb, int64_t v_sh, int64_t v_st,
@@ -432,7 +435,10 @@ extern "C" int motif_gdn_chunk_fwd(
     int B, int H, int L, int dk, int dv, int chunk,
     const int32_t *cu_seqlens, const int32_t *chunk_offsets, int nseq, int total_chunks,
     void *workspace, size_t workspace_bytes,
-    int in_dtype, int out_dtype, void *stream) {
+    int in_dtype, int out_dtype, void *stream,
+    const void *gate, int64_t gt_sb, int64_t gt_st, const void *norm_w, float norm_eps,
+    void *y, int64_t y_sb, int64_t y_st) {
+  const bool gated = gate != nullptr;
   if (B < 0 || H < 0 || L < 0 || dk <= 0 || dv <= 0 || chunk <= 0)
     return set_error(MOTIF_ERR_INVALID, "gdn_chunk: negative or zero size");
   if (dv % 32 != 0 || dv > 256)
@@ -456,7 +462,7 @@ extern "C" int motif_gdn_chunk_fwd(
     hipError_t e = hipMemcpyAsync(state_out, state_in, n, hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? MOTIF_OK : set_error(MOTIF_ERR_HIP, hipGetErrorString(e));
   }
-  if (!q || !k || !v || !beta || !g || !o)
+  if (!q || !k || !v || !beta || !g || (!o && !gated))
     return set_error(MOTIF_ERR_INVALID, "gdn_chunk: NULL input pointer");
   const size_t need = motif_gdn_chunk_workspace_bytes(H, dk, dv, chunk, total_chunks);
   if (!workspace || workspace_bytes < need)
@@ -465,6 +471,17 @@ extern "C" int motif_gdn_chunk_fwd(
   GdnArgs a = make_args(q, q_sb, q_sh, q_st, k, k_sb, k_sh, k_st, v, v_sb, v_sh, v_st,
                         beta, b_sb, b_sh, b_st, g, g_sb, g_sh, g_st, state_in, state_out,
                         o, o_sb, o_sh, o_st, B, H, L, dk, dv);
+  if (gated) {
+    if (!norm_w || !y) return set_error(MOTIF_ERR_INVALID, "gdn_chunk_gated: NULL norm weight or output");
+    // the epilogue lives in the bf16 MFMA output kernel; 8-byte gate / weight / output pieces
+    const uintptr_t al = reinterpret_cast<uintptr_t>(gate) | reinterpret_cast<uintptr_t>(norm_w) |
+                         reinterpret_cast<uintptr_t>(y);
+    if (!chunk_mfma_eligible(a, chunk, in_dtype, out_dtype) || (al & 7) || ((gt_sb | gt_st | y_sb | y_st) & 3))
+      return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_chunk_gated: needs the bf16 MFMA path and 8-byte aligned rows");
+    a.gate = gate; a.gt_sb = gt_sb; a.gt_st = gt_st;
+    a.nw = norm_w; a.neps = norm_eps;
+    a.y = y; a.y_sb = y_sb; a.y_st = y_st;
+  }
   ChunkArgs ca;
   ca.cu = cu_seqlens;
   ca.coff = chunk_offsets;
@@ -486,4 +503,45 @@ extern "C" int motif_gdn_chunk_fwd(
   if (in_dtype == MOTIF_F32) return launch_chunk<float>(a, ca, chunk, s);
   if (in_dtype == MOTIF_BF16) return launch_chunk<bf16_t>(a, ca, chunk, s);
   return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_chunk: unsupported dtype");
+}
+
+extern "C" int motif_gdn_chunk_fwd(
+    const void *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void *k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void *v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    const void *beta, int64_t b_sb, int64_t b_sh, int64_t b_st,
+    const void *g, int64_t g_sb, int64_t g_sh, int64_t g_st,
+    const float *state_in, float *state_out,
+    void *o, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    int B, int H, int L, int dk, int dv, int chunk,
+    const int32_t *cu_seqlens, const int32_t *chunk_offsets, int nseq, int total_chunks,
+    void *workspace, size_t workspace_bytes,
+    int in_dtype, int out_dtype, void *stream) {
+  return chunk_fwd_impl(q, q_sb, q_sh, q_st, k, k_sb, k_sh, k_st, v, v_sb, v_sh, v_st,
+                        beta, b_sb, b_sh, b_st, g, g_sb, g_sh, g_st, state_in, state_out,
+                        o, o_sb, o_sh, o_st, B, H, L, dk, dv, chunk, cu_seqlens, chunk_offsets, nseq,
+                        total_chunks, workspace, workspace_bytes, in_dtype, out_dtype, stream,
+                        nullptr, 0, 0, nullptr, 0.f, nullptr, 0, 0);
+}
+
+extern "C" int motif_gdn_chunk_fwd_gated(
+    const void *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void *k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void *v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    const void *beta, int64_t b_sb, int64_t b_sh, int64_t b_st,
+    const void *g, int64_t g_sb, int64_t g_sh, int64_t g_st,
+    const float *state_in, float *state_out,
+    void *o, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    int B, int H, int L, int dk, int dv, int chunk,
+    const int32_t *cu_seqlens, const int32_t *chunk_offsets, int nseq, int total_chunks,
+    void *workspace, size_t workspace_bytes,
+    const void *gate, int64_t gate_sb, int64_t gate_st, const void *norm_weight, float norm_eps,
+    void *y, int64_t y_sb, int64_t y_st,
+    int dtype, void *stream) {
+  if (!gate) return set_error(MOTIF_ERR_INVALID, "gdn_chunk_gated: NULL gate");
+  return chunk_fwd_impl(q, q_sb, q_sh, q_st, k, k_sb, k_sh, k_st, v, v_sb, v_sh, v_st,
+                        beta, b_sb, b_sh, b_st, g, g_sb, g_sh, g_st, state_in, state_out,
+                        o, o_sb, o_sh, o_st, B, H, L, dk, dv, chunk, cu_seqlens, chunk_offsets, nseq,
+                        total_chunks, workspace, workspace_bytes, dtype, dtype, stream,
+                        gate, gate_sb, gate_st, norm_weight, norm_eps, y, y_sb, y_st);
 }

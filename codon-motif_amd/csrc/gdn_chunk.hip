@@ -646,12 +646,27 @@ __global__ void __launch_bounds__(64 * (DK / 16)) gdn_state_scan(GdnArgs a, Chun
 template <typename TO, int DK>
 __global__ void __launch_bounds__(256) gdn_chunk_out(GdnArgs a, ChunkArgs ca, const char *ws, int vec_store) {
   constexpr int KS = DK / 32;
+  constexpr int kMaxCg = 2;  // 16-column groups per wave (dv <= 128)
   const int chunk = blockIdx.x, h = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ln = lane & 15, g = lane >> 4;
   const ChunkInfo ci = resolve_chunk(chunk, kC, a.L, ca);
   const WsLayout Lw(DK, a.dv);
   const char *cell = ws + (static_cast<size_t>(h) * ca.total_chunks + chunk) * Lw.cell;
+  const int ncg = a.dv / 16;
+
+  // gate pieces of the fused GatedRMSNorm, requested before the products
+  uint2 gv[kMaxCg][4];
+  if (a.gate) {
+    const bf16_t *gp = static_cast<const bf16_t *>(a.gate) + ci.batch * a.gt_sb + int64_t(ci.t0) * a.gt_st + h * a.dv;
+#pragma unroll
+    for (int i = 0; i < kMaxCg; ++i)
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const int row = min(16 * mt + ln, ci.len - 1), c0 = 16 * min(w + 4 * i, ncg - 1) + 4 * g;
+        gv[i][mt] = *reinterpret_cast<const uint2 *>(gp + int64_t(row) * a.gt_st + c0);
+      }
+  }
 
   bf16x8 qh[4][KS], ql[4][KS];
   const uint4 *qp = reinterpret_cast<const uint4 *>(cell + Lw.qp) + lane;
@@ -662,8 +677,12 @@ __global__ void __launch_bounds__(256) gdn_chunk_out(GdnArgs a, ChunkArgs ca, co
       qh[mt][ks] = __builtin_bit_cast(bf16x8, qp[((0 * 4 + mt) * KS + ks) * 64]);
       ql[mt][ks] = __builtin_bit_cast(bf16x8, qp[((1 * 4 + mt) * KS + ks) * 64]);
     }
-  TO *ob = static_cast<TO *>(a.o) + ci.batch * a.o_sb + h * a.o_sh + int64_t(ci.t0) * a.o_st;
-  for (int cg = w; cg < a.dv / 16; cg += 4) {
+  // O tiles of this wave's column groups cg = w + 4 i: lane holds O[16 mt + ln][16 cg + 4 g + r]
+  f32x4 res[kMaxCg][4];
+#pragma unroll
+  for (int i = 0; i < kMaxCg; ++i) {
+    const int cg = w + 4 * i;
+    if (cg >= ncg) break;
     const uint4 *sn = reinterpret_cast<const uint4 *>(cell + Lw.sn) + static_cast<size_t>(cg) * KS * 2 * 64 + lane;
     const f32x4 *op = reinterpret_cast<const f32x4 *>(cell + Lw.op) + static_cast<size_t>(cg) * 4 * 64 + lane;
     bf16x8 sh[KS], sl[KS];
@@ -684,21 +703,81 @@ __global__ void __launch_bounds__(256) gdn_chunk_out(GdnArgs a, ChunkArgs ca, co
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) acc[mt] = mma(sh[ks], qh[mt][ks], acc[mt]);
     }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) res[i][mt] = acc[mt];
+    if (a.o) {
+      TO *ob = static_cast<TO *>(a.o) + ci.batch * a.o_sb + h * a.o_sh + int64_t(ci.t0) * a.o_st;
+      const int c0 = 16 * cg + 4 * g;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const int row = 16 * mt + ln;
+        if (row >= ci.len) continue;
+        TO *dst = ob + int64_t(row) * a.o_st + c0;
+        if (vec_store) {
+          bf16x4 v;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = bf(acc[mt][r]);
+          *reinterpret_cast<bf16x4 *>(dst) = v;
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) st(dst + r, acc[mt][r]);
+        }
+      }
+    }
+  }
+  if (!a.gate) return;
+
+  // GatedRMSNorm of the head rows: sums of squares of the bf16-rounded O over this
+  // wave's columns, then over the lane groups and, through LDS, over the 4 waves.
+  __shared__ float sred[4][64];
+  float ss[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < kMaxCg; ++i) {
+    if (w + 4 * i >= ncg) break;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        res[i][mt][r] = fl(bf(res[i][mt][r]));
+        ss[mt] = fmaf(res[i][mt][r], res[i][mt][r], ss[mt]);
+      }
+  }
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    ss[mt] += __shfl_xor(ss[mt], 16, 64);
+    ss[mt] += __shfl_xor(ss[mt], 32, 64);
+  }
+  if (g == 0) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) sred[w][16 * mt + ln] = ss[mt];
+  }
+  __syncthreads();
+  float rs[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int row = 16 * mt + ln;
+    rs[mt] = rsqrtf((sred[0][row] + sred[1][row] + sred[2][row] + sred[3][row]) / a.dv + a.neps);
+  }
+  bf16_t *yb = static_cast<bf16_t *>(a.y) + ci.batch * a.y_sb + int64_t(ci.t0) * a.y_st + h * a.dv;
+#pragma unroll
+  for (int i = 0; i < kMaxCg; ++i) {
+    const int cg = w + 4 * i;
+    if (cg >= ncg) break;
     const int c0 = 16 * cg + 4 * g;
+    const uint2 wraw = *reinterpret_cast<const uint2 *>(static_cast<const bf16_t *>(a.nw) + c0);
+    const float wv[4] = {__uint_as_float(wraw.x << 16), __uint_as_float(wraw.x & 0xffff0000u),
+                         __uint_as_float(wraw.y << 16), __uint_as_float(wraw.y & 0xffff0000u)};
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
       const int row = 16 * mt + ln;
       if (row >= ci.len) continue;
-      TO *dst = ob + int64_t(row) * a.o_st + c0;
-      if (vec_store) {
-        bf16x4 v;
+      const float gf[4] = {__uint_as_float(gv[i][mt].x << 16), __uint_as_float(gv[i][mt].x & 0xffff0000u),
+                           __uint_as_float(gv[i][mt].y << 16), __uint_as_float(gv[i][mt].y & 0xffff0000u)};
+      bf16x4 v;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = bf(acc[mt][r]);
-        *reinterpret_cast<bf16x4 *>(dst) = v;
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) st(dst + r, acc[mt][r]);
-      }
+      for (int r = 0; r < 4; ++r)
+        v[r] = bf(fl(bf(fl(bf(res[i][mt][r] * rs[mt])) * wv[r])) * fl(bf(silu_fast(gf[r]))));
+      *reinterpret_cast<bf16x4 *>(yb + int64_t(row) * a.y_st + c0) = v;
     }
   }
 }

@@ -16,6 +16,12 @@ struct GdnArgs {
   float *s_out;
   void *o; int64_t o_sb, o_sh, o_st;
   int B, H, L, dk, dv;
+  // Optional GatedRMSNorm epilogue of the bf16 MFMA chunk path (gate == nullptr: off):
+  // y[b, t, h*dv + e] = T(T(T(o * rsqrt(mean_e o^2 + eps)) * w[e]) * T(silu(gate[b, t, h*dv + e])))
+  // with o rounded to T first; o itself is stored only when non-null.
+  const void *gate; int64_t gt_sb, gt_st;   // [B, L, H*dv]
+  const void *nw; float neps;               // [dv]
+  void *y; int64_t y_sb, y_st;              // [B, L, H*dv]
 };
 
 struct ChunkArgs {

@@ -38,6 +38,7 @@ from motif.ops import (
     short_conv_silu,
     short_conv_silu_varlen,
     chunk_gated_delta_rule_varlen,
+    chunk_gated_delta_rule_gated_norm,
 )
 
 
@@ -219,11 +220,19 @@ class GatedDeltaAttention(BasicAttention):
         q, k, v, (cq, ck, cv) = self._qkv((xq, xk, xv), tails, B, L)
         beta, g = self._gates(xa, xb)
 
-        if L == 1:
-            o, S = recurrent_gated_delta_rule(q, k, v, beta, g, S0)
+        fused = None
+        if L > 1 and self.o_norm.weight is not None:
+            fused = chunk_gated_delta_rule_gated_norm(q, k, v, beta, g, gate, self.o_norm.weight, self.o_norm.eps,
+                                                      S0, self.chunk_size)
+        if fused is not None:
+            y, S = fused
+            output = project(y, self.o_proj.weight, self.o_proj.bias)
         else:
-            o, S = chunk_gated_delta_rule(q, k, v, beta, g, S0, self.chunk_size)
-        output = self._output(o, gate, B, L)
+            if L == 1:
+                o, S = recurrent_gated_delta_rule(q, k, v, beta, g, S0)
+            else:
+                o, S = chunk_gated_delta_rule(q, k, v, beta, g, S0, self.chunk_size)
+            output = self._output(o, gate, B, L)
 
         if use_cache:
             past_key_value.update(S, (cq, ck, cv), steps=L)
@@ -243,6 +252,14 @@ class GatedDeltaAttention(BasicAttention):
         _, (xq, xk, xv, gate, xa, xb) = self._project(hidden_states)
         q, k, v, (cq, ck, cv) = self._qkv((xq, xk, xv), (None, None, None), B, L, cu_seqlens, max_len)
         beta, g = self._gates(xa, xb)
-        o, S = chunk_gated_delta_rule_varlen(q, k, v, beta, g, cu_seqlens, None, self.chunk_size)
-        output = self._output(o, gate, B, L)
+        fused = None
+        if self.o_norm.weight is not None:
+            fused = chunk_gated_delta_rule_gated_norm(q, k, v, beta, g, gate, self.o_norm.weight, self.o_norm.eps,
+                                                      None, self.chunk_size, cu_seqlens=cu_seqlens)
+        if fused is not None:
+            y, S = fused
+            output = project(y, self.o_proj.weight, self.o_proj.bias)
+        else:
+            o, S = chunk_gated_delta_rule_varlen(q, k, v, beta, g, cu_seqlens, None, self.chunk_size)
+            output = self._output(o, gate, B, L)
         return AttentionOutput(output=output, payload={'state': S, 'conv_state': (cq, ck, cv)})

@@ -13,6 +13,7 @@ from .gated_deltanet import (
     chunk_gated_delta_rule,
     chunk_gated_delta_rule_triton,
     chunk_gated_delta_rule_varlen,
+    chunk_gated_delta_rule_gated_norm,
 )
 from .short_conv import short_conv_silu, short_conv_silu_varlen
 from .attn_res import apply_block_attn_res, attn_res_read, attn_res_read_norms
@@ -26,7 +27,7 @@ __all__ = [
     'RMSNorm', 'GatedRMSNorm', 'SwiGLU',
     'apply_chord_attention', 'apply_chord_attention_varlen',
     'recurrent_gated_delta_rule', 'chunk_gated_delta_rule',
-    'chunk_gated_delta_rule_triton', 'chunk_gated_delta_rule_varlen',
+    'chunk_gated_delta_rule_triton', 'chunk_gated_delta_rule_varlen', 'chunk_gated_delta_rule_gated_norm',
     'short_conv_silu', 'short_conv_silu_varlen',
     'apply_block_attn_res', 'attn_res_read', 'attn_res_read_norms', 'gdn_decode_fused',
     'cat_weights', 'linear_rows', 'project', 'rows_eligible',

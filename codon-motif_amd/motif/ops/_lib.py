@@ -30,6 +30,9 @@ _SIGNATURES = {
     'motif_gdn_chunk_workspace_bytes': ([_I32] * 5, _SZ),
     'motif_gdn_chunk_fwd': (
         _T4 * 5 + [_P, _P] + _T4 + [_I32] * 6 + [_P, _P, _I32, _I32, _P, _SZ, _I32, _I32, _P], _I32),
+    'motif_gdn_chunk_fwd_gated': (
+        _T4 * 5 + [_P, _P] + _T4 + [_I32] * 6 + [_P, _P, _I32, _I32, _P, _SZ]
+        + [_P, _I64, _I64, _P, _F32, _P, _I64, _I64, _I32, _P], _I32),
     'motif_short_conv_silu': (
         [_P, _I64, _I64, _P, _P, _P, _P, _I64, _I64] + [_I32] * 4 + [_P, _I32, _I32, _I32, _P], _I32),
     'motif_gdn_decode_fused': (
@@ -95,14 +98,17 @@ def lib():
     return _lib
 
 
+ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP = 1, 2, 3
+
+
 def check(rc: int, what: str):
     '''Turn a non-zero motif_status into an exception (INVALID -> ValueError).'''
     if rc == 0:
         return
     msg = lib().motif_last_error().decode(errors='replace')
-    if rc == 1:
+    if rc == ERR_INVALID:
         raise ValueError(f'{what}: {msg}')
-    if rc == 2:
+    if rc == ERR_UNSUPPORTED:
         raise NotImplementedError(f'{what}: {msg}')
     raise RuntimeError(f'{what}: {msg}')
 

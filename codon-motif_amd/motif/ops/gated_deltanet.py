@@ -118,7 +118,10 @@ def gdn_recurrent_into(q, k, v, beta, g, S_in, S_out, o):
     _lib.check(rc, 'motif_gdn_recurrent_fwd')
 
 
-def _chunk_call(qc, kc, vc, bc, gc, S_in, C, cu=None, nseq=None):
+def _chunk_call(qc, kc, vc, bc, gc, S_in, C, cu=None, nseq=None, norm=None):
+    '''One chunk launch.  With `norm` = (gate [B, L, H*Dv], weight [Dv], eps) the
+    output is the GatedRMSNorm y [B, L, H*Dv] of the head outputs, fused into the
+    output pass (o is not stored); returns None when that fusion does not apply.'''
     B, H, L, Dk = qc.shape
     Dv = vc.shape[-1]
     dev = qc.device
@@ -137,11 +140,26 @@ def _chunk_call(qc, kc, vc, bc, gc, S_in, C, cu=None, nseq=None):
         total = int(coff[-1])
         cu_dev = cu_host.to(device=dev, dtype=torch.int32)
         coff_dev = coff.to(dev)
-    o = torch.empty(B, H, L, Dv, dtype=qc.dtype, device=dev)
     S_out = torch.empty(nseq, H, Dk, Dv, dtype=torch.float32, device=dev)
     nbytes = _lib.lib().motif_gdn_chunk_workspace_bytes(H, Dk, Dv, C, max(total, 1))
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     code = _lib.dtype_code(qc.dtype)
+    if norm is not None:
+        gate, weight, eps = norm
+        y = torch.empty(B, L, H * Dv, dtype=qc.dtype, device=dev)
+        rc = _lib.lib().motif_gdn_chunk_fwd_gated(
+            *_lib.t4(qc), *_lib.t4(kc), *_lib.t4(vc), *_lib.t4(bc), *_lib.t4(gc),
+            _lib.ptr(S_in), S_out.data_ptr(), 0, 0, 0, 0,
+            B, H, L, Dk, Dv, C,
+            _lib.ptr(cu_dev), _lib.ptr(coff_dev), nseq, total,
+            ws.data_ptr(), ws.numel(),
+            gate.data_ptr(), gate.stride(0), gate.stride(1), weight.data_ptr(), float(eps),
+            y.data_ptr(), y.stride(0), y.stride(1), code, _lib.stream_ptr(dev))
+        if rc == _lib.ERR_UNSUPPORTED:
+            return None
+        _lib.check(rc, 'motif_gdn_chunk_fwd_gated')
+        return y, S_out
+    o = torch.empty(B, H, L, Dv, dtype=qc.dtype, device=dev)
     rc = _lib.lib().motif_gdn_chunk_fwd(
         *_lib.t4(qc), *_lib.t4(kc), *_lib.t4(vc), *_lib.t4(bc), *_lib.t4(gc),
         _lib.ptr(S_in), S_out.data_ptr(), *_lib.t4(o),
@@ -172,6 +190,38 @@ def chunk_gated_delta_rule(q, k, v, beta, g, S=None, chunk_size=64):
     S_in = _state_in(S, B, H, Dk, vc.shape[-1], qc.device, name)
     o, S_out = _chunk_call(qc, kc, vc, bc, gc, S_in, _kernel_chunk(int(chunk_size)))
     return o.to(q.dtype), S_out
+
+
+def chunk_gated_delta_rule_gated_norm(q, k, v, beta, g, gate, norm_weight, norm_eps, S=None, chunk_size=64,
+                                      cu_seqlens=None):
+    '''The chunk rule with the GatedDeltaAttention output norm fused into its output
+    pass (no reference counterpart; replaces the chunk call plus the GatedRMSNorm of
+    motif/block/attention/gdn_attn.py:198-209).
+
+    Returns (y [B, L, H*Dv], S) where y = GatedRMSNorm(o; gate, norm_weight, norm_eps)
+    per head, or None when the fused kernel does not serve these inputs (bf16 MFMA
+    path only); the caller then runs the two steps separately.  `cu_seqlens` selects
+    the packed-sequence form (S then [nseq, H, Dk, Dv]).
+    '''
+    name = 'chunk_gated_delta_rule_gated_norm'
+    if q.dtype != torch.bfloat16 or gate.dtype != torch.bfloat16 or not q.is_cuda:
+        return None
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, beta, g, gate, norm_weight)):
+        return None
+    (qc, kc, vc, bc, gc), _ = _prepare(q, k, v, beta, g, name)
+    B, H, L, Dk = qc.shape
+    Dv = vc.shape[-1]
+    if gate.shape != (B, L, H * Dv) or gate.stride(-1) != 1:
+        return None
+    w = norm_weight.detach().to(torch.bfloat16).contiguous()
+    if cu_seqlens is None:
+        S_in = _state_in(S, B, H, Dk, Dv, qc.device, name)
+        return _chunk_call(qc, kc, vc, bc, gc, S_in, _kernel_chunk(int(chunk_size)), norm=(gate, w, norm_eps))
+    nseq = int(cu_seqlens.numel()) - 1
+    if B != 1 or nseq < 1 or S is not None:
+        return None
+    return _chunk_call(qc, kc, vc, bc, gc, None, _kernel_chunk(int(chunk_size)), cu_seqlens, nseq,
+                       norm=(gate, w, norm_eps))
 
 
 def chunk_gated_delta_rule_triton(q, k, v, beta, g, S=None, chunk_size=64):

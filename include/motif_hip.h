@@ -94,6 +94,32 @@ int motif_gdn_chunk_fwd(
     int in_dtype, int out_dtype, void *stream);
 
 /*
+ * motif_gdn_chunk_fwd with the layer's output norm fused into the output pass:
+ *   y[b,t,h*dv+e] = GatedRMSNorm(o[b,h,t,:]; gate[b,t,h*dv:(h+1)*dv], norm_weight, norm_eps)
+ * (o rounded to `dtype` first; y = T(T(T(o rsqrt(mean o^2 + eps)) w) T(silu(gate)))).
+ * Replaces the chunk call and the GatedRMSNorm of motif/block/attention/gdn_attn.py:
+ * 198-209 (motif/ops/rms_norm.py:530-553).  gate and y are [B,L,H*dv] (row strides
+ * gate_st / y_st, batch strides gate_sb / y_sb); o may be NULL (not stored).
+ * bf16 only, on the MFMA chunk path (chunk 64, dk in {32, 64}, dv % 16 == 0,
+ * dv <= 128); other shapes return MOTIF_ERR_UNSUPPORTED and the caller runs the
+ * two separate calls.
+ */
+int motif_gdn_chunk_fwd_gated(
+    const void *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void *k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void *v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    const void *beta, int64_t b_sb, int64_t b_sh, int64_t b_st,
+    const void *g, int64_t g_sb, int64_t g_sh, int64_t g_st,
+    const float *state_in, float *state_out,
+    void *o, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    int B, int H, int L, int dk, int dv, int chunk,
+    const int32_t *cu_seqlens, const int32_t *chunk_offsets, int nseq, int total_chunks,
+    void *workspace, size_t workspace_bytes,
+    const void *gate, int64_t gate_sb, int64_t gate_st, const void *norm_weight, float norm_eps,
+    void *y, int64_t y_sb, int64_t y_st,
+    int dtype, void *stream);
+
+/*
  * Short causal depthwise conv (kernel K) followed by SiLU.
  * Replaces motif/block/attention/gdn_attn.py:116-136 `GatedDeltaAttention._conv`.
  *   x [B,L,D] (strides x_sb, x_st; channel stride 1), weight [D,K] contiguous,

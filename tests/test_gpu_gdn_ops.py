@@ -102,6 +102,66 @@ def test_chunk_bf16_layer_shape():
     assert_state_close(S, rS, 1e-2, 'S')
 
 
+def _gated_inputs(B, H, T, dk, dv, seed):
+    q, k, v, b, g = gdn_inputs(B, H, T, dk, dv, seed=seed, dtype=torch.bfloat16)
+    gen = torch.Generator().manual_seed(seed + 100)
+    gate = torch.randn(B, T, H * dv, generator=gen).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(dv, generator=gen)).to(torch.bfloat16)
+    return q, k, v, b, g, gate, w
+
+
+@pytest.mark.parametrize('T', [512, 130, 1])
+def test_chunk_gated_norm_fused(T):
+    '''The chunk rule with the output GatedRMSNorm fused into its output pass equals
+    the two separate launches (chunk, then gated_rms_norm_heads) to one bf16 rounding,
+    and the fp64 oracle (chunk, o rounded to bf16, eager GatedRMSNorm) within the bf16 bar.'''
+    ops = _ops()
+    from motif.ops.epilogue import gated_rms_norm_heads
+    from oracle.gdn import gated_rms_norm
+    B, H, dk, dv = 2, 12, 64, 128
+    q, k, v, b, g, gate, w = _gated_inputs(B, H, T, dk, dv, seed=21)
+    dq, dk_, dv_, db, dg, dgate, dw = (t.to(DEV) for t in (q, k, v, b, g, gate, w))
+    y, S = ops.chunk_gated_delta_rule_gated_norm(dq, dk_, dv_, db, dg, dgate, dw, 1e-6)
+    o2, S2 = ops.chunk_gated_delta_rule(dq, dk_, dv_, db, dg)
+    y2 = gated_rms_norm_heads(o2, dgate, dw, 1e-6)
+    assert y.shape == (B, T, H * dv) and y.dtype == torch.bfloat16
+    assert torch.equal(S, S2)
+    d = (y.float() - y2.float()).abs()
+    assert d.max().item() <= 2 ** -7 * y2.float().abs().max().item(), d.max().item()
+    assert (d > 0).float().mean().item() < 0.01
+    ro, _ = _oracle_chunk(q, k, v, b, g)
+    ob = ro.to(torch.bfloat16).transpose(1, 2)                          # [B, T, H, dv]
+    ref = gated_rms_norm(torch.cat([ob, gate.view(B, T, H, dv)], -1), w, dv, 1e-6).reshape(B, T, H * dv)
+    # y reaches |y| ~ 10 (unit-RMS rows times silu(gate)): the bf16 bar is applied to
+    # y / max(1, max|ref| / 2), where one bf16 step of the largest values is < 1e-2
+    scale = max(1.0, ref.abs().max().item() / 2)
+    assert_bf16_close(y.double().cpu() / scale, ref.double() / scale, what='y')
+
+
+def test_chunk_gated_norm_fused_varlen():
+    ops = _ops()
+    from motif.ops.epilogue import gated_rms_norm_heads
+    lens = [70, 1, 200, 64, 33]
+    cu = torch.tensor([0] + list(torch.cumsum(torch.tensor(lens), 0)), dtype=torch.int32)
+    T = int(cu[-1])
+    q, k, v, b, g, gate, w = _gated_inputs(1, 4, T, 64, 128, seed=23)
+    args = [t.to(DEV) for t in (q, k, v, b, g)]
+    y, S = ops.chunk_gated_delta_rule_gated_norm(*args, gate.to(DEV), w.to(DEV), 1e-6, cu_seqlens=cu.to(DEV))
+    o2, S2 = ops.chunk_gated_delta_rule_varlen(*args, cu.to(DEV))
+    y2 = gated_rms_norm_heads(o2, gate.to(DEV), w.to(DEV), 1e-6)
+    assert torch.equal(S, S2)
+    d = (y.float() - y2.float()).abs()
+    assert d.max().item() <= 2 ** -7 * y2.float().abs().max().item(), d.max().item()
+
+
+def test_chunk_gated_norm_declines_fp32():
+    '''fp32 inputs are not served by the fused kernel: the op returns None.'''
+    ops = _ops()
+    q, k, v, b, g = (t.to(DEV) for t in gdn_inputs(1, 2, 80, 64, 128, seed=3))
+    gate = torch.randn(1, 80, 256, device=DEV)
+    assert ops.chunk_gated_delta_rule_gated_norm(q, k, v, b, g, gate, torch.ones(128, device=DEV), 1e-6) is None
+
+
 def test_chunk_triton_name_rejects_small_chunk():
     ops = _ops()
     q, k, v, b, g = (t.to(DEV) for t in gdn_inputs(1, 1, 8, 64, 64))
