@@ -23,6 +23,15 @@ struct ConvArgs {
   const int32_t *cu;
   int tch;  // timesteps per thread
   float scale;
+  int hd;    // vector kernel: head L2 normalisation on (HD channels a head) or off (0)
+};
+
+// Up to three independent conv problems (the GDN q, k, v front ends) in one launch of
+// the vector kernel: blocks [start[p], start[p + 1]) serve problem p.
+struct ConvGroup {
+  ConvArgs a[3];
+  int start[3];
+  int n;
 };
 
 constexpr int kConvStep = 16;  // timesteps per batch of loads (scalar kernel)
@@ -165,11 +174,17 @@ template <> struct Vec16<float> {
 };
 
 template <typename T, int K, int HD>
-__global__ void __launch_bounds__(256) short_conv_silu_vec_kernel(ConvArgs a) {
+__global__ void __launch_bounds__(256) short_conv_silu_vec_kernel(ConvGroup grp) {
   constexpr int E = Vec16<T>::E;
   constexpr int G = HD / E;  // lanes per head (HD > 0)
+  // this block's problem (selects on uniform values: no indexed copy of the group)
+  const int bx = blockIdx.x;
+  const int p = (grp.n > 2 && bx >= grp.start[2]) ? 2 : (grp.n > 1 && bx >= grp.start[1]) ? 1 : 0;
+  const ConvArgs a = p == 2 ? grp.a[2] : p == 1 ? grp.a[1] : grp.a[0];
+  const int blk = bx - (p == 2 ? grp.start[2] : p == 1 ? grp.start[1] : 0);
+  const bool norm = HD > 0 && a.hd > 0;
   const int nc = a.D / E;
-  const int idx = blockIdx.x * 256 + threadIdx.x;
+  const int idx = blk * 256 + threadIdx.x;
   const int sq = blockIdx.y;
   const int c = idx % nc, tb = idx / nc;
   int batch, t_begin, len;
@@ -273,7 +288,7 @@ __global__ void __launch_bounds__(256) short_conv_silu_vec_kernel(ConvArgs a) {
       for (int r = 0; r < K - 2; ++r) win[r][e] = win[r + 1][e];
       win[K - 2][e] = xt[e];
     }
-    if (HD > 0) {
+    if (norm) {
 #pragma unroll
       for (int off = 1; off < G; off <<= 1) ss += __shfl_xor(ss, off, 64);
       const float f = a.scale * rcp_fast(fmaxf(sqrtf(ss), 1e-12f));
@@ -297,18 +312,32 @@ __global__ void __launch_bounds__(256) short_conv_silu_vec_kernel(ConvArgs a) {
 }
 
 template <typename T, int HD>
-static int launch_conv_vec(const ConvArgs &a, int K, int nseq, int max_len, hipStream_t s) {
-  const int nc = a.D / Vec16<T>::E;
+static int launch_conv_group(ConvGroup g, int K, int nseq, int max_len, hipStream_t s) {
   const int ntb = max(1, (max_len + kVecStep - 1) / kVecStep);
-  const dim3 grid(static_cast<unsigned>((static_cast<int64_t>(nc) * ntb + 255) / 256), nseq), block(256);
+  int64_t blocks = 0;
+  for (int p = 0; p < g.n; ++p) {
+    g.start[p] = static_cast<int>(blocks);
+    blocks += (static_cast<int64_t>(g.a[p].D / Vec16<T>::E) * ntb + 255) / 256;
+  }
+  if (blocks > (int64_t(1) << 30)) return set_error(MOTIF_ERR_UNSUPPORTED, "short_conv_silu: grid too large");
+  const dim3 grid(static_cast<unsigned>(blocks), nseq), block(256);
   switch (K) {
-    case 2: short_conv_silu_vec_kernel<T, 2, HD><<<grid, block, 0, s>>>(a); break;
-    case 3: short_conv_silu_vec_kernel<T, 3, HD><<<grid, block, 0, s>>>(a); break;
-    case 4: short_conv_silu_vec_kernel<T, 4, HD><<<grid, block, 0, s>>>(a); break;
-    case 5: short_conv_silu_vec_kernel<T, 5, HD><<<grid, block, 0, s>>>(a); break;
+    case 2: short_conv_silu_vec_kernel<T, 2, HD><<<grid, block, 0, s>>>(g); break;
+    case 3: short_conv_silu_vec_kernel<T, 3, HD><<<grid, block, 0, s>>>(g); break;
+    case 4: short_conv_silu_vec_kernel<T, 4, HD><<<grid, block, 0, s>>>(g); break;
+    case 5: short_conv_silu_vec_kernel<T, 5, HD><<<grid, block, 0, s>>>(g); break;
     default: return set_error(MOTIF_ERR_UNSUPPORTED, "short_conv_silu: K must be in {2, 3, 4, 5}");
   }
   return check_launch("short_conv_silu_vec_kernel");
+}
+
+template <typename T, int HD>
+static int launch_conv_vec(ConvArgs a, int K, int nseq, int max_len, hipStream_t s) {
+  ConvGroup g;
+  a.hd = HD;
+  g.a[0] = a;
+  g.n = 1;
+  return launch_conv_group<T, HD>(g, K, nseq, max_len, s);
 }
 
 template <typename T, int HD>
@@ -416,4 +445,62 @@ extern "C" int motif_short_conv_silu_l2norm(
     return set_error(MOTIF_ERR_UNSUPPORTED, "short_conv_silu_l2norm: head_dim must be 16, 32 or 64");
   return conv_entry(x, x_sb, x_st, weight, tail_in, tail_out, y, y_sb, y_st, B, L, D, K, cu_seqlens, nseq,
                     max_seqlen, head_dim, scale, dtype, stream);
+}
+
+template <typename T>
+static int launch_multi(ConvGroup g, int K, int nseq, int max_len, int hd, hipStream_t s) {
+  switch (hd) {
+    case 0: return launch_conv_group<T, 0>(g, K, nseq, max_len, s);
+    case 16: return launch_conv_group<T, 16>(g, K, nseq, max_len, s);
+    case 32: return launch_conv_group<T, 32>(g, K, nseq, max_len, s);
+    case 64: return launch_conv_group<T, 64>(g, K, nseq, max_len, s);
+  }
+  return set_error(MOTIF_ERR_UNSUPPORTED, "short_conv_silu_multi: head_dim must be 0, 16, 32 or 64");
+}
+
+extern "C" int motif_short_conv_silu_multi(
+    int n, const void *const *x, const int64_t *x_sb, const int64_t *x_st,
+    const void *const *weight, const void *const *tail_in, void *const *tail_out,
+    void *const *y, const int64_t *y_sb, const int64_t *y_st,
+    const int *D, const int *head_dim, const float *scale,
+    int B, int L, int K,
+    const int32_t *cu_seqlens, int nseq, int max_seqlen,
+    int dtype, void *stream) {
+  if (n < 1 || n > 3 || !x || !x_sb || !x_st || !weight || !tail_in || !tail_out || !y || !y_sb || !y_st || !D ||
+      !head_dim || !scale)
+    return set_error(MOTIF_ERR_INVALID, "short_conv_silu_multi: n must be 1..3 and the arrays non-NULL");
+  if (B < 1 || L < 1 || K < 2 || K > 5 || nseq < 1 || max_seqlen < 1)
+    return set_error(MOTIF_ERR_UNSUPPORTED, "short_conv_silu_multi: needs tokens and K in 2..5");
+  const bool packed = cu_seqlens != nullptr;
+  if (packed && B != 1) return set_error(MOTIF_ERR_INVALID, "short_conv_silu_multi: packed sequences need B == 1");
+  if (!packed && (nseq != B || max_seqlen != L))
+    return set_error(MOTIF_ERR_INVALID, "short_conv_silu_multi: padded batches need nseq == B and max_seqlen == L");
+  if (dtype != MOTIF_F32 && dtype != MOTIF_BF16) return set_error(MOTIF_ERR_UNSUPPORTED, "short_conv_silu_multi: dtype");
+  const int E = dtype == MOTIF_BF16 ? 8 : 4;
+  ConvGroup g;
+  g.n = n;
+  int hd = 0;
+  for (int p = 0; p < n; ++p) {
+    if (!x[p] || !weight[p] || !y[p] || D[p] <= 0)
+      return set_error(MOTIF_ERR_INVALID, "short_conv_silu_multi: NULL pointer or empty channel range");
+    // the vector kernel only: 16-byte rows, separate tails, one head size for the
+    // normalised problems
+    const uintptr_t al = reinterpret_cast<uintptr_t>(x[p]) | reinterpret_cast<uintptr_t>(y[p]) |
+                         reinterpret_cast<uintptr_t>(weight[p]) | reinterpret_cast<uintptr_t>(tail_in[p]) |
+                         reinterpret_cast<uintptr_t>(tail_out[p]);
+    const int h = head_dim[p];
+    if ((al & 15) || (tail_out[p] && tail_out[p] == tail_in[p]) || D[p] % E || ((x_sb[p] | x_st[p] | y_sb[p] | y_st[p]) % E) ||
+        (h != 0 && (h % E || D[p] % h || (hd != 0 && h != hd))))
+      return set_error(MOTIF_ERR_UNSUPPORTED, "short_conv_silu_multi: problem not served by the vector kernel");
+    if (h) hd = h;
+    ConvArgs &a = g.a[p];
+    a.x = x[p]; a.x_sb = x_sb[p]; a.x_st = x_st[p];
+    a.w = weight[p]; a.tail_in = tail_in[p]; a.tail_out = tail_out[p];
+    a.y = y[p]; a.y_sb = y_sb[p]; a.y_st = y_st[p];
+    a.B = B; a.L = L; a.D = D[p]; a.cu = cu_seqlens;
+    a.scale = scale[p]; a.tch = kConvStep; a.hd = h;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return dtype == MOTIF_BF16 ? launch_multi<bf16_t>(g, K, nseq, max_seqlen, hd, s)
+                             : launch_multi<float>(g, K, nseq, max_seqlen, hd, s);
 }

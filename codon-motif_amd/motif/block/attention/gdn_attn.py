@@ -39,6 +39,7 @@ from motif.ops import (
     short_conv_silu_varlen,
     chunk_gated_delta_rule_varlen,
     chunk_gated_delta_rule_gated_norm,
+    short_conv_silu_multi,
 )
 
 
@@ -135,6 +136,13 @@ class GatedDeltaAttention(BasicAttention):
         hd = self.dk if fused else None
         ws = (self.q_conv.weight, self.k_conv.weight, self.v_conv.weight)
         opts = ((hd, self.dk ** -0.5), (hd, 1.0), (None, 1.0))
+        outs = None
+        if xs[0].is_cuda and not (torch.is_grad_enabled() and any(w.requires_grad for w in ws)):
+            outs = short_conv_silu_multi(xs, ws, tails, [o[0] for o in opts], [o[1] for o in opts],
+                                         cu_seqlens, max_len)
+        if outs is not None:
+            q, k, v = self._heads(outs[0][0], outs[1][0], outs[2][0], B, L, normalized=fused)
+            return q, k, v, tuple(o[1] for o in outs)
         outs = []
         for i in range(3):
             if cu_seqlens is None:

@@ -15,7 +15,7 @@ from .gated_deltanet import (
     chunk_gated_delta_rule_varlen,
     chunk_gated_delta_rule_gated_norm,
 )
-from .short_conv import short_conv_silu, short_conv_silu_varlen
+from .short_conv import short_conv_silu, short_conv_silu_multi, short_conv_silu_varlen
 from .attn_res import apply_block_attn_res, attn_res_read, attn_res_read_norms
 from .gdn_decode import gdn_decode_fused
 from .linear_rows import cat_weights, linear_rows, project, rows_eligible
@@ -28,7 +28,7 @@ __all__ = [
     'apply_chord_attention', 'apply_chord_attention_varlen',
     'recurrent_gated_delta_rule', 'chunk_gated_delta_rule',
     'chunk_gated_delta_rule_triton', 'chunk_gated_delta_rule_varlen', 'chunk_gated_delta_rule_gated_norm',
-    'short_conv_silu', 'short_conv_silu_varlen',
+    'short_conv_silu', 'short_conv_silu_multi', 'short_conv_silu_varlen',
     'apply_block_attn_res', 'attn_res_read', 'attn_res_read_norms', 'gdn_decode_fused',
     'cat_weights', 'linear_rows', 'project', 'rows_eligible',
     'HAS_TRITON', 'HAS_HIP',

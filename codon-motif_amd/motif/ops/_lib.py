@@ -35,6 +35,8 @@ _SIGNATURES = {
         + [_P, _I64, _I64, _P, _F32, _P, _I64, _I64, _I32, _P], _I32),
     'motif_short_conv_silu': (
         [_P, _I64, _I64, _P, _P, _P, _P, _I64, _I64] + [_I32] * 4 + [_P, _I32, _I32, _I32, _P], _I32),
+    'motif_short_conv_silu_multi': (
+        [_I32] + [_P] * 12 + [_I32] * 3 + [_P, _I32, _I32, _I32, _P], _I32),
     'motif_gdn_decode_fused': (
         [_P, _I64] + [_I32] * 6 + [_P] * 9 + [_F32, _P, _P, _I64] + [_I32] * 6 + [_P], _I32),
     'motif_linear_rows': (

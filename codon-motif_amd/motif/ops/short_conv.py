@@ -6,6 +6,8 @@ axis, y = SiLU(depthwise_conv1d(xc)), new cache = the last K-1 pre-activation
 inputs of xc.  Inputs stay in the [B, L, D] layout the projections produce (no
 transposes); the cache keeps the reference layout [B, D, K-1].
 '''
+import ctypes
+
 import torch
 
 from . import _lib
@@ -89,3 +91,62 @@ def short_conv_silu_varlen(x, weight, cu_seqlens, max_seqlen=None, head_dim=None
     tails = torch.empty(nseq, D, K - 1, dtype=x.dtype, device=x.device)
     _conv_call(x, w, None, tails, y, cu_dev, nseq, int(max_seqlen), head_dim, scale)
     return y, tails
+
+
+def short_conv_silu_multi(xs, weights, caches, head_dims, scales, cu_seqlens=None, max_seqlen=None):
+    '''Several conv + SiLU problems over the same tokens in one launch (the GDN q, k, v
+    front ends; no reference counterpart).  Problem i is
+    `short_conv_silu(xs[i], weights[i], caches[i], head_dim=head_dims[i], scale=scales[i])`
+    (or the `_varlen` form when `cu_seqlens` is given).
+
+    Returns the list of (y, new_cache) pairs, or None when the single-launch kernel does
+    not serve these inputs (the caller then makes the separate calls).
+    '''
+    n = len(xs)
+    x0 = xs[0]
+    if not 1 <= n <= 3 or not x0.is_cuda or x0.dtype not in (torch.bfloat16, torch.float32):
+        return None
+    B, L = x0.shape[0], x0.shape[1]
+    K = weights[0].shape[-1]
+    if L < 1 or any(x.shape[:2] != (B, L) or x.dtype != x0.dtype or x.stride(-1) != 1 for x in xs):
+        return None
+    if any(w.shape[-1] != K or w.numel() != x.shape[-1] * K for w, x in zip(weights, xs)):
+        return None
+    dev, dt = x0.device, x0.dtype
+    ws = [w.detach().reshape(x.shape[-1], K).to(dt).contiguous() for w, x in zip(weights, xs)]
+    if cu_seqlens is None:
+        nseq, max_len, cu_dev = B, L, None
+        cs = []
+        for c, x in zip(caches, xs):
+            if c is not None and (c.shape != (B, x.shape[-1], K - 1) or c.dtype != dt or not c.is_contiguous()):
+                return None
+            cs.append(c)
+    else:
+        if B != 1:
+            return None
+        cu_host = cu_seqlens.detach().to('cpu', torch.int64)
+        nseq = int(cu_host.numel()) - 1
+        if nseq < 1:
+            return None
+        max_len = int(max_seqlen) if max_seqlen is not None else int((cu_host[1:] - cu_host[:-1]).max())
+        if max_len < 1:
+            return None
+        cu_dev = cu_host.to(device=dev, dtype=torch.int32)
+        cs = [None] * n
+    ys = [torch.empty(B, L, x.shape[-1], dtype=dt, device=dev) for x in xs]
+    tails = [torch.empty(nseq, x.shape[-1], K - 1, dtype=dt, device=dev) for x in xs]
+    arr = lambda ct, vals: (ct * n)(*vals)
+    rc = _lib.lib().motif_short_conv_silu_multi(
+        n, arr(ctypes.c_void_p, [x.data_ptr() for x in xs]),
+        arr(ctypes.c_int64, [x.stride(0) for x in xs]), arr(ctypes.c_int64, [x.stride(1) for x in xs]),
+        arr(ctypes.c_void_p, [w.data_ptr() for w in ws]), arr(ctypes.c_void_p, [_lib.ptr(c) for c in cs]),
+        arr(ctypes.c_void_p, [t.data_ptr() for t in tails]), arr(ctypes.c_void_p, [y.data_ptr() for y in ys]),
+        arr(ctypes.c_int64, [y.stride(0) for y in ys]), arr(ctypes.c_int64, [y.stride(1) for y in ys]),
+        arr(ctypes.c_int, [x.shape[-1] for x in xs]), arr(ctypes.c_int, [int(h or 0) for h in head_dims]),
+        arr(ctypes.c_float, [float(sc) for sc in scales]),
+        B, L, K, _lib.ptr(cu_dev), nseq, max_len, _lib.dtype_code(dt), _lib.stream_ptr(dev))
+    if rc == _lib.ERR_UNSUPPORTED:
+        return None
+    _lib.check(rc, 'motif_short_conv_silu_multi')
+    return list(zip(ys, tails))
+

@@ -156,6 +156,25 @@ int motif_short_conv_silu_l2norm(
     int head_dim, float scale, int dtype, void *stream);
 
 /*
+ * Up to three conv + SiLU problems in one launch (the GDN q, k and v front ends of
+ * motif/block/attention/gdn_attn.py:116-136, :190-191): problem p is the call
+ * motif_short_conv_silu_l2norm(x[p], x_sb[p], x_st[p], weight[p], tail_in[p],
+ * tail_out[p], y[p], y_sb[p], y_st[p], B, L, D[p], K, ..., head_dim[p], scale[p])
+ * with head_dim[p] == 0 meaning no normalisation.  All arrays hold n host values.
+ * Served only where the 16-byte vector kernel applies (16-byte aligned rows and
+ * tails, tail_out != tail_in, one head size among the normalised problems, L >= 1);
+ * otherwise MOTIF_ERR_UNSUPPORTED and the caller makes the separate calls.
+ */
+int motif_short_conv_silu_multi(
+    int n, const void *const *x, const int64_t *x_sb, const int64_t *x_st,
+    const void *const *weight, const void *const *tail_in, void *const *tail_out,
+    void *const *y, const int64_t *y_sb, const int64_t *y_st,
+    const int *D, const int *head_dim, const float *scale,
+    int B, int L, int K,
+    const int32_t *cu_seqlens, int nseq, int max_seqlen,
+    int dtype, void *stream);
+
+/*
  * Workspace bytes needed by motif_chord_fwd (split-K partials); also returns
  * the split count the launcher will use in *splits (may be NULL).
  */

@@ -270,3 +270,42 @@ def test_short_conv_silu_l2norm_varlen():
     ry = torch.nn.functional.normalize(ry.view(1, -1, 2, 64), dim=-1).view(1, -1, D) * 0.125
     assert_fp32_close(y, ry, 1e-5, 'y')
     assert_fp32_close(tails, rt, 0.0, 'tails')
+
+
+@pytest.mark.parametrize('cache', [False, True])
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32])
+def test_short_conv_silu_multi_equals_separate(cache, dtype):
+    '''The GDN q / k / v front ends in one launch give the same bits as three calls.'''
+    ops = _ops()
+    gen = torch.Generator().manual_seed(31)
+    B, L, K = 2, 77, 4
+    Ds, hds, scales = (768, 768, 1536), (64, 64, None), (64 ** -0.5, 1.0, 1.0)
+    proj = torch.randn(B, L, sum(Ds) + 40, generator=gen).to(dtype).to(DEV)   # q | k | v | rest
+    offs = (0, 768, 1536)
+    xs = [proj[..., o:o + D] for o, D in zip(offs, Ds)]
+    ws = [(torch.randn(D, 1, K, generator=gen) * 0.3).to(dtype).to(DEV) for D in Ds]
+    cs = [(torch.randn(B, D, K - 1, generator=gen) * 0.5).to(dtype).to(DEV) if cache else None for D in Ds]
+    outs = ops.short_conv_silu_multi(xs, ws, cs, hds, scales)
+    assert outs is not None
+    for i in range(3):
+        y, t = ops.short_conv_silu(xs[i], ws[i], cs[i], head_dim=hds[i], scale=scales[i])
+        assert torch.equal(outs[i][0], y), i
+        assert torch.equal(outs[i][1], t), i
+
+
+def test_short_conv_silu_multi_varlen():
+    ops = _ops()
+    gen = torch.Generator().manual_seed(33)
+    lens = [70, 1, 200, 3]
+    cu = torch.tensor([0] + list(torch.cumsum(torch.tensor(lens), 0)), dtype=torch.int32)
+    T, K = int(cu[-1]), 4
+    Ds, hds, scales = (128, 128, 256), (64, 64, None), (0.125, 1.0, 1.0)
+    xs = [torch.randn(1, T, D, generator=gen).to(torch.bfloat16).to(DEV) for D in Ds]
+    ws = [(torch.randn(D, 1, K, generator=gen) * 0.3).to(torch.bfloat16).to(DEV) for D in Ds]
+    outs = ops.short_conv_silu_multi(xs, ws, [None] * 3, hds, scales, cu.to(DEV))
+    assert outs is not None
+    for i in range(3):
+        y, t = ops.short_conv_silu_varlen(xs[i], ws[i], cu.to(DEV), head_dim=hds[i], scale=scales[i])
+        assert torch.equal(outs[i][0], y), i
+        assert torch.equal(outs[i][1], t), i
+
