@@ -5,9 +5,10 @@
 // reference's fused read (motif/ops/attn_res.py:22-55 `_ar_logit`, :94-186) and
 // its eager form (motif/ops/attn_res.py:588-593).
 //
-// One wavefront per token; every source row is read once (16-byte loads) and kept
-// in registers for the weighted sum, so the op moves (nsrc + 1) * D elements per
-// token -- HBM-bound.
+// 32 lanes per token (64 for rows of more than 128 16-byte pieces); every source row
+// is read once (16-byte loads) and kept in registers for the weighted sum, so the op
+// moves (nsrc + 1) * D elements per token -- HBM-bound.  Row sums use DPP and lane
+// swaps, not LDS.
 #include "capi_internal.h"
 #include "common.h"
 
@@ -71,13 +72,33 @@ template <typename T> __device__ __forceinline__ float round_to(float v);
 template <> __device__ __forceinline__ float round_to<float>(float v) { return v; }
 template <> __device__ __forceinline__ float round_to<bf16_t>(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
-// PPL: 16-byte pieces per lane (D <= 64 * PPL * Piece::N).
-template <typename T, int PPL>
+// Sum over the LPT-lane group of a lane (LPT = 32 or 64) with DPP and lane swaps: no
+// LDS traffic, a few cycles per step.
+template <int LPT>
+__device__ __forceinline__ float group_sum(float x) {
+  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x141, 0xF, 0xF, false));  // row_half_mirror
+  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x140, 0xF, 0xF, false));  // row_mirror
+  const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
+  if (LPT == 64) {
+    const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
+  }
+  return x;
+}
+
+// LPT lanes per token (64 / LPT tokens per wave), PPL 16-byte pieces per lane
+// (D <= LPT * PPL * Piece::N).  Every lane of a wave takes part in the group sums;
+// lanes of tokens past the end compute on zeros and store nothing.
+template <typename T, int LPT, int PPL>
 __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
   constexpr int E = Piece<T>::N;
-  const int lane = threadIdx.x & 63;
-  const int tok = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (tok >= a.B * a.T) return;
+  const int sub = threadIdx.x & (LPT - 1);
+  const int tok_raw = blockIdx.x * (256 / LPT) + threadIdx.x / LPT;
+  const bool tok_ok = tok_raw < a.B * a.T;
+  const int tok = tok_ok ? tok_raw : 0;
   const int b = tok / a.T, t = tok - b * a.T;
   const int np = a.D / E;
 
@@ -87,8 +108,8 @@ __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
 #pragma unroll
   for (int i = 0; i < PPL; ++i) {
     float qv[E], wv[E];
-    Piece<T>::unpack(buf_ld16(qb, (lane + 64 * i) * 16), qv);
-    Piece<T>::unpack(buf_ld16(wb, (lane + 64 * i) * 16), wv);
+    Piece<T>::unpack(buf_ld16(qb, (sub + LPT * i) * 16), qv);
+    Piece<T>::unpack(buf_ld16(wb, (sub + LPT * i) * 16), wv);
 #pragma unroll
     for (int e = 0; e < E; ++e) qw[i][e] = qv[e] * wv[e];
   }
@@ -102,7 +123,7 @@ __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
     const buf_t row = make_buf(static_cast<const T *>(a.src[n]) + b * a.sb[n] + int64_t(t) * a.st[n],
                                dbytes);
 #pragma unroll
-    for (int i = 0; i < PPL; ++i) Piece<T>::unpack(buf_ld16(row, (lane + 64 * i) * 16), x[n][i]);
+    for (int i = 0; i < PPL; ++i) Piece<T>::unpack(buf_ld16(row, (sub + LPT * i) * 16), x[n][i]);
   }
   float logit[kMaxSrc];
   float mx = -INFINITY;
@@ -118,8 +139,8 @@ __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
           ss = fmaf(x[n][i][e], x[n][i][e], ss);
           dot = fmaf(x[n][i][e], qw[i][e], dot);
         }
-      ss = wave_sum(ss);
-      dot = wave_sum(dot);
+      ss = group_sum<LPT>(ss);
+      dot = group_sum<LPT>(dot);
       logit[n] = dot * rsqrtf(ss / a.D + a.eps);
       mx = fmaxf(mx, logit[n]);
     }
@@ -134,10 +155,8 @@ __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
   float h[PPL][E];
 #pragma unroll
   for (int i = 0; i < PPL; ++i) {
-    const int p = lane + 64 * i;
 #pragma unroll
     for (int e = 0; e < E; ++e) h[i][e] = 0.f;
-    if (p >= np) continue;
 #pragma unroll
     for (int n = 0; n < kMaxSrc; ++n)
       if (n < a.nsrc) {
@@ -145,17 +164,18 @@ __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
         for (int e = 0; e < E; ++e) h[i][e] = fmaf(alpha[n] * inv, x[n][i][e], h[i][e]);
       }
   }
-  if (a.out) {
+  if (a.out && tok_ok) {
     T *orow = static_cast<T *>(a.out) + b * a.ob + int64_t(t) * a.ot;
 #pragma unroll
     for (int i = 0; i < PPL; ++i) {
-      const int p = lane + 64 * i;
+      const int p = sub + LPT * i;
       if (p < np) Piece<T>::store(orow + p * E, h[i]);
     }
   }
   if (a.nnorm == 0) return;
   // RMSNorm of h as the reference computes it on the stored h (rms_norm.py:481-486):
-  // y = T(h * rsqrt(mean(h^2) + eps)) * weight, the product rounded to T.
+  // y = T(h * rsqrt(mean(h^2) + eps)) * weight, the product rounded to T (pieces past
+  // D hold h = 0 and add nothing).
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < PPL; ++i)
@@ -164,14 +184,15 @@ __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
       h[i][e] = round_to<T>(h[i][e]);
       ss = fmaf(h[i][e], h[i][e], ss);
     }
-  const float r = rsqrtf(wave_sum(ss) / a.D + a.neps);
+  const float r = rsqrtf(group_sum<LPT>(ss) / a.D + a.neps);
+  if (!tok_ok) return;
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     if (k >= a.nnorm) break;
     T *nrow = static_cast<T *>(a.nout[k]) + b * a.nb[k] + int64_t(t) * a.nt[k];
 #pragma unroll
     for (int i = 0; i < PPL; ++i) {
-      const int p = lane + 64 * i;
+      const int p = sub + LPT * i;
       if (p >= np) continue;
       float w[E], y[E];
       Piece<T>::unpack(buf_ld16(make_buf(a.nw[k], dbytes), p * 16), w);
@@ -182,16 +203,26 @@ __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
   }
 }
 
+template <typename T, int LPT>
+int launch_lpt(const AttnResArgs &a, int ppl, hipStream_t s) {
+  const dim3 grid((a.B * a.T + 256 / LPT - 1) / (256 / LPT)), block(256);
+  switch (ppl) {
+    case 1: attn_res_kernel<T, LPT, 1><<<grid, block, 0, s>>>(a); break;
+    case 2: attn_res_kernel<T, LPT, 2><<<grid, block, 0, s>>>(a); break;
+    case 3: attn_res_kernel<T, LPT, 3><<<grid, block, 0, s>>>(a); break;
+    case 4: attn_res_kernel<T, LPT, 4><<<grid, block, 0, s>>>(a); break;
+    default: return set_error(MOTIF_ERR_UNSUPPORTED, "attn_res_read: D too large (at most 256 16-byte pieces)");
+  }
+  return check_launch("attn_res_kernel");
+}
+
 template <typename T>
 int launch(const AttnResArgs &a, hipStream_t s) {
   constexpr int E = Piece<T>::N;
   const int np = a.D / E;
-  const dim3 grid((a.B * a.T + 3) / 4), block(256);
-  if (np <= 64) attn_res_kernel<T, 1><<<grid, block, 0, s>>>(a);
-  else if (np <= 128) attn_res_kernel<T, 2><<<grid, block, 0, s>>>(a);
-  else if (np <= 256) attn_res_kernel<T, 4><<<grid, block, 0, s>>>(a);
-  else return set_error(MOTIF_ERR_UNSUPPORTED, "attn_res_read: D too large (at most 256 16-byte pieces)");
-  return check_launch("attn_res_kernel");
+  // two tokens a wave (32 lanes each) up to 128 pieces, else one
+  if (np <= 128) return launch_lpt<T, 32>(a, (np + 31) / 32, s);
+  return launch_lpt<T, 64>(a, (np + 63) / 64, s);
 }
 
 }  // namespace

@@ -214,9 +214,8 @@ __global__ void __launch_bounds__(256) short_conv_silu_vec_kernel(ConvGroup grp)
 #pragma unroll
   for (int i = 0; i < K - 1 + kVecStep; ++i)
     raw[i] = buf_ld16(xbuf, static_cast<uint32_t>(((t_lo - (K - 1) + i) * a.x_st + d0) * sizeof(T)));
-  // The E channels' taps (E * K contiguous values = K 16-byte pieces) and their
-  // cached tails (K - 1 pieces), as 16-byte loads.
-  float wr[E][K], tv[E][K - 1];
+  // The E channels' taps (E * K contiguous values = K 16-byte pieces).
+  float wr[E][K];
   {
     const T *wp = static_cast<const T *>(a.w) + d0 * K;
     float wf[E * K];
@@ -226,51 +225,25 @@ __global__ void __launch_bounds__(256) short_conv_silu_vec_kernel(ConvGroup grp)
     for (int e = 0; e < E; ++e)
 #pragma unroll
       for (int r = 0; r < K; ++r) wr[e][r] = wf[e * K + r];
-    float tf[E * (K - 1)];
-#pragma unroll
-    for (int j = 0; j < K - 1; ++j) {
-      if (has_tail) Vec16<T>::unpack(*reinterpret_cast<const uint4 *>(tail0 + j * E), tf + j * E);
-      else {
-#pragma unroll
-        for (int e = 0; e < E; ++e) tf[j * E + e] = 0.f;
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < E; ++e)
-#pragma unroll
-      for (int u = 0; u < K - 1; ++u) tv[e][u] = tf[e * (K - 1) + u];
   }
   __builtin_amdgcn_sched_barrier(0);  // keep the loads above as one batch
 
-  // window: positions t_lo-K+1 .. t_lo-1; before the sequence start -> tail entries
+  // window: positions t_lo-K+1 .. t_lo-1 (rows before the sequence start read 0; with
+  // a cached tail the first run takes them from tail_in)
   float win[K - 1][E];
 #pragma unroll
-  for (int r = 0; r < K - 1; ++r) {
-    const int pos = t_lo - (K - 1) + r;
-    float xv[E];
-    Vec16<T>::unpack(raw[r], xv);
+  for (int r = 0; r < K - 1; ++r) Vec16<T>::unpack(raw[r], win[r]);
+  if (has_tail && t_lo < K - 1) {
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      float tw = 0.f;
+    for (int r = 0; r < K - 1; ++r) {
+      const int u = t_lo + r;  // tail entry of position t_lo - (K - 1) + r
+      if (u < K - 1) {
 #pragma unroll
-      for (int u = 0; u < K - 1; ++u) tw = (pos + K - 1 == u) ? tv[e][u] : tw;
-      win[r][e] = pos >= 0 ? xv[e] : tw;
+        for (int e = 0; e < E; ++e) win[r][e] = ld(tail0 + e * (K - 1) + u);
+      }
     }
   }
   const bool last_run = t_hi == len;
-  // entries of the last K-1 positions that come from tail_in (before any write)
-  float tail_keep[K - 1][E];
-#pragma unroll
-  for (int r = 0; r < K - 1; ++r) {
-    const int pk = len - (K - 1) + r;
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      float tk = 0.f;
-#pragma unroll
-      for (int u = 0; u < K - 1; ++u) tk = (pk + K - 1 == u) ? tv[e][u] : tk;
-      tail_keep[r][e] = pk < 0 ? tk : 0.f;
-    }
-  }
 
 #pragma unroll
   for (int i = 0; i < kVecStep; ++i) {
@@ -305,8 +278,10 @@ __global__ void __launch_bounds__(256) short_conv_silu_vec_kernel(ConvGroup grp)
       const int pos = len - (K - 1) + r;
       float xv[E];
       Vec16<T>::unpack(buf_ld16(xbuf, static_cast<uint32_t>((pos * a.x_st + d0) * sizeof(T))), xv);
+      // positions before the sequence start keep the incoming tail entries (0 without one)
 #pragma unroll
-      for (int e = 0; e < E; ++e) st(to + e * (K - 1) + r, pos >= 0 ? xv[e] : tail_keep[r][e]);
+      for (int e = 0; e < E; ++e)
+        st(to + e * (K - 1) + r, pos >= 0 ? xv[e] : has_tail ? ld(tail0 + e * (K - 1) + pos + K - 1) : 0.f);
     }
   }
 }
