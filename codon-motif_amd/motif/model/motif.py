@@ -2,11 +2,14 @@
 
 Same module tree and parameter names as the reference (motif/model/motif.py:154-630:
 embed, blocks, norm, tied lm_head) and the same forward contract
-(input_ids, cache, labels, mask, position) -> ModelOutput.  Generation,
-sampling and checkpoint IO are outside this build.
+(input_ids, cache, labels, mask, position) -> ModelOutput, and the checkpoint
+entry points `from_pretrained` / `save_pretrained` (motif/model/motif.py:237-380
+over motif/model/checkpoint.py).  Generation and sampling are outside this build.
 '''
+import dataclasses
+import os
 from dataclasses import dataclass
-from typing import Optional, Union
+from typing import Dict, Optional, Union
 
 import torch
 import torch.nn as nn
@@ -44,6 +47,58 @@ class MotifChordModel(nn.Module):
         self.lm_head = nn.Linear(config.model_dim, config.vocab_size, bias=False)
         if config.tied_weight:
             self.embed.weight = self.lm_head.weight
+
+    @classmethod
+    def from_pretrained(cls, path: str, config: Optional[Union[MotifChordConfig, Dict, str]] = None,
+                        map_location: Union[str, torch.device] = 'cpu',
+                        device: Optional[Union[str, torch.device]] = None, strict: bool = False,
+                        verbose: bool = True, **overrides) -> 'MotifChordModel':
+        '''Build the model a checkpoint describes and load its weights (eval mode).
+
+        The config comes from `config` (a MotifChordConfig, a mapping or a JSON file
+        path), else from the file, else from the tensor shapes
+        (`config_from_state_dict`); `**overrides` replace fields of the result.  A
+        tied model whose file lacks `lm_head.weight` takes it from `embed.weight`.
+        `strict` fails on missing / unexpected keys instead of reporting them.
+        '''
+        from motif.model.checkpoint import _as_config, config_from_state_dict, load_checkpoint
+        loaded = load_checkpoint(path, map_location=map_location)
+        sd = dict(loaded.state_dict)
+        if isinstance(config, str):
+            with open(config, 'r', encoding='utf-8') as fh:
+                import json
+                config = json.load(fh)
+        cfg = _as_config(config) if config is not None else None
+        if config is not None and cfg is None:
+            raise TypeError(f'config must be a MotifChordConfig, a mapping or a JSON path, got {type(config).__name__}')
+        cfg = cfg or loaded.config or config_from_state_dict(sd)
+        if overrides:
+            known = {f.name for f in dataclasses.fields(MotifChordConfig)}
+            unknown = sorted(set(overrides) - known)
+            if unknown:
+                raise TypeError(f'unknown MotifChordConfig override(s): {unknown}')
+            cfg = dataclasses.replace(cfg, **overrides)
+        model = cls(cfg)
+        if cfg.tied_weight and 'lm_head.weight' not in sd and 'embed.weight' in sd:
+            sd['lm_head.weight'] = sd['embed.weight']
+        try:
+            report = model.load_state_dict(sd, strict=False)
+        except RuntimeError as exc:
+            raise RuntimeError(f'{os.fspath(path)!r} does not match the model built from {cfg!r}: {exc}') from exc
+        if strict and (report.missing_keys or report.unexpected_keys):
+            raise RuntimeError(f'{os.fspath(path)!r}: missing {report.missing_keys}, '
+                               f'unexpected {report.unexpected_keys}')
+        if verbose:
+            print(f'[motif] {loaded.source} {os.fspath(path)}: {len(sd)} tensors, '
+                  f'{len(report.missing_keys)} missing, {len(report.unexpected_keys)} unexpected')
+        if device is not None:
+            model = model.to(device)
+        return model.eval()
+
+    def save_pretrained(self, path: str, metadata: Optional[Dict] = None) -> Dict:
+        '''Write the weights and config to one `.safetensors` file.'''
+        from motif.model.checkpoint import save_safetensors
+        return save_safetensors(self, path, self.config, metadata)
 
     def count_param(self) -> int:
         return sum(p.numel() for p in {id(p): p for p in self.parameters()}.values())
