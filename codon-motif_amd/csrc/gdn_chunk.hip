@@ -14,7 +14,8 @@
 // gdn_state_scan carries S across the chunks, one workgroup per (16 state columns,
 // head, sequence) with one wave per 16-row tile of S in accumulator registers (the
 // tiles meet in LDS once per chunk) and a six-chunk-deep register prefetch of
-// A_n / H_n; it writes every S_n as MFMA operands.  gdn_chunk_out then
+// A_n / H_n (the workgroups of one head share an XCD, so A_n is read from HBM once
+// and from that XCD's L2 after); it writes every S_n as MFMA operands.  gdn_chunk_out then
 // forms O_n = O' + Q' S_n for all chunks in parallel.
 //
 // The workspace holds A_n, Q', H_n, O' and S_n in the order the consuming kernel's
@@ -549,10 +550,25 @@ __device__ __forceinline__ void scan_load(ScanStage<DK> &st, const char *cell, c
 // buffered: one barrier per chunk) and forms its tile of S_{n+1} = A_n S_n + H_n: a
 // chain of 3 (DK / 32) MFMAs per wave instead of 3 DK^2 / 512 for one wave per column
 // group.
+// Workgroups of a scan launch: ngroups (head, sequence) groups of ncg column-group
+// workgroups that all read the same A_n.  Workgroups go to the 8 XCDs round-robin by
+// linear id, so a group is placed on one XCD (its A_n then comes from that XCD's L2
+// after the first read): linear id L runs on XCD L % 8, and slot L / 8 of that XCD
+// holds column group slot % ncg of group 8 (slot / ncg) + L % 8.  The grid is padded
+// to whole groups per XCD; padding workgroups exit at once.
+struct ScanGrid {
+  int ncg, ngroups;
+  static constexpr int kXcd = 8;
+  int blocks() const { return kXcd * ((ngroups + kXcd - 1) / kXcd) * ncg; }
+};
+
 template <int DK>
-__global__ void __launch_bounds__(64 * (DK / 16)) gdn_state_scan(GdnArgs a, ChunkArgs ca, char *ws) {
+__global__ void __launch_bounds__(64 * (DK / 16)) gdn_state_scan(GdnArgs a, ChunkArgs ca, char *ws, ScanGrid sgrid) {
   constexpr int TDK = DK / 16, KS = DK / 32;
-  const int cg = blockIdx.x, h = blockIdx.y, sq = blockIdx.z;
+  const int slot = blockIdx.x / ScanGrid::kXcd;
+  const int group = (slot / sgrid.ncg) * ScanGrid::kXcd + blockIdx.x % ScanGrid::kXcd;
+  if (group >= sgrid.ngroups) return;
+  const int cg = slot % sgrid.ncg, h = group % a.H, sq = group / a.H;
   const int lane = threadIdx.x & 63, mt = threadIdx.x >> 6;
   const int ln = lane & 15, g = lane >> 4;
   const int col = 16 * cg + ln;
@@ -800,7 +816,8 @@ int launch_dk(const GdnArgs &a, const ChunkArgs &ca, char *ws, hipStream_t s) {
   if (a.dv <= 64) rc = launch_prep<DK, 64>(a, ca, ws, s);
   else rc = launch_prep<DK, 128>(a, ca, ws, s);
   if (rc) return rc;
-  gdn_state_scan<DK><<<dim3(a.dv / 16, a.H, ca.nseq), dim3(64 * (DK / 16)), 0, s>>>(a, ca, ws);
+  const ScanGrid sgrid{a.dv / 16, a.H * ca.nseq};
+  gdn_state_scan<DK><<<sgrid.blocks(), dim3(64 * (DK / 16)), 0, s>>>(a, ca, ws, sgrid);
   if ((rc = check_launch("gdn_state_scan"))) return rc;
   // 8-byte output stores when every row start is 8-byte aligned
   const int vec = ((a.o_sb | a.o_sh | a.o_st) & 3) == 0 && (reinterpret_cast<uintptr_t>(a.o) & 7) == 0;

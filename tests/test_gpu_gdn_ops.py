@@ -102,6 +102,32 @@ def test_chunk_bf16_layer_shape():
     assert_state_close(S, rS, 1e-2, 'S')
 
 
+@pytest.mark.parametrize('B,H,T,init', [(2, 3, 1100, False), (1, 2, 1024, True), (1, 2, 4096, True)])
+def test_chunk_bf16_long_sequences(B, H, T, init):
+    '''Long sequences on the bf16 MFMA path (18 chunks with a partial last one, 16, and
+    the model's 64), from zero or a given state, against the fp64 oracle.'''
+    ops = _ops()
+    q, k, v, b, g = gdn_inputs(B, H, T, 64, 128, seed=31 + T, dtype=torch.bfloat16)
+    S0 = torch.randn(B, H, 64, 128, generator=torch.Generator().manual_seed(5)) * 0.1 if init else None
+    o, S = ops.chunk_gated_delta_rule(*(t.to(DEV) for t in (q, k, v, b, g)), None if S0 is None else S0.to(DEV))
+    ro, rS = _oracle_chunk(q, k, v, b, g, S0)
+    assert_bf16_close(o, ro, what='o')
+    assert_state_close(S, rS, 1e-2, 'S')
+
+
+def test_chunk_bf16_batch_equals_packed():
+    '''A fixed-length batch row and the same sequence packed (cu_seqlens) give the same
+    result on the bf16 MFMA path (the scan groups differ: batch rows vs sequences).'''
+    ops = _ops()
+    T = 2100
+    q, k, v, b, g = (t.to(DEV) for t in gdn_inputs(1, 4, T, 64, 128, seed=41, dtype=torch.bfloat16))
+    o2, S2 = ops.chunk_gated_delta_rule(q, k, v, b, g)
+    cu = torch.tensor([0, T], dtype=torch.int32, device=DEV)
+    o1, S1 = ops.chunk_gated_delta_rule_varlen(q, k, v, b, g, cu)
+    assert torch.equal(o2, o1)
+    assert torch.equal(S2, S1)
+
+
 def _gated_inputs(B, H, T, dk, dv, seed):
     q, k, v, b, g = gdn_inputs(B, H, T, dk, dv, seed=seed, dtype=torch.bfloat16)
     gen = torch.Generator().manual_seed(seed + 100)
