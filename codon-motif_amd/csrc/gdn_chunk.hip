@@ -115,19 +115,32 @@ __device__ __forceinline__ bf16x4 rd4s(const __bf16 *p, int row, int col) {
 __device__ __forceinline__ bf16x8 rd_perm_s(const __bf16 *p, int row, int k0, int g) {
   return __builtin_shufflevector(rd4s(p, row, k0 + 4 * g), rd4s(p, row, k0 + 16 + 4 * g), 0, 1, 2, 3, 4, 5, 6, 7);
 }
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+// two floats -> packed bf16 pair (round to nearest even), one instruction
+__device__ __forceinline__ uint32_t pk_bf16(float x0, float x1) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v){x0, x1}, bf16x2v));
+}
+// hi = RNE(x), lo = RNE(x - hi) for a pair, as packed words
+__device__ __forceinline__ void split2(float x0, float x1, uint32_t &h, uint32_t &l) {
+  h = pk_bf16(x0, x1);
+  l = pk_bf16(x0 - __uint_as_float(h << 16), x1 - __uint_as_float(h & 0xffff0000u));
+}
 __device__ __forceinline__ void split4(const float *x, bf16x4 &h, bf16x4 &l) {
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    h[t] = bf(x[t]);
-    l[t] = bf(x[t] - fl(h[t]));
-  }
+  uint2 hw, lw;
+  split2(x[0], x[1], hw.x, lw.x);
+  split2(x[2], x[3], hw.y, lw.y);
+  h = __builtin_bit_cast(bf16x4, hw);
+  l = __builtin_bit_cast(bf16x4, lw);
 }
 __device__ __forceinline__ void split8(const float *x, bf16x8 &h, bf16x8 &l) {
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    h[t] = bf(x[t]);
-    l[t] = bf(x[t] - fl(h[t]));
-  }
+  uint4 hw, lw;
+  split2(x[0], x[1], hw.x, lw.x);
+  split2(x[2], x[3], hw.y, lw.y);
+  split2(x[4], x[5], hw.z, lw.z);
+  split2(x[6], x[7], hw.w, lw.w);
+  h = __builtin_bit_cast(bf16x8, hw);
+  l = __builtin_bit_cast(bf16x8, lw);
 }
 __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
   return static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
@@ -399,9 +412,10 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
       const int d = 8 * kseg + t;
       *reinterpret_cast<uint32_t *>(kt + swz(d, j)) = pack2(bits(ka[t]), bits(kb_[t]));
       const float x0 = fl(ka[t]) * f0, x1 = fl(kb_[t]) * f1;
-      const __bf16 h0 = bf(x0), h1 = bf(x1);
-      *reinterpret_cast<uint32_t *>(ktt_h + swz(d, j)) = pack2(bits(h0), bits(h1));
-      *reinterpret_cast<uint32_t *>(ktt_l + swz(d, j)) = pack2(bits(bf(x0 - fl(h0))), bits(bf(x1 - fl(h1))));
+      uint32_t hw, lw;
+      split2(x0, x1, hw, lw);
+      *reinterpret_cast<uint32_t *>(ktt_h + swz(d, j)) = hw;
+      *reinterpret_cast<uint32_t *>(ktt_l + swz(d, j)) = lw;
     }
   }
 #pragma unroll
