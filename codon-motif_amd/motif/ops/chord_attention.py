@@ -14,6 +14,7 @@ from typing import Optional
 import torch
 
 from . import _lib
+from .autograd_path import chord_attention_torch
 
 HEAD_DIM = 64
 
@@ -129,9 +130,16 @@ def apply_chord_attention(
 
     Raises:
         ValueError: on unsupported inputs or a negative q_start.
-        NotImplementedError: for inputs requiring grad, fp16 inputs or D != 64.
+        NotImplementedError: for fp16 inputs or D != 64 (inputs requiring grad take
+            the differentiable torch form).
         RuntimeError: when the HIP library is unavailable or a launch fails.
     '''
+    needs_grad = torch.is_grad_enabled() and any(
+        t.requires_grad for t in (q, k, v, alpha, beta, mu, ssmax))
+    if needs_grad:  # forward-only kernels: training takes the differentiable torch form
+        if q_start is not None and int(q_start) < 0:
+            raise ValueError(f'q_start must not be negative, got {q_start}')
+        return chord_attention_torch(q, k, v, alpha, beta, mu, ssmax, log_n, q_start, softmax_scale, eps)
     if not _lib.available():
         raise RuntimeError('there is no usable HIP backend in the current environment')
     B, H, L, D, Hkv, S = _check_tensors(q, k, v, log_n)
@@ -143,10 +151,6 @@ def apply_chord_attention(
     q_start = int(q_start)
     if q_start < 0:
         raise ValueError(f'q_start must not be negative, got {q_start}')
-    needs_grad = torch.is_grad_enabled() and any(
-        t.requires_grad for t in (q, k, v, alpha, beta, mu, ssmax))
-    if needs_grad:
-        raise NotImplementedError('apply_chord_attention: backward is not implemented by the HIP kernels')
     out = torch.empty((B, H, L, D), dtype=q.dtype, device=q.device)
     if L == 0:
         return out

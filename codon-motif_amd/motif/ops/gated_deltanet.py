@@ -17,6 +17,13 @@ autograd raises NotImplementedError.
 import torch
 
 from . import _lib
+from .autograd_path import gdn_chunk_torch
+
+
+def _needs_grad(*ts):
+    '''True when autograd must see this call (training): the HIP kernels are
+    forward-only, so such calls take the differentiable torch form.'''
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
 
 __all__ = [
     'recurrent_gated_delta_rule',
@@ -92,6 +99,8 @@ def recurrent_gated_delta_rule(q, k, v, beta, g, S=None):
         (o [B, H, L, Dv] in q's dtype, S [B, H, Dk, Dv] fp32)
     '''
     name = 'recurrent_gated_delta_rule'
+    if _needs_grad(q, k, v, beta, g, S):
+        return gdn_chunk_torch(q, k, v, beta, g, S)
     (qc, kc, vc, bc, gc), cdt = _prepare(q, k, v, beta, g, name)
     B, H, L, Dk = qc.shape
     Dv = vc.shape[-1]
@@ -185,6 +194,8 @@ def chunk_gated_delta_rule(q, k, v, beta, g, S=None, chunk_size=64):
         (o [B, H, L, Dv] in q's dtype, S [B, H, Dk, Dv] fp32)
     '''
     name = 'chunk_gated_delta_rule'
+    if _needs_grad(q, k, v, beta, g, S):
+        return gdn_chunk_torch(q, k, v, beta, g, S, chunk_size)
     (qc, kc, vc, bc, gc), _ = _prepare(q, k, v, beta, g, name)
     B, H, L, Dk = qc.shape
     S_in = _state_in(S, B, H, Dk, vc.shape[-1], qc.device, name)
@@ -249,6 +260,16 @@ def chunk_gated_delta_rule_varlen(q, k, v, beta, g, cu_seqlens, S=None, chunk_si
         (o [1, H, L, Dv] in q's dtype, S [nseq, H, Dk, Dv] fp32)
     '''
     name = 'chunk_gated_delta_rule_varlen'
+    if _needs_grad(q, k, v, beta, g, S):
+        cu = [int(c) for c in cu_seqlens.detach().cpu()]
+        outs, states = [], []
+        for i in range(len(cu) - 1):
+            sl = slice(cu[i], cu[i + 1])
+            o_i, S_i = gdn_chunk_torch(q[:, :, sl], k[:, :, sl], v[:, :, sl], beta[:, :, sl], g[:, :, sl],
+                                       None if S is None else S[i:i + 1], chunk_size)
+            outs.append(o_i)
+            states.append(S_i)
+        return torch.cat(outs, 2), torch.cat(states, 0)
     (qc, kc, vc, bc, gc), _ = _prepare(q, k, v, beta, g, name)
     B, H, L, Dk = qc.shape
     if B != 1:

@@ -11,6 +11,7 @@ import ctypes
 import torch
 
 from . import _lib
+from .autograd_path import short_conv_silu_torch
 
 
 def _conv_call(x, w, cache, new_cache, y, cu, nseq, max_len, head_dim, scale):
@@ -44,6 +45,13 @@ def short_conv_silu(x, weight, cache=None, y=None, new_cache=None, head_dim=None
     Returns:
         (y [B, L, D], new_cache [B, D, K-1])
     '''
+    if torch.is_grad_enabled() and (x.requires_grad or weight.requires_grad):
+        # forward-only kernel: training takes the differentiable torch form
+        y_, tail = short_conv_silu_torch(x, weight, cache, head_dim, scale)
+        if new_cache is not None:
+            new_cache.copy_(tail.detach())
+            tail = new_cache
+        return y_, tail
     if not x.is_cuda:
         raise ValueError('short_conv_silu: x must live on the ROCm device')
     B, L, D = x.shape
@@ -72,6 +80,12 @@ def short_conv_silu_varlen(x, weight, cu_seqlens, max_seqlen=None, head_dim=None
     Returns:
         (y [1, T, D], tails [nseq, D, K-1])
     '''
+    if torch.is_grad_enabled() and (x.requires_grad or weight.requires_grad):
+        # per sequence in the differentiable torch form (training)
+        cu = [int(c) for c in cu_seqlens.detach().cpu()]
+        parts = [short_conv_silu_torch(x[:, cu[i]:cu[i + 1]], weight, None, head_dim, scale)
+                 for i in range(len(cu) - 1)]
+        return torch.cat([p[0] for p in parts], 1), torch.cat([p[1] for p in parts], 0)
     if not x.is_cuda:
         raise ValueError('short_conv_silu_varlen: x must live on the ROCm device')
     B, L, D = x.shape
