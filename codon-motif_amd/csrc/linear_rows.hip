@@ -211,19 +211,23 @@ int launch_tile(LinArgs a, hipStream_t s) {
 }
 
 // Tile choice: rows per tile 16 MT (MT = 4, 2, 1) and W tiles NT (2, or 1 when the
-// epilogue allows it), the largest tile whose grid still has about 256 workgroups.
+// epilogue allows it), the largest tile whose grid still has enough workgroups: 100
+// (200 for SWIGLU, whose tiles carry a value and a gate half).  Measured at M = 64,
+// K = 768: N = 4632 7.0 us with 145 whole-row tiles vs 8.1 us with 290 half-row tiles,
+// N = 2304 5.1 vs 6.4 us; SWIGLU N = 4096 5.5 us with 256 half-row tiles vs 7.0 with 128.
 template <int EPI>
 int launch_epi(const LinArgs &a, hipStream_t s) {
   const int nout = EPI == EPI_SWIGLU ? a.N / 2 : a.N;
   const int cols2 = EPI == EPI_SWIGLU ? 16 : 32;  // output columns of an NT = 2 tile
+  const int enough = EPI == EPI_SWIGLU ? 200 : 100;
   auto wgs = [&](int mt, int cols) { return ((a.M + 16 * mt - 1) / (16 * mt)) * ((nout + cols - 1) / cols); };
   const int mtmax = a.M > 32 ? 4 : (a.M > 16 ? 2 : 1);
-  if (mtmax >= 4 && wgs(4, cols2) >= 200) return launch_tile<4, 2, EPI>(a, s);
-  if (mtmax >= 2 && wgs(2, cols2) >= 200) return launch_tile<2, 2, EPI>(a, s);
+  if (mtmax >= 4 && wgs(4, cols2) >= enough) return launch_tile<4, 2, EPI>(a, s);
+  if (mtmax >= 2 && wgs(2, cols2) >= enough) return launch_tile<2, 2, EPI>(a, s);
   if constexpr (EPI == EPI_SWIGLU) {
     return launch_tile<1, 2, EPI>(a, s);  // a value tile and its gate tile
   } else {
-    if (wgs(1, cols2) >= 200) return launch_tile<1, 2, EPI>(a, s);
+    if (wgs(1, cols2) >= enough) return launch_tile<1, 2, EPI>(a, s);
     return launch_tile<1, 1, EPI>(a, s);
   }
 }
