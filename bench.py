@@ -43,20 +43,13 @@ def log(msg):
 
 
 def bench_config(vocab=32000):
-    from motif.model.config import MotifChordConfig
-    return MotifChordConfig(vocab_size=vocab, model_dim=768, num_heads=12, num_kv_heads=3,
-                            head_k_dim=64, block=('gdn', 'gdn', 'gdn', 'chord'), block_n=4)
+    from motif.model.presets import config_172m
+    return config_172m(vocab)
 
 
 def init_model(model, std=0.02, seed=0):
-    import torch
-    import torch.nn as nn
-    g = torch.Generator().manual_seed(seed)
-    with torch.no_grad():
-        for m in model.modules():
-            if isinstance(m, (nn.Linear, nn.Embedding, nn.Conv1d)):
-                m.weight.copy_(torch.randn(m.weight.shape, generator=g) * std)
-    return model
+    from motif.model.presets import init_random
+    return init_random(model, std, seed)
 
 
 def cuda_time(fn, steps, warmup):
@@ -216,35 +209,26 @@ def measured_traffic(op):
 
 
 def make_decode_cache(model, B, ctx, capacity, dev, dtype, seed=1):
-    '''Caches as after a ctx-token prefill, filled with random values (timing only).'''
+    '''Fixed-capacity caches as after a ctx-token prefill, filled with random values
+    (timing only): keys / values ~ 0.5 N(0, 1), states ~ 0.05 N(0, 1), tails ~ 0.5 N(0, 1).'''
     import torch
 
-    from motif.model.cache import (DecoderBlockCache, GatedDeltaAttentionLayerCache, ModelCache,
-                                   StaticKVLayerCache)
+    from motif.model.cache import ModelCache, StaticKVLayerCache
     g = torch.Generator().manual_seed(seed)
-    blocks = []
-    for block in model.blocks:
-        attn = []
-        for dec in block.features:
-            a = dec.attn
-            if dec.attn_type == 'chord':
-                c = StaticKVLayerCache().allocate(B, a.num_kv_heads, capacity, a.head_dim, dev, dtype)
-                c.k[:, :, :ctx].copy_((torch.randn(B, a.num_kv_heads, ctx, a.head_dim, generator=g) * 0.5).to(dtype))
-                c.v[:, :, :ctx].copy_((torch.randn(B, a.num_kv_heads, ctx, a.head_dim, generator=g) * 0.5).to(dtype))
-                c.length = ctx
-                c.length_dev.fill_(ctx)
-            else:
-                c = GatedDeltaAttentionLayerCache()
-                c.state = (torch.randn(B, a.num_heads, a.dk, a.dv, generator=g) * 0.05).to(dev)
-                c.conv_state = tuple((torch.randn(B, n, a.conv_size - 1, generator=g) * 0.5).to(dev, dtype)
-                                     for n in (a.num_heads * a.dk, a.num_heads * a.dk, a.num_heads * a.dv))
-                c.length = ctx
-            attn.append(c)
-        bc = DecoderBlockCache(attn=attn)
-        bc.attn_res.seq_len = ctx
-        bc.attn_res.blocks = [torch.zeros(B, 1, model.config.model_dim, device=dev, dtype=dtype)]
-        blocks.append(bc)
-    return ModelCache(blocks=blocks)
+    cache = ModelCache.for_decode(model, B, capacity, dev, dtype)
+    for lc in cache.layer_caches():
+        if isinstance(lc, StaticKVLayerCache):
+            shape = (B, lc._slab[0].shape[1], ctx, lc._slab[0].shape[3])
+            lc.fill((torch.randn(shape, generator=g) * 0.5).to(dev, dtype),
+                    (torch.randn(shape, generator=g) * 0.5).to(dev, dtype))
+        else:
+            lc.state.copy_(torch.randn(lc.state.shape, generator=g) * 0.05)
+            for t in lc.conv_state:
+                t.copy_(torch.randn(t.shape, generator=g) * 0.5)
+            lc.length = ctx
+    for b in cache.blocks:
+        b.attn_res.seq_len = ctx
+    return cache
 
 
 def cpu_baseline(T=4096, seed=0):
@@ -370,37 +354,26 @@ def main():
         f'logits equal eager: {graph_ok}')
     del pgraph, pout, eager_logits
 
-    log('[bench] decode B=64 ctx=4096 (hipGraph)')
+    log('[bench] decode B=64 ctx=4096 (one captured step replayed token after token)')
+    from motif.model.decode_graph import DecodeGraph
     Bd, ctx = args.decode_batch, 4096
-    dec_model = model
-    cache = make_decode_cache(dec_model, Bd, ctx, ctx + 8, dev, torch.bfloat16)
-    tok = torch.randint(0, cfg.vocab_size, (Bd, 1), generator=torch.Generator().manual_seed(1)).to(dev)
-    lengths = [[c.length for c in b.attn] for b in cache.blocks]
-
-    def rewind():
-        for b, ls in zip(cache.blocks, lengths):
-            for c, n in zip(b.attn, ls):
-                c.length = n
-            b.attn_res.seq_len = ctx
-
+    n_dec = max(args.steps * 5, 20)
+    cache = make_decode_cache(model, Bd, ctx, ctx + n_dec + 16, dev, torch.bfloat16)
+    toks = torch.randint(0, cfg.vocab_size, (n_dec + 8, Bd, 1), generator=torch.Generator().manual_seed(1)).to(dev)
     with torch.no_grad():
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            for _ in range(2):
-                rewind()
-                dec_model(tok, cache=cache)
-        torch.cuda.current_stream().wait_stream(s)
+        graph = DecodeGraph(model, cache, Bd)
+        for i in range(3):
+            graph.step(toks[i])
         torch.cuda.synchronize()
-        rewind()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            out = dec_model(tok, cache=cache)
-        rewind()
-        dec_ms = cuda_time(graph.replay, max(args.steps * 5, 20), 3)
+        ev0.record()
+        for i in range(n_dec):
+            graph.step(toks[3 + i])
+        ev1.record()
+        torch.cuda.synchronize()
+    dec_ms = ev0.elapsed_time(ev1) / n_dec
     decode_tok_s = Bd / (dec_ms * 1e-3)
-    log(f'[bench] decode {dec_ms:.3f} ms/step ({decode_tok_s:.0f} tok/s)')
-    del out, graph
+    log(f'[bench] decode {dec_ms:.3f} ms/step ({decode_tok_s:.0f} tok/s), context {ctx} -> {cache.seq_len}')
+    del graph, cache
 
     log('[bench] kernel timings')
     with torch.no_grad():
@@ -435,8 +408,10 @@ def main():
                           'note': 'the same forward launched from Python each step'},
         'prefill_graph_matches_eager': graph_ok,
         'decode': {'tok_s': round(decode_tok_s, 1), 'ms_per_step': round(dec_ms, 4), 'batch': Bd,
-                   'context': ctx, 'note': 'config 4: one hipGraph-captured decode step replayed; '
-                                           'caches random-filled to 4096 positions (timing only)'},
+                   'context': ctx, 'steps': n_dec,
+                   'note': 'config 4: one decode step captured as a hipGraph and replayed token after token '
+                           '(device-resident cache cursors, no host rewinds; the context grows from 4096 by one '
+                           'position per step); caches random-filled to 4096 positions (timing only)'},
         'roofline': roofline,
         'kernels': {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in kern.items()},

@@ -28,6 +28,6 @@ int zero_async(void *p, size_t n, hipStream_t s) {
 
 }  // namespace motif
 
-extern "C" int motif_abi_version(void) { return 1; }
+extern "C" int motif_abi_version(void) { return 2; }
 
 extern "C" const char *motif_last_error(void) { return motif::g_last_error.c_str(); }

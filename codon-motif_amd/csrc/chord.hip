@@ -24,6 +24,7 @@
 #include <type_traits>
 
 #include "capi_internal.h"
+#include "chord_internal.h"
 #include "common.h"
 
 namespace motif {
@@ -43,7 +44,25 @@ struct ChordArgs {
   float *part;        // [B][Hkv][splits][L * group][D + 2]
   int splits;         // key-range splits (decode kernel)
   int nqc;            // row chunks per (batch, kv head) (decode kernel)
+  // device cursor (decode kernels): when set, *len_dev positions are cached, the L
+  // new keys sit at [*len_dev, *len_dev + L), S holds the cache capacity, and the
+  // merge pass advances *len_dev by L
+  int *len_dev;
+  const float *log_tab;  // ln(1 .. n) when log_n is NULL: log_n[b, i] = log_tab[q_start + i]
 };
+
+// Keys and query start of a decode launch: from the host arguments, or from the
+// device cursor (clamped so the window stays inside the capacity).
+struct DecodeWindow { int S, q_start; };
+__device__ __forceinline__ DecodeWindow decode_window(const ChordArgs &a) {
+  if (!a.len_dev) return {min(a.S, a.q_start + a.L), a.q_start};
+  const int cached = min(max(__builtin_amdgcn_readfirstlane(*a.len_dev), 0), a.S - a.L);
+  return {cached + a.L, cached};
+}
+
+__device__ __forceinline__ float log_n_at(const ChordArgs &a, int b, int i, int q_start) {
+  return a.log_n ? a.log_n[b * a.ln_sb + int64_t(i) * a.ln_st] : a.log_tab[q_start + i];
+}
 
 constexpr int kD = 64;        // head dim
 constexpr int kBN = 64;       // keys per tile
@@ -500,11 +519,12 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a, const fl
   const T *qg = static_cast<const T *>(a.q);
   T *og = static_cast<T *>(a.out);
 
-  const int kv_len = min(a.S, a.q_start + a.L);
+  const DecodeWindow win = decode_window(a);
+  const int kv_len = win.S, q_start = win.q_start;
   const int per = ((kv_len + a.splits - 1) / a.splits + kBN - 1) / kBN * kBN;
   const int i_last = min(a.L - 1, (qc * R + R - 1) / group);
   const int k_lo = split * per;
-  const int k_hi = min(min(kv_len, k_lo + per), a.q_start + i_last + 1);
+  const int k_hi = min(min(kv_len, k_lo + per), q_start + i_last + 1);
 
   Row8<T> q[R];
   float c_qk[R], c_b[R];
@@ -517,10 +537,10 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a, const fl
     const int head = kvh * group + (ok ? gr % group : 0);
     const int i = ok ? gr / group : 0;
     q[r].load(qg + b * a.q_sb + head * a.q_sh + int64_t(i) * a.q_st + dc);
-    const float mul = ok ? a.ssmax[head] * a.log_n[b * a.ln_sb + int64_t(i) * a.ln_st] : 0.f;
+    const float mul = ok ? a.ssmax[head] * log_n_at(a, b, i, q_start) : 0.f;
     c_qk[r] = mul * a.scale * kLog2e;
     c_b[r] = mul;  // the table is in log2 units already
-    qabs[r] = ok ? a.q_start + i : -1;
+    qabs[r] = ok ? q_start + i : -1;
     tb[r] = make_buf(tab + static_cast<size_t>(head) * tab_n, static_cast<uint32_t>(tab_n) * 4u);
   }
 
@@ -653,7 +673,7 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a, const fl
       o += sacc[ww][r][d] * f;
       Ls += sl[ww][r] * f;
     }
-    if (a.splits == 1) {
+    if (!a.part) {
       const int head = kvh * group + gr % group, i = gr / group;
       st(og + b * a.o_sb + head * a.o_sh + int64_t(i) * a.o_st + d, o / fmaxf(Ls, 1e-20f));
       if (a.lse && d == 0) a.lse[(static_cast<size_t>(b) * a.H + head) * a.L + i] = M + fast_log2(Ls);
@@ -707,18 +727,20 @@ __global__ void __launch_bounds__(256) chord_decode_mfma_kernel(ChordArgs a) {
     qb[0] = __builtin_bit_cast(bf16x8, row_ok ? u0 : z);
     qb[1] = __builtin_bit_cast(bf16x8, row_ok ? u1 : z);
   }
-  const float mul = row_ok ? a.ssmax[head] * a.log_n[b * a.ln_sb + int64_t(qi) * a.ln_st] : 0.f;
+  const DecodeWindow win = decode_window(a);
+  const int q_start = win.q_start;
+  const float mul = row_ok ? a.ssmax[head] * log_n_at(a, b, qi, q_start) : 0.f;
   const float c_qk = mul * a.scale * kLog2e, c_b = mul;
-  const int qabs = row_ok ? a.q_start + qi : -1;
+  const int qabs = row_ok ? q_start + qi : -1;
   // GGD bias of (row, key) evaluated in registers, log2 units (the same function the
   // bias table holds): no table pass, no bias loads
   const float g_alpha = a.alpha[head] * kLog2e, g_beta = a.beta[head], g_mu = a.mu[head];
 
-  const int kv_len = min(a.S, a.q_start + a.L);
+  const int kv_len = win.S;
   const int per = ((kv_len + a.splits - 1) / a.splits + kBN - 1) / kBN * kBN;
   const int i_last = min(a.L - 1, (qc * kMfmaRows + kMfmaRows - 1) / group);
   const int k_lo = split * per;
-  const int k_hi = min(min(kv_len, k_lo + per), a.q_start + i_last + 1);
+  const int k_hi = min(min(kv_len, k_lo + per), q_start + i_last + 1);
 
   const bf16_t *kp = static_cast<const bf16_t *>(a.k) + b * a.k_sb + kvh * a.k_sh;
   const bf16_t *vp = static_cast<const bf16_t *>(a.v) + b * a.v_sb + kvh * a.v_sh;
@@ -850,7 +872,7 @@ __global__ void __launch_bounds__(256) chord_decode_mfma_kernel(ChordArgs a) {
       ov += so[ww][r][d] * f;
       Ls += sl[ww][r] * f;
     }
-    if (a.splits == 1) {
+    if (!a.part) {
       const int hh = kvh * group + grr % group, ii = grr / group;
       st(static_cast<bf16_t *>(a.out) + b * a.o_sb + hh * a.o_sh + int64_t(ii) * a.o_st + d, ov / fmaxf(Ls, 1e-20f));
       if (a.lse && d == 0) a.lse[(static_cast<size_t>(b) * a.H + hh) * a.L + ii] = M + fast_log2(Ls);
@@ -881,6 +903,9 @@ __global__ void __launch_bounds__(64) chord_merge_kernel(ChordArgs a) {
   const int head = kvh * group + gr % group, i = gr / group;
   st(static_cast<T *>(a.out) + b * a.o_sb + head * a.o_sh + int64_t(i) * a.o_st + d, o / fmaxf(Ls, 1e-20f));
   if (a.lse && d == 0) a.lse[(static_cast<size_t>(b) * a.H + head) * a.L + i] = M + fast_log2(Ls);
+  // the decode kernel (previous launch) has read the cursor; this kernel never does,
+  // so one thread may advance it
+  if (a.len_dev && (gr | kvh | b | d) == 0) *a.len_dev = min(*a.len_dev + a.L, a.S);
 }
 
 // ------------------------------------------------------------------ planning
@@ -993,6 +1018,7 @@ extern "C" int motif_chord_fwd(
   a.scale = scale; a.eps = eps;
   a.cu = cu_seqlens;
   a.part = nullptr; a.splits = 1; a.nqc = 1;
+  a.len_dev = nullptr; a.log_tab = nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int group = H / Hkv;
   const int rows = group * L;
@@ -1050,4 +1076,112 @@ extern "C" int motif_chord_fwd(
   else if (hpw == 2) chord_fwd_kernel<2><<<grid, block, 0, s>>>(a, tab, tl, e0);
   else chord_fwd_kernel<1><<<grid, block, 0, s>>>(a, tab, tl, e0);
   return check_launch("chord_fwd_kernel");
+}
+
+// ------------------------------------------------------------------ decode over a cursor
+
+namespace motif {
+
+// Workspace of motif_chord_decode: the fp32 path's bias table sized for the capacity,
+// then the split partials (always present: the merge pass advances the cursor).
+static size_t decode_ws_bytes(int B, int H, int Hkv, int L, int capacity, int D, int splits, bool fp32) {
+  const size_t tb = fp32 ? table_bytes(H, capacity) : 0;
+  return tb + static_cast<size_t>(B) * Hkv * splits * (static_cast<size_t>(H / Hkv) * L) * (D + 2) * sizeof(float);
+}
+
+}  // namespace motif
+
+extern "C" size_t motif_chord_decode_workspace_bytes(int B, int H, int Hkv, int L, int capacity, int D, int dtype,
+                                                     int *splits) {
+  if (B <= 0 || H <= 0 || Hkv <= 0 || H % Hkv || L <= 0 || capacity < L) {
+    if (splits) *splits = 1;
+    return 0;
+  }
+  const int sp = decode_splits(B, Hkv, capacity);
+  if (splits) *splits = sp;
+  return decode_ws_bytes(B, H, Hkv, L, capacity, D, sp, dtype == MOTIF_F32);
+}
+
+int motif::chord_decode_run(
+    const void *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void *k_cache, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void *v_cache, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    int *length_dev, int capacity,
+    const float *alpha, const float *beta, const float *mu, const float *ssmax,
+    const float *log_n, int64_t ln_sb, int64_t ln_st, const float *log_table, int log_table_len,
+    void *out, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    int B, int H, int Hkv, int L, int D, float scale, float eps,
+    void *workspace, size_t workspace_bytes, int dtype, void *stream) {
+  if (B < 0 || H <= 0 || Hkv <= 0 || L < 0 || H % Hkv)
+    return set_error(MOTIF_ERR_INVALID, "chord_decode: bad size");
+  if (D != kD) return set_error(MOTIF_ERR_UNSUPPORTED, "chord_decode: head_dim must be 64");
+  if (dtype != MOTIF_BF16 && dtype != MOTIF_F32)
+    return set_error(MOTIF_ERR_UNSUPPORTED, "chord_decode: dtype must be bf16 or fp32");
+  if (B == 0 || L == 0) return MOTIF_OK;
+  if (capacity < L) return set_error(MOTIF_ERR_INVALID, "chord_decode: capacity below the query count");
+  if (!q || !k_cache || !v_cache || !length_dev || !alpha || !beta || !mu || !ssmax || !out)
+    return set_error(MOTIF_ERR_INVALID, "chord_decode: NULL pointer");
+  if (!log_n && (!log_table || log_table_len < capacity))
+    return set_error(MOTIF_ERR_INVALID, "chord_decode: log_n is NULL and the log table is shorter than the capacity");
+  const int64_t vec = dtype == MOTIF_BF16 ? 8 : 4;
+  if (((q_st | k_st | v_st | o_st | q_sh | k_sh | v_sh | o_sh | q_sb | k_sb | v_sb | o_sb) % vec) != 0 ||
+      ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k_cache) |
+        reinterpret_cast<uintptr_t>(v_cache) | reinterpret_cast<uintptr_t>(out)) & 15) != 0)
+    return set_error(MOTIF_ERR_UNSUPPORTED, "chord_decode: q/k/v/out need 16-byte aligned rows");
+  const bool fp32 = dtype == MOTIF_F32;
+  const int splits = decode_splits(B, Hkv, capacity);
+  const size_t need = decode_ws_bytes(B, H, Hkv, L, capacity, D, splits, fp32);
+  if (!workspace || workspace_bytes < need)
+    return set_error(MOTIF_ERR_INVALID, "chord_decode: workspace too small (need " + std::to_string(need) + " bytes)");
+
+  ChordArgs a;
+  a.q = q; a.q_sb = q_sb; a.q_sh = q_sh; a.q_st = q_st;
+  a.k = k_cache; a.k_sb = k_sb; a.k_sh = k_sh; a.k_st = k_st;
+  a.v = v_cache; a.v_sb = v_sb; a.v_sh = v_sh; a.v_st = v_st;
+  a.alpha = alpha; a.beta = beta; a.mu = mu; a.ssmax = ssmax;
+  a.log_n = log_n; a.ln_sb = ln_sb; a.ln_st = ln_st;
+  a.out = out; a.o_sb = o_sb; a.o_sh = o_sh; a.o_st = o_st;
+  a.lse = nullptr;
+  a.B = B; a.H = H; a.Hkv = Hkv; a.L = L; a.S = capacity; a.q_start = 0;
+  a.scale = scale; a.eps = eps;
+  a.cu = nullptr;
+  a.splits = splits;
+  a.len_dev = length_dev; a.log_tab = log_table;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int rows = (H / Hkv) * L;
+  const size_t tb = fp32 ? table_bytes(H, capacity) : 0;
+  a.part = reinterpret_cast<float *>(static_cast<char *>(workspace) + tb);
+  int rc = MOTIF_OK;
+  if (fp32) {
+    const int R = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
+    a.nqc = (rows + R - 1) / R;
+    float *tab = static_cast<float *>(workspace);
+    const int tn = table_len(capacity);
+    chord_bias_table_kernel<<<dim3((tn + 255) / 256, H), dim3(256), 0, s>>>(a, tab, tn);
+    if ((rc = check_launch("chord_bias_table_kernel"))) return rc;
+    launch_decode<float>(a, R, tab, tn, s);
+  } else {
+    a.nqc = (rows + kMfmaRows - 1) / kMfmaRows;
+    chord_decode_mfma_kernel<<<dim3(splits, Hkv, B * a.nqc), dim3(256), 0, s>>>(a);
+  }
+  if ((rc = check_launch("chord_decode_kernel"))) return rc;
+  if (fp32) chord_merge_kernel<float><<<dim3(rows, Hkv, B), dim3(64), 0, s>>>(a);
+  else chord_merge_kernel<bf16_t><<<dim3(rows, Hkv, B), dim3(64), 0, s>>>(a);
+  return check_launch("chord_merge_kernel");
+}
+
+extern "C" int motif_chord_decode(
+    const void *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void *k_cache, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void *v_cache, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    int *length_dev, int capacity,
+    const float *alpha, const float *beta, const float *mu, const float *ssmax,
+    const float *log_n, int64_t ln_sb, int64_t ln_st, const float *log_table, int log_table_len,
+    void *out, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    int B, int H, int Hkv, int L, int D, float scale, float eps,
+    void *workspace, size_t workspace_bytes, int dtype, void *stream) {
+  return motif::chord_decode_run(q, q_sb, q_sh, q_st, k_cache, k_sb, k_sh, k_st, v_cache, v_sb, v_sh, v_st,
+                                 length_dev, capacity, alpha, beta, mu, ssmax, log_n, ln_sb, ln_st, log_table,
+                                 log_table_len, out, o_sb, o_sh, o_st, B, H, Hkv, L, D, scale, eps, workspace,
+                                 workspace_bytes, dtype, stream);
 }

@@ -25,8 +25,9 @@ struct PrepArgs {
   void *q; int64_t q_sb, q_sh, q_st;      // [B, H, L, D]
   void *kc; int64_t k_sb, k_sh, k_st;     // [B, Hkv, cap, D]
   void *vc; int64_t v_sb, v_sh, v_st;
-  int *len_dev;                           // optional: set to pos + L
-  int pos, B, L, H, Hkv, D;
+  int *len_dev;                           // host position: optional, set to pos + L;
+                                          // device position (pos < 0): read, not written
+  int pos, capacity, B, L, H, Hkv, D;
 };
 
 template <typename T> struct Vec;
@@ -95,13 +96,17 @@ __global__ void __launch_bounds__(256) chord_prep_kernel(PrepArgs a) {
   for (int off = 1; off < LPR; off <<= 1) ss += __shfl_xor(ss, off, 64);
   if (!valid) return;
 
+  // the cache position of this launch: the host's, or the device cursor (the decode
+  // kernel that follows reads the same cursor and advances it)
+  const int pos = a.pos >= 0 ? a.pos : __builtin_amdgcn_readfirstlane(*a.len_dev);
+  if (hh >= a.H && pos + t >= a.capacity) return;  // never write past the slab
   T *dst;
   if (hh < a.H) {
     dst = static_cast<T *>(a.q) + b * a.q_sb + hh * a.q_sh + static_cast<int64_t>(t) * a.q_st;
   } else if (!is_v) {
-    dst = static_cast<T *>(a.kc) + b * a.k_sb + (hh - a.H) * a.k_sh + static_cast<int64_t>(a.pos + t) * a.k_st;
+    dst = static_cast<T *>(a.kc) + b * a.k_sb + (hh - a.H) * a.k_sh + static_cast<int64_t>(pos + t) * a.k_st;
   } else {
-    dst = static_cast<T *>(a.vc) + b * a.v_sb + (hh - a.H - a.Hkv) * a.v_sh + static_cast<int64_t>(a.pos + t) * a.v_st;
+    dst = static_cast<T *>(a.vc) + b * a.v_sb + (hh - a.H - a.Hkv) * a.v_sh + static_cast<int64_t>(pos + t) * a.v_st;
   }
   if (!is_v) {
     const float rs = rsqrtf(ss / a.D + a.eps);
@@ -111,7 +116,7 @@ __global__ void __launch_bounds__(256) chord_prep_kernel(PrepArgs a) {
     for (int e = 0; e < E; ++e) x[e] = Vec<T>::round(x[e] * rs) * w[e];
   }
   *reinterpret_cast<uint4 *>(dst + sub * E) = Vec<T>::pack(x);
-  if (a.len_dev && row == 0) *a.len_dev = a.pos + a.L;
+  if (a.pos >= 0 && a.len_dev && row == 0) *a.len_dev = a.pos + a.L;
 }
 
 template <typename T>
@@ -139,11 +144,15 @@ extern "C" int motif_chord_qkv_prep(const void *proj, int64_t p_sb, int64_t p_st
                                     void *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
                                     void *k_cache, int64_t k_sb, int64_t k_sh, int64_t k_st,
                                     void *v_cache, int64_t v_sb, int64_t v_sh, int64_t v_st,
-                                    int *length_dev, int pos, int B, int L, int H, int Hkv, int D, int dtype,
-                                    void *stream) {
+                                    int *length_dev, int pos, int capacity, int B, int L, int H, int Hkv,
+                                    int D, int dtype, void *stream) {
   using namespace motif;
-  if (B < 0 || L < 0 || H <= 0 || Hkv <= 0 || D <= 0 || pos < 0 || H % Hkv)
+  if (B < 0 || L < 0 || H <= 0 || Hkv <= 0 || D <= 0 || H % Hkv || capacity < 0)
     return set_error(MOTIF_ERR_INVALID, "chord_prep: bad size");
+  if (pos < 0 && !length_dev)
+    return set_error(MOTIF_ERR_INVALID, "chord_prep: a device position (pos < 0) needs length_dev");
+  if (pos >= 0 && pos + L > capacity)
+    return set_error(MOTIF_ERR_INVALID, "chord_prep: pos + L exceeds the cache capacity");
   if (!proj || !q_norm_weight || !k_norm_weight || !q || !k_cache || !v_cache)
     return set_error(MOTIF_ERR_INVALID, "chord_prep: NULL pointer");
   if (dtype != MOTIF_F32 && dtype != MOTIF_BF16) return set_error(MOTIF_ERR_UNSUPPORTED, "chord_prep: dtype");
@@ -162,7 +171,7 @@ extern "C" int motif_chord_qkv_prep(const void *proj, int64_t p_sb, int64_t p_st
   a.q = q; a.q_sb = q_sb; a.q_sh = q_sh; a.q_st = q_st;
   a.kc = k_cache; a.k_sb = k_sb; a.k_sh = k_sh; a.k_st = k_st;
   a.vc = v_cache; a.v_sb = v_sb; a.v_sh = v_sh; a.v_st = v_st;
-  a.len_dev = length_dev; a.pos = pos;
+  a.len_dev = length_dev; a.pos = pos; a.capacity = capacity;
   a.B = B; a.L = L; a.H = H; a.Hkv = Hkv; a.D = D;
   if (B == 0 || L == 0) return MOTIF_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);

@@ -3,11 +3,13 @@
 //
 // One workgroup per (head, batch row), one thread per value column e (dv <= 128):
 //   1. short conv + SiLU of the new token against the conv tails for the head's
-//      q / k channels (threads c < 2 dk) and v channels (thread e), tails shifted in place;
+//      q / k channels (threads c < 2 dk) and v channels (thread e); the shifted tails
+//      and the new state go to their output buffers, which may be the input buffers
+//      (every thread reads its own tail channel and state column before writing them);
 //   2. q, k L2-normalised over dk (F.normalize, eps 1e-12), q scaled by dk^-1/2;
 //   3. gates beta = sigmoid(b), g = -exp(A_log) * softplus(a + dt_bias);
 //   4. the delta rule on the fp32 state column S[:, e] held in registers:
-//      S *= e^g; S += k (beta (v_e - k^T S)); o_e = q^T S  (state updated in place);
+//      S *= e^g; S += k (beta (v_e - k^T S)); o_e = q^T S;
 //   5. GatedRMSNorm of the head's dv outputs: o * rsqrt(mean(o^2) + eps) * w * SiLU(gate).
 // fp32 arithmetic throughout.  The reference runs these as separate steps
 // (motif/block/attention/gdn_attn.py:116-136 conv, :183-209 normalise / gates /
@@ -24,10 +26,12 @@ struct GdnDecodeArgs {
   const void *proj; int64_t p_sb;            // [B, ncols] projections (q | k | v | gate | a | b)
   int q_off, k_off, v_off, g_off, a_off, b_off;
   const void *wq, *wk, *wv;                  // conv weights [H*dk, K], [H*dk, K], [H*dv, K]
-  void *tq, *tk, *tv;                        // conv tails [B, C, K-1] (updated in place)
+  const void *tq, *tk, *tv;                  // conv tails [B, C, K-1]
+  void *oq, *ok, *ov;                        // shifted tails (may alias tq / tk / tv)
   const void *a_log, *dt_bias, *norm_w;      // [H], [H], [dv]
   float norm_eps;
-  float *state;                              // [B, H, dk, dv] fp32, in place
+  const float *state;                        // [B, H, dk, dv] fp32
+  float *state_out;                          // may alias state
   void *y; int64_t y_sb;                     // [B, H*dv]
   int B, H, dk, dv;
 };
@@ -43,6 +47,8 @@ __global__ void __launch_bounds__(128) gdn_decode_kernel(GdnDecodeArgs a) {
   // their loads first so their latency overlaps the conv / normalisation below.  The
   // state block of (b, h) is one buffer; row i sits at the uniform offset i * dv * 4.
   const buf_t sbuf = make_buf(a.state + (static_cast<size_t>(b) * a.H + h) * DK * a.dv,
+                              static_cast<uint32_t>(DK * a.dv * 4));
+  const buf_t obuf = make_buf(a.state_out + (static_cast<size_t>(b) * a.H + h) * DK * a.dv,
                               static_cast<uint32_t>(DK * a.dv * 4));
   const uint32_t col = static_cast<uint32_t>(tid) * 4, row = static_cast<uint32_t>(a.dv) * 4;
   float S[DK];
@@ -61,9 +67,11 @@ __global__ void __launch_bounds__(128) gdn_decode_kernel(GdnDecodeArgs a) {
   const float av = ld(pr + a.a_off + h), bv = ld(pr + a.b_off + h);
   const float dtb = ld(static_cast<const T *>(a.dt_bias) + h), alog = ld(static_cast<const T *>(a.a_log) + h);
 
-  auto conv = [&](const void *wgt, void *tails, int C, int ch, float xnew) {
+  auto conv = [&](const void *wgt, const void *tails, void *tails_out, int C, int ch, float xnew) {
     const T *wr = static_cast<const T *>(wgt) + static_cast<size_t>(ch) * K;
-    T *tl = static_cast<T *>(tails) + (static_cast<size_t>(b) * C + ch) * (K - 1);
+    const size_t off = (static_cast<size_t>(b) * C + ch) * (K - 1);
+    const T *tl = static_cast<const T *>(tails) + off;
+    T *to = static_cast<T *>(tails_out) + off;
     float t[K - 1];
 #pragma unroll
     for (int r = 0; r < K - 1; ++r) t[r] = ld(tl + r);
@@ -71,8 +79,8 @@ __global__ void __launch_bounds__(128) gdn_decode_kernel(GdnDecodeArgs a) {
 #pragma unroll
     for (int r = 0; r < K - 1; ++r) acc = fmaf(ld(wr + r), t[r], acc);
 #pragma unroll
-    for (int r = 0; r < K - 2; ++r) st(tl + r, t[r + 1]);
-    st(tl + K - 2, xnew);
+    for (int r = 0; r < K - 2; ++r) st(to + r, t[r + 1]);
+    st(to + K - 2, xnew);
     return silu_fast(acc);
   };
 
@@ -83,7 +91,7 @@ __global__ void __launch_bounds__(128) gdn_decode_kernel(GdnDecodeArgs a) {
     const int c = isq ? tid : tid - DK;
     const int ch = h * DK + c;
     const float x = ld(pr + (isq ? a.q_off : a.k_off) + ch);
-    const float y = conv(isq ? a.wq : a.wk, isq ? a.tq : a.tk, a.H * DK, ch, x);
+    const float y = conv(isq ? a.wq : a.wk, isq ? a.tq : a.tk, isq ? a.oq : a.ok, a.H * DK, ch, x);
     float ss = y * y;
 #pragma unroll
     for (int off = 1; off < DK; off <<= 1) ss += __shfl_xor(ss, off, 64);
@@ -92,7 +100,7 @@ __global__ void __launch_bounds__(128) gdn_decode_kernel(GdnDecodeArgs a) {
     else sk[c] = y / nrm;
   }
   float vcol = 0.f;
-  if (active) vcol = conv(a.wv, a.tv, a.H * a.dv, h * a.dv + tid, xv);
+  if (active) vcol = conv(a.wv, a.tv, a.ov, a.H * a.dv, h * a.dv + tid, xv);
   // 3. gates (uniform)
   const float beta = 1.f / (1.f + exp_f(-bv));
   const float xa = av + dtb;
@@ -117,7 +125,7 @@ __global__ void __launch_bounds__(128) gdn_decode_kernel(GdnDecodeArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < DK; ++i)
-      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, S[i]), sbuf, col, i * row, 0);
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, S[i]), obuf, col, i * row, 0);
   }
 
   // 5. GatedRMSNorm over the head's dv outputs (two waves: partial sums in LDS)
@@ -160,23 +168,27 @@ int launch(const GdnDecodeArgs &a, int K, hipStream_t s) {
 
 extern "C" int motif_gdn_decode_fused(
     const void *proj, int64_t proj_sb, int q_off, int k_off, int v_off, int g_off, int a_off, int b_off,
-    const void *wq, const void *wk, const void *wv, void *tail_q, void *tail_k, void *tail_v,
+    const void *wq, const void *wk, const void *wv, const void *tail_q, const void *tail_k, const void *tail_v,
+    void *tail_q_out, void *tail_k_out, void *tail_v_out,
     const void *a_log, const void *dt_bias, const void *norm_weight, float norm_eps,
-    float *state, void *y, int64_t y_sb, int B, int H, int dk, int dv, int K, int dtype, void *stream) {
+    const float *state, float *state_out, void *y, int64_t y_sb, int B, int H, int dk, int dv, int K, int dtype,
+    void *stream) {
   using namespace motif;
   if (B < 0 || H <= 0 || dk <= 0 || dv <= 0) return set_error(MOTIF_ERR_INVALID, "gdn_decode: bad size");
   if (dv > 128) return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_decode: dv must be <= 128");
   if (dtype != MOTIF_F32 && dtype != MOTIF_BF16) return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_decode: dtype");
   if (B == 0) return MOTIF_OK;
-  if (!proj || !wq || !wk || !wv || !tail_q || !tail_k || !tail_v || !a_log || !dt_bias || !norm_weight || !state || !y)
+  if (!proj || !wq || !wk || !wv || !tail_q || !tail_k || !tail_v || !tail_q_out || !tail_k_out || !tail_v_out ||
+      !a_log || !dt_bias || !norm_weight || !state || !state_out || !y)
     return set_error(MOTIF_ERR_INVALID, "gdn_decode: NULL pointer");
   GdnDecodeArgs a;
   a.proj = proj; a.p_sb = proj_sb;
   a.q_off = q_off; a.k_off = k_off; a.v_off = v_off; a.g_off = g_off; a.a_off = a_off; a.b_off = b_off;
   a.wq = wq; a.wk = wk; a.wv = wv;
   a.tq = tail_q; a.tk = tail_k; a.tv = tail_v;
+  a.oq = tail_q_out; a.ok = tail_k_out; a.ov = tail_v_out;
   a.a_log = a_log; a.dt_bias = dt_bias; a.norm_w = norm_weight; a.norm_eps = norm_eps;
-  a.state = state; a.y = y; a.y_sb = y_sb;
+  a.state = state; a.state_out = state_out; a.y = y; a.y_sb = y_sb;
   a.B = B; a.H = H; a.dk = dk; a.dv = dv;
   hipStream_t s = static_cast<hipStream_t>(stream);
   return dtype == MOTIF_BF16 ? launch<bf16_t>(a, K, s) : launch<float>(a, K, s);

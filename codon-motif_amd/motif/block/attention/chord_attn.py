@@ -1,44 +1,75 @@
-'''ChordAttention with the reference interface (motif/block/attention/chord_attn.py:59-379).
+'''ChordAttention: softmax attention with the per-head gated geometric-decay (GGD)
+bias, behind the reference layer interface (motif/block/attention/chord_attn.py:59-379:
+constructor, parameter names / shapes / initial values, cache type, forward
+arguments and AttentionOutput contract).
 
-Same constructor, parameters (theta_alpha / theta_beta / theta_mu frozen /
-ssmax_s), GGD helpers, cache handling, log_n table and forward contract.  The
-attention itself runs on the HIP Chord kernels (`apply_chord_attention`) for
-the inference path; as in the reference, a request for an additive / boolean
-attention mask or for the attention weights takes the explicit eager path,
-since neither is a kernel feature.  Kernel errors propagate (no silent
-fallback).
+How a call is served:
+  * decode over a StaticKVLayerCache (the graph-captured step): one projection
+    GEMM, one kernel for the q / k RMSNorms and the append at the device cursor,
+    the device-cursor attention kernel (which also advances the cursor), the gated
+    output projection -- no host value enters the launch sequence;
+  * other inference calls on bf16 / fp32 ROCm tensors with head_dim 64: the HIP
+    kernels with host positions (apply_chord_attention);
+  * calls that need gradients: the differentiable torch form (inside
+    apply_chord_attention);
+  * an attention mask, a request for the attention weights, a tensor position
+    (`embedding_start` as a tensor) or a shape the kernels do not serve (fp16,
+    head_dim != 64): the explicit materialised-bias computation below, the
+    reference's rule for leaving its kernel (chord_attn.py:295-298).
 '''
+import warnings
 from typing import Optional, Union
 
 import torch
 import torch.nn as nn
 
 from motif.block.attention.base import AttentionOutput, BasicAttention
-from motif.model.cache import KVLayerCache, StaticKVLayerCache
+from motif.model.cache import KVLayerCache, StaticKVLayerCache, expand_kv_heads
 from motif.ops import RMSNorm, apply_chord_attention, apply_chord_attention_varlen
 from motif.ops import _lib
+from motif.ops.autograd_path import wants_grad
+from motif.ops.chord_attention import HEAD_DIM, chord_decode_cursor, chord_decode_workspace
 from motif.ops.epilogue import mul_sigmoid, usable
 from motif.ops.linear_rows import cat_weights, linear_rows, project, rows_eligible
 
-_HALF_DTYPES = (torch.float16, torch.bfloat16)
-_GGD_EPS = 1e-5
-_LOG_TABLE = {}
+GGD_EPS = 1e-5
+_KERNEL_DTYPES = (torch.bfloat16, torch.float32)
+_DECODE_ROWS = 8  # (GQA group x L) up to this size is a decode-shaped call
 
 
-def _log_n_table(n: int, device, dtype=torch.float32) -> torch.Tensor:
-    '''log(1 .. size), size a power of two >= max(n, 8192), cached per (device, dtype).'''
-    key = (str(device), str(dtype))
-    table = _LOG_TABLE.get(key)
-    if table is None or table.numel() < n:
-        size = max(n, 8192)
-        size = 1 << (size - 1).bit_length()
-        table = torch.log(torch.arange(1, size + 1, device=device, dtype=dtype))
-        _LOG_TABLE[key] = table
-    return table
+class LogPositions:
+    '''ln(1), ln(2), ... in fp32, one table per device, grown in 4096-entry pages.
+    The log_n factor of a query at absolute position p is table[p] = ln(p + 1)
+    (motif/block/attention/chord_attn.py:21-43 with :274-283).'''
+
+    _tables = {}
+
+    @classmethod
+    def get(cls, n: int, device) -> torch.Tensor:
+        device = torch.device(device)
+        t = cls._tables.get(device)
+        if t is None or t.numel() < n:
+            size = max(4096, -(-n // 4096) * 4096)
+            t = torch.log(torch.arange(1, size + 1, dtype=torch.float32, device=device))
+            cls._tables[device] = t
+        return t
+
+    @classmethod
+    def at(cls, start: int, n: int, device) -> torch.Tensor:
+        return cls.get(start + n, device)[start:start + n]
 
 
-def _promote(t: torch.Tensor) -> torch.Tensor:
-    return t.float() if t.dtype in _HALF_DTYPES else t
+def ggd_bias(alpha: torch.Tensor, beta: torch.Tensor, mu: torch.Tensor, distance: torch.Tensor,
+             eps: float = GGD_EPS) -> torch.Tensor:
+    '''-alpha_h (|d - mu_h| + eps) ** beta_h for every head h and distance d = key -
+    query position; alpha, beta, mu [H], distance any shape -> [H, *distance.shape].'''
+    ex = (1,) * distance.dim()
+    dist = distance.to(alpha.dtype)[None]
+    return -alpha.view(-1, *ex) * ((dist - mu.view(-1, *ex)).abs() + eps) ** beta.view(-1, *ex)
+
+
+def _f32(t: torch.Tensor) -> torch.Tensor:
+    return t.float() if t.dtype in (torch.float16, torch.bfloat16) else t
 
 
 class ChordAttention(BasicAttention):
@@ -57,51 +88,160 @@ class ChordAttention(BasicAttention):
         self.theta_beta = nn.Parameter(torch.zeros(num_heads))
         self.theta_mu = nn.Parameter(torch.zeros(num_heads), requires_grad=False)
         self.ssmax_s = nn.Parameter(torch.ones(num_heads))
+        self._warned = False
 
     @classmethod
     def cache_type(cls) -> type:
         return KVLayerCache
 
-    def _ggd_parameters(self):
-        '''(alpha, beta, mu) = (exp(theta_alpha), theta_beta, exp(theta_mu) - exp(-theta_mu)) in fp32.'''
-        ta, tb, tm = _promote(self.theta_alpha), _promote(self.theta_beta), _promote(self.theta_mu)
-        return torch.exp(ta), tb, torch.exp(tm) - torch.exp(-tm)
+    # ------------------------------------------------------------------ parameters
+    def ggd_params(self):
+        '''(alpha, beta, mu, ssmax) in fp32: alpha = e^theta_alpha, beta = theta_beta,
+        mu = e^theta_mu - e^-theta_mu, ssmax = ssmax_s (chord_attn.py:126-138).
+        Inference reuses one contiguous copy until a parameter changes.'''
+        thetas = (self.theta_alpha, self.theta_beta, self.theta_mu, self.ssmax_s)
 
-    def _compute_ggd_bias(self, q_len: int, kv_len: int, q_start: Union[int, torch.Tensor],
-                          device: torch.device, dtype: torch.dtype = torch.float32) -> torch.Tensor:
-        '''[num_heads, q_len, kv_len] bias -alpha * (|d - mu| + eps) ** beta, d = key - query position.'''
-        alpha, beta, mu = self._ggd_parameters()
-        cd = alpha.dtype
-        if isinstance(q_start, torch.Tensor):
-            start = q_start.to(device=device, dtype=cd).reshape(-1)[0]
-        else:
-            start = float(q_start)
-        q_pos = torch.arange(q_len, device=device, dtype=cd) + start
-        k_pos = torch.arange(kv_len, device=device, dtype=cd)
-        d = k_pos[None, :] - q_pos[:, None]
-        b = torch.abs(d[None] - mu[:, None, None]) + _GGD_EPS
-        return (-alpha[:, None, None] * b ** beta[:, None, None]).to(dtype)
+        def compute():
+            ta, tb, tm, ss = (_f32(t) for t in thetas)
+            return tuple(t.contiguous() for t in (ta.exp(), tb, tm.exp() - (-tm).exp(), ss))
+
+        if wants_grad(*thetas):
+            return compute()
+        key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in thetas)
+        memo = self.__dict__.get('_ggd_memo')
+        if memo is None or memo[0] != key:
+            with torch.no_grad():
+                memo = (key, compute())
+            self.__dict__['_ggd_memo'] = memo
+        return memo[1]
 
     @torch.no_grad()
     def relative_prior(self, max_distance: int, device=None, dtype=torch.float32) -> torch.Tensor:
-        alpha, beta, mu = self._ggd_parameters()
-        device = device if device is not None else self.theta_alpha.device
-        d = torch.arange(-max_distance, max_distance + 1, device=device, dtype=alpha.dtype)
-        b = torch.abs(d[None, :] - mu[:, None]) + _GGD_EPS
-        return (-alpha[:, None] * b ** beta[:, None]).to(dtype)
+        '''The GGD bias of every head at distances -max_distance .. max_distance:
+        [num_heads, 2 * max_distance + 1].'''
+        alpha, beta, mu, _ = self.ggd_params()
+        device = self.theta_alpha.device if device is None else device
+        d = torch.arange(-max_distance, max_distance + 1, device=device)
+        return ggd_bias(alpha.to(device), beta.to(device), mu.to(device), d).to(dtype)
 
-    def _log_n(self, q_start, q_len, batch_size, device, section_log_len):
+    # ------------------------------------------------------------------ routing
+    def _kernel_serves(self, x: torch.Tensor) -> bool:
+        '''Inputs the HIP kernels take; ROCm inputs they do not take go to the
+        materialised path with a one-time warning.'''
+        if not x.is_cuda:
+            return False
+        if x.dtype in _KERNEL_DTYPES and self.head_dim == HEAD_DIM and _lib.available():
+            return True
+        if not self._warned:
+            warnings.warn(f'ChordAttention: no HIP kernel for {x.dtype} / head_dim {self.head_dim}; '
+                          'computing the attention with the materialised bias', RuntimeWarning)
+            self._warned = True
+        return False
+
+    def _prep_fusable(self, x: torch.Tensor, cache) -> bool:
+        '''The single input kernel (q / k RMSNorms, cache append) serves this call.'''
+        if not x.is_cuda or x.dtype not in _KERNEL_DTYPES or not _lib.available():
+            return False
+        row_bytes = self.head_dim * x.element_size()
+        if row_bytes % 16 or row_bytes > 512:
+            return False
+        if self.q_norm.weight is None or self.k_norm.weight is None or self.q_norm.eps != self.k_norm.eps:
+            return False
+        if cache is not None and (cache.wide or type(cache) not in (KVLayerCache, StaticKVLayerCache)):
+            return False
+        return not wants_grad(x, self)
+
+    def _on_cursor(self, x, cache, q_start) -> bool:
+        '''Decode over a static cache at its own position: the device-cursor path.'''
+        L = x.shape[1]
+        return (isinstance(cache, StaticKVLayerCache) and cache.capacity > 0 and not cache.wide
+                and q_start == cache.length and cache.length + L <= cache.capacity
+                and cache.k.dtype == x.dtype and self.num_kv_queries * L <= _DECODE_ROWS
+                and self._prep_fusable(x, cache))
+
+    # ------------------------------------------------------------------ inputs
+    def _fused_proj(self, x):
+        w, b = cat_weights(self, '_proj_cat', (self.q_proj, self.k_proj, self.v_proj, self.g_proj))
+        proj = project(x, w, b)
+        return proj if proj.stride(-1) == 1 else proj.contiguous()
+
+    def _prep(self, proj, q, k_dst, v_dst, length_dev, pos, capacity):
+        B, L = proj.shape[0], proj.shape[1]
+        hs, kd = self.hidden_size, self.kv_dim
+        dt = proj.dtype
+        rc = _lib.lib().motif_chord_qkv_prep(
+            proj.data_ptr(), proj.stride(0), proj.stride(1), 0, hs, hs + kd,
+            self.q_norm.weight.to(dt).contiguous().data_ptr(), self.k_norm.weight.to(dt).contiguous().data_ptr(),
+            float(self.q_norm.eps), *_lib.t4(q), *_lib.t4(k_dst), *_lib.t4(v_dst),
+            _lib.ptr(length_dev), pos, capacity, B, L, self.num_heads, self.num_kv_heads, self.head_dim,
+            _lib.dtype_code(dt), _lib.stream_ptr(proj.device))
+        _lib.check(rc, 'motif_chord_qkv_prep')
+
+    def _inputs(self, hidden_states, kv_states, cache, fused: bool):
+        '''(q [B, H, L, D], k / v [B, h, S, D] -- every cached position plus the new ones,
+        gate pre-activation g [B, L, hidden]).  The fused form writes k / v straight
+        into the cache's slab.'''
+        B, L, _ = hidden_states.shape
+        if fused:
+            proj = self._fused_proj(hidden_states)
+            hs, kd = self.hidden_size, self.kv_dim
+            q = torch.empty(B, self.num_heads, L, self.head_dim, dtype=proj.dtype, device=proj.device)
+            if cache is None:
+                k = torch.empty(B, self.num_kv_heads, L, self.head_dim, dtype=proj.dtype, device=proj.device)
+                v = torch.empty_like(k)
+                self._prep(proj, q, k, v, None, 0, L)
+            else:
+                ks, vs, first = cache.append_slots(L, q.new_empty(B, self.num_kv_heads, 0, self.head_dim))
+                length_dev = cache.length_dev if isinstance(cache, StaticKVLayerCache) else None
+                self._prep(proj, q, ks, vs, length_dev, first, ks.shape[2])
+                k, v = cache.k, cache.v
+            return q, k, v, proj[..., hs + 2 * kd:]
+        kv = hidden_states if kv_states is None else kv_states
+        if kv is hidden_states:
+            proj = self._fused_proj(hidden_states) if hidden_states.is_cuda else None
+        else:
+            proj = None
+        if proj is not None:
+            hs, kd = self.hidden_size, self.kv_dim
+            xq, xk, xv, g = (proj[..., :hs], proj[..., hs:hs + kd], proj[..., hs + kd:hs + 2 * kd],
+                             proj[..., hs + 2 * kd:])
+        else:
+            xq, xk, xv, g = self.q_proj(hidden_states), self.k_proj(kv), self.v_proj(kv), self.g_proj(hidden_states)
+        q = self.q_norm(self.reshape_q(xq, L, B))
+        k = self.k_norm(self.reshape_kv(xk, kv.shape[1], B))
+        v = self.reshape_kv(xv, kv.shape[1], B)
+        if cache is not None:
+            k, v = cache.update(k, v, dim=2)
+        return q, k, v, g
+
+    def _log_n(self, q_start, L, B, device, section_log_len):
+        '''log_n [B, L] or [L]: section_log_len when given, else ln(q_start + i + 1).'''
         if section_log_len is not None:
-            sl = section_log_len.squeeze(-1) if section_log_len.dim() == 3 else section_log_len
-            if sl.shape != (batch_size, q_len):
-                raise ValueError(f'section_log_len expects [B, q_len] or [B, q_len, 1], '
-                                 f'got {tuple(section_log_len.shape)}')
+            sl = section_log_len[..., 0] if section_log_len.dim() == 3 else section_log_len
+            if tuple(sl.shape) != (B, L):
+                raise ValueError(f'section_log_len must be [B, q_len] or [B, q_len, 1] with B={B}, '
+                                 f'q_len={L}; got {tuple(section_log_len.shape)}')
             return sl.float()
         if isinstance(q_start, torch.Tensor):
-            start = q_start.reshape(-1)[0].to(device=device, dtype=torch.float32)
-            return torch.log(start + torch.arange(1, q_len + 1, dtype=torch.float32, device=device))
-        return _log_n_table(q_start + q_len, device)[q_start:q_start + q_len]
+            first = q_start.reshape(-1)[:1].to(device=device, dtype=torch.float32)
+            return torch.log(first + torch.arange(1, L + 1, device=device, dtype=torch.float32))
+        return LogPositions.at(q_start, L, device)
 
+    def _gated_output(self, out, g_pre):
+        '''o_proj(out) * sigmoid(g_pre); decode-sized bf16 rows take one kernel with the
+        gate in its epilogue.'''
+        if self.o_proj.bias is None and rows_eligible(out, self.o_proj.weight) and not wants_grad(out, self.o_proj):
+            return linear_rows(out, self.o_proj.weight, 'gate', aux=g_pre)
+        o = self.o_proj(out)
+        if o.shape == g_pre.shape and usable(o, g_pre) and not wants_grad(o, g_pre):
+            return mul_sigmoid(o, g_pre)
+        return o * torch.sigmoid(g_pre)
+
+    def _merge_heads(self, out):
+        B, H, L, D = out.shape
+        return out.transpose(1, 2).reshape(B, L, H * D)
+
+    # ------------------------------------------------------------------ forward
     def forward(
         self,
         hidden_states: torch.Tensor,
@@ -112,193 +252,110 @@ class ChordAttention(BasicAttention):
         past_key_value: Optional[KVLayerCache] = None,
         section_log_len: Optional[torch.Tensor] = None,
     ) -> AttentionOutput:
-        if kv_states is None:
-            kv_states = hidden_states
-        batch_size, q_len, _ = hidden_states.shape
-        kv_len_input = kv_states.shape[1]
-        use_cache = isinstance(past_key_value, KVLayerCache)
-        q_start = embedding_start
-        if use_cache:
-            cached = past_key_value.seq_length
-            if isinstance(q_start, int) and q_start == 0 and cached > 0:
-                q_start = cached
-        if kv_states is hidden_states and self._prep_fusable(hidden_states):
-            q, k, v, xg = self._fused_inputs(hidden_states, past_key_value if use_cache else None)
-        else:
-            xq, xk, xv, xg = self._project(hidden_states, kv_states)
-            q = self.q_norm(self.reshape_q(xq, q_len, batch_size))
-            k = self.k_norm(self.reshape_kv(xk, kv_len_input, batch_size))
-            v = self.reshape_kv(xv, kv_len_input, batch_size)
-            if use_cache:
-                k, v = past_key_value.update(k, v, dim=2)
-        current_key_value = past_key_value if use_cache else None
-        kv_len = k.shape[2]
-        log_n = self._log_n(q_start, q_len, batch_size, hidden_states.device, section_log_len)
-
-        if attention_mask is None and not output_attentions:
-            alpha, beta, mu, ssmax = self._ggd_cached()
-            start = int(q_start.reshape(-1)[0]) if isinstance(q_start, torch.Tensor) else int(q_start)
-            out = apply_chord_attention(
-                q, k, v, alpha, beta, mu, ssmax,
-                log_n if log_n.dim() == 2 else log_n.expand(batch_size, q_len),
-                q_start=start, softmax_scale=self.head_dim ** -0.5, eps=_GGD_EPS)
-            out = out.transpose(1, 2).reshape(batch_size, q_len, self.hidden_size)
-            return AttentionOutput(output=self._gated_output(out, xg), past_key_value=current_key_value)
-
-        return self._eager(q, k, v, torch.sigmoid(xg), q_start, q_len, kv_len, batch_size, log_n,
-                           attention_mask, output_attentions, current_key_value)
-
-    def _ggd_cached(self):
-        '''(alpha, beta, mu, ssmax) as contiguous fp32, cached until a parameter changes.'''
-        params = (self.theta_alpha, self.theta_beta, self.theta_mu, self.ssmax_s)
-        if torch.is_grad_enabled() and any(p.requires_grad for p in params):
-            alpha, beta, mu = self._ggd_parameters()
-            return tuple(t.contiguous() for t in (alpha, beta, mu, _promote(self.ssmax_s)))
-        key = tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in params)
-        cached = self.__dict__.get('_ggd_cat')
-        if cached is None or cached[0] != key:
-            with torch.no_grad():
-                alpha, beta, mu = self._ggd_parameters()
-                vals = tuple(t.contiguous() for t in (alpha, beta, mu, _promote(self.ssmax_s)))
-            cached = (key, vals)
-            self.__dict__['_ggd_cat'] = cached
-        return cached[1]
-
-    def _prep_fusable(self, x):
-        '''Self-attention inputs the fused input kernel (motif_chord_qkv_prep) serves.'''
-        if not x.is_cuda or x.dtype not in (torch.bfloat16, torch.float32):
-            return False
-        if (self.head_dim * x.element_size()) % 16 or self.head_dim * x.element_size() > 512:
-            return False
-        if self.q_norm.weight is None or self.k_norm.weight is None or self.q_norm.eps != self.k_norm.eps:
-            return False
-        return not (torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()))
-
-    def _fused_inputs(self, hidden_states, cache):
-        '''(q, k, v, g) from one projection GEMM and one kernel for the q / k RMSNorms and
-        the placement of k / v: straight into a preallocated cache (StaticKVLayerCache with
-        room), else into new tensors that the cache (if any) appends.  k, v are the cache
-        views the attention reads; g is the gate pre-activation (G = sigmoid(g)).'''
+        cache = past_key_value if isinstance(past_key_value, KVLayerCache) else None
+        self_attn = kv_states is None or kv_states is hidden_states
         B, L, _ = hidden_states.shape
-        H, Hkv, D, hs, kd = self.num_heads, self.num_kv_heads, self.head_dim, self.hidden_size, self.kv_dim
-        dev, dt = hidden_states.device, hidden_states.dtype
-        w, b = cat_weights(self, '_proj_cat', (self.q_proj, self.k_proj, self.v_proj, self.g_proj))
-        proj = project(hidden_states, w, b)
-        if proj.stride(-1) != 1:
-            proj = proj.contiguous()
-        static = (isinstance(cache, StaticKVLayerCache) and cache.k is not None and cache.k.dtype == dt
-                  and cache.length + L <= cache.capacity)
-        if static:
-            pos = cache.reserve(L)
-            kd_t, vd_t, len_dev = cache.k, cache.v, cache.length_dev
-        else:
-            pos = 0
-            kd_t = torch.empty(B, Hkv, L, D, dtype=dt, device=dev)
-            vd_t = torch.empty(B, Hkv, L, D, dtype=dt, device=dev)
-            len_dev = None
-        q = torch.empty(B, H, L, D, dtype=dt, device=dev)
-        qw = self.q_norm.weight.to(dt).contiguous()
-        kw = self.k_norm.weight.to(dt).contiguous()
-        rc = _lib.lib().motif_chord_qkv_prep(
-            proj.data_ptr(), proj.stride(0), proj.stride(1), 0, hs, hs + kd,
-            qw.data_ptr(), kw.data_ptr(), float(self.q_norm.eps),
-            q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
-            kd_t.data_ptr(), kd_t.stride(0), kd_t.stride(1), kd_t.stride(2),
-            vd_t.data_ptr(), vd_t.stride(0), vd_t.stride(1), vd_t.stride(2),
-            _lib.ptr(len_dev), pos, B, L, H, Hkv, D, _lib.dtype_code(dt), _lib.stream_ptr(dev))
-        _lib.check(rc, 'motif_chord_qkv_prep')
-        if static:
-            k, v = cache.k[:, :, :cache.length], cache.v[:, :, :cache.length]
-        elif cache is not None:
-            k, v = cache.update(kd_t, vd_t, dim=2)
-        else:
-            k, v = kd_t, vd_t
-        return q, k, v, proj[..., hs + 2 * kd:]
+        q_start = embedding_start
+        # an int position of 0 means "continue the cache" (chord_attn.py:266-268)
+        if cache is not None and isinstance(q_start, int) and q_start == 0 and cache.seq_length > 0:
+            q_start = cache.seq_length
+        kernel = (attention_mask is None and not output_attentions and not isinstance(q_start, torch.Tensor)
+                  and self._kernel_serves(hidden_states))
 
-    def _project(self, hidden_states, kv_states):
-        '''q, k, v and the gate pre-activation g (G = sigmoid(g)).  Self-attention runs the
-        four projections as one GEMM against their concatenated weights (the results are
-        column views of it); cross-attention projects k, v from kv_states.'''
-        if kv_states is hidden_states:
-            w, b = cat_weights(self, '_proj_cat', (self.q_proj, self.k_proj, self.v_proj, self.g_proj))
-            proj = project(hidden_states, w, b)
-            hs, kd = self.hidden_size, self.kv_dim
-            return (proj[..., :hs], proj[..., hs:hs + kd], proj[..., hs + kd:hs + 2 * kd],
-                    proj[..., hs + 2 * kd:])
-        return (self.q_proj(hidden_states), self.k_proj(kv_states), self.v_proj(kv_states),
-                self.g_proj(hidden_states))
+        if kernel and self_attn and section_log_len is None and self._on_cursor(hidden_states, cache, q_start):
+            return self._cursor_step(hidden_states, cache)
 
-    def _gated_output(self, out, g_pre):
-        '''o_proj(out) * sigmoid(g_pre); one decode kernel (gate in the epilogue) for
-        decode-sized bf16 inputs.'''
-        if self.o_proj.bias is None and rows_eligible(out, self.o_proj.weight):
-            return linear_rows(out, self.o_proj.weight, 'gate', aux=g_pre)
-        o = self.o_proj(out)
-        if o.shape == g_pre.shape and usable(o, g_pre):
-            return mul_sigmoid(o, g_pre)
-        return o * torch.sigmoid(g_pre)
+        fused = kernel and self_attn and self._prep_fusable(hidden_states, cache)
+        q, k, v, g = self._inputs(hidden_states, None if self_attn else kv_states, cache, fused)
+        log_n = self._log_n(q_start, L, B, hidden_states.device, section_log_len)
+        if kernel:
+            alpha, beta, mu, ssmax = self.ggd_params()
+            out = apply_chord_attention(q, k, v, alpha, beta, mu, ssmax,
+                                        log_n if log_n.dim() == 2 else log_n.expand(B, L),
+                                        q_start=int(q_start), softmax_scale=self.head_dim ** -0.5, eps=GGD_EPS)
+            return AttentionOutput(output=self._gated_output(self._merge_heads(out), g), past_key_value=cache)
+        return self._materialised(q, k, v, g, q_start, log_n, attention_mask, output_attentions, cache)
+
+    def _cursor_step(self, x, cache: StaticKVLayerCache) -> AttentionOutput:
+        '''Decode at the static cache's device cursor: append, attend, advance -- all
+        on the device, so the launch sequence is the same for every token.'''
+        B, L, _ = x.shape
+        proj = self._fused_proj(x)
+        q = torch.empty(B, self.num_heads, L, self.head_dim, dtype=proj.dtype, device=proj.device)
+        ks, vs = cache._slab
+        self._prep(proj, q, ks, vs, cache.length_dev, -1, cache.capacity)
+        if cache.__dict__.get('log_table') is None or cache.log_table.numel() < cache.capacity:
+            cache.log_table = LogPositions.get(cache.capacity, x.device)  # held: a graph keeps its address
+        if cache.decode_workspace is None:
+            cache.decode_workspace = chord_decode_workspace(B, self.num_heads, self.num_kv_heads, L, cache.capacity,
+                                                            self.head_dim, x.dtype, x.device)
+        alpha, beta, mu, ssmax = self.ggd_params()
+        out = chord_decode_cursor(q, ks, vs, cache.length_dev, alpha, beta, mu, ssmax, cache.log_table,
+                                  self.head_dim ** -0.5, GGD_EPS, workspace=cache.decode_workspace)
+        cache.length += L
+        cache.cursor_steps = getattr(cache, 'cursor_steps', 0) + 1
+        return AttentionOutput(output=self._gated_output(self._merge_heads(out), proj[..., self.hidden_size
+                                                                                         + 2 * self.kv_dim:]),
+                               past_key_value=cache)
 
     def forward_varlen(self, hidden_states: torch.Tensor, cu_seqlens: torch.Tensor) -> AttentionOutput:
-        '''Packed sequences (B == 1): each sequence attends causally within itself
-        with positions (and log_n) restarting at 0.  Returns the output and the
-        packed keys / values in the payload.'''
-        batch_size, T, _ = hidden_states.shape
-        if batch_size != 1:
+        '''Packed sequences (B == 1; new): each sequence attends causally within itself
+        with positions (and log_n) restarting at 0.  The payload holds the packed keys
+        and values.'''
+        B, T, _ = hidden_states.shape
+        if B != 1:
             raise ValueError('forward_varlen expects packed sequences with B == 1')
-        if self._prep_fusable(hidden_states):
-            q, k, v, xg = self._fused_inputs(hidden_states, None)
-        else:
-            xq, xk, xv, xg = self._project(hidden_states, hidden_states)
-            q = self.q_norm(self.reshape_q(xq, T, 1))
-            k = self.k_norm(self.reshape_kv(xk, T, 1))
-            v = self.reshape_kv(xv, T, 1)
+        fused = self._prep_fusable(hidden_states, None)
+        q, k, v, g = self._inputs(hidden_states, None, None, fused)
         cu = cu_seqlens.detach().to('cpu', torch.int64)
-        pos = torch.arange(T) - torch.repeat_interleave(cu[:-1], cu[1:] - cu[:-1])
-        log_n = torch.log(pos.to(torch.float32) + 1).to(hidden_states.device)[None]
-        alpha, beta, mu = self._ggd_parameters()
-        out = apply_chord_attention_varlen(
-            q, k, v, alpha.contiguous(), beta.contiguous(), mu.contiguous(),
-            _promote(self.ssmax_s).contiguous(), log_n, cu_seqlens,
-            softmax_scale=self.head_dim ** -0.5, eps=_GGD_EPS)
-        out = out.transpose(1, 2).reshape(1, T, self.hidden_size)
-        return AttentionOutput(output=self._gated_output(out, xg), payload={'k': k, 'v': v})
+        lens = cu[1:] - cu[:-1]
+        pos = torch.arange(T) - torch.repeat_interleave(cu[:-1], lens)
+        table = LogPositions.get(int(lens.max()) if lens.numel() else 1, hidden_states.device)
+        log_n = table[pos.to(hidden_states.device)][None]
+        alpha, beta, mu, ssmax = self.ggd_params()
+        out = apply_chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, log_n, cu_seqlens,
+                                           softmax_scale=self.head_dim ** -0.5, eps=GGD_EPS)
+        return AttentionOutput(output=self._gated_output(self._merge_heads(out), g), payload={'k': k, 'v': v})
 
-    def _eager(self, q, k, v, G, q_start, q_len, kv_len, batch_size, log_n,
-               attention_mask, output_attentions, current_key_value):
-        '''Materialised-bias path for masks / attention weights (chord_attn.py:316-379).'''
-        if self.num_kv_queries > 1 and k.shape[1] != self.num_heads:
-            k = k.repeat_interleave(self.num_kv_queries, dim=1)
-            v = v.repeat_interleave(self.num_kv_queries, dim=1)
-        scores = (q @ k.transpose(-2, -1)) * (self.head_dim ** -0.5)
-        logit_dtype = torch.float32 if scores.dtype in _HALF_DTYPES else scores.dtype
-        bias = self._compute_ggd_bias(q_len, kv_len, q_start, scores.device, logit_dtype)
-        logits = scores.to(logit_dtype) + bias.unsqueeze(0)
-        ln = log_n.view(1, 1, q_len, 1) if log_n.dim() == 1 else log_n.view(batch_size, 1, q_len, 1)
-        logits = logits * (_promote(self.ssmax_s).view(1, -1, 1, 1) * ln.to(logit_dtype))
-        logits = logits.clamp_min(torch.finfo(logit_dtype).min / 4)
-        q_pos = torch.arange(q_len, device=logits.device) + q_start
-        k_pos = torch.arange(kv_len, device=logits.device)
+    def _materialised(self, q, k, v, g, q_start, log_n, attention_mask, output_attentions, cache):
+        '''Attention with the bias matrix built explicitly: for masks, attention weights,
+        tensor positions and shapes without a kernel.  Rounding follows the reference's
+        eager computation (chord_attn.py:316-361): q.k^T and its scaling in the input
+        dtype, then fp32 logits (+ bias, x ssmax * log_n, floor at finfo.min / 4), the
+        causal and user masks, softmax, weights cast back before the product with v.'''
+        B, H, L, D = q.shape
+        S = k.shape[2]
+        kf, vf = expand_kv_heads(k, H), expand_kv_heads(v, H)
+        scores = torch.matmul(q, kf.transpose(-2, -1)) * (D ** -0.5)
+        fdt = torch.float32 if scores.dtype in (torch.float16, torch.bfloat16) else scores.dtype
+        alpha, beta, mu, ssmax = self.ggd_params()
+        dev = scores.device
+        q_pos = torch.arange(L, device=dev) + (q_start.to(dev).reshape(-1)[:1] if isinstance(q_start, torch.Tensor)
+                                               else q_start)
+        k_pos = torch.arange(S, device=dev)
+        bias = ggd_bias(alpha, beta, mu, k_pos[None, :] - q_pos[:, None]).to(fdt)         # [H, L, S]
+        ln = log_n.view(1, 1, L, 1) if log_n.dim() == 1 else log_n.view(B, 1, L, 1)
+        logits = (scores.to(fdt) + bias[None]) * (ssmax.view(1, H, 1, 1).to(fdt) * ln.to(fdt))
+        logits = logits.clamp_min(torch.finfo(fdt).min / 4)
         logits = logits.masked_fill(k_pos[None, :] > q_pos[:, None], float('-inf'))
         if attention_mask is not None:
             if attention_mask.dtype == torch.bool:
                 keep = attention_mask
-                if keep.dim() == 2:
-                    keep = keep[:, None, None, :]
-                elif keep.dim() == 3:
-                    keep = keep[:, None]
+                while keep.dim() < 4:
+                    keep = keep.unsqueeze(1)
                 logits = logits.masked_fill(~keep, float('-inf'))
             else:
                 logits = logits + attention_mask
-        attn = torch.softmax(logits, dim=-1)
-        out = (attn.to(v.dtype) @ v).transpose(1, 2).reshape(batch_size, q_len, self.hidden_size)
-        out = self.o_proj(out) * G
+        weights = torch.softmax(logits, dim=-1)
+        out = self._merge_heads(torch.matmul(weights.to(vf.dtype), vf))
+        out = self.o_proj(out) * torch.sigmoid(g)
         payload = None
         if output_attentions:
-            start = q_start if isinstance(q_start, int) else int(q_start.reshape(-1)[0])
-            payload = {'prior': self.relative_prior(max(q_len - 1, kv_len - 1 - start, 1) + 1,
-                                                    device=logits.device)}
-        return AttentionOutput(output=out, attention_weights=attn if output_attentions else None,
-                               past_key_value=current_key_value, payload=payload)
+            first = int(q_start.reshape(-1)[0]) if isinstance(q_start, torch.Tensor) else q_start
+            reach = max(L - 1, S - 1 - first, 1) + 1
+            payload = {'prior': self.relative_prior(reach, device=dev)}
+        return AttentionOutput(output=out, attention_weights=weights if output_attentions else None,
+                               past_key_value=cache, payload=payload)
 
 
-__all__ = ['ChordAttention', 'StaticKVLayerCache']
+__all__ = ['ChordAttention', 'LogPositions', 'ggd_bias', 'StaticKVLayerCache']

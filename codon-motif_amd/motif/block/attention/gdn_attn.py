@@ -7,9 +7,11 @@ HIP kernels:
   * prefill (L > 1): short conv + SiLU with the q / k L2 norm fused in
     (motif_short_conv_silu_l2norm), then the chunked delta rule (motif_gdn_chunk_fwd);
   * decode (L == 1 with a cache): one fused kernel from the projections to the
-    GatedRMSNorm output (motif_gdn_decode_fused), updating the cache's recurrent
-    state and conv tails in place.
-GatedRMSNorm (prefill) and o_proj stay in PyTorch-ROCm.
+    GatedRMSNorm output (motif_gdn_decode_fused).  It writes the new recurrent
+    state and conv tails to fresh tensors that replace the cache's (the reference's
+    update semantics, motif/model/cache.py:332-356), or, for an in-place cache (the
+    graph-captured decode step), over the cache's own storage.
+Calls that need gradients take the differentiable torch forms inside the ops.
 
 Precision: the reference casts q/k/v/beta/g to fp32 before the delta rule
 (:197).  Those tensors are produced in the activation dtype, so casting is
@@ -26,6 +28,7 @@ import torch.nn.functional as F
 
 from motif.block.attention.base import AttentionOutput, BasicAttention
 from motif.model.cache import GatedDeltaAttentionLayerCache
+from motif.ops.autograd_path import wants_grad
 from motif.ops.epilogue import gated_rms_norm_heads, gdn_gates, usable
 from motif.ops import (
     GatedRMSNorm,
@@ -113,9 +116,8 @@ class GatedDeltaAttention(BasicAttention):
         return proj, tuple(proj[..., s:e] for s, e in zip(offs, ends))
 
     def _gates(self, a, b):
-        if a.is_cuda and a.dtype in (torch.bfloat16, torch.float32) and b.dtype == a.dtype and not (
-                torch.is_grad_enabled() and (self.A_log.requires_grad or a.requires_grad)):
-            return gdn_gates(a, b, self.A_log, self.dt_bias)
+        if a.is_cuda and a.dtype in (torch.bfloat16, torch.float32) and b.dtype == a.dtype:
+            return gdn_gates(a, b, self.A_log, self.dt_bias)  # torch form inside when grad is needed
         beta = torch.sigmoid(b).transpose(1, 2)
         g = -self.A_log.exp() * F.softplus(a + self.dt_bias)
         return beta, g.transpose(1, 2)
@@ -137,7 +139,7 @@ class GatedDeltaAttention(BasicAttention):
         ws = (self.q_conv.weight, self.k_conv.weight, self.v_conv.weight)
         opts = ((hd, self.dk ** -0.5), (hd, 1.0), (None, 1.0))
         outs = None
-        if xs[0].is_cuda and not (torch.is_grad_enabled() and any(w.requires_grad for w in ws)):
+        if xs[0].is_cuda and not wants_grad(xs, ws, tails):
             outs = short_conv_silu_multi(xs, ws, tails, [o[0] for o in opts], [o[1] for o in opts],
                                          cu_seqlens, max_len)
         if outs is not None:
@@ -157,7 +159,7 @@ class GatedDeltaAttention(BasicAttention):
         '''GatedRMSNorm of [o || gate] per head, then o_proj.  One HIP pass over o and the
         gate (no concatenation) when the kernel serves the tensors.'''
         o = o.to(gate.dtype)
-        if self.o_norm.weight is not None and usable(o, gate):
+        if self.o_norm.weight is not None and usable(o, gate) and not wants_grad(self.o_norm):
             y = gated_rms_norm_heads(o, gate, self.o_norm.weight, self.o_norm.eps)
             return project(y, self.o_proj.weight, self.o_proj.bias)
         o = o.transpose(1, 2)
@@ -173,7 +175,7 @@ class GatedDeltaAttention(BasicAttention):
             return False
         if self.dk not in (16, 32, 64) or self.dv > 128 or not 2 <= self.conv_size <= 5:
             return False
-        if self.o_norm.weight is None or (torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters())):
+        if self.o_norm.weight is None or wants_grad(hidden_states, self):
             return False
         S = cache.state
         if S is not None and (S.dtype != torch.float32 or not S.is_contiguous() or not S.is_cuda
@@ -188,22 +190,28 @@ class GatedDeltaAttention(BasicAttention):
         return True
 
     def _decode_step(self, hidden_states, cache):
-        '''One token through the fused decode kernel; the cache's state and conv tails are
-        updated in place (allocated as zeros on the first step).'''
+        '''One token through the fused decode kernel.  An empty cache starts from zero
+        state and tails; an in-place cache is updated over its own storage, any other
+        receives new tensors.'''
         B = hidden_states.shape[0]
         dev, dt = hidden_states.device, hidden_states.dtype
         H, K = self.num_heads, self.conv_size
-        if cache.state is None:
-            cache.state = torch.zeros(B, H, self.dk, self.dv, dtype=torch.float32, device=dev)
-        if cache.conv_state is None:
-            cache.conv_state = tuple(torch.zeros(B, c, K - 1, dtype=dt, device=dev)
-                                     for c in (H * self.dk, H * self.dk, H * self.dv))
+        chans = (H * self.dk, H * self.dk, H * self.dv)
+        state, tails = cache.state, cache.conv_state
+        if state is None:
+            state = torch.zeros(B, H, self.dk, self.dv, dtype=torch.float32, device=dev)
+        if tails is None:
+            tails = tuple(torch.zeros(B, c, K - 1, dtype=dt, device=dev) for c in chans)
+        if cache.in_place:
+            state_out, tails_out = state, tails
+        else:
+            state_out, tails_out = torch.empty_like(state), tuple(torch.empty_like(t) for t in tails)
         w, b = self._proj_weight()
         proj = project(hidden_states.view(B, -1), w, b)
         y = gdn_decode_fused(proj, self._proj_offsets(), (self.q_conv.weight, self.k_conv.weight, self.v_conv.weight),
-                             cache.conv_state, self.A_log, self.dt_bias, self.o_norm.weight, self.o_norm.eps,
-                             cache.state, H, self.dk, self.dv)
-        cache.update(cache.state, cache.conv_state, steps=1)
+                             tails, self.A_log, self.dt_bias, self.o_norm.weight, self.o_norm.eps,
+                             state, H, self.dk, self.dv, tails_out=tails_out, state_out=state_out)
+        cache.update(state_out, tails_out, steps=1)
         return project(y.view(B, 1, -1), self.o_proj.weight, self.o_proj.bias)
 
     def forward(self, hidden_states: torch.Tensor, past_key_value=None) -> AttentionOutput:

@@ -38,11 +38,11 @@ _SIGNATURES = {
     'motif_short_conv_silu_multi': (
         [_I32] + [_P] * 12 + [_I32] * 3 + [_P, _I32, _I32, _I32, _P], _I32),
     'motif_gdn_decode_fused': (
-        [_P, _I64] + [_I32] * 6 + [_P] * 9 + [_F32, _P, _P, _I64] + [_I32] * 6 + [_P], _I32),
+        [_P, _I64] + [_I32] * 6 + [_P] * 12 + [_F32, _P, _P, _P, _I64] + [_I32] * 6 + [_P], _I32),
     'motif_linear_rows': (
         [_P, _I64, _P, _I64, _P, _I64] + [_I32] * 4 + [_P, _I64, _P, _I64, _P, _I64, _P], _I32),
     'motif_chord_qkv_prep': (
-        [_P, _I64, _I64, _I32, _I32, _I32, _P, _P, _F32] + [_P, _I64, _I64, _I64] * 3 + [_P] + [_I32] * 7 + [_P],
+        [_P, _I64, _I64, _I32, _I32, _I32, _P, _P, _F32] + [_P, _I64, _I64, _I64] * 3 + [_P] + [_I32] * 8 + [_P],
         _I32),
     'motif_gated_rms_norm': (
         [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _F32, _P, _I64, _I64] + [_I32] * 5 + [_P], _I32),
@@ -58,6 +58,10 @@ _SIGNATURES = {
     'motif_short_conv_silu_l2norm': (
         [_P, _I64, _I64, _P, _P, _P, _P, _I64, _I64] + [_I32] * 4 + [_P, _I32, _I32, _I32, _F32, _I32, _P], _I32),
     'motif_chord_workspace_bytes': ([_I32] * 6 + [ctypes.POINTER(_I32)], _SZ),
+    'motif_chord_decode_workspace_bytes': ([_I32] * 7 + [ctypes.POINTER(_I32)], _SZ),
+    'motif_chord_decode': (
+        _T4 * 3 + [_P, _I32] + [_P] * 4 + [_P, _I64, _I64, _P, _I32] + _T4 + [_I32] * 5 + [_F32, _F32]
+        + [_P, _SZ, _I32, _P], _I32),
     'motif_chord_fwd': (
         _T4 * 3 + [_P, _P, _P, _P] + [_P, _I64, _I64] + _T4 + [_P] + [_I32] * 6
         + [_I32, _F32, _F32] + [_P, _I32, _I32] + [_P, _SZ] + [_I32, _P], _I32),

@@ -4,35 +4,56 @@ Softmax over the block's sources of <query, RMSNorm(source)>, then the weighted
 sum of the raw sources: the reference's fused read (motif/ops/attn_res.py:22-55,
 :94-186) and eager read (:588-593), and `apply_block_attn_res` (:596-622).  On
 CUDA tensors it runs as one HIP kernel (`motif_attn_res_read`, fp32 arithmetic,
-every source read once); CPU tensors take the eager torch formula.
+every source read once).  The torch formula serves CPU tensors, calls that need
+gradients (the kernel is forward-only) and reads of more than MAX_SRC sources (with
+one warning, as the reference's reader warns when it leaves its kernel,
+motif/ops/attn_res.py:570-586).
 '''
 import ctypes
+import warnings
 
 import torch
 
 from . import _lib
+from .autograd_path import wants_grad
 
 MAX_SRC = 8
+_warned_many = False
 
 
-def _eager(sources, query, norm):
-    V = torch.stack(list(sources), dim=0)
+def attn_res_torch(sources, query, norm):
+    '''The read in torch ops (differentiable): scores <query, norm(x_n)> in the sources'
+    dtype, softmax over the sources, weighted sum of the raw sources.'''
+    V = torch.stack(list(sources), dim=0)                      # [N, B, T, D]
     K = norm(V)
-    logits = torch.einsum('d,nbtd->nbt', query.to(K.dtype), K)
+    logits = torch.matmul(K, query.to(K.dtype))                # [N, B, T]
     alpha = logits.softmax(dim=0)
-    return torch.einsum('nbt,nbtd->btd', alpha, V)
+    w = alpha.permute(1, 2, 0).unsqueeze(-2)                   # [B, T, 1, N]
+    return torch.matmul(w, V.permute(1, 2, 0, 3).contiguous()).squeeze(-2)
+
+
+def _torch_route(sources, query, norm, *more) -> bool:
+    '''The read takes the torch formula: CPU tensors, gradients, too many sources.'''
+    global _warned_many
+    if not sources[0].is_cuda or wants_grad(sources, query, norm, *more):
+        return True
+    if len(sources) > MAX_SRC:
+        if not _warned_many:
+            _warned_many = True
+            warnings.warn(f'attention-residual read of {len(sources)} sources: the HIP kernel takes at most '
+                          f'{MAX_SRC}; computing it with torch ops', RuntimeWarning)
+        return True
+    return False
 
 
 def attn_res_read(sources, query, norm):
     '''h = sum_n softmax_n(<query, norm(x_n)>) x_n over sources x_n [B, T, D].'''
     sources = list(sources)
     x0 = sources[0]
-    if not x0.is_cuda:
-        return _eager(sources, query, norm)
+    if _torch_route(sources, query, norm):
+        return attn_res_torch(sources, query, norm)
     if not _lib.available():
         raise RuntimeError('attn_res_read: the HIP kernel library is not loaded')
-    if len(sources) > MAX_SRC:
-        raise NotImplementedError(f'attn_res_read: at most {MAX_SRC} sources, got {len(sources)}')
     B, T, D = x0.shape
     dt = x0.dtype
     if dt not in (torch.bfloat16, torch.float32):
@@ -62,11 +83,13 @@ def attn_res_read_norms(sources, query, norm, norm_a, norm_b):
     '''(norm_a(h), norm_b(h)) for h = attn_res_read(sources, query, norm), in one HIP
     kernel that never writes h: the decoder's attn_norm / mlp_norm inputs.  RMSNorm
     as the reference computes it on the stored h: T(h * rsqrt(mean(h^2) + eps)) * w.
-    Needs ROCm tensors, both norms with weights and one eps.'''
+    Needs ROCm tensors, both norms with weights and one eps; reads the torch route
+    would serve (see attn_res_read) are computed as attn_res_read then the two norms.'''
     sources = list(sources)
     x0 = sources[0]
-    if len(sources) > MAX_SRC:
-        raise NotImplementedError(f'attn_res_read_norms: at most {MAX_SRC} sources, got {len(sources)}')
+    if _torch_route(sources, query, norm, norm_a, norm_b):
+        h = attn_res_read(sources, query, norm) if len(sources) > 1 else sources[0]
+        return norm_a(h), norm_b(h)
     B, T, D = x0.shape
     dt = x0.dtype
     if dt not in (torch.bfloat16, torch.float32):

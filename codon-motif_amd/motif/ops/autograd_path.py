@@ -12,6 +12,28 @@ import torch
 import torch.nn.functional as F
 
 
+def wants_grad(*items) -> bool:
+    '''True when autograd is recording and any of `items` needs a gradient: a tensor
+    that requires grad, a module with such a parameter, or a sequence holding either.
+    Every kernel dispatch asks this of all its tensor inputs and parameters, since the
+    kernels are forward-only.'''
+    if not torch.is_grad_enabled():
+        return False
+    for it in items:
+        if it is None:
+            continue
+        if isinstance(it, torch.Tensor):
+            if it.requires_grad:
+                return True
+        elif isinstance(it, torch.nn.Module):
+            if any(p.requires_grad for p in it.parameters()):
+                return True
+        elif isinstance(it, (list, tuple)):
+            if wants_grad(*it):
+                return True
+    return False
+
+
 def _cdt(t):
     '''Compute dtype: float32, or float64 for float64 inputs.'''
     return torch.float64 if t.dtype == torch.float64 else torch.float32
@@ -98,3 +120,16 @@ def chord_attention_torch(q, k, v, alpha, beta, mu, ssmax, log_n, q_start=None, 
     visible = torch.arange(S, device=q.device)[None, :] <= i_abs[:, None]
     logits = logits.masked_fill(~visible, -math.inf)
     return (logits.softmax(-1) @ vf).to(q.dtype)
+
+
+def chord_attention_varlen_torch(q, k, v, alpha, beta, mu, ssmax, log_n, cu_seqlens, softmax_scale=None, eps=1e-5):
+    '''Packed-sequence Chord attention as separate differentiable runs: sequence i
+    (rows cu[i]:cu[i+1] of q [1, H, T, D] / k, v [1, Hkv, T, D]) attends causally within
+    itself from position 0 with its slice of log_n [1, T].'''
+    cu = [int(x) for x in cu_seqlens.detach().to('cpu')]
+    outs = [chord_attention_torch(q[:, :, a:b], k[:, :, a:b], v[:, :, a:b], alpha, beta, mu, ssmax,
+                                  log_n[:, a:b], 0, softmax_scale, eps)
+            for a, b in zip(cu[:-1], cu[1:]) if b > a]
+    if not outs:
+        return q.new_empty(q.shape)
+    return torch.cat(outs, dim=2)

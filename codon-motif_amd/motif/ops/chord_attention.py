@@ -7,14 +7,18 @@ picks the bf16 MFMA flash kernel for prefill shapes and the split-K vector
 kernel when a kv head serves at most 8 query rows (GQA group x L), which is
 the reference's long-KV / short-Q split path (:1128-1229).  fp32 inputs run on
 the vector kernel for every shape (fp32 FMA throughout, the accuracy mode).
-`apply_chord_attention_varlen` adds packed sequences (new).
+`apply_chord_attention_varlen` adds packed sequences (new) and
+`chord_decode_cursor` the decode step over a fixed-capacity cache whose length
+lives on the device (new; the graph-replayable form of the decode call).
+Calls that need gradients take the differentiable torch forms
+(motif/ops/autograd_path.py); the kernels are forward-only.
 '''
 from typing import Optional
 
 import torch
 
 from . import _lib
-from .autograd_path import chord_attention_torch
+from .autograd_path import chord_attention_torch, chord_attention_varlen_torch, wants_grad
 
 HEAD_DIM = 64
 
@@ -134,9 +138,8 @@ def apply_chord_attention(
             the differentiable torch form).
         RuntimeError: when the HIP library is unavailable or a launch fails.
     '''
-    needs_grad = torch.is_grad_enabled() and any(
-        t.requires_grad for t in (q, k, v, alpha, beta, mu, ssmax))
-    if needs_grad:  # forward-only kernels: training takes the differentiable torch form
+    if wants_grad(q, k, v, alpha, beta, mu, ssmax, log_n):
+        # forward-only kernels: training takes the differentiable torch form
         if q_start is not None and int(q_start) < 0:
             raise ValueError(f'q_start must not be negative, got {q_start}')
         return chord_attention_torch(q, k, v, alpha, beta, mu, ssmax, log_n, q_start, softmax_scale, eps)
@@ -165,7 +168,10 @@ def apply_chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, log_n, cu_seql
     sequence i covering rows [cu_seqlens[i], cu_seqlens[i+1]).  Each sequence is
     causal on its own with positions restarting at 0; log_n [1, T] is read at
     the packed row (log(1 .. len_i) per sequence reproduces separate runs).
+    Calls that need gradients run the sequences as separate differentiable torch runs.
     '''
+    if wants_grad(q, k, v, alpha, beta, mu, ssmax, log_n):
+        return chord_attention_varlen_torch(q, k, v, alpha, beta, mu, ssmax, log_n, cu_seqlens, softmax_scale, eps)
     if not _lib.available():
         raise RuntimeError('there is no usable HIP backend in the current environment')
     B, H, L, D, Hkv, S = _check_tensors(q, k, v, log_n)
@@ -184,3 +190,42 @@ def apply_chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, log_n, cu_seql
     cu_dev = cu_host.to(device=q.device, dtype=torch.int32)
     return _launch(q, k, v, alpha, beta, mu, ssmax, log_n, 0, softmax_scale, eps, out,
                    cu_dev=cu_dev, nseq=int(lens.numel()), max_seqlen=int(lens.max()))
+
+
+def chord_decode_workspace(B, H, Hkv, L, capacity, D, dtype, device) -> torch.Tensor:
+    '''A workspace for chord_decode_cursor at these sizes.'''
+    n = _lib.lib().motif_chord_decode_workspace_bytes(B, H, Hkv, L, capacity, D, _lib.dtype_code(dtype), None)
+    return torch.empty(max(int(n), 1), dtype=torch.uint8, device=device)
+
+
+def chord_decode_cursor(q, k_cache, v_cache, length_dev, alpha, beta, mu, ssmax, log_table, softmax_scale=None,
+                        eps=1e-5, log_n=None, workspace=None):
+    '''Chord attention of L new queries over a fixed-capacity cache (new).
+
+    k_cache / v_cache [B, Hkv, capacity, D] hold `length_dev[0]` cached positions and
+    the L new keys / values right after them.  Attends over length_dev + L keys with
+    q_start = length_dev (the cached length), log_n[b, i] = log_table[q_start + i]
+    unless `log_n` [B, L] is given, then advances length_dev by L -- on the device, so
+    a captured launch replays token after token.  Returns [B, H, L, D].
+    '''
+    B, H, L, D = q.shape
+    Hkv, cap = k_cache.shape[1], k_cache.shape[2]
+    if length_dev.dtype != torch.int32 or length_dev.device != q.device:
+        raise ValueError('chord_decode_cursor: length_dev must be a device int32 tensor')
+    if log_table.dtype != torch.float32 or log_table.numel() < cap:
+        raise ValueError('chord_decode_cursor: log_table must be fp32 with at least `capacity` entries')
+    if softmax_scale is None:
+        softmax_scale = D ** -0.5
+    q = _aligned(q)
+    if workspace is None:
+        workspace = chord_decode_workspace(B, H, Hkv, L, cap, D, q.dtype, q.device)
+    out = torch.empty((B, H, L, D), dtype=q.dtype, device=q.device)
+    ln_sb, ln_st = (log_n.stride(0), log_n.stride(1)) if log_n is not None else (0, 0)
+    rc = _lib.lib().motif_chord_decode(
+        *_lib.t4(q), *_lib.t4(k_cache), *_lib.t4(v_cache), length_dev.data_ptr(), cap,
+        alpha.data_ptr(), beta.data_ptr(), mu.data_ptr(), ssmax.data_ptr(),
+        _lib.ptr(log_n), ln_sb, ln_st, log_table.data_ptr(), log_table.numel(),
+        *_lib.t4(out), B, H, Hkv, L, D, float(softmax_scale), float(eps),
+        workspace.data_ptr(), workspace.numel(), _lib.dtype_code(q.dtype), _lib.stream_ptr(q.device))
+    _lib.check(rc, 'motif_chord_decode')
+    return out

@@ -9,11 +9,15 @@ over HBM, rounding to the activation dtype where the reference's separate ops ro
   (motif/block/decoder.py:208-213).
 
 `usable(*tensors)` says whether the kernels serve a call (ROCm, bf16/fp32, 16-byte
-aligned rows, no autograd); callers keep the torch formula otherwise.
+aligned rows, no autograd); callers keep the torch formula otherwise.  Each wrapper
+also computes its torch formula itself when any input or weight needs a gradient
+(the kernels are forward-only), so no caller can drop a gradient by accident.
 '''
 import torch
+import torch.nn.functional as F
 
 from . import _lib
+from .autograd_path import wants_grad
 
 
 def usable(*ts):
@@ -37,6 +41,10 @@ def gated_rms_norm_heads(o, gate, weight, eps):
     gate: [B, L, H*dv]).'''
     B, H, L, dv = o.shape
     dt = o.dtype
+    if wants_grad(o, gate, weight):
+        of = o.float()
+        y = (of * torch.rsqrt(of.pow(2).mean(-1, keepdim=True) + eps)).to(dt) * weight.to(dt)
+        return (y.transpose(1, 2) * F.silu(gate.reshape(B, L, H, dv))).reshape(B, L, H * dv)
     w = weight.detach().to(dt).contiguous()
     y = torch.empty(B, L, H * dv, dtype=dt, device=o.device)
     rc = _lib.lib().motif_gated_rms_norm(
@@ -49,6 +57,9 @@ def gated_rms_norm_heads(o, gate, weight, eps):
 
 def swiglu(x):
     '''x [..., 2I] -> x[..., :I] * SiLU(x[..., I:]).'''
+    if wants_grad(x):
+        out, gate = x.chunk(2, dim=-1)
+        return out * F.silu(gate)
     x2 = x.reshape(-1, x.shape[-1])
     M, I = x2.shape[0], x.shape[-1] // 2
     y = torch.empty(*x.shape[:-1], I, dtype=x.dtype, device=x.device)
@@ -61,6 +72,9 @@ def swiglu(x):
 def add_fold(a, b, p=None):
     '''(f, p') with f = a + b and p' = p + f (p' is None when p is None); a, b, p of one
     shape [..., N].'''
+    if wants_grad(a, b, p):
+        f = a + b
+        return f, (None if p is None else p + f)
     N = a.shape[-1]
     a2, b2 = a.reshape(-1, N), b.reshape(-1, N)
     f = torch.empty_like(a, memory_format=torch.contiguous_format)
@@ -84,6 +98,9 @@ def gdn_gates(a, b, a_log, dt_bias):
     the reference's six elementwise ops (motif/block/attention/gdn_attn.py:193-195).'''
     B, L, H = a.shape
     dt = a.dtype
+    if wants_grad(a, b, a_log, dt_bias):
+        g = -a_log.exp() * F.softplus(a + dt_bias)
+        return torch.sigmoid(b).transpose(1, 2), g.transpose(1, 2)
     al = a_log.detach().to(dt).contiguous()
     db = dt_bias.detach().to(dt).contiguous()
     beta = torch.empty(B, H, L, dtype=dt, device=a.device)
@@ -98,6 +115,8 @@ def gdn_gates(a, b, a_log, dt_bias):
 
 def mul_sigmoid(x, g):
     '''x * sigmoid(g) (both [..., N], row-major views).'''
+    if wants_grad(x, g):
+        return x * torch.sigmoid(g)
     N = x.shape[-1]
     x2, g2 = x.reshape(-1, N), g.reshape(-1, N)
     y = torch.empty(x.shape, dtype=x.dtype, device=x.device)

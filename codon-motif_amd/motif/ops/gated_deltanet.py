@@ -11,19 +11,14 @@ Differences that do not change results beyond rounding:
 - `chunk_size` is rounded down to one of the kernel chunk lengths
   {16, 32, 64} (values >= 64 use 64); the chunk length only changes the order
   of floating-point operations, not the recurrence.
-Backward is not implemented: calling with inputs that require grad under
-autograd raises NotImplementedError.
+The HIP kernels are forward-only: calls whose inputs need gradients (training)
+take the differentiable torch form of the chunked rule
+(motif/ops/autograd_path.py:gdn_chunk_torch), so autograd supplies the backward.
 '''
 import torch
 
 from . import _lib
-from .autograd_path import gdn_chunk_torch
-
-
-def _needs_grad(*ts):
-    '''True when autograd must see this call (training): the HIP kernels are
-    forward-only, so such calls take the differentiable torch form.'''
-    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
+from .autograd_path import gdn_chunk_torch, wants_grad as _needs_grad
 
 __all__ = [
     'recurrent_gated_delta_rule',
@@ -62,8 +57,8 @@ def _prepare(q, k, v, beta, g, name):
         raise ValueError(f'{name}: inputs must live on the ROCm device (the HIP kernels have no CPU path)')
     if len({t.device for t in ts}) != 1:
         raise ValueError(f'{name}: inputs must share one device')
-    if any(t.requires_grad for t in ts) and torch.is_grad_enabled():
-        raise NotImplementedError(f'{name}: backward is not implemented by the HIP kernels')
+    # calls that need gradients never get here: the public functions route them to
+    # the torch form first
     dts = {t.dtype for t in ts}
     if not dts <= {torch.float32, torch.bfloat16}:
         raise NotImplementedError(f'{name}: dtypes {sorted(map(str, dts))} unsupported (float32 / bfloat16)')
@@ -217,7 +212,7 @@ def chunk_gated_delta_rule_gated_norm(q, k, v, beta, g, gate, norm_weight, norm_
     name = 'chunk_gated_delta_rule_gated_norm'
     if q.dtype != torch.bfloat16 or gate.dtype != torch.bfloat16 or not q.is_cuda:
         return None
-    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, beta, g, gate, norm_weight)):
+    if _needs_grad(q, k, v, beta, g, gate, norm_weight, S):
         return None
     (qc, kc, vc, bc, gc), _ = _prepare(q, k, v, beta, g, name)
     B, H, L, Dk = qc.shape

@@ -11,8 +11,10 @@ round):
   'swiglu'  y = (x W_a^T) * SiLU(x W_b^T)        SwiGLU MLP, W = [W_a; W_b] (gate_up_proj)
 '''
 import torch
+import torch.nn.functional as F
 
 from . import _lib
+from .autograd_path import wants_grad
 
 EPILOGUES = {'none': 0, 'gate': 1, 'resid': 2, 'swiglu': 3}
 
@@ -35,7 +37,7 @@ def rows_eligible(x, weight, bias=None):
     MAX_ROWS rows, no bias, no autograd, and 16-byte aligned rows.'''
     if bias is not None or not x.is_cuda or x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
         return False
-    if torch.is_grad_enabled() and (x.requires_grad or weight.requires_grad):
+    if wants_grad(x, weight):
         return False
     K = x.shape[-1]
     if K % 32 or weight.dim() != 2 or weight.shape[1] != K or weight.stride(1) != 1 or weight.stride(0) % 8:
@@ -61,6 +63,8 @@ def linear_rows(x, weight, epilogue='none', aux=None, aux2=None, out=None, out2=
         y [..., Nout] (and y2 for 'resid' with aux2).
     '''
     code = EPILOGUES[epilogue]
+    if wants_grad(x, weight, aux, aux2):
+        return _torch_form(x, weight, code, aux, aux2)
     x2, lead = _rows2d(x)
     if x2 is None:
         x2 = x.reshape(-1, x.shape[-1]).contiguous()
@@ -95,6 +99,20 @@ def linear_rows(x, weight, epilogue='none', aux=None, aux2=None, out=None, out2=
         _lib.stream_ptr(dev))
     _lib.check(rc, 'motif_linear_rows')
     return (y, y2) if code == 2 and a2 is not None else y
+
+
+def _torch_form(x, weight, code, aux, aux2):
+    '''The projection and its epilogue as torch ops (differentiable).'''
+    y = F.linear(x, weight)
+    if code == 1:
+        return y * torch.sigmoid(aux)
+    if code == 2:
+        y = aux + y
+        return y if aux2 is None else (y, aux2 + y)
+    if code == 3:
+        out, gate = y.chunk(2, dim=-1)
+        return out * F.silu(gate)
+    return y
 
 
 def project(x, weight, bias=None):

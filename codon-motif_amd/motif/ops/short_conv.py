@@ -11,7 +11,7 @@ import ctypes
 import torch
 
 from . import _lib
-from .autograd_path import short_conv_silu_torch
+from .autograd_path import short_conv_silu_torch, wants_grad
 
 
 def _conv_call(x, w, cache, new_cache, y, cu, nseq, max_len, head_dim, scale):
@@ -45,7 +45,7 @@ def short_conv_silu(x, weight, cache=None, y=None, new_cache=None, head_dim=None
     Returns:
         (y [B, L, D], new_cache [B, D, K-1])
     '''
-    if torch.is_grad_enabled() and (x.requires_grad or weight.requires_grad):
+    if wants_grad(x, weight, cache):
         # forward-only kernel: training takes the differentiable torch form
         y_, tail = short_conv_silu_torch(x, weight, cache, head_dim, scale)
         if new_cache is not None:
@@ -80,7 +80,7 @@ def short_conv_silu_varlen(x, weight, cu_seqlens, max_seqlen=None, head_dim=None
     Returns:
         (y [1, T, D], tails [nseq, D, K-1])
     '''
-    if torch.is_grad_enabled() and (x.requires_grad or weight.requires_grad):
+    if wants_grad(x, weight):
         # per sequence in the differentiable torch form (training)
         cu = [int(c) for c in cu_seqlens.detach().cpu()]
         parts = [short_conv_silu_torch(x[:, cu[i]:cu[i + 1]], weight, None, head_dim, scale)
@@ -118,6 +118,8 @@ def short_conv_silu_multi(xs, weights, caches, head_dims, scales, cu_seqlens=Non
     '''
     n = len(xs)
     x0 = xs[0]
+    if wants_grad(xs, weights, caches):
+        return None
     if not 1 <= n <= 3 or not x0.is_cuda or x0.dtype not in (torch.bfloat16, torch.float32):
         return None
     B, L = x0.shape[0], x0.shape[1]

@@ -211,23 +211,26 @@ int motif_chord_fwd(
 
 /*
  * One decode step of a GatedDeltaAttention layer after its input projections, fused:
- * conv + SiLU of the new token (q, k, v; conv tails shifted in place), q / k L2
- * normalisation (q * dk^-1/2), gates beta = sigmoid(b), g = -exp(A_log) softplus(a +
- * dt_bias), the delta-rule update of the fp32 state (in place) and the GatedRMSNorm
- * of the head outputs.  Replaces the L == 1 path of
+ * conv + SiLU of the new token (q, k, v), q / k L2 normalisation (q * dk^-1/2), gates
+ * beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias), the delta-rule update of the
+ * fp32 state and the GatedRMSNorm of the head outputs.  Replaces the L == 1 path of
  * motif/block/attention/gdn_attn.py:183-209 (conv :116-136, recurrent_gated_delta_rule
  * motif/ops/gated_deltanet.py:26-59, GatedRMSNorm motif/ops/rms_norm.py:530-553).
  *   proj [B, ncols] (row stride proj_sb) holds the projections at column offsets
  *   q_off (H*dk), k_off (H*dk), v_off (H*dv), g_off (H*dv, the norm gate), a_off (H),
- *   b_off (H); wq, wk [H*dk, K], wv [H*dv, K] conv weights; tail_q/k/v [B, C, K-1];
- *   a_log, dt_bias [H]; norm_weight [dv]; state [B, H, dk, dv] fp32; y [B, H*dv]
- *   (row stride y_sb).  All but the state in `dtype`.  dk in {16, 32, 64}, dv <= 128.
+ *   b_off (H); wq, wk [H*dk, K], wv [H*dv, K] conv weights; tail_q/k/v [B, C, K-1] in,
+ *   tail_q/k/v_out [B, C, K-1] the shifted tails; a_log, dt_bias [H]; norm_weight [dv];
+ *   state [B, H, dk, dv] fp32 in, state_out the new state; y [B, H*dv] (row stride
+ *   y_sb).  Outputs may alias their inputs (an in-place step).  All but the states in
+ *   `dtype`.  dk in {16, 32, 64}, dv <= 128.
  */
 int motif_gdn_decode_fused(
     const void *proj, int64_t proj_sb, int q_off, int k_off, int v_off, int g_off, int a_off, int b_off,
-    const void *wq, const void *wk, const void *wv, void *tail_q, void *tail_k, void *tail_v,
+    const void *wq, const void *wk, const void *wv, const void *tail_q, const void *tail_k, const void *tail_v,
+    void *tail_q_out, void *tail_k_out, void *tail_v_out,
     const void *a_log, const void *dt_bias, const void *norm_weight, float norm_eps,
-    float *state, void *y, int64_t y_sb, int B, int H, int dk, int dv, int K, int dtype, void *stream);
+    const float *state, float *state_out, void *y, int64_t y_sb, int B, int H, int dk, int dv, int K, int dtype,
+    void *stream);
 
 /*
  * ChordAttention input stage for a preallocated KV cache: from the fused q | k | v
@@ -238,7 +241,12 @@ int motif_gdn_decode_fused(
  *   v_cache[b, g, pos + t]   = v_g
  * RMSNorm as motif/ops/rms_norm.py:481-486 (T(x * rsqrt(mean(x^2) + eps)) * w).
  * Replaces motif/block/attention/chord_attn.py:255-265 and the KV append
- * (motif/model/cache.py:170-215).  length_dev (optional) is set to pos + L.
+ * (motif/model/cache.py:170-215).
+ *   pos >= 0: a host position (pos + L <= capacity); length_dev, if given, is set to
+ *             pos + L.
+ *   pos < 0:  the position is read from the device cursor *length_dev (left as is:
+ *             motif_chord_decode advances it); cache rows at or past `capacity` are
+ *             not written.
  * All row starts 16-byte aligned; D * sizeof(T) in {64, 128, 256, 512} bytes.
  */
 int motif_chord_qkv_prep(const void *proj, int64_t p_sb, int64_t p_st, int q_off, int k_off, int v_off,
@@ -246,8 +254,45 @@ int motif_chord_qkv_prep(const void *proj, int64_t p_sb, int64_t p_st, int q_off
                          void *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
                          void *k_cache, int64_t k_sb, int64_t k_sh, int64_t k_st,
                          void *v_cache, int64_t v_sb, int64_t v_sh, int64_t v_st,
-                         int *length_dev, int pos, int B, int L, int H, int Hkv, int D, int dtype,
+                         int *length_dev, int pos, int capacity, int B, int L, int H, int Hkv, int D, int dtype,
                          void *stream);
+
+/*
+ * Workspace bytes of motif_chord_decode for a cache of `capacity` positions (the
+ * split partials, plus the fp32 path's bias table); *splits (may be NULL) receives
+ * the key-range split count.
+ */
+size_t motif_chord_decode_workspace_bytes(int B, int H, int Hkv, int L, int capacity, int D, int dtype,
+                                          int *splits);
+
+/*
+ * Chord attention of L new queries over a fixed-capacity KV cache whose length lives
+ * on the device: *length_dev positions are cached and the L new keys / values are
+ * already at [*length_dev, *length_dev + L) (motif_chord_qkv_prep with pos < 0 puts
+ * them there).  Attends over S = *length_dev + L keys with q_start = *length_dev (the
+ * reference rule chord_attn.py:266-268, q_start = cached length), then advances
+ * *length_dev by L, so one captured launch sequence serves token after token.
+ * Replaces the decode call of motif/ops/chord_attention.py:1557-1625 (split-K and
+ * merge :1128-1229) with the cached-length bookkeeping of motif/model/cache.py:170-215
+ * and the log_n lookup of motif/block/attention/chord_attn.py:274-283 moved to the
+ * device.
+ *   q [B,H,L,D]; k_cache, v_cache [B,Hkv,capacity,D]; out [B,H,L,D]   (dtype)
+ *   log_n [B,L] fp32, or NULL: log_n[b,i] = log_table[q_start + i] with log_table
+ *   ln(1..log_table_len), log_table_len >= capacity.
+ *   A cursor that would pass the capacity is clamped on the device (the window then
+ *   ends at the capacity); callers check the length on the host.
+ *   D == 64; bf16 or fp32.
+ */
+int motif_chord_decode(
+    const void *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void *k_cache, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void *v_cache, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    int *length_dev, int capacity,
+    const float *alpha, const float *beta, const float *mu, const float *ssmax,
+    const float *log_n, int64_t ln_sb, int64_t ln_st, const float *log_table, int log_table_len,
+    void *out, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    int B, int H, int Hkv, int L, int D, float scale, float eps,
+    void *workspace, size_t workspace_bytes, int dtype, void *stream);
 
 /*
  * Intra-block attention-residual read (one fused pass):

@@ -84,6 +84,14 @@ def test_op_entry_points_route_grad_calls():
     assert torch.allclose(o2, o, atol=1e-5)
 
 
+def _identity_read(name):
+    '''The first decoder of a block reads one source, which the attention-residual read
+    returns unchanged (motif/ops/attn_res.py:619-620): its pseudo-query and norm weight
+    never enter the graph, in the reference as here.'''
+    import re
+    return re.fullmatch(r'blocks\.\d+\.(pseudo_queries\.0|attn_res_norms\.0\.weight)', name) is not None
+
+
 def test_tiny_model_backward_on_cpu():
     from motif.model.config import MotifChordConfig
     from motif.model.motif import MotifChordModel
@@ -94,8 +102,10 @@ def test_tiny_model_backward_on_cpu():
     ids = torch.randint(0, 97, (2, 70), generator=torch.Generator().manual_seed(1))
     out = m(ids, labels=ids)
     out.loss.backward()
-    grads = [p.grad for p in m.parameters() if p.grad is not None]
-    assert len(grads) > 20 and all(torch.isfinite(gr).all() for gr in grads)
+    for name, p in m.named_parameters():
+        if p.requires_grad and not _identity_read(name):
+            assert p.grad is not None, f'{name} got no gradient'
+            assert torch.isfinite(p.grad).all(), name
 
 
 @pytest.mark.gpu
@@ -123,3 +133,57 @@ def test_training_forward_matches_kernel_inference():
     assert err <= 1e-4 * max(1.0, ref.abs().max().item()), err
     out.float().pow(2).mean().backward()
     assert all(torch.isfinite(p.grad).all() for p in m.parameters() if p.grad is not None)
+
+
+def _train_grads(model, ids, cu=None):
+    model.zero_grad(set_to_none=True)
+    logits = model(ids, cu_seqlens=cu).logits
+    logits.float().pow(2).mean().backward()
+    return {n: p.grad.detach().cpu().clone() for n, p in model.named_parameters() if p.grad is not None}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('case', ['plain', 'packed', 'frozen_conv', 'frozen_embed'])
+def test_gpu_gradients_match_cpu(case):
+    '''Training on the GPU (fp32 tiny model with head_dim 64, so the kernels would serve
+    its inference calls): every parameter that requires grad gets a gradient, and every
+    gradient equals the same model's gradient on the CPU within 1e-3 of its scale.
+    Cases: a padded batch, packed sequences (cu_seqlens), frozen conv weights (the
+    layer's other parameters still train), a frozen embedding (the first layer's input
+    needs no gradient, its weights do).'''
+    import copy
+
+    from motif.model.config import MotifChordConfig
+    from motif.model.motif import MotifChordModel
+    cfg = MotifChordConfig(vocab_size=128, model_dim=256, num_heads=4, num_kv_heads=2, head_k_dim=64,
+                           block=('gdn', 'chord'), block_n=2, tied_weight=False)
+    torch.manual_seed(0)
+    m = MotifChordModel(cfg)
+    with torch.no_grad():
+        for p in m.parameters():
+            p.add_(torch.randn_like(p) * 0.02)
+    if case == 'frozen_conv':
+        for blk in m.blocks:
+            for dec in blk.features:
+                if dec.attn_type == 'gdn':
+                    for c in (dec.attn.q_conv, dec.attn.k_conv, dec.attn.v_conv):
+                        c.weight.requires_grad_(False)
+    if case == 'frozen_embed':
+        m.embed.weight.requires_grad_(False)
+    m = m.train()
+    g_ = torch.Generator().manual_seed(1)
+    cu = None
+    if case == 'packed':
+        ids = torch.randint(0, 128, (1, 150), generator=g_)
+        cu = torch.tensor([0, 40, 41, 110, 150], dtype=torch.int32)
+    else:
+        ids = torch.randint(0, 128, (2, 90), generator=g_)
+    ref = _train_grads(m, ids, cu)
+    gm = copy.deepcopy(m).cuda()
+    got = _train_grads(gm, ids.cuda(), None if cu is None else cu.cuda())
+    want = {n for n, p in m.named_parameters() if p.requires_grad and not _identity_read(n)}
+    assert set(ref) == want and set(got) == want, (sorted(want - set(got)), sorted(want - set(ref)))
+    for n in sorted(want):
+        scale = ref[n].abs().max().item()
+        err = (got[n] - ref[n]).abs().max().item()
+        assert err <= 1e-3 * scale + 1e-7, f'{case}: {n} gradient differs by {err:.3e} (scale {scale:.3e})'

@@ -50,7 +50,7 @@ def test_static_cache_matches_general_path(dtype):
     ref_cache = KVLayerCache()
     ref = _run(layer, ref_cache, x, splits, unfused=True)
     st = StaticKVLayerCache().allocate(B, 2, 64, 64, DEV, dtype)
-    assert layer._prep_fusable(x[:, :1])
+    assert layer._prep_fusable(x[:, :1], None)
     out = _run(layer, st, x, splits)
     grow = _run(layer, KVLayerCache(), x, splits)
     if dtype == torch.float32:
