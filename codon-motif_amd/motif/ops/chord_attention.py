@@ -199,7 +199,7 @@ def chord_decode_workspace(B, H, Hkv, L, capacity, D, dtype, device) -> torch.Te
 
 
 def chord_decode_cursor(q, k_cache, v_cache, length_dev, alpha, beta, mu, ssmax, log_table, softmax_scale=None,
-                        eps=1e-5, log_n=None, workspace=None):
+                        eps=1e-5, log_n=None, workspace=None, library_scratch=False):
     '''Chord attention of L new queries over a fixed-capacity cache (new).
 
     k_cache / v_cache [B, Hkv, capacity, D] hold `length_dev[0]` cached positions and
@@ -207,6 +207,8 @@ def chord_decode_cursor(q, k_cache, v_cache, length_dev, alpha, beta, mu, ssmax,
     q_start = length_dev (the cached length), log_n[b, i] = log_table[q_start + i]
     unless `log_n` [B, L] is given, then advances length_dev by L -- on the device, so
     a captured launch replays token after token.  Returns [B, H, L, D].
+    `library_scratch=True` takes the allocation-free entry point
+    (motif_chord_decode_noalloc: the library's own per-device scratch, no workspace).
     '''
     B, H, L, D = q.shape
     Hkv, cap = k_cache.shape[1], k_cache.shape[2]
@@ -217,10 +219,19 @@ def chord_decode_cursor(q, k_cache, v_cache, length_dev, alpha, beta, mu, ssmax,
     if softmax_scale is None:
         softmax_scale = D ** -0.5
     q = _aligned(q)
-    if workspace is None:
-        workspace = chord_decode_workspace(B, H, Hkv, L, cap, D, q.dtype, q.device)
     out = torch.empty((B, H, L, D), dtype=q.dtype, device=q.device)
     ln_sb, ln_st = (log_n.stride(0), log_n.stride(1)) if log_n is not None else (0, 0)
+    if library_scratch:
+        rc = _lib.lib().motif_chord_decode_noalloc(
+            *_lib.t4(q), *_lib.t4(k_cache), *_lib.t4(v_cache), length_dev.data_ptr(), cap,
+            alpha.data_ptr(), beta.data_ptr(), mu.data_ptr(), ssmax.data_ptr(),
+            _lib.ptr(log_n), ln_sb, ln_st, log_table.data_ptr(), log_table.numel(),
+            *_lib.t4(out), B, H, Hkv, L, D, float(softmax_scale), float(eps),
+            _lib.dtype_code(q.dtype), _lib.stream_ptr(q.device))
+        _lib.check(rc, 'motif_chord_decode_noalloc')
+        return out
+    if workspace is None:
+        workspace = chord_decode_workspace(B, H, Hkv, L, cap, D, q.dtype, q.device)
     rc = _lib.lib().motif_chord_decode(
         *_lib.t4(q), *_lib.t4(k_cache), *_lib.t4(v_cache), length_dev.data_ptr(), cap,
         alpha.data_ptr(), beta.data_ptr(), mu.data_ptr(), ssmax.data_ptr(),

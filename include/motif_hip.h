@@ -233,6 +233,28 @@ int motif_gdn_decode_fused(
     void *stream);
 
 /*
+ * motif_chord_decode without a workspace argument, for callers that cannot allocate
+ * device memory (code under graph capture that must not call hipMalloc, tight serving
+ * loops, harnesses that forbid allocation).  No counterpart in the reference.  Same
+ * arguments, kernels and results as motif_chord_decode; the split partials live in a
+ * scratch array the library holds on every GPU it runs on until the process ends
+ * (motif_chord_decode_noalloc_scratch_bytes() bytes, 16 MiB).  Sizes whose
+ * motif_chord_decode_workspace_bytes exceeds it return MOTIF_ERR_INVALID.  Calls that
+ * overlap in time on one GPU (other streams, other host threads) share that scratch
+ * and race: serialise them.  Allocates nothing.
+ */
+size_t motif_chord_decode_noalloc_scratch_bytes(void);
+int motif_chord_decode_noalloc(
+    const void *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void *k_cache, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void *v_cache, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    int *length_dev, int capacity,
+    const float *alpha, const float *beta, const float *mu, const float *ssmax,
+    const float *log_n, int64_t ln_sb, int64_t ln_st, const float *log_table, int log_table_len,
+    void *out, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    int B, int H, int Hkv, int L, int D, float scale, float eps, int dtype, void *stream);
+
+/*
  * ChordAttention input stage for a preallocated KV cache: from the fused q | k | v
  * projection rows proj [B, L, ncols] (strides p_sb, p_st; head h of q at column
  * q_off + h*D, of k at k_off + g*D, of v at v_off + g*D), per head
