@@ -97,6 +97,21 @@ struct WsLayout {
   }
 };
 
+// Fused front end of the prefill (motif_gdn_prefill_fused): the prep kernel reads the
+// raw input projections of the chunk and computes q, k, v (short causal conv + SiLU,
+// q / k L2-normalised, q scaled) and the gates beta, g itself, so they never go
+// through HBM.  Conv kernel length kConvK.
+constexpr int kConvK = 4;
+struct FrontArgs {
+  const bf16_t *x; int64_t x_sb, x_st;        // projection rows [B, L, ncols]
+  int q_off, k_off, v_off, a_off, b_off;      // column offsets of q, k, v, a, b
+  const bf16_t *wq, *wk, *wv;                 // conv weights [C, kConvK]
+  const bf16_t *tq, *tk, *tv;                 // incoming conv tails [B, C, K-1] or nullptr
+  bf16_t *oq, *ok, *ov;                       // outgoing tails [nseq, C, K-1] or nullptr
+  const bf16_t *a_log, *dt_bias;              // [H]
+  float q_scale;                              // dk^-1/2
+};
+
 // ------------------------------------------------------------------ prep
 // LDS planes of [rows][64] bf16 (128-byte rows), 16-byte chunks XOR-swizzled by
 // row so that 16 rows read at one column hit distinct banks.  Element offset of
@@ -169,8 +184,8 @@ struct PrepLayout {
   static constexpr int bytes = small + 2 * 64 * 4;
 };
 
-template <int DK, int DV>
-__global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca, char *ws) {
+template <int DK, int DV, bool FRONT>
+__global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca, char *ws, FrontArgs fa) {
   using TI = bf16_t;
   using PL = PrepLayout<DK, DV>;
   constexpr int NTS = 68;  // NT row stride (floats)
@@ -189,59 +204,212 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
   const int ln = lane & 15, g = lane >> 4;
   const ChunkInfo ci = resolve_chunk(chunk, kC, a.L, ca);
 
-  const TI *qb = static_cast<const TI *>(a.q) + ci.batch * a.q_sb + h * a.q_sh + int64_t(ci.t0) * a.q_st;
-  const TI *kb = static_cast<const TI *>(a.k) + ci.batch * a.k_sb + h * a.k_sh + int64_t(ci.t0) * a.k_st;
-  const TI *vb = static_cast<const TI *>(a.v) + ci.batch * a.v_sb + h * a.v_sh + int64_t(ci.t0) * a.v_st;
-  const TI *bb = static_cast<const TI *>(a.beta) + ci.batch * a.b_sb + h * a.b_sh + int64_t(ci.t0) * a.b_st;
-  const TI *gb = static_cast<const TI *>(a.g) + ci.batch * a.g_sb + h * a.g_sh + int64_t(ci.t0) * a.g_st;
-
-  // ---- phase 1: rows 2p, 2p + 1 of one 8-column segment per thread (zero past len);
-  // p = tid % 32, so the 4-byte transposed writes of a wavefront cover 32 distinct
-  // column pairs of one LDS row (distinct banks).
-  constexpr int KSEG = DK / 8, VSEG = DV / 8, VP = 32 * VSEG / 256;
+  // variables phase 1 leaves for the later phases (the FRONT form uses its own)
+  constexpr int KSEG = DK / 8, VP = 32 * (DV / 8) / 256;
   const int kp = tid & 31, kseg = tid >> 5;
   const bool kval = kseg < KSEG;
-  // Loads go through range-checked buffers over the chunk's valid rows: rows past
-  // len read as zeros with no branches (so every load of the phase is in flight at once).
-  const int last = ci.len - 1;
-  const buf_t kbuf = make_buf(kb, (last * a.k_st + DK) * 2), qbuf = make_buf(qb, (last * a.q_st + DK) * 2);
-  const buf_t vbuf = make_buf(vb, (last * a.v_st + a.dv) * 2);
-  const buf_t gbuf = make_buf(gb, (last * a.g_st + 1) * 2), bbuf = make_buf(bb, (last * a.b_st + 1) * 2);
-  // gates (every wavefront loads them; wavefront 0 takes the prefix sum)
-  const float gv = buf_ld<TI>(gbuf, lane * a.g_st), bv = buf_ld<TI>(bbuf, lane * a.b_st);
-  const int kc = 8 * min(kseg, KSEG - 1);
-  const uint4 k0r = buf_ld16(kbuf, ((2 * kp) * a.k_st + kc) * 2), k1r = buf_ld16(kbuf, ((2 * kp + 1) * a.k_st + kc) * 2);
-  const uint4 q0r = buf_ld16(qbuf, ((2 * kp) * a.q_st + kc) * 2), q1r = buf_ld16(qbuf, ((2 * kp + 1) * a.q_st + kc) * 2);
-  uint4 v0r[VP], v1r[VP];
-#pragma unroll
-  for (int r = 0; r < VP; ++r) {
-    const int vp = tid & 31, vs = (tid >> 5) + 8 * r;
-    const int vc = 8 * min(vs, a.dv / 8 - 1);
-    v0r[r] = buf_ld16(vbuf, ((2 * vp) * a.v_st + vc) * 2);
-    v1r[r] = buf_ld16(vbuf, ((2 * vp + 1) * a.v_st + vc) * 2);
-  }
-  // Q rows of this wavefront's Q' row tile (tile w): Q[16 w + ln][16 dt + 4g .. +3].
+  uint4 k0r = {}, k1r = {}, v0r[VP], v1r[VP];
   bf16x4 qe[DK / 16];
+  constexpr int RQ = DK / 8, RV = DV / 16, RM = RQ > RV ? RQ : RV;
+  uint32_t cv[RM][4];  // FRONT: this thread's conv outputs, bf16 channel pairs per row
+  int f_seg = 0, f_r0 = 0;
+  if constexpr (!FRONT) {
+    const TI *qb = static_cast<const TI *>(a.q) + ci.batch * a.q_sb + h * a.q_sh + int64_t(ci.t0) * a.q_st;
+    const TI *kb = static_cast<const TI *>(a.k) + ci.batch * a.k_sb + h * a.k_sh + int64_t(ci.t0) * a.k_st;
+    const TI *vb = static_cast<const TI *>(a.v) + ci.batch * a.v_sb + h * a.v_sh + int64_t(ci.t0) * a.v_st;
+    const TI *bb = static_cast<const TI *>(a.beta) + ci.batch * a.b_sb + h * a.b_sh + int64_t(ci.t0) * a.b_st;
+    const TI *gb = static_cast<const TI *>(a.g) + ci.batch * a.g_sb + h * a.g_sh + int64_t(ci.t0) * a.g_st;
+
+    // ---- phase 1: rows 2p, 2p + 1 of one 8-column segment per thread (zero past len);
+    // p = tid % 32, so the 4-byte transposed writes of a wavefront cover 32 distinct
+    // column pairs of one LDS row (distinct banks).
+    // Loads go through range-checked buffers over the chunk's valid rows: rows past
+    // len read as zeros with no branches (so every load of the phase is in flight at once).
+    const int last = ci.len - 1;
+    const buf_t kbuf = make_buf(kb, (last * a.k_st + DK) * 2), qbuf = make_buf(qb, (last * a.q_st + DK) * 2);
+    const buf_t vbuf = make_buf(vb, (last * a.v_st + a.dv) * 2);
+    const buf_t gbuf = make_buf(gb, (last * a.g_st + 1) * 2), bbuf = make_buf(bb, (last * a.b_st + 1) * 2);
+    // gates (every wavefront loads them; wavefront 0 takes the prefix sum)
+    const float gv = buf_ld<TI>(gbuf, lane * a.g_st), bv = buf_ld<TI>(bbuf, lane * a.b_st);
+    const int kc = 8 * min(kseg, KSEG - 1);
+    k0r = buf_ld16(kbuf, ((2 * kp) * a.k_st + kc) * 2);
+    k1r = buf_ld16(kbuf, ((2 * kp + 1) * a.k_st + kc) * 2);
+    const uint4 q0r = buf_ld16(qbuf, ((2 * kp) * a.q_st + kc) * 2), q1r = buf_ld16(qbuf, ((2 * kp + 1) * a.q_st + kc) * 2);
 #pragma unroll
-  for (int dt = 0; dt < DK / 16; ++dt)
-    qe[dt] = __builtin_bit_cast(bf16x4, buf_ld8(qbuf, ((16 * w + ln) * a.q_st + 16 * dt + 4 * g) * 2));
-  if (w == 0) {  // the inclusive prefix sum of g
-    float s = gv;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float y = __shfl_up(s, off, 64);
-      if (lane >= off) s += y;
+    for (int r = 0; r < VP; ++r) {
+      const int vp = tid & 31, vs = (tid >> 5) + 8 * r;
+      const int vc = 8 * min(vs, a.dv / 8 - 1);
+      v0r[r] = buf_ld16(vbuf, ((2 * vp) * a.v_st + vc) * 2);
+      v1r[r] = buf_ld16(vbuf, ((2 * vp + 1) * a.v_st + vc) * 2);
     }
-    gam[lane] = s;
-    bet[lane] = bv;
-  }
-  if (kval) {
-    *reinterpret_cast<uint4 *>(kh + (2 * kp) * PL::kRow + 8 * kseg) = k0r;
-    *reinterpret_cast<uint4 *>(kh + (2 * kp + 1) * PL::kRow + 8 * kseg) = k1r;
-    *reinterpret_cast<uint4 *>(qh + (2 * kp) * PL::kRow + 8 * kseg) = q0r;
-    *reinterpret_cast<uint4 *>(qh + (2 * kp + 1) * PL::kRow + 8 * kseg) = q1r;
+    // Q rows of this wavefront's Q' row tile (tile w): Q[16 w + ln][16 dt + 4g .. +3].
+#pragma unroll
+    for (int dt = 0; dt < DK / 16; ++dt)
+      qe[dt] = __builtin_bit_cast(bf16x4, buf_ld8(qbuf, ((16 * w + ln) * a.q_st + 16 * dt + 4 * g) * 2));
+    if (w == 0) {  // the inclusive prefix sum of g
+      float s = gv;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float y = __shfl_up(s, off, 64);
+        if (lane >= off) s += y;
+      }
+      gam[lane] = s;
+      bet[lane] = bv;
+    }
+    if (kval) {
+      *reinterpret_cast<uint4 *>(kh + (2 * kp) * PL::kRow + 8 * kseg) = k0r;
+      *reinterpret_cast<uint4 *>(kh + (2 * kp + 1) * PL::kRow + 8 * kseg) = k1r;
+      *reinterpret_cast<uint4 *>(qh + (2 * kp) * PL::kRow + 8 * kseg) = q0r;
+      *reinterpret_cast<uint4 *>(qh + (2 * kp + 1) * PL::kRow + 8 * kseg) = q1r;
+    }
+  
+  } else {
+    // ---- phase 1 (fused front end): wave 0 convolves q, wave 1 k, waves 2-3 v.  A
+    // thread walks R consecutive chunk rows of one 8-channel segment with the conv
+    // window in registers; the S segments of a row are S adjacent lanes, so the q / k
+    // L2 norm of a row is a butterfly over them.  Arithmetic as the standalone conv
+    // kernel: fp32 conv, SiLU, norm, one rounding to bf16.
+    constexpr int KC = kConvK;
+    const int prob = w < 2 ? w : 2;
+    const int C = prob < 2 ? DK : DV;
+    const int S = C / 8;
+    const int t = prob < 2 ? lane : tid - 128;
+    const int rows = prob < 2 ? RQ : RV;  // wave-uniform
+    f_seg = t % S;
+    f_r0 = (t / S) * rows;
+    const int chan = h * C + 8 * f_seg;
+    const int col = (prob == 0 ? fa.q_off : prob == 1 ? fa.k_off : fa.v_off) + chan;
+    const bf16_t *wgt = (prob == 0 ? fa.wq : prob == 1 ? fa.wk : fa.wv) + static_cast<size_t>(chan) * KC;
+    const bf16_t *tin = ca.cu ? nullptr : (prob == 0 ? fa.tq : prob == 1 ? fa.tk : fa.tv);
+    const int s_lo = ca.cu ? ca.cu[ci.seq] : 0, s_hi = ca.cu ? ca.cu[ci.seq + 1] : a.L;
+    const bf16_t *xs = fa.x + ci.batch * fa.x_sb + int64_t(s_lo) * fa.x_st + col;
+    // rows outside [s_lo, s_hi) read zeros (a token before the start wraps to a huge offset)
+    const buf_t xbuf = make_buf(xs, s_hi > s_lo ? static_cast<uint32_t>(((s_hi - s_lo - 1) * fa.x_st + 8) * 2) : 0u);
+    const int rel0 = ci.t0 - s_lo + f_r0;  // sequence offset of this thread's first row
+    uint4 raw[KC - 1 + RM];
+#pragma unroll
+    for (int i = 0; i < KC - 1 + RM; ++i)
+      if (i < KC - 1 + rows)
+        raw[i] = buf_ld16(xbuf, static_cast<uint32_t>((rel0 - (KC - 1) + i) * fa.x_st * 2));
+    float wr[8][KC];
+    {
+      float wf[8 * KC];
+#pragma unroll
+      for (int j = 0; j < KC; ++j) {
+        const uint4 u = *reinterpret_cast<const uint4 *>(wgt + 8 * j);
+        const uint32_t ww[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          wf[8 * j + 2 * e] = __uint_as_float(ww[e] << 16);
+          wf[8 * j + 2 * e + 1] = __uint_as_float(ww[e] & 0xffff0000u);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int r = 0; r < KC; ++r) wr[e][r] = wf[e * KC + r];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the loads above stay one batch
+    auto unpack8 = [](const uint4 &u, float *x) {
+      const uint32_t ww[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[2 * e] = __uint_as_float(ww[e] << 16);
+        x[2 * e + 1] = __uint_as_float(ww[e] & 0xffff0000u);
+      }
+    };
+    float win[KC - 1][8];
+#pragma unroll
+    for (int r = 0; r < KC - 1; ++r) {
+      unpack8(raw[r], win[r]);
+      const int tok = rel0 - (KC - 1) + r;
+      if (tin && tok < 0) {  // before the start of a batch row: the cached tail
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          win[r][e] = bf16_to_f32(tin[(static_cast<size_t>(ci.batch) * a.H * C + chan + e) * (KC - 1) + (KC - 1) + tok]);
+      }
+    }
+    const float scale = prob == 0 ? fa.q_scale : 1.f;
+#pragma unroll
+    for (int i = 0; i < RM; ++i) {
+      if (i < rows) {
+        float xt[8], v[8];
+        unpack8(raw[KC - 1 + i], xt);
+        const bool live = f_r0 + i < ci.len;
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float acc = wr[e][KC - 1] * xt[e];
+#pragma unroll
+          for (int r = 0; r < KC - 1; ++r) acc = fmaf(wr[e][r], win[r][e], acc);
+          v[e] = live ? silu_fast(acc) : 0.f;
+          ss = fmaf(v[e], v[e], ss);
+#pragma unroll
+          for (int r = 0; r < KC - 2; ++r) win[r][e] = win[r + 1][e];
+          win[KC - 2][e] = xt[e];
+        }
+        if (prob < 2) {
+#pragma unroll
+          for (int off = 1; off < 8; off <<= 1)
+            if (off < S) ss += __shfl_xor(ss, off, 64);
+          const float f = scale * rcp_fast(fmaxf(sqrtf(ss), 1e-12f));
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] *= f;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) cv[i][e] = pk_bf16(v[2 * e], v[2 * e + 1]);
+        if (prob < 2)
+          *reinterpret_cast<uint4 *>((prob == 0 ? qh : kh) + (f_r0 + i) * PL::kRow + 8 * f_seg) =
+              uint4{cv[i][0], cv[i][1], cv[i][2], cv[i][3]};
+      }
+    }
+    // gates of the chunk's rows (zero past len, as the unfused loads read them)
+    if (w == 0) {
+      float gv = 0.f, bv = 0.f;
+      if (lane < ci.len) {
+        const bf16_t *xr = fa.x + ci.batch * fa.x_sb + int64_t(ci.t0 + lane) * fa.x_st;
+        const float av = bf16_to_f32(xr[fa.a_off + h]), braw = bf16_to_f32(xr[fa.b_off + h]);
+        // beta = T(sigmoid(b)), g = T(-T(exp(A_log)) * T(softplus(T(a + dt_bias)))), threshold 20
+        const float xa = fl(bf(av + bf16_to_f32(fa.dt_bias[h])));
+        const float sp = fl(bf(xa > 20.f ? xa : log1pf(expf(xa))));
+        const float A = fl(bf(expf(bf16_to_f32(fa.a_log[h]))));
+        bv = fl(bf(1.f / (1.f + expf(-braw))));
+        gv = fl(bf(-A * sp));
+      }
+      float sacc = gv;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float y = __shfl_up(sacc, off, 64);
+        if (lane >= off) sacc += y;
+      }
+      gam[lane] = sacc;
+      bet[lane] = bv;
+    }
+    // the sequence's last chunk writes the outgoing conv tails (the last K-1 inputs)
+    if (fa.oq && ci.t0 + ci.len == s_hi) {
+      for (int idx = tid; idx < (2 * DK + DV) * (KC - 1); idx += 256) {
+        const int ca_ = idx / (KC - 1), r = idx % (KC - 1);
+        const int pb = ca_ < DK ? 0 : ca_ < 2 * DK ? 1 : 2;
+        const int Cp = pb < 2 ? DK : DV, c = ca_ - (pb == 0 ? 0 : pb == 1 ? DK : 2 * DK);
+        const int ch = h * Cp + c;
+        const int rel = (s_hi - s_lo) - (KC - 1) + r;
+        const bf16_t *tp = ca.cu ? nullptr : (pb == 0 ? fa.tq : pb == 1 ? fa.tk : fa.tv);
+        bf16_t val = 0;
+        if (rel >= 0)
+          val = fa.x[ci.batch * fa.x_sb + int64_t(s_lo + rel) * fa.x_st + (pb == 0 ? fa.q_off : pb == 1 ? fa.k_off : fa.v_off) + ch];
+        else if (tp)
+          val = tp[(static_cast<size_t>(ci.batch) * a.H * Cp + ch) * (KC - 1) + (KC - 1) + rel];
+        bf16_t *op_ = pb == 0 ? fa.oq : pb == 1 ? fa.ok : fa.ov;
+        op_[(static_cast<size_t>(ci.seq) * a.H * Cp + ch) * (KC - 1) + r] = val;
+      }
+    }
   }
   __syncthreads();
+  if constexpr (FRONT) {
+#pragma unroll
+    for (int dt = 0; dt < DK / 16; ++dt)
+      qe[dt] = *reinterpret_cast<const bf16x4 *>(qh + (16 * w + ln) * PL::kRow + 16 * dt + 4 * g);
+  }
 
   // ---- phase 2: G = K K^T -> N, and K Q^T -> Attn, on 16x16 tiles (bi <= bj).
   // Tile (bi, bj) of G holds G[16 bi + 4g + r][16 bj + ln] = G[16 bj + ln][16 bi + 4g + r]
@@ -403,29 +571,60 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
   }
   const float glast = gam[kC - 1];
   __syncthreads();  // NT and the K / Q rows are dead from here on
-  if (kval) {
-    const int j = 2 * kp;
-    const float f0 = exp_fast(glast - gam[j]), f1 = exp_fast(glast - gam[j + 1]);
-    const bf16x8 ka = __builtin_bit_cast(bf16x8, k0r), kb_ = __builtin_bit_cast(bf16x8, k1r);
+  if constexpr (!FRONT) {
+    if (kval) {
+      const int j = 2 * kp;
+      const float f0 = exp_fast(glast - gam[j]), f1 = exp_fast(glast - gam[j + 1]);
+      const bf16x8 ka = __builtin_bit_cast(bf16x8, k0r), kb_ = __builtin_bit_cast(bf16x8, k1r);
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const int d = 8 * kseg + t;
-      *reinterpret_cast<uint32_t *>(kt + swz(d, j)) = pack2(bits(ka[t]), bits(kb_[t]));
-      const float x0 = fl(ka[t]) * f0, x1 = fl(kb_[t]) * f1;
-      uint32_t hw, lw;
-      split2(x0, x1, hw, lw);
-      *reinterpret_cast<uint32_t *>(ktt_h + swz(d, j)) = hw;
-      *reinterpret_cast<uint32_t *>(ktt_l + swz(d, j)) = lw;
+      for (int t = 0; t < 8; ++t) {
+        const int d = 8 * kseg + t;
+        *reinterpret_cast<uint32_t *>(kt + swz(d, j)) = pack2(bits(ka[t]), bits(kb_[t]));
+        const float x0 = fl(ka[t]) * f0, x1 = fl(kb_[t]) * f1;
+        uint32_t hw, lw;
+        split2(x0, x1, hw, lw);
+        *reinterpret_cast<uint32_t *>(ktt_h + swz(d, j)) = hw;
+        *reinterpret_cast<uint32_t *>(ktt_l + swz(d, j)) = lw;
+      }
     }
-  }
 #pragma unroll
-  for (int r = 0; r < VP; ++r) {
-    const int vp = tid & 31, vs = (tid >> 5) + 8 * r;
-    if (vs < a.dv / 8) {
-      const bf16x8 va = __builtin_bit_cast(bf16x8, v0r[r]), vb_ = __builtin_bit_cast(bf16x8, v1r[r]);
+    for (int r = 0; r < VP; ++r) {
+      const int vp = tid & 31, vs = (tid >> 5) + 8 * r;
+      if (vs < a.dv / 8) {
+        const bf16x8 va = __builtin_bit_cast(bf16x8, v0r[r]), vb_ = __builtin_bit_cast(bf16x8, v1r[r]);
 #pragma unroll
-      for (int t = 0; t < 8; ++t)
-        *reinterpret_cast<uint32_t *>(vt + swz(8 * vs + t, 2 * vp)) = pack2(bits(va[t]), bits(vb_[t]));
+        for (int t = 0; t < 8; ++t)
+          *reinterpret_cast<uint32_t *>(vt + swz(8 * vs + t, 2 * vp)) = pack2(bits(va[t]), bits(vb_[t]));
+      }
+    }
+  
+  } else if (w == 1) {  // K^T and K~^T planes from this thread's K rows (pairs of rows)
+#pragma unroll
+    for (int i = 0; i < RQ; i += 2) {
+      const int j = f_r0 + i;
+      const float f0 = exp_fast(glast - gam[j]), f1 = exp_fast(glast - gam[j + 1]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = 8 * f_seg + e;
+        const uint16_t b0 = static_cast<uint16_t>(cv[i][e >> 1] >> (16 * (e & 1)));
+        const uint16_t b1 = static_cast<uint16_t>(cv[i + 1][e >> 1] >> (16 * (e & 1)));
+        *reinterpret_cast<uint32_t *>(kt + swz(d, j)) = pack2(b0, b1);
+        uint32_t hw, lw;
+        split2(bf16_to_f32(b0) * f0, bf16_to_f32(b1) * f1, hw, lw);
+        *reinterpret_cast<uint32_t *>(ktt_h + swz(d, j)) = hw;
+        *reinterpret_cast<uint32_t *>(ktt_l + swz(d, j)) = lw;
+      }
+    }
+  } else if (w >= 2) {  // V^T plane
+#pragma unroll
+    for (int i = 0; i < RV; i += 2) {
+      const int j = f_r0 + i;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint16_t b0 = static_cast<uint16_t>(cv[i][e >> 1] >> (16 * (e & 1)));
+        const uint16_t b1 = static_cast<uint16_t>(cv[i + 1][e >> 1] >> (16 * (e & 1)));
+        *reinterpret_cast<uint32_t *>(vt + swz(8 * f_seg + e, j)) = pack2(b0, b1);
+      }
     }
   }
   __syncthreads();
@@ -812,14 +1011,14 @@ __global__ void __launch_bounds__(256) gdn_chunk_out(GdnArgs a, ChunkArgs ca, co
   }
 }
 
-template <int DK, int DV>
-int launch_prep(const GdnArgs &a, const ChunkArgs &ca, char *ws, hipStream_t s) {
+template <int DK, int DV, bool FRONT = false>
+int launch_prep(const GdnArgs &a, const ChunkArgs &ca, char *ws, hipStream_t s, const FrontArgs &fa = FrontArgs{}) {
   const size_t smem = PrepLayout<DK, DV>::bytes;
-  auto kern = gdn_prep_mfma<DK, DV>;
+  auto kern = gdn_prep_mfma<DK, DV, FRONT>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
   if (e != hipSuccess) return set_error(MOTIF_ERR_HIP, std::string("gdn_prep_mfma smem: ") + hipGetErrorString(e));
-  kern<<<dim3(ca.total_chunks, a.H), dim3(256), smem, s>>>(a, ca, ws);
+  kern<<<dim3(ca.total_chunks, a.H), dim3(256), smem, s>>>(a, ca, ws, fa);
   return check_launch("gdn_prep_mfma");
 }
 
@@ -863,5 +1062,94 @@ int launch_chunk_mfma(const GdnArgs &a, const ChunkArgs &ca, void *workspace, hi
   char *ws = static_cast<char *>(workspace);
   return a.dk == 32 ? launch_dk<32>(a, ca, ws, s) : launch_dk<64>(a, ca, ws, s);
 }
+namespace {
+
+template <int DK, int DV>
+int launch_fused(const GdnArgs &a, const ChunkArgs &ca, const FrontArgs &fa, char *ws, hipStream_t s) {
+  int rc = launch_prep<DK, DV, true>(a, ca, ws, s, fa);
+  if (rc) return rc;
+  const ScanGrid sgrid{a.dv / 16, a.H * ca.nseq};
+  gdn_state_scan<DK><<<sgrid.blocks(), dim3(64 * (DK / 16)), 0, s>>>(a, ca, ws, sgrid);
+  if ((rc = check_launch("gdn_state_scan"))) return rc;
+  gdn_chunk_out<bf16_t, DK><<<dim3(ca.total_chunks, a.H), dim3(256), 0, s>>>(a, ca, ws, 0);
+  return check_launch("gdn_chunk_out");
+}
+
+}  // namespace
+
+}  // namespace motif
+
+extern "C" int motif_gdn_prefill_fused(
+    const void *proj, int64_t p_sb, int64_t p_st, int q_off, int k_off, int v_off, int g_off, int a_off, int b_off,
+    const void *wq, const void *wk, const void *wv, int conv_k,
+    const void *tail_q, const void *tail_k, const void *tail_v, void *tail_q_out, void *tail_k_out, void *tail_v_out,
+    const void *a_log, const void *dt_bias, float q_scale, const void *norm_weight, float norm_eps,
+    const float *state_in, float *state_out, void *y, int64_t y_sb, int64_t y_st,
+    int B, int H, int L, int dk, int dv,
+    const int32_t *cu_seqlens, const int32_t *chunk_offsets, int nseq, int total_chunks,
+    void *workspace, size_t workspace_bytes, void *stream) {
+  using namespace motif;
+  if (B < 0 || H <= 0 || L < 0 || dk <= 0 || dv <= 0) return set_error(MOTIF_ERR_INVALID, "gdn_prefill: bad size");
+  if (!((dk == 32 || dk == 64) && (dv == 64 || dv == 128) && conv_k == kConvK))
+    return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_prefill: dk in {32, 64}, dv in {64, 128} and conv kernel 4 only");
+  const bool packed = cu_seqlens != nullptr;
+  if (packed && (B != 1 || !chunk_offsets || nseq <= 0))
+    return set_error(MOTIF_ERR_INVALID, "gdn_prefill: packed sequences need B == 1, chunk_offsets and nseq > 0");
+  if (!packed && nseq != B) return set_error(MOTIF_ERR_INVALID, "gdn_prefill: nseq must equal B");
+  if (packed && (tail_q || tail_k || tail_v))
+    return set_error(MOTIF_ERR_INVALID, "gdn_prefill: packed sequences start from zero conv tails");
+  const int nper = packed ? 0 : (L + kC - 1) / kC;
+  if (!packed && total_chunks != B * nper)
+    return set_error(MOTIF_ERR_INVALID, "gdn_prefill: total_chunks must be B * ceil(L / 64)");
+  if (!proj || !wq || !wk || !wv || !a_log || !dt_bias || !norm_weight || !state_out || !y)
+    return set_error(MOTIF_ERR_INVALID, "gdn_prefill: NULL pointer");
+  if ((tail_q_out || tail_k_out || tail_v_out) && !(tail_q_out && tail_k_out && tail_v_out))
+    return set_error(MOTIF_ERR_INVALID, "gdn_prefill: give all three outgoing tails or none");
+  if ((tail_q || tail_k || tail_v) && !(tail_q && tail_k && tail_v))
+    return set_error(MOTIF_ERR_INVALID, "gdn_prefill: give all three incoming tails or none");
+  const uintptr_t al16 = reinterpret_cast<uintptr_t>(proj) | reinterpret_cast<uintptr_t>(wq) |
+                         reinterpret_cast<uintptr_t>(wk) | reinterpret_cast<uintptr_t>(wv);
+  const uintptr_t al8 = reinterpret_cast<uintptr_t>(norm_weight) | reinterpret_cast<uintptr_t>(y);
+  if ((al16 & 15) || (al8 & 7) || ((p_sb | p_st | q_off | k_off | v_off) & 7) || ((g_off | y_sb | y_st) & 3))
+    return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_prefill: misaligned rows");
+  // sequence-relative byte offsets of the range-checked projection loads stay below 2^32
+  if ((static_cast<int64_t>(L) + kConvK) * p_st * 2 >= (int64_t(1) << 32))
+    return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_prefill: projection rows too long for the range-checked loads");
+  if (nseq == 0 || total_chunks == 0) {
+    if (total_chunks != 0 || L != 0) return set_error(MOTIF_ERR_INVALID, "gdn_prefill: inconsistent sizes");
+    return MOTIF_OK;
+  }
+  const size_t need = motif_gdn_chunk_workspace_bytes(H, dk, dv, kC, total_chunks);
+  if (!workspace || workspace_bytes < need)
+    return set_error(MOTIF_ERR_INVALID, "gdn_prefill: workspace too small (need " + std::to_string(need) + " bytes)");
+
+  GdnArgs a{};
+  a.q = a.k = a.v = a.beta = a.g = proj;  // the prep reads the projections through FrontArgs
+  a.s_in = state_in; a.s_out = state_out;
+  a.o = nullptr;
+  a.B = B; a.H = H; a.L = L; a.dk = dk; a.dv = dv;
+  a.gate = static_cast<const bf16_t *>(proj) + g_off; a.gt_sb = p_sb; a.gt_st = p_st;
+  a.nw = norm_weight; a.neps = norm_eps;
+  a.y = y; a.y_sb = y_sb; a.y_st = y_st;
+  ChunkArgs ca{};
+  ca.cu = cu_seqlens; ca.coff = chunk_offsets; ca.nseq = nseq; ca.nper = nper; ca.total_chunks = total_chunks;
+  FrontArgs fa{};
+  fa.x = static_cast<const bf16_t *>(proj); fa.x_sb = p_sb; fa.x_st = p_st;
+  fa.q_off = q_off; fa.k_off = k_off; fa.v_off = v_off; fa.a_off = a_off; fa.b_off = b_off;
+  fa.wq = static_cast<const bf16_t *>(wq); fa.wk = static_cast<const bf16_t *>(wk); fa.wv = static_cast<const bf16_t *>(wv);
+  fa.tq = static_cast<const bf16_t *>(tail_q); fa.tk = static_cast<const bf16_t *>(tail_k);
+  fa.tv = static_cast<const bf16_t *>(tail_v);
+  fa.oq = static_cast<bf16_t *>(tail_q_out); fa.ok = static_cast<bf16_t *>(tail_k_out);
+  fa.ov = static_cast<bf16_t *>(tail_v_out);
+  fa.a_log = static_cast<const bf16_t *>(a_log); fa.dt_bias = static_cast<const bf16_t *>(dt_bias);
+  fa.q_scale = q_scale;
+  char *ws = static_cast<char *>(workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dk == 64) return dv == 128 ? launch_fused<64, 128>(a, ca, fa, ws, s) : launch_fused<64, 64>(a, ca, fa, ws, s);
+  return dv == 128 ? launch_fused<32, 128>(a, ca, fa, ws, s) : launch_fused<32, 64>(a, ca, fa, ws, s);
+}
+
+namespace motif {
+
 
 }  // namespace motif

@@ -4,8 +4,11 @@ Same constructor arguments, parameter names / shapes / initialisation, cache
 type and forward contract.  The six input projections (q, k, v, gate, a, b) run
 as one GEMM against their concatenated weights.  The sequence mixing runs on the
 HIP kernels:
-  * prefill (L > 1): short conv + SiLU with the q / k L2 norm fused in
-    (motif_short_conv_silu_l2norm), then the chunked delta rule (motif_gdn_chunk_fwd);
+  * prefill (L > 1): one call from the projections to the o_proj input
+    (motif_gdn_prefill_fused: the chunk-preparation kernel computes the conv + SiLU,
+    the q / k L2 norm and the gates itself; the output pass applies the GatedRMSNorm);
+    shapes it does not serve run conv (motif_short_conv_silu_multi), gates and the
+    chunked rule (motif_gdn_chunk_fwd_gated) as separate kernels;
   * decode (L == 1 with a cache): one fused kernel from the projections to the
     GatedRMSNorm output (motif_gdn_decode_fused).  It writes the new recurrent
     state and conv tails to fresh tensors that replace the cache's (the reference's
@@ -42,6 +45,7 @@ from motif.ops import (
     short_conv_silu_varlen,
     chunk_gated_delta_rule_varlen,
     chunk_gated_delta_rule_gated_norm,
+    gdn_prefill_fused,
     short_conv_silu_multi,
 )
 
@@ -167,6 +171,16 @@ class GatedDeltaAttention(BasicAttention):
         o = self.o_norm(torch.cat([o, gate], dim=-1)).reshape(B, L, -1)
         return project(o, self.o_proj.weight, self.o_proj.bias)
 
+    def _prefill_fused(self, proj, tails, S0, cu_seqlens=None):
+        '''The whole prefill after the projections in three kernels, or None when the
+        fused kernels do not serve this layer / these inputs.'''
+        if self.o_norm.weight is None or self.conv_size != 4 or wants_grad(proj, self):
+            return None
+        return gdn_prefill_fused(proj, self._proj_offsets(), (self.q_conv.weight, self.k_conv.weight,
+                                                             self.v_conv.weight), tails, self.A_log, self.dt_bias,
+                                 self.dk ** -0.5, self.o_norm.weight, self.o_norm.eps, S0, self.num_heads, self.dk,
+                                 self.dv, cu_seqlens)
+
     def _decode_fusable(self, hidden_states, cache):
         '''True when one decode step can run as the fused kernel: one token, a cache whose
         state / tails (if present) are in the kernel's layout, inference only.'''
@@ -232,7 +246,15 @@ class GatedDeltaAttention(BasicAttention):
             output = self._decode_step(hidden_states, past_key_value)
             return AttentionOutput(output=output, past_key_value=past_key_value)
 
-        _, (xq, xk, xv, gate, xa, xb) = self._project(hidden_states)
+        proj, (xq, xk, xv, gate, xa, xb) = self._project(hidden_states)
+        whole = self._prefill_fused(proj, tails, S0) if L > 1 else None
+        if whole is not None:
+            y, S, conv_tails = whole
+            output = project(y, self.o_proj.weight, self.o_proj.bias)
+            if use_cache:
+                past_key_value.update(S, conv_tails, steps=L)
+                return AttentionOutput(output=output, past_key_value=past_key_value)
+            return AttentionOutput(output=output, payload={'state': S.detach(), 'conv_state': conv_tails})
         q, k, v, (cq, ck, cv) = self._qkv((xq, xk, xv), tails, B, L)
         beta, g = self._gates(xa, xb)
 
@@ -265,7 +287,12 @@ class GatedDeltaAttention(BasicAttention):
             raise ValueError('forward_varlen expects packed sequences with B == 1')
         lens = cu_seqlens.detach().cpu()
         max_len = int((lens[1:] - lens[:-1]).max()) if lens.numel() > 1 else 0
-        _, (xq, xk, xv, gate, xa, xb) = self._project(hidden_states)
+        proj, (xq, xk, xv, gate, xa, xb) = self._project(hidden_states)
+        whole = self._prefill_fused(proj, (None, None, None), None, cu_seqlens)
+        if whole is not None:
+            y, S, conv_tails = whole
+            return AttentionOutput(output=project(y, self.o_proj.weight, self.o_proj.bias),
+                                   payload={'state': S, 'conv_state': conv_tails})
         q, k, v, (cq, ck, cv) = self._qkv((xq, xk, xv), (None, None, None), B, L, cu_seqlens, max_len)
         beta, g = self._gates(xa, xb)
         fused = None

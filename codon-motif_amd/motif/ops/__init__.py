@@ -14,6 +14,7 @@ from .gated_deltanet import (
     chunk_gated_delta_rule_triton,
     chunk_gated_delta_rule_varlen,
     chunk_gated_delta_rule_gated_norm,
+    gdn_prefill_fused,
 )
 from .short_conv import short_conv_silu, short_conv_silu_multi, short_conv_silu_varlen
 from .attn_res import apply_block_attn_res, attn_res_read, attn_res_read_norms
@@ -28,6 +29,7 @@ __all__ = [
     'apply_chord_attention', 'apply_chord_attention_varlen',
     'recurrent_gated_delta_rule', 'chunk_gated_delta_rule',
     'chunk_gated_delta_rule_triton', 'chunk_gated_delta_rule_varlen', 'chunk_gated_delta_rule_gated_norm',
+    'gdn_prefill_fused',
     'short_conv_silu', 'short_conv_silu_multi', 'short_conv_silu_varlen',
     'apply_block_attn_res', 'attn_res_read', 'attn_res_read_norms', 'gdn_decode_fused',
     'cat_weights', 'linear_rows', 'project', 'rows_eligible',

@@ -33,6 +33,9 @@ _SIGNATURES = {
     'motif_gdn_chunk_fwd_gated': (
         _T4 * 5 + [_P, _P] + _T4 + [_I32] * 6 + [_P, _P, _I32, _I32, _P, _SZ]
         + [_P, _I64, _I64, _P, _F32, _P, _I64, _I64, _I32, _P], _I32),
+    'motif_gdn_prefill_fused': (
+        [_P, _I64, _I64] + [_I32] * 6 + [_P] * 3 + [_I32] + [_P] * 6 + [_P, _P, _F32, _P, _F32]
+        + [_P, _P, _P, _I64, _I64] + [_I32] * 5 + [_P, _P, _I32, _I32, _P, _SZ, _P], _I32),
     'motif_short_conv_silu': (
         [_P, _I64, _I64, _P, _P, _P, _P, _I64, _I64] + [_I32] * 4 + [_P, _I32, _I32, _I32, _P], _I32),
     'motif_short_conv_silu_multi': (

@@ -21,6 +21,7 @@ from . import _lib
 from .autograd_path import gdn_chunk_torch, wants_grad as _needs_grad
 
 __all__ = [
+    'gdn_prefill_fused',
     'recurrent_gated_delta_rule',
     'chunk_gated_delta_rule',
     'chunk_gated_delta_rule_triton',
@@ -280,3 +281,70 @@ def chunk_gated_delta_rule_varlen(q, k, v, beta, g, cu_seqlens, S=None, chunk_si
         S_in = S.to(device=qc.device, dtype=torch.float32).contiguous()
     o, S_out = _chunk_call(qc, kc, vc, bc, gc, S_in, _kernel_chunk(int(chunk_size)), cu_seqlens, nseq)
     return o.to(q.dtype), S_out
+
+
+def gdn_prefill_fused(proj, offsets, conv_weights, tails, a_log, dt_bias, q_scale, norm_weight, norm_eps, S=None,
+                      heads=None, dk=None, dv=None, cu_seqlens=None):
+    '''A GatedDeltaAttention prefill from its input projections to the o_proj input, in
+    three kernels (no reference counterpart as one call; replaces
+    motif/block/attention/gdn_attn.py:183-209: the q / k / v short conv + SiLU, the q / k
+    L2 norm, the gates, the chunked delta rule and the GatedRMSNorm).
+
+    proj [B, L, ncols] bf16 with columns (q, k, v, gate, a, b) at `offsets`;
+    conv_weights (wq, wk, wv) nn.Conv1d weights [C, 1, 4]; tails (tq, tk, tv) incoming
+    conv tails [B, C, 3] or Nones; S [B, H, dk, dv] fp32 or None; cu_seqlens (B == 1)
+    for packed sequences (zero tails and states).  Returns (y [B, L, H*dv],
+    S_out [B|nseq, H, dk, dv], (tq, tk, tv) outgoing tails), or None when the fused
+    kernels do not serve these inputs (the caller then runs the separate steps).
+    '''
+    if proj.dtype != torch.bfloat16 or not proj.is_cuda or proj.dim() != 3 or _needs_grad(
+            proj, a_log, dt_bias, norm_weight, S, *conv_weights, *[t for t in tails if t is not None]):
+        return None
+    if conv_weights[0].shape[-1] != 4 or proj.stride(-1) != 1:
+        return None
+    B, L, _ = proj.shape
+    H = heads
+    dev = proj.device
+    C = (H * dk, H * dk, H * dv)
+    ws_ = [w.detach().reshape(c, 4).to(torch.bfloat16).contiguous() for w, c in zip(conv_weights, C)]
+    tin = [None if t is None else t.detach().to(torch.bfloat16).contiguous() for t in tails]
+    if any(t is not None for t in tin) and (cu_seqlens is not None or not all(t is not None for t in tin)):
+        return None
+    if cu_seqlens is None:
+        nseq, total, cu_dev, coff_dev = B, B * ((L + 63) // 64), None, None
+        if S is not None and (S.shape != (B, H, dk, dv) or S.dtype != torch.float32 or not S.is_contiguous()):
+            return None
+    else:
+        if B != 1 or S is not None:
+            return None
+        cu_host = cu_seqlens.detach().to('cpu', torch.int64)
+        lens = cu_host[1:] - cu_host[:-1]
+        if (lens < 0).any() or int(cu_host[0]) != 0 or int(cu_host[-1]) != L:
+            raise ValueError('cu_seqlens must start at 0, be non-decreasing and end at L')
+        nseq = int(lens.numel())
+        coff = torch.zeros(nseq + 1, dtype=torch.int32)
+        coff[1:] = torch.cumsum((lens + 63) // 64, 0).to(torch.int32)
+        total = int(coff[-1])
+        cu_dev, coff_dev = cu_host.to(device=dev, dtype=torch.int32), coff.to(dev)
+    if L == 0 or nseq == 0:
+        return None
+    y = torch.empty(B, L, H * dv, dtype=torch.bfloat16, device=dev)
+    S_out = torch.empty(nseq, H, dk, dv, dtype=torch.float32, device=dev)
+    tout = [torch.empty(nseq, c, 3, dtype=torch.bfloat16, device=dev) for c in C]
+    nbytes = _lib.lib().motif_gdn_chunk_workspace_bytes(H, dk, dv, 64, max(total, 1))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    al = a_log.detach().to(torch.bfloat16).contiguous()
+    db = dt_bias.detach().to(torch.bfloat16).contiguous()
+    nw = norm_weight.detach().to(torch.bfloat16).contiguous()
+    rc = _lib.lib().motif_gdn_prefill_fused(
+        proj.data_ptr(), proj.stride(0), proj.stride(1), *[int(o) for o in offsets],
+        ws_[0].data_ptr(), ws_[1].data_ptr(), ws_[2].data_ptr(), 4,
+        *[_lib.ptr(t) for t in tin], *[t.data_ptr() for t in tout],
+        al.data_ptr(), db.data_ptr(), float(q_scale), nw.data_ptr(), float(norm_eps),
+        _lib.ptr(S), S_out.data_ptr(), y.data_ptr(), y.stride(0), y.stride(1),
+        B, H, L, dk, dv, _lib.ptr(cu_dev), _lib.ptr(coff_dev), nseq, total,
+        ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev))
+    if rc == _lib.ERR_UNSUPPORTED:
+        return None
+    _lib.check(rc, 'motif_gdn_prefill_fused')
+    return y, S_out, tuple(tout)

@@ -120,6 +120,35 @@ int motif_gdn_chunk_fwd_gated(
     int dtype, void *stream);
 
 /*
+ * A GatedDeltaAttention prefill from its input projections to the o_proj input, fused
+ * into three kernels: the chunk-preparation kernel reads the raw projection rows and
+ * computes the q / k / v short causal conv + SiLU (q, k L2-normalised per head, q scaled
+ * by q_scale), the gates beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias) and
+ * the outgoing conv tails itself; the state scan and the output pass (with the
+ * GatedRMSNorm by the gate columns) follow as in motif_gdn_chunk_fwd_gated.  Replaces
+ * motif/block/attention/gdn_attn.py:183-209 (conv :116-136, gates :193-195, chunk rule
+ * motif/ops/gated_deltanet.py:796-834, GatedRMSNorm motif/ops/rms_norm.py:530-553).
+ *   proj [B, L, ncols] bf16 (strides p_sb, p_st) with the columns of q (H*dk), k (H*dk),
+ *   v (H*dv), the norm gate (H*dv), a (H), b (H) at q_off .. b_off; wq, wk [H*dk, 4],
+ *   wv [H*dv, 4]; tail_q/k/v [B, C, 3] incoming tails or NULL (zeros); tail_*_out
+ *   [nseq, C, 3] or NULL; a_log, dt_bias [H]; norm_weight [dv]; state_in [nseq, H, dk, dv]
+ *   fp32 or NULL, state_out the final states; y [B, L, H*dv].  Packed sequences as
+ *   motif_gdn_chunk_fwd (B == 1, zero tails and states).  Workspace:
+ *   motif_gdn_chunk_workspace_bytes(H, dk, dv, 64, total_chunks).
+ *   dk in {32, 64}, dv in {64, 128}, conv_k == 4, bf16; other shapes return
+ *   MOTIF_ERR_UNSUPPORTED and the caller runs the separate calls.
+ */
+int motif_gdn_prefill_fused(
+    const void *proj, int64_t p_sb, int64_t p_st, int q_off, int k_off, int v_off, int g_off, int a_off, int b_off,
+    const void *wq, const void *wk, const void *wv, int conv_k,
+    const void *tail_q, const void *tail_k, const void *tail_v, void *tail_q_out, void *tail_k_out, void *tail_v_out,
+    const void *a_log, const void *dt_bias, float q_scale, const void *norm_weight, float norm_eps,
+    const float *state_in, float *state_out, void *y, int64_t y_sb, int64_t y_st,
+    int B, int H, int L, int dk, int dv,
+    const int32_t *cu_seqlens, const int32_t *chunk_offsets, int nseq, int total_chunks,
+    void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * Short causal depthwise conv (kernel K) followed by SiLU.
  * Replaces motif/block/attention/gdn_attn.py:116-136 `GatedDeltaAttention._conv`.
  *   x [B,L,D] (strides x_sb, x_st; channel stride 1), weight [D,K] contiguous,

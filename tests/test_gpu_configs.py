@@ -21,13 +21,17 @@ implementations drift apart over 16 layers.
   the fixed-capacity caches match the growing-cache path within the bf16 bar; two
   batch rows of every layer of the decode step pass the layer check above on the
   cache contents the GPU held before the step.
-- Config 5 (16 sequences, lengths uniform in [512, 8192], seed 0, packed): every
-  layer of the packed forward equals the same layer run on each sequence alone from
-  the same input (max-abs 2e-2, mean-rel 1e-4: the library GEMM rounds some rows of
-  a large-M call differently from the same rows alone, measured 2e-6 of the
-  elements); the packed model's final states equal the separate runs' for the
-  sequences the packed GEMMs compute identically (measured: the first 7); every
-  layer of the two shortest sequences passes the oracle layer check.
+- Config 5 (16 sequences, lengths uniform in [512, 8192], seed 0, packed): for every
+  layer, the packed sequence-mixing op (fused GatedDelta prefill, packed Chord
+  attention) on the packed projections equals the op run on each sequence's slice of
+  the same projections, bit for bit (outputs, final states, conv tails); each whole
+  layer on the packed input matches the layer run on each sequence alone within
+  mean-rel 5e-3 (the library GEMM rounds some rows of a large-M call differently from
+  the same rows alone, measured 2e-6 of the elements, and a sharp softmax at long
+  positions can turn one such flip into a visible change of a few outputs); the
+  packed model's final states equal the separate runs' for the sequences the packed
+  GEMMs compute identically (measured: the first 7); every layer of the two shortest
+  sequences passes the oracle layer check.
 '''
 import dataclasses
 import sys
@@ -245,7 +249,39 @@ def test_config5_packed_prefill():
         packed = model(ids, cu_seqlens=cu.to(DEV), logits=False).hidden_states
     assert len(tap.records) == 16
     bounds = list(zip(cu[:-1].tolist(), cu[1:].tolist()))
-    # every layer: packed output == the same layer on each sequence alone, same input
+    # every layer's sequence mixing on the projections of the packed input: the packed op
+    # equals the op run on each sequence's slice of the same projections, bit for bit
+    from motif.block.attention.chord_attn import LogPositions
+    from motif.ops import apply_chord_attention, apply_chord_attention_varlen, gdn_prefill_fused
+    cu_dev = cu.to(DEV)
+    for rec in tap.records:
+        attn = model.blocks[rec['block']].features[rec['layer']].attn
+        x = rec['x'].to(DEV)
+        if rec['kind'] == 'chord':
+            q, k, v, _ = attn._inputs(x, None, None, True)
+            alpha, beta, mu, ssmax = attn.ggd_params()
+            pos = torch.cat([torch.arange(b - a) for a, b in bounds]).to(DEV)
+            log_n = LogPositions.get(max(lens), DEV)[pos][None]
+            packed_o = apply_chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, log_n, cu_dev,
+                                                    softmax_scale=attn.head_dim ** -0.5)
+            for i, (a, b) in enumerate(bounds):
+                alone = apply_chord_attention(q[:, :, a:b], k[:, :, a:b], v[:, :, a:b], alpha, beta, mu, ssmax,
+                                              log_n[:, a:b].contiguous(), q_start=0,
+                                              softmax_scale=attn.head_dim ** -0.5)
+                assert torch.equal(packed_o[:, :, a:b], alone), f'chord op, sequence {i}'
+        else:
+            proj, _ = attn._project(x)
+            args = (attn._proj_offsets(), (attn.q_conv.weight, attn.k_conv.weight, attn.v_conv.weight),
+                    (None, None, None), attn.A_log, attn.dt_bias, attn.dk ** -0.5, attn.o_norm.weight,
+                    attn.o_norm.eps, None, attn.num_heads, attn.dk, attn.dv)
+            y, S, tails = gdn_prefill_fused(proj, *args, cu_seqlens=cu_dev)
+            for i, (a, b) in enumerate(bounds):
+                ya, Sa, ta = gdn_prefill_fused(proj[:, a:b], *args)
+                assert torch.equal(y[:, a:b], ya) and torch.equal(S[i:i + 1], Sa), f'gdn op, sequence {i}'
+                assert all(torch.equal(t[i:i + 1], u) for t, u in zip(tails, ta)), f'gdn tails, sequence {i}'
+        _say(f'config 5 block {rec["block"]} layer {rec["layer"]}: packed op == per-sequence op for all 16')
+    # every layer as a whole (projection GEMMs included) on the packed input vs each
+    # sequence alone: the bf16 bar (the GEMMs round some rows of a large-M call differently)
     for rec in tap.records:
         attn = model.blocks[rec['block']].features[rec['layer']].attn
         x, out = rec['x'].to(DEV), rec['out'].to(DEV)
@@ -254,9 +290,9 @@ def test_config5_packed_prefill():
             alone = attn(hidden_states=x[:, a:b]).output
             d = (out[:, a:b].double() - alone.double()).abs()
             gap = (d.max().item(), (d.sum() / alone.double().abs().sum()).item())
-            assert gap[0] <= 2e-2 and gap[1] <= 1e-4, f'block {rec["block"]} layer {rec["layer"]} sequence {i}: {gap}'
+            assert gap[1] <= 5e-3, f'block {rec["block"]} layer {rec["layer"]} sequence {i}: {gap}'
             worst = max(worst, gap)
-        _say(f'config 5 block {rec["block"]} layer {rec["layer"]}: packed vs separate, worst {worst}')
+        _say(f'config 5 block {rec["block"]} layer {rec["layer"]}: packed layer vs separate, worst {worst}')
     # whole model: sequences whose rows the packed GEMMs round like the separate runs
     for i, (a, b) in enumerate(bounds):
         alone = model(ids[:, a:b], logits=False).hidden_states

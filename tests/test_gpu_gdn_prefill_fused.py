@@ -1,0 +1,80 @@
+'''The fused GatedDelta prefill (motif_gdn_prefill_fused: conv + SiLU, q / k L2 norm and
+gates computed inside the chunk-preparation kernel) against the same layer run as
+separate kernels (conv kernel, gates kernel, chunk kernels): the fused front end
+repeats the separate kernels' arithmetic, so the layer output, the final state and the
+outgoing conv tails are compared bit for bit.  Padded batches with and without a cache
+to continue from, packed sequences of lengths 1..130 (tails of sequences shorter than
+the conv window), every supported head shape.  The separate path itself is pinned to
+the oracle by the layer and op tests.'''
+import pytest
+import torch
+
+from golden.weights import fill_params
+from support import gen
+
+pytestmark = pytest.mark.gpu
+
+DEV = 'cuda'
+
+
+def _layer(hidden, H, dk, dv, seed):
+    from motif.block.attention.gdn_attn import GatedDeltaAttention
+    layer = GatedDeltaAttention(hidden_size=hidden, num_heads=H, head_k_dim=dk, expand_v=dv / dk)
+    fill_params(layer, seed)
+    return layer.to(DEV, torch.bfloat16).eval()
+
+
+def _separate(monkeypatch):
+    import motif.block.attention.gdn_attn as ga
+    monkeypatch.setattr(ga, 'gdn_prefill_fused', lambda *a, **k: None)
+
+
+def _run(layer, x, first=None):
+    from motif.model.cache import GatedDeltaAttentionLayerCache
+    cache = GatedDeltaAttentionLayerCache()
+    if first is not None:
+        layer(first, past_key_value=cache)
+    out = layer(x, past_key_value=cache).output
+    return out, cache.state, cache.conv_state
+
+
+@pytest.mark.parametrize('hidden,H,dk,dv', [(768, 12, 64, 128), (256, 4, 32, 64), (256, 2, 64, 64), (128, 2, 32, 128)])
+@pytest.mark.parametrize('cont', [False, True])
+@torch.no_grad()
+def test_fused_prefill_equals_separate_kernels(monkeypatch, hidden, H, dk, dv, cont):
+    layer = _layer(hidden, H, dk, dv, seed=dk + dv)
+    g = gen(7)
+    x = (torch.randn(2, 150, hidden, generator=g) * 0.5).to(DEV, torch.bfloat16)
+    first = (torch.randn(2, 37, hidden, generator=g) * 0.5).to(DEV, torch.bfloat16) if cont else None
+    fused = _run(layer, x, first)
+    _separate(monkeypatch)
+    sep = _run(layer, x, first)
+    assert torch.equal(fused[0], sep[0]), (fused[0].float() - sep[0].float()).abs().max().item()
+    assert torch.equal(fused[1], sep[1]), (fused[1] - sep[1]).abs().max().item()
+    for a, b in zip(fused[2], sep[2]):
+        assert torch.equal(a, b)
+
+
+@torch.no_grad()
+def test_fused_prefill_model_shape_t4096(monkeypatch):
+    layer = _layer(768, 12, 64, 128, seed=3)
+    x = (torch.randn(1, 4096, 768, generator=gen(8)) * 0.5).to(DEV, torch.bfloat16)
+    fused = _run(layer, x)
+    _separate(monkeypatch)
+    sep = _run(layer, x)
+    assert torch.equal(fused[0], sep[0]) and torch.equal(fused[1], sep[1])
+
+
+@torch.no_grad()
+def test_fused_prefill_packed_sequences(monkeypatch):
+    layer = _layer(256, 4, 64, 128, seed=5)
+    lens = [1, 2, 3, 64, 65, 130, 5]
+    cu = torch.tensor([0] + list(torch.cumsum(torch.tensor(lens), 0)), dtype=torch.int32, device=DEV)
+    x = (torch.randn(1, sum(lens), 256, generator=gen(9)) * 0.5).to(DEV, torch.bfloat16)
+    fused = layer.forward_varlen(x, cu)
+    _separate(monkeypatch)
+    sep = layer.forward_varlen(x, cu)
+    assert torch.equal(fused.output, sep.output), (fused.output.float() - sep.output.float()).abs().max().item()
+    assert torch.equal(fused.payload['state'], sep.payload['state'])
+    for a, b in zip(fused.payload['conv_state'], sep.payload['conv_state']):
+        assert torch.equal(a, b)
