@@ -18,7 +18,8 @@
 // of 32) at once, so a launch costs one memory round trip rather than one per k-step.
 // The v_mfma_f32_16x16x32_bf16 partial sums meet in LDS for the epilogue.  What bounds
 // a workgroup is the bytes through its CU, (16 MT + 16 NT) * K * 2, so the host picks
-// the largest tile that still gives about 256 workgroups; the workgroups that share a
+// the largest tile whose grid still has 100 workgroups or more (200 for SWIGLU, below);
+// the workgroups that share a
 // weight tile are placed on one XCD (workgroups go to XCDs round-robin), so the tile
 // comes from HBM once and from that XCD's L2 after.
 #include "capi_internal.h"
@@ -39,6 +40,7 @@ struct LinArgs {
   bf16_t *y2; int64_t y2_rs;         // RESID: y2 = aux2 + y (skipped when y2 is NULL)
   int M, N, K;                       // N = rows of W (SWIGLU: 2 * Nout)
   int mblocks, ntiles;               // output tiles along M and along the columns
+  int grid;                          // workgroups of this problem
 };
 
 constexpr int kWaves = 8;
@@ -70,8 +72,14 @@ __device__ __forceinline__ int w_row(int n0, int t, int c, int nout) {
 // L1 asks L2 for full lines -- half the requests of P = 1 (16 rows x 64 bytes per
 // instruction).  MFMA j of the step sums k = 16 kq + 8 j .. +7 over the lane groups
 // kq, the same set in A and B, so the products are unchanged.
+// LDS of the cross-wave sum: [kWaves][tiles][64] f32x4.
+template <int MT, int NT>
+constexpr int red_bytes() { return kWaves * MT * NT * 64 * 16; }
+
+// One workgroup's output tile; `id` is its index among the launch's workgroups for this
+// problem, `red` the LDS for the cross-wave sum.
 template <int MT, int NT, int KS, int EPI, int P>
-__global__ void __launch_bounds__(512) linear_rows_kernel(LinArgs a) {
+__device__ __forceinline__ void rows_tile(const LinArgs &a, const int id, f32x4 *red_lds) {
   // The wave index in an SGPR: the k-range below is then wave-uniform to the compiler
   // (scalar branches, step offsets in the loads' scalar offset operand).
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -80,7 +88,6 @@ __global__ void __launch_bounds__(512) linear_rows_kernel(LinArgs a) {
   const int nout = EPI == EPI_SWIGLU ? a.N / 2 : a.N;
 
   // XCD-aware tile order: the mblocks workgroups of one column tile sit kXcds ids apart.
-  const int id = blockIdx.x;
   const int group = id / (kXcds * a.mblocks), r = id % (kXcds * a.mblocks);
   const int nt = group * kXcds + r % kXcds, mb = r / kXcds;
   if (nt >= a.ntiles) return;
@@ -141,7 +148,7 @@ __global__ void __launch_bounds__(512) linear_rows_kernel(LinArgs a) {
   }
 
   // Cross-wave sum in LDS: red[wave][tile][lane] (16 bytes per lane).
-  __shared__ f32x4 red[kWaves][MT * NT][64];
+  auto red = reinterpret_cast<f32x4 (*)[MT * NT][64]>(red_lds);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -179,6 +186,159 @@ __global__ void __launch_bounds__(512) linear_rows_kernel(LinArgs a) {
       if (a.y2) a.y2[m * a.y2_rs + col] = f32_to_bf16(bf16_to_f32(a.aux2[m * a.aux2_rs + col]) + val);
     }
     a.y[m * a.y_rs + col] = f32_to_bf16(val);
+  }
+}
+
+template <int MT, int NT, int KS, int EPI, int P>
+__global__ void __launch_bounds__(512) linear_rows_kernel(LinArgs a) {
+  __shared__ f32x4 red[red_bytes<MT, NT>() / 16];
+  rows_tile<MT, NT, KS, EPI, P>(a, blockIdx.x, red);
+}
+
+// Two independent projections in one launch (the decoder's attention input projection
+// and its MLP gate/up projection, whose inputs are ready together): workgroups
+// [0, a1.grid) take problem 1, the rest problem 2.  Each keeps its own tile shape.
+template <int MT1, int NT1, int KS1, int EPI1, int MT2, int NT2, int KS2, int EPI2, int P>
+__global__ void __launch_bounds__(512) linear_rows_pair_kernel(LinArgs a1, LinArgs a2) {
+  constexpr int b1 = red_bytes<MT1, NT1>(), b2 = red_bytes<MT2, NT2>();
+  __shared__ f32x4 red[(b1 > b2 ? b1 : b2) / 16];
+  const int id = blockIdx.x;
+  if (id < a1.grid) rows_tile<MT1, NT1, KS1, EPI1, P>(a1, id, red);
+  else rows_tile<MT2, NT2, KS2, EPI2, P>(a2, id - a1.grid, red);
+}
+
+// The decoder's two output projections into one output tile (no reference
+// counterpart as one op; motif/block/decoder.py:205-213 with the o_proj of the attention
+// layer and the MLP's down projection):
+//   u = T(x1 W1^T)            the attention output (o_proj), GATE: u = T(u * T(sigmoid(gate)))
+//   m = T(x2 W2^T)            the MLP output (down_proj)
+//   y = T(u + m)              f_h;   y2 = T(aux2 + y) when y2 != NULL (the block's running sum)
+// Rounded where the reference's separate ops round.  Each wave runs its share of both
+// products' k-steps back to back; each product keeps its own accumulator.
+struct DualArgs {
+  const bf16_t *x1; int64_t x1_rs; const bf16_t *w1; int64_t w1_rs; int K1;
+  const bf16_t *x2; int64_t x2_rs; const bf16_t *w2; int64_t w2_rs; int K2;
+  const bf16_t *gate; int64_t gate_rs;
+  const bf16_t *aux2; int64_t aux2_rs;
+  bf16_t *y; int64_t y_rs; bf16_t *y2; int64_t y2_rs;
+  int M, N;
+  int mblocks, ntiles;
+};
+
+template <int MT, int NT, int KS, bool GATE, int P>
+__global__ void __launch_bounds__(512) linear_rows_dual_kernel(DualArgs a) {
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, kq = lane >> 4;
+  constexpr int kCols = 16 * NT;
+  const int id = blockIdx.x;
+  const int group = id / (kXcds * a.mblocks), r = id % (kXcds * a.mblocks);
+  const int nt = group * kXcds + r % kXcds, mb = r / kXcds;
+  if (nt >= a.ntiles) return;
+  const int n0 = nt * kCols, m0 = mb * 16 * MT;
+  const int rows = min(a.M - m0, 16 * MT);
+
+  const buf_t xb1 = make_buf(a.x1 + static_cast<int64_t>(m0) * a.x1_rs,
+                             static_cast<uint32_t>(((rows - 1) * a.x1_rs + a.K1) * 2));
+  const buf_t xb2 = make_buf(a.x2 + static_cast<int64_t>(m0) * a.x2_rs,
+                             static_cast<uint32_t>(((rows - 1) * a.x2_rs + a.K2) * 2));
+  const buf_t wb1 = make_buf(a.w1, static_cast<uint32_t>(((a.N - 1) * a.w1_rs + a.K1) * 2));
+  const buf_t wb2 = make_buf(a.w2, static_cast<uint32_t>(((a.N - 1) * a.w2_rs + a.K2) * 2));
+  uint32_t xo1[MT], xo2[MT], wo1[NT], wo2[NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int row = min(mt * 16 + r16, rows - 1);
+    xo1[mt] = static_cast<uint32_t>((row * a.x1_rs + kq * 8 * P) * 2);
+    xo2[mt] = static_cast<uint32_t>((row * a.x2_rs + kq * 8 * P) * 2);
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int n = min(n0 + 16 * t + r16, a.N - 1);
+    wo1[t] = static_cast<uint32_t>((n * a.w1_rs + kq * 8 * P) * 2);
+    wo2[t] = static_cast<uint32_t>((n * a.w2_rs + kq * 8 * P) * 2);
+  }
+  // Wave w takes the same k-steps of each product as the single-product kernel gives
+  // it (w n / kWaves .. (w + 1) n / kWaves), so both sums are formed in the same order
+  // as two separate launches would form them: the result is identical to them.
+  const int n1 = a.K1 / (32 * P), n2 = a.K2 / (32 * P);
+  const int a0 = wv * n1 / kWaves, c1 = (wv + 1) * n1 / kWaves - a0;
+  const int b0 = wv * n2 / kWaves, c2 = (wv + 1) * n2 / kWaves - b0;
+  const int nv = c1 + c2;  // the wave's steps: c1 of product 1, then c2 of product 2
+
+  f32x4 acc[2][MT][NT];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[u][mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int s = 0; s < nv; s += KS) {
+    bf16x8 A[KS][P][MT], B[KS][P][NT];
+#pragma unroll
+    for (int c = 0; c < KS; ++c) {
+      const int v = s + c;
+      const bool first = v < c1;  // wave-uniform
+      // steps past the wave's range read zeros (offset >= 2^31 fails the range check)
+      const uint32_t soff = v < nv ? static_cast<uint32_t>(first ? a0 + v : b0 + v - c1) * (64u * P) : 0x80000000u;
+      // pick the operand, then load once (a select between two loads would issue both)
+      const buf_t xb = first ? xb1 : xb2, wb = first ? wb1 : wb2;
+#pragma unroll
+      for (int j = 0; j < P; ++j) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) A[c][j][mt] = ld8(xb, (first ? xo1[mt] : xo2[mt]) + 16 * j, soff);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) B[c][j][t] = ld8(wb, (first ? wo1[t] : wo2[t]) + 16 * j, soff);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < KS; ++c) {
+      // steps past the range add zeros to product 2, which changes nothing
+      const int u = __builtin_amdgcn_readfirstlane(s + c < c1 ? 0 : 1);
+#pragma unroll
+      for (int j = 0; j < P; ++j)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            if (u == 0) acc[0][mt][t] = mma(A[c][j][mt], B[c][j][t], acc[0][mt][t]);
+            else acc[1][mt][t] = mma(A[c][j][mt], B[c][j][t], acc[1][mt][t]);
+          }
+    }
+  }
+
+  __shared__ f32x4 red[kWaves][2][MT * NT][64];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) red[wv][u][mt * NT + t][lane] = acc[u][mt][t];
+  __syncthreads();
+  const int p = threadIdx.x;
+  if (p >= MT * NT * 64) return;
+  const int l = p & 63, tv = (p >> 6) % NT, mt = (p >> 6) / NT;
+  f32x4 v1 = red[0][0][mt * NT + tv][l], v2 = red[0][1][mt * NT + tv][l];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) {
+    v1 += red[w][0][mt * NT + tv][l];
+    v2 += red[w][1][mt * NT + tv][l];
+  }
+  const int col = n0 + 16 * tv + (l & 15);
+  if (col >= a.N) return;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int rr = mt * 16 + 4 * (l >> 4) + j;
+    if (rr >= rows) continue;
+    const int64_t m = m0 + rr;
+    float u = rb(v1[j]);
+    if (GATE) {
+      const float gp = bf16_to_f32(a.gate[m * a.gate_rs + col]);
+      u = rb(u * rb(rcp_fast(1.f + __builtin_amdgcn_exp2f(-gp * kLog2e))));
+    }
+    const float f = rb(u + rb(v2[j]));
+    a.y[m * a.y_rs + col] = f32_to_bf16(f);
+    if (a.y2) a.y2[m * a.y2_rs + col] = f32_to_bf16(bf16_to_f32(a.aux2[m * a.aux2_rs + col]) + f);
   }
 }
 
@@ -232,6 +392,57 @@ int launch_epi(const LinArgs &a, hipStream_t s) {
   }
 }
 
+// Paired launch: problem 1 (none or SwiGLU epilogue) with tile (MT1, 2), problem 2 a
+// SwiGLU projection with tile (2, 2) -- the shapes of the decoder's input projections at
+// 64 rows; both with the same K.
+template <int MT1, int EPI1, int KS>
+int launch_pair_k(LinArgs a1, LinArgs a2, hipStream_t s) {
+  auto prep = [](LinArgs &a, int MT, int NT, int EPI) {
+    const int cols = EPI == EPI_SWIGLU ? 8 * NT : 16 * NT;
+    const int nout = EPI == EPI_SWIGLU ? a.N / 2 : a.N;
+    a.ntiles = (nout + cols - 1) / cols;
+    a.mblocks = (a.M + 16 * MT - 1) / (16 * MT);
+    a.grid = (a.ntiles + kXcds - 1) / kXcds * kXcds * a.mblocks;
+  };
+  prep(a1, MT1, 2, EPI1);
+  prep(a2, 2, 2, EPI_SWIGLU);
+  linear_rows_pair_kernel<MT1, 2, KS, EPI1, 2, 2, KS, EPI_SWIGLU, 2><<<dim3(a1.grid + a2.grid), dim3(64 * kWaves), 0, s>>>(a1, a2);
+  return check_launch("linear_rows_pair_kernel");
+}
+
+template <int MT1, int EPI1>
+int launch_pair(const LinArgs &a1, const LinArgs &a2, hipStream_t s) {
+  const int per_wave = (a1.K / 64 + kWaves - 1) / kWaves;
+  if (per_wave <= 1) return launch_pair_k<MT1, EPI1, 1>(a1, a2, s);
+  if (per_wave <= 2) return launch_pair_k<MT1, EPI1, 2>(a1, a2, s);
+  return launch_pair_k<MT1, EPI1, 4>(a1, a2, s);
+}
+
+template <bool GATE, int KS>
+int launch_dual_k(DualArgs a, hipStream_t s) {
+  a.ntiles = (a.N + 15) / 16;
+  a.mblocks = (a.M + 15) / 16;
+  const int grid = (a.ntiles + kXcds - 1) / kXcds * kXcds * a.mblocks;
+  linear_rows_dual_kernel<1, 1, KS, GATE, 2><<<dim3(grid), dim3(64 * kWaves), 0, s>>>(a);
+  return check_launch("linear_rows_dual_kernel");
+}
+
+template <bool GATE>
+int launch_dual(const DualArgs &a, hipStream_t s) {
+  const int per_wave = (a.K1 / 64 + kWaves - 1) / kWaves + (a.K2 / 64 + kWaves - 1) / kWaves;
+  if (per_wave <= 2) return launch_dual_k<GATE, 2>(a, s);
+  if (per_wave <= 4) return launch_dual_k<GATE, 4>(a, s);
+  return launch_dual_k<GATE, 8>(a, s);
+}
+
+bool rows_ok(const void *x, int64_t x_rs, const void *w, int64_t w_rs, int N, int K) {
+  if (!x || !w || N <= 0 || K <= 0 || K % 64) return false;
+  if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15) || (x_rs % 8) || (w_rs % 8)) return false;
+  if (x_rs < K || w_rs < K) return false;
+  return (static_cast<int64_t>(N - 1) * w_rs + K) * 2 < (int64_t(1) << 31) &&
+         (static_cast<int64_t>(63) * x_rs + K) * 2 < (int64_t(1) << 31);
+}
+
 }  // namespace
 
 }  // namespace motif
@@ -271,4 +482,51 @@ extern "C" int motif_linear_rows(const void *x, int64_t x_rs, const void *w, int
     case EPI_SWIGLU: return launch_epi<EPI_SWIGLU>(a, s);
     default: return launch_epi<EPI_NONE>(a, s);
   }
+}
+
+extern "C" int motif_linear_rows_pair(const void *x1, int64_t x1_rs, const void *w1, int64_t w1_rs, void *y1,
+                                      int64_t y1_rs, int N1, int K1, int epilogue1, const void *x2, int64_t x2_rs,
+                                      const void *w2, int64_t w2_rs, void *y2, int64_t y2_rs, int N2, int K2,
+                                      int M, void *stream) {
+  using namespace motif;
+  if (M < 0 || M > 64) return set_error(MOTIF_ERR_UNSUPPORTED, "linear_rows_pair: 1 .. 64 rows");
+  if (epilogue1 != EPI_NONE && epilogue1 != EPI_SWIGLU)
+    return set_error(MOTIF_ERR_UNSUPPORTED, "linear_rows_pair: problem 1 takes no epilogue or SwiGLU");
+  if (K1 != K2 || !rows_ok(x1, x1_rs, w1, w1_rs, N1, K1) || !rows_ok(x2, x2_rs, w2, w2_rs, N2, K2) || !y1 || !y2 ||
+      (N2 & 1) || (epilogue1 == EPI_SWIGLU && (N1 & 1)))
+    return set_error(MOTIF_ERR_UNSUPPORTED, "linear_rows_pair: unsupported shapes or alignment");
+  if (M == 0) return MOTIF_OK;
+  LinArgs a1{}, a2{};
+  a1.x = static_cast<const bf16_t *>(x1); a1.x_rs = x1_rs; a1.w = static_cast<const bf16_t *>(w1); a1.w_rs = w1_rs;
+  a1.y = static_cast<bf16_t *>(y1); a1.y_rs = y1_rs; a1.M = M; a1.N = N1; a1.K = K1;
+  a2.x = static_cast<const bf16_t *>(x2); a2.x_rs = x2_rs; a2.w = static_cast<const bf16_t *>(w2); a2.w_rs = w2_rs;
+  a2.y = static_cast<bf16_t *>(y2); a2.y_rs = y2_rs; a2.M = M; a2.N = N2; a2.K = K2;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // problem 1's tile as launch_epi would pick it: whole 64-row tiles when they still give ~100 workgroups
+  const int cols = epilogue1 == EPI_SWIGLU ? 16 : 32, nout = epilogue1 == EPI_SWIGLU ? N1 / 2 : N1;
+  const bool big = M > 32 && ((nout + cols - 1) / cols) >= 100;
+  if (epilogue1 == EPI_SWIGLU) return big ? launch_pair<4, EPI_SWIGLU>(a1, a2, s) : launch_pair<2, EPI_SWIGLU>(a1, a2, s);
+  return big ? launch_pair<4, EPI_NONE>(a1, a2, s) : launch_pair<2, EPI_NONE>(a1, a2, s);
+}
+
+extern "C" int motif_linear_rows_dual(const void *x1, int64_t x1_rs, const void *w1, int64_t w1_rs, int K1,
+                                      const void *x2, int64_t x2_rs, const void *w2, int64_t w2_rs, int K2,
+                                      const void *gate, int64_t gate_rs, const void *aux2, int64_t aux2_rs, void *y,
+                                      int64_t y_rs, void *y2, int64_t y2_rs, int M, int N, void *stream) {
+  using namespace motif;
+  if (M < 0 || M > 64) return set_error(MOTIF_ERR_UNSUPPORTED, "linear_rows_dual: 1 .. 64 rows");
+  if (!rows_ok(x1, x1_rs, w1, w1_rs, N, K1) || !rows_ok(x2, x2_rs, w2, w2_rs, N, K2) || !y || (y2 && !aux2))
+    return set_error(MOTIF_ERR_UNSUPPORTED, "linear_rows_dual: unsupported shapes or alignment");
+  if (M == 0) return MOTIF_OK;
+  DualArgs a{};
+  a.x1 = static_cast<const bf16_t *>(x1); a.x1_rs = x1_rs; a.w1 = static_cast<const bf16_t *>(w1); a.w1_rs = w1_rs;
+  a.K1 = K1;
+  a.x2 = static_cast<const bf16_t *>(x2); a.x2_rs = x2_rs; a.w2 = static_cast<const bf16_t *>(w2); a.w2_rs = w2_rs;
+  a.K2 = K2;
+  a.gate = static_cast<const bf16_t *>(gate); a.gate_rs = gate_rs;
+  a.aux2 = static_cast<const bf16_t *>(aux2); a.aux2_rs = aux2_rs;
+  a.y = static_cast<bf16_t *>(y); a.y_rs = y_rs; a.y2 = static_cast<bf16_t *>(y2); a.y2_rs = y2_rs;
+  a.M = M; a.N = N;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return gate ? launch_dual<true>(a, s) : launch_dual<false>(a, s);
 }

@@ -279,24 +279,48 @@ class ChordAttention(BasicAttention):
     def _cursor_step(self, x, cache: StaticKVLayerCache) -> AttentionOutput:
         '''Decode at the static cache's device cursor: append, attend, advance -- all
         on the device, so the launch sequence is the same for every token.'''
-        B, L, _ = x.shape
-        proj = self._fused_proj(x)
+        out, g_pre = self._cursor_core(self._fused_proj(x), cache)
+        return AttentionOutput(output=self._gated_output(out, g_pre), past_key_value=cache)
+
+    def decode_split(self, hidden_states, cache, embedding_start=0, attention_mask=None):
+        '''A decode step in three parts, for a caller that batches the projections with
+        other launches: (W_in, core, W_out) or None when the device-cursor decode does not
+        serve this call (same conditions as forward()).  The caller computes
+        proj = hidden_states W_in^T, calls core(proj) -- which appends to `cache`,
+        attends, advances and returns (out, g_pre) -- and applies the gated o_proj,
+        (out W_out^T) * sigmoid(g_pre).  Together: what forward() computes for this step.'''
+        if not isinstance(cache, StaticKVLayerCache) or attention_mask is not None:
+            return None
+        q_start = embedding_start
+        if isinstance(q_start, int) and q_start == 0 and cache.seq_length > 0:
+            q_start = cache.seq_length
+        if isinstance(q_start, torch.Tensor) or not self._kernel_serves(hidden_states):
+            return None
+        if not self._on_cursor(hidden_states, cache, q_start):
+            return None
+        w, b = cat_weights(self, '_proj_cat', (self.q_proj, self.k_proj, self.v_proj, self.g_proj))
+        if b is not None or self.o_proj.bias is not None:
+            return None
+        return w, (lambda proj: self._cursor_core(proj, cache)), self.o_proj.weight
+
+    def _cursor_core(self, proj, cache: StaticKVLayerCache):
+        '''The cursor step from the projected tokens proj [B, L, q|k|v|g]: (merged
+        attention output [B, L, hidden], gate pre-activation [B, L, hidden]).'''
+        B, L = proj.shape[0], proj.shape[1]
         q = torch.empty(B, self.num_heads, L, self.head_dim, dtype=proj.dtype, device=proj.device)
         ks, vs = cache._slab
         self._prep(proj, q, ks, vs, cache.length_dev, -1, cache.capacity)
         if cache.__dict__.get('log_table') is None or cache.log_table.numel() < cache.capacity:
-            cache.log_table = LogPositions.get(cache.capacity, x.device)  # held: a graph keeps its address
+            cache.log_table = LogPositions.get(cache.capacity, proj.device)  # held: a graph keeps its address
         if cache.decode_workspace is None:
             cache.decode_workspace = chord_decode_workspace(B, self.num_heads, self.num_kv_heads, L, cache.capacity,
-                                                            self.head_dim, x.dtype, x.device)
+                                                            self.head_dim, proj.dtype, proj.device)
         alpha, beta, mu, ssmax = self.ggd_params()
         out = chord_decode_cursor(q, ks, vs, cache.length_dev, alpha, beta, mu, ssmax, cache.log_table,
                                   self.head_dim ** -0.5, GGD_EPS, workspace=cache.decode_workspace)
         cache.length += L
         cache.cursor_steps = getattr(cache, 'cursor_steps', 0) + 1
-        return AttentionOutput(output=self._gated_output(self._merge_heads(out), proj[..., self.hidden_size
-                                                                                         + 2 * self.kv_dim:]),
-                               past_key_value=cache)
+        return self._merge_heads(out), proj[..., self.hidden_size + 2 * self.kv_dim:]
 
     def forward_varlen(self, hidden_states: torch.Tensor, cu_seqlens: torch.Tensor) -> AttentionOutput:
         '''Packed sequences (B == 1; new): each sequence attends causally within itself

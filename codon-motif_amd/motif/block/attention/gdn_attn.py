@@ -204,11 +204,19 @@ class GatedDeltaAttention(BasicAttention):
         return True
 
     def _decode_step(self, hidden_states, cache):
-        '''One token through the fused decode kernel.  An empty cache starts from zero
-        state and tails; an in-place cache is updated over its own storage, any other
-        receives new tensors.'''
+        '''One token: the fused projection, the fused decode kernel, o_proj.'''
         B = hidden_states.shape[0]
-        dev, dt = hidden_states.device, hidden_states.dtype
+        w, b = self._proj_weight()
+        proj = project(hidden_states.view(B, -1), w, b)
+        return project(self._decode_core(proj, cache), self.o_proj.weight, self.o_proj.bias)
+
+    def _decode_core(self, proj, cache):
+        '''The step from the projected token (proj [B, ncols] or [B, 1, ncols]) to the
+        o_proj input [B, 1, H dv]: one fused kernel (conv, gates, recurrence, output
+        norm).  An empty cache starts from zero state and tails; an in-place cache is
+        updated over its own storage, any other receives new tensors.'''
+        B = proj.shape[0]
+        dev, dt = proj.device, proj.dtype
         H, K = self.num_heads, self.conv_size
         chans = (H * self.dk, H * self.dk, H * self.dv)
         state, tails = cache.state, cache.conv_state
@@ -220,13 +228,25 @@ class GatedDeltaAttention(BasicAttention):
             state_out, tails_out = state, tails
         else:
             state_out, tails_out = torch.empty_like(state), tuple(torch.empty_like(t) for t in tails)
-        w, b = self._proj_weight()
-        proj = project(hidden_states.view(B, -1), w, b)
-        y = gdn_decode_fused(proj, self._proj_offsets(), (self.q_conv.weight, self.k_conv.weight, self.v_conv.weight),
+        y = gdn_decode_fused(proj.view(B, -1), self._proj_offsets(),
+                             (self.q_conv.weight, self.k_conv.weight, self.v_conv.weight),
                              tails, self.A_log, self.dt_bias, self.o_norm.weight, self.o_norm.eps,
                              state, H, self.dk, self.dv, tails_out=tails_out, state_out=state_out)
         cache.update(state_out, tails_out, steps=1)
-        return project(y.view(B, 1, -1), self.o_proj.weight, self.o_proj.bias)
+        return y.view(B, 1, -1)
+
+    def decode_split(self, hidden_states, cache):
+        '''A decode step in three parts, for a caller that batches the projections with
+        other launches: (W_in, core, W_out) or None when the fused decode does not serve
+        this call.  The caller computes proj = hidden_states W_in^T, calls core(proj) --
+        which runs the step, updates `cache` and returns (o, None) -- and applies
+        o_proj as o W_out^T.  Together: what forward() computes for this step.'''
+        if not isinstance(cache, GatedDeltaAttentionLayerCache) or not self._decode_fusable(hidden_states, cache):
+            return None
+        w, b = self._proj_weight()
+        if b is not None or self.o_proj.bias is not None:
+            return None
+        return w, (lambda proj: (self._decode_core(proj, cache), None)), self.o_proj.weight
 
     def forward(self, hidden_states: torch.Tensor, past_key_value=None) -> AttentionOutput:
         '''Run the layer over [B, L, hidden]; continue from / update `past_key_value`.'''

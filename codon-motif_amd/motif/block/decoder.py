@@ -14,7 +14,7 @@ from motif.model.config import MotifChordConfig
 from motif.ops import RMSNorm
 from motif.ops.attn_res import apply_block_attn_res, attn_res_read_norms
 from motif.ops.epilogue import add_fold, usable
-from motif.ops.linear_rows import MAX_ROWS
+from motif.ops.linear_rows import MAX_ROWS, linear_rows_dual, linear_rows_pair, rows_eligible
 
 
 @dataclass
@@ -73,6 +73,34 @@ def _fold(attn, mlp, partial):
     return attn + mlp, None
 
 
+def _split_step(decoder, x, m, layer_cache, mask, position, prev):
+    '''One decoder's decode step as three launches around the attention core: the
+    attention input projection with the MLP gate/up projection (one launch), the core,
+    and o_proj with the MLP down projection and the residual fold (one launch).  The
+    result equals the layer-then-MLP sequence bit for bit.  Returns (f_h, partial), or
+    None (before anything ran) when the step does not qualify.'''
+    mlp = decoder.mlp
+    if not (mlp._fused(m) and rows_eligible(x, mlp.gate_up_proj.weight)):
+        return None
+    if isinstance(decoder.attn, ChordAttention):
+        split = decoder.attn.decode_split(x, layer_cache, embedding_start=position, attention_mask=mask)
+    elif isinstance(decoder.attn, GatedDeltaAttention):
+        split = decoder.attn.decode_split(x, layer_cache)
+    else:
+        split = None
+    if split is None:
+        return None
+    w_in, core, w_out = split
+    w_gu, w_down = mlp.gate_up_proj.weight, mlp.down_proj.weight
+    if (not rows_eligible(x, w_in) or x.shape[-1] % 64 or w_out.shape[1] % 64 or w_down.shape[1] % 64
+            or w_out.shape[0] != w_down.shape[0] or w_out.dtype != torch.bfloat16 or w_down.dtype != torch.bfloat16
+            or (prev is not None and (prev.dtype != x.dtype or prev.stride(-1) != 1))):
+        return None
+    proj, act = linear_rows_pair(x, w_in, m, w_gu)
+    o, g_pre = core(proj)
+    return linear_rows_dual(o, w_out, act, w_down, gate=g_pre, aux2=prev)
+
+
 class DecoderBlock(nn.Module):
     def __init__(self, config: MotifChordConfig):
         super().__init__()
@@ -118,6 +146,13 @@ class DecoderBlock(nn.Module):
         side = _side_stream(hidden_states)
         for i, decoder in enumerate(self.features):
             x, m = self._read(attn_res, i, decoder)
+            if use_attn_cache and side is None:
+                prev = attn_res.partial_block
+                done = _split_step(decoder, x, m, cache.attn[i], mask, position,
+                                   prev if prev is not None and prev.shape == m.shape else None)
+                if done is not None:
+                    attn_res.update_increment(*done)
+                    continue
             mlp_out = None
             if side is not None:
                 # The MLP branch depends only on h: it runs on a second stream while the

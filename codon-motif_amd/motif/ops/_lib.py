@@ -44,6 +44,11 @@ _SIGNATURES = {
         [_P, _I64] + [_I32] * 6 + [_P] * 12 + [_F32, _P, _P, _P, _I64] + [_I32] * 6 + [_P], _I32),
     'motif_linear_rows': (
         [_P, _I64, _P, _I64, _P, _I64] + [_I32] * 4 + [_P, _I64, _P, _I64, _P, _I64, _P], _I32),
+    'motif_linear_rows_pair': (
+        [_P, _I64, _P, _I64, _P, _I64, _I32, _I32, _I32, _P, _I64, _P, _I64, _P, _I64, _I32, _I32, _I32, _P], _I32),
+    'motif_linear_rows_dual': (
+        [_P, _I64, _P, _I64, _I32, _P, _I64, _P, _I64, _I32, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I32, _I32, _P],
+        _I32),
     'motif_chord_qkv_prep': (
         [_P, _I64, _I64, _I32, _I32, _I32, _P, _P, _F32] + [_P, _I64, _I64, _I64] * 3 + [_P] + [_I32] * 8 + [_P],
         _I32),

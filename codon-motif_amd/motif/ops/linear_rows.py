@@ -101,6 +101,73 @@ def linear_rows(x, weight, epilogue='none', aux=None, aux2=None, out=None, out2=
     return (y, y2) if code == 2 and a2 is not None else y
 
 
+def _rows_of(t, what):
+    t2, lead = _rows2d(t)
+    if t2 is None or t2.dtype != torch.bfloat16 or not t2.is_cuda:
+        raise ValueError(f'{what}: bf16 ROCm rows with unit feature stride required, got {tuple(t.shape)}')
+    return t2, lead
+
+
+def linear_rows_pair(x1, w1, x2, w2, epilogue1='none'):
+    '''(linear_rows(x1, w1, epilogue1), linear_rows(x2, w2, 'swiglu')) in one launch: the
+    decoder's attention input projection and its MLP gate/up projection.  Equal to the
+    two separate calls bit for bit.  K of both a multiple of 64, at most MAX_ROWS rows.'''
+    code = EPILOGUES[epilogue1]
+    if wants_grad(x1, w1, x2, w2):
+        return _torch_form(x1, w1, code, None, None), _torch_form(x2, w2, 3, None, None)
+    a, lead1 = _rows_of(x1, 'linear_rows_pair')
+    b, lead2 = _rows_of(x2, 'linear_rows_pair')
+    M, K = a.shape
+    if b.shape[0] != M:
+        raise ValueError('linear_rows_pair: both inputs need the same rows')
+    N1, N2 = w1.shape[0], w2.shape[0]
+    y1 = torch.empty(*lead1, N1 // 2 if code == 3 else N1, dtype=x1.dtype, device=x1.device)
+    y2 = torch.empty(*lead2, N2 // 2, dtype=x2.dtype, device=x2.device)
+    y1d, y2d = y1.view(M, -1), y2.view(M, -1)
+    rc = _lib.lib().motif_linear_rows_pair(
+        a.data_ptr(), a.stride(0), w1.data_ptr(), w1.stride(0), y1d.data_ptr(), y1d.stride(0), N1, K, code,
+        b.data_ptr(), b.stride(0), w2.data_ptr(), w2.stride(0), y2d.data_ptr(), y2d.stride(0), N2, b.shape[1],
+        M, _lib.stream_ptr(x1.device))
+    _lib.check(rc, 'motif_linear_rows_pair')
+    return y1, y2
+
+
+def linear_rows_dual(x1, w1, x2, w2, gate=None, aux2=None):
+    '''The decoder's output side in one launch: u = x1 W1^T (times sigmoid(gate) when
+    given: Chord's gated o_proj), f = u + x2 W2^T (the MLP's down projection), and
+    p = aux2 + f when aux2 is given (the block's running sum).  Returns (f, p or None);
+    equal bit for bit to linear_rows(x1, w1, 'gate' / 'none') followed by
+    linear_rows(x2, w2, 'resid', aux=u, aux2=aux2).'''
+    if wants_grad(x1, w1, x2, w2, gate, aux2):
+        u = F.linear(x1, w1)
+        if gate is not None:
+            u = u * torch.sigmoid(gate)
+        f = u + F.linear(x2, w2)
+        return f, (None if aux2 is None else aux2 + f)
+    a, lead = _rows_of(x1, 'linear_rows_dual')
+    b, _ = _rows_of(x2, 'linear_rows_dual')
+    M, N = a.shape[0], w1.shape[0]
+    if b.shape[0] != M or w2.shape[0] != N:
+        raise ValueError('linear_rows_dual: the two products must have the same rows and columns')
+    g = _rows_of(gate, 'linear_rows_dual')[0] if gate is not None else None
+    p = _rows_of(aux2, 'linear_rows_dual')[0] if aux2 is not None else None
+    for t in (g, p):
+        if t is not None and tuple(t.shape) != (M, N):
+            raise ValueError(f'linear_rows_dual: gate / aux2 must be [..., {N}]')
+    f = torch.empty(*lead, N, dtype=x1.dtype, device=x1.device)
+    y2 = torch.empty_like(f) if p is not None else None
+    fd = f.view(M, N)
+    y2d = None if y2 is None else y2.view(M, N)
+    rc = _lib.lib().motif_linear_rows_dual(
+        a.data_ptr(), a.stride(0), w1.data_ptr(), w1.stride(0), a.shape[1],
+        b.data_ptr(), b.stride(0), w2.data_ptr(), w2.stride(0), b.shape[1],
+        _lib.ptr(g), 0 if g is None else g.stride(0), _lib.ptr(p), 0 if p is None else p.stride(0),
+        fd.data_ptr(), fd.stride(0), _lib.ptr(y2d), 0 if y2d is None else y2d.stride(0), M, N,
+        _lib.stream_ptr(x1.device))
+    _lib.check(rc, 'motif_linear_rows_dual')
+    return f, y2
+
+
 def _torch_form(x, weight, code, aux, aux2):
     '''The projection and its epilogue as torch ops (differentiable).'''
     y = F.linear(x, weight)

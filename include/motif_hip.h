@@ -396,6 +396,39 @@ int motif_linear_rows(const void *x, int64_t x_rs, const void *w, int64_t w_rs, 
                       const void *aux2, int64_t aux2_rs, void *y2, int64_t y2_rs, void *stream);
 
 /*
+ * Two independent decode projections in one launch: the decoder's attention input
+ * projection (epilogue1 0 none or 3 swiglu) and its MLP gate/up projection (SwiGLU
+ * epilogue), whose inputs -- attn_norm(h) and mlp_norm(h) -- are ready together.
+ * Replaces the projections at motif/block/attention/gdn_attn.py:183-207 (q/k/v/g/a/b
+ * of the new token) or motif/block/attention/chord_attn.py:252-256 (g/q/k/v), together
+ * with motif/block/mlp.py:63 (gate_up_proj + SwiGLU), as two motif_linear_rows calls
+ * would: each output equals that call's bit for bit.
+ *   problem 1: x1 [M, K1] W1 [N1, K1] -> y1 [M, N1] (N1/2 for swiglu)
+ *   problem 2: x2 [M, K2] W2 [N2, K2] -> y2 [M, N2/2]
+ * K1 == K2, a multiple of 64; M <= 64; rows 16-byte aligned.
+ */
+int motif_linear_rows_pair(const void *x1, int64_t x1_rs, const void *w1, int64_t w1_rs, void *y1, int64_t y1_rs,
+                           int N1, int K1, int epilogue1, const void *x2, int64_t x2_rs, const void *w2,
+                           int64_t w2_rs, void *y2, int64_t y2_rs, int N2, int K2, int M, void *stream);
+
+/*
+ * The decoder's two output projections and the residual fold in one launch:
+ *   u = T(x1 W1^T), or with a gate  u = T(T(x1 W1^T) * T(sigmoid(gate)))   (o_proj)
+ *   y = T(u + T(x2 W2^T))                                                   (f_h = attn + down_proj)
+ *   y2 = T(aux2 + y)  when y2 != NULL                                       (the block's running sum)
+ * Replaces motif/block/attention/gdn_attn.py:210 or motif/block/attention/chord_attn.py:313, :361
+ * (o_proj, gated), motif/block/mlp.py:63 (down_proj) and motif/block/decoder.py:207-213
+ * (f_h, update_increment) -- what motif_linear_rows with the gate epilogue followed by
+ * one with the resid epilogue computes, bit for bit.
+ *   x1 [M, K1], W1 [N, K1], x2 [M, K2], W2 [N, K2], gate / aux2 / y / y2 [M, N];
+ *   K1, K2 multiples of 64; M <= 64; rows 16-byte aligned.
+ */
+int motif_linear_rows_dual(const void *x1, int64_t x1_rs, const void *w1, int64_t w1_rs, int K1, const void *x2,
+                           int64_t x2_rs, const void *w2, int64_t w2_rs, int K2, const void *gate, int64_t gate_rs,
+                           const void *aux2, int64_t aux2_rs, void *y, int64_t y_rs, void *y2, int64_t y2_rs, int M,
+                           int N, void *stream);
+
+/*
  * GatedRMSNorm of the GDN layer output per head without the concatenation:
  *   y[b, t, h*dv + e] = T(T(T(o * rsqrt(mean_e o^2 + eps)) * weight[e]) * T(SiLU(gate[b, t, h*dv + e])))
  * for o = o[b, h, t, :].  Replaces motif/block/attention/gdn_attn.py:206-209 (cat + o_norm,

@@ -64,7 +64,10 @@ def _layer_params(model, bi, li, dtype):
 
 class _Tap:
     '''Records every attention layer call of `model`: its input, output and (for calls
-    with a cache) the cache contents before the call, keeping batch rows `rows`.'''
+    with a cache) the cache contents before the call, keeping batch rows `rows`.  While
+    active, decode steps run layer by layer (the decoder's split step, which batches the
+    layer's projections with the MLP's and equals the layer-by-layer step bit for bit,
+    calls no layer forward).'''
 
     def __init__(self, model, rows=None):
         self.model, self.rows, self.records = model, rows, []
@@ -85,6 +88,8 @@ class _Tap:
         return self._keep(cache.state), tuple(self._keep(t) for t in cache.conv_state)
 
     def __enter__(self):
+        import motif.block.decoder as dec
+        self._split, dec._split_step = dec._split_step, (lambda *a, **k: None)
         self.layers = []
         for bi, block in enumerate(self.model.blocks):
             for li, dec in enumerate(block.features):
@@ -109,6 +114,8 @@ class _Tap:
         return self
 
     def __exit__(self, *exc):
+        import motif.block.decoder as dec
+        dec._split_step = self._split
         for attn in self.layers:
             del attn.forward, attn.forward_varlen
 
