@@ -114,15 +114,6 @@ __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
     for (int e = 0; e < E; ++e) qw[i][e] = qv[e] * wv[e];
   }
 
-  // the norm weights of the outputs, requested with the sources (not after the
-  // reductions: that would add a memory round trip at the end)
-  float nwv[2][PPL][E];
-#pragma unroll
-  for (int k = 0; k < 2; ++k)
-#pragma unroll
-    for (int i = 0; i < PPL; ++i)
-      // a norm that is not asked for gets a zero-size buffer: its loads return 0 and touch no memory
-      Piece<T>::unpack(buf_ld16(make_buf(a.nw[k], k < a.nnorm ? dbytes : 0u), (sub + LPT * i) * 16), nwv[k][i]);
   // every source row is loaded before any reduction, so the loads overlap
   float x[kMaxSrc][PPL][E];
 #pragma unroll
@@ -203,9 +194,10 @@ __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
     for (int i = 0; i < PPL; ++i) {
       const int p = sub + LPT * i;
       if (p >= np) continue;
-      float y[E];
+      float w[E], y[E];
+      Piece<T>::unpack(buf_ld16(make_buf(a.nw[k], dbytes), p * 16), w);
 #pragma unroll
-      for (int e = 0; e < E; ++e) y[e] = round_to<T>(h[i][e] * r) * nwv[k][i][e];
+      for (int e = 0; e < E; ++e) y[e] = round_to<T>(h[i][e] * r) * w[e];
       Piece<T>::store(nrow + p * E, y);
     }
   }
