@@ -146,29 +146,201 @@ def kernel_timings(dev):
     a_log = torch.empty(H).uniform_(1, 16, generator=g).log().to(dev, torch.bfloat16)
     dt_bias = (torch.rand(H, generator=g) * 0.1).to(dev, torch.bfloat16)
     nw = torch.ones(dv, device=dev, dtype=torch.bfloat16)
-    S = (torch.randn(Bd, H, dk, dv, generator=g) * 0.05).to(dev)
-    ms = op_time(lambda: ops.gdn_decode_fused(proj, offs, cw, tails, a_log, dt_bias, nw, 1e-6, S, H, dk, dv), 50)
+    # cache-cold: the launches rotate over 12 state / tail sets (302 MB, more than the
+    # 256 MB last-level cache), as the 12 GDN layers of a decode step do
+    n_sets = 12
+    S0 = (torch.randn(Bd, H, dk, dv, generator=g) * 0.05).to(dev)
+    Ss = [S0.clone() for _ in range(n_sets)]
+    tls = [[t.clone() for t in tails] for _ in range(n_sets)]
+    turn = [0]
+
+    def gdn_step():
+        i = turn[0] % n_sets
+        turn[0] += 1
+        ops.gdn_decode_fused(proj, offs, cw, tls[i], a_log, dt_bias, nw, 1e-6, Ss[i], H, dk, dv)
+    ms = op_time(gdn_step, 48)
     byts = (Bd * H * dk * dv * 4 * 2                      # state read + write
             + Bd * (2 * hk + hv) * (K - 1) * 2 * 2        # conv tails read + write
             + Bd * ncols * 2 + (2 * hk + hv) * K * 2      # projections, conv weights
             + Bd * hv * 2)                                # output
     res['gdn_decode'] = dict(us=ms * 1e3, unit='GB/s', achieved=byts / (ms * 1e-3) / 1e9,
                              peak=PEAK_HBM_GBS, bound='hbm', work=byts,
-                             shape='B=64 H=12 dk=64 dv=128 K=4, fused layer step, fp32 state in place')
+                             shape='B=64 H=12 dk=64 dv=128 K=4, fused layer step, fp32 state in place; '
+                                   'cache-cold (12 rotating state sets)')
+    del Ss, tls
 
     Sk = 4097
     qk = (torch.randn(Bd, Hc, 1, D, generator=g) * 0.5).to(dev, torch.bfloat16)
     kk = (torch.randn(Bd, Hkv, Sk, D, generator=g) * 0.5).to(dev, torch.bfloat16)
     vk = (torch.randn(Bd, Hkv, Sk, D, generator=g) * 0.5).to(dev, torch.bfloat16)
     lnd = torch.full((Bd, 1), float(torch.log(torch.tensor(float(Sk)))), device=dev)
-    ms = op_time(lambda: ops.apply_chord_attention(qk, kk, vk, al, be, mu, ss, lnd), 20)
+    # cache-cold: four K / V sets (805 MB) in rotation, as the 4 Chord layers of a step
+    kvs = [(kk, vk)] + [(kk.clone(), vk.clone()) for _ in range(3)]
+    turn = [0]
+
+    def chord_step():
+        kx, vx = kvs[turn[0] % len(kvs)]
+        turn[0] += 1
+        ops.apply_chord_attention(qk, kx, vx, al, be, mu, ss, lnd)
+    ms = op_time(chord_step, 20)
     byts = 2 * Bd * Hkv * Sk * D * 2 + 2 * Bd * Hc * D * 2
     res['chord_decode'] = dict(us=ms * 1e3, unit='GB/s', achieved=byts / (ms * 1e-3) / 1e9,
                                peak=PEAK_HBM_GBS, bound='hbm', work=byts,
-                               shape='B=64 H=12 Hkv=3 S=4097 D=64 bf16 (split-K + merge)')
+                               shape='B=64 H=12 Hkv=3 S=4097 D=64 bf16 (split-K + merge); cache-cold '
+                                     '(4 rotating K / V sets)')
+    del kvs
     for r in res.values():
         r['frac'] = r['achieved'] / r['peak']
     return res
+
+
+def _median_ms(fn, reps=10):
+    '''Median device milliseconds of fn() over `reps` launches, one HIP event pair each.'''
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    return sorted(ts)[len(ts) // 2]
+
+
+def measured_peaks(dev):
+    '''The roofline denominators measured on this GPU (median of 10 launches each):
+    a 1 GiB device copy (2 GiB of traffic), a 2 GiB read-only reduction and a loop of
+    independent dense bf16 MFMAs (motif_probe_* in codon-motif_amd/csrc/peaks.hip).'''
+    import torch
+
+    from motif.ops import _lib
+    lib = _lib.lib()
+    st = _lib.stream_ptr(dev)
+    ncu = torch.cuda.get_device_properties(dev).multi_processor_count
+    src = torch.ones(2 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    red = torch.empty(16 * ncu, dtype=torch.int32, device=dev)
+
+    def run(rc, what):
+        _lib.check(rc, what)
+
+    copy_ms = _median_ms(lambda: run(lib.motif_probe_copy(src.data_ptr(), dst.data_ptr(), 1 << 30, 16 * ncu, st),
+                                     'motif_probe_copy'))
+    read_ms = _median_ms(lambda: run(lib.motif_probe_read(src.data_ptr(), red.data_ptr(), 2 << 30, 16 * ncu, st),
+                                     'motif_probe_read'))
+    grid, iters = 8 * ncu, 2048
+    out = torch.empty(grid * 256, dtype=torch.float32, device=dev)
+    rates = {}
+    for shape, per in ((16, 8 * 16384), (32, 4 * 32768)):
+        ms = _median_ms(lambda: run(lib.motif_probe_mfma_bf16(out.data_ptr(), grid, iters, shape, st),
+                                    'motif_probe_mfma_bf16'))
+        rates[shape] = grid * 4 * iters * per / (ms * 1e-3) / 1e12
+    del src, dst, red, out
+    return {'hbm_copy_GBs': round(2 * 2 ** 30 / (copy_ms * 1e-3) / 1e9, 1),
+            'hbm_read_GBs': round(2 * 2 ** 30 / (read_ms * 1e-3) / 1e9, 1),
+            'mfma_bf16_TFLOPs': round(max(rates.values()), 1),
+            'mfma_bf16_16x16x32_TFLOPs': round(rates[16], 1), 'mfma_bf16_32x32x16_TFLOPs': round(rates[32], 1),
+            'published': {'hbm_GBs': PEAK_HBM_GBS, 'mfma_bf16_TFLOPs': PEAK_BF16_TFLOPS},
+            'method': '1 GiB copy (bytes read + written), 2 GiB read-only reduction, '
+                      f'{grid} workgroups x 4 waves x {iters} rounds of 8 independent '
+                      'v_mfma_f32_16x16x32_bf16 or 4 independent v_mfma_f32_32x32x16_bf16; '
+                      'median of 10 launches each'}
+
+
+def _cpu_time(fn, reps=1):
+    import torch
+    torch.set_num_threads(os.cpu_count() or 1)
+    t0 = time.perf_counter()
+    with torch.no_grad():
+        for _ in range(reps):
+            fn()
+    return (time.perf_counter() - t0) / reps
+
+
+def config_rows(dev, model, with_cpu=True):
+    '''The other configurations of the scope table at their own shapes: config 1 (GDN op,
+    fp32), config 2 (Chord op, bf16, Hkv 12 and 3) and, for the CPU baseline only,
+    config 4 (decode steps of the oracle model on random-filled caches).  GPU figures are
+    op_time averages (graph-replayed launches); CPU figures one run of the oracle.'''
+    import torch
+    import torch.nn.functional as F
+
+    import motif.ops as ops
+    from oracle.chord import chord_attention, chord_prefill_flops
+    from oracle.gdn import chunked, gdn_prefill_flops
+    rows = {}
+
+    # config 1: B=1 H=4 T=256 dk=dv=64 fp32, q / k L2-normalised
+    g = torch.Generator().manual_seed(0)
+    B, H, T, dk, dv = 1, 4, 256, 64, 64
+    q = F.normalize(torch.randn(B, H, T, dk, generator=g), dim=-1)
+    k = F.normalize(torch.randn(B, H, T, dk, generator=g), dim=-1)
+    v = torch.randn(B, H, T, dv, generator=g)
+    beta = torch.sigmoid(torch.randn(B, H, T, generator=g))
+    gg = F.logsigmoid(torch.randn(B, H, T, generator=g))
+    dq, dk_, dv_, db, dg = (t.to(dev) for t in (q, k, v, beta, gg))
+    ms = op_time(lambda: ops.chunk_gated_delta_rule(dq, dk_, dv_, db, dg), 20)
+    fl = gdn_prefill_flops(B, T, H, dk, dv)
+    rows['config1_gdn_chunk_fp32'] = {
+        'shape': 'B=1 H=4 T=256 dk=dv=64 fp32', 'gpu_us': round(ms * 1e3, 2),
+        'gpu_tok_s': round(B * T / (ms * 1e-3), 1), 'flops': fl}
+    if with_cpu:
+        dt = _cpu_time(lambda: chunked(q, k, v, beta, gg), reps=3)
+        rows['config1_gdn_chunk_fp32']['cpu_oracle_us'] = round(dt * 1e6, 1)
+
+    # config 2: B=2 H=12 T=2048 D=64 bf16, Hkv 12 (the configuration) and 3 (the model's)
+    Bc, Hc, Tc, D = 2, 12, 2048, 64
+    al = torch.randn(Hc, generator=g) * 0.1
+    be = torch.randn(Hc, generator=g) * 0.1
+    mu, ss = torch.zeros(Hc), torch.ones(Hc)
+    ln = torch.log(torch.arange(1, Tc + 1, dtype=torch.float32))[None].expand(Bc, Tc).contiguous()
+    fl = chord_prefill_flops(Bc, Hc, D, Tc)
+    for hkv in (12, 3):
+        qc = (torch.randn(Bc, Hc, Tc, D, generator=g) * 0.5).to(torch.bfloat16)
+        kc = (torch.randn(Bc, hkv, Tc, D, generator=g) * 0.5).to(torch.bfloat16)
+        vc = (torch.randn(Bc, hkv, Tc, D, generator=g) * 0.5).to(torch.bfloat16)
+        args = [t.to(dev) for t in (qc, kc, vc, al, be, mu, ss, ln)]
+        ms = op_time(lambda: ops.apply_chord_attention(*args, q_start=0), 20)
+        r = {'shape': f'B=2 H=12 Hkv={hkv} T=2048 D=64 bf16 causal', 'gpu_us': round(ms * 1e3, 2),
+             'gpu_TFLOPs': round(fl / (ms * 1e-3) / 1e12, 2), 'frac_of_published_mfma':
+             round(fl / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), 'flops': fl}
+        if with_cpu and hkv == 12:
+            dt = _cpu_time(lambda: chord_attention(qc.float(), kc.float(), vc.float(), al, be, mu, ss, ln,
+                                                   q_start=0, compute_dtype=torch.float32))
+            r['cpu_oracle_us'] = round(dt * 1e6, 1)
+        rows[f'config2_chord_prefill_hkv{hkv}'] = r
+
+    # config 4 on the CPU: decode steps of the oracle model over random-filled caches
+    if with_cpu:
+        from oracle.model import OracleModel
+        cfg = model.config
+        p = {kk: vv.detach().float().cpu() for kk, vv in model.state_dict().items()}
+        om = OracleModel(p, dict(model_dim=cfg.model_dim, num_heads=cfg.num_heads, num_kv_heads=cfg.num_kv_heads,
+                                 head_k_dim=cfg.head_k_dim, block=cfg.block, block_n=cfg.block_n),
+                         dtype=torch.float32)
+        Bd, ctx, hd = 64, 4096, cfg.model_dim // cfg.num_heads
+        gd = torch.Generator().manual_seed(1)
+        for li, kind in enumerate(list(cfg.block) * cfg.block_n):
+            if kind == 'chord':
+                om.kc[li] = torch.randn(Bd, cfg.num_kv_heads, ctx, hd, generator=gd) * 0.5
+                om.vc[li] = torch.randn(Bd, cfg.num_kv_heads, ctx, hd, generator=gd) * 0.5
+            else:
+                om.state[li] = torch.randn(Bd, om.H, om.dk, om.dv, generator=gd) * 0.05
+                om.conv[li] = tuple(torch.randn(Bd, c, 3, generator=gd) * 0.5
+                                    for c in (om.H * om.dk, om.H * om.dk, om.H * om.dv))
+        om.pos = ctx
+        ids = torch.randint(0, cfg.vocab_size, (Bd, 1), generator=gd)
+        dt = _cpu_time(lambda: om.forward(ids), reps=2)
+        rows['config4_decode_cpu'] = {
+            'shape': 'B=64, context 4096 (random-filled caches), one token per step', 'cpu_oracle_ms_per_step':
+            round(dt * 1e3, 1), 'cpu_tok_s': round(Bd / dt, 1), 'cores': torch.get_num_threads()}
+    rows['config5_packed_prefill'] = {
+        'skipped': 'kept off the GPU this build: a packed 73364-token prefill exceeded its test time limit '
+                   'with the fused GatedDelta front end (now switched off for packed input); cause not established'}
+    return rows
 
 
 def copy_calibration(dev, mib=256, reps=5):
@@ -350,6 +522,8 @@ def main():
         graph_ok = bool(torch.equal(pout.logits, eager_logits))
     ms_step = ev0.elapsed_time(ev1) / args.steps
     prefill_tok_s = T / (ms_step * 1e-3)
+    with torch.no_grad():
+        pre_med = _median_ms(pgraph.replay, reps=max(args.steps, 10))
     log(f'[bench] prefill (graph) {ms_step:.2f} ms/step ({prefill_tok_s:.0f} tok/s, wall {wall:.2f} s), '
         f'logits equal eager: {graph_ok}')
     del pgraph, pout, eager_logits
@@ -357,8 +531,8 @@ def main():
     log('[bench] decode B=64 ctx=4096 (one captured step replayed token after token)')
     from motif.model.decode_graph import DecodeGraph
     Bd, ctx = args.decode_batch, 4096
-    n_dec = max(args.steps * 5, 20)
-    cache = make_decode_cache(model, Bd, ctx, ctx + n_dec + 16, dev, torch.bfloat16)
+    n_dec = max(args.steps * 10, 100)
+    cache = make_decode_cache(model, Bd, ctx, ctx + 2 * n_dec + 16, dev, torch.bfloat16)
     toks = torch.randint(0, cfg.vocab_size, (n_dec + 8, Bd, 1), generator=torch.Generator().manual_seed(1)).to(dev)
     with torch.no_grad():
         graph = DecodeGraph(model, cache, Bd)
@@ -372,6 +546,8 @@ def main():
         torch.cuda.synchronize()
     dec_ms = ev0.elapsed_time(ev1) / n_dec
     decode_tok_s = Bd / (dec_ms * 1e-3)
+    with torch.no_grad():
+        dec_med = _median_ms(graph.step, reps=n_dec)
     log(f'[bench] decode {dec_ms:.3f} ms/step ({decode_tok_s:.0f} tok/s), context {ctx} -> {cache.seq_len}')
     del graph, cache
 
@@ -385,9 +561,20 @@ def main():
                'chord_prefill': kern['chord_prefill']['us'] * 4}
     dom = max(per_fwd, key=per_fwd.get)
     r = kern[dom]
+    log('[bench] measured peaks')
+    with torch.no_grad():
+        peaks = measured_peaks(dev)
+    log(f'[bench]   {peaks}')
+    mpeak = peaks['mfma_bf16_TFLOPs'] if r['bound'] == 'mfma' else peaks['hbm_copy_GBs']
     roofline = dict(kernel=dom, bound=r['bound'], achieved=round(r['achieved'], 3), peak=r['peak'],
                     unit=r['unit'], frac=round(r['frac'], 5), traffic=measured_traffic(dom), avg_us=round(r['us'], 2),
-                    work_per_launch=r['work'], shape=r['shape'])
+                    work_per_launch=r['work'], shape=r['shape'], measured_peak=mpeak,
+                    frac_of_measured=round(r['achieved'] / mpeak, 5))
+    log('[bench] configs 1, 2 (GPU ops) and CPU baselines of configs 1, 2, 4')
+    with torch.no_grad():
+        configs = config_rows(dev, model, with_cpu=not args.no_cpu)
+    for name, row in configs.items():
+        log(f'[bench]   {name}: {row}')
 
     cpu = None
     if not args.no_cpu:
@@ -407,12 +594,16 @@ def main():
         'prefill_eager': {'tok_s': round(T / (ms_eager * 1e-3), 1), 'ms_per_step': round(ms_eager, 4),
                           'note': 'the same forward launched from Python each step'},
         'prefill_graph_matches_eager': graph_ok,
-        'decode': {'tok_s': round(decode_tok_s, 1), 'ms_per_step': round(dec_ms, 4), 'batch': Bd,
+        'prefill_median_ms': round(pre_med, 4),
+        'decode': {'tok_s': round(decode_tok_s, 1), 'ms_per_step': round(dec_ms, 4),
+                   'median_ms_per_step': round(dec_med, 4), 'batch': Bd,
                    'context': ctx, 'steps': n_dec,
                    'note': 'config 4: one decode step captured as a hipGraph and replayed token after token '
                            '(device-resident cache cursors, no host rewinds; the context grows from 4096 by one '
                            'position per step); caches random-filled to 4096 positions (timing only)'},
         'roofline': roofline,
+        'peaks': peaks,
+        'configs': configs,
         'kernels': {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in kern.items()},
         'cpu_baseline': cpu,

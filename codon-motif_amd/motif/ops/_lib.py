@@ -74,6 +74,9 @@ _SIGNATURES = {
     'motif_chord_decode_noalloc': (
         _T4 * 3 + [_P, _I32] + [_P] * 4 + [_P, _I64, _I64, _P, _I32] + _T4 + [_I32] * 5 + [_F32, _F32]
         + [_I32, _P], _I32),
+    'motif_probe_copy': ([_P, _P, _SZ, _I32, _P], _I32),
+    'motif_probe_read': ([_P, _P, _SZ, _I32, _P], _I32),
+    'motif_probe_mfma_bf16': ([_P, _I32, _I32, _I32, _P], _I32),
     'motif_chord_fwd': (
         _T4 * 3 + [_P, _P, _P, _P] + [_P, _I64, _I64] + _T4 + [_P] + [_I32] * 6
         + [_I32, _F32, _F32] + [_P, _I32, _I32] + [_P, _SZ] + [_I32, _P], _I32),

@@ -471,6 +471,23 @@ int motif_gdn_gates(const void *a, int64_t a_sb, int64_t a_st, const void *b, in
 int motif_mul_sigmoid(const void *x, int64_t x_rs, const void *g, int64_t g_rs, void *y, int64_t y_rs,
                       int M, int N, int dtype, void *stream);
 
+/*
+ * Measurement probes (no reference counterpart): the measured denominators of the
+ * roofline fractions bench.py reports beside the published MI355X peaks.
+ *   motif_probe_copy       dst = src over `bytes` (a multiple of 16): each byte read
+ *                          once and written once;
+ *   motif_probe_read       a reduction of src (`bytes`, a multiple of 16) to one word
+ *                          per workgroup in out [grid];
+ *   motif_probe_mfma_bf16  `iters` rounds per wave of eight independent
+ *                          v_mfma_f32_16x16x32_bf16 (shape 16) or four independent
+ *                          v_mfma_f32_32x32x16_bf16 (shape 32), 16384 / 32768 flops each,
+ *                          256-thread workgroups; out [grid * 256] fp32 receives one value
+ *                          per thread.
+ */
+int motif_probe_copy(const void *src, void *dst, size_t bytes, int grid, void *stream);
+int motif_probe_read(const void *src, void *out, size_t bytes, int grid, void *stream);
+int motif_probe_mfma_bf16(void *out, int grid, int iters, int shape, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
