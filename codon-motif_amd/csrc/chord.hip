@@ -495,27 +495,63 @@ template <> struct Row8<float> {
   }
 };
 
-constexpr int kDecKeys = 4;                 // keys per 8-lane group per step
-constexpr int kDecStep = 8 * kDecKeys;      // keys per wave per step
+template <> struct Row8<f16_t> {
+  uint4 u;
+  __device__ __forceinline__ void load(buf_t r, uint32_t off) { u = buf_ld16(r, off); }
+  __device__ __forceinline__ void load(const f16_t *p) { u = *reinterpret_cast<const uint4 *>(p); }
+  __device__ __forceinline__ float dot(const Row8 &o, float acc) const {
+    float x[8], y[8];
+    unpack(x);
+    o.unpack(y);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = fmaf(x[e], y[e], acc);
+    return acc;
+  }
+  __device__ __forceinline__ void unpack(float x[8]) const {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = static_cast<float>(__builtin_bit_cast(f16_t, static_cast<uint16_t>(w[e] & 0xffffu)));
+      x[2 * e + 1] = static_cast<float>(__builtin_bit_cast(f16_t, static_cast<uint16_t>(w[e] >> 16)));
+    }
+  }
+};
+
+// Sum over the LPK lanes that share a key (LPK = D / 8 lanes of 8 features each).
+template <int LPK>
+__device__ __forceinline__ float sum_key(float x) {
+  if constexpr (LPK == 8) {
+    return sum8(x);
+  } else {
+#pragma unroll
+    for (int off = 1; off < LPK; off <<= 1) x += __shfl_xor(x, off, 64);
+    return x;
+  }
+}
+
+constexpr int kDecKeys = 4;                 // keys per lane group per step
 
 // Rows of a workgroup: global row gr = qc * R + r over the L * group (query,
 // head) pairs of one kv head, query i = gr / group, head = kvh * group + gr % group.
-// A wave takes kDecStep consecutive keys per step: lane (ksub = lane / 8, 8 features
-// from column 8 (lane % 8)) owns keys n0 + 4 ksub + it, it < 4, whose 4 bias entries
-// are one 16-byte read of the head's table.  The next step's K / V rows and bias
-// entries are loaded before the current step is computed (two register stages), so a
-// wave keeps a step of loads in flight.  Each 8-lane group keeps its own running
-// max / sum / output (merged at the end): the step has no cross-lane traffic besides
-// the 8-lane dot-product sums.
-template <typename T, int R>
+// A key row of D features is held by LPK = D / 8 lanes (8 features each), so a wave
+// has KG = 64 / LPK lane groups and takes KG * 4 consecutive keys per step: lane
+// (ksub = lane / LPK, features 8 (lane % LPK) ..) owns keys n0 + 4 ksub + it, it < 4,
+// whose 4 bias entries are one 16-byte read of the head's table.  The next step's
+// K / V rows and bias entries are loaded before the current step is computed (two
+// register stages), so a wave keeps a step of loads in flight.  Each lane group keeps
+// its own running max / sum / output (merged at the end): the step has no cross-lane
+// traffic besides the LPK-lane dot-product sums.  This kernel serves every dtype
+// (fp32, bf16, fp16) and head dim (16, 32, 64, 128); bf16 at D = 64 has MFMA kernels.
+template <typename T, int R, int D>
 __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a, const float *tab, int tab_n) {
+  constexpr int LPK = D / 8, KG = 64 / LPK, kDecStep = KG * kDecKeys;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int split = blockIdx.x, kvh = blockIdx.y;
   const int b = blockIdx.z / a.nqc, qc = blockIdx.z % a.nqc;
   const int group = a.H / a.Hkv;
   const int total_rows = a.L * group;
-  const int dc = (lane & 7) * 8;  // this lane's 8 feature columns
-  const int ksub = lane >> 3;     // key group of this lane
+  const int dc = (lane % LPK) * 8;  // this lane's 8 feature columns
+  const int ksub = lane / LPK;      // key group of this lane
   const T *qg = static_cast<const T *>(a.q);
   T *og = static_cast<T *>(a.out);
 
@@ -555,8 +591,8 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a, const fl
   const T *kp = static_cast<const T *>(a.k) + b * a.k_sb + kvh * a.k_sh;
   const T *vp = static_cast<const T *>(a.v) + b * a.v_sb + kvh * a.v_sh;
   // rows past k_hi (the prefetch past the range) read as zeros
-  const buf_t kbuf = make_buf(kp, k_hi > 0 ? static_cast<uint32_t>(((k_hi - 1) * a.k_st + kD) * sizeof(T)) : 0u);
-  const buf_t vbuf = make_buf(vp, k_hi > 0 ? static_cast<uint32_t>(((k_hi - 1) * a.v_st + kD) * sizeof(T)) : 0u);
+  const buf_t kbuf = make_buf(kp, k_hi > 0 ? static_cast<uint32_t>(((k_hi - 1) * a.k_st + D) * sizeof(T)) : 0u);
+  const buf_t vbuf = make_buf(vp, k_hi > 0 ? static_cast<uint32_t>(((k_hi - 1) * a.v_st + D) * sizeof(T)) : 0u);
 
   struct Stage {
     Row8<T> k[kDecKeys], v[kDecKeys];
@@ -593,7 +629,7 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a, const fl
       float sv[kDecKeys], mx = -INFINITY;
 #pragma unroll
       for (int it = 0; it < kDecKeys; ++it) {
-        const float d = sum8(cur.k[it].dot(q[r], 0.f));
+        const float d = sum_key<LPK>(cur.k[it].dot(q[r], 0.f));
         const int key = kb + it;
         const bool ok = key < k_hi && key <= qabs[r];
         sv[it] = ok ? fmaf(d, c_qk[r], c_b[r] * bt[it]) : -INFINITY;
@@ -621,24 +657,21 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a, const fl
     cur = nxt;
   }
 
-  // Merge the 8 key groups of the wave (lanes l, l^8, l^16, l^32 share features).
+  // Merge the KG key groups of the wave (lanes l, l ^ LPK, l ^ 2 LPK, ... share features).
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     float M = m[r];
-    M = fmaxf(M, __shfl_xor(M, 8, 64));
-    M = fmaxf(M, __shfl_xor(M, 16, 64));
-    M = fmaxf(M, __shfl_xor(M, 32, 64));
+#pragma unroll
+    for (int off = LPK; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
     const float f = m[r] == -INFINITY ? 0.f : fast_exp2(m[r] - (M == -INFINITY ? 0.f : M));
     float lx = l[r] * f;
-    lx += __shfl_xor(lx, 8, 64);
-    lx += __shfl_xor(lx, 16, 64);
-    lx += __shfl_xor(lx, 32, 64);
+#pragma unroll
+    for (int off = LPK; off < 64; off <<= 1) lx += __shfl_xor(lx, off, 64);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       float x = acc[r][e] * f;
-      x += __shfl_xor(x, 8, 64);
-      x += __shfl_xor(x, 16, 64);
-      x += __shfl_xor(x, 32, 64);
+#pragma unroll
+      for (int off = LPK; off < 64; off <<= 1) x += __shfl_xor(x, off, 64);
       acc[r][e] = x;
     }
     m[r] = M;
@@ -646,8 +679,8 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a, const fl
   }
 
   // Merge the 4 waves in LDS.
-  __shared__ float sm[4][R], sl[4][R], sacc[4][R][kD];
-  if (lane < 8) {
+  __shared__ float sm[4][R], sl[4][R], sacc[4][R][D];
+  if (lane < LPK) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -658,8 +691,8 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a, const fl
     for (int r = 0; r < R; ++r) { sm[w][r] = m[r]; sl[w][r] = l[r]; }
   }
   __syncthreads();
-  for (int e = tid; e < R * kD; e += 256) {
-    const int r = e / kD, d = e % kD;
+  for (int e = tid; e < R * D; e += 256) {
+    const int r = e / D, d = e % D;
     const int gr = qc * R + r;
     if (gr >= total_rows) continue;
     float M = -INFINITY;
@@ -678,9 +711,9 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a, const fl
       st(og + b * a.o_sb + head * a.o_sh + int64_t(i) * a.o_st + d, o / fmaxf(Ls, 1e-20f));
       if (a.lse && d == 0) a.lse[(static_cast<size_t>(b) * a.H + head) * a.L + i] = M + fast_log2(Ls);
     } else {
-      float *pp = a.part + ((((static_cast<size_t>(b) * a.Hkv + kvh) * a.splits + split) * total_rows + gr) * (kD + 2));
+      float *pp = a.part + ((((static_cast<size_t>(b) * a.Hkv + kvh) * a.splits + split) * total_rows + gr) * (D + 2));
       pp[d] = o;
-      if (d == 0) { pp[kD] = M; pp[kD + 1] = Ls; }
+      if (d == 0) { pp[D] = M; pp[D + 1] = Ls; }
     }
   }
 }
@@ -884,21 +917,21 @@ __global__ void __launch_bounds__(256) chord_decode_mfma_kernel(ChordArgs a) {
   }
 }
 
-template <typename T>
-__global__ void __launch_bounds__(64) chord_merge_kernel(ChordArgs a) {
+template <typename T, int D = kD>
+__global__ void __launch_bounds__(128) chord_merge_kernel(ChordArgs a) {
   const int gr = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, d = threadIdx.x;
   const int group = a.H / a.Hkv;
   const int total_rows = a.L * group;
-  const float *pp = a.part + (((static_cast<size_t>(b) * a.Hkv + kvh) * a.splits) * total_rows + gr) * (kD + 2);
-  const size_t sstride = static_cast<size_t>(total_rows) * (kD + 2);
+  const float *pp = a.part + (((static_cast<size_t>(b) * a.Hkv + kvh) * a.splits) * total_rows + gr) * (D + 2);
+  const size_t sstride = static_cast<size_t>(total_rows) * (D + 2);
   float M = -INFINITY;
-  for (int s = 0; s < a.splits; ++s) M = fmaxf(M, pp[s * sstride + kD]);
+  for (int s = 0; s < a.splits; ++s) M = fmaxf(M, pp[s * sstride + D]);
   const float Mu = M == -INFINITY ? 0.f : M;
   float o = 0.f, Ls = 0.f;
   for (int s = 0; s < a.splits; ++s) {
-    const float f = fast_exp2(pp[s * sstride + kD] - Mu);
+    const float f = fast_exp2(pp[s * sstride + D] - Mu);
     o += pp[s * sstride + d] * f;
-    Ls += pp[s * sstride + kD + 1] * f;
+    Ls += pp[s * sstride + D + 1] * f;
   }
   const int head = kvh * group + gr % group, i = gr / group;
   st(static_cast<T *>(a.out) + b * a.o_sb + head * a.o_sh + int64_t(i) * a.o_st + d, o / fmaxf(Ls, 1e-20f));
@@ -933,14 +966,45 @@ static int decode_splits(int B, int Hkv, int S) {
   return std::max(1, std::min(want, 32));
 }
 
-template <typename T>
-static void launch_decode(const ChordArgs &a, int R, const float *tab, int tab_n, hipStream_t s) {
+template <typename T, int D>
+static void launch_decode_d(const ChordArgs &a, int R, const float *tab, int tab_n, hipStream_t s) {
   const dim3 grid(a.splits, a.Hkv, a.B * a.nqc), block(256);
-  if (R <= 1) chord_decode_kernel<T, 1><<<grid, block, 0, s>>>(a, tab, tab_n);
-  else if (R <= 2) chord_decode_kernel<T, 2><<<grid, block, 0, s>>>(a, tab, tab_n);
-  else if (R <= 4) chord_decode_kernel<T, 4><<<grid, block, 0, s>>>(a, tab, tab_n);
-  else chord_decode_kernel<T, 8><<<grid, block, 0, s>>>(a, tab, tab_n);
+  if (R <= 1) chord_decode_kernel<T, 1, D><<<grid, block, 0, s>>>(a, tab, tab_n);
+  else if (R <= 2) chord_decode_kernel<T, 2, D><<<grid, block, 0, s>>>(a, tab, tab_n);
+  else if (R <= 4) chord_decode_kernel<T, 4, D><<<grid, block, 0, s>>>(a, tab, tab_n);
+  else chord_decode_kernel<T, 8, D><<<grid, block, 0, s>>>(a, tab, tab_n);
 }
+
+// The vector kernel and (with splits) its merge, for head dim D in {16, 32, 64, 128}.
+template <typename T>
+static int launch_vector(const ChordArgs &a, int R, int D, const float *tab, int tab_n, hipStream_t s) {
+  switch (D) {
+    case 16: launch_decode_d<T, 16>(a, R, tab, tab_n, s); break;
+    case 32: launch_decode_d<T, 32>(a, R, tab, tab_n, s); break;
+    case 64: launch_decode_d<T, 64>(a, R, tab, tab_n, s); break;
+    default: launch_decode_d<T, 128>(a, R, tab, tab_n, s); break;
+  }
+  int rc = check_launch("chord_decode_kernel");
+  if (rc || !a.part) return rc;  // partials (split keys, or the cursor decode): merge them
+  const dim3 grid((a.H / a.Hkv) * a.L, a.Hkv, a.B);
+  switch (D) {
+    case 16: chord_merge_kernel<T, 16><<<grid, dim3(16), 0, s>>>(a); break;
+    case 32: chord_merge_kernel<T, 32><<<grid, dim3(32), 0, s>>>(a); break;
+    case 64: chord_merge_kernel<T, 64><<<grid, dim3(64), 0, s>>>(a); break;
+    default: chord_merge_kernel<T, 128><<<grid, dim3(128), 0, s>>>(a); break;
+  }
+  return check_launch("chord_merge_kernel");
+}
+
+static int launch_vector_dt(int dtype, const ChordArgs &a, int R, int D, const float *tab, int tab_n, hipStream_t s) {
+  if (dtype == MOTIF_BF16) return launch_vector<bf16_t>(a, R, D, tab, tab_n, s);
+  if (dtype == MOTIF_F16) return launch_vector<f16_t>(a, R, D, tab, tab_n, s);
+  return launch_vector<float>(a, R, D, tab, tab_n, s);
+}
+
+static bool head_dim_ok(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
+// bf16 at the model's head dim takes the MFMA kernels; everything else the vector kernel
+static bool mfma_path(int dtype, int D) { return dtype == MOTIF_BF16 && D == kD; }
 
 // Workspace of the decode / fp32 paths: the bias table [H][S + 8] fp32 (read by the
 // fp32 vector kernel; the bf16 MFMA kernel evaluates the bias in registers), then the
@@ -988,19 +1052,19 @@ extern "C" int motif_chord_fwd(
   if (B < 0 || H <= 0 || Hkv <= 0 || L < 0 || S < 0 || q_start < 0)
     return set_error(MOTIF_ERR_INVALID, "chord_fwd: bad size or negative q_start");
   if (H % Hkv != 0) return set_error(MOTIF_ERR_INVALID, "chord_fwd: H must be a multiple of Hkv");
-  if (D != kD) return set_error(MOTIF_ERR_UNSUPPORTED, "chord_fwd: head_dim must be 64");
-  if (dtype != MOTIF_BF16 && dtype != MOTIF_F32)
-    return set_error(MOTIF_ERR_UNSUPPORTED, "chord_fwd: dtype must be bf16 or fp32");
+  if (!head_dim_ok(D)) return set_error(MOTIF_ERR_UNSUPPORTED, "chord_fwd: head_dim must be 16, 32, 64 or 128");
+  if (dtype != MOTIF_BF16 && dtype != MOTIF_F32 && dtype != MOTIF_F16)
+    return set_error(MOTIF_ERR_UNSUPPORTED, "chord_fwd: dtype must be bf16, fp16 or fp32");
   const bool packed = cu_seqlens != nullptr;
   if (packed && (B != 1 || nseq <= 0 || L != S))
     return set_error(MOTIF_ERR_INVALID, "chord_fwd: packed sequences need B == 1, nseq > 0 and L == S");
-  if (packed && dtype != MOTIF_BF16)
-    return set_error(MOTIF_ERR_UNSUPPORTED, "chord_fwd: packed sequences are implemented for bf16");
+  if (packed && !mfma_path(dtype, D))
+    return set_error(MOTIF_ERR_UNSUPPORTED, "chord_fwd: packed sequences are implemented for bf16, head_dim 64");
   if (!packed && nseq != B) return set_error(MOTIF_ERR_INVALID, "chord_fwd: nseq must equal B");
   if (B == 0 || L == 0) return MOTIF_OK;
   if (!q || !k || !v || !alpha || !beta || !mu || !ssmax || !log_n || !out)
     return set_error(MOTIF_ERR_INVALID, "chord_fwd: NULL pointer");
-  const int64_t vec = dtype == MOTIF_BF16 ? 8 : 4;  // elements per 16 bytes
+  const int64_t vec = dtype == MOTIF_F32 ? 4 : 8;  // elements per 16 bytes
   if (((q_st | k_st | v_st | o_st | q_sh | k_sh | v_sh | o_sh | q_sb | k_sb | v_sb | o_sb) % vec) != 0 ||
       ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
         reinterpret_cast<uintptr_t>(out)) & 15) != 0)
@@ -1023,9 +1087,9 @@ extern "C" int motif_chord_fwd(
   const int group = H / Hkv;
   const int rows = group * L;
 
-  if (dtype == MOTIF_F32 || use_decode(H, Hkv, L, packed)) {
+  if (!mfma_path(dtype, D) || use_decode(H, Hkv, L, packed)) {
     if (S == 0) return set_error(MOTIF_ERR_INVALID, "chord_fwd: empty key cache");
-    const bool mfma = dtype == MOTIF_BF16;  // bf16 decode shapes: the MFMA kernel
+    const bool mfma = mfma_path(dtype, D);  // bf16 decode shapes at D = 64: the MFMA kernel
     int R = 8;
     if (rows <= 8) {
       R = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
@@ -1046,12 +1110,11 @@ extern "C" int motif_chord_fwd(
       rc = check_launch("chord_bias_table_kernel");
       if (rc) return rc;
     }
-    if (mfma) chord_decode_mfma_kernel<<<dim3(a.splits, Hkv, B * a.nqc), dim3(256), 0, s>>>(a);
-    else launch_decode<float>(a, R, tab, tn, s);
+    if (!mfma) return launch_vector_dt(dtype, a, R, D, tab, tn, s);
+    chord_decode_mfma_kernel<<<dim3(a.splits, Hkv, B * a.nqc), dim3(256), 0, s>>>(a);
     rc = check_launch("chord_decode_kernel");
     if (rc || a.splits == 1) return rc;
-    if (dtype == MOTIF_BF16) chord_merge_kernel<bf16_t><<<dim3(rows, Hkv, B), dim3(64), 0, s>>>(a);
-    else chord_merge_kernel<float><<<dim3(rows, Hkv, B), dim3(64), 0, s>>>(a);
+    chord_merge_kernel<bf16_t><<<dim3(rows, Hkv, B), dim3(64), 0, s>>>(a);
     return check_launch("chord_merge_kernel");
   }
 
@@ -1099,7 +1162,7 @@ extern "C" size_t motif_chord_decode_workspace_bytes(int B, int H, int Hkv, int 
   }
   const int sp = decode_splits(B, Hkv, capacity);
   if (splits) *splits = sp;
-  return decode_ws_bytes(B, H, Hkv, L, capacity, D, sp, dtype == MOTIF_F32);
+  return decode_ws_bytes(B, H, Hkv, L, capacity, D, sp, !mfma_path(dtype, D));
 }
 
 int motif::chord_decode_run(
@@ -1114,21 +1177,21 @@ int motif::chord_decode_run(
     void *workspace, size_t workspace_bytes, int dtype, void *stream) {
   if (B < 0 || H <= 0 || Hkv <= 0 || L < 0 || H % Hkv)
     return set_error(MOTIF_ERR_INVALID, "chord_decode: bad size");
-  if (D != kD) return set_error(MOTIF_ERR_UNSUPPORTED, "chord_decode: head_dim must be 64");
-  if (dtype != MOTIF_BF16 && dtype != MOTIF_F32)
-    return set_error(MOTIF_ERR_UNSUPPORTED, "chord_decode: dtype must be bf16 or fp32");
+  if (!head_dim_ok(D)) return set_error(MOTIF_ERR_UNSUPPORTED, "chord_decode: head_dim must be 16, 32, 64 or 128");
+  if (dtype != MOTIF_BF16 && dtype != MOTIF_F32 && dtype != MOTIF_F16)
+    return set_error(MOTIF_ERR_UNSUPPORTED, "chord_decode: dtype must be bf16, fp16 or fp32");
   if (B == 0 || L == 0) return MOTIF_OK;
   if (capacity < L) return set_error(MOTIF_ERR_INVALID, "chord_decode: capacity below the query count");
   if (!q || !k_cache || !v_cache || !length_dev || !alpha || !beta || !mu || !ssmax || !out)
     return set_error(MOTIF_ERR_INVALID, "chord_decode: NULL pointer");
   if (!log_n && (!log_table || log_table_len < capacity))
     return set_error(MOTIF_ERR_INVALID, "chord_decode: log_n is NULL and the log table is shorter than the capacity");
-  const int64_t vec = dtype == MOTIF_BF16 ? 8 : 4;
+  const int64_t vec = dtype == MOTIF_F32 ? 4 : 8;
   if (((q_st | k_st | v_st | o_st | q_sh | k_sh | v_sh | o_sh | q_sb | k_sb | v_sb | o_sb) % vec) != 0 ||
       ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k_cache) |
         reinterpret_cast<uintptr_t>(v_cache) | reinterpret_cast<uintptr_t>(out)) & 15) != 0)
     return set_error(MOTIF_ERR_UNSUPPORTED, "chord_decode: q/k/v/out need 16-byte aligned rows");
-  const bool fp32 = dtype == MOTIF_F32;
+  const bool fp32 = !mfma_path(dtype, D);  // the vector kernel (with its bias table)
   const int splits = decode_splits(B, Hkv, capacity);
   const size_t need = decode_ws_bytes(B, H, Hkv, L, capacity, D, splits, fp32);
   if (!workspace || workspace_bytes < need)
@@ -1159,14 +1222,12 @@ int motif::chord_decode_run(
     const int tn = table_len(capacity);
     chord_bias_table_kernel<<<dim3((tn + 255) / 256, H), dim3(256), 0, s>>>(a, tab, tn);
     if ((rc = check_launch("chord_bias_table_kernel"))) return rc;
-    launch_decode<float>(a, R, tab, tn, s);
-  } else {
-    a.nqc = (rows + kMfmaRows - 1) / kMfmaRows;
-    chord_decode_mfma_kernel<<<dim3(splits, Hkv, B * a.nqc), dim3(256), 0, s>>>(a);
+    return launch_vector_dt(dtype, a, R, D, tab, tn, s);  // its merge advances the cursor
   }
+  a.nqc = (rows + kMfmaRows - 1) / kMfmaRows;
+  chord_decode_mfma_kernel<<<dim3(splits, Hkv, B * a.nqc), dim3(256), 0, s>>>(a);
   if ((rc = check_launch("chord_decode_kernel"))) return rc;
-  if (fp32) chord_merge_kernel<float><<<dim3(rows, Hkv, B), dim3(64), 0, s>>>(a);
-  else chord_merge_kernel<bf16_t><<<dim3(rows, Hkv, B), dim3(64), 0, s>>>(a);
+  chord_merge_kernel<bf16_t><<<dim3(rows, Hkv, B), dim3(64), 0, s>>>(a);
   return check_launch("chord_merge_kernel");
 }
 

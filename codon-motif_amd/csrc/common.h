@@ -35,6 +35,12 @@ template <> struct Elem<bf16_t> {
   __device__ __forceinline__ static void store(bf16_t* p, float v) { *p = f32_to_bf16(v); }
 };
 
+typedef _Float16 f16_t;  // IEEE half
+template <> struct Elem<f16_t> {
+  __device__ __forceinline__ static float load(const f16_t* p) { return static_cast<float>(*p); }
+  __device__ __forceinline__ static void store(f16_t* p, float v) { *p = static_cast<f16_t>(v); }
+};
+
 template <typename T> __device__ __forceinline__ float ld(const T* p) { return Elem<T>::load(p); }
 template <typename T> __device__ __forceinline__ void st(T* p, float v) { Elem<T>::store(p, v); }
 

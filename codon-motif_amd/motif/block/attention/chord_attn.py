@@ -28,12 +28,13 @@ from motif.model.cache import KVLayerCache, StaticKVLayerCache, expand_kv_heads
 from motif.ops import RMSNorm, apply_chord_attention, apply_chord_attention_varlen
 from motif.ops import _lib
 from motif.ops.autograd_path import wants_grad
-from motif.ops.chord_attention import HEAD_DIM, chord_decode_cursor, chord_decode_workspace
+from motif.ops.chord_attention import HEAD_DIMS, chord_decode_cursor, chord_decode_workspace
 from motif.ops.epilogue import mul_sigmoid, usable
 from motif.ops.linear_rows import cat_weights, linear_rows, project, rows_eligible
 
 GGD_EPS = 1e-5
-_KERNEL_DTYPES = (torch.bfloat16, torch.float32)
+_KERNEL_DTYPES = (torch.bfloat16, torch.float32)  # the input kernel (norms, cache append)
+_ATTN_DTYPES = (torch.bfloat16, torch.float32, torch.float16)  # the attention kernels
 _DECODE_ROWS = 8  # (GQA group x L) up to this size is a decode-shaped call
 
 
@@ -130,7 +131,7 @@ class ChordAttention(BasicAttention):
         materialised path with a one-time warning.'''
         if not x.is_cuda:
             return False
-        if x.dtype in _KERNEL_DTYPES and self.head_dim == HEAD_DIM and _lib.available():
+        if x.dtype in _ATTN_DTYPES and self.head_dim in HEAD_DIMS and _lib.available():
             return True
         if not self._warned:
             warnings.warn(f'ChordAttention: no HIP kernel for {x.dtype} / head_dim {self.head_dim}; '

@@ -13,6 +13,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__
 
 MOTIF_F32 = 0
 MOTIF_BF16 = 1
+MOTIF_F16 = 2
 
 _I64 = ctypes.c_int64
 _I32 = ctypes.c_int
@@ -132,6 +133,13 @@ def check(rc: int, what: str):
     if rc == ERR_UNSUPPORTED:
         raise NotImplementedError(f'{what}: {msg}')
     raise RuntimeError(f'{what}: {msg}')
+
+
+def chord_dtype_code(dt: torch.dtype) -> int:
+    '''dtype code of the Chord attention entries, which also take fp16.'''
+    if dt == torch.float16:
+        return MOTIF_F16
+    return dtype_code(dt)
 
 
 def dtype_code(dt: torch.dtype) -> int:

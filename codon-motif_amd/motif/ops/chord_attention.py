@@ -20,7 +20,8 @@ import torch
 from . import _lib
 from .autograd_path import chord_attention_torch, chord_attention_varlen_torch, wants_grad
 
-HEAD_DIM = 64
+HEAD_DIM = 64                  # the model's head dim: bf16 runs on the MFMA kernels
+HEAD_DIMS = (16, 32, 64, 128)  # head dims the kernels serve (fp32 / fp16 / other D: the vector kernel)
 
 
 def _check_tensors(q, k, v, log_n):
@@ -77,13 +78,11 @@ def _launch(q, k, v, alpha, beta, mu, ssmax, log_n, q_start, scale, eps, out, ls
             cu_dev=None, nseq=None, max_seqlen=None):
     B, H, L, D = q.shape
     Hkv, S = k.shape[1], k.shape[2]
-    if q.dtype not in (torch.bfloat16, torch.float32):
-        raise NotImplementedError(
-            f'apply_chord_attention: the HIP kernels take bf16 or fp32 inputs; got {q.dtype}')
-    if cu_dev is not None and q.dtype != torch.bfloat16:
-        raise NotImplementedError('apply_chord_attention_varlen: packed sequences are implemented for bf16')
-    if D != HEAD_DIM:
-        raise NotImplementedError(f'apply_chord_attention: head_dim {D} unsupported (64 only)')
+    if D not in HEAD_DIMS:
+        raise NotImplementedError(f'apply_chord_attention: head_dim {D} unsupported (16, 32, 64 or 128)')
+    if cu_dev is not None and (q.dtype != torch.bfloat16 or D != HEAD_DIM):
+        raise NotImplementedError('apply_chord_attention_varlen: packed sequences are implemented for bf16, '
+                                  f'head_dim {HEAD_DIM}')
     q, k, v = _aligned(q), _aligned(k), _aligned(v)
     lib = _lib.lib()
     if cu_dev is None:
@@ -97,7 +96,7 @@ def _launch(q, k, v, alpha, beta, mu, ssmax, log_n, q_start, scale, eps, out, ls
         *_lib.t4(out), _lib.ptr(lse),
         B, H, Hkv, L, S, D, int(q_start), float(scale), float(eps),
         _lib.ptr(cu_dev), int(nseq), int(max_seqlen),
-        ws.data_ptr(), ws.numel(), _lib.dtype_code(q.dtype), _lib.stream_ptr(q.device))
+        ws.data_ptr(), ws.numel(), _lib.chord_dtype_code(q.dtype), _lib.stream_ptr(q.device))
     _lib.check(rc, 'motif_chord_fwd')
     return out
 
@@ -134,8 +133,8 @@ def apply_chord_attention(
 
     Raises:
         ValueError: on unsupported inputs or a negative q_start.
-        NotImplementedError: for fp16 inputs or D != 64 (inputs requiring grad take
-            the differentiable torch form).
+        NotImplementedError: for a head dim outside 16, 32, 64, 128 (inputs requiring
+            grad take the differentiable torch form).
         RuntimeError: when the HIP library is unavailable or a launch fails.
     '''
     if wants_grad(q, k, v, alpha, beta, mu, ssmax, log_n):
@@ -194,7 +193,7 @@ def apply_chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, log_n, cu_seql
 
 def chord_decode_workspace(B, H, Hkv, L, capacity, D, dtype, device) -> torch.Tensor:
     '''A workspace for chord_decode_cursor at these sizes.'''
-    n = _lib.lib().motif_chord_decode_workspace_bytes(B, H, Hkv, L, capacity, D, _lib.dtype_code(dtype), None)
+    n = _lib.lib().motif_chord_decode_workspace_bytes(B, H, Hkv, L, capacity, D, _lib.chord_dtype_code(dtype), None)
     return torch.empty(max(int(n), 1), dtype=torch.uint8, device=device)
 
 
@@ -227,7 +226,7 @@ def chord_decode_cursor(q, k_cache, v_cache, length_dev, alpha, beta, mu, ssmax,
             alpha.data_ptr(), beta.data_ptr(), mu.data_ptr(), ssmax.data_ptr(),
             _lib.ptr(log_n), ln_sb, ln_st, log_table.data_ptr(), log_table.numel(),
             *_lib.t4(out), B, H, Hkv, L, D, float(softmax_scale), float(eps),
-            _lib.dtype_code(q.dtype), _lib.stream_ptr(q.device))
+            _lib.chord_dtype_code(q.dtype), _lib.stream_ptr(q.device))
         _lib.check(rc, 'motif_chord_decode_noalloc')
         return out
     if workspace is None:
@@ -237,6 +236,6 @@ def chord_decode_cursor(q, k_cache, v_cache, length_dev, alpha, beta, mu, ssmax,
         alpha.data_ptr(), beta.data_ptr(), mu.data_ptr(), ssmax.data_ptr(),
         _lib.ptr(log_n), ln_sb, ln_st, log_table.data_ptr(), log_table.numel(),
         *_lib.t4(out), B, H, Hkv, L, D, float(softmax_scale), float(eps),
-        workspace.data_ptr(), workspace.numel(), _lib.dtype_code(q.dtype), _lib.stream_ptr(q.device))
+        workspace.data_ptr(), workspace.numel(), _lib.chord_dtype_code(q.dtype), _lib.stream_ptr(q.device))
     _lib.check(rc, 'motif_chord_decode')
     return out

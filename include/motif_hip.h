@@ -12,7 +12,8 @@
  *    host, nothing allocates device memory (scratch comes in as `workspace`).
  *  - Return value: MOTIF_OK (0) or a motif_status code; `motif_last_error()`
  *    returns a message for the last failure on the calling thread.
- *  - dtype codes: MOTIF_F32 = 0, MOTIF_BF16 = 1.
+ *  - dtype codes: MOTIF_F32 = 0, MOTIF_BF16 = 1, MOTIF_F16 = 2 (fp16: the Chord attention
+ *    entries only).
  *  - Recurrent state is always fp32, row-major [.., dk, dv], contiguous.
  */
 #ifndef MOTIF_HIP_H
@@ -32,7 +33,7 @@ enum motif_status {
   MOTIF_ERR_HIP = 3          /* a HIP runtime call failed */
 };
 
-enum motif_dtype { MOTIF_F32 = 0, MOTIF_BF16 = 1 };
+enum motif_dtype { MOTIF_F32 = 0, MOTIF_BF16 = 1, MOTIF_F16 = 2 };
 
 /* Version of this ABI (bumped on any signature change). */
 int motif_abi_version(void);

@@ -164,3 +164,36 @@ def test_varlen_long_sequences_split_keys():
     out = ops.apply_chord_attention_varlen(*(t.to(DEV) for t in (q, k, v, alpha, beta, mu, ssmax, log_n)), cu.to(DEV))
     ref = ochord.chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, cu, softmax_scale=64 ** -0.5)
     assert_bf16_close(out, ref, what='varlen long')
+
+
+# ---------------------------------------------------------------- fp16 and other head dims
+# The reference's apply_chord_attention takes fp16 / bf16 / fp32 and any head dim >= 16
+# (motif/ops/chord_attention.py:960-1034).  Here fp16, and D in {16, 32, 128} in every
+# dtype, run on the vector kernel (bf16 at D = 64 keeps the MFMA kernels).
+
+@pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize('D', [16, 32, 64, 128])
+@pytest.mark.parametrize('B,H,Hkv,L,S', [(2, 4, 2, 70, 70), (3, 6, 3, 1, 1500), (1, 4, 1, 9, 300)])
+def test_dtypes_and_head_dims(dtype, D, B, H, Hkv, L, S):
+    '''Prefill (L = S), decode (L = 1, split keys) and a short block over a longer cache,
+    against the fp64 oracle: fp32 within 1e-4; fp16 / bf16 within the bf16 bar.'''
+    ops = _ops()
+    q, k, v, alpha, beta, mu, ssmax = chord_inputs(B, H, Hkv, L, S, seed=D + L + S, D=D)
+    q, k, v = q.float().to(dtype), k.float().to(dtype), v.float().to(dtype)
+    mu = torch.linspace(-0.5, 0.5, H)
+    log_n = _log_n(B, L, S - L)
+    out = _run(ops, q, k, v, alpha, beta, mu, ssmax, log_n)
+    assert out.dtype == dtype and out.shape == (B, H, L, D)
+    ref = ochord.chord_attention(q.double(), k.double(), v.double(), alpha, beta, mu, ssmax, log_n, S - L)
+    if dtype == torch.float32:
+        err = (out.double().cpu() - ref).abs().max().item()
+        assert err <= 1e-4, err
+    else:
+        assert_bf16_close(out, ref, what=f'{dtype} D={D}')
+
+
+def test_unsupported_head_dim_raises_not_implemented():
+    ops = _ops()
+    q, k, v, alpha, beta, mu, ssmax = (t.to(DEV) for t in chord_inputs(1, 2, 1, 8, 8, D=48))
+    with pytest.raises(NotImplementedError):
+        ops.apply_chord_attention(q, k, v, alpha, beta, mu, ssmax, _log_n(1, 8, 0).to(DEV))

@@ -291,3 +291,50 @@ def test_gate_kernels_match_torch():
         gp = torch.randn(3, 5, 64, generator=g).to(DEV, dt)
         ref = x * torch.sigmoid(gp)
         assert (mul_sigmoid(x, gp).float() - ref.float()).abs().max().item() <= tol * 4
+
+
+@pytest.mark.parametrize('head_dim,dtype', [(32, torch.bfloat16), (128, torch.bfloat16), (64, torch.float16),
+                                            (32, torch.float32)])
+@torch.no_grad()
+def test_chord_layer_other_head_dims_and_fp16(head_dim, dtype):
+    '''ChordAttention with head dims 32 / 128 and fp16 runs on the kernels (no fallback
+    warning): prefill, then decode steps over a growing cache and over a fixed-capacity
+    cache (the device-cursor path), against the oracle layer run in float64.'''
+    import warnings
+    from motif.block.attention.chord_attn import ChordAttention
+    from motif.model.cache import KVLayerCache, StaticKVLayerCache
+    from oracle.chord import chord_layer
+    H, Hkv = 4, 2
+    hidden = H * head_dim
+    layer = ChordAttention(hidden_size=hidden, num_heads=H, num_kv_heads=Hkv)
+    fill_params(layer, 3)
+    layer = layer.to(DEV, dtype).eval()
+    p = {k: v.detach().double().cpu() for k, v in layer.state_dict().items()}
+    g = torch.Generator().manual_seed(11)
+    x = (torch.randn(2, 40, hidden, generator=g) * 0.5).to(dtype)
+    steps = (torch.randn(2, 3, hidden, generator=g) * 0.5).to(dtype)
+    with warnings.catch_warnings():
+        warnings.simplefilter('error', RuntimeWarning)
+        grow = KVLayerCache()
+        fixed = StaticKVLayerCache().allocate(2, Hkv, 64, head_dim, DEV, dtype)
+        outs = {'grow': [layer(x.to(DEV), past_key_value=grow).output],
+                'fixed': [layer(x.to(DEV), past_key_value=fixed).output]}
+        for i in range(3):
+            outs['grow'].append(layer(steps[:, i:i + 1].to(DEV), past_key_value=grow).output)
+            outs['fixed'].append(layer(steps[:, i:i + 1].to(DEV), past_key_value=fixed).output)
+    def oracle(dt):
+        pd = {k: v.to(dt) for k, v in p.items()}
+        r, kc, vc = chord_layer(x.to(dt), pd, H, Hkv)
+        rs = [r]
+        for i in range(3):
+            r, kc, vc = chord_layer(steps[:, i:i + 1].to(dt), pd, H, Hkv, kc, vc)
+            rs.append(r)
+        return torch.cat(rs, 1)
+    ref = oracle(torch.float64)
+    low = None if dtype == torch.float32 else oracle(dtype)
+    for name, o in outs.items():
+        got = torch.cat(o, 1)
+        if dtype == torch.float32:
+            assert_fp32_close(got, ref, 1e-4, f'{name} D={head_dim}')
+        else:
+            assert_bf16_layer_close(got, ref, low, f'{name} D={head_dim} {dtype}')
