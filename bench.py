@@ -19,8 +19,8 @@ Also reported in the same JSON line:
   (oracle/, float32, torch threads) on one config-3 forward.
 
 Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu]
-       python bench.py --kernels-only   # hot-path ops + a copy kernel of known size,
-                                        # the target of the rocprofv3 --pmc traffic runs
+       python bench.py --kernels-only   # hot-path ops + a copy of known size and the peak
+                                        # probes: the target of the rocprofv3 --pmc runs
 '''
 import argparse
 import json
@@ -468,6 +468,9 @@ def main():
         with torch.no_grad():
             kern = kernel_timings(dev)
             copy_calibration(dev)
+            # the probes of known rate: the copy scales the traffic counters, the MFMA
+            # loop marks a fully busy matrix pipe for the MFMA-busy counter
+            kern['peaks'] = measured_peaks(dev)
         print(json.dumps({k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                           for k, v in kern.items()}), flush=True)
         return

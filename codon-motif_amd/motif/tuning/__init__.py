@@ -1,6 +1,7 @@
 '''Library-GEMM tuning results for the shapes the model runs on hipBLASLt / rocBLAS
 (prefill projections at T = 4096, the vocabulary projection), produced on an MI355X
-by `tune_gemms.py` with PyTorch TunableOp.
+with PyTorch TunableOp (tuning enabled, each projection shape run once, the results
+file written by torch.cuda.tunable.write_file).
 
 `enable()` loads them read-only (no tuning at run time).  PyTorch checks the
 recorded PyTorch / HIP / hipBLASLt / rocBLAS versions and the GPU architecture
