@@ -358,7 +358,7 @@ def copy_calibration(dev, mib=256, reps=5):
 # rocprofv3 --pmc summary (FETCH_SIZE / WRITE_SIZE, copy-calibrated) of bench.py --kernels-only
 TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'hot_path_ops_hbm_traffic.txt')
 OP_KERNELS = {'gdn_chunk_prefill': ('gdn_prep_mfma', 'gdn_state_scan', 'gdn_chunk_out'),
-              'chord_prefill': ('chord_prefill_table_kernel', 'chord_fwd_kernel'),
+              'chord_prefill': ('chord_fwd_kernel',),
               'gdn_decode': ('gdn_decode_kernel',),
               'chord_decode': ('chord_decode_mfma_kernel', 'chord_merge_kernel')}
 

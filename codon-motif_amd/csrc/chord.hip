@@ -10,9 +10,10 @@
 // from the score accumulators (two 16-key tiles per 32-key MFMA step) and V^T
 // staged in LDS in the matching key order.  K / V tiles are double-buffered in
 // LDS, loaded through range-checked buffers, one barrier per 64-key tile.  The
-// GGD bias depends only on d = key - i_abs: each wave evaluates it once per tile
-// for the 79 distances of its 16x64 tile into 4 shifted LDS copies, so every
-// lane reads its 4 consecutive distances with one aligned 16-byte load.
+// GGD bias depends only on d = key - i_abs: each wave evaluates it in registers
+// once per tile for the 79 distances of its 16x64 tile (two per lane) into 4
+// shifted LDS copies, so every lane reads its 4 consecutive distances with one
+// aligned 16-byte load; no bias is stored in HBM.
 //
 // chord_decode_kernel (decode / short queries over a long cache): split-K
 // flash-decoding.  A workgroup owns (split, kv head, batch row) and serves all
@@ -103,29 +104,11 @@ __device__ __forceinline__ float max_lane_groups(float x) {
 
 constexpr int kRow = 72;  // LDS row stride (bf16) of the K and V^T tiles: 144 B rows
 
-// Per-head bias rows of the prefill kernel: tab[h][e] with e = key - q_abs + e0 holds
-// kappa_h * GGD(key - q_abs) for key <= q_abs and -inf for key > q_abs (the causal
-// mask), kappa_h = sign(ssmax_h) / |scale| (sign(ssmax_h) when scale == 0).  With q
-// multiplied by rho_h = sign(ssmax_h * scale) (0 when scale == 0) the MFMA that starts
-// from these entries yields acc = rho_h (q.k + bias / scale), and the logit is
+// Prefill logit form: q is multiplied by rho_h = sign(ssmax_h * scale) (exact; 0 when
+// scale == 0) and each S^T = K Q^T MFMA starts from kappa_h * GGD(key - q_abs) for
+// key <= q_abs (-inf above: the causal mask), kappa_h = sign(ssmax_h) / |scale|
+// (sign(ssmax_h) when scale == 0), so acc = rho_h (q.k + bias / scale) and the logit is
 // |ssmax_h log_n[i] scale| acc (|ssmax_h log_n[i]| acc when scale == 0).
-__global__ void __launch_bounds__(256) chord_prefill_table_kernel(ChordArgs a, float *tab, int len, int e0) {
-  const int h = blockIdx.y, e = blockIdx.x * 256 + threadIdx.x;
-  if (e >= len) return;
-  const int dist = e - e0;
-  float v = -INFINITY;
-  if (dist <= 0) {
-    const float sg = a.ssmax[h] < 0.f ? -1.f : 1.f;
-    const float kappa = a.scale != 0.f ? sg / fabsf(a.scale) : sg;
-    v = kappa * ggd_bias(static_cast<float>(dist), a.alpha[h], a.beta[h], a.mu[h], a.eps);
-  }
-  tab[static_cast<size_t>(h) * len + e] = v;
-}
-
-// Bias-row length for the largest q_abs e0: entries up to e0 + 78 are read (keys of a
-// 64-key tile reach 63 past the wave's last row, which is 15 past its first), the
-// 16-byte reads 3 more.
-__host__ __device__ constexpr int prefill_table_len(int e0) { return (e0 + 82 + 3) / 4 * 4; }
 
 // LDS tile rows of 64 bf16 (128 B) hold their eight 16-byte pieces in the order
 // piece ^ (row & 7): the row-per-lane 16-byte reads of the MFMA operands and the
@@ -144,7 +127,7 @@ __device__ __forceinline__ int swz(int row, int col) { return row * 64 + ((((col
 // dword loads per lane.  Tile data and windows are fetched two steps ahead: the
 // loads issued in step i are written to LDS at the end of step i + 1.
 template <int HPW>  // query heads per half (the rest of a half's 4 waves take query blocks)
-__global__ void __launch_bounds__(512) chord_fwd_kernel(ChordArgs a, const float *tab, int tab_len, int e0) {
+__global__ void __launch_bounds__(512) chord_fwd_kernel(ChordArgs a) {
   constexpr int QBPW = 4 / HPW;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -189,9 +172,8 @@ __global__ void __launch_bounds__(512) chord_fwd_kernel(ChordArgs a, const float
   const buf_t qbuf = make_buf(qp, Lq > 0 ? static_cast<uint32_t>(((Lq - 1) * a.q_st + kD) * 2) : 0u);
   const buf_t kbuf = make_buf(kp, kv_end > 0 ? static_cast<uint32_t>(((kv_end - 1) * a.k_st + kD) * 2) : 0u);
   const buf_t vbuf = make_buf(vp, kv_end > 0 ? static_cast<uint32_t>(((kv_end - 1) * a.v_st + kD) * 2) : 0u);
-  const buf_t tbuf = make_buf(tab + static_cast<size_t>(head) * tab_len, static_cast<uint32_t>(tab_len) * 4u);
 
-  // logit = a_row * acc (see chord_prefill_table_kernel), a_row = |ssmax log_n scale|;
+  // logit = a_row * acc (the prefill logit form above), a_row = |ssmax log_n scale|;
   // the kernel works in log2 units, p = exp2(A (acc - m)) with A = log2e a_row.
   const float ssm = a.ssmax[head];
   const float sg = ssm < 0.f ? -1.f : 1.f;
@@ -216,17 +198,20 @@ __global__ void __launch_bounds__(512) chord_fwd_kernel(ChordArgs a, const float
   __shared__ __attribute__((aligned(16))) bf16_t sV[2][2][kD * kBN];   // V^T rows, keys in vperm order (swizzled)
   __shared__ __attribute__((aligned(16))) float sB[8][4 * 80];         // per wave: 4 shifted bias windows
 
-  // Bias window of tile t: entries wbase(t) + j, j = 0..78, of the head's row, where
-  // entry j serves key n0 + 16 kt + 4 g + r of row ln with j = 16 kt + 4 g + r + 15 - ln
-  // (table index key - q_abs + e0).  Lane l fetches entries l and 64 + l; an offset
-  // below the row start wraps past its end and reads 0 (only invalid rows read it).
-  const uint32_t woff = 4u * static_cast<uint32_t>(-q_start - q0 + e0 - 15 + lane);
-  float bwin[2];
-  auto load_window = [&](int t) {
-    const uint32_t o = woff + 4u * static_cast<uint32_t>(t * kBN);
-    bwin[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(tbuf, o, 0, 0));
-    bwin[1] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(tbuf, o + 256u, 0, 0));
+  // Bias window of tile t: entry j (0..78) serves key n0 + 16 kt + 4 g + r of row ln with
+  // j = 16 kt + 4 g + r + 15 - ln, i.e. distance key - q_abs = t kBN - q_start - q0 - 15 + j.
+  // Lane l computes entries l and 64 + l in registers: kappa * GGD(distance) for
+  // distance <= 0 and -inf past the diagonal (the causal mask), kappa = sign(ssmax) /
+  // |scale| (sign(ssmax) when scale == 0).  Nothing of the bias is stored in HBM.
+  const float g_alpha = a.alpha[head], g_beta = a.beta[head], g_mu = a.mu[head];
+  const float kappa = a.scale != 0.f ? sg / fabsf(a.scale) : sg;
+  const int dist0 = -q_start - q0 - 15 + lane;
+  // Entry 64 + l of tile t is entry l of tile t + 1, so after the first tile each
+  // step evaluates one new distance per lane and shifts the other.
+  auto eval_bias = [&](int dist) {
+    return dist <= 0 ? kappa * ggd_bias(static_cast<float>(dist), g_alpha, g_beta, g_mu, a.eps) : -INFINITY;
   };
+  float bwin[2] = {eval_bias(t_first * kBN + dist0), eval_bias(t_first * kBN + dist0 + 64)};
   // Copy c (80 floats; a stride of 20 16-byte units keeps the reads free of bank
   // conflicts) holds entry j at position j - c.  Reads stay at positions <= 75; the
   // stores of entries no lane reads (lane < c, lane 15) land at positions >= 76 of
@@ -301,11 +286,9 @@ __global__ void __launch_bounds__(512) chord_fwd_kernel(ChordArgs a, const float
   // Prologue: tile and window of the first step in LDS, the second step's in flight.
   // Every load and store of the loop is unconditional (tiles and entries past the end
   // read zeros through the range checks), so the wait counts are path independent.
-  load_window(t_first);
   load_tile(t_first);
   store_tile(std::integral_constant<int, 0>());
   store_window();
-  load_window(t_first + 1);
   load_tile(t_first + 1);
   __syncthreads();
 
@@ -314,6 +297,8 @@ __global__ void __launch_bounds__(512) chord_fwd_kernel(ChordArgs a, const float
   auto step = [&](int i, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
     const int n0 = (t_first + i) * kBN;
+    // the new entry of the next step's window, evaluated ahead of this step's work
+    const float bnew = eval_bias(n0 + 2 * kBN + dist0);
     if (i < t_count && n0 < wave_kv_end) {
       // acc^T = bias + rho K Q^T: tile kt holds key n0 + 16 kt + 4g + r of row ln.
       f32x4 sacc[4];
@@ -376,11 +361,12 @@ __global__ void __launch_bounds__(512) chord_fwd_kernel(ChordArgs a, const float
       }
     }
 
-    // The next step's window and tile (fetched one step ago) into LDS, the one after
+    // The next step's window and tile (fetched one step ago) into LDS, the tile after
     // into flight.  The window region is this wave's own (its reads above come first
     // in program order); the tile buffer was last read before the previous barrier.
+    bwin[0] = bwin[1];
+    bwin[1] = bnew;
     store_window();
-    load_window(t_first + i + 2);
     store_tile(std::integral_constant<int, buf ^ 1>());
     load_tile(t_first + i + 2);
     __syncthreads();
@@ -1014,9 +1000,6 @@ static size_t table_bytes(int H, int S) {
   return (static_cast<size_t>(H) * table_len(S) * sizeof(float) + 255) / 256 * 256;
 }
 
-static size_t prefill_table_bytes(int H, int e0) {
-  return (static_cast<size_t>(H) * prefill_table_len(e0) * sizeof(float) + 255) / 256 * 256;
-}
 
 }  // namespace motif
 
@@ -1028,10 +1011,9 @@ extern "C" size_t motif_chord_workspace_bytes(int B, int H, int Hkv, int L, int 
     sp = decode_splits(B, Hkv, S);
   if (splits) *splits = sp;
   if (B <= 0 || H <= 0 || Hkv <= 0 || L <= 0) return 0;
-  // the distance table of the vector kernel (decode shapes and fp32 inputs), or the
-  // bias rows of the bf16 prefill kernel sized for any q_start <= S (largest q_abs
-  // S + L - 1); both are small, so the larger is always included
-  size_t n = std::max(table_bytes(H, S), prefill_table_bytes(H, S + L - 1));
+  // the distance table of the vector kernel (decode shapes and fp32 / fp16 / other head
+  // dims); the bf16 prefill kernel evaluates its bias in registers and needs none
+  size_t n = table_bytes(H, S);
   if (sp > 1) n += static_cast<size_t>(B) * Hkv * sp * (static_cast<size_t>(H / Hkv) * L) * (D + 2) * sizeof(float);
   return n;
 }
@@ -1122,22 +1104,13 @@ extern "C" int motif_chord_fwd(
   const int qbpw = 4 / hpw;
   const int maxlen = packed ? max_seqlen : L;
   if (maxlen <= 0) return MOTIF_OK;
-  // bias rows up to the largest query position (packed: positions restart per sequence)
-  const int64_t e0l = packed ? static_cast<int64_t>(max_seqlen) - 1 : std::max<int64_t>(S, int64_t(q_start) + L) - 1;
-  if (e0l > (int64_t(1) << 28)) return set_error(MOTIF_ERR_UNSUPPORTED, "chord_fwd: sequence too long");
-  const int e0 = static_cast<int>(e0l), tl = prefill_table_len(e0);
-  const size_t need = prefill_table_bytes(H, e0);
-  if (!workspace || workspace_bytes < need)
-    return set_error(MOTIF_ERR_INVALID, "chord_fwd: workspace too small (need " + std::to_string(need) + " bytes)");
-  float *tab = static_cast<float *>(workspace);
-  chord_prefill_table_kernel<<<dim3((tl + 255) / 256, H), dim3(256), 0, s>>>(a, tab, tl, e0);
-  const int rc = check_launch("chord_prefill_table_kernel");
-  if (rc) return rc;
+  if (std::max<int64_t>(S, int64_t(q_start) + L) > (int64_t(1) << 28))
+    return set_error(MOTIF_ERR_UNSUPPORTED, "chord_fwd: sequence too long");
   const int nqbg = (maxlen + 16 * qbpw - 1) / (16 * qbpw);
   dim3 grid(nqbg, H / hpw, packed ? nseq : B), block(512);
-  if (hpw == 4) chord_fwd_kernel<4><<<grid, block, 0, s>>>(a, tab, tl, e0);
-  else if (hpw == 2) chord_fwd_kernel<2><<<grid, block, 0, s>>>(a, tab, tl, e0);
-  else chord_fwd_kernel<1><<<grid, block, 0, s>>>(a, tab, tl, e0);
+  if (hpw == 4) chord_fwd_kernel<4><<<grid, block, 0, s>>>(a);
+  else if (hpw == 2) chord_fwd_kernel<2><<<grid, block, 0, s>>>(a);
+  else chord_fwd_kernel<1><<<grid, block, 0, s>>>(a);
   return check_launch("chord_fwd_kernel");
 }
 
