@@ -11,21 +11,24 @@
 //   O'  = Attn U                      (C x dv)
 // so that for the state S_n entering chunk n
 //   S_{n+1} = A_n S_n + H_n,   O_n = O' + Q' S_n.
-// gdn_state_scan carries S across the chunks, one workgroup per (16 state columns,
-// head, sequence) with one wave per 16-row tile of S in accumulator registers (the
-// tiles meet in LDS once per chunk) and a six-chunk-deep register prefetch of
-// A_n / H_n (the workgroups of one head share an XCD, so A_n is read from HBM once
-// and from that XCD's L2 after); it writes every S_n as MFMA operands.  gdn_chunk_out then
-// forms O_n = O' + Q' S_n for all chunks in parallel.
+// gdn_state_scan carries S across the chunks, one wavefront per (16 state columns,
+// head, sequence) holding all dk rows of its columns in accumulator registers (the
+// columns of S evolve independently, so no wavefront waits on another), with a
+// register prefetch of A_n / H_n several chunks deep (the wavefronts of one head share
+// an XCD, so A_n is read from HBM once and from that XCD's L2 after); it writes every
+// S_n as MFMA operands.  gdn_chunk_out then forms O_n = O' + Q' S_n for all chunks in
+// parallel, with the GatedRMSNorm of each head row fused.
 //
-// The workspace holds A_n, Q', H_n, O' and S_n in the order the consuming kernel's
-// lanes read them (one 16-byte piece per lane per operand tile), so every load of
-// the two scan kernels is a coalesced 1 KB wavefront access with no LDS staging.
+// The workspace holds A_n, Q', H_n, O' and S_n as bf16 in the order the consuming
+// kernel's lanes read them (one 8- or 16-byte piece per lane per operand tile), so
+// every load of the two later kernels is a coalesced wavefront access with no LDS
+// staging.  Rounding these five to bf16 moves the output by about 2^-9 of its size
+// and the final state by ~2e-3 (relative), inside the bf16 bar.
 //
-// Inputs are bf16 (exact as MFMA operands).  fp32-derived operands (T, N, Attn, K~,
-// M, A_n, Q', the state) are split into bf16 hi + lo and their products take three
-// MFMA passes (hi.hi + hi.lo + lo.hi, fp32 accumulation), products with an exact
-// bf16 operand two: about 16 mantissa bits per product, fp32 accumulation throughout.
+// Inputs are bf16 (exact as MFMA operands).  Inside the prep, fp32-derived operands
+// (T, N, Attn, K~, M) are split into bf16 hi + lo and their products take three MFMA
+// passes (hi.hi + hi.lo + lo.hi, fp32 accumulation), products with an exact bf16
+// operand two: about 16 mantissa bits per product, fp32 accumulation throughout.
 #include <algorithm>
 #include <cstdlib>
 
@@ -77,23 +80,24 @@ template <typename T> __device__ __forceinline__ float ldf(const T *p) { return 
 
 template <bool B> struct BoolC { static constexpr bool value = B; };
 
-// Workspace per (head, chunk) cell, every piece 16 bytes per lane of a 64-lane tile:
-//   an [2 planes][DK/16 mt][DK/32 ks][64]  bf16x8  A_n rows 16 mt + (l % 16), k slots
-//                                                  32 ks + 4 (l / 16) + {0..3, 16..19}
-//   qp [2][4][DK/32][64]                   bf16x8  Q' in the same operand order
-//   hn [dv/16 cg][DK/16 mt][64]            f32x4   H_n[16 mt + 4 (l / 16) + r][16 cg + l % 16]
-//   op [dv/16 cg][4 mt][64]                f32x4   O'[16 mt + l % 16][16 cg + 4 (l / 16) + r]
-//   sn [dv/16 cg][DK/32 ks][2 planes][64]  bf16x8  S_n rows 32 ks + 4 (l / 16) + {0..3, 16..19},
-//                                                  column 16 cg + l % 16
+// Workspace per (head, chunk) cell, bf16, every piece 8 or 16 bytes per lane of a
+// 64-lane tile:
+//   an [DK/16 mt][DK/32 ks][64]   bf16x8  A_n rows 16 mt + (l % 16), k slots
+//                                         32 ks + 4 (l / 16) + {0..3, 16..19}
+//   qp [4 mt][DK/32 ks][64]       bf16x8  Q' in the same operand order
+//   hn [dv/16 cg][DK/16 mt][64]   bf16x4  H_n[16 mt + 4 (l / 16) + r][16 cg + l % 16]
+//   op [dv/16 cg][4 mt][64]       bf16x4  O'[16 mt + l % 16][16 cg + 4 (l / 16) + r]
+//   sn [dv/16 cg][DK/32 ks][64]   bf16x8  S_n rows 32 ks + 4 (l / 16) + {0..3, 16..19},
+//                                         column 16 cg + l % 16
 struct WsLayout {
   size_t an, qp, hn, op, sn, cell;
   __host__ __device__ WsLayout(int dk, int dv) {
     an = 0;
-    qp = an + 2ull * dk * dk * 2;
-    hn = qp + 2ull * kC * dk * 2;
-    op = hn + 4ull * dk * dv;
-    sn = op + 4ull * kC * dv;
-    cell = sn + 4ull * dk * dv;
+    qp = an + 2ull * dk * dk;
+    hn = qp + 2ull * kC * dk;
+    op = hn + 2ull * dk * dv;
+    sn = op + 2ull * kC * dv;
+    cell = sn + 2ull * dk * dv;
   }
 };
 
@@ -162,41 +166,48 @@ __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
 }
 __device__ __forceinline__ uint16_t bits(__bf16 x) { return __builtin_bit_cast(uint16_t, x); }
 
-// Byte offsets of the prep kernel's LDS.  Phase 7 (the operator products) keeps
-//   att hi/lo  [64][64]   Attn = (Q K^T) * D, rows i', columns i
-//   tt  hi/lo  [64][64]   T^T, rows j, columns i
-//   kt         [DK][64]   K^T (exact), vt [DV][64] V^T (exact), ktt hi/lo [DK][64] K~^T
-// Phases 1-5 use the kt.. region for K and Q rows (padded, row-major) and NT, one fp32
-// [64][68] array holding N = strict(beta K K^T * D) below the diagonal and T^T on and
-// above it; the level-2 product Y^T lives in the tt region until T^T is written there.
+// Byte offsets of the prep kernel's LDS (planes of [rows][64] bf16 are swizzled, swz):
+//   A: [K rows | spare | Q rows | K^T] 8 KB each.  The K and Q rows and the exact K^T
+//      plane are written in phase 1; after phase 2 the exact V^T plane [DV][64] goes
+//      over the K rows and the spare piece.  The Q rows stay for phase 7 (Q').
+//   B: NT, one fp32 [64][68] array holding N = strict(beta K K^T * D) below the
+//      diagonal and T^T on and above it (phases 2-6), then T^T as bf16 hi / lo planes
+//      [64][64], rows j, columns i (phases 6-7).
+// 49.5 KB at dk = 64, dv = 128: three workgroups per CU.
 template <int DK, int DV>
 struct PrepLayout {
   static constexpr int kPlane = 64 * 64 * 2;
-  static constexpr int att_h = 0, att_l = kPlane, tt_h = 2 * kPlane, tt_l = 3 * kPlane;
-  static constexpr int base = 4 * kPlane;
-  static constexpr int kt = base, vt = kt + DK * 128, ktt_h = vt + DV * 128, ktt_l = ktt_h + DK * 128;
-  static constexpr int end7 = ktt_l + DK * 128;
-  static constexpr int kRow = DK + kPad;  // K / Q rows (bf16 elements)
-  static constexpr int kh = base, qh = kh + 64 * kRow * 2, nt = qh + 64 * kRow * 2;
-  static constexpr int end1 = nt + 64 * 68 * 4;
-  static constexpr int yt = tt_h;  // [32][36] fp32
-  static constexpr int small = end7 > end1 ? end7 : end1;  // gam[64], beta[64]
+  static constexpr int kh = 0, vt = 0, qh = 2 * kPlane, kt = 3 * kPlane;
+  static_assert(DV * 128 <= 2 * kPlane && DK * 128 <= kPlane, "V^T / K^T planes exceed their pieces");
+  static constexpr int nt = 4 * kPlane, tt_h = nt, tt_l = nt + kPlane;
+  static constexpr int small = nt + (64 * 68 * 4 > 2 * kPlane ? 64 * 68 * 4 : 2 * kPlane);  // gam[64], beta[64]
   static constexpr int bytes = small + 2 * 64 * 4;
 };
 
+// v_mfma_f32_32x32x16_bf16: A lane l holds row l % 32, k 8 (l / 32) + 0..7; B lane l
+// column l % 32, the same k; accumulator register r of lane l holds row
+// 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
+__device__ __forceinline__ f32x16 mma32(const bf16x8 &a, const bf16x8 &b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+// The 16 k of one 32x32x16 step as an operand built from accumulator rows: slot s of
+// lane half h stands for k = 16 ks + 8 (s / 4) + 4 h + s % 4, so a B operand comes
+// straight from accumulator registers 8 (ks % 2) .. +7 of the same lane.  A row-major
+// LDS operand in that order is two 8-byte reads, columns 16 ks + 4 h and + 8.
+__device__ __forceinline__ bf16x8 rd_pair_s(const __bf16 *p, int row, int c0) {
+  return __builtin_shufflevector(rd4s(p, row, c0), rd4s(p, row, c0 + 8), 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
 template <int DK, int DV, bool FRONT>
-__global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca, char *ws, FrontArgs fa) {
+__global__ void __launch_bounds__(256, 3) gdn_prep_mfma(GdnArgs a, ChunkArgs ca, char *ws, FrontArgs fa) {
   using TI = bf16_t;
   using PL = PrepLayout<DK, DV>;
   constexpr int NTS = 68;  // NT row stride (floats)
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  __bf16 *att_h = reinterpret_cast<__bf16 *>(smem + PL::att_h), *att_l = reinterpret_cast<__bf16 *>(smem + PL::att_l);
   __bf16 *tt_h = reinterpret_cast<__bf16 *>(smem + PL::tt_h), *tt_l = reinterpret_cast<__bf16 *>(smem + PL::tt_l);
   __bf16 *kt = reinterpret_cast<__bf16 *>(smem + PL::kt), *vt = reinterpret_cast<__bf16 *>(smem + PL::vt);
-  __bf16 *ktt_h = reinterpret_cast<__bf16 *>(smem + PL::ktt_h), *ktt_l = reinterpret_cast<__bf16 *>(smem + PL::ktt_l);
   __bf16 *kh = reinterpret_cast<__bf16 *>(smem + PL::kh), *qh = reinterpret_cast<__bf16 *>(smem + PL::qh);
   float *nt = reinterpret_cast<float *>(smem + PL::nt);
-  float *yt = reinterpret_cast<float *>(smem + PL::yt);
   float *gam = reinterpret_cast<float *>(smem + PL::small), *bet = gam + 64;
 
   const int chunk = blockIdx.x, h = blockIdx.y;
@@ -209,7 +220,6 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
   const int kp = tid & 31, kseg = tid >> 5;
   const bool kval = kseg < KSEG;
   uint4 k0r = {}, k1r = {}, v0r[VP], v1r[VP];
-  bf16x4 qe[DK / 16];
   constexpr int RQ = DK / 8, RV = DV / 16, RM = RQ > RV ? RQ : RV;
   uint32_t cv[RM][4];  // FRONT: this thread's conv outputs, bf16 channel pairs per row
   int f_seg = 0, f_r0 = 0;
@@ -242,10 +252,6 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
       v0r[r] = buf_ld16(vbuf, ((2 * vp) * a.v_st + vc) * 2);
       v1r[r] = buf_ld16(vbuf, ((2 * vp + 1) * a.v_st + vc) * 2);
     }
-    // Q rows of this wavefront's Q' row tile (tile w): Q[16 w + ln][16 dt + 4g .. +3].
-#pragma unroll
-    for (int dt = 0; dt < DK / 16; ++dt)
-      qe[dt] = __builtin_bit_cast(bf16x4, buf_ld8(qbuf, ((16 * w + ln) * a.q_st + 16 * dt + 4 * g) * 2));
     if (w == 0) {  // the inclusive prefix sum of g
       float s = gv;
 #pragma unroll
@@ -257,10 +263,15 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
       bet[lane] = bv;
     }
     if (kval) {
-      *reinterpret_cast<uint4 *>(kh + (2 * kp) * PL::kRow + 8 * kseg) = k0r;
-      *reinterpret_cast<uint4 *>(kh + (2 * kp + 1) * PL::kRow + 8 * kseg) = k1r;
-      *reinterpret_cast<uint4 *>(qh + (2 * kp) * PL::kRow + 8 * kseg) = q0r;
-      *reinterpret_cast<uint4 *>(qh + (2 * kp + 1) * PL::kRow + 8 * kseg) = q1r;
+      *reinterpret_cast<uint4 *>(kh + swz(2 * kp, 8 * kseg)) = k0r;
+      *reinterpret_cast<uint4 *>(kh + swz(2 * kp + 1, 8 * kseg)) = k1r;
+      *reinterpret_cast<uint4 *>(qh + swz(2 * kp, 8 * kseg)) = q0r;
+      *reinterpret_cast<uint4 *>(qh + swz(2 * kp + 1, 8 * kseg)) = q1r;
+      // the K^T plane (its own region) from the same registers
+      const bf16x8 ka = __builtin_bit_cast(bf16x8, k0r), kb_ = __builtin_bit_cast(bf16x8, k1r);
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        *reinterpret_cast<uint32_t *>(kt + swz(8 * kseg + t, 2 * kp)) = pack2(bits(ka[t]), bits(kb_[t]));
     }
   
   } else {
@@ -359,8 +370,20 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
 #pragma unroll
         for (int e = 0; e < 4; ++e) cv[i][e] = pk_bf16(v[2 * e], v[2 * e + 1]);
         if (prob < 2)
-          *reinterpret_cast<uint4 *>((prob == 0 ? qh : kh) + (f_r0 + i) * PL::kRow + 8 * f_seg) =
+          *reinterpret_cast<uint4 *>((prob == 0 ? qh : kh) + swz(f_r0 + i, 8 * f_seg)) =
               uint4{cv[i][0], cv[i][1], cv[i][2], cv[i][3]};
+      }
+    }
+    if (w == 1) {  // the K^T plane (its own region) from this thread's K rows, in pairs
+#pragma unroll
+      for (int i = 0; i < RQ; i += 2) {
+        const int j = f_r0 + i;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint16_t b0 = static_cast<uint16_t>(cv[i][e >> 1] >> (16 * (e & 1)));
+          const uint16_t b1 = static_cast<uint16_t>(cv[i + 1][e >> 1] >> (16 * (e & 1)));
+          *reinterpret_cast<uint32_t *>(kt + swz(8 * f_seg + e, j)) = pack2(b0, b1);
+        }
       }
     }
     // gates of the chunk's rows (zero past len, as the unfused loads read them)
@@ -405,60 +428,82 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
     }
   }
   __syncthreads();
-  if constexpr (FRONT) {
-#pragma unroll
-    for (int dt = 0; dt < DK / 16; ++dt)
-      qe[dt] = *reinterpret_cast<const bf16x4 *>(qh + (16 * w + ln) * PL::kRow + 16 * dt + 4 * g);
-  }
 
-  // ---- phase 2: G = K K^T -> N, and K Q^T -> Attn, on 16x16 tiles (bi <= bj).
-  // Tile (bi, bj) of G holds G[16 bi + 4g + r][16 bj + ln] = G[16 bj + ln][16 bi + 4g + r]
-  // (symmetric), i.e. N row 16 bj + ln, columns 16 bi + 4g .. +3: one float4 per lane.
-  // Tile (bi, bj) of K Q^T holds (Q K^T)[16 bj + ln][16 bi + 4g + r]: Attn row 16 bj + ln.
-  // Wave w takes Attn row block w and N row block 3 - w (all four column blocks, the
-  // ones above the diagonal masked to zero); operand reads are issued before the products.
-  {
-    const int ba = w, bn = 3 - w;
-    bf16x8 kop[4][DK / 32], qop[DK / 32], nop[DK / 32];
+  // ---- phase 2 on 32x32x16 products (k = the dk columns of the K / Q rows in LDS).
+  // Waves 0, 1: N = strict(beta K K^T * D), rows 32 w .. +31, into NT (the tile right
+  // of the diagonal block is zero and skipped; entries on and above the diagonal are
+  // written as zeros, where T goes later).  Waves 2, 3: Attn^T = (K Q^T) * D^T for the
+  // 32 queries m = 32 (w - 2) + l % 32, kept in registers as the hi / lo B operands
+  // of phase 7 (k = key row i, in the slot order of rd_pair_s), plus the Q row pieces
+  // that Q' needs.
+  const int lc = lane & 31, hh = lane >> 5;
+  bf16x8 ath[4], atl[4];    // Attn^T B operands, k-step ks
+  if (w < 2) {
+    const int i0 = 32 * w;
+    for (int jt = 0; jt <= w; ++jt) {
+      f32x16 acc = {};
 #pragma unroll
-    for (int ks = 0; ks < DK / 32; ++ks) {
-      const int k0 = 32 * ks + 8 * g;
+      for (int kd = 0; kd < DK / 16; ++kd)
+        acc = mma32(rd8s(kh, i0 + lc, 16 * kd + 8 * hh), rd8s(kh, 32 * jt + lc, 16 * kd + 8 * hh), acc);
+      const int j = 32 * jt + lc;
+      const float gj = gam[j];
 #pragma unroll
-      for (int bi = 0; bi < 4; ++bi) kop[bi][ks] = rd8(kh + (16 * bi + ln) * PL::kRow, k0);
-      qop[ks] = rd8(qh + (16 * ba + ln) * PL::kRow, k0);
-      nop[ks] = rd8(kh + (16 * bn + ln) * PL::kRow, k0);
-    }
-    f32x4 at[4], nt4[4];
-#pragma unroll
-    for (int bi = 0; bi < 4; ++bi) {
-      at[bi] = f32x4{0.f, 0.f, 0.f, 0.f};
-      nt4[bi] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < DK / 32; ++ks) {  // tiles above the diagonal are masked below
-        at[bi] = mma(kop[bi][ks], qop[ks], at[bi]);
-        nt4[bi] = mma(kop[bi][ks], nop[ks], nt4[bi]);
+      for (int r = 0; r < 16; ++r) {
+        const int i = i0 + 8 * (r >> 2) + 4 * hh + (r & 3);
+        const float val = bet[i] * acc[r] * exp_fast(gam[i] - gj);
+        nt[i * NTS + j] = j < i ? val : 0.f;
       }
     }
-    const int rowa = 16 * ba + ln, rown = 16 * bn + ln;
-    const float ga = gam[rowa], gn = gam[rown], bn_ = bet[rown];
+  } else {
+    const int m = 32 * (w - 2) + lc;
+    const float gm = gam[m];
 #pragma unroll
-    for (int bi = 0; bi < 4; ++bi) {
-      const int col = 16 * bi + 4 * g;
-      float x[4];
+    for (int it = 0; it < 2; ++it) {
+      f32x16 acc = {};
+      if (it <= w - 2) {  // key tiles past the query tile are masked whole
 #pragma unroll
-      for (int r = 0; r < 4; ++r) x[r] = (col + r <= rowa) ? at[bi][r] * exp_fast(ga - gam[col + r]) : 0.f;
-      bf16x4 hv, lv;
-      split4(x, hv, lv);
-      *reinterpret_cast<bf16x4 *>(att_h + swz(rowa, col)) = hv;
-      *reinterpret_cast<bf16x4 *>(att_l + swz(rowa, col)) = lv;
-      // (the zeros written above the diagonal land where T is written later)
-      f32x4 y;
+        for (int kd = 0; kd < DK / 16; ++kd)
+          acc = mma32(rd8s(kh, 32 * it + lc, 16 * kd + 8 * hh), rd8s(qh, m, 16 * kd + 8 * hh), acc);
+      }
+      float x[16];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) y[r] = (col + r < rown) ? bn_ * nt4[bi][r] * exp_fast(gn - gam[col + r]) : 0.f;
-      *reinterpret_cast<f32x4 *>(nt + rown * NTS + col) = y;
+      for (int r = 0; r < 16; ++r) {
+        const int i = 32 * it + 8 * (r >> 2) + 4 * hh + (r & 3);
+        const float val = acc[r] * exp_fast(gm - gam[i]);
+        x[r] = i <= m ? val : 0.f;
+      }
+      split8(x, ath[2 * it], atl[2 * it]);
+      split8(x + 8, ath[2 * it + 1], atl[2 * it + 1]);
     }
   }
   __syncthreads();
+
+  // ---- V^T plane over the dead K rows and the spare piece (read in phase 7 only,
+  // after several barriers), freeing the registers that hold V.
+  if constexpr (!FRONT) {
+#pragma unroll
+    for (int r = 0; r < VP; ++r) {
+      const int vp = tid & 31, vs = (tid >> 5) + 8 * r;
+      if (vs < a.dv / 8) {
+        const bf16x8 va = __builtin_bit_cast(bf16x8, v0r[r]), vb_ = __builtin_bit_cast(bf16x8, v1r[r]);
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+          *reinterpret_cast<uint32_t *>(vt + swz(8 * vs + t, 2 * vp)) = pack2(bits(va[t]), bits(vb_[t]));
+      }
+    }
+  
+  } else if (w >= 2) {  // V^T plane
+#pragma unroll
+    for (int i = 0; i < RV; i += 2) {
+      const int j = f_r0 + i;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint16_t b0 = static_cast<uint16_t>(cv[i][e >> 1] >> (16 * (e & 1)));
+        const uint16_t b1 = static_cast<uint16_t>(cv[i + 1][e >> 1] >> (16 * (e & 1)));
+        *reinterpret_cast<uint32_t *>(vt + swz(8 * f_seg + e, j)) = pack2(b0, b1);
+      }
+    }
+  }
 
   // ---- phase 3: diagonal 16x16 blocks of T = (I + N)^{-1} by forward substitution,
   // wave w -> block w, lane c < 16 -> column c; T[16w + i][16w + c] goes to NT row 16w + c.
@@ -520,42 +565,47 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
   __syncthreads();
 
   // ---- phase 5: the 64x64 inverse: T[32:, :32] = -T[32:, 32:] N[32:, :32] T[:32, :32].
+  // Wave w = (ti, tj) forms both row tiles of column tile tj of Y = N[32:, :32] T[:32, :32]
+  // itself, so the second product takes Y from its own registers (k in the slot order
+  // {4g .. 4g + 3, 16 + 4g .. + 3}), with no exchange.  Phase 5 reads NT rows 32.. and
+  // the block T[:32, :32] and writes only the block T[32:, :32] (NT rows 0-31, columns
+  // 32-63), so it needs no barrier inside.
   {
     const int ti = w >> 1, tj = w & 1;
-    // Y = N[32:, :32] T[:32, :32], tile (ti, tj), K = 32.
-    float av[8], bv[8];
-    {
-      const float *nrow = nt + (32 + 16 * ti + ln) * NTS + 8 * g;
+    f32x4 y[2];
+#pragma unroll
+    for (int yi = 0; yi < 2; ++yi) {
+      float av[8], bv[8];
+      const float *nrow = nt + (32 + 16 * yi + ln) * NTS + 8 * g;
       const float *trow = nt + (16 * tj + ln) * NTS + 8 * g;  // T[8g + t][16 tj + ln]
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
         av[t] = nrow[t];
         bv[t] = (8 * g + t >= 16 * tj + ln) ? trow[t] : 0.f;
       }
+      bf16x8 ah, al, bh, bl;
+      split8(av, ah, al);
+      split8(bv, bh, bl);
+      y[yi] = mma3<true, true>(ah, al, bh, bl, f32x4{0.f, 0.f, 0.f, 0.f});  // Y[16 yi + 4g + r][16 tj + ln]
+    }
+    // T[32 + 16 ti + m][16 tj + n] = -sum_k T[32 + 16 ti + m][32 + k] Y[k][16 tj + n]
+    float av[8], bv[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int k = t < 4 ? 4 * g + t : 16 + 4 * g + (t - 4);
+      av[t] = (k <= 16 * ti + ln) ? nt[(32 + k) * NTS + 32 + 16 * ti + ln] : 0.f;
+      bv[t] = t < 4 ? y[0][t] : y[1][t - 4];
     }
     bf16x8 ah, al, bh, bl;
     split8(av, ah, al);
     split8(bv, bh, bl);
-    f32x4 y = {0.f, 0.f, 0.f, 0.f};
-    y = mma3<true, true>(ah, al, bh, bl, y);
-    *reinterpret_cast<f32x4 *>(yt + (16 * tj + ln) * 36 + 16 * ti + 4 * g) = y;  // Y^T
-    __syncthreads();
-    // T[32 + 16 ti + m][16 tj + n] = -sum_k T[32 + 16 ti + m][32 + k] Y[k][16 tj + n]
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const int k = 8 * g + t;
-      av[t] = (k <= 16 * ti + ln) ? nt[(32 + k) * NTS + 32 + 16 * ti + ln] : 0.f;
-      bv[t] = yt[(16 * tj + ln) * 36 + k];
-    }
-    split8(av, ah, al);
-    split8(bv, bh, bl);
-    f32x4 o = {0.f, 0.f, 0.f, 0.f};
-    o = mma3<true, true>(ah, al, bh, bl, o);
+    const f32x4 o = mma3<true, true>(ah, al, bh, bl, f32x4{0.f, 0.f, 0.f, 0.f});
     *reinterpret_cast<f32x4 *>(nt + (16 * tj + ln) * NTS + 32 + 16 * ti + 4 * g) = -o;
   }
   __syncthreads();
 
-  // ---- phase 6: T^T (bf16 hi/lo), then the transposed K, K~ and V planes.
+  // ---- phase 6: T^T as bf16 hi / lo planes, written over NT once every thread holds
+  // its 16 entries.
   {
     const int j = tid >> 2, i0 = 16 * (tid & 3);
     float x[16];
@@ -564,205 +614,169 @@ __global__ void __launch_bounds__(256, 2) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
     bf16x8 h0, l0, h1, l1;
     split8(x, h0, l0);
     split8(x + 8, h1, l1);
+    __syncthreads();
     *reinterpret_cast<bf16x8 *>(tt_h + swz(j, i0)) = h0;
     *reinterpret_cast<bf16x8 *>(tt_l + swz(j, i0)) = l0;
     *reinterpret_cast<bf16x8 *>(tt_h + swz(j, i0 + 8)) = h1;
     *reinterpret_cast<bf16x8 *>(tt_l + swz(j, i0 + 8)) = l1;
   }
   const float glast = gam[kC - 1];
-  __syncthreads();  // NT and the K / Q rows are dead from here on
-  if constexpr (!FRONT) {
-    if (kval) {
-      const int j = 2 * kp;
-      const float f0 = exp_fast(glast - gam[j]), f1 = exp_fast(glast - gam[j + 1]);
-      const bf16x8 ka = __builtin_bit_cast(bf16x8, k0r), kb_ = __builtin_bit_cast(bf16x8, k1r);
+  __syncthreads();
+  // ---- phase 7: wave w takes a 32-row tile of M = [K~^T ; Attn] T: top tiles
+  // (w < DK / 32) rows d' of K~^T T, bottom tiles (waves 2, 3) rows i' of Attn T.
+  // M^T (rows j, columns m) = T^T L^T on 32x32x16 MFMAs, A = T^T (hi / lo planes), B =
+  // K~ (K^T plane times e^{gamma_C - gamma_i}, split here) or Attn^T (registers).  The
+  // M^T accumulator, scaled per row j, is already in the slot order of a B operand
+  // (and, for the same lane, of an A operand over k = j), so
+  //   Z^T = K^T (diag(beta e^gamma) M^T)    -> A_n = e^{gamma_C} I - Z,  Q' = Q e^gamma - Z
+  //   Y   = (M diag(beta)) V (top: H_n),  Y^T = V^T (diag(beta) M^T) (bottom: O')
+  // take their M operands straight from registers.  Each result goes to the workspace
+  // as bf16 in 8-byte pieces of the consuming kernel's operand order.
+  const WsLayout Lw(DK, a.dv);
+  char *cell = ws + (static_cast<size_t>(h) * ca.total_chunks + chunk) * Lw.cell;
+  const bool top = w < DK / 32, bottom = w >= 2;
+  if (top || bottom) {
+    const int tile = top ? w : w - 2;
+    const int m = 32 * tile + lc;  // d' (top) or i' (bottom): this lane's column of M^T
+    bf16x8 bh[4], bl[4];
+    if (top) {
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const int d = 8 * kseg + t;
-        *reinterpret_cast<uint32_t *>(kt + swz(d, j)) = pack2(bits(ka[t]), bits(kb_[t]));
-        const float x0 = fl(ka[t]) * f0, x1 = fl(kb_[t]) * f1;
-        uint32_t hw, lw;
-        split2(x0, x1, hw, lw);
-        *reinterpret_cast<uint32_t *>(ktt_h + swz(d, j)) = hw;
-        *reinterpret_cast<uint32_t *>(ktt_l + swz(d, j)) = lw;
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8 kv = rd_pair_s(kt, m, 16 * ks + 4 * hh);
+        float x[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) x[t] = fl(kv[t]) * exp_fast(glast - gam[16 * ks + 8 * (t >> 2) + 4 * hh + (t & 3)]);
+        split8(x, bh[ks], bl[ks]);
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        bh[ks] = ath[ks];
+        bl[ks] = atl[ks];
       }
     }
+    // M^T rows j = 32 jt + 8 (r / 4) + 4 hh + r % 4
+    f32x16 mt2[2];
 #pragma unroll
-    for (int r = 0; r < VP; ++r) {
-      const int vp = tid & 31, vs = (tid >> 5) + 8 * r;
-      if (vs < a.dv / 8) {
-        const bf16x8 va = __builtin_bit_cast(bf16x8, v0r[r]), vb_ = __builtin_bit_cast(bf16x8, v1r[r]);
+    for (int jt = 0; jt < 2; ++jt) {
+      f32x16 acc = {};
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
-          *reinterpret_cast<uint32_t *>(vt + swz(8 * vs + t, 2 * vp)) = pack2(bits(va[t]), bits(vb_[t]));
+      for (int ks = 0; ks < 4; ++ks) {
+        if (jt == 1 && ks < 2) continue;  // T^T rows j >= 32 vanish on columns i < 32
+        const bf16x8 th = rd_pair_s(tt_h, 32 * jt + lc, 16 * ks + 4 * hh);
+        const bf16x8 tl = rd_pair_s(tt_l, 32 * jt + lc, 16 * ks + 4 * hh);
+        acc = mma32(tl, bh[ks], acc);
+        acc = mma32(th, bl[ks], acc);
+        acc = mma32(th, bh[ks], acc);
+      }
+      mt2[jt] = acc;
+    }
+    // operands over k = j of diag(s) M^T, s = beta e^gamma (K side) or beta (V side)
+    auto m_operands = [&](bool kside, bf16x8 *oh, bf16x8 *ol) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        float x[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const int r = 8 * (ks & 1) + t, j = 16 * ks + 8 * (t >> 2) + 4 * hh + (t & 3);
+          x[t] = mt2[ks >> 1][r] * (kside ? bet[j] * exp_fast(gam[j]) : bet[j]);
+        }
+        split8(x, oh[ks], ol[ks]);
+      }
+    };
+    bf16x8 oh[4], ol[4];
+    m_operands(true, oh, ol);
+    // Z^T[d][m] = sum_j K^T[d][j] (s M^T)[j][m]; z[r]: d = 32 dt + 8 (r / 4) + 4 hh + r % 4
+    const float eq = top ? exp_fast(glast) : exp_fast(gam[m]);
+    char *zbase = cell + (top ? Lw.an : Lw.qp);
+#pragma unroll
+    for (int dt = 0; dt < DK / 32; ++dt) {
+      f32x16 z = {};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8 ka = rd_pair_s(kt, 32 * dt + lc, 16 * ks + 4 * hh);
+        z = mma32(ka, ol[ks], z);
+        z = mma32(ka, oh[ks], z);
+      }
+      // rows m, columns d = 32 dt + 8 q + 4 hh + p (p = 0..3): tile mt = m / 16, k-step
+      // dt, lane (m % 16) + 16 (2 (q % 2) + hh), half q / 2
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const bf16x4 qrow = top ? bf16x4{} : rd4s(qh, m, 32 * dt + 8 * q + 4 * hh);
+        float x[4];
+#pragma unroll
+        for (int p4 = 0; p4 < 4; ++p4) {
+          const int d = 32 * dt + 8 * q + 4 * hh + p4;
+          x[p4] = (top ? (d == m ? eq : 0.f) : fl(qrow[p4]) * eq) - z[4 * q + p4];
+        }
+        const size_t o = ((static_cast<size_t>(m >> 4) * (DK / 32) + dt) * 64 + (m & 15) + 16 * (2 * (q & 1) + hh)) * 16 +
+                         8 * (q >> 1);
+        *reinterpret_cast<uint2 *>(zbase + o) = uint2{pk_bf16(x[0], x[1]), pk_bf16(x[2], x[3])};
       }
     }
-  
-  } else if (w == 1) {  // K^T and K~^T planes from this thread's K rows (pairs of rows)
+    m_operands(false, oh, ol);
+    bf16_t *yb = reinterpret_cast<bf16_t *>(cell + (top ? Lw.hn : Lw.op));
+    for (int vt2 = 0; vt2 < a.dv / 32; ++vt2) {
+      f32x16 y = {};
 #pragma unroll
-    for (int i = 0; i < RQ; i += 2) {
-      const int j = f_r0 + i;
-      const float f0 = exp_fast(glast - gam[j]), f1 = exp_fast(glast - gam[j + 1]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int d = 8 * f_seg + e;
-        const uint16_t b0 = static_cast<uint16_t>(cv[i][e >> 1] >> (16 * (e & 1)));
-        const uint16_t b1 = static_cast<uint16_t>(cv[i + 1][e >> 1] >> (16 * (e & 1)));
-        *reinterpret_cast<uint32_t *>(kt + swz(d, j)) = pack2(b0, b1);
-        uint32_t hw, lw;
-        split2(bf16_to_f32(b0) * f0, bf16_to_f32(b1) * f1, hw, lw);
-        *reinterpret_cast<uint32_t *>(ktt_h + swz(d, j)) = hw;
-        *reinterpret_cast<uint32_t *>(ktt_l + swz(d, j)) = lw;
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8 vv = rd_pair_s(vt, 32 * vt2 + lc, 16 * ks + 4 * hh);
+        if (top) {
+          y = mma32(ol[ks], vv, y);
+          y = mma32(oh[ks], vv, y);
+        } else {
+          y = mma32(vv, ol[ks], y);
+          y = mma32(vv, oh[ks], y);
+        }
       }
-    }
-  } else if (w >= 2) {  // V^T plane
 #pragma unroll
-    for (int i = 0; i < RV; i += 2) {
-      const int j = f_r0 + i;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint16_t b0 = static_cast<uint16_t>(cv[i][e >> 1] >> (16 * (e & 1)));
-        const uint16_t b1 = static_cast<uint16_t>(cv[i + 1][e >> 1] >> (16 * (e & 1)));
-        *reinterpret_cast<uint32_t *>(vt + swz(8 * f_seg + e, j)) = pack2(b0, b1);
+      for (int q = 0; q < 4; ++q) {
+        size_t o;
+        if (top) {  // H_n[d' = 32 tile + 8 q + 4 hh + p][v = 32 vt2 + lc], layout [cg][DK/16][64] x 4
+          const int cg = 2 * vt2 + (lc >> 4), mt = 2 * tile + (q >> 1);
+          o = ((static_cast<size_t>(cg) * (DK / 16) + mt) * 64 + (lc & 15) + 16 * (2 * (q & 1) + hh)) * 4;
+        } else {    // O'[m][v = 32 vt2 + 8 q + 4 hh + p], layout [cg][4][64] x 4
+          const int cg = 2 * vt2 + (q >> 1), mt = m >> 4;
+          o = ((static_cast<size_t>(cg) * 4 + mt) * 64 + (m & 15) + 16 * (2 * (q & 1) + hh)) * 4;
+        }
+        *reinterpret_cast<uint2 *>(yb + o) = uint2{pk_bf16(y[4 * q], y[4 * q + 1]), pk_bf16(y[4 * q + 2], y[4 * q + 3])};
       }
     }
   }
-  __syncthreads();
-
-  // ---- phase 7: M = [K~^T ; Attn] T, computed as M^T tiles (rows j, columns m) and fed
-  // straight from the accumulators into  Z^T = K^T (diag(beta e^gamma) M^T)  and
-  // Y = (M diag(beta)) V  (or Y^T).  m-tiles 0 .. DK/16-1 give A_n and H_n, the rest Q' and O'.
-  const WsLayout Lw(DK, a.dv);
-  char *cell = ws + (static_cast<size_t>(h) * ca.total_chunks + chunk) * Lw.cell;
-  float *hn = reinterpret_cast<float *>(cell + Lw.hn);
-  float *op = reinterpret_cast<float *>(cell + Lw.op);
-  const float eC = exp_fast(glast);
-  float sk[4][4], sv[4][4];  // per-row scales of M^T for rows j = 16 jt + 4g + r
-#pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int j = 16 * jt + 4 * g + r;
-      sv[jt][r] = bet[j];
-      sk[jt][r] = bet[j] * exp_fast(gam[j]);
-    }
-  // One m-tile: TOP -> rows d' = 16 mti + ln of A_n / H_n, else rows i' of Q' / O'.
-  auto mtile = [&](auto top_c, int mti, const bf16x4 *qrow) {
-    constexpr bool top = decltype(top_c)::value;
-    const int mrow = 16 * mti + ln;  // d' (top) or i' (bottom)
-    const __bf16 *Lh = top ? ktt_h : att_h, *Ll = top ? ktt_l : att_l;
-    bf16x8 lh[2], ll[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      lh[ks] = rd8s(Lh, mrow, 32 * ks + 8 * g);
-      ll[ks] = rd8s(Ll, mrow, 32 * ks + 8 * g);
-    }
-    bf16x4 mkh[4], mkl[4], mvh[4], mvl[4];
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        if (ks == 0 && jt >= 2) continue;  // T^T rows j >= 32 vanish on columns i < 32
-        acc = mma3<true, true>(rd8s(tt_h, 16 * jt + ln, 32 * ks + 8 * g), rd8s(tt_l, 16 * jt + ln, 32 * ks + 8 * g),
-                               lh[ks], ll[ks], acc);
-      }
-      float xk[4], xv[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        xk[r] = acc[r] * sk[jt][r];
-        xv[r] = acc[r] * sv[jt][r];
-      }
-      split4(xk, mkh[jt], mkl[jt]);
-      split4(xv, mvh[jt], mvl[jt]);
-    }
-    bf16x8 bkh[2], bkl[2], bvh[2], bvl[2];
-#pragma unroll
-    for (int jp = 0; jp < 2; ++jp) {
-      bkh[jp] = __builtin_shufflevector(mkh[2 * jp], mkh[2 * jp + 1], 0, 1, 2, 3, 4, 5, 6, 7);
-      bkl[jp] = __builtin_shufflevector(mkl[2 * jp], mkl[2 * jp + 1], 0, 1, 2, 3, 4, 5, 6, 7);
-      bvh[jp] = __builtin_shufflevector(mvh[2 * jp], mvh[2 * jp + 1], 0, 1, 2, 3, 4, 5, 6, 7);
-      bvl[jp] = __builtin_shufflevector(mvl[2 * jp], mvl[2 * jp + 1], 0, 1, 2, 3, 4, 5, 6, 7);
-    }
-    const float eq = top ? eC : exp_fast(gam[mrow]);
-    char *base = cell + (top ? Lw.an : Lw.qp);
-    constexpr int ntile = top ? DK / 16 : kC / 16;
-#pragma unroll
-    for (int dt = 0; dt < DK / 16; ++dt) {
-      f32x4 z = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int jp = 0; jp < 2; ++jp) {
-        const bf16x8 ak = rd_perm_s(kt, 16 * dt + ln, 32 * jp, g);
-        z = mma(ak, bkl[jp], z);
-        z = mma(ak, bkh[jp], z);
-      }
-      // z[r] = Z^T[16 dt + 4g + r][m] = (M_k K)[m][16 dt + 4g + r]
-      const int col = 16 * dt + 4 * g;
-      float x[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        x[r] = (top ? (col + r == mrow ? eq : 0.f) : fl(qrow[dt][r]) * eq) - z[r];
-      bf16x4 hv, lv;
-      split4(x, hv, lv);
-      // operand order: tile (plane, mti, ks = dt / 2), lane, half dt % 2
-      const size_t o_h = ((static_cast<size_t>(0 * ntile + mti) * (DK / 32) + dt / 2) * 64 + lane) * 16 + 8 * (dt & 1);
-      const size_t o_l = ((static_cast<size_t>(1 * ntile + mti) * (DK / 32) + dt / 2) * 64 + lane) * 16 + 8 * (dt & 1);
-      *reinterpret_cast<bf16x4 *>(base + o_h) = hv;
-      *reinterpret_cast<bf16x4 *>(base + o_l) = lv;
-    }
-    // H_n as Y = M_v V (accumulator layout of the state), O' as Y^T (layout of O^T).
-    float *dst0 = top ? hn + mti * 256 : op + mti * 256;
-#pragma unroll
-    for (int et = 0; et < DV / 16; ++et) {
-      if (et < a.dv / 16) {
-        f32x4 y = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int jp = 0; jp < 2; ++jp) {
-          const bf16x8 avv = rd_perm_s(vt, 16 * et + ln, 32 * jp, g);
-          if (top) {
-            y = mma(bvl[jp], avv, y);
-            y = mma(bvh[jp], avv, y);
-          } else {
-            y = mma(avv, bvl[jp], y);
-            y = mma(avv, bvh[jp], y);
-          }
-        }
-        *reinterpret_cast<f32x4 *>(dst0 + static_cast<size_t>(et) * ntile * 256 + 4 * lane) = y;
-      }
-    }
-  };
-  // wave w: A_n / H_n row tile w (when w < DK/16) and Q' / O' row tile w
-  if (w < DK / 16) mtile(BoolC<true>{}, w, nullptr);
-  mtile(BoolC<false>{}, w, qe);
 }
 
 // ------------------------------------------------------------------ state scan
-// One wave per 16-row tile of S.
+// A_n / H_n of one chunk as one wavefront of the scan needs them.
 template <int DK>
 struct ScanStage {
-  uint4 an[2][DK / 32];  // A_n hi / lo operand rows of this wave's tile
-  f32x4 hn;              // H_n tile, accumulator layout
+  uint4 an[DK / 16][DK / 32];  // A_n operand rows, every row tile
+  uint2 hn[DK / 16];           // H_n tiles of this column group (bf16, accumulator layout)
 };
 
+// Loads of one chunk through a buffer over the group's cells: the chunk's byte offset
+// is the (uniform) soffset, so a stage costs no address registers.
 template <int DK>
-__device__ __forceinline__ void scan_load(ScanStage<DK> &st, const char *cell, const WsLayout &Lw, int cg, int mt,
-                                          int lane) {
+__device__ __forceinline__ void scan_load(ScanStage<DK> &st, buf_t cells, uint32_t cell_off, uint32_t an_v,
+                                          uint32_t hn_v) {
   constexpr int TDK = DK / 16, KS = DK / 32;
-  const uint4 *an = reinterpret_cast<const uint4 *>(cell + Lw.an) + lane;
 #pragma unroll
-  for (int p = 0; p < 2; ++p)
+  for (int mt = 0; mt < TDK; ++mt)
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) st.an[p][ks] = an[((p * TDK + mt) * KS + ks) * 64];
-  st.hn = reinterpret_cast<const f32x4 *>(cell + Lw.hn)[(static_cast<size_t>(cg) * TDK + mt) * 64 + lane];
+    for (int ks = 0; ks < KS; ++ks)
+      st.an[mt][ks] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(cells, an_v + (mt * KS + ks) * 1024, cell_off, 0));
+#pragma unroll
+  for (int mt = 0; mt < TDK; ++mt)
+    st.hn[mt] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(cells, hn_v + mt * 512, cell_off, 0));
 }
 
-// One workgroup per (16 state columns, head, sequence), one wave per 16-row tile mt of
-// S: S[r] = S[16 mt + 4g + r][16 cg + l % 16].  Per chunk every wave turns its tile
-// into hi / lo bf16 halves of the B operand (slots 0..3 of a 32-row k-step come from
-// tile 2 ks, slots 4..7 from tile 2 ks + 1), exchanges them through LDS (double
-// buffered: one barrier per chunk) and forms its tile of S_{n+1} = A_n S_n + H_n: a
-// chain of 3 (DK / 32) MFMAs per wave instead of 3 DK^2 / 512 for one wave per column
-// group.
+// One wavefront per (16 state columns, head, sequence) holds all DK rows of its columns:
+// tile mt, S[mt][r] = S[16 mt + 4g + r][16 cg + l % 16].  S_{n+1} = A_n S_n + H_n mixes
+// rows only, so the wavefront needs no other's columns: the B operand of k-step ks is
+// the bf16 rounding of its own tiles 2 ks (slots 0..3) and 2 ks + 1 (slots 4..7), i.e.
+// k slots 32 ks + 4g + {0..3, 16..19} in the order A_n's operand rows are stored, and
+// that same operand is the S_n piece the output kernel reads.  Per chunk DK/16 x DK/32
+// MFMAs in DK/16 independent chains, no LDS and no barrier.
 // Workgroups of a scan launch: ngroups (head, sequence) groups of ncg column-group
 // workgroups that all read the same A_n.  Workgroups go to the 8 XCDs round-robin by
 // linear id, so a group is placed on one XCD (its A_n then comes from that XCD's L2
@@ -776,16 +790,12 @@ struct ScanGrid {
 };
 
 template <int DK>
-__global__ void __launch_bounds__(64 * (DK / 16)) gdn_state_scan(GdnArgs a, ChunkArgs ca, char *ws, ScanGrid sgrid) {
+__global__ void __launch_bounds__(64) gdn_state_scan(GdnArgs a, ChunkArgs ca, char *ws, ScanGrid sgrid) {
   constexpr int TDK = DK / 16, KS = DK / 32;
   const int slot = blockIdx.x / ScanGrid::kXcd;
   const int group = (slot / sgrid.ncg) * ScanGrid::kXcd + blockIdx.x % ScanGrid::kXcd;
   if (group >= sgrid.ngroups) return;
   const int cg = slot % sgrid.ncg, h = group % a.H, sq = group / a.H;
-  const int lane = threadIdx.x & 63, mt = threadIdx.x >> 6;
-  const int ln = lane & 15, g = lane >> 4;
-  const int col = 16 * cg + ln;
-  const int ks_own = mt >> 1, half = mt & 1;  // where this tile sits in the B operand
 
   int first, count;
   if (ca.cu == nullptr) {
@@ -798,62 +808,55 @@ __global__ void __launch_bounds__(64 * (DK / 16)) gdn_state_scan(GdnArgs a, Chun
   const WsLayout Lw(DK, a.dv);
   char *cell0 = ws + (static_cast<size_t>(h) * ca.total_chunks + first) * Lw.cell;
 
-  f32x4 S;
+  const int lane = threadIdx.x;
+  const int ln = lane & 15, g = lane >> 4;
+  const int col = 16 * cg + ln;
+
+  f32x4 S[TDK];
   const size_t sbase = (static_cast<size_t>(sq) * a.H + h) * DK * a.dv;
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-    S[r] = a.s_in ? a.s_in[sbase + static_cast<size_t>(16 * mt + 4 * g + r) * a.dv + col] : 0.f;
-
-  // [buffer][plane][ks][lane] bf16x8 B operands of S
-  __shared__ __attribute__((aligned(16))) uint4 sB[2][2][KS][64];
+  for (int mt = 0; mt < TDK; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      S[mt][r] = a.s_in ? a.s_in[sbase + static_cast<size_t>(16 * mt + 4 * g + r) * a.dv + col] : 0.f;
 
   // kScanDepth stages of A_n / H_n in flight (chunk n + kScanDepth is requested while
   // chunk n is computed)
-  constexpr int kScanDepth = 6;
+  constexpr int kScanDepth = DK == 64 ? 4 : 8;
+  const uint32_t cell_bytes = static_cast<uint32_t>(Lw.cell);
+  const buf_t cells = make_buf(cell0, static_cast<uint32_t>(count) * cell_bytes);
+  const uint32_t an_v = static_cast<uint32_t>(Lw.an) + 16u * lane;
+  const uint32_t hn_v = static_cast<uint32_t>(Lw.hn) + static_cast<uint32_t>(cg) * TDK * 512u + 8u * lane;
   ScanStage<DK> st[kScanDepth];
   if (count > 0) {
 #pragma unroll
-    for (int j = 0; j < kScanDepth; ++j)
-      scan_load<DK>(st[j], cell0 + static_cast<size_t>(min(j, count - 1)) * Lw.cell, Lw, cg, mt, lane);
+    for (int j = 0; j < kScanDepth; ++j) scan_load<DK>(st[j], cells, min(j, count - 1) * cell_bytes, an_v, hn_v);
   }
 
-  // S_n as hi / lo operands (shared, and stored for the output kernel), then this
-  // wave's tile of S_{n+1}; the stage is then refilled with chunk
-  // min(n + kScanDepth, count - 1) (a repeat load of the last chunk near the end keeps
-  // the loop free of branches).
+  // S_n as bf16 operands (stored for the output kernel), then S_{n+1}; the stage is
+  // then refilled with chunk min(n + kScanDepth, count - 1) (a repeat load of the last
+  // chunk near the end keeps the loop free of branches).
   auto step = [&](ScanStage<DK> &stg, int n) {
     char *cell = cell0 + static_cast<size_t>(n) * Lw.cell;
-    const int buf = n & 1;
-    uint2 hv, lv;
-    {
-      bf16_t hb[4], lb[4];
+    uint4 sb[KS];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const __bf16 hh = bf(S[r]);
-        hb[r] = __builtin_bit_cast(bf16_t, hh);
-        lb[r] = __builtin_bit_cast(bf16_t, bf(S[r] - fl(hh)));
-      }
-      hv = uint2{hb[0] | (static_cast<uint32_t>(hb[1]) << 16), hb[2] | (static_cast<uint32_t>(hb[3]) << 16)};
-      lv = uint2{lb[0] | (static_cast<uint32_t>(lb[1]) << 16), lb[2] | (static_cast<uint32_t>(lb[3]) << 16)};
-    }
-    reinterpret_cast<uint2 *>(&sB[buf][0][ks_own][lane])[half] = hv;
-    reinterpret_cast<uint2 *>(&sB[buf][1][ks_own][lane])[half] = lv;
-    __syncthreads();
-    // S_n for the output kernel: the 2 KS = TDK operand arrays, one full 1 KB array per
-    // wave (array mt = plane mt % 2 of k-step mt / 2)
-    reinterpret_cast<uint4 *>(cell + Lw.sn)[(static_cast<size_t>(cg) * KS * 2 + mt) * 64 + lane] =
-        sB[buf][mt & 1][mt >> 1][lane];
-    f32x4 acc = stg.hn;
+    for (int ks = 0; ks < KS; ++ks)
+      sb[ks] = uint4{pk_bf16(S[2 * ks][0], S[2 * ks][1]), pk_bf16(S[2 * ks][2], S[2 * ks][3]),
+                     pk_bf16(S[2 * ks + 1][0], S[2 * ks + 1][1]), pk_bf16(S[2 * ks + 1][2], S[2 * ks + 1][3])};
+    uint4 *sn = reinterpret_cast<uint4 *>(cell + Lw.sn) + static_cast<size_t>(cg) * KS * 64 + lane;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const bf16x8 sh = __builtin_bit_cast(bf16x8, sB[buf][0][ks][lane]);
-      const bf16x8 sl = __builtin_bit_cast(bf16x8, sB[buf][1][ks][lane]);
-      acc = mma(__builtin_bit_cast(bf16x8, stg.an[1][ks]), sh, acc);
-      acc = mma(__builtin_bit_cast(bf16x8, stg.an[0][ks]), sl, acc);
-      acc = mma(__builtin_bit_cast(bf16x8, stg.an[0][ks]), sh, acc);
+    for (int ks = 0; ks < KS; ++ks) sn[ks * 64] = sb[ks];
+#pragma unroll
+    for (int mt = 0; mt < TDK; ++mt) {
+      const uint2 hv = stg.hn[mt];
+      f32x4 acc = {__uint_as_float(hv.x << 16), __uint_as_float(hv.x & 0xffff0000u),
+                   __uint_as_float(hv.y << 16), __uint_as_float(hv.y & 0xffff0000u)};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        acc = mma(__builtin_bit_cast(bf16x8, stg.an[mt][ks]), __builtin_bit_cast(bf16x8, sb[ks]), acc);
+      S[mt] = acc;
     }
-    S = acc;
-    scan_load<DK>(stg, cell0 + static_cast<size_t>(min(n + kScanDepth, count - 1)) * Lw.cell, Lw, cg, mt, lane);
+    scan_load<DK>(stg, cells, min(n + kScanDepth, count - 1) * cell_bytes, an_v, hn_v);
   };
   int n = 0;
   for (; n + kScanDepth <= count; n += kScanDepth) {
@@ -865,7 +868,9 @@ __global__ void __launch_bounds__(64 * (DK / 16)) gdn_state_scan(GdnArgs a, Chun
     if (n + j < count) step(st[j], n + j);
 
 #pragma unroll
-  for (int r = 0; r < 4; ++r) a.s_out[sbase + static_cast<size_t>(16 * mt + 4 * g + r) * a.dv + col] = S[r];
+  for (int mt = 0; mt < TDK; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) a.s_out[sbase + static_cast<size_t>(16 * mt + 4 * g + r) * a.dv + col] = S[mt][r];
 }
 
 // ------------------------------------------------------------------ chunk output
@@ -897,41 +902,34 @@ __global__ void __launch_bounds__(256) gdn_chunk_out(GdnArgs a, ChunkArgs ca, co
       }
   }
 
-  bf16x8 qh[4][KS], ql[4][KS];
+  bf16x8 qh[4][KS];
   const uint4 *qp = reinterpret_cast<const uint4 *>(cell + Lw.qp) + lane;
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      qh[mt][ks] = __builtin_bit_cast(bf16x8, qp[((0 * 4 + mt) * KS + ks) * 64]);
-      ql[mt][ks] = __builtin_bit_cast(bf16x8, qp[((1 * 4 + mt) * KS + ks) * 64]);
-    }
+    for (int ks = 0; ks < KS; ++ks) qh[mt][ks] = __builtin_bit_cast(bf16x8, qp[(mt * KS + ks) * 64]);
   // O tiles of this wave's column groups cg = w + 4 i: lane holds O[16 mt + ln][16 cg + 4 g + r]
   f32x4 res[kMaxCg][4];
 #pragma unroll
   for (int i = 0; i < kMaxCg; ++i) {
     const int cg = w + 4 * i;
     if (cg >= ncg) break;
-    const uint4 *sn = reinterpret_cast<const uint4 *>(cell + Lw.sn) + static_cast<size_t>(cg) * KS * 2 * 64 + lane;
-    const f32x4 *op = reinterpret_cast<const f32x4 *>(cell + Lw.op) + static_cast<size_t>(cg) * 4 * 64 + lane;
-    bf16x8 sh[KS], sl[KS];
+    const uint4 *sn = reinterpret_cast<const uint4 *>(cell + Lw.sn) + static_cast<size_t>(cg) * KS * 64 + lane;
+    const uint2 *op = reinterpret_cast<const uint2 *>(cell + Lw.op) + static_cast<size_t>(cg) * 4 * 64 + lane;
+    bf16x8 sh[KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      sh[ks] = __builtin_bit_cast(bf16x8, sn[(2 * ks) * 64]);
-      sl[ks] = __builtin_bit_cast(bf16x8, sn[(2 * ks + 1) * 64]);
-    }
+    for (int ks = 0; ks < KS; ++ks) sh[ks] = __builtin_bit_cast(bf16x8, sn[ks * 64]);
     f32x4 acc[4];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) acc[mt] = op[mt * 64];
+    for (int mt = 0; mt < 4; ++mt) {
+      const uint2 ov = op[mt * 64];
+      acc[mt] = f32x4{__uint_as_float(ov.x << 16), __uint_as_float(ov.x & 0xffff0000u),
+                      __uint_as_float(ov.y << 16), __uint_as_float(ov.y & 0xffff0000u)};
+    }
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) acc[mt] = mma(sl[ks], qh[mt][ks], acc[mt]);
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) acc[mt] = mma(sh[ks], ql[mt][ks], acc[mt]);
+    for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) acc[mt] = mma(sh[ks], qh[mt][ks], acc[mt]);
-    }
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) res[i][mt] = acc[mt];
     if (a.o) {
@@ -1030,7 +1028,7 @@ int launch_dk(const GdnArgs &a, const ChunkArgs &ca, char *ws, hipStream_t s) {
   else rc = launch_prep<DK, 128>(a, ca, ws, s);
   if (rc) return rc;
   const ScanGrid sgrid{a.dv / 16, a.H * ca.nseq};
-  gdn_state_scan<DK><<<sgrid.blocks(), dim3(64 * (DK / 16)), 0, s>>>(a, ca, ws, sgrid);
+  gdn_state_scan<DK><<<sgrid.blocks(), dim3(64), 0, s>>>(a, ca, ws, sgrid);
   if ((rc = check_launch("gdn_state_scan"))) return rc;
   // 8-byte output stores when every row start is 8-byte aligned
   const int vec = ((a.o_sb | a.o_sh | a.o_st) & 3) == 0 && (reinterpret_cast<uintptr_t>(a.o) & 7) == 0;
@@ -1041,7 +1039,7 @@ int launch_dk(const GdnArgs &a, const ChunkArgs &ca, char *ws, hipStream_t s) {
 }  // namespace
 
 bool chunk_mfma_supported(int dk, int dv, int chunk) {
-  return chunk == kC && (dk == 32 || dk == 64) && dv % 16 == 0 && dv > 0 && dv <= 128;
+  return chunk == kC && (dk == 32 || dk == 64) && dv % 32 == 0 && dv > 0 && dv <= 128;
 }
 
 size_t chunk_mfma_workspace_bytes(int H, int dk, int dv, int total_chunks) {
@@ -1069,7 +1067,7 @@ int launch_fused(const GdnArgs &a, const ChunkArgs &ca, const FrontArgs &fa, cha
   int rc = launch_prep<DK, DV, true>(a, ca, ws, s, fa);
   if (rc) return rc;
   const ScanGrid sgrid{a.dv / 16, a.H * ca.nseq};
-  gdn_state_scan<DK><<<sgrid.blocks(), dim3(64 * (DK / 16)), 0, s>>>(a, ca, ws, sgrid);
+  gdn_state_scan<DK><<<sgrid.blocks(), dim3(64), 0, s>>>(a, ca, ws, sgrid);
   if ((rc = check_launch("gdn_state_scan"))) return rc;
   gdn_chunk_out<bf16_t, DK><<<dim3(ca.total_chunks, a.H), dim3(256), 0, s>>>(a, ca, ws, 0);
   return check_launch("gdn_chunk_out");
