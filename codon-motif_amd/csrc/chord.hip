@@ -67,8 +67,6 @@ __device__ __forceinline__ float log_n_at(const ChordArgs &a, int b, int i, int 
 
 constexpr int kD = 64;        // head dim
 constexpr int kBN = 64;       // keys per tile
-constexpr int kKStride = 72;  // sK row stride (bf16): 144 B keeps 16 B reads conflict-free
-constexpr int kVStride = 68;  // sVt row stride (bf16): 136 B keeps 8 B reads conflict-free
 
 __device__ __forceinline__ float ggd_bias(float dist, float alpha, float beta, float mu, float eps) {
   // -alpha * (|d - mu| + eps)^beta, the power through exp2(beta * log2(.)).
@@ -86,23 +84,24 @@ __device__ __forceinline__ f32x4 mma16(const bf16x8 &a, const bf16x8 &b, f32x4 c
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// Position of key k (0..63) in a V^T row: inside each 32-key group the keys
-// 4g..4g+3 and 16+4g..16+4g+3 are stored together at 8g, so one 16-byte read is the
-// MFMA A operand that pairs with P^T taken from two 16-key accumulator tiles.
-__device__ __forceinline__ int vperm(int k) {
-  return (k & 32) | ((k & 12) << 1) | ((k & 16) >> 2) | (k & 3);
+// v_mfma_f32_32x32x16_bf16 (twice the work of 16x16x32 per issue slot on gfx950): A
+// lane l holds row l % 32, k 8 (l / 32) + 0..7; B lane l column l % 32, the same k;
+// accumulator register r of lane l holds row 8 (r / 4) + 4 (l / 32) + r % 4, column
+// l % 32.
+__device__ __forceinline__ f32x16 mma32(const bf16x8 &a, const bf16x8 &b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// Max of x over the four 16-lane groups (lanes l, l^16, l^32, l^48) via the gfx950
-// lane-swap instructions: each returned pair holds x of both partners.
-__device__ __forceinline__ float max_lane_groups(float x) {
-  const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
-  const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(s16[0]), __uint_as_float(s16[1]));
-}
+// Position of key k in a V^T row.  P^T comes straight from S^T accumulators, whose
+// lane half h holds keys 8a + 4h + (0..3) (a = 0, 1) of each 16-key group, so those
+// eight keys are stored together at 8h + 4a: one 16-byte read is the matching A operand.
+__device__ __forceinline__ int vperm32(int k) { return (k & ~15) | ((k & 4) << 1) | ((k & 8) >> 1) | (k & 3); }
 
-constexpr int kRow = 72;  // LDS row stride (bf16) of the K and V^T tiles: 144 B rows
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk2bf(float x0, float x1) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v){x0, x1}, bf16x2v));
+}
 
 // Prefill logit form: q is multiplied by rho_h = sign(ssmax_h * scale) (exact; 0 when
 // scale == 0) and each S^T = K Q^T MFMA starts from kappa_h * GGD(key - q_abs) for
@@ -110,33 +109,51 @@ constexpr int kRow = 72;  // LDS row stride (bf16) of the K and V^T tiles: 144 B
 // (sign(ssmax_h) when scale == 0), so acc = rho_h (q.k + bias / scale) and the logit is
 // |ssmax_h log_n[i] scale| acc (|ssmax_h log_n[i]| acc when scale == 0).
 
-// LDS tile rows of 64 bf16 (128 B) hold their eight 16-byte pieces in the order
-// piece ^ (row & 7): the row-per-lane 16-byte reads of the MFMA operands and the
-// staging stores are then free of bank conflicts (measured with SQ_LDS_BANK_CONFLICT).
-__device__ __forceinline__ int swz(int row, int col) { return row * 64 + ((((col >> 3) ^ row) & 7) << 3) + (col & 7); }
+// LDS tile rows of 64 bf16 are padded to 72 (144 B): the row-per-lane 16-byte reads of
+// the MFMA operands are free of bank conflicts, and the pieces of one row sit at fixed
+// offsets from its start, so every operand read of a step is one base register plus
+// an immediate.
+constexpr int kRow = 72;
 
-// Each workgroup is two halves of 4 waves over the same query rows and heads: half 0
-// takes the first ceil(n / 2) of the rows' n key tiles, half 1 the rest, each with
-// its own double-buffered K / V tiles, and the two partial softmaxes are merged
-// through LDS at the end.  Splitting the keys halves the longest chain of tiles and
-// gives 8 waves per workgroup (two workgroups fill a CU's LDS: 4 waves per SIMD).
+// Each workgroup is kParts parts of 4 waves over the same query rows and heads: part p
+// takes the p-th run of ceil(n / kParts) of the rows' n key tiles, each with its own
+// double-buffered K / V tiles, and the partial softmaxes are merged through LDS at the
+// end.  Splitting the keys four ways keeps the chain of tiles of the longest (last)
+// query rows short; one 16-wave workgroup fills a CU (4 waves per SIMD).
 //
-// Per 64-key step a wave reads its tile's bias entries from a 79-entry window of
-// its head's bias row kept in LDS as 4 copies shifted by 0..3 (every lane's four
-// consecutive entries are one aligned 16-byte read); the window is fetched with two
-// dword loads per lane.  Tile data and windows are fetched two steps ahead: the
-// loads issued in step i are written to LDS at the end of step i + 1.
-template <int HPW>  // query heads per half (the rest of a half's 4 waves take query blocks)
-__global__ void __launch_bounds__(512) chord_fwd_kernel(ChordArgs a) {
-  constexpr int QBPW = 4 / HPW;
+// A wave owns 32 score columns: 16 queries of two heads of the GQA group (HPW >= 2)
+// or 32 queries of one head, so S^T = K Q^T is a 32 x 32 accumulator per 32 keys.
+// Lane l owns column l % 32 (its query row and head), and its keys in each 32-key
+// sub-tile are 8 (r / 4) + 4 (l / 32) + r % 4: the row max is 16 in-lane values plus
+// one swap with lane l ^ 32, and P^T enters O^T += V^T P^T from the same registers.
+// Row sums of P (bf16, as P enters the output) by v_dot2 against ones.
+//
+// The GGD bias of a 64-key tile is read from a window of kappa GGD(key - q_abs) over the
+// distances the wave meets in that tile (63 + queries per wave entries per head),
+// evaluated in registers (one new entry per lane per tile: the window of tile t + 1
+// starts at entry 64 of tile t's) and kept in LDS, where every lane reads its 4
+// consecutive entries per key group with 4-byte loads.  Tile data
+// is fetched two steps ahead: the loads issued in step i are written to LDS at the
+// end of step i + 1.
+constexpr int kParts = 4;
+
+template <int HPW>  // query heads per part
+__global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 4))) chord_fwd_kernel(ChordArgs a) {
+  constexpr int RH = HPW >= 2 ? 2 : 1;  // heads per wave
+  constexpr int RQ = 32 / RH;           // queries per wave
+  constexpr int HGW = HPW / RH;         // head groups per part
+  constexpr int QW = (4 / HGW) * RQ;    // queries per workgroup
+  constexpr int kWin = 64 + RQ;         // bias window entries per copy (>= 63 + RQ)
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int half = wv >> 2, w = wv & 3;
-  const int htid = tid & 255;  // thread index inside the half
-  const int ln = lane & 15, g = lane >> 4;
+  const int part = wv >> 2, w = wv & 3;
+  const int htid = tid & 255;  // thread index inside the part
+  const int lc = lane & 31, hh = lane >> 5;
   const int group = a.H / a.Hkv;
-  const int hg = blockIdx.y, sq = blockIdx.z;
+  // grid (head groups, query blocks, sequences): the head groups vary fastest, so the
+  // dispatch order runs heaviest (latest) query blocks first across all heads
+  const int hg = blockIdx.x, sq = blockIdx.z;
 
   // Sequence geometry (padded batch row, or one packed sequence).
   int batch, tok0, Lq, Skv, q_start;
@@ -145,33 +162,30 @@ __global__ void __launch_bounds__(512) chord_fwd_kernel(ChordArgs a) {
   } else {
     batch = 0; tok0 = a.cu[sq]; Lq = a.cu[sq + 1] - tok0; Skv = Lq; q_start = 0;
   }
-  const int nqbg = (Lq + 16 * QBPW - 1) / (16 * QBPW);
-  if (static_cast<int>(blockIdx.x) >= nqbg) return;
-  const int qbg = nqbg - 1 - blockIdx.x;  // heaviest (latest) query blocks first
+  const int nqbg = (Lq + QW - 1) / QW;
+  if (static_cast<int>(blockIdx.y) >= nqbg) return;
+  const int qbg = nqbg - 1 - blockIdx.y;
 
-  const int head = hg * HPW + (w % HPW);
+  const int head0 = hg * HPW + (w % HGW) * RH;  // the wave's first head
+  const int cq = lc % RQ;                         // this lane's query inside the wave
+  const int head = head0 + lc / RQ;               // this lane's head
   const int kvh = (hg * HPW) / group;
-  const int q0 = (qbg * QBPW + w / HPW) * 16;
-  const int my_q = q0 + ln;  // this lane's query row (shared by its 4 lane groups)
+  const int q0 = qbg * QW + (w / HGW) * RQ;
+  const int my_q = q0 + cq;
   const bool q_valid = my_q < Lq;
 
-  const int wg_q_last = min(Lq, (qbg + 1) * QBPW * 16) - 1;
+  const int wg_q_last = min(Lq, (qbg + 1) * QW) - 1;
   const int kv_end = min(Skv, q_start + wg_q_last + 1);
   const int ntiles = (kv_end + kBN - 1) / kBN;
-  const int nsteps = (ntiles + 1) / 2;                   // tiles of half 0
-  const int t_first = half ? nsteps : 0;
-  const int t_count = half ? ntiles - nsteps : nsteps;   // half 1 may have one fewer
-  const int wave_kv_end = min(Skv, q_start + min(Lq, q0 + 16));
-  // Keys past the cache end are masked by the table unless a query sits past it.
-  const bool kmask = q_start + min(Lq, q0 + 16) > Skv;
+  const int nsteps = (ntiles + kParts - 1) / kParts;    // tiles of each part but the last ones
+  const int t_first = part * nsteps;
+  const int t_count = max(0, min(nsteps, ntiles - t_first));
+  const int wave_kv_end = min(Skv, q_start + min(Lq, q0 + RQ));
+  // Keys past the cache end are masked here unless no query sits past it.
+  const bool kmask = q_start + min(Lq, q0 + RQ) > Skv;
 
-  const bf16_t *qp = static_cast<const bf16_t *>(a.q) + batch * a.q_sb + head * a.q_sh + int64_t(tok0) * a.q_st;
   const bf16_t *kp = static_cast<const bf16_t *>(a.k) + batch * a.k_sb + kvh * a.k_sh + int64_t(tok0) * a.k_st;
   const bf16_t *vp = static_cast<const bf16_t *>(a.v) + batch * a.v_sb + kvh * a.v_sh + int64_t(tok0) * a.v_st;
-  // Range-checked buffers over the visible keys (rows past kv_end read 0).
-  const buf_t qbuf = make_buf(qp, Lq > 0 ? static_cast<uint32_t>(((Lq - 1) * a.q_st + kD) * 2) : 0u);
-  const buf_t kbuf = make_buf(kp, kv_end > 0 ? static_cast<uint32_t>(((kv_end - 1) * a.k_st + kD) * 2) : 0u);
-  const buf_t vbuf = make_buf(vp, kv_end > 0 ? static_cast<uint32_t>(((kv_end - 1) * a.v_st + kD) * 2) : 0u);
 
   // logit = a_row * acc (the prefill logit form above), a_row = |ssmax log_n scale|;
   // the kernel works in log2 units, p = exp2(A (acc - m)) with A = log2e a_row.
@@ -184,51 +198,68 @@ __global__ void __launch_bounds__(512) chord_fwd_kernel(ChordArgs a) {
   // finite logits A * acc that round to 0 against the max, as the exact 0 logits do.
   const float A = q_valid ? fmaxf(a_head * lnv, 1e-30f) : 1.f;
 
-  // rho Q^T as the B operand: lane holds rho Q[my_q][32 ks + 8g .. +8] (exact: rho in {-1, 0, 1}).
-  bf16x8 qreg[2];
+  // rho Q^T as the B operand: lane holds rho Q[my_q][16 ds + 8 hh .. +8] of its head
+  // (exact: rho in {-1, 0, 1}); rows past Lq are zero.
+  bf16x8 qreg[4];
+  {
+    const bf16_t *qrow = static_cast<const bf16_t *>(a.q) + batch * a.q_sb + head * a.q_sh +
+                         int64_t(tok0 + min(my_q, max(Lq - 1, 0))) * a.q_st;
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    uint4 u = buf_ld16(qbuf, (my_q * a.q_st + 32 * ks + 8 * g) * 2);
-    if (rho < 0.f) { u.x ^= 0x80008000u; u.y ^= 0x80008000u; u.z ^= 0x80008000u; u.w ^= 0x80008000u; }
-    else if (rho == 0.f) u = uint4{0u, 0u, 0u, 0u};
-    qreg[ks] = __builtin_bit_cast(bf16x8, u);
+    for (int ds = 0; ds < 4; ++ds) {
+      uint4 u = *reinterpret_cast<const uint4 *>(qrow + 16 * ds + 8 * hh);
+      if (rho < 0.f) { u.x ^= 0x80008000u; u.y ^= 0x80008000u; u.z ^= 0x80008000u; u.w ^= 0x80008000u; }
+      if (rho == 0.f || !q_valid) u = uint4{0u, 0u, 0u, 0u};
+      qreg[ds] = __builtin_bit_cast(bf16x8, u);
+    }
   }
 
-  __shared__ __attribute__((aligned(16))) bf16_t sK[2][2][kBN * kD];   // [half][buffer] K rows (swizzled)
-  __shared__ __attribute__((aligned(16))) bf16_t sV[2][2][kD * kBN];   // V^T rows, keys in vperm order (swizzled)
-  __shared__ __attribute__((aligned(16))) float sB[8][4 * 80];         // per wave: 4 shifted bias windows
+  // [part][buffer] K rows and V^T rows (keys in vperm32 order), then per wave a window
+  // per head (at least 128 floats: the merge keeps (l, m) there); the merge puts the
+  // output partials of parts 1.. over the K / V buffers
+  constexpr int kTile = kBN * kRow;  // bf16 elements of one K (or V^T) buffer
+  constexpr int kWinF = RH * kWin > 128 ? RH * kWin : 128;
+  __shared__ __attribute__((aligned(16))) bf16_t sKV[2][kParts][2][kTile];
+  __shared__ __attribute__((aligned(16))) float sB[4 * kParts][kWinF];
+  bf16_t (*sK)[2][kTile] = sKV[0];
+  bf16_t (*sV)[2][kTile] = sKV[1];
 
-  // Bias window of tile t: entry j (0..78) serves key n0 + 16 kt + 4 g + r of row ln with
-  // j = 16 kt + 4 g + r + 15 - ln, i.e. distance key - q_abs = t kBN - q_start - q0 - 15 + j.
-  // Lane l computes entries l and 64 + l in registers: kappa * GGD(distance) for
-  // distance <= 0 and -inf past the diagonal (the causal mask), kappa = sign(ssmax) /
-  // |scale| (sign(ssmax) when scale == 0).  Nothing of the bias is stored in HBM.
-  const float g_alpha = a.alpha[head], g_beta = a.beta[head], g_mu = a.mu[head];
-  const float kappa = a.scale != 0.f ? sg / fabsf(a.scale) : sg;
-  const int dist0 = -q_start - q0 - 15 + lane;
-  // Entry 64 + l of tile t is entry l of tile t + 1, so after the first tile each
-  // step evaluates one new distance per lane and shifts the other.
-  auto eval_bias = [&](int dist) {
-    return dist <= 0 ? kappa * ggd_bias(static_cast<float>(dist), g_alpha, g_beta, g_mu, a.eps) : -INFINITY;
+  // Bias window of tile t for wave head hw: entry j (0 .. 63 + RQ - 1) is distance
+  // key - q_abs = t kBN - q_start - q0 - (RQ - 1) + j; lane l computes entries l and
+  // 64 + l: kappa GGD(distance) for distance <= 0 and -inf past the diagonal (the
+  // causal mask), kappa = sign(ssmax) / |scale| (sign(ssmax) when scale == 0).
+  const int dist0 = -q_start - q0 - (RQ - 1) + lane;
+  float gal[RH], gbe[RH], gmu[RH], gka[RH];
+#pragma unroll
+  for (int hw = 0; hw < RH; ++hw) {
+    gal[hw] = a.alpha[head0 + hw];
+    gbe[hw] = a.beta[head0 + hw];
+    gmu[hw] = a.mu[head0 + hw];
+    const float sgh = a.ssmax[head0 + hw] < 0.f ? -1.f : 1.f;
+    gka[hw] = a.scale != 0.f ? sgh / fabsf(a.scale) : sgh;
+  }
+  auto eval_bias = [&](int hw, int dist) {
+    return dist <= 0 ? gka[hw] * ggd_bias(static_cast<float>(dist), gal[hw], gbe[hw], gmu[hw], a.eps) : -INFINITY;
   };
-  float bwin[2] = {eval_bias(t_first * kBN + dist0), eval_bias(t_first * kBN + dist0 + 64)};
-  // Copy c (80 floats; a stride of 20 16-byte units keeps the reads free of bank
-  // conflicts) holds entry j at position j - c.  Reads stay at positions <= 75; the
-  // stores of entries no lane reads (lane < c, lane 15) land at positions >= 76 of
-  // the previous copy or this one.
+  float bwin[RH][2];
+#pragma unroll
+  for (int hw = 0; hw < RH; ++hw) {
+    bwin[hw][0] = eval_bias(hw, t_first * kBN + dist0);
+    bwin[hw][1] = eval_bias(hw, t_first * kBN + dist0 + 64);
+  }
+  // (entries past 63 + RQ - 1 are never read)
   float *bw = &sB[wv][0];
   auto store_window = [&]() {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) bw[79 * c + lane] = bwin[0];
-    if (lane < 16) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) bw[79 * c + 64 + lane] = bwin[1];
+    for (int hw = 0; hw < RH; ++hw) {
+      bw[hw * kWin + lane] = bwin[hw][0];
+      if (lane < RQ) bw[hw * kWin + 64 + lane] = bwin[hw][1];
     }
   };
-  // this lane's bias entries of tile kt: bwr[16 kt .. +3]
-  const float *bwr = bw + 79 * ((15 - ln) & 3) + 4 * g + 15 - ln;
+  // This lane's entries for keys 32 kt + 8 q4 + 4 hh + (0..3): j = 32 kt + 8 q4 + jb0 + p
+  // with jb0 = 4 hh - cq + RQ - 1.
+  const float *bwr = bw + (lc / RQ) * kWin + 4 * hh - cq + RQ - 1;
 
-  // Tile staging by the half's 256 threads: K rows (2 x 16 B per thread); V as key
+  // Tile staging by the part's 256 threads: K rows (2 x 16 B per thread); V as key
   // pairs (2 keys x 8 d).  The per-lane offsets are fixed; step t moves the buffer
   // base to its first key (the range shrinks with it, so keys past kv_end read 0).
   uint4 kst[2], vst[2];
@@ -249,39 +280,30 @@ __global__ void __launch_bounds__(512) chord_fwd_kernel(ChordArgs a) {
     vst[0] = buf_ld16(vr, voff);
     vst[1] = buf_ld16(vr, voff2);
   };
-  // K rows (c >> 3) and (c >> 3) + 32 of this thread, V^T rows 8 vseg + m (m = 0..7)
-  const int ks_off = swz(htid >> 3, (htid & 7) * 8);
-  const int vcol = vperm(2 * vpair);
-  int vs_off[8];
-#pragma unroll
-  for (int m = 0; m < 8; ++m) vs_off[m] = swz(8 * vseg + m, vcol);
+  // K rows (htid >> 3) and (htid >> 3) + 32 of this thread, V^T rows 8 vseg + m
+  const int ks_off = (htid >> 3) * kRow + (htid & 7) * 8;
+  const int vs_off = 8 * vseg * kRow + vperm32(2 * vpair);
   auto store_tile = [&](auto bufc) {
     constexpr int buf = decltype(bufc)::value;
-    *reinterpret_cast<uint4 *>(&sK[half][buf][ks_off]) = kst[0];
-    *reinterpret_cast<uint4 *>(&sK[half][buf][ks_off + 32 * 64]) = kst[1];
+    *reinterpret_cast<uint4 *>(&sK[part][buf][ks_off]) = kst[0];
+    *reinterpret_cast<uint4 *>(&sK[part][buf][ks_off + 32 * kRow]) = kst[1];
     const uint32_t *v0 = reinterpret_cast<const uint32_t *>(&vst[0]);
     const uint32_t *v1 = reinterpret_cast<const uint32_t *>(&vst[1]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t lo = (v0[i] & 0xffffu) | (v1[i] << 16);      // d = 8 vseg + 2i
       const uint32_t hi = (v0[i] >> 16) | (v1[i] & 0xffff0000u);  // d = 8 vseg + 2i + 1
-      *reinterpret_cast<uint32_t *>(&sV[half][buf][vs_off[2 * i]]) = lo;
-      *reinterpret_cast<uint32_t *>(&sV[half][buf][vs_off[2 * i + 1]]) = hi;
+      *reinterpret_cast<uint32_t *>(&sV[part][buf][vs_off + (2 * i) * kRow]) = lo;
+      *reinterpret_cast<uint32_t *>(&sV[part][buf][vs_off + (2 * i + 1) * kRow]) = hi;
     }
   };
-  // operand reads: rows 16 kt + ln (K) / 16 mt + ln (V^T), 16-byte pieces g and 4 + g
-  const int rd0 = swz(ln, 8 * g), rd1 = swz(ln, 32 + 8 * g);
 
-  float m_run = -INFINITY;  // in acc units
-  // O^T accumulators (tiles 0..3) and a fifth tile that multiplies P by ones: its
-  // entries are the row sums of P (bf16-rounded, as used in the output), so the
-  // normaliser follows the rescales of the output for free.
-  f32x4 oacc[5];
-#pragma unroll
-  for (int mt = 0; mt < 5; ++mt) oacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  bf16x8 ones;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) ones[i] = static_cast<__bf16>(1.f);
+  float m_run = -INFINITY;  // in acc units, per column (both lane halves agree)
+  float l_run = 0.f;        // this lane's share of the column's row sum of P
+  f32x16 oacc[2];           // O^T rows d = 32 dt + 8 (r / 4) + 4 hh + r % 4, column lc
+  oacc[0] = f32x16{};
+  oacc[1] = f32x16{};
+  const bf16x2v ones2 = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
 
   // Prologue: tile and window of the first step in LDS, the second step's in flight.
   // Every load and store of the loop is unconditional (tiles and entries past the end
@@ -297,75 +319,82 @@ __global__ void __launch_bounds__(512) chord_fwd_kernel(ChordArgs a) {
   auto step = [&](int i, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
     const int n0 = (t_first + i) * kBN;
-    // the new entry of the next step's window, evaluated ahead of this step's work
-    const float bnew = eval_bias(n0 + 2 * kBN + dist0);
+    // the new entries of the next step's windows, evaluated ahead of this step's work
+    float bnew[RH];
+#pragma unroll
+    for (int hw = 0; hw < RH; ++hw) bnew[hw] = eval_bias(hw, n0 + 2 * kBN + dist0);
     if (i < t_count && n0 < wave_kv_end) {
-      // acc^T = bias + rho K Q^T: tile kt holds key n0 + 16 kt + 4g + r of row ln.
-      f32x4 sacc[4];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        const f32x4 bias = *reinterpret_cast<const f32x4 *>(bwr + 16 * kt);
-        const bf16x8 k0 = *reinterpret_cast<const bf16x8 *>(&sK[half][buf][rd0 + 1024 * kt]);
-        const bf16x8 k1 = *reinterpret_cast<const bf16x8 *>(&sK[half][buf][rd1 + 1024 * kt]);
-        sacc[kt] = mma16(k1, qreg[1], mma16(k0, qreg[0], bias));
-      }
-      if (kmask && n0 + kBN > Skv) {
+      for (int kt = 0; kt < 2; ++kt) {
+        // acc^T = bias + rho K Q^T over keys n0 + 32 kt + ..
+        f32x16 acc;
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+        for (int q4 = 0; q4 < 4; ++q4)
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (n0 + 16 * kt + 4 * g + r >= Skv) sacc[kt][r] = -INFINITY;
-      }
-      float mx = -INFINITY;
+          for (int p4 = 0; p4 < 4; ++p4) acc[4 * q4 + p4] = bwr[32 * kt + 8 * q4 + p4];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sacc[kt][r]);
-      mx = max_lane_groups(mx);
-      // Lazy rescaling: the running max moves only when the tile exceeds it by more
-      // than 8 (log2 units of the logits), so p <= 2^8 and most tiles skip the
-      // rescale of the output accumulators.
-      const bool grow = A * (mx - m_run) > 8.f || m_run == -INFINITY;
-      const float m_new = grow ? mx : m_run;
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float resc = m_run == -INFINITY ? 0.f : fast_exp2(A * (m_run - m_use));
-      const float nb = -A * m_use;
-      // p = exp2(A (acc - m)); masked keys (acc = -inf) give exactly 0.
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sacc[kt][r] = fast_exp2(fmaf(sacc[kt][r], A, nb));
-      if (__builtin_amdgcn_read_exec() & __ballot(grow)) {
-#pragma unroll
-        for (int mt = 0; mt < 5; ++mt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) oacc[mt][r] *= resc;
-      }
-      m_run = m_new;
-
-      // O^T += V^T P^T: P^T from two accumulator tiles per 32-key step.
-#pragma unroll
-      for (int kp2 = 0; kp2 < 2; ++kp2) {
-        bf16x8 pb;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          pb[r] = to_bf(sacc[2 * kp2][r]);
-          pb[4 + r] = to_bf(sacc[2 * kp2 + 1][r]);
+        for (int ds = 0; ds < 4; ++ds) {
+          const bf16x8 kop = *reinterpret_cast<const bf16x8 *>(&sK[part][buf][(32 * kt + lc) * kRow + 16 * ds + 8 * hh]);
+          acc = mma32(kop, qreg[ds], acc);
         }
+        if (kmask && n0 + 32 * kt + 32 > Skv) {
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          const bf16x8 va = *reinterpret_cast<const bf16x8 *>(&sV[half][buf][(kp2 ? rd1 : rd0) + 1024 * mt]);
-          oacc[mt] = mma16(va, pb, oacc[mt]);
+          for (int r = 0; r < 16; ++r)
+            if (n0 + 32 * kt + 8 * (r >> 2) + 4 * hh + (r & 3) >= Skv) acc[r] = -INFINITY;
         }
-        oacc[4] = mma16(ones, pb, oacc[4]);  // every row of tile 4: the row sum of P
+        float mx = acc[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, acc[r]);
+        {
+          const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+          mx = fmaxf(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
+        }
+        // Lazy rescaling: the running max moves only when the sub-tile exceeds it by
+        // more than 8 (log2 units of the logits), so p <= 2^8 and most sub-tiles skip
+        // the rescale of the output accumulators.
+        const bool grow = A * (mx - m_run) > 8.f || m_run == -INFINITY;
+        const float m_new = grow ? mx : m_run;
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        const float resc = m_run == -INFINITY ? 0.f : fast_exp2(A * (m_run - m_use));
+        const float nb = -A * m_use;
+        if (__builtin_amdgcn_read_exec() & __ballot(grow)) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            oacc[0][r] *= resc;
+            oacc[1][r] *= resc;
+          }
+          l_run *= resc;
+        }
+        m_run = m_new;
+        // p = exp2(A (acc - m)); masked keys (acc = -inf) give exactly 0.  P^T k-steps
+        // 2 kt and 2 kt + 1 are registers 0..7 and 8..15.
+#pragma unroll
+        for (int hk = 0; hk < 2; ++hk) {
+          uint32_t pw[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            pw[e] = pk2bf(fast_exp2(fmaf(acc[8 * hk + 2 * e], A, nb)), fast_exp2(fmaf(acc[8 * hk + 2 * e + 1], A, nb)));
+            l_run = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, pw[e]), ones2, l_run, false);
+          }
+          const bf16x8 pb = __builtin_bit_cast(bf16x8, uint4{pw[0], pw[1], pw[2], pw[3]});
+          const int ks = 2 * kt + hk;
+#pragma unroll
+          for (int dt = 0; dt < 2; ++dt) {
+            const bf16x8 va = *reinterpret_cast<const bf16x8 *>(&sV[part][buf][(32 * dt + lc) * kRow + 16 * ks + 8 * hh]);
+            oacc[dt] = mma32(va, pb, oacc[dt]);
+          }
+        }
       }
     }
 
-    // The next step's window and tile (fetched one step ago) into LDS, the tile after
+    // The next step's windows and tile (fetched one step ago) into LDS, the tile after
     // into flight.  The window region is this wave's own (its reads above come first
     // in program order); the tile buffer was last read before the previous barrier.
-    bwin[0] = bwin[1];
-    bwin[1] = bnew;
+#pragma unroll
+    for (int hw = 0; hw < RH; ++hw) {
+      bwin[hw][0] = bwin[hw][1];
+      bwin[hw][1] = bnew[hw];
+    }
     store_window();
     store_tile(std::integral_constant<int, buf ^ 1>());
     load_tile(t_first + i + 2);
@@ -378,37 +407,58 @@ __global__ void __launch_bounds__(512) chord_fwd_kernel(ChordArgs a) {
   }
   if (i < nsteps) step(i, std::integral_constant<int, 0>());
 
-  // Merge: half 1 leaves O in its K buffers (4 waves x 16 x 64 floats = sK[1]) and
-  // (l, m) in its window region; half 0 combines them with its own and writes the rows.
-  float *mo = reinterpret_cast<float *>(&sK[1][0][0]) + w * 16 * 64 + lane;
-  float *mlm = &sB[4 + w][lane];
-  if (half == 1) {
+  // The column's row sum: this lane's keys plus those of lane l ^ 32.
+  {
+    const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+    l_run = __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
+  }
+
+  // Merge: parts 1.. leave O^T (32 floats per lane) over the K / V buffers and (l, m)
+  // in their window rows; part 0 combines them and writes the rows.
+  float *mo = reinterpret_cast<float *>(&sKV[0][0][0][0]) + lane;  // [(part - 1) * 4 + w][32][64]
+  if (part > 0) {
+    float *dst = mo + ((part - 1) * 4 + w) * 32 * 64;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) mo[j * 64] = oacc[j >> 2][j & 3];
-    mlm[0] = oacc[4][0];
-    mlm[64] = m_run;
+    for (int r = 0; r < 16; ++r) {
+      dst[r * 64] = oacc[0][r];
+      dst[(16 + r) * 64] = oacc[1][r];
+    }
+    sB[wv][lane] = l_run;
+    sB[wv][64 + lane] = m_run;
   }
   __syncthreads();
-  if (half == 0 && q_valid) {
-    const float lB = mlm[0], mB = mlm[64];
-    const float m = fmaxf(m_run, mB);
-    const float fA = m_run == -INFINITY ? 0.f : fast_exp2(A * (m_run - m));
-    const float fB = mB == -INFINITY ? 0.f : fast_exp2(A * (mB - m));
-    const float l = oacc[4][0] * fA + lB * fB;
+  if (part == 0 && q_valid) {
+    float m = m_run;
+#pragma unroll
+    for (int p = 1; p < kParts; ++p) m = fmaxf(m, sB[4 * p + w][64 + lane]);
+    float f[kParts];
+    f[0] = m_run == -INFINITY ? 0.f : fast_exp2(A * (m_run - m));
+    float l = l_run * f[0];
+#pragma unroll
+    for (int p = 1; p < kParts; ++p) {
+      const float mp = sB[4 * p + w][64 + lane];
+      f[p] = mp == -INFINITY ? 0.f : fast_exp2(A * (mp - m));
+      l += sB[4 * p + w][lane] * f[p];
+    }
     const float inv = 1.f / fmaxf(l, 1e-20f);
     bf16_t *op = static_cast<bf16_t *>(a.out) + batch * a.o_sb + head * a.o_sh + int64_t(tok0 + my_q) * a.o_st;
-    // lane holds O[my_q][16 mt + 4g + r]
+    // lane holds O[my_q][32 dt + 8 q4 + 4 hh + (0..3)]
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      float o[4];
+    for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) o[r] = (oacc[mt][r] * fA + mo[(4 * mt + r) * 64] * fB) * inv;
-      uint2 pk;
-      pk.x = static_cast<uint32_t>(f32_to_bf16(o[0])) | (static_cast<uint32_t>(f32_to_bf16(o[1])) << 16);
-      pk.y = static_cast<uint32_t>(f32_to_bf16(o[2])) | (static_cast<uint32_t>(f32_to_bf16(o[3])) << 16);
-      *reinterpret_cast<uint2 *>(op + 16 * mt + 4 * g) = pk;
-    }
-    if (a.lse && g == 0)
+      for (int q4 = 0; q4 < 4; ++q4) {
+        float o[4];
+#pragma unroll
+        for (int p4 = 0; p4 < 4; ++p4) {
+          const int r = 4 * q4 + p4;
+          float x = oacc[dt][r] * f[0];
+#pragma unroll
+          for (int p = 1; p < kParts; ++p) x += mo[(((p - 1) * 4 + w) * 32 + 16 * dt + r) * 64] * f[p];
+          o[p4] = x * inv;
+        }
+        *reinterpret_cast<uint2 *>(op + 32 * dt + 8 * q4 + 4 * hh) = uint2{pk2bf(o[0], o[1]), pk2bf(o[2], o[3])};
+      }
+    if (a.lse && hh == 0)
       a.lse[(static_cast<size_t>(batch) * a.H + head) * a.L + tok0 + my_q] = A * (m == -INFINITY ? 0.f : m) + fast_log2(l);
   }
 }
@@ -1101,13 +1151,15 @@ extern "C" int motif_chord_fwd(
   }
 
   const int hpw = (group % 4 == 0) ? 4 : (group % 2 == 0) ? 2 : 1;
-  const int qbpw = 4 / hpw;
+  // queries per workgroup: 4 waves x 32 columns per half, the columns being 16 queries
+  // of two heads (hpw >= 2) or 32 queries of one head
+  const int qw = hpw == 4 ? 32 : hpw == 2 ? 64 : 128;
   const int maxlen = packed ? max_seqlen : L;
   if (maxlen <= 0) return MOTIF_OK;
   if (std::max<int64_t>(S, int64_t(q_start) + L) > (int64_t(1) << 28))
     return set_error(MOTIF_ERR_UNSUPPORTED, "chord_fwd: sequence too long");
-  const int nqbg = (maxlen + 16 * qbpw - 1) / (16 * qbpw);
-  dim3 grid(nqbg, H / hpw, packed ? nseq : B), block(512);
+  const int nqbg = (maxlen + qw - 1) / qw;
+  dim3 grid(H / hpw, nqbg, packed ? nseq : B), block(256 * kParts);
   if (hpw == 4) chord_fwd_kernel<4><<<grid, block, 0, s>>>(a);
   else if (hpw == 2) chord_fwd_kernel<2><<<grid, block, 0, s>>>(a);
   else chord_fwd_kernel<1><<<grid, block, 0, s>>>(a);

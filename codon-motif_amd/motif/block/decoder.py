@@ -13,8 +13,7 @@ from motif.model.cache import DecoderBlockCache, GatedDeltaAttentionLayerCache, 
 from motif.model.config import MotifChordConfig
 from motif.ops import RMSNorm
 from motif.ops.attn_res import apply_block_attn_res, attn_res_read_norms
-from motif.ops.epilogue import add_fold, usable
-from motif.ops.linear_rows import MAX_ROWS, linear_rows_dual, linear_rows_pair, rows_eligible
+from motif.ops.linear_rows import linear_rows_dual, linear_rows_pair, rows_eligible
 
 
 @dataclass
@@ -45,32 +44,6 @@ class Decoder(nn.Module):
     @property
     def cache_type(self):
         return KVLayerCache if self.attn_type == 'chord' else GatedDeltaAttentionLayerCache
-
-
-_SIDE_STREAMS = {}
-
-
-def _side_stream(x):
-    '''A second stream of x's device (default priority) for the MLP branch, or None when
-    the branches run in sequence (CPU tensors, autograd, decode-sized inputs).'''
-    # decode-sized inputs keep the MLP in sequence: its down projection then folds the
-    # residual and the block sum in its epilogue (fewer launches than the overlap saves)
-    if not x.is_cuda or torch.is_grad_enabled() or x.numel() // x.shape[-1] <= MAX_ROWS:
-        return None
-    dev = x.device
-    s = _SIDE_STREAMS.get(dev)
-    if s is None:
-        s = torch.cuda.Stream(device=dev)
-        _SIDE_STREAMS[dev] = s
-    return s
-
-
-def _fold(attn, mlp, partial):
-    '''(f, p) = (attn + mlp, partial + f); p None when partial is None or on the torch
-    fallback (the cache then folds f itself).'''
-    if attn.shape == mlp.shape and usable(attn, mlp) and (partial is None or usable(partial)):
-        return add_fold(attn, mlp, partial)
-    return attn + mlp, None
 
 
 def _split_step(decoder, x, m, layer_cache, mask, position, prev):
@@ -143,25 +116,19 @@ class DecoderBlock(nn.Module):
                                  f'{len(self.features)} layers')
         use_attn_cache = cu_seqlens is None and len(cache.attn) == len(self.features)
 
-        side = _side_stream(hidden_states)
+        # The attention and MLP branches of a layer run in sequence on the current stream.
+        # (The MLP on a second stream overlapped little, now and then let a prefill read
+        # memory that the other stream had taken over, and kept whole-CU attention
+        # workgroups waiting for CUs.)
         for i, decoder in enumerate(self.features):
             x, m = self._read(attn_res, i, decoder)
-            if use_attn_cache and side is None:
+            if use_attn_cache:
                 prev = attn_res.partial_block
                 done = _split_step(decoder, x, m, cache.attn[i], mask, position,
                                    prev if prev is not None and prev.shape == m.shape else None)
                 if done is not None:
                     attn_res.update_increment(*done)
                     continue
-            mlp_out = None
-            if side is not None:
-                # The MLP branch depends only on h: it runs on a second stream while the
-                # attention runs on this one (joined before the residual add).
-                main = torch.cuda.current_stream()
-                side.wait_stream(main)
-                with torch.cuda.stream(side):
-                    mlp_out = decoder.mlp(m)
-                m.record_stream(side)
             if cu_seqlens is not None:
                 attn_out = decoder.attn.forward_varlen(x, cu_seqlens)
             elif isinstance(decoder.attn, ChordAttention):
@@ -171,12 +138,7 @@ class DecoderBlock(nn.Module):
                 attn_out = decoder.attn(hidden_states=x, past_key_value=cache.attn[i] if use_attn_cache else None)
             prev = attn_res.partial_block
             prev = prev if prev is not None and prev.shape == attn_out.output.shape else None
-            if mlp_out is not None:
-                main.wait_stream(side)
-                mlp_out.record_stream(main)
-                f_h, partial = _fold(attn_out.output, mlp_out, prev)
-            else:
-                f_h, partial = decoder.mlp.forward_residual(m, attn_out.output, prev)
+            f_h, partial = decoder.mlp.forward_residual(m, attn_out.output, prev)
             if use_attn_cache:
                 cache.attn[i] = attn_out.past_key_value
             attn_res.update_increment(f_h, partial)

@@ -74,12 +74,14 @@ class DecodeGraph:
         kv = [lc for lc in cache.layer_caches() if isinstance(lc, StaticKVLayerCache)]
         for lc in kv:
             lc.cursor_steps = 0
-        # warm-up on a side stream (lazy set-up: fused weights, workspaces, tables), undone
-        side = torch.cuda.Stream(device=device)
-        side.wait_stream(torch.cuda.current_stream(device))
-        with torch.no_grad(), torch.cuda.stream(side):
+        # warm-up step (lazy set-up: fused weights, workspaces, tables), undone after.  It
+        # runs on the current stream, so the tensors it creates and keeps (cached fused
+        # weights, the decode workspaces) belong to the pool of the stream that later uses
+        # them: the caching allocator then cannot hand their memory to another stream while
+        # this one's kernels may still read it.  (With the warm-up on a side stream, runs
+        # after a capture now and then differed from the same runs before it.)
+        with torch.no_grad():
             model(self.tokens, cache=cache)
-        torch.cuda.current_stream(device).wait_stream(side)
         snap.restore_device()
         snap.restore_host()
         if any(lc.cursor_steps != 1 for lc in kv):
