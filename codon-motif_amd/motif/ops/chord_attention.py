@@ -10,8 +10,11 @@ the vector kernel for every shape (fp32 FMA throughout, the accuracy mode).
 `apply_chord_attention_varlen` adds packed sequences (new) and
 `chord_decode_cursor` the decode step over a fixed-capacity cache whose length
 lives on the device (new; the graph-replayable form of the decode call).
-Calls that need gradients take the differentiable torch forms
-(motif/ops/autograd_path.py); the kernels are forward-only.
+Calls that need gradients run `ChordFunction` (bf16, head dim 64, padded batch): the
+forward kernel with its log-sum-exp, then the backward kernels (motif_chord_bwd: dq, dk,
+dv and the four per-head parameter gradients, the reference's custom backward
+:1348-1554).  Other gradient calls take the differentiable torch forms
+(motif/ops/autograd_path.py).
 '''
 from typing import Optional
 
@@ -22,6 +25,69 @@ from .autograd_path import chord_attention_torch, chord_attention_varlen_torch, 
 
 HEAD_DIM = 64                  # the model's head dim: bf16 runs on the MFMA kernels
 HEAD_DIMS = (16, 32, 64, 128)  # head dims the kernels serve (fp32 / fp16 / other D: the vector kernel)
+
+
+def _grad_kernels_serve(q, k, v, alpha, beta, mu, ssmax, log_n, q_start):
+    '''The backward kernels take bf16 q / k / v with head dim 64 on a GPU, fp32 [H]
+    parameters and no gradient into log_n (as the reference's backward).'''
+    if not (q.is_cuda and q.dtype == torch.bfloat16 and k.dtype == q.dtype and v.dtype == q.dtype
+            and q.dim() == 4 and q.shape[-1] == HEAD_DIM and k.shape == v.shape and k.shape[-1] == HEAD_DIM
+            and _lib.available()):
+        return False
+    if log_n.requires_grad or any(t.dtype != torch.float32 or t.dim() != 1 for t in (alpha, beta, mu, ssmax)):
+        return False
+    S, L = k.shape[2], q.shape[2]
+    qs = S - L if q_start is None else int(q_start)
+    return 0 <= qs and qs + L <= S and log_n.dtype == torch.float32 and log_n.shape == (q.shape[0], L)
+
+
+class ChordFunction(torch.autograd.Function):
+    '''Chord attention with the HIP forward (which also writes the base-2 log-sum-exp)
+    and the HIP backward (motif_chord_bwd), the reference's `_TritonChordFunction`
+    (motif/ops/chord_attention.py:1475-1554): gradients for q, k, v, alpha, beta, mu and
+    ssmax; none for log_n.'''
+
+    @staticmethod
+    def forward(ctx, q, k, v, alpha, beta, mu, ssmax, log_n, q_start, scale, eps):
+        B, H, L, D = q.shape
+        q, k, v = _aligned(q.contiguous()), _aligned(k.contiguous()), _aligned(v.contiguous())
+        params = [t.detach().contiguous() for t in (alpha, beta, mu, ssmax)]
+        ln = log_n.detach().contiguous()
+        out = torch.empty((B, H, L, D), dtype=q.dtype, device=q.device)
+        lse = torch.empty((B, H, L), dtype=torch.float32, device=q.device)
+        if L > 0:
+            _launch(q, k, v, *params, ln, q_start, scale, eps, out, lse)
+        ctx.save_for_backward(q, k, v, out, lse, *params, ln)
+        ctx.q_start, ctx.scale, ctx.eps = q_start, scale, eps
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, lse, alpha, beta, mu, ssmax, ln = ctx.saved_tensors
+        B, H, L, D = q.shape
+        Hkv, S = k.shape[1], k.shape[2]
+        dout = _aligned(dout.contiguous())
+        dq, dk, dv = torch.empty_like(q), torch.zeros_like(k), torch.zeros_like(v)
+        lib = _lib.lib()
+        npart = int(lib.motif_chord_bwd_dparam_len(B, H, L))
+        part = torch.empty(max(npart, 1), dtype=torch.float32, device=q.device)
+        ws = torch.empty(max(int(lib.motif_chord_bwd_workspace_bytes(B, H, L)), 1), dtype=torch.uint8, device=q.device)
+        rc = lib.motif_chord_bwd(
+            *_lib.t4(q), *_lib.t4(k), *_lib.t4(v), *_lib.t4(out), *_lib.t4(dout),
+            lse.data_ptr(), alpha.data_ptr(), beta.data_ptr(), mu.data_ptr(), ssmax.data_ptr(),
+            ln.data_ptr(), ln.stride(0), ln.stride(1),
+            *_lib.t4(dq), *_lib.t4(dk), *_lib.t4(dv), part.data_ptr(),
+            B, H, Hkv, L, S, D, int(ctx.q_start), float(ctx.scale), float(ctx.eps),
+            ws.data_ptr(), ws.numel(), _lib.chord_dtype_code(q.dtype), _lib.stream_ptr(q.device))
+        _lib.check(rc, 'motif_chord_bwd')
+        if npart:
+            d_params = part[:npart].view(-1, H, 4).sum(0)
+        else:
+            d_params = torch.zeros(H, 4, dtype=torch.float32, device=q.device)
+        needs = ctx.needs_input_grad
+        grads = [dq, dk, dv] + [d_params[:, i].contiguous() for i in range(4)]
+        grads = [g if needs[i] else None for i, g in enumerate(grads)]
+        return (*grads, None, None, None, None)
 
 
 def _check_tensors(q, k, v, log_n):
@@ -138,9 +204,12 @@ def apply_chord_attention(
         RuntimeError: when the HIP library is unavailable or a launch fails.
     '''
     if wants_grad(q, k, v, alpha, beta, mu, ssmax, log_n):
-        # forward-only kernels: training takes the differentiable torch form
         if q_start is not None and int(q_start) < 0:
             raise ValueError(f'q_start must not be negative, got {q_start}')
+        if _grad_kernels_serve(q, k, v, alpha, beta, mu, ssmax, log_n, q_start):
+            scale = q.shape[-1] ** -0.5 if softmax_scale is None else float(softmax_scale)
+            qs = k.shape[2] - q.shape[2] if q_start is None else int(q_start)
+            return ChordFunction.apply(q, k, v, alpha, beta, mu, ssmax, log_n, qs, scale, float(eps))
         return chord_attention_torch(q, k, v, alpha, beta, mu, ssmax, log_n, q_start, softmax_scale, eps)
     if not _lib.available():
         raise RuntimeError('there is no usable HIP backend in the current environment')

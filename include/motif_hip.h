@@ -240,6 +240,34 @@ int motif_chord_fwd(
     int dtype, void *stream);
 
 /*
+ * Chord attention backward: dq, dk, dv of the forward above and the per-head partial
+ * sums of d alpha, d beta, d mu, d ssmax.  Replaces the reference's custom backward
+ * motif/ops/chord_attention.py:1348-1470 `_chord_backward_impl` (kernels :518-949,
+ * called from `_TritonChordFunction.backward` :1520-1554).
+ *   q, out, dout, dq [B,H,L,D]; k, v, dk, dv [B,Hkv,S,D] (bf16, D == 64, padded batch)
+ *   lse [B,H,L] fp32: the forward's base-2 log-sum-exp.
+ *   dparam_partial: motif_chord_bwd_dparam_len(B, H, L) floats laid out
+ *   [B][ceil(L / 128)][H][4] (alpha, beta, mu, ssmax); the caller sums them over the first
+ *   two axes.  workspace: motif_chord_bwd_workspace_bytes(B, H, L) bytes (row sums
+ *   dout . out).  Needs 0 <= q_start and q_start + L <= S.
+ */
+size_t motif_chord_bwd_workspace_bytes(int B, int H, int L);
+size_t motif_chord_bwd_dparam_len(int B, int H, int L);
+int motif_chord_bwd(
+    const void *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void *k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void *v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    const void *out, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    const void *dout, int64_t d_sb, int64_t d_sh, int64_t d_st,
+    const float *lse, const float *alpha, const float *beta, const float *mu, const float *ssmax,
+    const float *log_n, int64_t ln_sb, int64_t ln_st,
+    void *dq, int64_t dq_sb, int64_t dq_sh, int64_t dq_st,
+    void *dk, int64_t dk_sb, int64_t dk_sh, int64_t dk_st,
+    void *dv, int64_t dv_sb, int64_t dv_sh, int64_t dv_st,
+    float *dparam_partial, int B, int H, int Hkv, int L, int S, int D, int q_start, float scale, float eps,
+    void *workspace, size_t workspace_bytes, int dtype, void *stream);
+
+/*
  * One decode step of a GatedDeltaAttention layer after its input projections, fused:
  * conv + SiLU of the new token (q, k, v), q / k L2 normalisation (q * dk^-1/2), gates
  * beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias), the delta-rule update of the
