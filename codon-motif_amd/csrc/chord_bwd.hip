@@ -15,9 +15,11 @@
 // query column l % 32, so the row values -- Delta, the log-sum-exp, c -- are scalars per
 // lane), dQ^T += K^T (s c dZ)^T from the same registers.  It also computes Delta (written
 // for the second kernel) and per-workgroup partial sums of the four parameter gradients.
-// chord_bwd_dkdv_kernel: one workgroup per (kv head, 128 keys, batch row), a wave per 32
-// keys (lane l owns key column l % 32), looping over the GQA group's heads and the query
-// tiles that see its keys: S = Q K^T, dP = dO V^T, dV^T += dO^T P, dK^T += Q^T (s c dZ).
+// chord_bwd_dkdv_kernel: one workgroup per (query head, 128 keys, batch row), a wave per
+// 32 keys (lane l owns key column l % 32), looping over the query tiles that see its keys:
+// S = Q K^T, dP = dO V^T, dV^T += dO^T P, dK^T += Q^T (s c dZ), into fp32 partials per
+// query head that chord_bwd_reduce_kernel sums over each GQA group.  Both loops stage
+// the next tile's global loads in registers while the current tile is computed.
 // The GGD bias (and, in the dQ kernel, its three parameter derivatives) come from
 // per-tile windows over the 63 distances a 32 x 32 tile meets, evaluated in registers.
 #include <algorithm>
@@ -47,6 +49,7 @@ struct ChordBwdArgs {
   bf16_t *dk; int64_t dk_sb, dk_sh, dk_st;
   bf16_t *dv; int64_t dv_sb, dv_sh, dv_st;
   float *delta;   // [B][H][L] workspace
+  float *pk, *pv; // [H][B][S][64] workspace: per query head dK / dV partials
   float *dparam;  // [B][nqb][H][4] partial sums (alpha, beta, mu, ssmax), summed by the caller
   int B, H, Hkv, L, S, q_start, nqb;
   float scale, eps;
@@ -69,34 +72,31 @@ __device__ __forceinline__ bf16x8 pack8(const float *x) {
 }
 __device__ __forceinline__ uint4 ld16(const bf16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 
-// A 32-row x 64 tile of [rows][64] bf16 rows (row r at base + r * st) into LDS: rows
-// (padded) and the transposed tile [64][32] (elements in tperm order), by 128 threads
-// t: rows 2 (t & 15) and + 1, 8-element segment t >> 4.  Rows at or past `nrows` read 0.
-__device__ __forceinline__ void stage_rows_t(const bf16_t *base, int64_t st, int nrows, int t, bf16_t *rows,
-                                             bf16_t *tr) {
+// Tile staging by 128 threads t: rows 2 (t & 15) and + 1, 8-element segment t >> 4 of a
+// 32-row x 64 tile of [rows][64] bf16 rows (row r at base + r * st); rows at or past
+// `nrows` read 0.  The loads go to registers one tile ahead of the stores.
+struct Stage2 { uint4 a, b; };
+__device__ __forceinline__ Stage2 stage_load(const bf16_t *base, int64_t st, int nrows, int t) {
   const int pr = t & 15, seg = t >> 4;
   const int r0 = 2 * pr, r1 = 2 * pr + 1;
   const uint4 z = {0u, 0u, 0u, 0u};
-  const uint4 a = r0 < nrows ? ld16(base + r0 * st + 8 * seg) : z;
-  const uint4 b = r1 < nrows ? ld16(base + r1 * st + 8 * seg) : z;
-  *reinterpret_cast<uint4 *>(rows + r0 * kRowP + 8 * seg) = a;
-  *reinterpret_cast<uint4 *>(rows + r1 * kRowP + 8 * seg) = b;
-  const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
-  const int col = tperm(r0);  // r0 even: r1 sits right after it
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    *reinterpret_cast<uint32_t *>(tr + (8 * seg + 2 * i) * kTRow + col) = (aw[i] & 0xffffu) | (bw[i] << 16);
-    *reinterpret_cast<uint32_t *>(tr + (8 * seg + 2 * i + 1) * kTRow + col) = (aw[i] >> 16) | (bw[i] & 0xffff0000u);
-  }
+  return {r0 < nrows ? ld16(base + r0 * st + 8 * seg) : z, r1 < nrows ? ld16(base + r1 * st + 8 * seg) : z};
 }
-// Rows only (no transpose), same thread mapping.
-__device__ __forceinline__ void stage_rows(const bf16_t *base, int64_t st, int nrows, int t, bf16_t *rows) {
+// The rows (padded) into `rows`, and, when `tr` is set, the transposed tile [64][32]
+// (elements in tperm order) into `tr`.
+__device__ __forceinline__ void stage_store(const Stage2 &g, int t, bf16_t *rows, bf16_t *tr) {
   const int pr = t & 15, seg = t >> 4;
-  const uint4 z = {0u, 0u, 0u, 0u};
+  const int r0 = 2 * pr, r1 = 2 * pr + 1;
+  *reinterpret_cast<uint4 *>(rows + r0 * kRowP + 8 * seg) = g.a;
+  *reinterpret_cast<uint4 *>(rows + r1 * kRowP + 8 * seg) = g.b;
+  if (tr) {
+    const uint32_t aw[4] = {g.a.x, g.a.y, g.a.z, g.a.w}, bw[4] = {g.b.x, g.b.y, g.b.z, g.b.w};
+    const int col = tperm(r0);  // r0 even: r1 sits right after it
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int r = 2 * pr + u;
-    *reinterpret_cast<uint4 *>(rows + r * kRowP + 8 * seg) = r < nrows ? ld16(base + r * st + 8 * seg) : z;
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<uint32_t *>(tr + (8 * seg + 2 * i) * kTRow + col) = (aw[i] & 0xffffu) | (bw[i] << 16);
+      *reinterpret_cast<uint32_t *>(tr + (8 * seg + 2 * i + 1) * kTRow + col) = (aw[i] >> 16) | (bw[i] & 0xffff0000u);
+    }
   }
 }
 
@@ -157,11 +157,19 @@ __global__ void __launch_bounds__(256) chord_bwd_dq_kernel(ChordBwdArgs a) {
   float sa = 0.f, sb = 0.f, sm = 0.f, ss = 0.f;
   float *win = &sW[w][0][0];
 
+  // threads 0-127 stage K (rows and K^T), 128-255 V (rows)
+  const bool kside = tid < 128;
+  const int st_t = tid & 127;
+  auto load_kv = [&](int n0) {
+    return kside ? stage_load(kbase + int64_t(n0) * a.k_st, a.k_st, kv_end - n0, st_t)
+                 : stage_load(vbase + int64_t(n0) * a.v_st, a.v_st, kv_end - n0, st_t);
+  };
+  Stage2 stg = load_kv(0);
   for (int kt = 0; kt < ntiles; ++kt) {
     const int n0 = kt * kT;
     __syncthreads();  // the previous tile's reads are done
-    if (tid < 128) stage_rows_t(kbase + int64_t(n0) * a.k_st, a.k_st, kv_end - n0, tid, sK, sKT);
-    else stage_rows(vbase + int64_t(n0) * a.v_st, a.v_st, kv_end - n0, tid - 128, sV);
+    stage_store(stg, st_t, kside ? sK : sV, kside ? sKT : nullptr);
+    if (kt + 1 < ntiles) stg = load_kv(n0 + kT);  // in flight during this tile's work
     const bool active = n0 < wave_kv_end;
     if (active) {
       // window entry j (lane j < 63): distance d = key - q_abs = n0 - q_start - q0 - 31 + j
@@ -237,12 +245,15 @@ __global__ void __launch_bounds__(256) chord_bwd_dq_kernel(ChordBwdArgs a) {
 }
 
 // ------------------------------------------------------------------ dK, dV
-__global__ void __launch_bounds__(256) chord_bwd_dkdv_kernel(ChordBwdArgs a) {
-  const int kvh = blockIdx.x, kb = blockIdx.y, b = blockIdx.z;
+// One workgroup per (query head, 128 keys, batch row): the head's share of dK and dV in
+// fp32 partials [H][B][S][64] (each query head of a GQA group separately, so the group's
+// heads run in parallel); chord_bwd_reduce_kernel sums a group's partials.
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) chord_bwd_dkdv_kernel(ChordBwdArgs a) {
+  const int h = blockIdx.x, kb = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lc = lane & 31, hh = lane >> 5;
-  const int G = a.H / a.Hkv;
+  const int kvh = h / (a.H / a.Hkv);
   const int k0w = kb * 128 + 32 * w;
   const int my_k = k0w + lc;
   const bool kvld = my_k < a.S;
@@ -267,96 +278,141 @@ __global__ void __launch_bounds__(256) chord_bwd_dkdv_kernel(ChordBwdArgs a) {
   f32x16 dkacc[2], dvacc[2];
   dkacc[0] = dkacc[1] = dvacc[0] = dvacc[1] = f32x16{};
   const float s = a.scale;
+  const float sig = a.ssmax[h], al = a.alpha[h], be = a.beta[h], mu = a.mu[h];
+  const bf16_t *qbase = a.q + b * a.q_sb + h * a.q_sh;
+  const bf16_t *dbase = a.dout + b * a.d_sb + h * a.d_sh;
+  const size_t rbase = (static_cast<size_t>(b) * a.H + h) * a.L;
   // queries that see a key of this workgroup: i >= kb * 128 - q_start
   const int i_first = max(0, kb * 128 - a.q_start);
   const int qt_first = i_first / kT, qt_end = (a.L + kT - 1) / kT;
 
-  for (int gi = 0; gi < G; ++gi) {
-    const int h = kvh * G + gi;
-    const float sig = a.ssmax[h], al = a.alpha[h], be = a.beta[h], mu = a.mu[h];
-    const bf16_t *qbase = a.q + b * a.q_sb + h * a.q_sh;
-    const bf16_t *dbase = a.dout + b * a.d_sb + h * a.d_sh;
-    for (int qt = qt_first; qt < qt_end; ++qt) {
-      const int i0 = qt * kT;
-      __syncthreads();  // the previous tile's reads are done
-      if (tid < 128) stage_rows_t(qbase + int64_t(i0) * a.q_st, a.q_st, a.L - i0, tid, sQ, sQT);
-      else stage_rows_t(dbase + int64_t(i0) * a.d_st, a.d_st, a.L - i0, tid - 128, sD, sDT);
-      if (tid < kT) {
-        const int i = i0 + tid;
-        const bool iv = i < a.L;
-        const size_t ri = (static_cast<size_t>(b) * a.H + h) * a.L + (iv ? i : 0);
-        sRow[0][tid] = iv ? a.lse[ri] : 0.f;
-        sRow[1][tid] = iv ? a.delta[ri] : 0.f;
-        sRow[2][tid] = iv ? sig * a.log_n[b * a.ln_sb + int64_t(i) * a.ln_st] : 0.f;
-      }
-      // a wave whose keys all lie past the tile's last query skips it
-      const bool active = a.q_start + i0 + kT - 1 >= k0w;
-      if (active) {
-        // window entry j: distance key - q_abs = k0w - q_start - i0 - 31 + j
-        const int d = k0w - a.q_start - i0 - 31 + lane;
-        const float x = fabsf(static_cast<float>(d) - mu) + a.eps;
-        sW[w][lane] = d <= 0 ? -al * fast_exp2(be * fast_log2(x)) : 0.f;
-      }
-      __syncthreads();
-      if (!active) continue;
+  // threads 0-127 stage Q, 128-255 dO (rows and transposed); threads 0-31 the row values
+  const bool qside = tid < 128;
+  const int st_t = tid & 127;
+  auto load_q = [&](int i0) {
+    return qside ? stage_load(qbase + int64_t(i0) * a.q_st, a.q_st, a.L - i0, st_t)
+                 : stage_load(dbase + int64_t(i0) * a.d_st, a.d_st, a.L - i0, st_t);
+  };
+  auto load_row = [&](int i0) {
+    const int i = i0 + (tid & (kT - 1));
+    const bool iv = i < a.L;
+    const size_t ri = rbase + (iv ? i : 0);
+    return float4{iv ? a.lse[ri] : 0.f, iv ? a.delta[ri] : 0.f,
+                  iv ? sig * a.log_n[b * a.ln_sb + int64_t(i) * a.ln_st] : 0.f, 0.f};
+  };
+  Stage2 stg = {};
+  float4 rowv = {};
+  if (qt_first < qt_end) {
+    stg = load_q(qt_first * kT);
+    if (tid < kT) rowv = load_row(qt_first * kT);
+  }
+  for (int qt = qt_first; qt < qt_end; ++qt) {
+    const int i0 = qt * kT;
+    __syncthreads();  // the previous tile's reads are done
+    stage_store(stg, st_t, qside ? sQ : sD, qside ? sQT : sDT);
+    if (tid < kT) {
+      sRow[0][tid] = rowv.x;
+      sRow[1][tid] = rowv.y;
+      sRow[2][tid] = rowv.z;
+    }
+    if (qt + 1 < qt_end) {  // in flight during this tile's work
+      stg = load_q(i0 + kT);
+      if (tid < kT) rowv = load_row(i0 + kT);
+    }
+    // a wave whose keys all lie past the tile's last query skips it
+    const bool active = a.q_start + i0 + kT - 1 >= k0w;
+    if (active) {
+      // window entry j: distance key - q_abs = k0w - q_start - i0 - 31 + j
+      const int d = k0w - a.q_start - i0 - 31 + lane;
+      const float x = fabsf(static_cast<float>(d) - mu) + a.eps;
+      sW[w][lane] = d <= 0 ? -al * fast_exp2(be * fast_log2(x)) : 0.f;
+    }
+    __syncthreads();
+    if (!active) continue;
 
-      f32x16 sacc = {}, pacc = {};
+    f32x16 sacc = {}, pacc = {};
 #pragma unroll
-      for (int ds = 0; ds < 4; ++ds) {
-        const bf16x8 qo = *reinterpret_cast<const bf16x8 *>(sQ + lc * kRowP + 16 * ds + 8 * hh);
-        const bf16x8 dov = *reinterpret_cast<const bf16x8 *>(sD + lc * kRowP + 16 * ds + 8 * hh);
-        sacc = mma32(qo, kreg[ds], sacc);
-        pacc = mma32(dov, vreg[ds], pacc);
-      }
-      float pv[16], dz[16];
+    for (int ds = 0; ds < 4; ++ds) {
+      const bf16x8 qo = *reinterpret_cast<const bf16x8 *>(sQ + lc * kRowP + 16 * ds + 8 * hh);
+      const bf16x8 dov = *reinterpret_cast<const bf16x8 *>(sD + lc * kRowP + 16 * ds + 8 * hh);
+      sacc = mma32(qo, kreg[ds], sacc);
+      pacc = mma32(dov, vreg[ds], pacc);
+    }
+    float pv[16], dz[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int qq = 8 * (r >> 2) + 4 * hh + (r & 3);
-        const int i = i0 + qq;
-        const bool vis = kvld && i < a.L && my_k <= a.q_start + i;
-        const float cq = sRow[2][qq];
-        const float rr = fmaf(s, sacc[r], sW[w][lc - qq + 31]);
-        const float p = vis ? fast_exp2(fmaf(cq * kLog2e, rr, -sRow[0][qq])) : 0.f;
-        pv[r] = p;
-        dz[r] = p * (pacc[r] - sRow[1][qq]) * cq * s;
-      }
+    for (int r = 0; r < 16; ++r) {
+      const int qq = 8 * (r >> 2) + 4 * hh + (r & 3);
+      const int i = i0 + qq;
+      const bool vis = kvld && i < a.L && my_k <= a.q_start + i;
+      const float cq = sRow[2][qq];
+      const float rr = fmaf(s, sacc[r], sW[w][lc - qq + 31]);
+      const float p = vis ? fast_exp2(fmaf(cq * kLog2e, rr, -sRow[0][qq])) : 0.f;
+      pv[r] = p;
+      dz[r] = p * (pacc[r] - sRow[1][qq]) * cq * s;
+    }
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const bf16x8 pb = pack8(pv + 8 * ks), zb = pack8(dz + 8 * ks);
+    for (int ks = 0; ks < 2; ++ks) {
+      const bf16x8 pb = pack8(pv + 8 * ks), zb = pack8(dz + 8 * ks);
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt) {
-          const bf16x8 dto = *reinterpret_cast<const bf16x8 *>(sDT + (32 * dt + lc) * kTRow + 16 * ks + 8 * hh);
-          const bf16x8 qto = *reinterpret_cast<const bf16x8 *>(sQT + (32 * dt + lc) * kTRow + 16 * ks + 8 * hh);
-          dvacc[dt] = mma32(dto, pb, dvacc[dt]);
-          dkacc[dt] = mma32(qto, zb, dkacc[dt]);
-        }
+      for (int dt = 0; dt < 2; ++dt) {
+        const bf16x8 dto = *reinterpret_cast<const bf16x8 *>(sDT + (32 * dt + lc) * kTRow + 16 * ks + 8 * hh);
+        const bf16x8 qto = *reinterpret_cast<const bf16x8 *>(sQT + (32 * dt + lc) * kTRow + 16 * ks + 8 * hh);
+        dvacc[dt] = mma32(dto, pb, dvacc[dt]);
+        dkacc[dt] = mma32(qto, zb, dkacc[dt]);
       }
     }
   }
 
   if (kvld) {
-    bf16_t *dkd = a.dk + b * a.dk_sb + kvh * a.dk_sh + int64_t(my_k) * a.dk_st;
-    bf16_t *dvd = a.dv + b * a.dv_sb + kvh * a.dv_sh + int64_t(my_k) * a.dv_st;
+    const size_t o = ((static_cast<size_t>(h) * a.B + b) * a.S + my_k) * kBD;
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
-        const int o = 32 * dt + 8 * q4 + 4 * hh;
-        *reinterpret_cast<uint2 *>(dkd + o) =
-            uint2{pk2bf(dkacc[dt][4 * q4], dkacc[dt][4 * q4 + 1]), pk2bf(dkacc[dt][4 * q4 + 2], dkacc[dt][4 * q4 + 3])};
-        *reinterpret_cast<uint2 *>(dvd + o) =
-            uint2{pk2bf(dvacc[dt][4 * q4], dvacc[dt][4 * q4 + 1]), pk2bf(dvacc[dt][4 * q4 + 2], dvacc[dt][4 * q4 + 3])};
+        const int d0 = 32 * dt + 8 * q4 + 4 * hh;
+        *reinterpret_cast<f32x4 *>(a.pk + o + d0) =
+            f32x4{dkacc[dt][4 * q4], dkacc[dt][4 * q4 + 1], dkacc[dt][4 * q4 + 2], dkacc[dt][4 * q4 + 3]};
+        *reinterpret_cast<f32x4 *>(a.pv + o + d0) =
+            f32x4{dvacc[dt][4 * q4], dvacc[dt][4 * q4 + 1], dvacc[dt][4 * q4 + 2], dvacc[dt][4 * q4 + 3]};
       }
   }
+}
+
+// dK / dV of kv head kvh = the sum of its group's query-head partials, rounded to bf16;
+// one thread per 4 elements.
+__global__ void __launch_bounds__(256) chord_bwd_reduce_kernel(ChordBwdArgs a) {
+  const int64_t n4 = static_cast<int64_t>(a.B) * a.Hkv * a.S * (kBD / 4);
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (e >= n4) return;
+  const int d0 = 4 * static_cast<int>(e % (kBD / 4));
+  const int64_t rest = e / (kBD / 4);
+  const int sk = static_cast<int>(rest % a.S);
+  const int kvh = static_cast<int>((rest / a.S) % a.Hkv), b = static_cast<int>(rest / (static_cast<int64_t>(a.S) * a.Hkv));
+  const int G = a.H / a.Hkv;
+  f32x4 ks = {0.f, 0.f, 0.f, 0.f}, vs = {0.f, 0.f, 0.f, 0.f};
+  for (int g = 0; g < G; ++g) {
+    const size_t o = ((static_cast<size_t>(kvh * G + g) * a.B + b) * a.S + sk) * kBD + d0;
+    const f32x4 pk = *reinterpret_cast<const f32x4 *>(a.pk + o), pv = *reinterpret_cast<const f32x4 *>(a.pv + o);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ks[i] += pk[i];
+      vs[i] += pv[i];
+    }
+  }
+  bf16_t *dk = a.dk + b * a.dk_sb + kvh * a.dk_sh + int64_t(sk) * a.dk_st + d0;
+  bf16_t *dv = a.dv + b * a.dv_sb + kvh * a.dv_sh + int64_t(sk) * a.dv_st + d0;
+  *reinterpret_cast<uint2 *>(dk) = uint2{pk2bf(ks[0], ks[1]), pk2bf(ks[2], ks[3])};
+  *reinterpret_cast<uint2 *>(dv) = uint2{pk2bf(vs[0], vs[1]), pk2bf(vs[2], vs[3])};
 }
 
 }  // namespace
 
 }  // namespace motif
 
-extern "C" size_t motif_chord_bwd_workspace_bytes(int B, int H, int L) {
-  if (B <= 0 || H <= 0 || L <= 0) return 0;
-  return static_cast<size_t>(B) * H * L * sizeof(float);  // Delta
+extern "C" size_t motif_chord_bwd_workspace_bytes(int B, int H, int L, int S) {
+  if (B <= 0 || H <= 0 || L < 0 || S < 0) return 0;
+  const size_t delta = (static_cast<size_t>(B) * H * L * sizeof(float) + 255) / 256 * 256;
+  return delta + 2 * static_cast<size_t>(H) * B * S * motif::kBD * sizeof(float);  // Delta, dK / dV partials
 }
 
 extern "C" size_t motif_chord_bwd_dparam_len(int B, int H, int L) {
@@ -384,7 +440,7 @@ extern "C" int motif_chord_bwd(
     return set_error(MOTIF_ERR_UNSUPPORTED, "chord_bwd: bf16 with head_dim 64 only");
   if (q_start < 0 || static_cast<int64_t>(q_start) + L > S)
     return set_error(MOTIF_ERR_INVALID, "chord_bwd: need 0 <= q_start and q_start + L <= S");
-  if (B == 0 || L == 0) return MOTIF_OK;
+  if (B == 0 || S == 0) return MOTIF_OK;  // (L <= S) nothing to differentiate
   if (!q || !k || !v || !out || !dout || !lse || !alpha || !beta || !mu || !ssmax || !log_n || !dq || !dk || !dv ||
       !dparam_partial)
     return set_error(MOTIF_ERR_INVALID, "chord_bwd: NULL pointer");
@@ -394,7 +450,7 @@ extern "C" int motif_chord_bwd(
                        reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(dout) |
                        reinterpret_cast<uintptr_t>(dq) | reinterpret_cast<uintptr_t>(dk) | reinterpret_cast<uintptr_t>(dv);
   if ((st & 7) != 0 || (al & 15) != 0) return set_error(MOTIF_ERR_UNSUPPORTED, "chord_bwd: need 16-byte aligned rows");
-  const size_t need = motif_chord_bwd_workspace_bytes(B, H, L);
+  const size_t need = motif_chord_bwd_workspace_bytes(B, H, L, S);
   if (!workspace || workspace_bytes < need)
     return set_error(MOTIF_ERR_INVALID, "chord_bwd: workspace too small (need " + std::to_string(need) + " bytes)");
   ChordBwdArgs a;
@@ -409,15 +465,22 @@ extern "C" int motif_chord_bwd(
   a.dk = static_cast<bf16_t *>(dk); a.dk_sb = dk_sb; a.dk_sh = dk_sh; a.dk_st = dk_st;
   a.dv = static_cast<bf16_t *>(dv); a.dv_sb = dv_sb; a.dv_sh = dv_sh; a.dv_st = dv_st;
   a.delta = static_cast<float *>(workspace);
+  const size_t delta_bytes = (static_cast<size_t>(B) * H * L * sizeof(float) + 255) / 256 * 256;
+  a.pk = reinterpret_cast<float *>(static_cast<char *>(workspace) + delta_bytes);
+  a.pv = a.pk + static_cast<size_t>(H) * B * S * kBD;
   a.B = B; a.H = H; a.Hkv = Hkv; a.L = L; a.S = S; a.q_start = q_start;
   a.nqb = (L + 127) / 128;
   a.dparam = dparam_partial;
   a.scale = scale; a.eps = eps;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  chord_bwd_dq_kernel<<<dim3(H, a.nqb, B), dim3(256), 0, s>>>(a);
-  int rc = check_launch("chord_bwd_dq_kernel");
-  if (rc) return rc;
-  if (S == 0) return MOTIF_OK;
-  chord_bwd_dkdv_kernel<<<dim3(Hkv, (S + 127) / 128, B), dim3(256), 0, s>>>(a);
-  return check_launch("chord_bwd_dkdv_kernel");
+  int rc = MOTIF_OK;
+  if (L > 0) {  // with no queries dK and dV are zero: the partials below stay zero
+    chord_bwd_dq_kernel<<<dim3(H, a.nqb, B), dim3(256), 0, s>>>(a);
+    if ((rc = check_launch("chord_bwd_dq_kernel"))) return rc;
+  }
+  chord_bwd_dkdv_kernel<<<dim3(H, (S + 127) / 128, B), dim3(256), 0, s>>>(a);
+  if ((rc = check_launch("chord_bwd_dkdv_kernel"))) return rc;
+  const int64_t n4 = static_cast<int64_t>(B) * Hkv * S * (kBD / 4);
+  chord_bwd_reduce_kernel<<<dim3(static_cast<unsigned>((n4 + 255) / 256)), dim3(256), 0, s>>>(a);
+  return check_launch("chord_bwd_reduce_kernel");
 }

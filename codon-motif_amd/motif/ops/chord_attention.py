@@ -67,11 +67,12 @@ class ChordFunction(torch.autograd.Function):
         B, H, L, D = q.shape
         Hkv, S = k.shape[1], k.shape[2]
         dout = _aligned(dout.contiguous())
-        dq, dk, dv = torch.empty_like(q), torch.zeros_like(k), torch.zeros_like(v)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
         lib = _lib.lib()
         npart = int(lib.motif_chord_bwd_dparam_len(B, H, L))
         part = torch.empty(max(npart, 1), dtype=torch.float32, device=q.device)
-        ws = torch.empty(max(int(lib.motif_chord_bwd_workspace_bytes(B, H, L)), 1), dtype=torch.uint8, device=q.device)
+        ws = torch.empty(max(int(lib.motif_chord_bwd_workspace_bytes(B, H, L, S)), 1), dtype=torch.uint8,
+                         device=q.device)
         rc = lib.motif_chord_bwd(
             *_lib.t4(q), *_lib.t4(k), *_lib.t4(v), *_lib.t4(out), *_lib.t4(dout),
             lse.data_ptr(), alpha.data_ptr(), beta.data_ptr(), mu.data_ptr(), ssmax.data_ptr(),

@@ -248,10 +248,10 @@ int motif_chord_fwd(
  *   lse [B,H,L] fp32: the forward's base-2 log-sum-exp.
  *   dparam_partial: motif_chord_bwd_dparam_len(B, H, L) floats laid out
  *   [B][ceil(L / 128)][H][4] (alpha, beta, mu, ssmax); the caller sums them over the first
- *   two axes.  workspace: motif_chord_bwd_workspace_bytes(B, H, L) bytes (row sums
- *   dout . out).  Needs 0 <= q_start and q_start + L <= S.
+ *   two axes.  workspace: motif_chord_bwd_workspace_bytes(B, H, L, S) bytes (row sums
+ *   dout . out, per query head dk / dv partials).  Needs 0 <= q_start and q_start + L <= S.
  */
-size_t motif_chord_bwd_workspace_bytes(int B, int H, int L);
+size_t motif_chord_bwd_workspace_bytes(int B, int H, int L, int S);
 size_t motif_chord_bwd_dparam_len(int B, int H, int L);
 int motif_chord_bwd(
     const void *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
