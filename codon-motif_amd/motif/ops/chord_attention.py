@@ -69,24 +69,19 @@ class ChordFunction(torch.autograd.Function):
         dout = _aligned(dout.contiguous())
         dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
         lib = _lib.lib()
-        npart = int(lib.motif_chord_bwd_dparam_len(B, H, L))
-        part = torch.empty(max(npart, 1), dtype=torch.float32, device=q.device)
-        ws = torch.empty(max(int(lib.motif_chord_bwd_workspace_bytes(B, H, L, S)), 1), dtype=torch.uint8,
-                         device=q.device)
+        d_params = torch.empty((4, H), dtype=torch.float32, device=q.device)
+        nbytes = int(lib.motif_chord_bwd_workspace_bytes(B, H, Hkv, L, S, int(ctx.q_start)))
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
         rc = lib.motif_chord_bwd(
             *_lib.t4(q), *_lib.t4(k), *_lib.t4(v), *_lib.t4(out), *_lib.t4(dout),
             lse.data_ptr(), alpha.data_ptr(), beta.data_ptr(), mu.data_ptr(), ssmax.data_ptr(),
             ln.data_ptr(), ln.stride(0), ln.stride(1),
-            *_lib.t4(dq), *_lib.t4(dk), *_lib.t4(dv), part.data_ptr(),
+            *_lib.t4(dq), *_lib.t4(dk), *_lib.t4(dv), d_params.data_ptr(),
             B, H, Hkv, L, S, D, int(ctx.q_start), float(ctx.scale), float(ctx.eps),
             ws.data_ptr(), ws.numel(), _lib.chord_dtype_code(q.dtype), _lib.stream_ptr(q.device))
         _lib.check(rc, 'motif_chord_bwd')
-        if npart:
-            d_params = part[:npart].view(-1, H, 4).sum(0)
-        else:
-            d_params = torch.zeros(H, 4, dtype=torch.float32, device=q.device)
         needs = ctx.needs_input_grad
-        grads = [dq, dk, dv] + [d_params[:, i].contiguous() for i in range(4)]
+        grads = [dq, dk, dv] + list(d_params.unbind(0))
         grads = [g if needs[i] else None for i, g in enumerate(grads)]
         return (*grads, None, None, None, None)
 

@@ -240,19 +240,19 @@ int motif_chord_fwd(
     int dtype, void *stream);
 
 /*
- * Chord attention backward: dq, dk, dv of the forward above and the per-head partial
- * sums of d alpha, d beta, d mu, d ssmax.  Replaces the reference's custom backward
+ * Chord attention backward: dq, dk, dv of the forward above and the gradients of the [H]
+ * parameters alpha, beta, mu, ssmax.  Replaces the reference's custom backward
  * motif/ops/chord_attention.py:1348-1470 `_chord_backward_impl` (kernels :518-949,
  * called from `_TritonChordFunction.backward` :1520-1554).
  *   q, out, dout, dq [B,H,L,D]; k, v, dk, dv [B,Hkv,S,D] (bf16, D == 64, padded batch)
  *   lse [B,H,L] fp32: the forward's base-2 log-sum-exp.
- *   dparam_partial: motif_chord_bwd_dparam_len(B, H, L) floats laid out
- *   [B][ceil(L / 128)][H][4] (alpha, beta, mu, ssmax); the caller sums them over the first
- *   two axes.  workspace: motif_chord_bwd_workspace_bytes(B, H, L, S) bytes (row sums
- *   dout . out, per query head dk / dv partials).  Needs 0 <= q_start and q_start + L <= S.
+ *   dparam [4][H] fp32 (written): d alpha, d beta, d mu, d ssmax.
+ *   workspace: motif_chord_bwd_workspace_bytes(B, H, Hkv, L, S, q_start) bytes (row sums
+ *   dout . out and the fp32 partials of the chunked causal loops).  Needs 0 <= q_start
+ *   and q_start + L <= S.  Results do not depend on the run: partials are summed in a
+ *   fixed order.
  */
-size_t motif_chord_bwd_workspace_bytes(int B, int H, int L, int S);
-size_t motif_chord_bwd_dparam_len(int B, int H, int L);
+size_t motif_chord_bwd_workspace_bytes(int B, int H, int Hkv, int L, int S, int q_start);
 int motif_chord_bwd(
     const void *q, int64_t q_sb, int64_t q_sh, int64_t q_st,
     const void *k, int64_t k_sb, int64_t k_sh, int64_t k_st,
@@ -264,7 +264,7 @@ int motif_chord_bwd(
     void *dq, int64_t dq_sb, int64_t dq_sh, int64_t dq_st,
     void *dk, int64_t dk_sb, int64_t dk_sh, int64_t dk_st,
     void *dv, int64_t dv_sb, int64_t dv_sh, int64_t dv_st,
-    float *dparam_partial, int B, int H, int Hkv, int L, int S, int D, int q_start, float scale, float eps,
+    float *dparam, int B, int H, int Hkv, int L, int S, int D, int q_start, float scale, float eps,
     void *workspace, size_t workspace_bytes, int dtype, void *stream);
 
 /*

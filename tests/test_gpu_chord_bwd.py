@@ -63,6 +63,8 @@ def _close(got, ref, what, max_rel=2.5e-2, mean_rel=1e-2):
     (2, 4, 2, 160, 160, 0),      # GQA group 2, ragged last tiles
     (1, 4, 4, 96, 300, 204),     # MHA, queries after a cached prefix
     (1, 12, 3, 512, 512, 0),     # the model's grouping (4 heads per kv head)
+    (1, 4, 2, 1024, 1024, 0),    # causal loops cut into chunks (fp32 partials summed)
+    (1, 2, 1, 700, 1500, 800),   # chunks after a cached prefix, ragged tiles
 ])
 def test_chord_backward_matches_torch_form(B, H, Hkv, L, S, q_start):
     q, k, v, alpha, beta, mu, ssmax, dout = _inputs(B, H, Hkv, L, S, seed=L + S + H)
