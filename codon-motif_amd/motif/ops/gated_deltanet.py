@@ -15,10 +15,13 @@ The HIP kernels are forward-only: calls whose inputs need gradients (training)
 take the differentiable torch form of the chunked rule
 (motif/ops/autograd_path.py:gdn_chunk_torch), so autograd supplies the backward.
 '''
+import functools
+
 import torch
 
 from . import _lib
 from .autograd_path import gdn_chunk_torch, wants_grad as _needs_grad
+from .gdn_grad import GDNChunkFunction, scans_serve
 
 __all__ = [
     'gdn_prefill_fused',
@@ -189,13 +192,22 @@ def chunk_gated_delta_rule(q, k, v, beta, g, S=None, chunk_size=64):
     Returns:
         (o [B, H, L, Dv] in q's dtype, S [B, H, Dk, Dv] fp32)
     '''
-    name = 'chunk_gated_delta_rule'
+    C = _kernel_chunk(int(chunk_size))
     if _needs_grad(q, k, v, beta, g, S):
+        if q.is_cuda and _lib.available() and q.dtype in (torch.float32, torch.bfloat16) \
+                and scans_serve(q.shape[-1], v.shape[-1], C):
+            fwd = functools.partial(_chunk_fwd, chunk=C)
+            return GDNChunkFunction.apply(q, k, v, beta, g, S, C, fwd)
         return gdn_chunk_torch(q, k, v, beta, g, S, chunk_size)
+    return _chunk_fwd(q, k, v, beta, g, S, C)
+
+
+def _chunk_fwd(q, k, v, beta, g, S, chunk):
+    name = 'chunk_gated_delta_rule'
     (qc, kc, vc, bc, gc), _ = _prepare(q, k, v, beta, g, name)
     B, H, L, Dk = qc.shape
     S_in = _state_in(S, B, H, Dk, vc.shape[-1], qc.device, name)
-    o, S_out = _chunk_call(qc, kc, vc, bc, gc, S_in, _kernel_chunk(int(chunk_size)))
+    o, S_out = _chunk_call(qc, kc, vc, bc, gc, S_in, chunk)
     return o.to(q.dtype), S_out
 
 

@@ -1,0 +1,172 @@
+'''Backward of the chunked gated delta rule: the HIP forward for the output and the fp32
+backward of the reference's training path.
+
+The reference differentiates its chunk rule in three pieces
+(motif/ops/gated_deltanet.py): the chunk preparation `_PrepareChunksFunction.backward`
+(:180-260, the triangular solve differentiated in closed form), the scan
+`_FusedScanFunction.backward` (:727-765, a reverse scan kernel plus batched products) and
+the per-chunk output combination (autograd through :851-855).  `GDNChunkFunction` runs
+the same pieces: the two sequential scans are the HIP kernels `motif_gdn_scan_fwd_f32`
+(re-scan for the per-chunk states P and residuals X) and `motif_gdn_scan_bwd_f32` (the
+reverse scan), the per-chunk products are batched fp32 GEMMs (the library GEMMs the
+reference also calls) and elementwise terms.
+
+Per chunk, with gamma the within-chunk cumulative log decay, D[i, j] = e^{gamma_i -
+gamma_j} (j <= i), Kb = beta k, Vb = beta v, A = -(Kb k^T * D) strictly lower,
+T = (I - A)^{-1}, W = T (Kb e^gamma), U = T Vb:
+    X = U - W P,   S' = e^{gamma_C} P + (k e^{gamma_C - gamma})^T X,
+    o = (q e^gamma) P + ((q k^T) * D) X.
+'''
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+
+
+def scans_serve(Dk: int, Dv: int, C: int) -> bool:
+    return C in (16, 32, 64) and Dk % 16 == 0 and Dk <= 128 and Dv % 16 == 0
+
+
+def fused_scan(k, W, U, g, S0):
+    '''The forward chunk scan on the HIP kernel: (P [B,H,N,Dk,Dv], S [B,H,Dk,Dv],
+    X [B,H,N,C,Dv]) from chunked fp32 k, W [B,H,N,C,Dk], U [B,H,N,C,Dv], cumulative g
+    [B,H,N,C] and S0 [B,H,Dk,Dv] (or None); the reference's `_fused_scan_triton`
+    (motif/ops/gated_deltanet.py:644-694).'''
+    B, H, N, C, Dk = k.shape
+    Dv = U.shape[-1]
+    k, W, U, g = (t.float().contiguous() for t in (k, W, U, g))
+    S0 = None if S0 is None else S0.float().contiguous()
+    P = torch.empty(B, H, N, Dk, Dv, dtype=torch.float32, device=k.device)
+    X = torch.empty(B, H, N, C, Dv, dtype=torch.float32, device=k.device)
+    S = torch.empty(B, H, Dk, Dv, dtype=torch.float32, device=k.device)
+    rc = _lib.lib().motif_gdn_scan_fwd_f32(k.data_ptr(), W.data_ptr(), U.data_ptr(), g.data_ptr(), _lib.ptr(S0),
+                                           P.data_ptr(), X.data_ptr(), S.data_ptr(), B * H, N, C, Dk, Dv,
+                                           _lib.stream_ptr(k.device))
+    _lib.check(rc, 'motif_gdn_scan_fwd_f32')
+    return P, S, X
+
+
+def bwd_scan(k, W, g, dX, dP, dS_final):
+    '''The reverse chunk scan on the HIP kernel: (dSn [B,H,N,Dk,Dv], dS0 [B,H,Dk,Dv]);
+    dX, dP and dS_final may be None.  The reference's `_bwd_scan`
+    (motif/ops/gated_deltanet.py:558-612).'''
+    B, H, N, C, Dk = k.shape
+    Dv = (dS_final if dS_final is not None else dX if dX is not None else dP).shape[-1]
+    k, W, g = (t.float().contiguous() for t in (k, W, g))
+    dX, dP, dS_final = (None if t is None else t.float().contiguous() for t in (dX, dP, dS_final))
+    dSn = torch.empty(B, H, N, Dk, Dv, dtype=torch.float32, device=k.device)
+    dS0 = torch.empty(B, H, Dk, Dv, dtype=torch.float32, device=k.device)
+    rc = _lib.lib().motif_gdn_scan_bwd_f32(k.data_ptr(), W.data_ptr(), g.data_ptr(), _lib.ptr(dX), _lib.ptr(dP),
+                                           _lib.ptr(dS_final), dSn.data_ptr(), dS0.data_ptr(), B * H, N, C, Dk, Dv,
+                                           _lib.stream_ptr(k.device))
+    _lib.check(rc, 'motif_gdn_scan_bwd_f32')
+    return dSn, dS0
+
+
+def _chunks(t, C, pad):
+    '''[B, H, L, ...] fp32, zero-padded to N * C steps, as [B, H, N, C, ...].'''
+    t = t.float()
+    if pad:
+        t = F.pad(t, (0, 0, 0, pad)) if t.dim() == 4 else F.pad(t, (0, pad))
+    B, H, Lp = t.shape[:3]
+    return t.reshape(B, H, Lp // C, C, *t.shape[3:])
+
+
+def _factors(q, k, v, beta, g, C):
+    '''The chunk factors of the forward, recomputed in fp32 (the reference's
+    `_PrepareChunksFunction.forward`, motif/ops/gated_deltanet.py:116-176).'''
+    L = q.shape[2]
+    pad = (C - L % C) % C
+    qc, kc, vc = (_chunks(t, C, pad) for t in (q, k, v))
+    bc, gc = _chunks(beta, C, pad), _chunks(g, C, pad).cumsum(-1)
+    dev = q.device
+    lower = torch.ones(C, C, dtype=torch.bool, device=dev).tril()
+    strict = lower.tril(-1)
+    D = (gc[..., :, None] - gc[..., None, :]).masked_fill(~lower, float('-inf')).exp()
+    kb, vb = kc * bc[..., None], vc * bc[..., None]
+    G1 = kb @ kc.transpose(-1, -2)
+    A = (-G1 * D).masked_fill(~strict, 0.0)
+    eye = torch.eye(C, device=dev, dtype=torch.float32)
+    T = torch.linalg.solve_triangular(eye - A, eye.expand_as(A), upper=False, unitriangular=True)
+    E = gc.exp()
+    Z = kb * E[..., None]
+    return dict(qc=qc, kc=kc, vc=vc, bc=bc, gc=gc, D=D, kb=kb, vb=vb, G1=G1, T=T, E=E, Z=Z,
+                W=T @ Z, U=T @ vb, strict=strict, pad=pad)
+
+
+class GDNChunkFunction(torch.autograd.Function):
+    '''Chunked gated delta rule: HIP forward (`chunk_gated_delta_rule`'s kernels), fp32
+    backward with the HIP scans.  Gradients for q, k, v, beta, g and the initial state.'''
+
+    @staticmethod
+    def forward(ctx, q, k, v, beta, g, S, C, fwd):
+        o, S_out = fwd(q.detach(), k.detach(), v.detach(), beta.detach(), g.detach(),
+                       None if S is None else S.detach())
+        ctx.save_for_backward(q, k, v, beta, g, S)
+        ctx.C = C
+        return o, S_out
+
+    @staticmethod
+    def backward(ctx, do, dS_fin):
+        q, k, v, beta, g, S0 = ctx.saved_tensors
+        C = ctx.C
+        B, H, L, Dk = q.shape
+        f = _factors(q, k, v, beta, g, C)
+        qc, kc, vc, bc, gc, D, E = f['qc'], f['kc'], f['vc'], f['bc'], f['gc'], f['D'], f['E']
+        W, U, T, Z, kb, vb, G1 = f['W'], f['U'], f['T'], f['Z'], f['kb'], f['vb'], f['G1']
+        N = qc.shape[2]
+
+        # forward states and residuals
+        P, _, X = fused_scan(kc, W, U, gc, S0)
+
+        # output o = (q e^gamma) P + ((q k^T) * D) X
+        doc = _chunks(do if do is not None else torch.zeros(B, H, L, v.shape[-1], device=q.device), C, f['pad'])
+        qg = qc * E[..., None]
+        qk = qc @ kc.transpose(-1, -2)
+        attn = qk * D
+        dP_out = qg.transpose(-1, -2) @ doc
+        dX_out = attn.transpose(-1, -2) @ doc
+        dattn = (doc @ X.transpose(-1, -2)) * D                   # zero above the diagonal
+        dqg = doc @ P.transpose(-1, -2)
+        dq = dqg * E[..., None] + dattn @ kc
+        dk = dattn.transpose(-1, -2) @ qc
+        dgam = (dqg * qg).sum(-1)                                  # d/d gamma through q e^gamma
+        ddec = dattn * qk                                          # d/d D (times D already in dattn)
+
+        # the scan: X = U - W P, S' = e^{gamma_C} P + Kd^T X
+        dSn, dS0 = bwd_scan(kc, W, gc, dX_out, dP_out, dS_fin)
+        gl = gc[..., -1:]
+        dec = (gl - gc).exp()                                      # e^{gamma_C - gamma_c}
+        dxt = dX_out + (kc @ dSn) * dec[..., None]                 # total d/dX
+        dU = dxt
+        dW = -(dxt @ P.transpose(-1, -2))
+        dKd = X @ dSn.transpose(-1, -2)                            # [C, Dk]
+        dk = dk + dKd * dec[..., None]
+        kdk = (dKd * kc * dec[..., None]).sum(-1)                  # per row: dKd . Kd
+        dgam = dgam - kdk
+        last = kdk.sum(-1) + gl.squeeze(-1).exp() * (dSn * P).sum((-1, -2))
+        dgam[..., -1] += last
+
+        # the preparation: W = T Z, U = T Vb, T = (I - A)^{-1}, A = -(Kb k^T * D) strict
+        Tt = T.transpose(-1, -2)
+        dT = dW @ Z.transpose(-1, -2) + dU @ vb.transpose(-1, -2)
+        dZ = Tt @ dW
+        dvb = Tt @ dU
+        dA = (Tt @ dT @ Tt).masked_fill(~f['strict'], 0.0)
+        dG1 = -dA * D
+        ddec = ddec - dA * G1 * D                                  # d/d D, times D
+        dkb = dG1 @ kc + dZ * E[..., None]
+        dk = dk + dG1.transpose(-1, -2) @ kb
+        dgam = dgam + (dZ * Z).sum(-1) + ddec.sum(-1) - ddec.sum(-2)
+        dbeta = (dkb * kc).sum(-1) + (dvb * vc).sum(-1)
+        dk = dk + dkb * bc[..., None]
+        dv = dvb * bc[..., None]
+        dg = dgam.flip(-1).cumsum(-1).flip(-1)                     # gamma = cumsum(g)
+
+        def back(t, like):
+            t = t.reshape(B, H, N * C, *t.shape[4:])[:, :, :L]
+            return t.to(like.dtype)
+        grads = (back(dq, q), back(dk, k), back(dv, v), back(dbeta, beta), back(dg, g),
+                 None if S0 is None else dS0.to(S0.dtype))
+        needs = ctx.needs_input_grad
+        return tuple(gr if needs[i] else None for i, gr in enumerate(grads)) + (None, None)

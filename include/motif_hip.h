@@ -95,6 +95,27 @@ int motif_gdn_chunk_fwd(
     int in_dtype, int out_dtype, void *stream);
 
 /*
+ * GatedDeltaNet chunk scans in fp32 for the backward pass (all tensors contiguous fp32,
+ * chunked as [BH, N, C, .], g the within-chunk cumulative log decay [BH, N, C]):
+ * forward re-scan P [BH,N,Dk,Dv] (state entering each chunk), X [BH,N,C,Dv] = U - W P,
+ * S_out [BH,Dk,Dv]; replaces the reference's _gdn_fused_scan_kernel
+ * (motif/ops/gated_deltanet.py:327-408, host _fused_scan_triton :644-694).  S0 may be
+ * NULL (zeros).
+ * Needs C <= 64 and Dk <= 128, both multiples of 16, and Dv a multiple of 16.
+ */
+int motif_gdn_scan_fwd_f32(const float *k, const float *W, const float *U, const float *g, const float *S0,
+                           float *P, float *X, float *S_out, int BH, int N, int C, int Dk, int Dv, void *stream);
+/*
+ * Reverse scan: dSn [BH,N,Dk,Dv] (gradient of the state leaving each chunk) and dS0 from
+ * dS_final, with the upstream dX [BH,N,C,Dv] and dP [BH,N,Dk,Dv] (either may be NULL, as
+ * may dS_final); replaces the reference's _gdn_bwd_scan_kernel (:428-520, host
+ * _bwd_scan :558-612).  Same size limits.
+ */
+int motif_gdn_scan_bwd_f32(const float *k, const float *W, const float *g, const float *dX, const float *dP,
+                           const float *dS_final, float *dSn, float *dS0, int BH, int N, int C, int Dk, int Dv,
+                           void *stream);
+
+/*
  * motif_gdn_chunk_fwd with the layer's output norm fused into the output pass:
  *   y[b,t,h*dv+e] = GatedRMSNorm(o[b,h,t,:]; gate[b,t,h*dv:(h+1)*dv], norm_weight, norm_eps)
  * (o rounded to `dtype` first; y = T(T(T(o rsqrt(mean o^2 + eps)) w) T(silu(gate)))).

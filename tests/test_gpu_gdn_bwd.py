@@ -1,0 +1,118 @@
+'''GPU parity of the GDN backward: the fp32 chunk scans (motif_gdn_scan_fwd_f32 /
+motif_gdn_scan_bwd_f32 through the C ABI) against their defining loops in float64 on
+the CPU, and the gradients of `chunk_gated_delta_rule` (GDNChunkFunction) against
+autograd through the differentiable torch form (motif/ops/autograd_path.py, whose
+gradients tests/test_autograd_path.py pins with gradcheck) in float64.
+
+Bars: the scans are fp32 products of 64..128 terms: max-abs within 1e-4 of the largest
+reference entry.  Gradients: the backward computes in fp32 from the same inputs, so
+max-abs within 2e-3 of the largest reference entry and mean-relative 1e-3 (the
+triangular solve and the per-chunk sums of the decay gradient cancel, which costs a
+few fp32 ulps of the largest terms); for bf16 inputs the gradients come back in bf16
+(one rounding of 2^-9 relative), so 1e-2 and 5e-3.'''
+import pytest
+import torch
+
+from support import gdn_inputs
+
+pytestmark = pytest.mark.gpu
+
+DEV = 'cuda'
+
+
+def _scan_fwd_ref(k, W, U, g, S0):
+    B, H, N, C, Dk = k.shape
+    P, X, S = [], [], S0.clone()
+    for n in range(N):
+        P.append(S)
+        gl = g[:, :, n, -1:]
+        kd = k[:, :, n] * (gl - g[:, :, n]).exp()[..., None]
+        x = U[:, :, n] - W[:, :, n] @ S
+        X.append(x)
+        S = gl.exp()[..., None] * S + kd.transpose(-1, -2) @ x
+    return torch.stack(P, 2), S, torch.stack(X, 2)
+
+
+def _scan_bwd_ref(k, W, g, dX, dP, dS):
+    B, H, N, C, Dk = k.shape
+    dSn = [None] * N
+    for n in range(N - 1, -1, -1):
+        dSn[n] = dS
+        gl = g[:, :, n, -1:]
+        kd = k[:, :, n] * (gl - g[:, :, n]).exp()[..., None]
+        dx = kd @ dS + dX[:, :, n]
+        dS = gl.exp()[..., None] * dS - W[:, :, n].transpose(-1, -2) @ dx + dP[:, :, n]
+    return torch.stack(dSn, 2), dS
+
+
+def _close(got, ref, what, rel=1e-4, mean_rel=None):
+    got, ref = got.detach().double().cpu(), ref.detach().double().cpu()
+    d = (got - ref).abs()
+    scale = ref.abs().max().item()
+    mr = d.sum().item() / max(ref.abs().sum().item(), 1e-30)
+    print(f'{what}: max_abs={d.max().item():.3e} (of {scale:.3e}) mean_rel={mr:.3e}', flush=True)
+    assert d.max().item() <= rel * max(scale, 1e-6), what
+    if mean_rel is not None:
+        assert mr <= mean_rel, what
+
+
+@pytest.mark.parametrize('N,C,Dk,Dv', [(5, 64, 64, 128), (3, 32, 128, 32), (4, 16, 16, 16)])
+def test_scans_match_loops(N, C, Dk, Dv):
+    from motif.ops.gdn_grad import bwd_scan, fused_scan
+    g0 = torch.Generator().manual_seed(N * 7 + C)
+    B, H = 2, 3
+    k = torch.nn.functional.normalize(torch.randn(B, H, N, C, Dk, generator=g0), dim=-1)
+    W = torch.randn(B, H, N, C, Dk, generator=g0) * 0.2
+    U = torch.randn(B, H, N, C, Dv, generator=g0)
+    g = torch.nn.functional.logsigmoid(torch.randn(B, H, N, C, generator=g0)).cumsum(-1) * 0.2
+    S0 = torch.randn(B, H, Dk, Dv, generator=g0) * 0.3
+    P, S, X = fused_scan(*(t.to(DEV) for t in (k, W, U, g, S0)))
+    rP, rS, rX = _scan_fwd_ref(*(t.double() for t in (k, W, U, g, S0)))
+    _close(P, rP, 'P')
+    _close(S, rS, 'S')
+    _close(X, rX, 'X')
+    dX = torch.randn(B, H, N, C, Dv, generator=g0)
+    dP = torch.randn(B, H, N, Dk, Dv, generator=g0) * 0.1
+    dS = torch.randn(B, H, Dk, Dv, generator=g0)
+    dSn, dS0 = bwd_scan(*(t.to(DEV) for t in (k, W, g, dX, dP, dS)))
+    rdSn, rdS0 = _scan_bwd_ref(*(t.double() for t in (k, W, g, dX, dP, dS)))
+    _close(dSn, rdSn, 'dSn')
+    _close(dS0, rdS0, 'dS0')
+
+
+def _grads(fn, q, k, v, b, g, S0, do, dS, dev, dtype):
+    ts = [t.to(dev, dtype).requires_grad_(True) for t in (q, k, v, b, g)]
+    s0 = S0.to(dev, torch.float64 if dtype == torch.float64 else torch.float32).requires_grad_(True)
+    o, S = fn(*ts, s0)
+    loss = (o.to(do.dtype) * do.to(dev)).sum() + (S.to(dS.dtype) * dS.to(dev)).sum()
+    loss.backward()
+    return o.detach(), S.detach(), [t.grad for t in ts] + [s0.grad]
+
+
+@pytest.mark.parametrize('dtype', [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize('B,H,L,dk,dv,C', [(2, 3, 200, 64, 128, 64), (1, 2, 77, 32, 64, 32)])
+def test_chunk_rule_gradients_match_torch_form(dtype, B, H, L, dk, dv, C):
+    from motif.ops import chunk_gated_delta_rule
+    from motif.ops.autograd_path import gdn_chunk_torch
+    q, k, v, b, g = gdn_inputs(B, H, L, dk, dv, seed=L + dk, dtype=dtype)
+    g0 = torch.Generator().manual_seed(L)
+    S0 = torch.randn(B, H, dk, dv, generator=g0) * 0.1
+    do = torch.randn(B, H, L, dv, generator=g0, dtype=torch.float64)
+    dS = torch.randn(B, H, dk, dv, generator=g0, dtype=torch.float64) * 0.1
+    ro, rS, rg = _grads(lambda *a: gdn_chunk_torch(*a, chunk=C), q, k, v, b, g, S0, do, dS, 'cpu', torch.float64)
+    go, gS, gg = _grads(lambda *a: chunk_gated_delta_rule(*a, chunk_size=C), q, k, v, b, g, S0, do, dS, DEV, dtype)
+    _close(go, ro, 'o', 2e-2 if dtype == torch.bfloat16 else 1e-4)
+    bars = (1e-2, 5e-3) if dtype == torch.bfloat16 else (2e-3, 1e-3)   # bf16: gradients rounded to bf16
+    for name, got, ref in zip(('dq', 'dk', 'dv', 'dbeta', 'dg', 'dS0'), gg, rg):
+        _close(got, ref, name, *bars)
+
+
+def test_only_state_output_used():
+    '''A loss on the final state alone (no output gradient) still reaches every input.'''
+    from motif.ops import chunk_gated_delta_rule
+    q, k, v, b, g = (t.to(DEV).requires_grad_(True) for t in gdn_inputs(1, 2, 70, 64, 64, seed=4))
+    _, S = chunk_gated_delta_rule(q, k, v, b, g)
+    S.square().sum().backward()
+    for t in (q, k, v, b, g):
+        assert t.grad is not None and torch.isfinite(t.grad).all()
+    assert q.grad.abs().max().item() == 0.0   # the state does not depend on q
