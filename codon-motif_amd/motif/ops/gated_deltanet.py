@@ -11,9 +11,10 @@ Differences that do not change results beyond rounding:
 - `chunk_size` is rounded down to one of the kernel chunk lengths
   {16, 32, 64} (values >= 64 use 64); the chunk length only changes the order
   of floating-point operations, not the recurrence.
-The HIP kernels are forward-only: calls whose inputs need gradients (training)
-take the differentiable torch form of the chunked rule
-(motif/ops/autograd_path.py:gdn_chunk_torch), so autograd supplies the backward.
+Gradients: `chunk_gated_delta_rule` runs its HIP forward inside `GDNChunkFunction`
+(motif/ops/gdn_grad.py), whose backward uses the HIP fp32 scans; the recurrent and
+packed forms, and shapes the scans do not take, differentiate through the torch form
+of the chunked rule (motif/ops/autograd_path.py:gdn_chunk_torch).
 '''
 import functools
 
