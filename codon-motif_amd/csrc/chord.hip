@@ -1,19 +1,17 @@
 // Chord attention (causal softmax with the gated geometric-decay bias) for gfx950.
 //
 // chord_fwd_kernel (prefill): flash-style online softmax on bf16 MFMA
-// (v_mfma_f32_16x16x32_bf16, fp32 accumulation), 16 query rows per wave.  A
-// workgroup is 4 waves that share one kv head: with GQA the waves take different
-// query heads of the same 16-row query block, otherwise consecutive query blocks
-// of one head.  Scores are computed transposed, S^T = K Q^T, so each lane owns one
-// query row (spread over the 4 lane groups of 16) and the row max needs two lane
-// swaps; the output is accumulated transposed too, O^T += V^T P^T, with P^T fed
-// from the score accumulators (two 16-key tiles per 32-key MFMA step) and V^T
-// staged in LDS in the matching key order.  K / V tiles are double-buffered in
-// LDS, loaded through range-checked buffers, one barrier per 64-key tile.  The
-// GGD bias depends only on d = key - i_abs: each wave evaluates it in registers
-// once per tile for the 79 distances of its 16x64 tile (two per lane) into 4
-// shifted LDS copies, so every lane reads its 4 consecutive distances with one
-// aligned 16-byte load; no bias is stored in HBM.
+// (v_mfma_f32_32x32x16_bf16, fp32 accumulation).  A workgroup is kParts parts of 4
+// waves over the same query rows of one kv head; part p walks its own run of the key
+// tiles and the partial softmaxes meet in LDS at the end.  A wave owns 32 score
+// columns (16 queries of two GQA heads, or 32 queries of one head).  Scores are
+// computed transposed, S^T = K Q^T, so lane l owns column l % 32 and its row max is 16
+// in-lane values plus one lane swap; the output is accumulated transposed too,
+// O^T += V^T P^T, with P^T fed straight from the score accumulators and V^T staged in
+// LDS in the matching key order.  K / V tiles are double-buffered in LDS (padded rows),
+// one barrier per 64-key tile, workgroups dispatched heaviest query blocks first.  The
+// GGD bias depends only on d = key - i_abs: each wave evaluates it in registers (one new
+// distance per lane per tile) into an LDS window; no bias is stored in HBM.
 //
 // chord_decode_kernel (decode / short queries over a long cache): split-K
 // flash-decoding.  A workgroup owns (split, kv head, batch row) and serves all
