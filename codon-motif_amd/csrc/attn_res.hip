@@ -96,7 +96,7 @@ template <typename T, int LPT, int PPL>
 __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
   constexpr int E = Piece<T>::N;
   const int sub = threadIdx.x & (LPT - 1);
-  const int tok_raw = blockIdx.x * (256 / LPT) + threadIdx.x / LPT;
+  const int tok_raw = blockIdx.x * (blockDim.x / LPT) + threadIdx.x / LPT;
   const bool tok_ok = tok_raw < a.B * a.T;
   const int tok = tok_ok ? tok_raw : 0;
   const int b = tok / a.T, t = tok - b * a.T;
@@ -203,9 +203,13 @@ __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
   }
 }
 
+// Up to 256 tokens (decode batches) each token gets a one-wave workgroup, so the
+// launch spreads over as many CUs as there are tokens (64 decode rows: 5.6 us per read
+// against 8.2 us with four waves and eight tokens per workgroup).
 template <typename T, int LPT>
 int launch_lpt(const AttnResArgs &a, int ppl, hipStream_t s) {
-  const dim3 grid((a.B * a.T + 256 / LPT - 1) / (256 / LPT)), block(256);
+  const int bs = a.B * a.T <= 256 ? LPT : 256;
+  const dim3 grid((a.B * a.T + bs / LPT - 1) / (bs / LPT)), block(bs);
   switch (ppl) {
     case 1: attn_res_kernel<T, LPT, 1><<<grid, block, 0, s>>>(a); break;
     case 2: attn_res_kernel<T, LPT, 2><<<grid, block, 0, s>>>(a); break;
@@ -220,8 +224,9 @@ template <typename T>
 int launch(const AttnResArgs &a, hipStream_t s) {
   constexpr int E = Piece<T>::N;
   const int np = a.D / E;
-  // two tokens a wave (32 lanes each) up to 128 pieces, else one
-  if (np <= 128) return launch_lpt<T, 32>(a, (np + 31) / 32, s);
+  // two tokens a wave (32 lanes each) up to 128 pieces, else one; one token a wave
+  // (and a workgroup) for up to 256 tokens
+  if (np <= 128 && a.B * a.T > 256) return launch_lpt<T, 32>(a, (np + 31) / 32, s);
   return launch_lpt<T, 64>(a, (np + 63) / 64, s);
 }
 
