@@ -256,6 +256,22 @@ __global__ void __launch_bounds__(512) linear_rows_dual_kernel(DualArgs a) {
     wo1[t] = static_cast<uint32_t>((n * a.w1_rs + kq * 8 * P) * 2);
     wo2[t] = static_cast<uint32_t>((n * a.w2_rs + kq * 8 * P) * 2);
   }
+  // The epilogue's gate and running-sum inputs, loaded first: they arrive during the
+  // product loads instead of costing a round trip after the reduction.
+  const int ep_l = threadIdx.x & 63, ep_tv = (threadIdx.x >> 6) % NT, ep_mt = (threadIdx.x >> 6) / NT;
+  const int ep_col = n0 + 16 * ep_tv + (ep_l & 15);
+  const bool ep_on = static_cast<int>(threadIdx.x) < MT * NT * 64 && ep_col < a.N;
+  // (kept as raw bf16 until the epilogue: a conversion here would wait for each load)
+  uint32_t gpre[4] = {0u, 0u, 0u, 0u}, apre[4] = {0u, 0u, 0u, 0u};
+  if (ep_on) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int rr = min(ep_mt * 16 + 4 * (ep_l >> 4) + j, rows - 1);
+      const int64_t m = m0 + rr;
+      if (GATE) gpre[j] = static_cast<uint32_t>(a.gate[m * a.gate_rs + ep_col]);
+      if (a.y2) apre[j] = static_cast<uint32_t>(a.aux2[m * a.aux2_rs + ep_col]);
+    }
+  }
   // Wave w takes the same k-steps of each product as the single-product kernel gives
   // it (w n / kWaves .. (w + 1) n / kWaves), so both sums are formed in the same order
   // as two separate launches would form them: the result is identical to them.
@@ -331,14 +347,15 @@ __global__ void __launch_bounds__(512) linear_rows_dual_kernel(DualArgs a) {
     const int rr = mt * 16 + 4 * (l >> 4) + j;
     if (rr >= rows) continue;
     const int64_t m = m0 + rr;
+    // (the empty asm keeps the compiler from hoisting the conversions, and with them
+    // the waits for these loads, to the top of the kernel)
+    uint32_t graw = gpre[j], araw = apre[j];
+    asm volatile("" : "+v"(graw), "+v"(araw));
     float u = rb(v1[j]);
-    if (GATE) {
-      const float gp = bf16_to_f32(a.gate[m * a.gate_rs + col]);
-      u = rb(u * rb(rcp_fast(1.f + __builtin_amdgcn_exp2f(-gp * kLog2e))));
-    }
+    if (GATE) u = rb(u * rb(rcp_fast(1.f + __builtin_amdgcn_exp2f(-bf16_to_f32(static_cast<bf16_t>(graw)) * kLog2e))));
     const float f = rb(u + rb(v2[j]));
     a.y[m * a.y_rs + col] = f32_to_bf16(f);
-    if (a.y2) a.y2[m * a.y2_rs + col] = f32_to_bf16(bf16_to_f32(a.aux2[m * a.aux2_rs + col]) + f);
+    if (a.y2) a.y2[m * a.y2_rs + col] = f32_to_bf16(bf16_to_f32(static_cast<bf16_t>(araw)) + f);
   }
 }
 
