@@ -211,7 +211,7 @@ __global__ void __launch_bounds__(256, 3) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
   float *gam = reinterpret_cast<float *>(smem + PL::small), *bet = gam + 64;
 
   const int chunk = blockIdx.x, h = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ln = lane & 15, g = lane >> 4;
   const ChunkInfo ci = resolve_chunk(chunk, kC, a.L, ca);
 
@@ -289,19 +289,28 @@ __global__ void __launch_bounds__(256, 3) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
     f_seg = t % S;
     f_r0 = (t / S) * rows;
     const int chan = h * C + 8 * f_seg;
-    const int col = (prob == 0 ? fa.q_off : prob == 1 ? fa.k_off : fa.v_off) + chan;
+    const int col0 = (prob == 0 ? fa.q_off : prob == 1 ? fa.k_off : fa.v_off) + h * C;  // the wave's head slice
     const bf16_t *wgt = (prob == 0 ? fa.wq : prob == 1 ? fa.wk : fa.wv) + static_cast<size_t>(chan) * KC;
     const bf16_t *tin = ca.cu ? nullptr : (prob == 0 ? fa.tq : prob == 1 ? fa.tk : fa.tv);
     const int s_lo = ca.cu ? ca.cu[ci.seq] : 0, s_hi = ca.cu ? ca.cu[ci.seq + 1] : a.L;
-    const bf16_t *xs = fa.x + ci.batch * fa.x_sb + int64_t(s_lo) * fa.x_st + col;
-    // rows outside [s_lo, s_hi) read zeros (a token before the start wraps to a huge offset)
-    const buf_t xbuf = make_buf(xs, s_hi > s_lo ? static_cast<uint32_t>(((s_hi - s_lo - 1) * fa.x_st + 8) * 2) : 0u);
+    // one buffer over the wave's head slice of the sequence's rows (a uniform resource:
+    // a per-lane base would make every load a loop over the lanes' distinct bases); rows
+    // outside [s_lo, s_hi) read zeros (a token before the start wraps to a huge offset,
+    // the segment's 16 f_seg bytes staying below one row)
+    const bf16_t *xs = fa.x + ci.batch * fa.x_sb + int64_t(s_lo) * fa.x_st + col0;
+    const buf_t xbuf = make_buf(xs, s_hi > s_lo ? static_cast<uint32_t>(((s_hi - s_lo - 1) * fa.x_st + C) * 2) : 0u);
     const int rel0 = ci.t0 - s_lo + f_r0;  // sequence offset of this thread's first row
+    // the gate inputs of row `lane` (clamped to the chunk; zeroed past len below), issued
+    // ahead of the conv inputs so that wave 0 forms the gates while those are in flight
+    // (every wave loads them: no branch around the batch of loads)
+    const bf16_t *xg = fa.x + ci.batch * fa.x_sb + int64_t(ci.t0 + min(lane, ci.len - 1)) * fa.x_st;
+    const bf16_t g_a = xg[fa.a_off + h], g_b = xg[fa.b_off + h];
+    const bf16_t g_dt = fa.dt_bias[h], g_al = fa.a_log[h];
     uint4 raw[KC - 1 + RM];
 #pragma unroll
     for (int i = 0; i < KC - 1 + RM; ++i)
       if (i < KC - 1 + rows)
-        raw[i] = buf_ld16(xbuf, static_cast<uint32_t>((rel0 - (KC - 1) + i) * fa.x_st * 2));
+        raw[i] = buf_ld16(xbuf, static_cast<uint32_t>((rel0 - (KC - 1) + i) * fa.x_st * 2 + 16 * f_seg));
     float wr[8][KC];
     {
       float wf[8 * KC];
@@ -321,6 +330,26 @@ __global__ void __launch_bounds__(256, 3) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
         for (int r = 0; r < KC; ++r) wr[e][r] = wf[e * KC + r];
     }
     __builtin_amdgcn_sched_barrier(0);  // the loads above stay one batch
+    // gates of the chunk's rows (zero past len, as the unfused loads read them)
+    if (w == 0) {
+      float gv = 0.f, bv = 0.f;
+      if (lane < ci.len) {
+        // beta = T(sigmoid(b)), g = T(-T(exp(A_log)) * T(softplus(T(a + dt_bias)))), threshold 20
+        const float xa = fl(bf(bf16_to_f32(g_a) + bf16_to_f32(g_dt)));
+        const float sp = fl(bf(xa > 20.f ? xa : log1pf(expf(xa))));
+        const float A = fl(bf(expf(bf16_to_f32(g_al))));
+        bv = fl(bf(1.f / (1.f + expf(-bf16_to_f32(g_b)))));
+        gv = fl(bf(-A * sp));
+      }
+      float sacc = gv;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float y = __shfl_up(sacc, off, 64);
+        if (lane >= off) sacc += y;
+      }
+      gam[lane] = sacc;
+      bet[lane] = bv;
+    }
     auto unpack8 = [](const uint4 &u, float *x) {
       const uint32_t ww[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
@@ -385,28 +414,6 @@ __global__ void __launch_bounds__(256, 3) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
           *reinterpret_cast<uint32_t *>(kt + swz(8 * f_seg + e, j)) = pack2(b0, b1);
         }
       }
-    }
-    // gates of the chunk's rows (zero past len, as the unfused loads read them)
-    if (w == 0) {
-      float gv = 0.f, bv = 0.f;
-      if (lane < ci.len) {
-        const bf16_t *xr = fa.x + ci.batch * fa.x_sb + int64_t(ci.t0 + lane) * fa.x_st;
-        const float av = bf16_to_f32(xr[fa.a_off + h]), braw = bf16_to_f32(xr[fa.b_off + h]);
-        // beta = T(sigmoid(b)), g = T(-T(exp(A_log)) * T(softplus(T(a + dt_bias)))), threshold 20
-        const float xa = fl(bf(av + bf16_to_f32(fa.dt_bias[h])));
-        const float sp = fl(bf(xa > 20.f ? xa : log1pf(expf(xa))));
-        const float A = fl(bf(expf(bf16_to_f32(fa.a_log[h]))));
-        bv = fl(bf(1.f / (1.f + expf(-braw))));
-        gv = fl(bf(-A * sp));
-      }
-      float sacc = gv;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const float y = __shfl_up(sacc, off, 64);
-        if (lane >= off) sacc += y;
-      }
-      gam[lane] = sacc;
-      bet[lane] = bv;
     }
     // the sequence's last chunk writes the outgoing conv tails (the last K-1 inputs)
     if (fa.oq && ci.t0 + ci.len == s_hi) {
