@@ -114,16 +114,34 @@ __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
     for (int e = 0; e < E; ++e) qw[i][e] = qv[e] * wv[e];
   }
 
-  // every source row is loaded before any reduction, so the loads overlap
-  float x[kMaxSrc][PPL][E];
+  // every source row is loaded before any reduction, so the loads overlap.  Plain loads
+  // from per-lane row addresses (a buffer resource per row would differ between the
+  // tokens of a wave and turn each load into a loop over them); pieces past D load the
+  // row's last piece and are masked to zeros by an AND (a select on the loaded value
+  // would become a branch around the load, and a wait for it).  The unpacking runs for
+  // every source slot after all loads (absent sources read as zeros): unpacked inside
+  // each source's branch, the loads of a source would wait for the previous one.
+  uint4 raw[kMaxSrc][PPL];
+#pragma unroll
+  for (int n = 0; n < kMaxSrc; ++n)
+#pragma unroll
+    for (int i = 0; i < PPL; ++i) raw[n][i] = uint4{0u, 0u, 0u, 0u};
 #pragma unroll
   for (int n = 0; n < kMaxSrc; ++n) {
     if (n >= a.nsrc) break;
-    // range-checked buffer over the row: pieces past D read as zeros, no branch
-    const buf_t row = make_buf(static_cast<const T *>(a.src[n]) + b * a.sb[n] + int64_t(t) * a.st[n],
-                               dbytes);
+    const T *row = static_cast<const T *>(a.src[n]) + b * a.sb[n] + int64_t(t) * a.st[n];
 #pragma unroll
-    for (int i = 0; i < PPL; ++i) Piece<T>::unpack(buf_ld16(row, (sub + LPT * i) * 16), x[n][i]);
+    for (int i = 0; i < PPL; ++i) raw[n][i] = *reinterpret_cast<const uint4 *>(row + min(sub + LPT * i, np - 1) * E);
+  }
+  float x[kMaxSrc][PPL][E];
+#pragma unroll
+  for (int i = 0; i < PPL; ++i) {
+    const uint32_t keep = sub + LPT * i < np ? 0xffffffffu : 0u;
+#pragma unroll
+    for (int n = 0; n < kMaxSrc; ++n) {
+      const uint4 u = raw[n][i];
+      Piece<T>::unpack(uint4{u.x & keep, u.y & keep, u.z & keep, u.w & keep}, x[n][i]);
+    }
   }
   float logit[kMaxSrc];
   float mx = -INFINITY;
