@@ -896,9 +896,12 @@ __global__ void __launch_bounds__(256) gdn_chunk_out(GdnArgs a, ChunkArgs ca, co
   const char *cell = ws + (static_cast<size_t>(h) * ca.total_chunks + chunk) * Lw.cell;
   const int ncg = a.dv / 16;
 
-  // gate pieces of the fused GatedRMSNorm, requested before the products
-  uint2 gv[kMaxCg][4];
+  // gate and norm-weight pieces of the fused GatedRMSNorm, requested before the products
+  uint2 gv[kMaxCg][4], nwv[kMaxCg];
   if (a.gate) {
+#pragma unroll
+    for (int i = 0; i < kMaxCg; ++i)
+      nwv[i] = *reinterpret_cast<const uint2 *>(static_cast<const bf16_t *>(a.nw) + 16 * min(w + 4 * i, ncg - 1) + 4 * g);
     const bf16_t *gp = static_cast<const bf16_t *>(a.gate) + ci.batch * a.gt_sb + int64_t(ci.t0) * a.gt_st + h * a.dv;
 #pragma unroll
     for (int i = 0; i < kMaxCg; ++i)
@@ -998,7 +1001,7 @@ __global__ void __launch_bounds__(256) gdn_chunk_out(GdnArgs a, ChunkArgs ca, co
     const int cg = w + 4 * i;
     if (cg >= ncg) break;
     const int c0 = 16 * cg + 4 * g;
-    const uint2 wraw = *reinterpret_cast<const uint2 *>(static_cast<const bf16_t *>(a.nw) + c0);
+    const uint2 wraw = nwv[i];
     const float wv[4] = {__uint_as_float(wraw.x << 16), __uint_as_float(wraw.x & 0xffff0000u),
                          __uint_as_float(wraw.y << 16), __uint_as_float(wraw.y & 0xffff0000u)};
 #pragma unroll
