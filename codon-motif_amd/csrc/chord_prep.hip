@@ -84,8 +84,16 @@ __global__ void __launch_bounds__(256) chord_prep_kernel(PrepArgs a) {
   else if (hh < a.H + a.Hkv) col = a.k_off + (hh - a.H) * a.D;
   else col = a.v_off + (hh - a.H - a.Hkv) * a.D;
   const T *src = static_cast<const T *>(a.proj) + b * a.p_sb + static_cast<int64_t>(t) * a.p_st + col;
+  // the row, its norm-weight piece (v rows load the q one and ignore it) and the device
+  // cache cursor are requested together, ahead of any use
+  const uint4 xraw = *reinterpret_cast<const uint4 *>(src + sub * E);
+  const uint4 wraw = *reinterpret_cast<const uint4 *>(static_cast<const T *>(hh >= a.H && hh < a.H + a.Hkv ? a.kw : a.qw) +
+                                                      sub * E);
+  // the cache position of this launch: the host's, or the device cursor (the decode
+  // kernel that follows reads the same cursor and advances it)
+  const int pos = a.pos >= 0 ? a.pos : __builtin_amdgcn_readfirstlane(*a.len_dev);
   float x[E];
-  Vec<T>::unpack(*reinterpret_cast<const uint4 *>(src + sub * E), x);
+  Vec<T>::unpack(xraw, x);
 
   const bool is_v = hh >= a.H + a.Hkv;
   // sum of squares over the row's LPR lanes (every lane joins the butterfly)
@@ -96,9 +104,6 @@ __global__ void __launch_bounds__(256) chord_prep_kernel(PrepArgs a) {
   for (int off = 1; off < LPR; off <<= 1) ss += __shfl_xor(ss, off, 64);
   if (!valid) return;
 
-  // the cache position of this launch: the host's, or the device cursor (the decode
-  // kernel that follows reads the same cursor and advances it)
-  const int pos = a.pos >= 0 ? a.pos : __builtin_amdgcn_readfirstlane(*a.len_dev);
   if (hh >= a.H && pos + t >= a.capacity) return;  // never write past the slab
   T *dst;
   if (hh < a.H) {
@@ -111,7 +116,7 @@ __global__ void __launch_bounds__(256) chord_prep_kernel(PrepArgs a) {
   if (!is_v) {
     const float rs = rsqrtf(ss / a.D + a.eps);
     float w[E];
-    Vec<T>::unpack(*reinterpret_cast<const uint4 *>(static_cast<const T *>(hh < a.H ? a.qw : a.kw) + sub * E), w);
+    Vec<T>::unpack(wraw, w);
 #pragma unroll
     for (int e = 0; e < E; ++e) x[e] = Vec<T>::round(x[e] * rs) * w[e];
   }
