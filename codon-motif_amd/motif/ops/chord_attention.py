@@ -232,9 +232,19 @@ def apply_chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, log_n, cu_seql
     sequence i covering rows [cu_seqlens[i], cu_seqlens[i+1]).  Each sequence is
     causal on its own with positions restarting at 0; log_n [1, T] is read at
     the packed row (log(1 .. len_i) per sequence reproduces separate runs).
-    Calls that need gradients run the sequences as separate differentiable torch runs.
+    Calls that need gradients run the sequences separately: through the HIP forward /
+    backward pair (`ChordFunction`) where it serves, else as differentiable torch runs.
     '''
     if wants_grad(q, k, v, alpha, beta, mu, ssmax, log_n):
+        if (q.shape[0] == 1 and q.shape[2] > 0 and k.shape[2] == q.shape[2]
+                and _grad_kernels_serve(q, k, v, alpha, beta, mu, ssmax, log_n, 0)):
+            cu = [int(x) for x in cu_seqlens.detach().to('cpu')]
+            if cu[0] != 0 or cu[-1] != q.shape[2] or any(b < a for a, b in zip(cu[:-1], cu[1:])):
+                raise ValueError('cu_seqlens must start at 0, be non-decreasing and end at T')
+            outs = [apply_chord_attention(q[:, :, a:b], k[:, :, a:b], v[:, :, a:b], alpha, beta, mu, ssmax,
+                                          log_n[:, a:b], q_start=0, softmax_scale=softmax_scale, eps=eps)
+                    for a, b in zip(cu[:-1], cu[1:]) if b > a]
+            return torch.cat(outs, dim=2)
         return chord_attention_varlen_torch(q, k, v, alpha, beta, mu, ssmax, log_n, cu_seqlens, softmax_scale, eps)
     if not _lib.available():
         raise RuntimeError('there is no usable HIP backend in the current environment')
