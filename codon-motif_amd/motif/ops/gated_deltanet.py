@@ -273,9 +273,17 @@ def chunk_gated_delta_rule_varlen(q, k, v, beta, g, cu_seqlens, S=None, chunk_si
         cu = [int(c) for c in cu_seqlens.detach().cpu()]
         outs, states = [], []
         for i in range(len(cu) - 1):
+            # each sequence through the chunk op's own gradient route (HIP scans where they
+            # serve); an empty one passes its state through
             sl = slice(cu[i], cu[i + 1])
-            o_i, S_i = gdn_chunk_torch(q[:, :, sl], k[:, :, sl], v[:, :, sl], beta[:, :, sl], g[:, :, sl],
-                                       None if S is None else S[i:i + 1], chunk_size)
+            if cu[i + 1] == cu[i]:
+                B_, H_, _, Dk_ = q.shape
+                o_i = q.new_empty(B_, H_, 0, v.shape[-1])
+                S_i = (S[i:i + 1].float() if S is not None
+                       else torch.zeros(1, H_, Dk_, v.shape[-1], dtype=torch.float32, device=q.device))
+            else:
+                o_i, S_i = chunk_gated_delta_rule(q[:, :, sl], k[:, :, sl], v[:, :, sl], beta[:, :, sl],
+                                                  g[:, :, sl], None if S is None else S[i:i + 1], chunk_size)
             outs.append(o_i)
             states.append(S_i)
         return torch.cat(outs, 2), torch.cat(states, 0)

@@ -116,3 +116,40 @@ def test_only_state_output_used():
     for t in (q, k, v, b, g):
         assert t.grad is not None and torch.isfinite(t.grad).all()
     assert q.grad.abs().max().item() == 0.0   # the state does not depend on q
+
+
+@pytest.mark.parametrize('dtype', [torch.float32, torch.bfloat16])
+def test_varlen_gradients_match_torch_form(dtype):
+    '''Packed sequences with gradients (each non-empty sequence through
+    GDNChunkFunction) against the per-sequence torch form in float64.'''
+    from motif.ops import chunk_gated_delta_rule_varlen
+    from motif.ops.autograd_path import gdn_chunk_torch
+    lens = [70, 0, 5, 130]
+    cu = torch.tensor([0] + list(torch.cumsum(torch.tensor(lens), 0)), dtype=torch.int32)
+    T = sum(lens)
+    q, k, v, b, g = gdn_inputs(1, 2, T, 64, 64, seed=31, dtype=dtype)
+    g0 = torch.Generator().manual_seed(5)
+    S0 = torch.randn(len(lens), 2, 64, 64, generator=g0) * 0.1
+    do = torch.randn(1, 2, T, 64, generator=g0, dtype=torch.float64)
+    dS = torch.randn(len(lens), 2, 64, 64, generator=g0, dtype=torch.float64) * 0.1
+
+    def ref_fn(q_, k_, v_, b_, g_, s_):
+        outs, sts = [], []
+        for i in range(len(lens)):
+            sl = slice(int(cu[i]), int(cu[i + 1]))
+            if sl.stop == sl.start:   # an empty sequence keeps its state
+                o_i, s_i = q_.new_empty(1, 2, 0, 64), s_[i:i + 1]
+            else:
+                o_i, s_i = gdn_chunk_torch(q_[:, :, sl], k_[:, :, sl], v_[:, :, sl], b_[:, :, sl], g_[:, :, sl],
+                                           s_[i:i + 1], 64)
+            outs.append(o_i)
+            sts.append(s_i)
+        return torch.cat(outs, 2), torch.cat(sts, 0)
+
+    ro, rS, rg = _grads(ref_fn, q, k, v, b, g, S0, do, dS, 'cpu', torch.float64)
+    go, gS, gg = _grads(lambda *a: chunk_gated_delta_rule_varlen(*a[:5], cu.to(DEV), S=a[5]),
+                        q, k, v, b, g, S0, do, dS, DEV, dtype)
+    _close(go, ro, 'o', 2e-2 if dtype == torch.bfloat16 else 1e-4)
+    bars = (1e-2, 5e-3) if dtype == torch.bfloat16 else (2e-3, 1e-3)
+    for name, got, ref in zip(('dq', 'dk', 'dv', 'dbeta', 'dg', 'dS0'), gg, rg):
+        _close(got, ref, name, *bars)
