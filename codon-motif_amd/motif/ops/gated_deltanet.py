@@ -12,9 +12,10 @@ Differences that do not change results beyond rounding:
   {16, 32, 64} (values >= 64 use 64); the chunk length only changes the order
   of floating-point operations, not the recurrence.
 Gradients: `chunk_gated_delta_rule` runs its HIP forward inside `GDNChunkFunction`
-(motif/ops/gdn_grad.py), whose backward uses the HIP fp32 scans; the recurrent and
-packed forms, and shapes the scans do not take, differentiate through the torch form
-of the chunked rule (motif/ops/autograd_path.py:gdn_chunk_torch).
+(motif/ops/gdn_grad.py), whose backward uses the HIP fp32 scans, and the packed form
+runs each sequence through it; the recurrent form and shapes the scans do not take
+differentiate through the torch form of the chunked rule
+(motif/ops/autograd_path.py:gdn_chunk_torch).
 '''
 import functools
 
