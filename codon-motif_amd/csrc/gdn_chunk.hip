@@ -919,20 +919,32 @@ __global__ void __launch_bounds__(256) gdn_chunk_out(GdnArgs a, ChunkArgs ca, co
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qh[mt][ks] = __builtin_bit_cast(bf16x8, qp[(mt * KS + ks) * 64]);
   // O tiles of this wave's column groups cg = w + 4 i: lane holds O[16 mt + ln][16 cg + 4 g + r]
+  // S_n and O' pieces of every column group of the wave, requested before any product
+  // (a group whose index passes ncg loads the last group again and is skipped below)
+  uint4 snv[kMaxCg][KS];
+  uint2 opv[kMaxCg][4];
+#pragma unroll
+  for (int i = 0; i < kMaxCg; ++i) {
+    const int cgl = min(w + 4 * i, ncg - 1);
+    const uint4 *sn = reinterpret_cast<const uint4 *>(cell + Lw.sn) + static_cast<size_t>(cgl) * KS * 64 + lane;
+    const uint2 *op = reinterpret_cast<const uint2 *>(cell + Lw.op) + static_cast<size_t>(cgl) * 4 * 64 + lane;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) snv[i][ks] = sn[ks * 64];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) opv[i][mt] = op[mt * 64];
+  }
   f32x4 res[kMaxCg][4];
 #pragma unroll
   for (int i = 0; i < kMaxCg; ++i) {
     const int cg = w + 4 * i;
     if (cg >= ncg) break;
-    const uint4 *sn = reinterpret_cast<const uint4 *>(cell + Lw.sn) + static_cast<size_t>(cg) * KS * 64 + lane;
-    const uint2 *op = reinterpret_cast<const uint2 *>(cell + Lw.op) + static_cast<size_t>(cg) * 4 * 64 + lane;
     bf16x8 sh[KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) sh[ks] = __builtin_bit_cast(bf16x8, sn[ks * 64]);
+    for (int ks = 0; ks < KS; ++ks) sh[ks] = __builtin_bit_cast(bf16x8, snv[i][ks]);
     f32x4 acc[4];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
-      const uint2 ov = op[mt * 64];
+      const uint2 ov = opv[i][mt];
       acc[mt] = f32x4{__uint_as_float(ov.x << 16), __uint_as_float(ov.x & 0xffff0000u),
                       __uint_as_float(ov.y << 16), __uint_as_float(ov.y & 0xffff0000u)};
     }
