@@ -208,7 +208,10 @@ __global__ void __launch_bounds__(256) chord_bwd_dq_kernel(ChordBwdArgs a) {
         sW[w][lane] = d <= 0 ? float4{bias, -xb, bias * l2 * 0.6931471805599453f, al * be * xb * rcp_fast(x) * sgn}
                              : float4{0.f, 0.f, 0.f, 0.f};
       }
-      // (the wave reads its own window below: LDS operations of a wave complete in order)
+      // The wave reads other lanes' window entries below: LDS operations of a wave complete
+      // in order, and the wave barrier keeps the compiler from moving those reads above
+      // this store.
+      __builtin_amdgcn_wave_barrier();
       f32x16 sacc = {}, pacc = {};
 #pragma unroll
       for (int ds = 0; ds < 4; ++ds) {
@@ -370,7 +373,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         const float x = fabsf(static_cast<float>(d) - mu) + a.eps;
         sW[w][lane] = d <= 0 ? -al * fast_exp2(be * fast_log2(x)) : 0.f;
       }
-      // (the wave reads its own window below: LDS operations of a wave complete in order)
+      // The wave reads other lanes' window entries below: LDS operations of a wave complete
+      // in order, and the wave barrier keeps the compiler from moving those reads above
+      // this store.
+      __builtin_amdgcn_wave_barrier();
       f32x16 sacc = {}, pacc = {};
 #pragma unroll
       for (int ds = 0; ds < 4; ++ds) {

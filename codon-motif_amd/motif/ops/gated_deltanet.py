@@ -270,8 +270,22 @@ def chunk_gated_delta_rule_varlen(q, k, v, beta, g, cu_seqlens, S=None, chunk_si
         (o [1, H, L, Dv] in q's dtype, S [nseq, H, Dk, Dv] fp32)
     '''
     name = 'chunk_gated_delta_rule_varlen'
+    for n, t in (('q', q), ('v', v)):
+        if t.dim() != 4:
+            raise ValueError(f'{name}: {n} must be 4-D [B, H, L, D], got {tuple(t.shape)}')
+    B, H, L, Dk = q.shape
+    Dv = v.shape[-1]
+    if B != 1:
+        raise ValueError(f'{name}: packed sequences need B == 1, got B={B}')
+    nseq = int(cu_seqlens.numel()) - 1
+    if nseq < 1:
+        raise ValueError(f'{name}: cu_seqlens needs at least two entries')
+    if S is not None and S.shape != (nseq, H, Dk, Dv):
+        raise ValueError(f'{name}: S must be [nseq, H, Dk, Dv] = {(nseq, H, Dk, Dv)}')
     if _needs_grad(q, k, v, beta, g, S):
         cu = [int(c) for c in cu_seqlens.detach().cpu()]
+        if cu[0] != 0 or cu[-1] != L or any(b < a for a, b in zip(cu, cu[1:])):
+            raise ValueError('cu_seqlens must start at 0, be non-decreasing and end at L')
         outs, states = [], []
         for i in range(len(cu) - 1):
             # each sequence through the chunk op's own gradient route (HIP scans where they
@@ -289,18 +303,7 @@ def chunk_gated_delta_rule_varlen(q, k, v, beta, g, cu_seqlens, S=None, chunk_si
             states.append(S_i)
         return torch.cat(outs, 2), torch.cat(states, 0)
     (qc, kc, vc, bc, gc), _ = _prepare(q, k, v, beta, g, name)
-    B, H, L, Dk = qc.shape
-    if B != 1:
-        raise ValueError(f'{name}: packed sequences need B == 1, got B={B}')
-    nseq = int(cu_seqlens.numel()) - 1
-    if nseq < 1:
-        raise ValueError(f'{name}: cu_seqlens needs at least two entries')
-    Dv = vc.shape[-1]
-    S_in = None
-    if S is not None:
-        if S.shape != (nseq, H, Dk, Dv):
-            raise ValueError(f'{name}: S must be [nseq, H, Dk, Dv] = {(nseq, H, Dk, Dv)}')
-        S_in = S.to(device=qc.device, dtype=torch.float32).contiguous()
+    S_in = None if S is None else S.to(device=qc.device, dtype=torch.float32).contiguous()
     o, S_out = _chunk_call(qc, kc, vc, bc, gc, S_in, _kernel_chunk(int(chunk_size)), cu_seqlens, nseq)
     return o.to(q.dtype), S_out
 

@@ -24,7 +24,10 @@ from . import _lib
 
 
 def scans_serve(Dk: int, Dv: int, C: int) -> bool:
-    return C in (16, 32, 64) and Dk % 16 == 0 and Dk <= 128 and Dv % 16 == 0
+    '''True when both the HIP chunk forward (dk 32 / 64 / 128) and the two fp32 scans
+    (C 16 / 32 / 64, Dv a multiple of 16) take this shape; other shapes differentiate
+    through the torch form.'''
+    return C in (16, 32, 64) and Dk in (32, 64, 128) and Dv % 16 == 0
 
 
 def fused_scan(k, W, U, g, S0):

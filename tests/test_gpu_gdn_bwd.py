@@ -90,7 +90,10 @@ def _grads(fn, q, k, v, b, g, S0, do, dS, dev, dtype):
 
 
 @pytest.mark.parametrize('dtype', [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize('B,H,L,dk,dv,C', [(2, 3, 200, 64, 128, 64), (1, 2, 77, 32, 64, 32)])
+# dk = 16 / 48: head sizes the HIP chunk forward does not take, differentiated through the
+# torch form on the device
+@pytest.mark.parametrize('B,H,L,dk,dv,C', [(2, 3, 200, 64, 128, 64), (1, 2, 77, 32, 64, 32),
+                                           (1, 2, 90, 16, 32, 64), (1, 1, 70, 48, 16, 16)])
 def test_chunk_rule_gradients_match_torch_form(dtype, B, H, L, dk, dv, C):
     from motif.ops import chunk_gated_delta_rule
     from motif.ops.autograd_path import gdn_chunk_torch
@@ -153,3 +156,23 @@ def test_varlen_gradients_match_torch_form(dtype):
     bars = (1e-2, 5e-3) if dtype == torch.bfloat16 else (2e-3, 1e-3)
     for name, got, ref in zip(('dq', 'dk', 'dv', 'dbeta', 'dg', 'dS0'), gg, rg):
         _close(got, ref, name, *bars)
+
+
+def test_varlen_gradient_branch_validates_cu_seqlens():
+    '''The packed form checks B, S and cu_seqlens before choosing its gradient or
+    no-gradient branch, with the same errors either way.'''
+    from motif.ops import chunk_gated_delta_rule_varlen
+    q, k, v, b, g = (t.to(DEV) for t in gdn_inputs(1, 2, 50, 64, 64, seed=9))
+    for grad in (False, True):
+        ts = [t.clone().requires_grad_(grad) for t in (q, k, v, b, g)]
+        for cu in ([0, 20, 40], [5, 20, 50], [0, 30, 20, 50]):
+            with pytest.raises(ValueError, match='cu_seqlens'):
+                chunk_gated_delta_rule_varlen(*ts, torch.tensor(cu, dtype=torch.int32, device=DEV))
+        with pytest.raises(ValueError, match='S must be'):
+            chunk_gated_delta_rule_varlen(*ts, torch.tensor([0, 50], dtype=torch.int32, device=DEV),
+                                          S=torch.zeros(2, 2, 64, 64, device=DEV))
+        q2 = torch.cat([ts[0]] * 2)
+        with pytest.raises(ValueError, match='B == 1'):
+            chunk_gated_delta_rule_varlen(q2, torch.cat([ts[1]] * 2), torch.cat([ts[2]] * 2),
+                                          torch.cat([ts[3]] * 2), torch.cat([ts[4]] * 2),
+                                          torch.tensor([0, 50], dtype=torch.int32, device=DEV))
