@@ -84,6 +84,27 @@ template <> __device__ __forceinline__ float buf_ld<bf16_t>(buf_t r, uint32_t el
   return bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(r, elem * 2, 0, 0));
 }
 
+// x rounded to the storage type T and back (identity for float).
+template <typename T> __device__ __forceinline__ float round_as(float x) { return x; }
+template <> __device__ __forceinline__ float round_as<bf16_t>(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+template <> __device__ __forceinline__ float round_as<f16_t>(float x) { return static_cast<float>(static_cast<f16_t>(x)); }
+
+// The GatedDelta q / k / v front end in the arithmetic of the reference layer run in the
+// activation type T (motif/block/attention/gdn_attn.py:116-136, :187-191): the causal
+// conv's output is rounded to T, SiLU of that value is rounded to T; F.normalize takes
+// the vector norm (fp32 sum of squares) rounded to T and clamped at eps, the quotient
+// rounded to T, and q's product with dk^-1/2 rounded to T (a product with 1 for k is
+// exact).
+template <typename T> __device__ __forceinline__ float gdn_conv_act(float acc) {
+  return round_as<T>(silu_fast(round_as<T>(acc)));
+}
+template <typename T> __device__ __forceinline__ float gdn_norm_denom(float sum_sq) {
+  return fmaxf(round_as<T>(sqrtf(sum_sq)), round_as<T>(1e-12f));
+}
+template <typename T> __device__ __forceinline__ float gdn_normalized(float y, float denom, float scale) {
+  return round_as<T>(round_as<T>(y / denom) * scale);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);

@@ -6,6 +6,8 @@
 // Each run is processed 16 timesteps at a time with all 16 loads issued before the
 // arithmetic.  With HD > 0 a head is HD consecutive lanes: the sum of squares is a
 // butterfly over those lanes, y / max(||y||, 1e-12) * scale (F.normalize semantics).
+// Every intermediate the reference layer rounds to the activation type (conv output,
+// SiLU, the norm, the quotient, q's scaled value) is rounded here at the same point.
 // The conv tail (last K-1 pre-activation inputs) is written by the thread that owns
 // the sequence's final run.
 #include "capi_internal.h"
@@ -115,12 +117,12 @@ __global__ void __launch_bounds__(256) short_conv_silu_kernel(ConvArgs a) {
       float acc = wr[K - 1] * xs[i];
 #pragma unroll
       for (int r = 0; r < K - 1; ++r) acc = fmaf(wr[r], win[r], acc);
-      float v = silu_fast(acc);
+      float v = gdn_conv_act<T>(acc);
       if (HD > 0) {
         float ss = v * v;
 #pragma unroll
         for (int off = 1; off < HD; off <<= 1) ss += __shfl_xor(ss, off, 64);
-        v *= a.scale * rcp_fast(fmaxf(sqrtf(ss), 1e-12f));
+        v = gdn_normalized<T>(v, gdn_norm_denom<T>(ss), a.scale);
       }
       if (active && t0 + i < t_hi) st(y + int64_t(t0 + i) * a.y_st, v);
 #pragma unroll
@@ -255,7 +257,7 @@ __global__ void __launch_bounds__(256) short_conv_silu_vec_kernel(ConvGroup grp)
       float acc = wr[e][K - 1] * xt[e];
 #pragma unroll
       for (int r = 0; r < K - 1; ++r) acc = fmaf(wr[e][r], win[r][e], acc);
-      v[e] = silu_fast(acc);
+      v[e] = gdn_conv_act<T>(acc);
       ss = fmaf(v[e], v[e], ss);
 #pragma unroll
       for (int r = 0; r < K - 2; ++r) win[r][e] = win[r + 1][e];
@@ -264,9 +266,9 @@ __global__ void __launch_bounds__(256) short_conv_silu_vec_kernel(ConvGroup grp)
     if (norm) {
 #pragma unroll
       for (int off = 1; off < G; off <<= 1) ss += __shfl_xor(ss, off, 64);
-      const float f = a.scale * rcp_fast(fmaxf(sqrtf(ss), 1e-12f));
+      const float den = gdn_norm_denom<T>(ss);
 #pragma unroll
-      for (int e = 0; e < E; ++e) v[e] *= f;
+      for (int e = 0; e < E; ++e) v[e] = gdn_normalized<T>(v[e], den, a.scale);
     }
     if (t_lo + i < t_hi) *reinterpret_cast<uint4 *>(y + int64_t(t_lo + i) * a.y_st) = Vec16<T>::pack(v);
   }

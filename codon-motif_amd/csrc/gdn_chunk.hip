@@ -279,7 +279,8 @@ __global__ void __launch_bounds__(256, 3) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
     // thread walks R consecutive chunk rows of one 8-channel segment with the conv
     // window in registers; the S segments of a row are S adjacent lanes, so the q / k
     // L2 norm of a row is a butterfly over them.  Arithmetic as the standalone conv
-    // kernel: fp32 conv, SiLU, norm, one rounding to bf16.
+    // kernel: fp32 conv accumulation, then the reference layer's bf16 roundings (conv
+    // output, SiLU, norm, quotient, scaled q).
     constexpr int KC = kConvK;
     const int prob = w < 2 ? w : 2;
     const int C = prob < 2 ? DK : DV;
@@ -382,7 +383,7 @@ __global__ void __launch_bounds__(256, 3) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
           float acc = wr[e][KC - 1] * xt[e];
 #pragma unroll
           for (int r = 0; r < KC - 1; ++r) acc = fmaf(wr[e][r], win[r][e], acc);
-          v[e] = live ? silu_fast(acc) : 0.f;
+          v[e] = live ? gdn_conv_act<bf16_t>(acc) : 0.f;
           ss = fmaf(v[e], v[e], ss);
 #pragma unroll
           for (int r = 0; r < KC - 2; ++r) win[r][e] = win[r + 1][e];
@@ -392,9 +393,9 @@ __global__ void __launch_bounds__(256, 3) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
 #pragma unroll
           for (int off = 1; off < 8; off <<= 1)
             if (off < S) ss += __shfl_xor(ss, off, 64);
-          const float f = scale * rcp_fast(fmaxf(sqrtf(ss), 1e-12f));
+          const float den = gdn_norm_denom<bf16_t>(ss);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) v[e] *= f;
+          for (int e = 0; e < 8; ++e) v[e] = gdn_normalized<bf16_t>(v[e], den, scale);
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) cv[i][e] = pk_bf16(v[2 * e], v[2 * e + 1]);

@@ -11,7 +11,11 @@
 //   4. the delta rule on the fp32 state column S[:, e] held in registers:
 //      S *= e^g; S += k (beta (v_e - k^T S)); o_e = q^T S;
 //   5. GatedRMSNorm of the head's dv outputs: o * rsqrt(mean(o^2) + eps) * w * SiLU(gate).
-// fp32 arithmetic throughout.  The reference runs these as separate steps
+// fp32 arithmetic, with every value the reference layer holds in the activation type T
+// rounded to T at the same point: the conv output and its SiLU, the norm, quotient and
+// scaled q, beta and the g chain (a + dt_bias, softplus, e^A_log, the product), the
+// recurrence's output o, and the three products of the GatedRMSNorm (the recurrence
+// itself runs in fp32, as the reference's does).  The reference runs these as separate steps
 // (motif/block/attention/gdn_attn.py:116-136 conv, :183-209 normalise / gates /
 // recurrent_gated_delta_rule (motif/ops/gated_deltanet.py:26-59) / o_norm,
 // motif/ops/rms_norm.py:530-553 GatedRMSNorm).
@@ -81,7 +85,7 @@ __global__ void __launch_bounds__(128) gdn_decode_kernel(GdnDecodeArgs a) {
 #pragma unroll
     for (int r = 0; r < K - 2; ++r) st(to + r, t[r + 1]);
     st(to + K - 2, xnew);
-    return silu_fast(acc);
+    return gdn_conv_act<T>(acc);
   };
 
   // 1-2. q / k channels: threads [0, DK) -> q, [DK, 2 DK) -> k; an aligned group of
@@ -95,17 +99,20 @@ __global__ void __launch_bounds__(128) gdn_decode_kernel(GdnDecodeArgs a) {
     float ss = y * y;
 #pragma unroll
     for (int off = 1; off < DK; off <<= 1) ss += __shfl_xor(ss, off, 64);
-    const float nrm = fmaxf(sqrtf(ss), 1e-12f);
-    if (isq) sq[c] = y * (rsqrtf(static_cast<float>(DK)) / nrm);
-    else sk[c] = y / nrm;
+    // dk^-1/2 as the host's float(dk ** -0.5)
+    constexpr float qs = DK == 16 ? 0.25f : DK == 32 ? 0.17677669529663687f : DK == 64 ? 0.125f : 0.08838834764831845f;
+    const float den = gdn_norm_denom<T>(ss);
+    if (isq) sq[c] = gdn_normalized<T>(y, den, qs);
+    else sk[c] = gdn_normalized<T>(y, den, 1.f);
   }
   float vcol = 0.f;
   if (active) vcol = conv(a.wv, a.tv, a.ov, a.H * a.dv, h * a.dv + tid, xv);
-  // 3. gates (uniform)
-  const float beta = 1.f / (1.f + exp_f(-bv));
-  const float xa = av + dtb;
-  const float sp = xa > 20.f ? xa : log1pf(exp_f(xa));  // softplus, threshold 20
-  const float decay = exp_f(-exp_f(alog) * sp);
+  // 3. gates (uniform): beta = T(sigmoid(b)), g = T(-T(e^A_log) * T(softplus(T(a + dt_bias))))
+  // (softplus threshold 20), decay = e^g in fp32
+  const float beta = round_as<T>(1.f / (1.f + expf(-bv)));
+  const float xa = round_as<T>(av + dtb);
+  const float sp = round_as<T>(xa > 20.f ? xa : log1pf(expf(xa)));
+  const float decay = expf(round_as<T>(-round_as<T>(expf(alog)) * sp));
   __syncthreads();
 
   // 4. delta rule on column e
@@ -128,13 +135,15 @@ __global__ void __launch_bounds__(128) gdn_decode_kernel(GdnDecodeArgs a) {
       __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, S[i]), obuf, col, i * row, 0);
   }
 
-  // 5. GatedRMSNorm over the head's dv outputs (two waves: partial sums in LDS)
+  // 5. GatedRMSNorm over the head's dv outputs (two waves: partial sums in LDS) of o
+  // rounded to T: y = T(T(T(o rsqrt(mean o^2 + eps)) w) T(silu(gate)))
+  o = round_as<T>(o);
   const float part = wave_sum(active ? o * o : 0.f);
   if (lane == 0) sred[w] = part;
   __syncthreads();
   const float ms = (sred[0] + (blockDim.x > 64 ? sred[1] : 0.f)) / static_cast<float>(a.dv);
   if (active) {
-    const float yv = o * rsqrtf(ms + a.norm_eps) * nw * silu_fast(gt);
+    const float yv = round_as<T>(round_as<T>(o * rsqrtf(ms + a.norm_eps)) * nw) * round_as<T>(silu_fast(gt));
     st(static_cast<T *>(a.y) + b * a.y_sb + h * a.dv + tid, yv);
   }
 }

@@ -28,7 +28,7 @@ from motif.model.cache import KVLayerCache, StaticKVLayerCache, expand_kv_heads
 from motif.ops import RMSNorm, apply_chord_attention, apply_chord_attention_varlen
 from motif.ops import _lib
 from motif.ops.autograd_path import wants_grad
-from motif.ops.chord_attention import HEAD_DIMS, chord_decode_cursor, chord_decode_workspace
+from motif.ops.chord_attention import HEAD_DIMS, chord_decode_cursor, chord_decode_workspace, serves_head_dim
 from motif.ops.epilogue import mul_sigmoid, usable
 from motif.ops.linear_rows import cat_weights, linear_rows, project, rows_eligible
 
@@ -131,7 +131,7 @@ class ChordAttention(BasicAttention):
         materialised path with a one-time warning.'''
         if not x.is_cuda:
             return False
-        if x.dtype in _ATTN_DTYPES and self.head_dim in HEAD_DIMS and _lib.available():
+        if x.dtype in _ATTN_DTYPES and serves_head_dim(self.head_dim) and _lib.available():
             return True
         if not self._warned:
             warnings.warn(f'ChordAttention: no HIP kernel for {x.dtype} / head_dim {self.head_dim}; '
@@ -156,6 +156,7 @@ class ChordAttention(BasicAttention):
         '''Decode over a static cache at its own position: the device-cursor path.'''
         L = x.shape[1]
         return (isinstance(cache, StaticKVLayerCache) and cache.capacity > 0 and not cache.wide
+                and self.head_dim in HEAD_DIMS
                 and q_start == cache.length and cache.length + L <= cache.capacity
                 and cache.k.dtype == x.dtype and self.num_kv_queries * L <= _DECODE_ROWS
                 and self._prep_fusable(x, cache))

@@ -89,13 +89,23 @@ class GatedDeltaAttention(BasicAttention):
         self.k_conv = nn.Conv1d(dk_all, dk_all, conv_size, groups=dk_all, bias=False)
         self.v_conv = nn.Conv1d(dv_all, dv_all, conv_size, groups=dv_all, bias=False)
 
-        # A ~ U(1, 16); dt log-uniform in [1e-3, 1e-1] stored as softplus^-1(dt).
-        A = torch.empty(self.num_heads).uniform_(1, 16)
-        self.A_log = nn.Parameter(A.log())
-        dt = torch.exp(torch.rand(self.num_heads) * (math.log(0.1) - math.log(0.001)) + math.log(0.001))
-        self.dt_bias = nn.Parameter(dt + torch.log(-torch.expm1(-dt)))
+        self.A_log = nn.Parameter(torch.empty(self.num_heads))
+        self.dt_bias = nn.Parameter(torch.empty(self.num_heads))
+        self.init_gates()
 
         self.o_norm = GatedRMSNorm(self.dv)
+
+    @torch.no_grad()
+    def init_gates(self, generator: Optional[torch.Generator] = None) -> None:
+        '''The decay parameters' initial values: A ~ U(1, 16) stored as log A, dt
+        log-uniform in [1e-3, 1e-1] stored as softplus^-1(dt) (motif/block/attention/
+        gdn_attn.py:99-104).  Drawn from `generator`, or from the global RNG as the
+        reference's constructor does.'''
+        n = self.num_heads
+        A = torch.rand(n, generator=generator) * 15 + 1
+        dt = torch.exp(torch.rand(n, generator=generator) * (math.log(0.1) - math.log(0.001)) + math.log(0.001))
+        self.A_log.copy_(A.log().to(self.A_log))
+        self.dt_bias.copy_((dt + torch.log(-torch.expm1(-dt))).to(self.dt_bias))
 
     @classmethod
     def cache_type(cls) -> type:

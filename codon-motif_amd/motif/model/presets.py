@@ -3,10 +3,13 @@
 - `config_172m`: the published model shape (d=768, 4 blocks x (3 GatedDelta + 1
   Chord), 12 heads, GDN dk=64 / dv=128, Chord D=64 with 3 kv heads, SwiGLU 2048) at
   a chosen vocabulary (32000 in the benchmark configurations).
-- `init_random`: random initialisation of a model with no checkpoint: every
-  Linear / Embedding / Conv1d weight ~ N(0, std) from a seeded CPU generator, the
-  semantic parameters (A_log, dt_bias, theta_*, ssmax_s, pseudo-queries, norms)
-  left at their constructor values, so the recurrence stays in its designed regime.
+- `init_random`: random initialisation of a model with no checkpoint, wholly
+  determined by the seed: every Linear / Embedding / Conv1d weight ~ N(0, std) and
+  the GatedDelta decay parameters (A_log, dt_bias: their constructor distributions)
+  from one seeded CPU generator; the other semantic parameters (theta_*, ssmax_s,
+  pseudo-queries, norms) keep their constant constructor values, so the recurrence
+  stays in its designed regime.  (The constructor draws A_log / dt_bias from the
+  global RNG, whose seed differs from process to process.)
 - `packed_lengths`: the sequence lengths of the packed prefill configuration
   (uniform in [lo, hi], seeded).
 '''
@@ -29,6 +32,8 @@ def init_random(model: nn.Module, std: float = 0.02, seed: int = 0) -> nn.Module
         for m in model.modules():
             if isinstance(m, (nn.Linear, nn.Embedding, nn.Conv1d)):
                 m.weight.copy_(torch.randn(m.weight.shape, generator=g) * std)
+            elif hasattr(m, 'init_gates'):
+                m.init_gates(g)
     return model
 
 

@@ -27,6 +27,12 @@ HEAD_DIM = 64                  # the model's head dim: bf16 runs on the MFMA ker
 HEAD_DIMS = (16, 32, 64, 128)  # head dims the kernels serve (fp32 / fp16 / other D: the vector kernel)
 
 
+def serves_head_dim(D: int) -> bool:
+    '''Head dims apply_chord_attention takes: the kernels' own (HEAD_DIMS) and every
+    size between them (zero-padded to the next one).'''
+    return HEAD_DIMS[0] <= D <= HEAD_DIMS[-1]
+
+
 def _grad_kernels_serve(q, k, v, alpha, beta, mu, ssmax, log_n, q_start):
     '''The backward kernels take bf16 q / k / v with head dim 64 on a GPU, fp32 [H]
     parameters and no gradient into log_n (as the reference's backward).'''
@@ -137,14 +143,30 @@ def _aligned(t):
 
 
 def _launch(q, k, v, alpha, beta, mu, ssmax, log_n, q_start, scale, eps, out, lse=None,
-            cu_dev=None, nseq=None, max_seqlen=None):
+            cu_dev=None, nseq=None, max_seqlen=None, cu_host=None):
     B, H, L, D = q.shape
     Hkv, S = k.shape[1], k.shape[2]
     if D not in HEAD_DIMS:
-        raise NotImplementedError(f'apply_chord_attention: head_dim {D} unsupported (16, 32, 64 or 128)')
+        # a head dim between the kernels' sizes: q, k, v zero-padded to the next one (the
+        # extra features add nothing to q.k and give zero output columns), output cut back
+        Dp = next((d for d in HEAD_DIMS if d > D), None)
+        if Dp is None or lse is not None:
+            raise NotImplementedError(f'apply_chord_attention: head_dim {D} unsupported (16 to 128)')
+        pad = lambda t: torch.nn.functional.pad(t, (0, Dp - D))
+        out_p = torch.empty((B, H, L, Dp), dtype=out.dtype, device=out.device)
+        _launch(pad(q), pad(k), pad(v), alpha, beta, mu, ssmax, log_n, q_start, scale, eps, out_p,
+                cu_dev=cu_dev, nseq=nseq, max_seqlen=max_seqlen, cu_host=cu_host)
+        out.copy_(out_p[..., :D])
+        return out
     if cu_dev is not None and (q.dtype != torch.bfloat16 or D != HEAD_DIM):
-        raise NotImplementedError('apply_chord_attention_varlen: packed sequences are implemented for bf16, '
-                                  f'head_dim {HEAD_DIM}')
+        # the packed kernel serves bf16 at head dim 64; other packed inputs run sequence
+        # by sequence (each one causal from position 0) on the same kernels
+        cu = [int(x) for x in cu_host]
+        for a, b in zip(cu[:-1], cu[1:]):
+            if b > a:
+                _launch(q[:, :, a:b], k[:, :, a:b], v[:, :, a:b], alpha, beta, mu, ssmax, log_n[:, a:b], 0,
+                        scale, eps, out[:, :, a:b])
+        return out
     q, k, v = _aligned(q), _aligned(k), _aligned(v)
     lib = _lib.lib()
     if cu_dev is None:
@@ -183,7 +205,7 @@ def apply_chord_attention(
     keys j <= q_start + i, softmax over keys, times v.
 
     Args:
-        q: [B, H, L, D];  k, v: [B, H_kv, S, D] (bf16 or fp32, D == 64).
+        q: [B, H, L, D];  k, v: [B, H_kv, S, D] (fp16, bf16 or fp32; 16 <= D <= 128).
         alpha, beta, mu, ssmax: [H] fp32 contiguous.
         log_n: [B, L] fp32.
         q_start: absolute position of the first query; defaults to S - L.
@@ -195,8 +217,8 @@ def apply_chord_attention(
 
     Raises:
         ValueError: on unsupported inputs or a negative q_start.
-        NotImplementedError: for a head dim outside 16, 32, 64, 128 (inputs requiring
-            grad take the differentiable torch form).
+        NotImplementedError: for a head dim above 128 (inputs requiring grad take the
+            differentiable torch form).
         RuntimeError: when the HIP library is unavailable or a launch fails.
     '''
     if wants_grad(q, k, v, alpha, beta, mu, ssmax, log_n):
@@ -263,7 +285,7 @@ def apply_chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, log_n, cu_seql
         return out
     cu_dev = cu_host.to(device=q.device, dtype=torch.int32)
     return _launch(q, k, v, alpha, beta, mu, ssmax, log_n, 0, softmax_scale, eps, out,
-                   cu_dev=cu_dev, nseq=int(lens.numel()), max_seqlen=int(lens.max()))
+                   cu_dev=cu_dev, nseq=int(lens.numel()), max_seqlen=int(lens.max()), cu_host=cu_host)
 
 
 def chord_decode_workspace(B, H, Hkv, L, capacity, D, dtype, device) -> torch.Tensor:

@@ -43,14 +43,14 @@ def _check_heads(out, q, k, v, alpha, beta, mu, ssmax, log_n, q_start, heads=Non
 
 @pytest.mark.parametrize('Hkv', [12, 3])
 def test_prefill_config2_shape(Hkv):
-    '''Config 2 (B=2, H=12, T=2048, D=64, causal), checked on 3 heads against fp64.'''
+    '''Config 2 (B=2, H=12, T=2048, D=64, causal), every head checked against fp64.'''
     ops = _ops()
     B, H, L = 2, 12, 2048
     q, k, v, alpha, beta, mu, ssmax = chord_inputs(B, H, Hkv, L, L, seed=0)
     log_n = _log_n(B, L, 0)
     out = _run(ops, q, k, v, alpha, beta, mu, ssmax, log_n, q_start=0)
     assert out.dtype == torch.bfloat16 and out.shape == (B, H, L, 64)
-    _check_heads(out.cpu(), q, k, v, alpha, beta, mu, ssmax, log_n, 0, heads=[0, 5, 11], what='cfg2')
+    _check_heads(out.cpu(), q, k, v, alpha, beta, mu, ssmax, log_n, 0, heads=range(H), what='cfg2')
 
 
 @pytest.mark.parametrize('L', [1, 31, 77, 200])
@@ -192,8 +192,57 @@ def test_dtypes_and_head_dims(dtype, D, B, H, Hkv, L, S):
         assert_bf16_close(out, ref, what=f'{dtype} D={D}')
 
 
-def test_unsupported_head_dim_raises_not_implemented():
+@pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize('D', [20, 48, 80, 112])
+@pytest.mark.parametrize('B,H,Hkv,L,S', [(2, 4, 2, 70, 70), (3, 6, 3, 1, 700)])
+def test_head_dims_between_kernel_sizes(dtype, D, B, H, Hkv, L, S):
+    '''Any head dim from 16 to 128 (the reference takes any D >= 16): sizes between the
+    kernels' own run zero-padded to the next one, with the caller's softmax scale.'''
     ops = _ops()
-    q, k, v, alpha, beta, mu, ssmax = (t.to(DEV) for t in chord_inputs(1, 2, 1, 8, 8, D=48))
+    q, k, v, alpha, beta, mu, ssmax = chord_inputs(B, H, Hkv, L, S, seed=D + L, D=D)
+    q, k, v = q.float().to(dtype), k.float().to(dtype), v.float().to(dtype)
+    log_n = _log_n(B, L, S - L)
+    out = _run(ops, q, k, v, alpha, beta, mu, ssmax, log_n)
+    assert out.dtype == dtype and out.shape == (B, H, L, D)
+    ref = ochord.chord_attention(q.double(), k.double(), v.double(), alpha, beta, mu, ssmax, log_n, S - L)
+    if dtype == torch.float32:
+        err = (out.double().cpu() - ref).abs().max().item()
+        assert err <= 1e-4, err
+    else:
+        assert_bf16_close(out, ref, what=f'{dtype} D={D}')
+
+
+def test_head_dim_above_128_raises_not_implemented():
+    ops = _ops()
+    q, k, v, alpha, beta, mu, ssmax = (t.to(DEV) for t in chord_inputs(1, 2, 1, 8, 8, D=160))
     with pytest.raises(NotImplementedError):
         ops.apply_chord_attention(q, k, v, alpha, beta, mu, ssmax, _log_n(1, 8, 0).to(DEV))
+
+
+@pytest.mark.parametrize('dtype,D', [(torch.float32, 64), (torch.float16, 64), (torch.bfloat16, 32),
+                                     (torch.float32, 48)])
+def test_varlen_other_dtypes_and_head_dims(dtype, D):
+    '''Packed sequences outside the packed kernel's bf16 / D = 64 (each sequence on the
+    kernels by itself): equal to the separate runs, and within the bar of the oracle.'''
+    ops = _ops()
+    lens = [40, 1, 0, 97]
+    T = sum(lens)
+    cu = torch.tensor([0] + list(torch.cumsum(torch.tensor(lens), 0)), dtype=torch.int32)
+    q, k, v, alpha, beta, mu, ssmax = chord_inputs(1, 4, 2, T, T, seed=D, D=D)
+    q, k, v = q.float().to(dtype), k.float().to(dtype), v.float().to(dtype)
+    pos = torch.cat([torch.arange(n) for n in lens])
+    log_n = torch.log(pos.float() + 1)[None]
+    dev = [t.to(DEV) for t in (q, k, v, alpha, beta, mu, ssmax, log_n)]
+    out = ops.apply_chord_attention_varlen(*dev, cu.to(DEV))
+    for a, b in zip(cu[:-1].tolist(), cu[1:].tolist()):
+        if b == a:
+            continue
+        alone = ops.apply_chord_attention(*[t[:, :, a:b] for t in dev[:3]], *dev[3:7], dev[7][:, a:b].contiguous(),
+                                          q_start=0)
+        assert torch.equal(out[:, :, a:b], alone), (a, b)
+        ref = ochord.chord_attention(q[:, :, a:b].double(), k[:, :, a:b].double(), v[:, :, a:b].double(),
+                                     alpha, beta, mu, ssmax, log_n[:, a:b], 0)
+        if dtype == torch.float32:
+            assert (out[:, :, a:b].double().cpu() - ref).abs().max().item() <= 1e-4
+        else:
+            assert_bf16_close(out[:, :, a:b], ref, what=f'{dtype} D={D} rows {a}:{b}')

@@ -168,11 +168,26 @@ def test_config3_bf16_every_layer_matches_oracle():
     with _Tap(model) as tap:
         model(ids.to(DEV), logits=False)
     assert len(tap.records) == 16
+    misses = []
     for rec in tap.records:
         _say(f'config 3 bf16: oracle block {rec["block"]} layer {rec["layer"]} ({rec["kind"]})')
         r64 = _oracle_layer(model, rec, rec['x'], rec['before'], torch.float64)
         r16 = _oracle_layer(model, rec, rec['x'], rec['before'], torch.bfloat16)
-        assert_bf16_layer_close(rec['out'], r64, r16, f'config 3 block {rec["block"]} layer {rec["layer"]}')
+        what = f'config 3 block {rec["block"]} layer {rec["layer"]}'
+        assert_bf16_layer_close(rec['out'], r64, r16, what)
+        _vs_reference_bf16(rec['out'], r16, what, misses)
+    assert not misses, f'layers outside the bf16 bar against the reference bf16 arithmetic: {misses}'
+
+
+def _vs_reference_bf16(out, r16, what, misses):
+    '''The HIP layer against the oracle layer run in bf16 on the same inputs (the
+    reference's own arithmetic): the bf16 bar, max-abs 2e-2 and mean-rel 5e-3.  Layers
+    outside it are collected by name.'''
+    ma, mr = bf16_gap(out, r16)
+    ok = ma <= 2e-2 and mr <= 5e-3
+    _say(f'{what}: vs reference bf16 arithmetic max_abs={ma:.3e} mean_rel={mr:.3e}{"" if ok else "  OUTSIDE"}')
+    if not ok:
+        misses.append((what, round(ma, 5), round(mr, 5)))
 
 
 def _snapshot(cache):
@@ -197,6 +212,21 @@ def _snapshot(cache):
     return restore
 
 
+def _copy_prefill(fixed, dyn, T):
+    '''Set the growing caches `dyn` (after their own T-token prefill) to the contents of
+    the fixed-capacity caches `fixed`: key / value prefixes, recurrent states, conv tails.'''
+    from motif.model.cache import StaticKVLayerCache
+    for src, dst in zip(fixed.layer_caches(), dyn.layer_caches()):
+        assert src.length == dst.length == T
+        if isinstance(src, StaticKVLayerCache):
+            dst._slab[0][:, :, :T].copy_(src._slab[0][:, :, :T])
+            dst._slab[1][:, :, :T].copy_(src._slab[1][:, :, :T])
+        else:
+            dst.state.copy_(src.state)
+            for a, b in zip(dst.conv_state, src.conv_state):
+                a.copy_(b)
+
+
 @torch.no_grad()
 def test_config4_graph_decode_after_real_prefill():
     from motif.model.cache import ModelCache
@@ -206,7 +236,7 @@ def test_config4_graph_decode_after_real_prefill():
     ids = torch.randint(0, cfg.vocab_size, (B, T + N), generator=gen(1)).to(DEV)
     _say('config 4: B=64 T=4096 prefill into fixed-capacity caches')
     cache = ModelCache.for_decode(model, B, T + 8, DEV, torch.bfloat16)
-    model(ids[:, :T], cache=cache, logits=False)
+    h_fixed = model(ids[:, :T], cache=cache, logits=False).hidden_states.clone()
     assert cache.seq_len == T and all(lc.length == T for lc in cache.layer_caches())
     restore = _snapshot(cache)
 
@@ -229,23 +259,34 @@ def test_config4_graph_decode_after_real_prefill():
     e_logits = torch.stack(e_logits)
     assert torch.equal(g_logits, e_logits), (g_logits - e_logits).abs().max().item()
 
-    _say('config 4: growing caches (separate prefill) for comparison')
+    _say('config 4: growing caches on the same prefill contents, for comparison')
+    # The growing caches run their own prefill (their slab layout and bookkeeping), then
+    # take the fixed-capacity caches' prefill contents, so both decode paths start from
+    # the same bits and the comparison measures the cache layouts alone.  Whether the two
+    # prefills (the same computation run twice; its library GEMMs included) agreed bit for
+    # bit is printed; the determinism of this build's own kernels is asserted in
+    # tests/test_gpu_determinism.py.
     dyn = model.create_cache()
-    model(ids[:, :T], cache=dyn, logits=False)
+    h_dyn = model(ids[:, :T], cache=dyn, logits=False).hidden_states
+    _say(f'config 4: the two B=64 T=4096 prefills agree bit for bit: {torch.equal(h_fixed, h_dyn)} '
+         f'{bf16_gap(h_dyn, h_fixed)}')
+    restore()
+    _copy_prefill(cache, dyn, T)
     d_logits = torch.stack([model(ids[:, T + i:T + i + 1], cache=dyn).logits for i in range(N)])
-    # The two cache layouts normally give the same bits (max_abs 0 is printed); one run out
-    # of several on one box differed by max-abs 4.3e-2, mean-relative 1.2e-4 (cause not
-    # found: the GEMMs and the prefill repeat bit for bit), so this model-level check takes
-    # 1e-1; the per-layer oracle checks below hold the op bars.
-    ma, mr = assert_bf16_close(e_logits, d_logits, 1e-1, 5e-3, 'fixed-capacity vs growing caches')
-    _say(f'config 4: fixed-capacity vs growing caches: max_abs={ma:.3e} mean_rel={mr:.3e}')
+    ma, mr = assert_bf16_close(e_logits, d_logits, 2e-2, 5e-3, 'fixed-capacity vs growing caches')
+    _say(f'config 4: fixed-capacity vs growing caches: max_abs={ma:.3e} mean_rel={mr:.3e} '
+         f'(bits equal: {torch.equal(e_logits, d_logits)})')
 
     assert len(tap.records) == 16
+    misses = []
     for rec in tap.records:
         _say(f'config 4: oracle decode rows {rows} block {rec["block"]} layer {rec["layer"]} ({rec["kind"]})')
         r64 = _oracle_layer(model, rec, rec['x'], rec['before'], torch.float64)
         r16 = _oracle_layer(model, rec, rec['x'], rec['before'], torch.bfloat16)
-        assert_bf16_layer_close(rec['out'], r64, r16, f'config 4 decode block {rec["block"]} layer {rec["layer"]}')
+        what = f'config 4 decode block {rec["block"]} layer {rec["layer"]}'
+        assert_bf16_layer_close(rec['out'], r64, r16, what)
+        _vs_reference_bf16(rec['out'], r16, what, misses)
+    assert not misses, f'layers outside the bf16 bar against the reference bf16 arithmetic: {misses}'
 
 
 @pytest.mark.skip(reason='kept off the GPU: this packed 73364-token prefill exceeded the 120 s test limit '
