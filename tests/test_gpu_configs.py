@@ -22,8 +22,9 @@ implementations drift apart over 16 layers.
   batch rows of every layer of the decode step pass the layer check above on the
   cache contents the GPU held before the step.
 - Config 5 (16 sequences, lengths uniform in [512, 8192], seed 0, packed): for every
-  layer, the packed sequence-mixing op (fused GatedDelta prefill, packed Chord
-  attention) on the packed projections equals the op run on each sequence's slice of
+  layer, the packed sequence-mixing op (the GatedDelta conv / gates / chunk rule with
+  the fused output norm, packed Chord attention) on the packed projections equals the
+  op run on each sequence's slice of
   the same projections, bit for bit (outputs, final states, conv tails); each whole
   layer on the packed input matches the layer run on each sequence alone within
   mean-rel 5e-3 (the library GEMM rounds some rows of a large-M call differently from
@@ -309,7 +310,7 @@ def test_config5_packed_prefill():
     # every layer's sequence mixing on the projections of the packed input: the packed op
     # equals the op run on each sequence's slice of the same projections, bit for bit
     from motif.block.attention.chord_attn import LogPositions
-    from motif.ops import apply_chord_attention, apply_chord_attention_varlen, gdn_prefill_fused
+    from motif.ops import apply_chord_attention, apply_chord_attention_varlen
     cu_dev = cu.to(DEV)
     for rec in tap.records:
         attn = model.blocks[rec['block']].features[rec['layer']].attn
@@ -327,13 +328,20 @@ def test_config5_packed_prefill():
                                               softmax_scale=attn.head_dim ** -0.5)
                 assert torch.equal(packed_o[:, :, a:b], alone), f'chord op, sequence {i}'
         else:
-            proj, _ = attn._project(x)
-            args = (attn._proj_offsets(), (attn.q_conv.weight, attn.k_conv.weight, attn.v_conv.weight),
-                    (None, None, None), attn.A_log, attn.dt_bias, attn.dk ** -0.5, attn.o_norm.weight,
-                    attn.o_norm.eps, None, attn.num_heads, attn.dk, attn.dv)
-            y, S, tails = gdn_prefill_fused(proj, *args, cu_seqlens=cu_dev)
+            # the packed path the layer runs (forward_varlen): conv + SiLU + norms, gates and
+            # the chunk rule with the fused GatedRMSNorm, packed vs each sequence alone
+            from motif.ops import chunk_gated_delta_rule_gated_norm
+            proj, (xq, xk, xv, gate, xa, xb) = attn._project(x)
+            q, k, v, tails = attn._qkv((xq, xk, xv), (None, None, None), 1, total, cu_dev, max(lens))
+            beta, g = attn._gates(xa, xb)
+            y, S = chunk_gated_delta_rule_gated_norm(q, k, v, beta, g, gate, attn.o_norm.weight, attn.o_norm.eps,
+                                                     None, attn.chunk_size, cu_seqlens=cu_dev)
             for i, (a, b) in enumerate(bounds):
-                ya, Sa, ta = gdn_prefill_fused(proj[:, a:b], *args)
+                sl = (xq[:, a:b], xk[:, a:b], xv[:, a:b])
+                qa, ka, va, ta = attn._qkv(sl, (None, None, None), 1, b - a)
+                ba, ga = attn._gates(xa[:, a:b], xb[:, a:b])
+                ya, Sa = chunk_gated_delta_rule_gated_norm(qa, ka, va, ba, ga, gate[:, a:b], attn.o_norm.weight,
+                                                           attn.o_norm.eps, None, attn.chunk_size)
                 assert torch.equal(y[:, a:b], ya) and torch.equal(S[i:i + 1], Sa), f'gdn op, sequence {i}'
                 assert all(torch.equal(t[i:i + 1], u) for t, u in zip(tails, ta)), f'gdn tails, sequence {i}'
         _say(f'config 5 block {rec["block"]} layer {rec["layer"]}: packed op == per-sequence op for all 16')
