@@ -8,8 +8,11 @@ The reference differentiates its chunk rule in three pieces
 the per-chunk output combination (autograd through :851-855).  `GDNChunkFunction` runs
 the same pieces: the two sequential scans are the HIP kernels `motif_gdn_scan_fwd_f32`
 (re-scan for the per-chunk states P and residuals X) and `motif_gdn_scan_bwd_f32` (the
-reverse scan), the per-chunk products are batched fp32 GEMMs (the library GEMMs the
-reference also calls) and elementwise terms.
+reverse scan), the per-chunk terms are the HIP kernels `motif_gdn_bwd_prep_f32` (the chunk factors, the
+inverse by blocked substitution and the output's upstream terms) and
+`motif_gdn_bwd_chunk_f32` (every gradient of the preparation, the scan products and the
+output combination) for chunk 64, dk 64 and dv 64 / 128; other shapes take the same
+formulas as batched fp32 torch products (`_backward_torch`).
 
 Per chunk, with gamma the within-chunk cumulative log decay, D[i, j] = e^{gamma_i -
 gamma_j} (j <= i), Kb = beta k, Vb = beta v, A = -(Kb k^T * D) strictly lower,
@@ -66,6 +69,44 @@ def bwd_scan(k, W, g, dX, dP, dS_final):
     return dSn, dS0
 
 
+def chunk_kernels_serve(Dk: int, Dv: int, C: int) -> bool:
+    '''True when the per-chunk backward kernels take this shape (chunk 64, dk 64, dv 64 or
+    128); other shapes run the per-chunk terms as torch products.'''
+    return C == 64 and Dk == 64 and Dv in (64, 128)
+
+
+def bwd_prep(qc, kc, vc, bc, gc, doc):
+    '''Per-chunk terms before the scans on the HIP kernel, from chunked fp32 inputs
+    q, k [B,H,N,C,Dk], v, do [B,H,N,C,Dv], beta, g [B,H,N,C]: (W, U, gamma, T, dP, dX).'''
+    B, H, N, C, Dk = kc.shape
+    Dv = vc.shape[-1]
+    dev = kc.device
+    f = lambda *shape: torch.empty(B, H, N, *shape, dtype=torch.float32, device=dev)
+    W, U, gam, T, dP, dX = f(C, Dk), f(C, Dv), f(C), f(C, C), f(Dk, Dv), f(C, Dv)
+    rc = _lib.lib().motif_gdn_bwd_prep_f32(qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), bc.data_ptr(),
+                                           gc.data_ptr(), doc.data_ptr(), W.data_ptr(), U.data_ptr(),
+                                           gam.data_ptr(), T.data_ptr(), dP.data_ptr(), dX.data_ptr(),
+                                           B * H, N, C, Dk, Dv, _lib.stream_ptr(dev))
+    _lib.check(rc, 'motif_gdn_bwd_prep_f32')
+    return W, U, gam, T, dP, dX
+
+
+def bwd_chunk(qc, kc, vc, bc, gam, T, P, X, dSn, doc, dX):
+    '''Per-chunk gradients after the scans on the HIP kernel: (dq, dk, dv, dbeta, dg),
+    chunked [B,H,N,C,...] fp32.'''
+    B, H, N, C, Dk = kc.shape
+    Dv = vc.shape[-1]
+    dq, dk, dv = torch.empty_like(qc), torch.empty_like(kc), torch.empty_like(vc)
+    dbeta, dg = torch.empty_like(bc), torch.empty_like(bc)
+    rc = _lib.lib().motif_gdn_bwd_chunk_f32(qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), bc.data_ptr(),
+                                            gam.data_ptr(), T.data_ptr(), P.data_ptr(), X.data_ptr(),
+                                            dSn.data_ptr(), doc.data_ptr(), dX.data_ptr(), dq.data_ptr(),
+                                            dk.data_ptr(), dv.data_ptr(), dbeta.data_ptr(), dg.data_ptr(),
+                                            B * H, N, C, Dk, Dv, _lib.stream_ptr(kc.device))
+    _lib.check(rc, 'motif_gdn_bwd_chunk_f32')
+    return dq, dk, dv, dbeta, dg
+
+
 def _chunks(t, C, pad):
     '''[B, H, L, ...] fp32, zero-padded to N * C steps, as [B, H, N, C, ...].'''
     t = t.float()
@@ -114,62 +155,93 @@ class GDNChunkFunction(torch.autograd.Function):
         q, k, v, beta, g, S0 = ctx.saved_tensors
         C = ctx.C
         B, H, L, Dk = q.shape
-        f = _factors(q, k, v, beta, g, C)
-        qc, kc, vc, bc, gc, D, E = f['qc'], f['kc'], f['vc'], f['bc'], f['gc'], f['D'], f['E']
-        W, U, T, Z, kb, vb, G1 = f['W'], f['U'], f['T'], f['Z'], f['kb'], f['vb'], f['G1']
-        N = qc.shape[2]
-
-        # forward states and residuals
-        P, _, X = fused_scan(kc, W, U, gc, S0)
-
-        # output o = (q e^gamma) P + ((q k^T) * D) X
-        doc = _chunks(do if do is not None else torch.zeros(B, H, L, v.shape[-1], device=q.device), C, f['pad'])
-        qg = qc * E[..., None]
-        qk = qc @ kc.transpose(-1, -2)
-        attn = qk * D
-        dP_out = qg.transpose(-1, -2) @ doc
-        dX_out = attn.transpose(-1, -2) @ doc
-        dattn = (doc @ X.transpose(-1, -2)) * D                   # zero above the diagonal
-        dqg = doc @ P.transpose(-1, -2)
-        dq = dqg * E[..., None] + dattn @ kc
-        dk = dattn.transpose(-1, -2) @ qc
-        dgam = (dqg * qg).sum(-1)                                  # d/d gamma through q e^gamma
-        ddec = dattn * qk                                          # d/d D (times D already in dattn)
-
-        # the scan: X = U - W P, S' = e^{gamma_C} P + Kd^T X
-        dSn, dS0 = bwd_scan(kc, W, gc, dX_out, dP_out, dS_fin)
-        gl = gc[..., -1:]
-        dec = (gl - gc).exp()                                      # e^{gamma_C - gamma_c}
-        dxt = dX_out + (kc @ dSn) * dec[..., None]                 # total d/dX
-        dU = dxt
-        dW = -(dxt @ P.transpose(-1, -2))
-        dKd = X @ dSn.transpose(-1, -2)                            # [C, Dk]
-        dk = dk + dKd * dec[..., None]
-        kdk = (dKd * kc * dec[..., None]).sum(-1)                  # per row: dKd . Kd
-        dgam = dgam - kdk
-        last = kdk.sum(-1) + gl.squeeze(-1).exp() * (dSn * P).sum((-1, -2))
-        dgam[..., -1] += last
-
-        # the preparation: W = T Z, U = T Vb, T = (I - A)^{-1}, A = -(Kb k^T * D) strict
-        Tt = T.transpose(-1, -2)
-        dT = dW @ Z.transpose(-1, -2) + dU @ vb.transpose(-1, -2)
-        dZ = Tt @ dW
-        dvb = Tt @ dU
-        dA = (Tt @ dT @ Tt).masked_fill(~f['strict'], 0.0)
-        dG1 = -dA * D
-        ddec = ddec - dA * G1 * D                                  # d/d D, times D
-        dkb = dG1 @ kc + dZ * E[..., None]
-        dk = dk + dG1.transpose(-1, -2) @ kb
-        dgam = dgam + (dZ * Z).sum(-1) + ddec.sum(-1) - ddec.sum(-2)
-        dbeta = (dkb * kc).sum(-1) + (dvb * vc).sum(-1)
-        dk = dk + dkb * bc[..., None]
-        dv = dvb * bc[..., None]
-        dg = dgam.flip(-1).cumsum(-1).flip(-1)                     # gamma = cumsum(g)
-
-        def back(t, like):
-            t = t.reshape(B, H, N * C, *t.shape[4:])[:, :, :L]
-            return t.to(like.dtype)
-        grads = (back(dq, q), back(dk, k), back(dv, v), back(dbeta, beta), back(dg, g),
-                 None if S0 is None else dS0.to(S0.dtype))
+        Dv = v.shape[-1]
+        if do is None:
+            do = torch.zeros(B, H, L, Dv, device=q.device)
+        if chunk_kernels_serve(Dk, Dv, C):
+            grads = _backward_kernels(q, k, v, beta, g, S0, do, dS_fin, C)
+        else:
+            grads = _backward_torch(q, k, v, beta, g, S0, do, dS_fin, C)
         needs = ctx.needs_input_grad
         return tuple(gr if needs[i] else None for i, gr in enumerate(grads)) + (None, None)
+
+
+def _back(t, like, L):
+    '''Chunked [B, H, N, C, ...] back to [B, H, L, ...] in `like`'s dtype.'''
+    B, H, N, C = t.shape[:4]
+    return t.reshape(B, H, N * C, *t.shape[4:])[:, :, :L].to(like.dtype)
+
+
+def _backward_kernels(q, k, v, beta, g, S0, do, dS_fin, C):
+    '''The backward on the HIP kernels: per-chunk terms, forward re-scan, reverse scan,
+    per-chunk gradients (four launches plus the input chunking).'''
+    L = q.shape[2]
+    pad = (C - L % C) % C
+    qc, kc, vc, doc = (_chunks(t, C, pad).contiguous() for t in (q, k, v, do))
+    bc, gc = (_chunks(t, C, pad).contiguous() for t in (beta, g))
+    W, U, gam, T, dP, dX = bwd_prep(qc, kc, vc, bc, gc, doc)
+    P, _, X = fused_scan(kc, W, U, gam, S0)
+    dSn, dS0 = bwd_scan(kc, W, gam, dX, dP, dS_fin)
+    dq, dk, dv, dbeta, dg = bwd_chunk(qc, kc, vc, bc, gam, T, P, X, dSn, doc, dX)
+    return (_back(dq, q, L), _back(dk, k, L), _back(dv, v, L), _back(dbeta, beta, L), _back(dg, g, L),
+            None if S0 is None else dS0.to(S0.dtype))
+
+
+def _backward_torch(q, k, v, beta, g, S0, do, dS_fin, C):
+    '''The same backward with the per-chunk terms as batched fp32 torch products (shapes
+    the per-chunk kernels do not take); the scans still run on the HIP kernels.'''
+    B, H, L, Dk = q.shape
+    f = _factors(q, k, v, beta, g, C)
+    qc, kc, vc, bc, gc, D, E = f['qc'], f['kc'], f['vc'], f['bc'], f['gc'], f['D'], f['E']
+    W, U, T, Z, kb, vb, G1 = f['W'], f['U'], f['T'], f['Z'], f['kb'], f['vb'], f['G1']
+    N = qc.shape[2]
+
+    # forward states and residuals
+    P, _, X = fused_scan(kc, W, U, gc, S0)
+
+    # output o = (q e^gamma) P + ((q k^T) * D) X
+    doc = _chunks(do, C, f['pad'])
+    qg = qc * E[..., None]
+    qk = qc @ kc.transpose(-1, -2)
+    attn = qk * D
+    dP_out = qg.transpose(-1, -2) @ doc
+    dX_out = attn.transpose(-1, -2) @ doc
+    dattn = (doc @ X.transpose(-1, -2)) * D                   # zero above the diagonal
+    dqg = doc @ P.transpose(-1, -2)
+    dq = dqg * E[..., None] + dattn @ kc
+    dk = dattn.transpose(-1, -2) @ qc
+    dgam = (dqg * qg).sum(-1)                                  # d/d gamma through q e^gamma
+    ddec = dattn * qk                                          # d/d D (times D already in dattn)
+
+    # the scan: X = U - W P, S' = e^{gamma_C} P + Kd^T X
+    dSn, dS0 = bwd_scan(kc, W, gc, dX_out, dP_out, dS_fin)
+    gl = gc[..., -1:]
+    dec = (gl - gc).exp()                                      # e^{gamma_C - gamma_c}
+    dxt = dX_out + (kc @ dSn) * dec[..., None]                 # total d/dX
+    dU = dxt
+    dW = -(dxt @ P.transpose(-1, -2))
+    dKd = X @ dSn.transpose(-1, -2)                            # [C, Dk]
+    dk = dk + dKd * dec[..., None]
+    kdk = (dKd * kc * dec[..., None]).sum(-1)                  # per row: dKd . Kd
+    dgam = dgam - kdk
+    last = kdk.sum(-1) + gl.squeeze(-1).exp() * (dSn * P).sum((-1, -2))
+    dgam[..., -1] += last
+
+    # the preparation: W = T Z, U = T Vb, T = (I - A)^{-1}, A = -(Kb k^T * D) strict
+    Tt = T.transpose(-1, -2)
+    dT = dW @ Z.transpose(-1, -2) + dU @ vb.transpose(-1, -2)
+    dZ = Tt @ dW
+    dvb = Tt @ dU
+    dA = (Tt @ dT @ Tt).masked_fill(~f['strict'], 0.0)
+    dG1 = -dA * D
+    ddec = ddec - dA * G1 * D                                  # d/d D, times D
+    dkb = dG1 @ kc + dZ * E[..., None]
+    dk = dk + dG1.transpose(-1, -2) @ kb
+    dgam = dgam + (dZ * Z).sum(-1) + ddec.sum(-1) - ddec.sum(-2)
+    dbeta = (dkb * kc).sum(-1) + (dvb * vc).sum(-1)
+    dk = dk + dkb * bc[..., None]
+    dv = dvb * bc[..., None]
+    dg = dgam.flip(-1).cumsum(-1).flip(-1)                     # gamma = cumsum(g)
+
+    return (_back(dq, q, L), _back(dk, k, L), _back(dv, v, L), _back(dbeta, beta, L), _back(dg, g, L),
+            None if S0 is None else dS0.to(S0.dtype))

@@ -114,6 +114,34 @@ int motif_gdn_scan_fwd_f32(const float *k, const float *W, const float *U, const
 int motif_gdn_scan_bwd_f32(const float *k, const float *W, const float *g, const float *dX, const float *dP,
                            const float *dS_final, float *dSn, float *dS0, int BH, int N, int C, int Dk, int Dv,
                            void *stream);
+/*
+ * Chunk backward, the per-chunk terms before the scans (fp32).  Inputs are chunked and
+ * zero-padded: q, k [BH,N,C,Dk], v, dout [BH,N,C,Dv], beta, g [BH,N,C].  Writes
+ * gam = cumsum(g) per chunk [BH,N,C], T = (I + strict(beta k k^T * D))^{-1} [BH,N,C,C],
+ * W = T (beta e^gam k) [BH,N,C,Dk], U = T (beta v) [BH,N,C,Dv] (the forward re-scan's
+ * inputs) and the output's upstream terms dP = (q e^gam)^T dout [BH,N,Dk,Dv],
+ * dX = ((q k^T) * D)^T dout [BH,N,C,Dv] (the reverse scan's inputs).  Replaces the
+ * reference's chunk preparation forward recomputed for the backward
+ * (motif/ops/gated_deltanet.py:118-177, the solve_triangular at :161-166) and the
+ * autograd of the output combination (:830-832).  C == 64, Dk == 64, Dv in {64, 128};
+ * q, k, v, dout 16-byte aligned.
+ */
+int motif_gdn_bwd_prep_f32(const float *q, const float *k, const float *v, const float *beta, const float *g,
+                           const float *dout, float *W, float *U, float *gam, float *T, float *dP, float *dX,
+                           int BH, int N, int C, int Dk, int Dv, void *stream);
+/*
+ * Chunk backward, the per-chunk gradients after the scans (fp32): from the prep's gam, T
+ * and dX, the forward re-scan's P [BH,N,Dk,Dv] and X [BH,N,C,Dv] and the reverse scan's
+ * dSn [BH,N,Dk,Dv], writes dq, dk [BH,N,C,Dk], dv [BH,N,C,Dv], dbeta, dg [BH,N,C]
+ * (chunked, padded rows included).  Replaces the reference's
+ * _PrepareChunksFunction.backward (motif/ops/gated_deltanet.py:180-260), the per-chunk
+ * products of _FusedScanFunction.backward (:742-765) and the output combination's
+ * gradient.  Same size limits.
+ */
+int motif_gdn_bwd_chunk_f32(const float *q, const float *k, const float *v, const float *beta, const float *gam,
+                            const float *T, const float *P, const float *X, const float *dSn, const float *dout,
+                            const float *dX, float *dq, float *dk, float *dv, float *dbeta, float *dg, int BH, int N,
+                            int C, int Dk, int Dv, void *stream);
 
 /*
  * motif_gdn_chunk_fwd with the layer's output norm fused into the output pass:

@@ -176,3 +176,22 @@ def test_varlen_gradient_branch_validates_cu_seqlens():
             chunk_gated_delta_rule_varlen(q2, torch.cat([ts[1]] * 2), torch.cat([ts[2]] * 2),
                                           torch.cat([ts[3]] * 2), torch.cat([ts[4]] * 2),
                                           torch.tensor([0, 50], dtype=torch.int32, device=DEV))
+
+
+@pytest.mark.parametrize('B,H,L,dv', [(1, 2, 64, 64), (2, 3, 200, 128), (1, 12, 1000, 128)])
+def test_chunk_kernels_equal_torch_products(B, H, L, dv):
+    '''The per-chunk backward kernels (motif_gdn_bwd_prep_f32 / motif_gdn_bwd_chunk_f32)
+    against the same backward with the per-chunk terms as fp32 torch products, on the
+    same inputs: both fp32, so within 1e-4 of the largest entry.'''
+    from motif.ops.gdn_grad import _backward_kernels, _backward_torch, chunk_kernels_serve
+    assert chunk_kernels_serve(64, dv, 64)
+    q, k, v, b, g = (t.to(DEV) for t in gdn_inputs(B, H, L, 64, dv, seed=L + dv))
+    g0 = torch.Generator().manual_seed(L)
+    S0 = (torch.randn(B, H, 64, dv, generator=g0) * 0.1).to(DEV)
+    do = torch.randn(B, H, L, dv, generator=g0).to(DEV)
+    dS = (torch.randn(B, H, 64, dv, generator=g0) * 0.1).to(DEV)
+    got = _backward_kernels(q, k, v, b, g, S0, do, dS, 64)
+    ref = _backward_torch(q, k, v, b, g, S0, do, dS, 64)
+    for name, x, y in zip(('dq', 'dk', 'dv', 'dbeta', 'dg', 'dS0'), got, ref):
+        assert x.shape == y.shape, name
+        _close(x, y, f'{name} (B={B} H={H} L={L} dv={dv})', 1e-4)
