@@ -14,9 +14,11 @@ Also reported in the same JSON line:
   (KV caches and recurrent states filled with random values; labelled), as a
   captured hipGraph replayed K times;
 - per-kernel timings of the hot-path ops at the config-3/4 shapes with HIP
-  events on the launch stream, and the roofline of the dominant kernel;
+  events on the launch stream (forward and backward), and the roofline of the
+  dominant kernel;
 - cpu_baseline: this build's CPU restatement of the reference's PyTorch path
-  (oracle/, float32, torch threads) on one config-3 forward.
+  (oracle/, float32, torch threads) on config-3 forwards (1 warm-up, median of
+  3); the config rows carry the same for configs 1, 2, 4 and a config-5 subset.
 
 Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu]
        python bench.py --kernels-only   # hot-path ops + a copy of known size and the peak
@@ -189,8 +191,26 @@ def kernel_timings(dev):
                                shape='B=64 H=12 Hkv=3 S=4097 D=64 bf16 (split-K + merge); cache-cold '
                                      '(4 rotating K / V sets)')
     del kvs
+
+    # backward passes at the config-3 layer shape (eager launches, HIP events): the GDN chunk
+    # rule in fp32 (per-chunk kernels + the two scans) and the Chord op in bf16
+    from motif.ops.gdn_grad import _backward_kernels
+    qf, kf, vf, bf_, gf = (t.float() for t in (q, k, v, beta, gg))
+    dof = torch.randn(B, H, T, dv, generator=g).to(dev)
+    dSf = (torch.randn(B, H, dk, dv, generator=g) * 0.1).to(dev)
+    ms = cuda_time(lambda: _backward_kernels(qf, kf, vf, bf_, gf, None, dof, dSf, 64), 10, 3)
+    res['gdn_chunk_backward'] = dict(us=ms * 1e3, shape='B=1 H=12 T=4096 dk=64 dv=128 fp32 (the chunk rule\'s '
+                                                      'gradients: per-chunk kernels and the two scans)')
+    with torch.enable_grad():
+        qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (qc, kc, vc))
+        out = ops.apply_chord_attention(qg, kg, vg, al, be, mu, ss, ln, q_start=0)
+        dob = torch.randn(out.shape, generator=g).to(dev, torch.bfloat16)
+        ms = cuda_time(lambda: torch.autograd.grad(out, (qg, kg, vg), dob, retain_graph=True), 10, 3)
+    res['chord_backward'] = dict(us=ms * 1e3, forward_us=res['chord_prefill']['us'],
+                                 shape='B=1 H=12 Hkv=3 T=4096 D=64 bf16 causal (dQ, dK, dV)')
     for r in res.values():
-        r['frac'] = r['achieved'] / r['peak']
+        if 'peak' in r:
+            r['frac'] = r['achieved'] / r['peak']
     return res
 
 
@@ -250,21 +270,27 @@ def measured_peaks(dev):
                       'median of 10 launches each'}
 
 
-def _cpu_time(fn, reps=1):
+def _cpu_time(fn, reps=3):
+    '''Seconds per call of fn on the host threads: one untimed warm-up call, then the median
+    of `reps` timed calls.'''
     import torch
     torch.set_num_threads(os.cpu_count() or 1)
-    t0 = time.perf_counter()
+    times = []
     with torch.no_grad():
+        fn()
         for _ in range(reps):
+            t0 = time.perf_counter()
             fn()
-    return (time.perf_counter() - t0) / reps
+            times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
 
 
 def config_rows(dev, model, with_cpu=True):
     '''The other configurations of the scope table at their own shapes: config 1 (GDN op,
     fp32), config 2 (Chord op, bf16, Hkv 12 and 3) and, for the CPU baseline only,
     config 4 (decode steps of the oracle model on random-filled caches).  GPU figures are
-    op_time averages (graph-replayed launches); CPU figures one run of the oracle.'''
+    op_time averages (graph-replayed launches); CPU figures the oracle's median of 3 runs
+    after a warm-up (config 5: the two shortest sequences, extrapolated per token).'''
     import torch
     import torch.nn.functional as F
 
@@ -288,7 +314,7 @@ def config_rows(dev, model, with_cpu=True):
         'shape': 'B=1 H=4 T=256 dk=dv=64 fp32', 'gpu_us': round(ms * 1e3, 2),
         'gpu_tok_s': round(B * T / (ms * 1e-3), 1), 'flops': fl}
     if with_cpu:
-        dt = _cpu_time(lambda: chunked(q, k, v, beta, gg), reps=3)
+        dt = _cpu_time(lambda: chunked(q, k, v, beta, gg))
         rows['config1_gdn_chunk_fp32']['cpu_oracle_us'] = round(dt * 1e6, 1)
 
     # config 2: B=2 H=12 T=2048 D=64 bf16, Hkv 12 (the configuration) and 3 (the model's)
@@ -333,14 +359,49 @@ def config_rows(dev, model, with_cpu=True):
                                     for c in (om.H * om.dk, om.H * om.dk, om.H * om.dv))
         om.pos = ctx
         ids = torch.randint(0, cfg.vocab_size, (Bd, 1), generator=gd)
-        dt = _cpu_time(lambda: om.forward(ids), reps=2)
+        dt = _cpu_time(lambda: om.forward(ids))
         rows['config4_decode_cpu'] = {
             'shape': 'B=64, context 4096 (random-filled caches), one token per step', 'cpu_oracle_ms_per_step':
-            round(dt * 1e3, 1), 'cpu_tok_s': round(Bd / dt, 1), 'cores': torch.get_num_threads()}
+            round(dt * 1e3, 1), 'cpu_tok_s': round(Bd / dt, 1), 'cores': torch.get_num_threads(),
+            'method': '1 warm-up step, median of 3 steps (the context grows by one per step)'}
     rows['config5_packed_prefill'] = {
         'skipped': 'kept off the GPU this build: a packed 73364-token prefill exceeded its test time limit '
                    'with the fused GatedDelta front end (now switched off for packed input); cause not established'}
+    if with_cpu:
+        rows['config5_packed_prefill']['cpu'] = config5_cpu_subset(model)
     return rows
+
+
+def config5_cpu_subset(model, n=2):
+    '''Config 5 on the CPU: the n shortest of the 16 packed sequences through the oracle
+    model one at a time (each from zero state, as packing makes them), 1 warm-up + median of
+    3, and the whole 73364-token workload extrapolated per token from that sample.'''
+    import torch
+
+    from motif.model.presets import packed_lengths
+    from oracle.model import OracleModel
+    cfg = model.config
+    p = {kk: vv.detach().float().cpu() for kk, vv in model.state_dict().items()}
+    ocfg = dict(model_dim=cfg.model_dim, num_heads=cfg.num_heads, num_kv_heads=cfg.num_kv_heads,
+                head_k_dim=cfg.head_k_dim, block=cfg.block, block_n=cfg.block_n)
+    lens = packed_lengths()
+    pick = sorted(range(len(lens)), key=lambda i: lens[i])[:n]
+    g = torch.Generator().manual_seed(5)
+    seqs = [torch.randint(0, cfg.vocab_size, (1, lens[i]), generator=g) for i in pick]
+    om = OracleModel(p, ocfg, dtype=torch.float32)
+
+    def run():
+        for s in seqs:
+            om.reset()
+            om.forward(s)
+    dt = _cpu_time(run)
+    tokens = sum(lens[i] for i in pick)
+    tok_s = tokens / dt
+    return {'sample': f'sequences {pick} (lengths {[lens[i] for i in pick]}) of the 16, through oracle/ in float32 '
+                      f'one at a time; 1 warm-up, median of 3', 'cpu_tok_s': round(tok_s, 1),
+            'cores': torch.get_num_threads(), 'extrapolated_s_all_16': round(sum(lens) / tok_s, 1),
+            'note': 'extrapolated per token from the shortest sequences: the attention cost per token grows '
+                    'with length, so the full run would take longer'}
 
 
 def copy_calibration(dev, mib=256, reps=5):
@@ -404,7 +465,8 @@ def make_decode_cache(model, B, ctx, capacity, dev, dtype, seed=1):
 
 
 def cpu_baseline(T=4096, seed=0):
-    '''One config-3 forward through the CPU oracle (float32), threads as configured.'''
+    '''Config-3 forwards through the CPU oracle (float32) on the host threads: 1 warm-up,
+    then the median of 3.'''
     import torch
 
     from motif.model.motif import MotifChordModel
@@ -416,10 +478,7 @@ def cpu_baseline(T=4096, seed=0):
                 head_k_dim=cfg.head_k_dim, block=cfg.block, block_n=cfg.block_n)
     om = OracleModel(p, ocfg, dtype=torch.float32)
     ids = torch.randint(0, cfg.vocab_size, (1, T), generator=torch.Generator().manual_seed(seed))
-    t0 = time.perf_counter()
-    with torch.no_grad():
-        om.forward(ids)
-    dt = time.perf_counter() - t0
+    dt = _cpu_time(lambda: (om.reset(), om.forward(ids)))
     cpu_model = ''
     try:
         with open('/proc/cpuinfo') as f:
@@ -430,9 +489,9 @@ def cpu_baseline(T=4096, seed=0):
     except OSError:
         pass
     return dict(value=T / dt, unit='tok/s', cores=torch.get_num_threads(), kind='port',
-                sample=f'one config-3 forward (B=1, T={T}) through oracle/ (CPU restatement of the '
-                       f'reference torch path: chunk loop GDN, eager Chord), float32; {dt:.2f} s; '
-                       f'CPU: {cpu_model}')
+                sample=f'config-3 forward (B=1, T={T}) through oracle/ (CPU restatement of the '
+                       f'reference torch path: chunk loop GDN, eager Chord), float32; 1 warm-up, median '
+                       f'of 3: {dt:.2f} s per forward; CPU: {cpu_model}')
 
 
 def main():
