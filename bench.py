@@ -242,14 +242,14 @@ def measured_peaks(dev):
     ncu = torch.cuda.get_device_properties(dev).multi_processor_count
     src = torch.ones(2 << 30, dtype=torch.uint8, device=dev)
     dst = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-    red = torch.empty(16 * ncu, dtype=torch.int32, device=dev)
+    red = torch.empty(32 * ncu, dtype=torch.int32, device=dev)
 
     def run(rc, what):
         _lib.check(rc, what)
 
     copy_ms = _median_ms(lambda: run(lib.motif_probe_copy(src.data_ptr(), dst.data_ptr(), 1 << 30, 16 * ncu, st),
                                      'motif_probe_copy'))
-    read_ms = _median_ms(lambda: run(lib.motif_probe_read(src.data_ptr(), red.data_ptr(), 2 << 30, 16 * ncu, st),
+    read_ms = _median_ms(lambda: run(lib.motif_probe_read(src.data_ptr(), red.data_ptr(), 2 << 30, 32 * ncu, st),
                                      'motif_probe_read'))
     grid, iters = 8 * ncu, 2048
     out = torch.empty(grid * 256, dtype=torch.float32, device=dev)
@@ -264,7 +264,8 @@ def measured_peaks(dev):
             'mfma_bf16_TFLOPs': round(max(rates.values()), 1),
             'mfma_bf16_16x16x32_TFLOPs': round(rates[16], 1), 'mfma_bf16_32x32x16_TFLOPs': round(rates[32], 1),
             'published': {'hbm_GBs': PEAK_HBM_GBS, 'mfma_bf16_TFLOPs': PEAK_BF16_TFLOPS},
-            'method': '1 GiB copy (bytes read + written), 2 GiB read-only reduction, '
+            'method': '1 GiB copy (bytes read + written; a contiguous block per workgroup), 2 GiB read-only '
+                      'reduction, both with nontemporal 16-byte accesses, 8 in flight per thread; '
                       f'{grid} workgroups x 4 waves x {iters} rounds of 8 independent '
                       'v_mfma_f32_16x16x32_bf16 or 4 independent v_mfma_f32_32x32x16_bf16; '
                       'median of 10 launches each'}

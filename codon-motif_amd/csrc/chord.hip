@@ -826,12 +826,12 @@ __global__ void __launch_bounds__(256) chord_decode_mfma_kernel(ChordArgs a) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const uint32_t off = static_cast<uint32_t>(((n0 + 16 * t + c16) * a.k_st + 16 * g) * 2);
-      st.k[t][0] = buf_ld16(kbuf, off);
-      st.k[t][1] = buf_ld16(kbuf, off + 16);
+      st.k[t][0] = buf_ld16_nt(kbuf, off);
+      st.k[t][1] = buf_ld16_nt(kbuf, off + 16);
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      st.v[r] = buf_ld16(vbuf, static_cast<uint32_t>(((n0 + 8 * r + (lane >> 3)) * a.v_st + 8 * (lane & 7)) * 2));
+      st.v[r] = buf_ld16_nt(vbuf, static_cast<uint32_t>(((n0 + 8 * r + (lane >> 3)) * a.v_st + 8 * (lane & 7)) * 2));
   };
 
   float m = -INFINITY, lsum = 0.f;

@@ -73,6 +73,12 @@ __device__ __forceinline__ buf_t make_buf(const void *base, uint32_t bytes) {
 __device__ __forceinline__ uint4 buf_ld16(buf_t r, uint32_t off) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
+// The same load marked nontemporal (cache-policy operand 2: the `nt` bit on gfx950), for
+// data a kernel streams once (KV caches, recurrent states): it is not kept in the caches
+// at the expense of data that is reused.
+__device__ __forceinline__ uint4 buf_ld16_nt(buf_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
+}
 __device__ __forceinline__ uint2 buf_ld8(buf_t r, uint32_t off) {
   return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
 }

@@ -49,7 +49,8 @@ __global__ void __launch_bounds__(128) gdn_decode_kernel(GdnDecodeArgs a) {
 
   // The state column, the gate and the norm weight do not depend on the conv: issue
   // their loads first so their latency overlaps the conv / normalisation below.  The
-  // state block of (b, h) is one buffer; row i sits at the uniform offset i * dv * 4.
+  // state block of (b, h) is one buffer; row i sits at the uniform offset i * dv * 4.  The
+  // state is streamed once per step: its loads and stores are nontemporal (cache policy 2).
   const buf_t sbuf = make_buf(a.state + (static_cast<size_t>(b) * a.H + h) * DK * a.dv,
                               static_cast<uint32_t>(DK * a.dv * 4));
   const buf_t obuf = make_buf(a.state_out + (static_cast<size_t>(b) * a.H + h) * DK * a.dv,
@@ -59,7 +60,7 @@ __global__ void __launch_bounds__(128) gdn_decode_kernel(GdnDecodeArgs a) {
   if (active) {
 #pragma unroll
     for (int i = 0; i < DK; ++i)
-      S[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sbuf, col, i * row, 0));
+      S[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sbuf, col, i * row, 2));
   }
   const T *pr = static_cast<const T *>(a.proj) + b * a.p_sb;
   float gt = 0.f, nw = 0.f, xv = 0.f;
@@ -132,7 +133,7 @@ __global__ void __launch_bounds__(128) gdn_decode_kernel(GdnDecodeArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < DK; ++i)
-      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, S[i]), obuf, col, i * row, 0);
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, S[i]), obuf, col, i * row, 2);
   }
 
   // 5. GatedRMSNorm over the head's dv outputs (two waves: partial sums in LDS) of o

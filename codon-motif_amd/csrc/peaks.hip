@@ -1,8 +1,10 @@
 // Probes for the measured roofline denominators (no reference counterpart; used by
 // bench.py beside the published MI355X peaks):
-//   motif_probe_copy       dst = src, 16-byte vector loads and stores, grid-stride:
-//                          the HBM rate of a stream that reads and writes every byte once;
-//   motif_probe_read       a reduction of src to one word per workgroup: the read-only rate;
+//   motif_probe_copy       dst = src, nontemporal 16-byte loads and stores, a contiguous
+//                          block per workgroup, eight loads in flight per thread: the HBM
+//                          rate of a stream that reads and writes every byte once;
+//   motif_probe_read       a reduction of src to one word per workgroup (nontemporal
+//                          16-byte loads, eight in flight per thread): the read-only rate;
 //   motif_probe_mfma_bf16  v_mfma_f32_16x16x32_bf16 (eight independent accumulators per
 //                          wave) or v_mfma_f32_32x32x16_bf16 (four) back to back on register
 //                          operands: the dense bf16 MFMA rate.
@@ -16,29 +18,44 @@ namespace {
 
 constexpr int kProbeThreads = 256;
 
+// 16-byte accesses marked nontemporal (the probed data is touched once)
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_nt(const uint4 *p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+  return uint4{v.x, v.y, v.z, v.w};
+}
+__device__ __forceinline__ void st_nt(uint4 v, uint4 *p) {
+  __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4 *>(p));
+}
+
+constexpr int kProbeUnroll = 8;  // 16-byte loads in flight per thread
+
+// Each workgroup copies one contiguous block (a grid-stride interleave over all
+// workgroups keeps many more DRAM pages open at once and measured ~20% slower).
 __global__ void __launch_bounds__(kProbeThreads) probe_copy_kernel(const uint4 *src, uint4 *dst, size_t n) {
-  const size_t stride = static_cast<size_t>(gridDim.x) * kProbeThreads;
-  size_t i = static_cast<size_t>(blockIdx.x) * kProbeThreads + threadIdx.x;
-  // four loads in flight per thread per iteration
-  for (; i + 3 * stride < n; i += 4 * stride) {
-    const uint4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
-    dst[i] = a;
-    dst[i + stride] = b;
-    dst[i + 2 * stride] = c;
-    dst[i + 3 * stride] = d;
+  const size_t per = n / gridDim.x, base = static_cast<size_t>(blockIdx.x) * per;
+  const size_t end = blockIdx.x + 1 == gridDim.x ? n : base + per;
+  size_t i = base + threadIdx.x;
+  for (; i + (kProbeUnroll - 1) * kProbeThreads < end; i += kProbeUnroll * kProbeThreads) {
+    uint4 v[kProbeUnroll];
+#pragma unroll
+    for (int u = 0; u < kProbeUnroll; ++u) v[u] = ld_nt(src + i + u * kProbeThreads);
+#pragma unroll
+    for (int u = 0; u < kProbeUnroll; ++u) st_nt(v[u], dst + i + u * kProbeThreads);
   }
-  for (; i < n; i += stride) dst[i] = src[i];
+  for (; i < end; i += kProbeThreads) dst[i] = src[i];
 }
 
 __global__ void __launch_bounds__(kProbeThreads) probe_read_kernel(const uint4 *src, uint32_t *out, size_t n) {
   const size_t stride = static_cast<size_t>(gridDim.x) * kProbeThreads;
   uint32_t acc = 0;
   size_t i = static_cast<size_t>(blockIdx.x) * kProbeThreads + threadIdx.x;
-  // four loads in flight per thread per iteration
-  for (; i + 3 * stride < n; i += 4 * stride) {
-    const uint4 a = src[i], b = src[i + stride];
-    const uint4 c = src[i + 2 * stride], d = src[i + 3 * stride];
-    acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^ d.z ^ d.w;
+  for (; i + (kProbeUnroll - 1) * stride < n; i += kProbeUnroll * stride) {
+    uint4 v[kProbeUnroll];
+#pragma unroll
+    for (int u = 0; u < kProbeUnroll; ++u) v[u] = ld_nt(src + i + u * stride);
+#pragma unroll
+    for (int u = 0; u < kProbeUnroll; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
   }
   for (; i < n; i += stride) {
     const uint4 a = src[i];
