@@ -618,7 +618,10 @@ def main():
     with torch.no_grad():
         kern = kernel_timings(dev)
     for name, r in kern.items():
-        log(f'[bench]   {name}: {r["us"]:.1f} us, {r["achieved"]:.1f} {r["unit"]} ({100 * r["frac"]:.1f}% of peak)')
+        if 'frac' in r:
+            log(f'[bench]   {name}: {r["us"]:.1f} us, {r["achieved"]:.1f} {r["unit"]} ({100 * r["frac"]:.1f}% of peak)')
+        else:
+            log(f'[bench]   {name}: {r["us"]:.1f} us')
     # the dominant prefill kernel: the one that takes the most time per forward
     per_fwd = {'gdn_chunk_prefill': kern['gdn_chunk_prefill']['us'] * 12,
                'chord_prefill': kern['chord_prefill']['us'] * 4}

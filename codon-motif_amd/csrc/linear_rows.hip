@@ -54,6 +54,13 @@ __device__ __forceinline__ f32x4 mma(const bf16x8 &a, const bf16x8 &b, f32x4 c) 
 __device__ __forceinline__ bf16x8 ld8(buf_t r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
+// A weight piece read by this workgroup alone (whole-row tiles: no other workgroup of the
+// launch reads it): a nontemporal load (cache policy 2), so the stream does not evict
+// the activation rows every workgroup re-reads.
+template <bool STREAM>
+__device__ __forceinline__ bf16x8 ldw(buf_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, STREAM ? 2 : 0));
+}
 
 __device__ __forceinline__ float rb(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
@@ -131,7 +138,7 @@ __device__ __forceinline__ void rows_tile(const LinArgs &a, const int id, f32x4 
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) A[c][j][mt] = ld8(xb, xo[mt] + 16 * j, soff);
 #pragma unroll
-        for (int t = 0; t < NT; ++t) B[c][j][t] = ld8(wb, wo[t] + 16 * j, soff);
+        for (int t = 0; t < NT; ++t) B[c][j][t] = ldw<MT == 4>(wb, wo[t] + 16 * j, soff);
       }
     }
     // keep the whole batch of loads ahead of the MFMAs (the scheduler would otherwise
