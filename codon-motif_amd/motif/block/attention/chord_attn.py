@@ -26,6 +26,7 @@ import torch.nn as nn
 from motif.block.attention.base import AttentionOutput, BasicAttention
 from motif.model.cache import KVLayerCache, StaticKVLayerCache, expand_kv_heads
 from motif.ops import RMSNorm, apply_chord_attention, apply_chord_attention_varlen
+from motif.ops.packed import PackedSeqs
 from motif.ops import _lib
 from motif.ops.autograd_path import wants_grad
 from motif.ops.chord_attention import HEAD_DIMS, chord_decode_cursor, chord_decode_workspace, serves_head_dim
@@ -324,22 +325,21 @@ class ChordAttention(BasicAttention):
         cache.cursor_steps = getattr(cache, 'cursor_steps', 0) + 1
         return self._merge_heads(out), proj[..., self.hidden_size + 2 * self.kv_dim:]
 
-    def forward_varlen(self, hidden_states: torch.Tensor, cu_seqlens: torch.Tensor) -> AttentionOutput:
+    def forward_varlen(self, hidden_states: torch.Tensor, cu_seqlens) -> AttentionOutput:
         '''Packed sequences (B == 1; new): each sequence attends causally within itself
-        with positions (and log_n) restarting at 0.  The payload holds the packed keys
-        and values.'''
+        with positions (and log_n) restarting at 0.  `cu_seqlens` is an int tensor or a
+        motif.ops.packed.PackedSeqs (then nothing is read back from the device).  The
+        payload holds the packed keys and values.'''
         B, T, _ = hidden_states.shape
         if B != 1:
             raise ValueError('forward_varlen expects packed sequences with B == 1')
+        ps = PackedSeqs.of(cu_seqlens, T, hidden_states.device)
         fused = self._prep_fusable(hidden_states, None)
         q, k, v, g = self._inputs(hidden_states, None, None, fused)
-        cu = cu_seqlens.detach().to('cpu', torch.int64)
-        lens = cu[1:] - cu[:-1]
-        pos = torch.arange(T) - torch.repeat_interleave(cu[:-1], lens)
-        table = LogPositions.get(int(lens.max()) if lens.numel() else 1, hidden_states.device)
-        log_n = table[pos.to(hidden_states.device)][None]
+        table = LogPositions.get(max(ps.max_len, 1), hidden_states.device)
+        log_n = table[ps.positions()][None]
         alpha, beta, mu, ssmax = self.ggd_params()
-        out = apply_chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, log_n, cu_seqlens,
+        out = apply_chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, log_n, ps,
                                            softmax_scale=self.head_dim ** -0.5, eps=GGD_EPS)
         return AttentionOutput(output=self._gated_output(self._merge_heads(out), g), payload={'k': k, 'v': v})
 

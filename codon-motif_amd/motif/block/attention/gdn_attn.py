@@ -33,6 +33,7 @@ from motif.block.attention.base import AttentionOutput, BasicAttention
 from motif.model.cache import GatedDeltaAttentionLayerCache
 from motif.ops.autograd_path import wants_grad
 from motif.ops.epilogue import gated_rms_norm_heads, gdn_gates, usable
+from motif.ops.packed import PackedSeqs
 from motif.ops import (
     GatedRMSNorm,
     cat_weights,
@@ -308,15 +309,16 @@ class GatedDeltaAttention(BasicAttention):
         payload = {'state': S.detach(), 'conv_state': tuple(c.detach() for c in (cq, ck, cv))}
         return AttentionOutput(output=output, payload=payload)
 
-    def forward_varlen(self, hidden_states: torch.Tensor, cu_seqlens: torch.Tensor) -> AttentionOutput:
+    def forward_varlen(self, hidden_states: torch.Tensor, cu_seqlens) -> AttentionOutput:
         '''Packed sequences (B == 1): every sequence starts from zero state and zero
-        conv tails.  Returns the output and a payload with the per-sequence final
-        states [nseq, H, dk, dv] and conv tails [nseq, D, K-1].'''
+        conv tails.  `cu_seqlens` is an int tensor or a motif.ops.packed.PackedSeqs (then
+        nothing is read back from the device).  Returns the output and a payload with
+        the per-sequence final states [nseq, H, dk, dv] and conv tails [nseq, D, K-1].'''
         B, L, _ = hidden_states.shape
         if B != 1:
             raise ValueError('forward_varlen expects packed sequences with B == 1')
-        lens = cu_seqlens.detach().cpu()
-        max_len = int((lens[1:] - lens[:-1]).max()) if lens.numel() > 1 else 0
+        cu_seqlens = PackedSeqs.of(cu_seqlens, L, hidden_states.device)
+        max_len = cu_seqlens.max_len
         proj, (xq, xk, xv, gate, xa, xb) = self._project(hidden_states)
         whole = self._prefill_fused(proj, (None, None, None), None, cu_seqlens)
         if whole is not None:

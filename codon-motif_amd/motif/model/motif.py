@@ -19,6 +19,7 @@ from motif.block.decoder import DecoderBlock
 from motif.model.cache import ModelCache, build_cache
 from motif.model.config import MotifChordConfig
 from motif.ops import RMSNorm
+from motif.ops.packed import PackedSeqs
 
 
 @dataclass
@@ -117,8 +118,13 @@ class MotifChordModel(nn.Module):
         '''Run the model over [B, T] ids.
 
         `cu_seqlens` (new): packed sequences, B == 1 -- every sequence starts from
-        empty state.  `logits=False` skips the vocabulary projection.'''
+        empty state; an int tensor (its host-side metadata is then built once, one read
+        back from the device) or a motif.ops.packed.PackedSeqs built beforehand (the
+        forward then reads nothing back and can be captured in a graph).  `logits=False`
+        skips the vocabulary projection.'''
         cached = cache.seq_len if cache is not None else 0
+        if cu_seqlens is not None:
+            cu_seqlens = PackedSeqs.of(cu_seqlens, input_ids.shape[1], input_ids.device)
         if mask is not None:
             width = cached + input_ids.shape[1]
             if mask.dim() != 2:

@@ -21,6 +21,7 @@ from typing import Optional
 import torch
 
 from . import _lib
+from .packed import PackedSeqs
 from .autograd_path import chord_attention_torch, chord_attention_varlen_torch, wants_grad
 
 HEAD_DIM = 64                  # the model's head dim: bf16 runs on the MFMA kernels
@@ -254,38 +255,35 @@ def apply_chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, log_n, cu_seql
     sequence i covering rows [cu_seqlens[i], cu_seqlens[i+1]).  Each sequence is
     causal on its own with positions restarting at 0; log_n [1, T] is read at
     the packed row (log(1 .. len_i) per sequence reproduces separate runs).
+    `cu_seqlens` is an int tensor or a motif.ops.packed.PackedSeqs (whose host-side
+    metadata then spares the call every read back from the device).
     Calls that need gradients run the sequences separately: through the HIP forward /
     backward pair (`ChordFunction`) where it serves, else as differentiable torch runs.
     '''
     if wants_grad(q, k, v, alpha, beta, mu, ssmax, log_n):
         if (q.shape[0] == 1 and q.shape[2] > 0 and k.shape[2] == q.shape[2]
                 and _grad_kernels_serve(q, k, v, alpha, beta, mu, ssmax, log_n, 0)):
-            cu = [int(x) for x in cu_seqlens.detach().to('cpu')]
-            if cu[0] != 0 or cu[-1] != q.shape[2] or any(b < a for a, b in zip(cu[:-1], cu[1:])):
-                raise ValueError('cu_seqlens must start at 0, be non-decreasing and end at T')
+            cu = PackedSeqs.of(cu_seqlens, q.shape[2], q.device).cu_host.tolist()
             outs = [apply_chord_attention(q[:, :, a:b], k[:, :, a:b], v[:, :, a:b], alpha, beta, mu, ssmax,
                                           log_n[:, a:b], q_start=0, softmax_scale=softmax_scale, eps=eps)
                     for a, b in zip(cu[:-1], cu[1:]) if b > a]
             return torch.cat(outs, dim=2)
-        return chord_attention_varlen_torch(q, k, v, alpha, beta, mu, ssmax, log_n, cu_seqlens, softmax_scale, eps)
+        cu_t = cu_seqlens.cu_host if isinstance(cu_seqlens, PackedSeqs) else cu_seqlens
+        return chord_attention_varlen_torch(q, k, v, alpha, beta, mu, ssmax, log_n, cu_t, softmax_scale, eps)
     if not _lib.available():
         raise RuntimeError('there is no usable HIP backend in the current environment')
     B, H, L, D, Hkv, S = _check_tensors(q, k, v, log_n)
     _check_params(alpha, beta, mu, ssmax, H)
     if B != 1 or S != L:
         raise ValueError('apply_chord_attention_varlen: needs B == 1 and packed q / k of equal length')
-    cu_host = cu_seqlens.detach().to('cpu', torch.int64)
-    lens = cu_host[1:] - cu_host[:-1]
-    if int(cu_host[0]) != 0 or int(cu_host[-1]) != L or (lens < 0).any():
-        raise ValueError('cu_seqlens must start at 0, be non-decreasing and end at T')
+    ps = PackedSeqs.of(cu_seqlens, L, q.device)
     if softmax_scale is None:
         softmax_scale = D ** -0.5
     out = torch.empty((B, H, L, D), dtype=q.dtype, device=q.device)
     if L == 0:
         return out
-    cu_dev = cu_host.to(device=q.device, dtype=torch.int32)
     return _launch(q, k, v, alpha, beta, mu, ssmax, log_n, 0, softmax_scale, eps, out,
-                   cu_dev=cu_dev, nseq=int(lens.numel()), max_seqlen=int(lens.max()), cu_host=cu_host)
+                   cu_dev=ps.cu, nseq=ps.nseq, max_seqlen=ps.max_len, cu_host=ps.cu_host)
 
 
 def chord_decode_workspace(B, H, Hkv, L, capacity, D, dtype, device) -> torch.Tensor:

@@ -22,6 +22,7 @@ import functools
 import torch
 
 from . import _lib
+from .packed import PackedSeqs
 from .autograd_path import gdn_chunk_torch, wants_grad as _needs_grad
 from .gdn_grad import GDNChunkFunction, scans_serve
 
@@ -140,16 +141,10 @@ def _chunk_call(qc, kc, vc, bc, gc, S_in, C, cu=None, nseq=None, norm=None):
         total = B * ((L + C - 1) // C)
         cu_dev = coff_dev = None
     else:
-        cu_host = cu.detach().to('cpu', torch.int64)
-        lens = cu_host[1:] - cu_host[:-1]
-        if (lens < 0).any() or int(cu_host[0]) != 0 or int(cu_host[-1]) != L:
-            raise ValueError('cu_seqlens must start at 0, be non-decreasing and end at L')
-        nch = (lens + C - 1) // C
-        coff = torch.zeros(nseq + 1, dtype=torch.int32)
-        coff[1:] = torch.cumsum(nch, 0).to(torch.int32)
-        total = int(coff[-1])
-        cu_dev = cu_host.to(device=dev, dtype=torch.int32)
-        coff_dev = coff.to(dev)
+        ps = PackedSeqs.of(cu, L, dev)
+        nseq = ps.nseq
+        coff_dev, total = ps.chunk_offsets(C)
+        cu_dev = ps.cu
     S_out = torch.empty(nseq, H, Dk, Dv, dtype=torch.float32, device=dev)
     nbytes = _lib.lib().motif_gdn_chunk_workspace_bytes(H, Dk, Dv, C, max(total, 1))
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
@@ -221,8 +216,9 @@ def chunk_gated_delta_rule_gated_norm(q, k, v, beta, g, gate, norm_weight, norm_
 
     Returns (y [B, L, H*Dv], S) where y = GatedRMSNorm(o; gate, norm_weight, norm_eps)
     per head, or None when the fused kernel does not serve these inputs (bf16 MFMA
-    path only); the caller then runs the two steps separately.  `cu_seqlens` selects
-    the packed-sequence form (S then [nseq, H, Dk, Dv]).
+    path only); the caller then runs the two steps separately.  `cu_seqlens` (a tensor
+    or a motif.ops.packed.PackedSeqs) selects the packed-sequence form (S then
+    [nseq, H, Dk, Dv]).
     '''
     name = 'chunk_gated_delta_rule_gated_norm'
     if q.dtype != torch.bfloat16 or gate.dtype != torch.bfloat16 or not q.is_cuda:
@@ -238,11 +234,11 @@ def chunk_gated_delta_rule_gated_norm(q, k, v, beta, g, gate, norm_weight, norm_
     if cu_seqlens is None:
         S_in = _state_in(S, B, H, Dk, Dv, qc.device, name)
         return _chunk_call(qc, kc, vc, bc, gc, S_in, _kernel_chunk(int(chunk_size)), norm=(gate, w, norm_eps))
-    nseq = int(cu_seqlens.numel()) - 1
+    nseq = cu_seqlens.nseq if isinstance(cu_seqlens, PackedSeqs) else int(cu_seqlens.numel()) - 1
     if B != 1 or nseq < 1 or S is not None:
         return None
-    return _chunk_call(qc, kc, vc, bc, gc, None, _kernel_chunk(int(chunk_size)), cu_seqlens, nseq,
-                       norm=(gate, w, norm_eps))
+    ps = PackedSeqs.of(cu_seqlens, L, qc.device)
+    return _chunk_call(qc, kc, vc, bc, gc, None, _kernel_chunk(int(chunk_size)), ps, nseq, norm=(gate, w, norm_eps))
 
 
 def chunk_gated_delta_rule_triton(q, k, v, beta, g, S=None, chunk_size=64):
@@ -265,6 +261,8 @@ def chunk_gated_delta_rule_varlen(q, k, v, beta, g, cu_seqlens, S=None, chunk_si
 
     B must be 1; sequence i covers tokens [cu_seqlens[i], cu_seqlens[i+1]) and
     runs independently from its own initial state S[i] (zeros when S is None).
+    `cu_seqlens` is an int tensor or a motif.ops.packed.PackedSeqs (whose host-side
+    metadata then spares the call every read back from the device).
 
     Returns:
         (o [1, H, L, Dv] in q's dtype, S [nseq, H, Dk, Dv] fp32)
@@ -277,15 +275,15 @@ def chunk_gated_delta_rule_varlen(q, k, v, beta, g, cu_seqlens, S=None, chunk_si
     Dv = v.shape[-1]
     if B != 1:
         raise ValueError(f'{name}: packed sequences need B == 1, got B={B}')
-    nseq = int(cu_seqlens.numel()) - 1
+    ps = cu_seqlens if isinstance(cu_seqlens, PackedSeqs) else None
+    nseq = ps.nseq if ps is not None else int(cu_seqlens.numel()) - 1
     if nseq < 1:
         raise ValueError(f'{name}: cu_seqlens needs at least two entries')
     if S is not None and S.shape != (nseq, H, Dk, Dv):
         raise ValueError(f'{name}: S must be [nseq, H, Dk, Dv] = {(nseq, H, Dk, Dv)}')
+    ps = PackedSeqs.of(cu_seqlens, L, q.device)
     if _needs_grad(q, k, v, beta, g, S):
-        cu = [int(c) for c in cu_seqlens.detach().cpu()]
-        if cu[0] != 0 or cu[-1] != L or any(b < a for a, b in zip(cu, cu[1:])):
-            raise ValueError('cu_seqlens must start at 0, be non-decreasing and end at L')
+        cu = ps.cu_host.tolist()
         outs, states = [], []
         for i in range(len(cu) - 1):
             # each sequence through the chunk op's own gradient route (HIP scans where they
@@ -304,7 +302,7 @@ def chunk_gated_delta_rule_varlen(q, k, v, beta, g, cu_seqlens, S=None, chunk_si
         return torch.cat(outs, 2), torch.cat(states, 0)
     (qc, kc, vc, bc, gc), _ = _prepare(q, k, v, beta, g, name)
     S_in = None if S is None else S.to(device=qc.device, dtype=torch.float32).contiguous()
-    o, S_out = _chunk_call(qc, kc, vc, bc, gc, S_in, _kernel_chunk(int(chunk_size)), cu_seqlens, nseq)
+    o, S_out = _chunk_call(qc, kc, vc, bc, gc, S_in, _kernel_chunk(int(chunk_size)), ps, nseq)
     return o.to(q.dtype), S_out
 
 
@@ -352,15 +350,10 @@ def gdn_prefill_fused(proj, offsets, conv_weights, tails, a_log, dt_bias, q_scal
     else:
         if B != 1 or S is not None:
             return None
-        cu_host = cu_seqlens.detach().to('cpu', torch.int64)
-        lens = cu_host[1:] - cu_host[:-1]
-        if (lens < 0).any() or int(cu_host[0]) != 0 or int(cu_host[-1]) != L:
-            raise ValueError('cu_seqlens must start at 0, be non-decreasing and end at L')
-        nseq = int(lens.numel())
-        coff = torch.zeros(nseq + 1, dtype=torch.int32)
-        coff[1:] = torch.cumsum((lens + 63) // 64, 0).to(torch.int32)
-        total = int(coff[-1])
-        cu_dev, coff_dev = cu_host.to(device=dev, dtype=torch.int32), coff.to(dev)
+        ps = PackedSeqs.of(cu_seqlens, L, dev)
+        nseq = ps.nseq
+        coff_dev, total = ps.chunk_offsets(64)
+        cu_dev = ps.cu
     if L == 0 or nseq == 0:
         return None
     y = torch.empty(B, L, H * dv, dtype=torch.bfloat16, device=dev)

@@ -11,6 +11,7 @@ import ctypes
 import torch
 
 from . import _lib
+from .packed import PackedSeqs
 from .autograd_path import short_conv_silu_torch, wants_grad
 
 
@@ -82,7 +83,7 @@ def short_conv_silu_varlen(x, weight, cu_seqlens, max_seqlen=None, head_dim=None
     '''
     if wants_grad(x, weight):
         # per sequence in the differentiable torch form (training)
-        cu = [int(c) for c in cu_seqlens.detach().cpu()]
+        cu = PackedSeqs.of(cu_seqlens, x.shape[1]).cu_host.tolist()
         parts = [short_conv_silu_torch(x[:, cu[i]:cu[i + 1]], weight, None, head_dim, scale)
                  for i in range(len(cu) - 1)]
         return torch.cat([p[0] for p in parts], 1), torch.cat([p[1] for p in parts], 0)
@@ -95,12 +96,11 @@ def short_conv_silu_varlen(x, weight, cu_seqlens, max_seqlen=None, head_dim=None
     if x.stride(-1) != 1:
         x = x.contiguous()
     w = weight.detach().reshape(D, K).to(x.dtype).contiguous()
-    cu_host = cu_seqlens.detach().to('cpu', torch.int64)
-    nseq = int(cu_host.numel()) - 1
-    lens = cu_host[1:] - cu_host[:-1]
+    ps = PackedSeqs.of(cu_seqlens, L, x.device)
+    nseq = ps.nseq
     if max_seqlen is None:
-        max_seqlen = int(lens.max()) if nseq > 0 else 0
-    cu_dev = cu_host.to(device=x.device, dtype=torch.int32)
+        max_seqlen = ps.max_len
+    cu_dev = ps.cu
     y = torch.empty(B, L, D, dtype=x.dtype, device=x.device)
     tails = torch.empty(nseq, D, K - 1, dtype=x.dtype, device=x.device)
     _conv_call(x, w, None, tails, y, cu_dev, nseq, int(max_seqlen), head_dim, scale)
@@ -140,14 +140,14 @@ def short_conv_silu_multi(xs, weights, caches, head_dims, scales, cu_seqlens=Non
     else:
         if B != 1:
             return None
-        cu_host = cu_seqlens.detach().to('cpu', torch.int64)
-        nseq = int(cu_host.numel()) - 1
+        ps = PackedSeqs.of(cu_seqlens, L, dev)
+        nseq = ps.nseq
         if nseq < 1:
             return None
-        max_len = int(max_seqlen) if max_seqlen is not None else int((cu_host[1:] - cu_host[:-1]).max())
+        max_len = int(max_seqlen) if max_seqlen is not None else ps.max_len
         if max_len < 1:
             return None
-        cu_dev = cu_host.to(device=dev, dtype=torch.int32)
+        cu_dev = ps.cu
         cs = [None] * n
     ys = [torch.empty(B, L, x.shape[-1], dtype=dt, device=dev) for x in xs]
     tails = [torch.empty(nseq, x.shape[-1], K - 1, dtype=dt, device=dev) for x in xs]

@@ -243,6 +243,37 @@ def test_tiny_model_varlen_equals_independent_runs():
 
 
 @torch.no_grad()
+def test_tiny_model_packed_forward_captures_in_a_graph():
+    """With the packed-sequence metadata built beforehand (motif.ops.packed.PackedSeqs), a
+    packed forward reads nothing back from the device, so it can be captured as a
+    hipGraph: every replay, with eager work and synchronizations between the replays,
+    equals the eager packed forward bit for bit (and the eager forward with the plain
+    cu_seqlens tensor)."""
+    from motif.ops.packed import PackedSeqs
+    cfg, t, model = _tiny_model(torch.bfloat16)
+    ids = t['ids'][0, :80].to(DEV)[None]
+    cu = torch.tensor([0, 30, 31, 80], dtype=torch.int32)
+    ps = PackedSeqs(cu, total=80, device=DEV)
+    eager = model(ids, cu_seqlens=ps).logits.clone()
+    assert torch.equal(eager, model(ids, cu_seqlens=cu.to(DEV)).logits)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        model(ids, cu_seqlens=ps)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = model(ids, cu_seqlens=ps).logits
+    for i in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f'replay {i}'
+        model(ids[:, :40])
+        torch.cuda.synchronize()
+
+
+@torch.no_grad()
 def test_elementwise_stage_kernels_match_torch():
     """GatedRMSNorm of the GDN output (from o and the gate, no concatenation), SwiGLU and
     the residual add-fold, against the torch formulas they replace (same roundings:
