@@ -31,7 +31,7 @@ FLAGS = [
 # Per-source extras.  chord.hip: MFMA accumulators in ordinary VGPRs, so the softmax
 # and rescale code reads them without accumulator-register copies (the GDN kernels
 # keep the default: their register budgets rely on the accumulator file).
-EXTRA = {'chord.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form']}
+EXTRA = {'chord.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form'], 'gdn_chunk.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form']}
 
 
 def _run(cmd, verbose):
