@@ -100,15 +100,22 @@ template <> __device__ __forceinline__ float round_as<f16_t>(float x) { return s
 // conv's output is rounded to T, SiLU of that value is rounded to T; F.normalize takes
 // the vector norm (fp32 sum of squares) rounded to T and clamped at eps, the quotient
 // rounded to T, and q's product with dk^-1/2 rounded to T (a product with 1 for k is
-// exact).
+// exact).  The quotient is formed as y * (1 / denom), the reciprocal taken once per
+// vector and refined by one Newton step: within about one fp32 ulp of the quotient, so its
+// rounding to bf16 is the reference's except when the quotient falls within that ulp of a
+// bf16 rounding boundary (a few elements in 10^5, one bf16 ulp each); an IEEE division
+// per element costs about ten instructions.
 template <typename T> __device__ __forceinline__ float gdn_conv_act(float acc) {
   return round_as<T>(silu_fast(round_as<T>(acc)));
 }
-template <typename T> __device__ __forceinline__ float gdn_norm_denom(float sum_sq) {
-  return fmaxf(round_as<T>(sqrtf(sum_sq)), round_as<T>(1e-12f));
+// 1 / max(T(||y||), T(eps)) from the sum of squares
+template <typename T> __device__ __forceinline__ float gdn_norm_inv(float sum_sq) {
+  const float d = fmaxf(round_as<T>(sqrtf(sum_sq)), round_as<T>(1e-12f));
+  const float r = __builtin_amdgcn_rcpf(d);
+  return fmaf(r, fmaf(-d, r, 1.f), r);
 }
-template <typename T> __device__ __forceinline__ float gdn_normalized(float y, float denom, float scale) {
-  return round_as<T>(round_as<T>(y / denom) * scale);
+template <typename T> __device__ __forceinline__ float gdn_normalized(float y, float inv, float scale) {
+  return round_as<T>(round_as<T>(y * inv) * scale);
 }
 
 __device__ __forceinline__ float wave_sum(float v) {

@@ -122,7 +122,7 @@ __global__ void __launch_bounds__(256) short_conv_silu_kernel(ConvArgs a) {
         float ss = v * v;
 #pragma unroll
         for (int off = 1; off < HD; off <<= 1) ss += __shfl_xor(ss, off, 64);
-        v = gdn_normalized<T>(v, gdn_norm_denom<T>(ss), a.scale);
+        v = gdn_normalized<T>(v, gdn_norm_inv<T>(ss), a.scale);
       }
       if (active && t0 + i < t_hi) st(y + int64_t(t0 + i) * a.y_st, v);
 #pragma unroll
@@ -266,9 +266,9 @@ __global__ void __launch_bounds__(256) short_conv_silu_vec_kernel(ConvGroup grp)
     if (norm) {
 #pragma unroll
       for (int off = 1; off < G; off <<= 1) ss += __shfl_xor(ss, off, 64);
-      const float den = gdn_norm_denom<T>(ss);
+      const float inv = gdn_norm_inv<T>(ss);
 #pragma unroll
-      for (int e = 0; e < E; ++e) v[e] = gdn_normalized<T>(v[e], den, a.scale);
+      for (int e = 0; e < E; ++e) v[e] = gdn_normalized<T>(v[e], inv, a.scale);
     }
     if (t_lo + i < t_hi) *reinterpret_cast<uint4 *>(y + int64_t(t_lo + i) * a.y_st) = Vec16<T>::pack(v);
   }

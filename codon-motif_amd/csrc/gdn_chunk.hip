@@ -393,9 +393,9 @@ __global__ void __launch_bounds__(256, 3) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
 #pragma unroll
           for (int off = 1; off < 8; off <<= 1)
             if (off < S) ss += __shfl_xor(ss, off, 64);
-          const float den = gdn_norm_denom<bf16_t>(ss);
+          const float inv = gdn_norm_inv<bf16_t>(ss);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) v[e] = gdn_normalized<bf16_t>(v[e], den, scale);
+          for (int e = 0; e < 8; ++e) v[e] = gdn_normalized<bf16_t>(v[e], inv, scale);
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) cv[i][e] = pk_bf16(v[2 * e], v[2 * e + 1]);

@@ -102,9 +102,9 @@ __global__ void __launch_bounds__(128) gdn_decode_kernel(GdnDecodeArgs a) {
     for (int off = 1; off < DK; off <<= 1) ss += __shfl_xor(ss, off, 64);
     // dk^-1/2 as the host's float(dk ** -0.5)
     constexpr float qs = DK == 16 ? 0.25f : DK == 32 ? 0.17677669529663687f : DK == 64 ? 0.125f : 0.08838834764831845f;
-    const float den = gdn_norm_denom<T>(ss);
-    if (isq) sq[c] = gdn_normalized<T>(y, den, qs);
-    else sk[c] = gdn_normalized<T>(y, den, 1.f);
+    const float inv = gdn_norm_inv<T>(ss);
+    if (isq) sq[c] = gdn_normalized<T>(y, inv, qs);
+    else sk[c] = gdn_normalized<T>(y, inv, 1.f);
   }
   float vcol = 0.f;
   if (active) vcol = conv(a.wv, a.tv, a.ov, a.H * a.dv, h * a.dv + tid, xv);
