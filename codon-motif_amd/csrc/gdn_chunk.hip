@@ -180,8 +180,9 @@ struct PrepLayout {
   static constexpr int kh = 0, vt = 0, qh = 2 * kPlane, kt = 3 * kPlane;
   static_assert(DV * 128 <= 2 * kPlane && DK * 128 <= kPlane, "V^T / K^T planes exceed their pieces");
   static constexpr int nt = 4 * kPlane, tt_h = nt, tt_l = nt + kPlane;
-  static constexpr int small = nt + (64 * 68 * 4 > 2 * kPlane ? 64 * 68 * 4 : 2 * kPlane);  // gam[64], beta[64]
-  static constexpr int bytes = small + 2 * 64 * 4;
+  // gam[64], beta[64], ek[64] = e^{gamma_C - gamma}, sb[64] = beta e^gamma
+  static constexpr int small = nt + (64 * 68 * 4 > 2 * kPlane ? 64 * 68 * 4 : 2 * kPlane);
+  static constexpr int bytes = small + 4 * 64 * 4;
 };
 
 // v_mfma_f32_32x32x16_bf16: A lane l holds row l % 32, k 8 (l / 32) + 0..7; B lane l
@@ -208,12 +209,19 @@ __global__ void __launch_bounds__(256, 3) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
   __bf16 *kt = reinterpret_cast<__bf16 *>(smem + PL::kt), *vt = reinterpret_cast<__bf16 *>(smem + PL::vt);
   __bf16 *kh = reinterpret_cast<__bf16 *>(smem + PL::kh), *qh = reinterpret_cast<__bf16 *>(smem + PL::qh);
   float *nt = reinterpret_cast<float *>(smem + PL::nt);
-  float *gam = reinterpret_cast<float *>(smem + PL::small), *bet = gam + 64;
+  float *gam = reinterpret_cast<float *>(smem + PL::small), *bet = gam + 64, *ek = gam + 128, *sb = gam + 192;
 
   const int chunk = blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ln = lane & 15, g = lane >> 4;
   const ChunkInfo ci = resolve_chunk(chunk, kC, a.L, ca);
+  // wavefront 0, lane = chunk row: the gates and the per-row decay factors phase 7 scales by
+  auto put_gates = [&](float gsum, float b) {
+    gam[lane] = gsum;
+    bet[lane] = b;
+    ek[lane] = exp_fast(__shfl(gsum, 63, 64) - gsum);
+    sb[lane] = b * exp_fast(gsum);
+  };
 
   // variables phase 1 leaves for the later phases (the FRONT form uses its own)
   constexpr int KSEG = DK / 8, VP = 32 * (DV / 8) / 256;
@@ -259,8 +267,7 @@ __global__ void __launch_bounds__(256, 3) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
         const float y = __shfl_up(s, off, 64);
         if (lane >= off) s += y;
       }
-      gam[lane] = s;
-      bet[lane] = bv;
+      put_gates(s, bv);
     }
     if (kval) {
       *reinterpret_cast<uint4 *>(kh + swz(2 * kp, 8 * kseg)) = k0r;
@@ -348,8 +355,7 @@ __global__ void __launch_bounds__(256, 3) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
         const float y = __shfl_up(sacc, off, 64);
         if (lane >= off) sacc += y;
       }
-      gam[lane] = sacc;
-      bet[lane] = bv;
+      put_gates(sacc, bv);
     }
     auto unpack8 = [](const uint4 &u, float *x) {
       const uint32_t ww[4] = {u.x, u.y, u.z, u.w};
@@ -642,8 +648,9 @@ __global__ void __launch_bounds__(256, 3) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
   // as bf16 in 8-byte pieces of the consuming kernel's operand order.
   const WsLayout Lw(DK, a.dv);
   char *cell = ws + (static_cast<size_t>(h) * ca.total_chunks + chunk) * Lw.cell;
-  const bool top = w < DK / 32, bottom = w >= 2;
-  if (top || bottom) {
+  // (one specialised body per tile kind: no wave-uniform branches inside its loops)
+  auto phase7 = [&](auto top_c) {
+    constexpr bool top = decltype(top_c)::value;
     const int tile = top ? w : w - 2;
     const int m = 32 * tile + lc;  // d' (top) or i' (bottom): this lane's column of M^T
     bf16x8 bh[4], bl[4];
@@ -653,7 +660,7 @@ __global__ void __launch_bounds__(256, 3) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
         const bf16x8 kv = rd_pair_s(kt, m, 16 * ks + 4 * hh);
         float x[8];
 #pragma unroll
-        for (int t = 0; t < 8; ++t) x[t] = fl(kv[t]) * exp_fast(glast - gam[16 * ks + 8 * (t >> 2) + 4 * hh + (t & 3)]);
+        for (int t = 0; t < 8; ++t) x[t] = fl(kv[t]) * ek[16 * ks + 8 * (t >> 2) + 4 * hh + (t & 3)];
         split8(x, bh[ks], bl[ks]);
       }
     } else {
@@ -687,7 +694,7 @@ __global__ void __launch_bounds__(256, 3) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
           const int r = 8 * (ks & 1) + t, j = 16 * ks + 8 * (t >> 2) + 4 * hh + (t & 3);
-          x[t] = mt2[ks >> 1][r] * (kside ? bet[j] * exp_fast(gam[j]) : bet[j]);
+          x[t] = mt2[ks >> 1][r] * (kside ? sb[j] : bet[j]);
         }
         split8(x, oh[ks], ol[ks]);
       }
@@ -750,7 +757,9 @@ __global__ void __launch_bounds__(256, 3) gdn_prep_mfma(GdnArgs a, ChunkArgs ca,
         *reinterpret_cast<uint2 *>(yb + o) = uint2{pk_bf16(y[4 * q], y[4 * q + 1]), pk_bf16(y[4 * q + 2], y[4 * q + 3])};
       }
     }
-  }
+  };
+  if (w < DK / 32) phase7(BoolC<true>{});
+  else if (w >= 2) phase7(BoolC<false>{});
 }
 
 // ------------------------------------------------------------------ state scan
