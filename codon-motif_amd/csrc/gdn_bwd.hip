@@ -244,6 +244,153 @@ int launch_scan(const ScanArgs &a, int BH, hipStream_t stream) {
   return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_scan_f32: C in {16, 32, 64} and Dk in {16, 32, 64, 128}");
 }
 
+// ------------------------------------------------------------------ operator-form scan
+// The same two recurrences with each chunk's step folded into one affine operator, formed
+// in parallel before the scan (all chunks at once):
+//   forward   S_{n+1} = A_n S_n + H_n,     A_n = e^{gamma_C} I - Kd_n^T W_n,  H_n = Kd_n^T U_n
+//   reverse   gS_n    = A_n^T gS_{n+1} + G_n,                 G_n = dP_n - W_n^T dX_n
+// (expanding the loops above: X_n = U_n - W_n S_n and dx = Kd_n gS + dX_n substituted),
+// so a chunk costs one Dk x Dk x 16 product per workgroup and one barrier instead of two
+// products and three barriers; X_n = U_n - W_n P_n is then formed outside the scan, for
+// all chunks in parallel.  The kernel walks S <- M_n S + Q_n over the chunks in order
+// (REV: last to first) and records S before each step: P_n (forward) or dSn_n (reverse),
+// with M = A (forward) or A^T (reverse) handed in row-major.
+// Workgroup = (16 state columns, batch.head), 4 waves; wave w owns state row tiles
+// w, w + 4, ...  M_n goes through LDS (double buffered, filled from registers loaded
+// kOpDepth chunks ahead), S^T through LDS (double buffered) for the B operands; the k-sum
+// of each tile is split over four accumulators (independent MFMA chains).  TRANS reads
+// M_n transposed (the reverse scan takes A_n as the forward scan does).  Workgroups go
+// to the 8 XCDs round-robin by linear id: the column groups of one batch.head are
+// placed on one XCD, so each M_n comes from HBM once and from that XCD's L2 after.
+constexpr int kOpDepth = 4;
+constexpr int kXcds = 8;
+
+template <int DK>
+struct OpPre {
+  static constexpr int kMv = DK * DK / 4 / 256 > 0 ? DK * DK / 4 / 256 : 1;  // float4 of M per thread
+  static constexpr int kJt = (DK / 16 + 3) / 4;                             // row tiles per wave
+  f32x4 m[kMv];
+  f32x4 q[kJt];
+};
+
+template <int DK, bool TRANS>
+__global__ void __launch_bounds__(256) gdn_opscan_f32_kernel(const float *__restrict__ M, const float *__restrict__ Q,
+                                                             const float *__restrict__ s0, float *__restrict__ rec,
+                                                             float *__restrict__ s_out, int N, int Dv, int BH, int rev) {
+  constexpr int TT = DK / 16, MS = DK + 4;  // row tiles; LDS row stride (floats) of M and S^T
+  using PR = OpPre<DK>;
+  __shared__ __attribute__((aligned(16))) float sM[2][DK * MS];
+  __shared__ __attribute__((aligned(16))) float sS[2][kCols * MS];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int lr = lane & 15, lq = lane >> 4;
+  // linear id L on XCD L % 8: slot L / 8 of that XCD holds column group slot % ncg of
+  // batch.head 8 (slot / ncg) + L % 8 (the grid is padded to whole groups per XCD)
+  const int ncg = Dv / kCols, slot = blockIdx.x / kXcds;
+  const int bh = (slot / ncg) * kXcds + blockIdx.x % kXcds, v0 = (slot % ncg) * kCols;
+  if (bh >= BH) return;
+  const size_t mstride = static_cast<size_t>(DK) * DK, qstride = static_cast<size_t>(DK) * Dv;
+  const float *Mb = M + static_cast<size_t>(bh) * N * mstride;
+  const float *Qb = Q + static_cast<size_t>(bh) * N * qstride;
+  float *recb = rec + static_cast<size_t>(bh) * N * qstride;
+  auto order = [&](int i) { return rev ? N - 1 - i : i; };
+
+  // element (row, col) of a state-shaped [DK][Dv] matrix held by this lane for tile m, r
+  auto qoff = [&](int m, int r) { return static_cast<size_t>(16 * m + 4 * lq + r) * Dv + v0 + lr; };
+  auto load = [&](PR &pr, int n) {
+    const float *mp = Mb + static_cast<size_t>(n) * mstride;
+#pragma unroll
+    for (int e = 0; e < PR::kMv; ++e) {
+      const int idx = tid + 256 * e;  // float4 index
+      if (idx < DK * DK / 4) pr.m[e] = *reinterpret_cast<const f32x4 *>(mp + 4 * idx);
+    }
+    const float *qp = Qb + static_cast<size_t>(n) * qstride;
+#pragma unroll
+    for (int j = 0; j < PR::kJt; ++j) {
+      const int m = w + 4 * j;
+      if (m < TT)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pr.q[j][r] = qp[qoff(m, r)];
+    }
+  };
+  auto put_m = [&](const PR &pr, int buf) {
+#pragma unroll
+    for (int e = 0; e < PR::kMv; ++e) {
+      const int idx = tid + 256 * e;
+      if (idx < DK * DK / 4) {
+        const int row = (4 * idx) / DK, col = (4 * idx) % DK;
+        *reinterpret_cast<f32x4 *>(&sM[buf][row * MS + col]) = pr.m[e];
+      }
+    }
+  };
+
+  f32x4 sreg[PR::kJt];
+#pragma unroll
+  for (int j = 0; j < PR::kJt; ++j) {
+    const int m = w + 4 * j;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      sreg[j][r] = (s0 && m < TT) ? s0[static_cast<size_t>(bh) * qstride + qoff(m, r)] : 0.f;
+    if (m < TT) *reinterpret_cast<f32x4 *>(&sS[0][lr * MS + 16 * m + 4 * lq]) = sreg[j];
+  }
+  PR pre[kOpDepth];
+#pragma unroll
+  for (int d = 0; d < kOpDepth; ++d)
+    if (d < N) load(pre[d], order(d));
+  if (N > 0) put_m(pre[0], 0);
+  __syncthreads();
+
+  // step i with the register stages of chunk i (cur) and of chunk i + 1 (nxt); the loop
+  // below is unrolled by kOpDepth so the stage indices are compile-time constants
+  auto step = [&](int i, PR &cur, const PR &nxt) {
+    const int n = order(i), buf = i & 1;
+    float *rp = recb + static_cast<size_t>(n) * qstride;
+#pragma unroll
+    for (int j = 0; j < PR::kJt; ++j) {
+      const int m = w + 4 * j;
+      if (m < TT) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) rp[qoff(m, r)] = sreg[j][r];
+        f32x4 acc[4] = {cur.q[j], {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        const float *mrow = TRANS ? &sM[buf][4 * lq * MS + 16 * m + lr] : &sM[buf][(16 * m + lr) * MS + 4 * lq];
+        const float *srow = &sS[buf][lr * MS + 4 * lq];
+#pragma unroll
+        for (int b = 0; b < TT; ++b) {
+          f32x4 a4;
+          if (TRANS) {  // M^T[16 m + lr][16 b + 4 lq + t] = M[16 b + 4 lq + t][16 m + lr]
+#pragma unroll
+            for (int t = 0; t < 4; ++t) a4[t] = mrow[(16 * b + t) * MS];
+          } else {
+            a4 = *reinterpret_cast<const f32x4 *>(mrow + 16 * b);
+          }
+          const f32x4 s4 = *reinterpret_cast<const f32x4 *>(srow + 16 * b);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) acc[t] = mma4(a4[t], s4[t], acc[t]);
+        }
+        sreg[j] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        *reinterpret_cast<f32x4 *>(&sS[buf ^ 1][lr * MS + 16 * m + 4 * lq]) = sreg[j];
+      }
+    }
+    if (i + 1 < N) put_m(nxt, buf ^ 1);
+    if (i + kOpDepth < N) load(cur, order(i + kOpDepth));
+    __syncthreads();
+  };
+  int i = 0;
+  for (; i + kOpDepth <= N; i += kOpDepth) {
+#pragma unroll
+    for (int j = 0; j < kOpDepth; ++j) step(i + j, pre[j], pre[(j + 1) % kOpDepth]);
+  }
+#pragma unroll
+  for (int j = 0; j < kOpDepth - 1; ++j)
+    if (i + j < N) step(i + j, pre[j], pre[(j + 1) % kOpDepth]);
+#pragma unroll
+  for (int j = 0; j < PR::kJt; ++j) {
+    const int m = w + 4 * j;
+    if (m < TT)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s_out[static_cast<size_t>(bh) * qstride + qoff(m, r)] = sreg[j][r];
+  }
+}
+
 int check_scan_sizes(int BH, int N, int C, int Dk, int Dv, const char *who) {
   if (BH < 0 || N < 0 || C <= 0 || Dk <= 0 || Dv <= 0) return set_error(MOTIF_ERR_INVALID, std::string(who) + ": bad sizes");
   if ((C != 16 && C != 32 && C != 64) || (Dk != 16 && Dk != 32 && Dk != 64 && Dk != 128) || Dv % kCols)
@@ -282,4 +429,23 @@ extern "C" int motif_gdn_scan_bwd_f32(const float *k, const float *W, const floa
     return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_scan_bwd_f32: k and W need 16-byte alignment");
   ScanArgs a{k, W, nullptr, g, dS_final, dX, dP, dSn, nullptr, dS0, N, C, Dk, Dv};
   return launch_scan<true>(a, BH, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int motif_gdn_opscan_f32(const float *M, const float *Q, const float *S0, float *rec, float *S_out, int BH,
+                                    int N, int Dk, int Dv, int reverse, int transpose, void *stream) {
+  using namespace motif;
+  if (BH < 0 || N < 0 || Dk <= 0 || Dv <= 0) return set_error(MOTIF_ERR_INVALID, "gdn_opscan_f32: bad sizes");
+  if ((Dk != 16 && Dk != 32 && Dk != 64) || Dv % kCols)
+    return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_opscan_f32: needs Dk in {16, 32, 64} and Dv a multiple of 16");
+  if (BH == 0) return MOTIF_OK;
+  if ((N > 0 && (!M || !Q || !rec)) || !S_out) return set_error(MOTIF_ERR_INVALID, "gdn_opscan_f32: NULL pointer");
+  if (reinterpret_cast<uintptr_t>(M) & 15) return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_opscan_f32: M needs 16-byte alignment");
+  const dim3 grid((BH + kXcds - 1) / kXcds * kXcds * (Dv / kCols)), block(256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define MOTIF_OPSCAN(D, T) gdn_opscan_f32_kernel<D, T><<<grid, block, 0, s>>>(M, Q, S0, rec, S_out, N, Dv, BH, reverse)
+  if (Dk == 16) { if (transpose) MOTIF_OPSCAN(16, true); else MOTIF_OPSCAN(16, false); }
+  else if (Dk == 32) { if (transpose) MOTIF_OPSCAN(32, true); else MOTIF_OPSCAN(32, false); }
+  else { if (transpose) MOTIF_OPSCAN(64, true); else MOTIF_OPSCAN(64, false); }
+#undef MOTIF_OPSCAN
+  return check_launch("gdn_opscan_f32_kernel");
 }

@@ -10,7 +10,9 @@
 //   gdn_bwd_prep_kernel   gamma = cumsum(g), A = -strict(beta k k^T * D), T = (I - A)^{-1}
 //                         (blocked substitution), W = T (beta e^gamma k), U = T (beta v), and
 //                         the output's upstream terms dP = (q e^gamma)^T do and
-//                         dX = ((q k^T) * D)^T do that feed the reverse scan;
+//                         dX = ((q k^T) * D)^T do that feed the reverse scan, and (when
+//                         asked) the scans' per-chunk operators A = e^{gamma_C} I - Kd^T W,
+//                         H = Kd^T U and G = dP - W^T dX (Kd = k e^{gamma_C - gamma});
 //   gdn_bwd_chunk_kernel  from the scans' P, X and dSn: dq, dk, dv, dbeta, dg
 //                         (the formulas of ops/gdn_grad.py's GDNChunkFunction.backward).
 //
@@ -51,6 +53,7 @@ __device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 *
 struct BwdPrepArgs {
   const float *q, *k, *v, *beta, *g, *dout;  // [BH * N][C][dk | dv], [BH * N][C]
   float *W, *U, *gam, *T, *dP, *dX;          // [..][C][dk], [..][C][dv], [..][C], [..][C][C], [..][dk][dv], [..][C][dv]
+  float *A, *Hn, *G;                         // optional scan operators [..][dk][dk], [..][dk][dv], [..][dk][dv]
 };
 
 struct BwdChunkArgs {
@@ -163,39 +166,87 @@ __global__ void __launch_bounds__(256) gdn_bwd_prep_kernel(BwdPrepArgs a) {
     }
   }
   // W = T (beta e^gamma k)
-  {
-    f32x16 acc = {};
-    mm<C>(acc, [&](int m, int k) { return sT[(r0 + m) * LD + k]; },
-          [&](int k, int n) { return sB[k] * sE[k] * sK[k * LD + c0 + n]; });
+  f32x16 wreg = {};
+  mm<C>(wreg, [&](int m, int k) { return sT[(r0 + m) * LD + k]; },
+        [&](int k, int n) { return sB[k] * sE[k] * sK[k * LD + c0 + n]; });
 #pragma unroll
-    for (int r = 0; r < 16; ++r) a.W[(cb * C + r0 + acc_row(r, h)) * DK + c0 + i] = acc[r];
-  }
+  for (int r = 0; r < 16; ++r) a.W[(cb * C + r0 + acc_row(r, h)) * DK + c0 + i] = wreg[r];
   // U = T (beta v), dP = (q e^gamma)^T do: column tiles c0 + 64 j of the dv columns
+  f32x16 ureg[DV / 64], dpreg[DV / 64];
 #pragma unroll
   for (int j = 0; j < DV / 64; ++j) {
     const int n0 = c0 + 64 * j;
-    f32x16 u = {}, dp = {};
-    mm<C>(u, [&](int m, int k) { return sT[(r0 + m) * LD + k]; }, [&](int k, int n) { return sB[k] * sV[k * LV + n0 + n]; });
-    mm<C>(dp, [&](int m, int k) { return sQ[k * LD + r0 + m] * sE[k]; }, [&](int k, int n) { return sDo[k * LV + n0 + n]; });
+    ureg[j] = f32x16{};
+    dpreg[j] = f32x16{};
+    mm<C>(ureg[j], [&](int m, int k) { return sT[(r0 + m) * LD + k]; }, [&](int k, int n) { return sB[k] * sV[k * LV + n0 + n]; });
+    mm<C>(dpreg[j], [&](int m, int k) { return sQ[k * LD + r0 + m] * sE[k]; }, [&](int k, int n) { return sDo[k * LV + n0 + n]; });
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int R = r0 + acc_row(r, h);
-      a.U[(cb * C + R) * DV + n0 + i] = u[r];
-      a.dP[(cb * DK + R) * DV + n0 + i] = dp[r];
+      a.U[(cb * C + R) * DV + n0 + i] = ureg[j][r];
+      if (a.dP) a.dP[(cb * DK + R) * DV + n0 + i] = dpreg[j][r];
     }
   }
   for (int e = tid; e < C * C; e += 256) a.T[cb * C * C + e] = sT[(e >> 6) * LD + (e & 63)];
-  __syncthreads();  // Attn complete
+  __syncthreads();  // Attn complete; the reads of T, V and Q above are done
+  // With the scan operators requested: W over the T rows, U over the V rows, and
+  // ek = e^{gamma_C - gamma} in the inverse's scratch (all dead here).
+  const bool ops = a.A != nullptr;
+  float *sEk = sXs;
+  if (ops) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sT[(r0 + acc_row(r, h)) * LD + c0 + i] = wreg[r];
+#pragma unroll
+    for (int j = 0; j < DV / 64; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sV[(r0 + acc_row(r, h)) * LV + c0 + 64 * j + i] = ureg[j][r];
+    if (w == 0) sEk[lane] = __expf(sGam[C - 1] - sGam[lane]);
+  }
   // dX = Attn^T do
+  f32x16 dxreg[DV / 64];
 #pragma unroll
   for (int j = 0; j < DV / 64; ++j) {
     const int n0 = c0 + 64 * j;
-    f32x16 dx = {};
-    mm<C>(dx, [&](int m, int k) { return sA[k * LD + r0 + m]; }, [&](int k, int n) { return sDo[k * LV + n0 + n]; });
+    dxreg[j] = f32x16{};
+    mm<C>(dxreg[j], [&](int m, int k) { return sA[k * LD + r0 + m]; }, [&](int k, int n) { return sDo[k * LV + n0 + n]; });
 #pragma unroll
-    for (int r = 0; r < 16; ++r) a.dX[(cb * C + r0 + acc_row(r, h)) * DV + n0 + i] = dx[r];
+    for (int r = 0; r < 16; ++r) a.dX[(cb * C + r0 + acc_row(r, h)) * DV + n0 + i] = dxreg[j][r];
+  }
+  if (!ops) return;
+  // The per-chunk operators of the operator-form scans (gdn_bwd.hip):
+  //   A = e^{gamma_C} I - Kd^T W,  H = Kd^T U,  G = dP - W^T dX,  Kd = k e^{gamma_C - gamma}
+  __syncthreads();  // the reads of do are done; W, U and ek are visible
+#pragma unroll
+  for (int j = 0; j < DV / 64; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sDo[(r0 + acc_row(r, h)) * LV + c0 + 64 * j + i] = dxreg[j][r];
+  __syncthreads();  // dX over the do rows
+  auto kdT = [&](int m, int k) { return sK[k * LD + r0 + m] * sEk[k]; };
+  {
+    f32x16 acc = {};
+    mm<C>(acc, kdT, [&](int k, int n) { return sT[k * LD + c0 + n]; });
+    const float ec = sE[C - 1];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int R = r0 + acc_row(r, h), Nc = c0 + i;
+      a.A[(cb * DK + R) * DK + Nc] = (R == Nc ? ec : 0.f) - acc[r];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < DV / 64; ++j) {
+    const int n0 = c0 + 64 * j;
+    f32x16 hacc = {}, gacc = {};
+    mm<C>(hacc, kdT, [&](int k, int n) { return sV[k * LV + n0 + n]; });
+    mm<C>(gacc, [&](int m, int k) { return sT[k * LD + r0 + m]; }, [&](int k, int n) { return sDo[k * LV + n0 + n]; });
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int R = r0 + acc_row(r, h);
+      a.Hn[(cb * DK + R) * DV + n0 + i] = hacc[r];
+      a.G[(cb * DK + R) * DV + n0 + i] = dpreg[j][r] - gacc[r];
+    }
   }
 }
+
 
 template <int DV>
 __global__ void __launch_bounds__(256) gdn_bwd_chunk_kernel(BwdChunkArgs a) {
@@ -432,16 +483,18 @@ bool aligned16(std::initializer_list<const void *> ps) {
 
 extern "C" int motif_gdn_bwd_prep_f32(const float *q, const float *k, const float *v, const float *beta,
                                       const float *g, const float *dout, float *W, float *U, float *gam, float *T,
-                                      float *dP, float *dX, int BH, int N, int C, int Dk, int Dv, void *stream) {
+                                      float *dP, float *dX, float *A, float *Hn, float *G, int BH, int N, int C,
+                                      int Dk, int Dv, void *stream) {
   using namespace motif;
   if (int rc = check_bwd_sizes(BH, N, C, Dk, Dv, "gdn_bwd_prep_f32")) return rc;
   const int64_t blocks = static_cast<int64_t>(BH) * N;
   if (blocks == 0) return MOTIF_OK;
-  if (!q || !k || !v || !beta || !g || !dout || !W || !U || !gam || !T || !dP || !dX)
+  if (!q || !k || !v || !beta || !g || !dout || !W || !U || !gam || !T || !dX || (!dP && !A) ||
+      (A && (!Hn || !G)))
     return set_error(MOTIF_ERR_INVALID, "gdn_bwd_prep_f32: NULL pointer");
   if (!aligned16({q, k, v, dout}))
     return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_bwd_prep_f32: q, k, v and dout need 16-byte alignment");
-  BwdPrepArgs a{q, k, v, beta, g, dout, W, U, gam, T, dP, dX};
+  BwdPrepArgs a{q, k, v, beta, g, dout, W, U, gam, T, dP, dX, A, Hn, G};
   hipStream_t s = static_cast<hipStream_t>(stream);
   const size_t smem = prep_smem(Dv);
   if (Dv == 64) {

@@ -69,25 +69,65 @@ def bwd_scan(k, W, g, dX, dP, dS_final):
     return dSn, dS0
 
 
+def opscan(M, Q, S0, reverse, transpose=False):
+    '''S <- M_n S + Q_n (transpose: M_n^T S + Q_n) over the chunks on the HIP kernel
+    (reverse: last chunk first), recording S before each step: (rec [B,H,N,Dk,Dv],
+    S_final [B,H,Dk,Dv]) from fp32 M [B,H,N,Dk,Dk], Q [B,H,N,Dk,Dv] and S0 [B,H,Dk,Dv]
+    (or None: zeros).  The two scans of the reference's backward
+    (motif/ops/gated_deltanet.py:327-408, :428-520) in operator form: M = A_n =
+    e^{gamma_C} I - Kd_n^T W_n with Q = H_n = Kd_n^T U_n (forward, records P), M^T = A_n^T
+    with Q = G_n = dP_n - W_n^T dX_n (reverse, records dSn).'''
+    B, H, N, Dk, Dv = Q.shape
+    M, Q = M.float().contiguous(), Q.float().contiguous()
+    S0 = None if S0 is None else S0.float().contiguous()
+    rec = torch.empty(B, H, N, Dk, Dv, dtype=torch.float32, device=Q.device)
+    S = torch.empty(B, H, Dk, Dv, dtype=torch.float32, device=Q.device)
+    rc = _lib.lib().motif_gdn_opscan_f32(M.data_ptr(), Q.data_ptr(), _lib.ptr(S0), rec.data_ptr(), S.data_ptr(),
+                                         B * H, N, Dk, Dv, int(bool(reverse)), int(bool(transpose)),
+                                         _lib.stream_ptr(Q.device))
+    _lib.check(rc, 'motif_gdn_opscan_f32')
+    return rec, S
+
+
+def scan_operators(kc, W, U, gam, dP, dX):
+    '''The per-chunk affine operators of both scans, for all chunks at once (fp32 batched
+    products): A = e^{gamma_C} I - Kd^T W, H = Kd^T U, G = dP - W^T dX, Kd = k e^{gamma_C - gamma}.'''
+    gl = gam[..., -1:]
+    kdT = (kc * (gl - gam).exp()[..., None]).transpose(-1, -2)
+    A = torch.matmul(kdT, W).neg_()
+    A.diagonal(dim1=-2, dim2=-1).add_(gl.exp())
+    return A, torch.matmul(kdT, U), dP - torch.matmul(W.transpose(-1, -2), dX)
+
+
 def chunk_kernels_serve(Dk: int, Dv: int, C: int) -> bool:
     '''True when the per-chunk backward kernels take this shape (chunk 64, dk 64, dv 64 or
     128); other shapes run the per-chunk terms as torch products.'''
     return C == 64 and Dk == 64 and Dv in (64, 128)
 
 
-def bwd_prep(qc, kc, vc, bc, gc, doc):
+def bwd_prep(qc, kc, vc, bc, gc, doc, operators=False):
     '''Per-chunk terms before the scans on the HIP kernel, from chunked fp32 inputs
-    q, k [B,H,N,C,Dk], v, do [B,H,N,C,Dv], beta, g [B,H,N,C]: (W, U, gamma, T, dP, dX).'''
+    q, k [B,H,N,C,Dk], v, do [B,H,N,C,Dv], beta, g [B,H,N,C]: (W, U, gamma, T, dP, dX), or
+    with `operators` (W, U, gamma, T, dX, A, Hn, G), the scans' per-chunk operators
+    A = e^{gamma_C} I - Kd^T W [B,H,N,Dk,Dk], Hn = Kd^T U and G = dP - W^T dX
+    [B,H,N,Dk,Dv] in place of dP.'''
     B, H, N, C, Dk = kc.shape
     Dv = vc.shape[-1]
     dev = kc.device
     f = lambda *shape: torch.empty(B, H, N, *shape, dtype=torch.float32, device=dev)
-    W, U, gam, T, dP, dX = f(C, Dk), f(C, Dv), f(C), f(C, C), f(Dk, Dv), f(C, Dv)
+    W, U, gam, T, dX = f(C, Dk), f(C, Dv), f(C), f(C, C), f(C, Dv)
+    if operators:
+        dP, A, Hn, G = None, f(Dk, Dk), f(Dk, Dv), f(Dk, Dv)
+    else:
+        dP, A, Hn, G = f(Dk, Dv), None, None, None
     rc = _lib.lib().motif_gdn_bwd_prep_f32(qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), bc.data_ptr(),
                                            gc.data_ptr(), doc.data_ptr(), W.data_ptr(), U.data_ptr(),
-                                           gam.data_ptr(), T.data_ptr(), dP.data_ptr(), dX.data_ptr(),
+                                           gam.data_ptr(), T.data_ptr(), _lib.ptr(dP), dX.data_ptr(),
+                                           _lib.ptr(A), _lib.ptr(Hn), _lib.ptr(G),
                                            B * H, N, C, Dk, Dv, _lib.stream_ptr(dev))
     _lib.check(rc, 'motif_gdn_bwd_prep_f32')
+    if operators:
+        return W, U, gam, T, dX, A, Hn, G
     return W, U, gam, T, dP, dX
 
 
@@ -179,9 +219,12 @@ def _backward_kernels(q, k, v, beta, g, S0, do, dS_fin, C):
     pad = (C - L % C) % C
     qc, kc, vc, doc = (_chunks(t, C, pad).contiguous() for t in (q, k, v, do))
     bc, gc = (_chunks(t, C, pad).contiguous() for t in (beta, g))
-    W, U, gam, T, dP, dX = bwd_prep(qc, kc, vc, bc, gc, doc)
-    P, _, X = fused_scan(kc, W, U, gam, S0)
-    dSn, dS0 = bwd_scan(kc, W, gam, dX, dP, dS_fin)
+    W, U, gam, T, dX, A, Hn, G = bwd_prep(qc, kc, vc, bc, gc, doc, operators=True)
+    P, _ = opscan(A, Hn, S0, reverse=False)
+    # the residuals X_n = U_n - W_n P_n, all chunks in one batched product
+    X = torch.baddbmm(U.reshape(-1, *U.shape[-2:]), W.reshape(-1, *W.shape[-2:]), P.reshape(-1, *P.shape[-2:]),
+                      alpha=-1.0).view_as(U)
+    dSn, dS0 = opscan(A, G, dS_fin, reverse=True, transpose=True)
     dq, dk, dv, dbeta, dg = bwd_chunk(qc, kc, vc, bc, gam, T, P, X, dSn, doc, dX)
     return (_back(dq, q, L), _back(dk, k, L), _back(dv, v, L), _back(dbeta, beta, L), _back(dg, g, L),
             None if S0 is None else dS0.to(S0.dtype))

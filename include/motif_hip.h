@@ -115,12 +115,28 @@ int motif_gdn_scan_bwd_f32(const float *k, const float *W, const float *g, const
                            const float *dS_final, float *dSn, float *dS0, int BH, int N, int C, int Dk, int Dv,
                            void *stream);
 /*
+ * Both chunk scans of the backward in operator form (fp32): walks S <- M_n S + Q_n
+ * (transpose != 0: S <- M_n^T S + Q_n) over the chunks (reverse != 0: last chunk first)
+ * from S0 [BH,Dk,Dv] (NULL: zeros), writing S before each step to rec [BH,N,Dk,Dv] and the
+ * final S to S_out.  M [BH,N,Dk,Dk] (16-byte aligned), Q [BH,N,Dk,Dv]; Dk in {16, 32, 64},
+ * Dv a multiple of 16.  With M = A_n = e^{gamma_C} I - Kd^T W and Q = Kd^T U it is the
+ * forward re-scan (rec = P), with the same M transposed and Q = dP - W^T dX the reverse
+ * scan (rec = dSn): the reference's _gdn_fused_scan_kernel and _gdn_bwd_scan_kernel
+ * (motif/ops/gated_deltanet.py:327-408, :428-520) with the per-chunk products folded into
+ * one operator per chunk, formed beforehand for all chunks at once.
+ */
+int motif_gdn_opscan_f32(const float *M, const float *Q, const float *S0, float *rec, float *S_out, int BH, int N,
+                         int Dk, int Dv, int reverse, int transpose, void *stream);
+/*
  * Chunk backward, the per-chunk terms before the scans (fp32).  Inputs are chunked and
  * zero-padded: q, k [BH,N,C,Dk], v, dout [BH,N,C,Dv], beta, g [BH,N,C].  Writes
  * gam = cumsum(g) per chunk [BH,N,C], T = (I + strict(beta k k^T * D))^{-1} [BH,N,C,C],
  * W = T (beta e^gam k) [BH,N,C,Dk], U = T (beta v) [BH,N,C,Dv] (the forward re-scan's
  * inputs) and the output's upstream terms dP = (q e^gam)^T dout [BH,N,Dk,Dv],
- * dX = ((q k^T) * D)^T dout [BH,N,C,Dv] (the reverse scan's inputs).  Replaces the
+ * dX = ((q k^T) * D)^T dout [BH,N,C,Dv] (the reverse scan's inputs).  With A non-NULL it
+ * also writes the operators of motif_gdn_opscan_f32: A = e^{gam_C} I - Kd^T W [BH,N,Dk,Dk],
+ * Hn = Kd^T U and G = dP - W^T dX [BH,N,Dk,Dv] (Kd = k e^{gam_C - gam}); dP may then be
+ * NULL.  Replaces the
  * reference's chunk preparation forward recomputed for the backward
  * (motif/ops/gated_deltanet.py:118-177, the solve_triangular at :161-166) and the
  * autograd of the output combination (:830-832).  C == 64, Dk == 64, Dv in {64, 128};
@@ -128,7 +144,7 @@ int motif_gdn_scan_bwd_f32(const float *k, const float *W, const float *g, const
  */
 int motif_gdn_bwd_prep_f32(const float *q, const float *k, const float *v, const float *beta, const float *g,
                            const float *dout, float *W, float *U, float *gam, float *T, float *dP, float *dX,
-                           int BH, int N, int C, int Dk, int Dv, void *stream);
+                           float *A, float *Hn, float *G, int BH, int N, int C, int Dk, int Dv, void *stream);
 /*
  * Chunk backward, the per-chunk gradients after the scans (fp32): from the prep's gam, T
  * and dX, the forward re-scan's P [BH,N,Dk,Dv] and X [BH,N,C,Dv] and the reverse scan's

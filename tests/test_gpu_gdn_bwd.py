@@ -80,6 +80,42 @@ def test_scans_match_loops(N, C, Dk, Dv):
     _close(dS0, rdS0, 'dS0')
 
 
+@pytest.mark.parametrize('N,Dk,Dv', [(5, 64, 128), (64, 64, 128), (1, 64, 64), (3, 32, 48), (2, 16, 16)])
+def test_operator_scans_match_loops(N, Dk, Dv):
+    '''The operator-form scans (motif_gdn_opscan_f32 with the per-chunk operators formed
+    beforehand) against the same defining loops as the direct scans.'''
+    from motif.ops.gdn_grad import opscan, scan_operators
+    g0 = torch.Generator().manual_seed(N * 11 + Dv)
+    B, H, C = 2, 3, 64
+    k = torch.nn.functional.normalize(torch.randn(B, H, N, C, Dk, generator=g0), dim=-1)
+    W = torch.randn(B, H, N, C, Dk, generator=g0) * 0.2
+    U = torch.randn(B, H, N, C, Dv, generator=g0)
+    g = torch.nn.functional.logsigmoid(torch.randn(B, H, N, C, generator=g0)).cumsum(-1) * 0.2
+    S0 = torch.randn(B, H, Dk, Dv, generator=g0) * 0.3
+    dX = torch.randn(B, H, N, C, Dv, generator=g0)
+    dP = torch.randn(B, H, N, Dk, Dv, generator=g0) * 0.1
+    dS = torch.randn(B, H, Dk, Dv, generator=g0)
+    kd, Wd, Ud, gd, dPd, dXd = (t.to(DEV) for t in (k, W, U, g, dP, dX))
+    A, Hn, G = scan_operators(kd, Wd, Ud, gd, dPd, dXd)
+    P, S = opscan(A, Hn, S0.to(DEV), reverse=False)
+    X = Ud - torch.matmul(Wd, P)
+    rP, rS, rX = _scan_fwd_ref(*(t.double() for t in (k, W, U, g, S0)))
+    _close(P, rP, 'P')
+    _close(S, rS, 'S')
+    _close(X, rX, 'X')
+    dSn, dS0 = opscan(A, G, dS.to(DEV), reverse=True, transpose=True)
+    dSn2, _ = opscan(A.transpose(-1, -2), G, dS.to(DEV), reverse=True)
+    _close(dSn2, dSn, 'dSn (transposed operand handed in)')
+    rdSn, rdS0 = _scan_bwd_ref(*(t.double() for t in (k, W, g, dX, dP, dS)))
+    _close(dSn, rdSn, 'dSn')
+    _close(dS0, rdS0, 'dS0')
+    P0, S00 = opscan(A, Hn, None, reverse=False)   # zero initial state
+    rP0, rS00, _ = _scan_fwd_ref(*(t.double() for t in (k, W, U, g, torch.zeros_like(S0))))
+    _close(P0, rP0, 'P (S0 = 0)')
+    _close(S00, rS00, 'S (S0 = 0)')
+
+
+
 def _grads(fn, q, k, v, b, g, S0, do, dS, dev, dtype):
     ts = [t.to(dev, dtype).requires_grad_(True) for t in (q, k, v, b, g)]
     s0 = S0.to(dev, torch.float64 if dtype == torch.float64 else torch.float32).requires_grad_(True)
@@ -195,3 +231,25 @@ def test_chunk_kernels_equal_torch_products(B, H, L, dv):
     for name, x, y in zip(('dq', 'dk', 'dv', 'dbeta', 'dg', 'dS0'), got, ref):
         assert x.shape == y.shape, name
         _close(x, y, f'{name} (B={B} H={H} L={L} dv={dv})', 1e-4)
+
+
+@pytest.mark.parametrize('dv', [64, 128])
+def test_prep_scan_operators_equal_torch_products(dv):
+    '''The backward prep kernel's scan operators (A, Hn, G) against the same operators
+    formed from its other outputs by fp32 torch products (scan_operators), and its W, U,
+    gamma, T, dX unchanged by asking for them.'''
+    from motif.ops.gdn_grad import _chunks, bwd_prep, scan_operators
+    B, H, L = 1, 3, 300
+    q, k, v, b, g = (t.to(DEV) for t in gdn_inputs(B, H, L, 64, dv, seed=dv))
+    do = torch.randn(B, H, L, dv, generator=torch.Generator().manual_seed(dv)).to(DEV)
+    pad = (64 - L % 64) % 64
+    qc, kc, vc, doc = (_chunks(t, 64, pad).contiguous() for t in (q, k, v, do))
+    bc, gc = (_chunks(t, 64, pad).contiguous() for t in (b, g))
+    W, U, gam, T, dP, dX = bwd_prep(qc, kc, vc, bc, gc, doc)
+    W2, U2, gam2, T2, dX2, A, Hn, G = bwd_prep(qc, kc, vc, bc, gc, doc, operators=True)
+    for name, x, y in (('W', W2, W), ('U', U2, U), ('gam', gam2, gam), ('T', T2, T), ('dX', dX2, dX)):
+        assert torch.equal(x, y), name
+    rA, rH, rG = scan_operators(kc, W, U, gam, dP, dX)
+    _close(A, rA, 'A', 1e-5)
+    _close(Hn, rH, 'Hn', 1e-5)
+    _close(G, rG, 'G', 1e-5)
