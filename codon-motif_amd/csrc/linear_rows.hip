@@ -79,14 +79,37 @@ __device__ __forceinline__ int w_row(int n0, int t, int c, int nout) {
 // L1 asks L2 for full lines -- half the requests of P = 1 (16 rows x 64 bytes per
 // instruction).  MFMA j of the step sums k = 16 kq + 8 j .. +7 over the lane groups
 // kq, the same set in A and B, so the products are unchanged.
-// LDS of the cross-wave sum: [kWaves][tiles][64] f32x4.
-template <int MT, int NT>
-constexpr int red_bytes() { return kWaves * MT * NT * 64 * 16; }
+// The activation rows of a wave's k-steps go through LDS when they fit (P == 2, at most
+// 8 row tiles x k-steps): direct buffer-to-LDS loads of whole 128-byte row segments, 8 rows
+// per instruction (a load instruction spanning 16 rows x 64 bytes, the MFMA operand
+// layout, keeps twice the lines in flight per byte and measured slower), then 16-byte LDS
+// reads in operand order.  Each wave stages its rows in its own LDS region, which then
+// takes its partial sums for the cross-wave sum; a row's 16-byte chunks are XOR-swizzled
+// by row so the operand reads of 16 rows spread over the banks.
+template <int MT, int KS, int P>
+constexpr bool x_staged() { return P == 2 && MT * KS <= 8; }
+// LDS per wave: partials [MT * NT][64] f32x4 or the staged rows [KS][16 MT][128 B]
+template <int MT, int NT, int KS, int P>
+constexpr int wave_lds() {
+  return MT * NT * 1024 > (x_staged<MT, KS, P>() ? KS * MT * 2048 : 0) ? MT * NT * 1024 : KS * MT * 2048;
+}
+template <int MT, int NT, int KS, int P>
+constexpr int tile_lds() { return kWaves * wave_lds<MT, NT, KS, P>(); }
+
+typedef __attribute__((address_space(3))) void lds_void;
+// 16 bytes per lane of rows [8 g, 8 g + 8) x one 128-byte k-step of the staged rows
+// (lane l: row 8 g + l / 8, physical chunk l % 8 holding logical chunk (l % 8) ^ (row % 8)),
+// into dst + 16 l
+__device__ __forceinline__ void x_stage(buf_t xb, char *dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(xb, (lds_void *)dst, 16, voff, soff, 0, 0);
+}
 
 // One workgroup's output tile; `id` is its index among the launch's workgroups for this
 // problem, `red` the LDS for the cross-wave sum.
 template <int MT, int NT, int KS, int EPI, int P>
-__device__ __forceinline__ void rows_tile(const LinArgs &a, const int id, f32x4 *red_lds) {
+__device__ __forceinline__ void rows_tile(const LinArgs &a, const int id, char *lds) {
+  constexpr bool XS = x_staged<MT, KS, P>();
+  constexpr int WL = wave_lds<MT, NT, KS, P>();
   // The wave index in an SGPR: the k-range below is then wave-uniform to the compiler
   // (scalar branches, step offsets in the loads' scalar offset operand).
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -116,6 +139,15 @@ __device__ __forceinline__ void rows_tile(const LinArgs &a, const int id, f32x4 
 
   const int nsteps = a.K / (32 * P);
   const int s0 = wv * nsteps / kWaves, s1 = (wv + 1) * nsteps / kWaves;
+  char *wlds = lds + wv * WL;  // this wave's LDS region
+  uint32_t xso[XS ? 2 * MT : 1];
+  if constexpr (XS) {
+#pragma unroll
+    for (int g8 = 0; g8 < 2 * MT; ++g8) {
+      const int rl = 8 * g8 + (lane >> 3);
+      xso[g8] = static_cast<uint32_t>((min(rl, rows - 1) * a.x_rs + 8 * ((lane & 7) ^ (rl & 7))) * 2);
+    }
+  }
 
   f32x4 acc[MT][NT];
 #pragma unroll
@@ -133,10 +165,16 @@ __device__ __forceinline__ void rows_tile(const LinArgs &a, const int id, f32x4 
 #pragma unroll
     for (int c = 0; c < KS; ++c) {
       const uint32_t soff = s + c < s1 ? static_cast<uint32_t>(s + c) * (64u * P) : 0x80000000u;
+      if constexpr (XS) {
+#pragma unroll
+        for (int g8 = 0; g8 < 2 * MT; ++g8) x_stage(xb, wlds + (c * MT * 16 + 8 * g8) * 128, xso[g8], soff);
+      }
 #pragma unroll
       for (int j = 0; j < P; ++j) {
+        if constexpr (!XS) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) A[c][j][mt] = ld8(xb, xo[mt] + 16 * j, soff);
+          for (int mt = 0; mt < MT; ++mt) A[c][j][mt] = ld8(xb, xo[mt] + 16 * j, soff);
+        }
 #pragma unroll
         for (int t = 0; t < NT; ++t) B[c][j][t] = ldw<MT == 4>(wb, wo[t] + 16 * j, soff);
       }
@@ -144,6 +182,17 @@ __device__ __forceinline__ void rows_tile(const LinArgs &a, const int id, f32x4 
     // keep the whole batch of loads ahead of the MFMAs (the scheduler would otherwise
     // interleave them to save registers, serialising the round trips)
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (XS) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the staged rows have landed
+#pragma unroll
+      for (int c = 0; c < KS; ++c)
+#pragma unroll
+        for (int j = 0; j < P; ++j)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            A[c][j][mt] = *reinterpret_cast<const bf16x8 *>(wlds + (c * MT * 16 + 16 * mt + r16) * 128 +
+                                                            ((2 * kq + j) ^ (r16 & 7)) * 16);
+    }
 #pragma unroll
     for (int c = 0; c < KS; ++c)
 #pragma unroll
@@ -154,12 +203,16 @@ __device__ __forceinline__ void rows_tile(const LinArgs &a, const int id, f32x4 
           for (int t = 0; t < NT; ++t) acc[mt][t] = mma(A[c][j][mt], B[c][j][t], acc[mt][t]);
   }
 
-  // Cross-wave sum in LDS: red[wave][tile][lane] (16 bytes per lane).
-  auto red = reinterpret_cast<f32x4 (*)[MT * NT][64]>(red_lds);
+  // Cross-wave sum in LDS: wave w's partials at lds + w * WL, [tile][lane] (16 bytes per
+  // lane), over its own staged rows (its reads of them are done: LDS operations of a wave
+  // complete in order).
+  auto red = [&](int w, int tile, int l) -> f32x4 & {
+    return reinterpret_cast<f32x4 *>(lds + w * WL)[tile * 64 + l];
+  };
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int t = 0; t < NT; ++t) red[wv][mt * NT + t][lane] = acc[mt][t];
+    for (int t = 0; t < NT; ++t) red(wv, mt * NT + t, lane) = acc[mt][t];
   __syncthreads();
 
   // Thread p (p, p + 512, ...) finishes (row tile mt, value tile tv, lane l): one C tile
@@ -167,12 +220,12 @@ __device__ __forceinline__ void rows_tile(const LinArgs &a, const int id, f32x4 
   constexpr int kOut = EPI == EPI_SWIGLU ? NT / 2 : NT;  // output tiles per row tile
   for (int p = threadIdx.x; p < MT * kOut * 64; p += 64 * kWaves) {
   const int l = p & 63, tv = (p >> 6) % kOut, mt = (p >> 6) / kOut;
-  f32x4 v = red[0][mt * NT + tv][l], g = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (EPI == EPI_SWIGLU) g = red[0][mt * NT + tv + kOut][l];
+  f32x4 v = red(0, mt * NT + tv, l), g = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (EPI == EPI_SWIGLU) g = red(0, mt * NT + tv + kOut, l);
 #pragma unroll
   for (int w = 1; w < kWaves; ++w) {
-    v += red[w][mt * NT + tv][l];
-    if (EPI == EPI_SWIGLU) g += red[w][mt * NT + tv + kOut][l];
+    v += red(w, mt * NT + tv, l);
+    if (EPI == EPI_SWIGLU) g += red(w, mt * NT + tv + kOut, l);
   }
   const int col = n0 + 16 * tv + (l & 15);
   if (col >= nout) continue;
@@ -198,8 +251,8 @@ __device__ __forceinline__ void rows_tile(const LinArgs &a, const int id, f32x4 
 
 template <int MT, int NT, int KS, int EPI, int P>
 __global__ void __launch_bounds__(512) linear_rows_kernel(LinArgs a) {
-  __shared__ f32x4 red[red_bytes<MT, NT>() / 16];
-  rows_tile<MT, NT, KS, EPI, P>(a, blockIdx.x, red);
+  __shared__ f32x4 lds[tile_lds<MT, NT, KS, P>() / 16];
+  rows_tile<MT, NT, KS, EPI, P>(a, blockIdx.x, reinterpret_cast<char *>(lds));
 }
 
 // Two independent projections in one launch (the decoder's attention input projection
@@ -207,11 +260,11 @@ __global__ void __launch_bounds__(512) linear_rows_kernel(LinArgs a) {
 // [0, a1.grid) take problem 1, the rest problem 2.  Each keeps its own tile shape.
 template <int MT1, int NT1, int KS1, int EPI1, int MT2, int NT2, int KS2, int EPI2, int P>
 __global__ void __launch_bounds__(512) linear_rows_pair_kernel(LinArgs a1, LinArgs a2) {
-  constexpr int b1 = red_bytes<MT1, NT1>(), b2 = red_bytes<MT2, NT2>();
-  __shared__ f32x4 red[(b1 > b2 ? b1 : b2) / 16];
+  constexpr int b1 = tile_lds<MT1, NT1, KS1, P>(), b2 = tile_lds<MT2, NT2, KS2, P>();
+  __shared__ f32x4 lds[(b1 > b2 ? b1 : b2) / 16];
   const int id = blockIdx.x;
-  if (id < a1.grid) rows_tile<MT1, NT1, KS1, EPI1, P>(a1, id, red);
-  else rows_tile<MT2, NT2, KS2, EPI2, P>(a2, id - a1.grid, red);
+  if (id < a1.grid) rows_tile<MT1, NT1, KS1, EPI1, P>(a1, id, reinterpret_cast<char *>(lds));
+  else rows_tile<MT2, NT2, KS2, EPI2, P>(a2, id - a1.grid, reinterpret_cast<char *>(lds));
 }
 
 // The decoder's two output projections into one output tile (no reference
@@ -234,6 +287,11 @@ struct DualArgs {
 
 template <int MT, int NT, int KS, bool GATE, int P>
 __global__ void __launch_bounds__(512) linear_rows_dual_kernel(DualArgs a) {
+  // per wave: both products' partials [2][MT * NT][64] f32x4, or before them the staged rows
+  constexpr bool XS = x_staged<MT, KS, P>();
+  constexpr int WL = 2 * MT * NT * 1024 > (XS ? KS * MT * 2048 : 0) ? 2 * MT * NT * 1024 : KS * MT * 2048;
+  __shared__ f32x4 lds_[kWaves * WL / 16];
+  char *lds = reinterpret_cast<char *>(lds_);
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r16 = lane & 15, kq = lane >> 4;
   constexpr int kCols = 16 * NT;
@@ -256,6 +314,16 @@ __global__ void __launch_bounds__(512) linear_rows_dual_kernel(DualArgs a) {
     const int row = min(mt * 16 + r16, rows - 1);
     xo1[mt] = static_cast<uint32_t>((row * a.x1_rs + kq * 8 * P) * 2);
     xo2[mt] = static_cast<uint32_t>((row * a.x2_rs + kq * 8 * P) * 2);
+  }
+  char *wlds = lds + wv * WL;  // this wave's LDS region
+  uint32_t xso1[XS ? 2 * MT : 1], xso2[XS ? 2 * MT : 1];
+  if constexpr (XS) {
+#pragma unroll
+    for (int g8 = 0; g8 < 2 * MT; ++g8) {
+      const int rl = 8 * g8 + (lane >> 3), row = min(rl, rows - 1), ch = 8 * ((lane & 7) ^ (rl & 7));
+      xso1[g8] = static_cast<uint32_t>((row * a.x1_rs + ch) * 2);
+      xso2[g8] = static_cast<uint32_t>((row * a.x2_rs + ch) * 2);
+    }
   }
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
@@ -305,15 +373,33 @@ __global__ void __launch_bounds__(512) linear_rows_dual_kernel(DualArgs a) {
       const uint32_t soff = v < nv ? static_cast<uint32_t>(first ? a0 + v : b0 + v - c1) * (64u * P) : 0x80000000u;
       // pick the operand, then load once (a select between two loads would issue both)
       const buf_t xb = first ? xb1 : xb2, wb = first ? wb1 : wb2;
+      if constexpr (XS) {
+#pragma unroll
+        for (int g8 = 0; g8 < 2 * MT; ++g8)
+          x_stage(xb, wlds + (c * MT * 16 + 8 * g8) * 128, first ? xso1[g8] : xso2[g8], soff);
+      }
 #pragma unroll
       for (int j = 0; j < P; ++j) {
+        if constexpr (!XS) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) A[c][j][mt] = ld8(xb, (first ? xo1[mt] : xo2[mt]) + 16 * j, soff);
+          for (int mt = 0; mt < MT; ++mt) A[c][j][mt] = ld8(xb, (first ? xo1[mt] : xo2[mt]) + 16 * j, soff);
+        }
 #pragma unroll
         for (int t = 0; t < NT; ++t) B[c][j][t] = ld8(wb, (first ? wo1[t] : wo2[t]) + 16 * j, soff);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (XS) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the staged rows have landed
+#pragma unroll
+      for (int c = 0; c < KS; ++c)
+#pragma unroll
+        for (int j = 0; j < P; ++j)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            A[c][j][mt] = *reinterpret_cast<const bf16x8 *>(wlds + (c * MT * 16 + 16 * mt + r16) * 128 +
+                                                            ((2 * kq + j) ^ (r16 & 7)) * 16);
+    }
 #pragma unroll
     for (int c = 0; c < KS; ++c) {
       // steps past the range add zeros to product 2, which changes nothing
@@ -330,22 +416,26 @@ __global__ void __launch_bounds__(512) linear_rows_dual_kernel(DualArgs a) {
     }
   }
 
-  __shared__ f32x4 red[kWaves][2][MT * NT][64];
+  // partials of wave w, product u at lds + w * WL: [u][tile][lane] (over the wave's own
+  // staged rows, whose reads are done)
+  auto red = [&](int w, int u, int tile, int l) -> f32x4 & {
+    return reinterpret_cast<f32x4 *>(lds + w * WL)[(u * MT * NT + tile) * 64 + l];
+  };
 #pragma unroll
   for (int u = 0; u < 2; ++u)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int t = 0; t < NT; ++t) red[wv][u][mt * NT + t][lane] = acc[u][mt][t];
+      for (int t = 0; t < NT; ++t) red(wv, u, mt * NT + t, lane) = acc[u][mt][t];
   __syncthreads();
   const int p = threadIdx.x;
   if (p >= MT * NT * 64) return;
   const int l = p & 63, tv = (p >> 6) % NT, mt = (p >> 6) / NT;
-  f32x4 v1 = red[0][0][mt * NT + tv][l], v2 = red[0][1][mt * NT + tv][l];
+  f32x4 v1 = red(0, 0, mt * NT + tv, l), v2 = red(0, 1, mt * NT + tv, l);
 #pragma unroll
   for (int w = 1; w < kWaves; ++w) {
-    v1 += red[w][0][mt * NT + tv][l];
-    v2 += red[w][1][mt * NT + tv][l];
+    v1 += red(w, 0, mt * NT + tv, l);
+    v2 += red(w, 1, mt * NT + tv, l);
   }
   const int col = n0 + 16 * tv + (l & 15);
   if (col >= a.N) return;
