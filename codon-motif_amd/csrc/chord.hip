@@ -816,19 +816,27 @@ __global__ void __launch_bounds__(256) chord_decode_mfma_kernel(ChordArgs a) {
   const buf_t vbuf = make_buf(vp, k_hi > 0 ? static_cast<uint32_t>(((k_hi - 1) * a.v_st + kD) * 2) : 0u);
 
   __shared__ __attribute__((aligned(16))) bf16_t sV[4][32 * kVRow];
-  bf16_t *myV = sV[w];
+  // per wave: the step's 32 K rows (128 bytes each, 16-byte chunks XOR-swizzled by row),
+  // filled by buffer-to-LDS loads of whole rows, 8 rows per instruction (the operand
+  // layout would read 16 rows x 64 bytes per instruction: half of each line)
+  __shared__ __attribute__((aligned(16))) bf16_t sKs[4][32 * 64];
+  bf16_t *myV = sV[w], *myK = sKs[w];
 
   struct Stage {
-    uint4 k[2][2];   // [tile][piece]
     uint4 v[4];      // V rows 8 r + lane / 8, features 8 (lane % 8)
   };
-  auto load_stage = [&](int n0, Stage &st) {
+  // K: instruction i, lane l: row 8 i + l / 8, physical chunk l % 8 = logical chunk
+  // (features 8 c .. 8 c + 7) c = (l % 8) ^ (row % 8)
+  uint32_t kdo[4];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const uint32_t off = static_cast<uint32_t>(((n0 + 16 * t + c16) * a.k_st + 16 * g) * 2);
-      st.k[t][0] = buf_ld16_nt(kbuf, off);
-      st.k[t][1] = buf_ld16_nt(kbuf, off + 16);
-    }
+  for (int i = 0; i < 4; ++i) {
+    const int r = 8 * i + (lane >> 3);
+    kdo[i] = static_cast<uint32_t>((r * a.k_st + 8 * ((lane & 7) ^ (r & 7))) * 2);
+  }
+  auto load_stage = [&](int n0, Stage &st) {
+    const uint32_t ks = static_cast<uint32_t>(n0 * a.k_st * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) buf_ld16_lds<2>(kbuf, myK + 8 * i * 64, kdo[i], ks);
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       st.v[r] = buf_ld16_nt(vbuf, static_cast<uint32_t>(((n0 + 8 * r + (lane >> 3)) * a.v_st + 8 * (lane & 7)) * 2));
@@ -843,6 +851,16 @@ __global__ void __launch_bounds__(256) chord_decode_mfma_kernel(ChordArgs a) {
   Stage cur;
   if (n0 < k_hi) load_stage(n0, cur);
   for (; n0 < k_hi; n0 += 4 * 32) {
+    // this step's K rows have landed in LDS (and its V rows in registers): operands out,
+    // then the buffer takes the next step's rows
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    uint4 kop[2][2];  // [tile][piece]: key 16 t + c16, features 16 g + 8 piece .. + 7
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int pc = 0; pc < 2; ++pc)
+        kop[t][pc] = *reinterpret_cast<const uint4 *>(myK + (16 * t + c16) * 64 + 8 * ((2 * g + pc) ^ (c16 & 7)));
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     Stage nxt;
     load_stage(n0 + 4 * 32, nxt);
     __builtin_amdgcn_sched_barrier(0);
@@ -855,8 +873,8 @@ __global__ void __launch_bounds__(256) chord_decode_mfma_kernel(ChordArgs a) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
-      sacc = mma16(__builtin_bit_cast(bf16x8, cur.k[t][0]), qb[0], sacc);
-      sacc = mma16(__builtin_bit_cast(bf16x8, cur.k[t][1]), qb[1], sacc);
+      sacc = mma16(__builtin_bit_cast(bf16x8, kop[t][0]), qb[0], sacc);
+      sacc = mma16(__builtin_bit_cast(bf16x8, kop[t][1]), qb[1], sacc);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int key = n0 + 16 * t + 4 * g + i;
@@ -911,6 +929,7 @@ __global__ void __launch_bounds__(256) chord_decode_mfma_kernel(ChordArgs a) {
     }
     cur = nxt;
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last (empty) K fill has landed
 
   // row sum over the 4 lanes of a row
   lsum += __shfl_xor(lsum, 16, 64);

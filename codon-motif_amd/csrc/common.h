@@ -79,6 +79,13 @@ __device__ __forceinline__ uint4 buf_ld16(buf_t r, uint32_t off) {
 __device__ __forceinline__ uint4 buf_ld16_nt(buf_t r, uint32_t off) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
 }
+// 16 bytes per lane straight from a buffer into LDS at dst + 16 * lane (dst the same
+// for the whole wave; offsets past the range write zeros); AUX is the cache policy.
+typedef __attribute__((address_space(3))) void lds_void;
+template <int AUX = 0>
+__device__ __forceinline__ void buf_ld16_lds(buf_t r, void *dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)dst, 16, voff, soff, 0, AUX);
+}
 __device__ __forceinline__ uint2 buf_ld8(buf_t r, uint32_t off) {
   return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
 }

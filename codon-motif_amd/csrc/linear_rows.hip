@@ -96,12 +96,11 @@ constexpr int wave_lds() {
 template <int MT, int NT, int KS, int P>
 constexpr int tile_lds() { return kWaves * wave_lds<MT, NT, KS, P>(); }
 
-typedef __attribute__((address_space(3))) void lds_void;
 // 16 bytes per lane of rows [8 g, 8 g + 8) x one 128-byte k-step of the staged rows
 // (lane l: row 8 g + l / 8, physical chunk l % 8 holding logical chunk (l % 8) ^ (row % 8)),
 // into dst + 16 l
 __device__ __forceinline__ void x_stage(buf_t xb, char *dst, uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(xb, (lds_void *)dst, 16, voff, soff, 0, 0);
+  buf_ld16_lds(xb, dst, voff, soff);
 }
 
 // One workgroup's output tile; `id` is its index among the launch's workgroups for this
