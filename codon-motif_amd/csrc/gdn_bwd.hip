@@ -273,20 +273,31 @@ struct OpPre {
   f32x4 q[kJt];
 };
 
+struct OpScanArgs {
+  const float *M, *Q, *s0;  // [BH][N][DK][DK], [BH][N][DK][Dv], [BH][DK][Dv] or null
+  float *rec, *s_out;       // [BH][N][DK][Dv], [BH][DK][Dv]
+  int N, Dv, BH, rev;
+};
+template <int DK> constexpr int opscan_ms() { return DK + 4; }  // LDS row stride (floats) of M and S^T
+// workgroups of one scan: whole groups of column-group workgroups per XCD
+inline int opscan_blocks(int BH, int Dv) { return (BH + kXcds - 1) / kXcds * kXcds * (Dv / kCols); }
+
+// One scan on workgroup `id` of its launch range, with the caller's LDS: sM [2][DK * MS]
+// and sS [2][16 * MS] floats.
 template <int DK, bool TRANS>
-__global__ void __launch_bounds__(256) gdn_opscan_f32_kernel(const float *__restrict__ M, const float *__restrict__ Q,
-                                                             const float *__restrict__ s0, float *__restrict__ rec,
-                                                             float *__restrict__ s_out, int N, int Dv, int BH, int rev) {
-  constexpr int TT = DK / 16, MS = DK + 4;  // row tiles; LDS row stride (floats) of M and S^T
+__device__ __forceinline__ void opscan_body(const OpScanArgs &oa, int id, float (*sM)[DK * opscan_ms<DK>()],
+                                            float (*sS)[kCols * opscan_ms<DK>()]) {
+  constexpr int TT = DK / 16, MS = opscan_ms<DK>();  // row tiles; LDS row stride
   using PR = OpPre<DK>;
-  __shared__ __attribute__((aligned(16))) float sM[2][DK * MS];
-  __shared__ __attribute__((aligned(16))) float sS[2][kCols * MS];
+  const float *__restrict__ M = oa.M, *__restrict__ Q = oa.Q, *__restrict__ s0 = oa.s0;
+  float *__restrict__ rec = oa.rec, *__restrict__ s_out = oa.s_out;
+  const int N = oa.N, Dv = oa.Dv, BH = oa.BH, rev = oa.rev;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int lr = lane & 15, lq = lane >> 4;
   // linear id L on XCD L % 8: slot L / 8 of that XCD holds column group slot % ncg of
   // batch.head 8 (slot / ncg) + L % 8 (the grid is padded to whole groups per XCD)
-  const int ncg = Dv / kCols, slot = blockIdx.x / kXcds;
-  const int bh = (slot / ncg) * kXcds + blockIdx.x % kXcds, v0 = (slot % ncg) * kCols;
+  const int ncg = Dv / kCols, slot = id / kXcds;
+  const int bh = (slot / ncg) * kXcds + id % kXcds, v0 = (slot % ncg) * kCols;
   if (bh >= BH) return;
   const size_t mstride = static_cast<size_t>(DK) * DK, qstride = static_cast<size_t>(DK) * Dv;
   const float *Mb = M + static_cast<size_t>(bh) * N * mstride;
@@ -391,6 +402,25 @@ __global__ void __launch_bounds__(256) gdn_opscan_f32_kernel(const float *__rest
   }
 }
 
+template <int DK, bool TRANS>
+__global__ void __launch_bounds__(256) gdn_opscan_f32_kernel(OpScanArgs oa) {
+  __shared__ __attribute__((aligned(16))) float sM[2][DK * opscan_ms<DK>()];
+  __shared__ __attribute__((aligned(16))) float sS[2][kCols * opscan_ms<DK>()];
+  opscan_body<DK, TRANS>(oa, blockIdx.x, sM, sS);
+}
+
+// Both scans of the backward in one launch (they are independent: the reverse scan needs
+// only A and G): workgroups [0, g1) walk the forward scan, the rest the reverse one (A
+// read transposed), so the two serial chains run side by side.
+template <int DK>
+__global__ void __launch_bounds__(256) gdn_opscan_pair_f32_kernel(OpScanArgs fwd, OpScanArgs rev, int g1) {
+  __shared__ __attribute__((aligned(16))) float sM[2][DK * opscan_ms<DK>()];
+  __shared__ __attribute__((aligned(16))) float sS[2][kCols * opscan_ms<DK>()];
+  const int id = blockIdx.x;
+  if (id < g1) opscan_body<DK, false>(fwd, id, sM, sS);
+  else opscan_body<DK, true>(rev, id - g1, sM, sS);
+}
+
 int check_scan_sizes(int BH, int N, int C, int Dk, int Dv, const char *who) {
   if (BH < 0 || N < 0 || C <= 0 || Dk <= 0 || Dv <= 0) return set_error(MOTIF_ERR_INVALID, std::string(who) + ": bad sizes");
   if ((C != 16 && C != 32 && C != 64) || (Dk != 16 && Dk != 32 && Dk != 64 && Dk != 128) || Dv % kCols)
@@ -440,12 +470,35 @@ extern "C" int motif_gdn_opscan_f32(const float *M, const float *Q, const float 
   if (BH == 0) return MOTIF_OK;
   if ((N > 0 && (!M || !Q || !rec)) || !S_out) return set_error(MOTIF_ERR_INVALID, "gdn_opscan_f32: NULL pointer");
   if (reinterpret_cast<uintptr_t>(M) & 15) return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_opscan_f32: M needs 16-byte alignment");
-  const dim3 grid((BH + kXcds - 1) / kXcds * kXcds * (Dv / kCols)), block(256);
+  const dim3 grid(opscan_blocks(BH, Dv)), block(256);
   hipStream_t s = static_cast<hipStream_t>(stream);
-#define MOTIF_OPSCAN(D, T) gdn_opscan_f32_kernel<D, T><<<grid, block, 0, s>>>(M, Q, S0, rec, S_out, N, Dv, BH, reverse)
+  const OpScanArgs oa{M, Q, S0, rec, S_out, N, Dv, BH, reverse};
+#define MOTIF_OPSCAN(D, T) gdn_opscan_f32_kernel<D, T><<<grid, block, 0, s>>>(oa)
   if (Dk == 16) { if (transpose) MOTIF_OPSCAN(16, true); else MOTIF_OPSCAN(16, false); }
   else if (Dk == 32) { if (transpose) MOTIF_OPSCAN(32, true); else MOTIF_OPSCAN(32, false); }
   else { if (transpose) MOTIF_OPSCAN(64, true); else MOTIF_OPSCAN(64, false); }
 #undef MOTIF_OPSCAN
   return check_launch("gdn_opscan_f32_kernel");
+}
+
+extern "C" int motif_gdn_opscan_pair_f32(const float *A, const float *Hn, const float *S0, float *P, float *S_out,
+                                         const float *G, const float *dS_final, float *dSn, float *dS0, int BH, int N,
+                                         int Dk, int Dv, void *stream) {
+  using namespace motif;
+  if (BH < 0 || N < 0 || Dk <= 0 || Dv <= 0) return set_error(MOTIF_ERR_INVALID, "gdn_opscan_pair_f32: bad sizes");
+  if ((Dk != 16 && Dk != 32 && Dk != 64) || Dv % kCols)
+    return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_opscan_pair_f32: needs Dk in {16, 32, 64} and Dv a multiple of 16");
+  if (BH == 0) return MOTIF_OK;
+  if ((N > 0 && (!A || !Hn || !P || !G || !dSn)) || !S_out || !dS0)
+    return set_error(MOTIF_ERR_INVALID, "gdn_opscan_pair_f32: NULL pointer");
+  if (reinterpret_cast<uintptr_t>(A) & 15)
+    return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_opscan_pair_f32: A needs 16-byte alignment");
+  const int g1 = opscan_blocks(BH, Dv);
+  const dim3 grid(2 * g1), block(256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const OpScanArgs fwd{A, Hn, S0, P, S_out, N, Dv, BH, 0}, rev{A, G, dS_final, dSn, dS0, N, Dv, BH, 1};
+  if (Dk == 16) gdn_opscan_pair_f32_kernel<16><<<grid, block, 0, s>>>(fwd, rev, g1);
+  else if (Dk == 32) gdn_opscan_pair_f32_kernel<32><<<grid, block, 0, s>>>(fwd, rev, g1);
+  else gdn_opscan_pair_f32_kernel<64><<<grid, block, 0, s>>>(fwd, rev, g1);
+  return check_launch("gdn_opscan_pair_f32_kernel");
 }

@@ -84,6 +84,7 @@ _SIGNATURES = {
     'motif_gdn_scan_fwd_f32': ([_P] * 8 + [_I32] * 5 + [_P], _I32),
     'motif_gdn_scan_bwd_f32': ([_P] * 8 + [_I32] * 5 + [_P], _I32),
     'motif_gdn_opscan_f32': ([_P] * 5 + [_I32] * 6 + [_P], _I32),
+    'motif_gdn_opscan_pair_f32': ([_P] * 9 + [_I32] * 4 + [_P], _I32),
     'motif_gdn_bwd_prep_f32': ([_P] * 15 + [_I32] * 5 + [_P], _I32),
     'motif_gdn_bwd_chunk_f32': ([_P] * 16 + [_I32] * 5 + [_P], _I32),
     'motif_chord_bwd_workspace_bytes': ([_I32] * 6, _SZ),

@@ -89,6 +89,22 @@ def opscan(M, Q, S0, reverse, transpose=False):
     return rec, S
 
 
+def opscan_pair(A, Hn, S0, G, dS_final):
+    '''Both operator-form scans in one HIP launch (independent of each other):
+    (P, S_final) of the forward re-scan S <- A_n S + Hn_n from S0 and (dSn, dS0) of the
+    reverse scan gS <- A_n^T gS + G_n from dS_final (either may be None: zeros).'''
+    B, H, N, Dk, Dv = Hn.shape
+    A, Hn, G = (t.float().contiguous() for t in (A, Hn, G))
+    S0, dS_final = (None if t is None else t.float().contiguous() for t in (S0, dS_final))
+    f = lambda *shape: torch.empty(B, H, *shape, dtype=torch.float32, device=Hn.device)
+    P, S, dSn, dS0 = f(N, Dk, Dv), f(Dk, Dv), f(N, Dk, Dv), f(Dk, Dv)
+    rc = _lib.lib().motif_gdn_opscan_pair_f32(A.data_ptr(), Hn.data_ptr(), _lib.ptr(S0), P.data_ptr(), S.data_ptr(),
+                                              G.data_ptr(), _lib.ptr(dS_final), dSn.data_ptr(), dS0.data_ptr(),
+                                              B * H, N, Dk, Dv, _lib.stream_ptr(Hn.device))
+    _lib.check(rc, 'motif_gdn_opscan_pair_f32')
+    return P, S, dSn, dS0
+
+
 def scan_operators(kc, W, U, gam, dP, dX):
     '''The per-chunk affine operators of both scans, for all chunks at once (fp32 batched
     products): A = e^{gamma_C} I - Kd^T W, H = Kd^T U, G = dP - W^T dX, Kd = k e^{gamma_C - gamma}.'''
@@ -220,11 +236,10 @@ def _backward_kernels(q, k, v, beta, g, S0, do, dS_fin, C):
     qc, kc, vc, doc = (_chunks(t, C, pad).contiguous() for t in (q, k, v, do))
     bc, gc = (_chunks(t, C, pad).contiguous() for t in (beta, g))
     W, U, gam, T, dX, A, Hn, G = bwd_prep(qc, kc, vc, bc, gc, doc, operators=True)
-    P, _ = opscan(A, Hn, S0, reverse=False)
+    P, _, dSn, dS0 = opscan_pair(A, Hn, S0, G, dS_fin)
     # the residuals X_n = U_n - W_n P_n, all chunks in one batched product
     X = torch.baddbmm(U.reshape(-1, *U.shape[-2:]), W.reshape(-1, *W.shape[-2:]), P.reshape(-1, *P.shape[-2:]),
                       alpha=-1.0).view_as(U)
-    dSn, dS0 = opscan(A, G, dS_fin, reverse=True, transpose=True)
     dq, dk, dv, dbeta, dg = bwd_chunk(qc, kc, vc, bc, gam, T, P, X, dSn, doc, dX)
     return (_back(dq, q, L), _back(dk, k, L), _back(dv, v, L), _back(dbeta, beta, L), _back(dg, g, L),
             None if S0 is None else dS0.to(S0.dtype))

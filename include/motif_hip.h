@@ -128,6 +128,16 @@ int motif_gdn_scan_bwd_f32(const float *k, const float *W, const float *g, const
 int motif_gdn_opscan_f32(const float *M, const float *Q, const float *S0, float *rec, float *S_out, int BH, int N,
                          int Dk, int Dv, int reverse, int transpose, void *stream);
 /*
+ * Both operator-form scans of the backward in one launch (they are independent): the
+ * forward re-scan S <- A_n S + Hn_n from S0 (NULL: zeros), writing P [BH,N,Dk,Dv] and
+ * S_out, side by side with the reverse scan gS <- A_n^T gS + G_n from dS_final (NULL:
+ * zeros), writing dSn [BH,N,Dk,Dv] and dS0 -- motif_gdn_opscan_f32 forward and reverse
+ * (transpose) as one launch; same operands and limits.
+ */
+int motif_gdn_opscan_pair_f32(const float *A, const float *Hn, const float *S0, float *P, float *S_out, const float *G,
+                              const float *dS_final, float *dSn, float *dS0, int BH, int N, int Dk, int Dv,
+                              void *stream);
+/*
  * Chunk backward, the per-chunk terms before the scans (fp32).  Inputs are chunked and
  * zero-padded: q, k [BH,N,C,Dk], v, dout [BH,N,C,Dv], beta, g [BH,N,C].  Writes
  * gam = cumsum(g) per chunk [BH,N,C], T = (I + strict(beta k k^T * D))^{-1} [BH,N,C,C],

@@ -84,7 +84,7 @@ def test_scans_match_loops(N, C, Dk, Dv):
 def test_operator_scans_match_loops(N, Dk, Dv):
     '''The operator-form scans (motif_gdn_opscan_f32 with the per-chunk operators formed
     beforehand) against the same defining loops as the direct scans.'''
-    from motif.ops.gdn_grad import opscan, scan_operators
+    from motif.ops.gdn_grad import opscan, opscan_pair, scan_operators
     g0 = torch.Generator().manual_seed(N * 11 + Dv)
     B, H, C = 2, 3, 64
     k = torch.nn.functional.normalize(torch.randn(B, H, N, C, Dk, generator=g0), dim=-1)
@@ -109,6 +109,9 @@ def test_operator_scans_match_loops(N, Dk, Dv):
     rdSn, rdS0 = _scan_bwd_ref(*(t.double() for t in (k, W, g, dX, dP, dS)))
     _close(dSn, rdSn, 'dSn')
     _close(dS0, rdS0, 'dS0')
+    P2, S2, dSn3, dS03 = opscan_pair(A, Hn, S0.to(DEV), G, dS.to(DEV))   # both scans in one launch
+    for name, x, y in (('P', P2, P), ('S', S2, S), ('dSn', dSn3, dSn), ('dS0', dS03, dS0)):
+        assert torch.equal(x, y), name
     P0, S00 = opscan(A, Hn, None, reverse=False)   # zero initial state
     rP0, rS00, _ = _scan_fwd_ref(*(t.double() for t in (k, W, U, g, torch.zeros_like(S0))))
     _close(P0, rP0, 'P (S0 = 0)')
