@@ -61,6 +61,7 @@ struct BwdChunkArgs {
   const float *P, *X, *dSn;                 // the scans' prefix states, residuals, state gradients
   const float *dout, *dX;                   // do, and the prep kernel's dX
   float *dq, *dk, *dv, *dbeta, *dg;
+  const float *W, *U;                       // with X NULL: the residuals X = U - W P formed here
 };
 
 // rows [C][cols] of a chunk (global, float4 loads) into LDS rows of stride ld
@@ -280,10 +281,21 @@ __global__ void __launch_bounds__(256) gdn_bwd_chunk_kernel(BwdChunkArgs a) {
   for (int j = 0; j < DV / 64; ++j) {
     const int e0 = 64 * j;
     load_rows<64>(b0, LD, a.dout + cb * C * DV, DV, e0);
-    load_rows<64>(b1, LD, a.X + cb * C * DV, DV, e0);
+    load_rows<64>(b1, LD, (a.X ? a.X : a.U) + cb * C * DV, DV, e0);
     load_rows<64>(b2, LD, a.P + cb * DK * DV, DV, e0);
     load_rows<64>(b3, LD, a.dSn + cb * DK * DV, DV, e0);
     load_rows<64>(b4, LD, a.v + cb * C * DV, DV, e0);
+    if (!a.X) {  // X = U - W P for these columns: W over b5 (free until dxt), U in b1
+      load_rows<DK>(b5, LD, a.W + cb * C * DK, DK, 0);
+      __syncthreads();
+      f32x16 wp = {};
+      mm<DK>(wp, [&](int m, int k) { return b5[(r0 + m) * LD + k]; }, [&](int k, int n) { return b2[k * LD + c0 + n]; });
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {  // each wave rewrites only its own tile of b1
+        const int R = r0 + acc_row(r, h), Nc = c0 + i;
+        b1[R * LD + Nc] -= wp[r];
+      }
+    }
     float dxo[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) dxo[r] = a.dX[(cb * C + r0 + acc_row(r, h)) * DV + e0 + c0 + i];
@@ -510,17 +522,18 @@ extern "C" int motif_gdn_bwd_prep_f32(const float *q, const float *k, const floa
 extern "C" int motif_gdn_bwd_chunk_f32(const float *q, const float *k, const float *v, const float *beta,
                                        const float *gam, const float *T, const float *P, const float *X,
                                        const float *dSn, const float *dout, const float *dX, float *dq, float *dk,
-                                       float *dv, float *dbeta, float *dg, int BH, int N, int C, int Dk, int Dv,
-                                       void *stream) {
+                                       float *dv, float *dbeta, float *dg, const float *W, const float *U, int BH,
+                                       int N, int C, int Dk, int Dv, void *stream) {
   using namespace motif;
   if (int rc = check_bwd_sizes(BH, N, C, Dk, Dv, "gdn_bwd_chunk_f32")) return rc;
   const int64_t blocks = static_cast<int64_t>(BH) * N;
   if (blocks == 0) return MOTIF_OK;
-  if (!q || !k || !v || !beta || !gam || !T || !P || !X || !dSn || !dout || !dX || !dq || !dk || !dv || !dbeta || !dg)
+  if (!q || !k || !v || !beta || !gam || !T || !P || !dSn || !dout || !dX || !dq || !dk || !dv || !dbeta || !dg ||
+      (!X && (!W || !U)))
     return set_error(MOTIF_ERR_INVALID, "gdn_bwd_chunk_f32: NULL pointer");
-  if (!aligned16({q, k, v, T, P, X, dSn, dout}))
+  if (!aligned16({q, k, v, T, P, X, dSn, dout, W, U}))
     return set_error(MOTIF_ERR_UNSUPPORTED, "gdn_bwd_chunk_f32: the row operands need 16-byte alignment");
-  BwdChunkArgs a{q, k, v, beta, gam, T, P, X, dSn, dout, dX, dq, dk, dv, dbeta, dg};
+  BwdChunkArgs a{q, k, v, beta, gam, T, P, X, dSn, dout, dX, dq, dk, dv, dbeta, dg, X ? nullptr : W, X ? nullptr : U};
   hipStream_t s = static_cast<hipStream_t>(stream);
   const size_t smem = chunk_smem();
   if (Dv == 64) {

@@ -86,7 +86,7 @@ _SIGNATURES = {
     'motif_gdn_opscan_f32': ([_P] * 5 + [_I32] * 6 + [_P], _I32),
     'motif_gdn_opscan_pair_f32': ([_P] * 9 + [_I32] * 4 + [_P], _I32),
     'motif_gdn_bwd_prep_f32': ([_P] * 15 + [_I32] * 5 + [_P], _I32),
-    'motif_gdn_bwd_chunk_f32': ([_P] * 16 + [_I32] * 5 + [_P], _I32),
+    'motif_gdn_bwd_chunk_f32': ([_P] * 18 + [_I32] * 5 + [_P], _I32),
     'motif_chord_bwd_workspace_bytes': ([_I32] * 6, _SZ),
     'motif_chord_bwd': (
         _T4 * 5 + [_P] * 5 + [_P, _I64, _I64] + _T4 * 3 + [_P] + [_I32] * 7 + [_F32, _F32]

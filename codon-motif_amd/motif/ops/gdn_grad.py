@@ -147,18 +147,19 @@ def bwd_prep(qc, kc, vc, bc, gc, doc, operators=False):
     return W, U, gam, T, dP, dX
 
 
-def bwd_chunk(qc, kc, vc, bc, gam, T, P, X, dSn, doc, dX):
+def bwd_chunk(qc, kc, vc, bc, gam, T, P, X, dSn, doc, dX, W=None, U=None):
     '''Per-chunk gradients after the scans on the HIP kernel: (dq, dk, dv, dbeta, dg),
-    chunked [B,H,N,C,...] fp32.'''
+    chunked [B,H,N,C,...] fp32.  With X None the residuals X = U - W P are formed in the
+    kernel from the prep's W and U.'''
     B, H, N, C, Dk = kc.shape
     Dv = vc.shape[-1]
     dq, dk, dv = torch.empty_like(qc), torch.empty_like(kc), torch.empty_like(vc)
     dbeta, dg = torch.empty_like(bc), torch.empty_like(bc)
     rc = _lib.lib().motif_gdn_bwd_chunk_f32(qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), bc.data_ptr(),
-                                            gam.data_ptr(), T.data_ptr(), P.data_ptr(), X.data_ptr(),
+                                            gam.data_ptr(), T.data_ptr(), P.data_ptr(), _lib.ptr(X),
                                             dSn.data_ptr(), doc.data_ptr(), dX.data_ptr(), dq.data_ptr(),
                                             dk.data_ptr(), dv.data_ptr(), dbeta.data_ptr(), dg.data_ptr(),
-                                            B * H, N, C, Dk, Dv, _lib.stream_ptr(kc.device))
+                                            _lib.ptr(W), _lib.ptr(U), B * H, N, C, Dk, Dv, _lib.stream_ptr(kc.device))
     _lib.check(rc, 'motif_gdn_bwd_chunk_f32')
     return dq, dk, dv, dbeta, dg
 
@@ -237,10 +238,8 @@ def _backward_kernels(q, k, v, beta, g, S0, do, dS_fin, C):
     bc, gc = (_chunks(t, C, pad).contiguous() for t in (beta, g))
     W, U, gam, T, dX, A, Hn, G = bwd_prep(qc, kc, vc, bc, gc, doc, operators=True)
     P, _, dSn, dS0 = opscan_pair(A, Hn, S0, G, dS_fin)
-    # the residuals X_n = U_n - W_n P_n, all chunks in one batched product
-    X = torch.baddbmm(U.reshape(-1, *U.shape[-2:]), W.reshape(-1, *W.shape[-2:]), P.reshape(-1, *P.shape[-2:]),
-                      alpha=-1.0).view_as(U)
-    dq, dk, dv, dbeta, dg = bwd_chunk(qc, kc, vc, bc, gam, T, P, X, dSn, doc, dX)
+    # (the residuals X_n = U_n - W_n P_n are formed inside the per-chunk kernel)
+    dq, dk, dv, dbeta, dg = bwd_chunk(qc, kc, vc, bc, gam, T, P, None, dSn, doc, dX, W=W, U=U)
     return (_back(dq, q, L), _back(dk, k, L), _back(dv, v, L), _back(dbeta, beta, L), _back(dg, g, L),
             None if S0 is None else dS0.to(S0.dtype))
 

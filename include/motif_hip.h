@@ -159,15 +159,17 @@ int motif_gdn_bwd_prep_f32(const float *q, const float *k, const float *v, const
  * Chunk backward, the per-chunk gradients after the scans (fp32): from the prep's gam, T
  * and dX, the forward re-scan's P [BH,N,Dk,Dv] and X [BH,N,C,Dv] and the reverse scan's
  * dSn [BH,N,Dk,Dv], writes dq, dk [BH,N,C,Dk], dv [BH,N,C,Dv], dbeta, dg [BH,N,C]
- * (chunked, padded rows included).  Replaces the reference's
+ * (chunked, padded rows included).  With X NULL the residuals X = U - W P are formed in
+ * the kernel from the prep's W [BH,N,C,Dk] and U [BH,N,C,Dv] (else W, U may be NULL).
+ * Replaces the reference's
  * _PrepareChunksFunction.backward (motif/ops/gated_deltanet.py:180-260), the per-chunk
  * products of _FusedScanFunction.backward (:742-765) and the output combination's
  * gradient.  Same size limits.
  */
 int motif_gdn_bwd_chunk_f32(const float *q, const float *k, const float *v, const float *beta, const float *gam,
                             const float *T, const float *P, const float *X, const float *dSn, const float *dout,
-                            const float *dX, float *dq, float *dk, float *dv, float *dbeta, float *dg, int BH, int N,
-                            int C, int Dk, int Dv, void *stream);
+                            const float *dX, float *dq, float *dk, float *dv, float *dbeta, float *dg, const float *W,
+                            const float *U, int BH, int N, int C, int Dk, int Dv, void *stream);
 
 /*
  * motif_gdn_chunk_fwd with the layer's output norm fused into the output pass:

@@ -256,3 +256,25 @@ def test_prep_scan_operators_equal_torch_products(dv):
     _close(A, rA, 'A', 1e-5)
     _close(Hn, rH, 'Hn', 1e-5)
     _close(G, rG, 'G', 1e-5)
+
+
+def test_chunk_kernel_forms_residuals_itself():
+    '''The per-chunk gradient kernel given the residuals X = U - W P against the same kernel
+    forming them from W, U and P itself: equal up to the fp32 rounding of X.'''
+    from motif.ops.gdn_grad import _chunks, bwd_chunk, bwd_prep, opscan_pair
+    B, H, L, dv = 1, 2, 250, 128
+    q, k, v, b, g = (t.to(DEV) for t in gdn_inputs(B, H, L, 64, dv, seed=5))
+    g0 = torch.Generator().manual_seed(5)
+    do = torch.randn(B, H, L, dv, generator=g0).to(DEV)
+    S0 = (torch.randn(B, H, 64, dv, generator=g0) * 0.1).to(DEV)
+    dS = (torch.randn(B, H, 64, dv, generator=g0) * 0.1).to(DEV)
+    pad = (64 - L % 64) % 64
+    qc, kc, vc, doc = (_chunks(t, 64, pad).contiguous() for t in (q, k, v, do))
+    bc, gc = (_chunks(t, 64, pad).contiguous() for t in (b, g))
+    W, U, gam, T, dX, A, Hn, G = bwd_prep(qc, kc, vc, bc, gc, doc, operators=True)
+    P, _, dSn, _ = opscan_pair(A, Hn, S0, G, dS)
+    X = U - torch.matmul(W, P)
+    given = bwd_chunk(qc, kc, vc, bc, gam, T, P, X, dSn, doc, dX)
+    formed = bwd_chunk(qc, kc, vc, bc, gam, T, P, None, dSn, doc, dX, W=W, U=U)
+    for name, x, y in zip(('dq', 'dk', 'dv', 'dbeta', 'dg'), formed, given):
+        _close(x, y, name, 1e-5)
