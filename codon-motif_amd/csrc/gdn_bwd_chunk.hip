@@ -190,10 +190,9 @@ __global__ void __launch_bounds__(256) gdn_bwd_prep_kernel(BwdPrepArgs a) {
   }
   for (int e = tid; e < C * C; e += 256) a.T[cb * C * C + e] = sT[(e >> 6) * LD + (e & 63)];
   __syncthreads();  // Attn complete; the reads of T, V and Q above are done
-  // With the scan operators requested: W over the T rows, U over the V rows, and
-  // ek = e^{gamma_C - gamma} in the inverse's scratch (all dead here).
+  // With the scan operators requested: W over the T rows, U over the V rows and the
+  // decayed keys Kd = k e^{gamma_C - gamma} over the Q rows (all dead here).
   const bool ops = a.A != nullptr;
-  float *sEk = sXs;
   if (ops) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) sT[(r0 + acc_row(r, h)) * LD + c0 + i] = wreg[r];
@@ -201,7 +200,10 @@ __global__ void __launch_bounds__(256) gdn_bwd_prep_kernel(BwdPrepArgs a) {
     for (int j = 0; j < DV / 64; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) sV[(r0 + acc_row(r, h)) * LV + c0 + 64 * j + i] = ureg[j][r];
-    if (w == 0) sEk[lane] = __expf(sGam[C - 1] - sGam[lane]);
+    for (int e = tid; e < C * DK; e += 256) {
+      const int rr = e / DK, cc = e % DK;
+      sQ[rr * LD + cc] = sK[rr * LD + cc] * __expf(sGam[C - 1] - sGam[rr]);
+    }
   }
   // dX = Attn^T do
   f32x16 dxreg[DV / 64];
@@ -216,13 +218,13 @@ __global__ void __launch_bounds__(256) gdn_bwd_prep_kernel(BwdPrepArgs a) {
   if (!ops) return;
   // The per-chunk operators of the operator-form scans (gdn_bwd.hip):
   //   A = e^{gamma_C} I - Kd^T W,  H = Kd^T U,  G = dP - W^T dX,  Kd = k e^{gamma_C - gamma}
-  __syncthreads();  // the reads of do are done; W, U and ek are visible
+  __syncthreads();  // the reads of do are done; W, U and Kd are visible
 #pragma unroll
   for (int j = 0; j < DV / 64; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) sDo[(r0 + acc_row(r, h)) * LV + c0 + 64 * j + i] = dxreg[j][r];
   __syncthreads();  // dX over the do rows
-  auto kdT = [&](int m, int k) { return sK[k * LD + r0 + m] * sEk[k]; };
+  auto kdT = [&](int m, int k) { return sQ[k * LD + r0 + m]; };  // Kd^T
   {
     f32x16 acc = {};
     mm<C>(acc, kdT, [&](int k, int n) { return sT[k * LD + c0 + n]; });
