@@ -47,6 +47,43 @@ __device__ __forceinline__ void mm(f32x16 &acc, FA fa, FB fb) {
   for (int k0 = 0; k0 < K; k0 += 2) acc = mfma32(fa(i, k0 + h), fb(k0 + h, i), acc);
 }
 
+// Two, three or four independent products over the same K in one loop: their MFMA chains
+// interleave, so each waits on its operand reads less (one wave per SIMD here).  Each
+// accumulator sums in the same order as mm alone.
+template <int K, typename FA1, typename FB1, typename FA2, typename FB2>
+__device__ __forceinline__ void mm2(f32x16 &c1, FA1 a1, FB1 b1, f32x16 &c2, FA2 a2, FB2 b2) {
+  const int lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
+#pragma unroll 8
+  for (int k0 = 0; k0 < K; k0 += 2) {
+    c1 = mfma32(a1(i, k0 + h), b1(k0 + h, i), c1);
+    c2 = mfma32(a2(i, k0 + h), b2(k0 + h, i), c2);
+  }
+}
+template <int K, typename FA1, typename FB1, typename FA2, typename FB2, typename FA3, typename FB3>
+__device__ __forceinline__ void mm3(f32x16 &c1, FA1 a1, FB1 b1, f32x16 &c2, FA2 a2, FB2 b2, f32x16 &c3, FA3 a3,
+                                    FB3 b3) {
+  const int lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
+#pragma unroll 4
+  for (int k0 = 0; k0 < K; k0 += 2) {
+    c1 = mfma32(a1(i, k0 + h), b1(k0 + h, i), c1);
+    c2 = mfma32(a2(i, k0 + h), b2(k0 + h, i), c2);
+    c3 = mfma32(a3(i, k0 + h), b3(k0 + h, i), c3);
+  }
+}
+template <int K, typename FA1, typename FB1, typename FA2, typename FB2, typename FA3, typename FB3, typename FA4,
+          typename FB4>
+__device__ __forceinline__ void mm4(f32x16 &c1, FA1 a1, FB1 b1, f32x16 &c2, FA2 a2, FB2 b2, f32x16 &c3, FA3 a3,
+                                    FB3 b3, f32x16 &c4, FA4 a4, FB4 b4) {
+  const int lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
+#pragma unroll 4
+  for (int k0 = 0; k0 < K; k0 += 2) {
+    c1 = mfma32(a1(i, k0 + h), b1(k0 + h, i), c1);
+    c2 = mfma32(a2(i, k0 + h), b2(k0 + h, i), c2);
+    c3 = mfma32(a3(i, k0 + h), b3(k0 + h, i), c3);
+    c4 = mfma32(a4(i, k0 + h), b4(k0 + h, i), c4);
+  }
+}
+
 // Row of accumulator register r for lane half h, relative to the tile: 8 (r / 4) + 4 h + r % 4.
 __device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
 
@@ -168,10 +205,6 @@ __global__ void __launch_bounds__(256) gdn_bwd_prep_kernel(BwdPrepArgs a) {
   }
   // W = T (beta e^gamma k)
   f32x16 wreg = {};
-  mm<C>(wreg, [&](int m, int k) { return sT[(r0 + m) * LD + k]; },
-        [&](int k, int n) { return sB[k] * sE[k] * sK[k * LD + c0 + n]; });
-#pragma unroll
-  for (int r = 0; r < 16; ++r) a.W[(cb * C + r0 + acc_row(r, h)) * DK + c0 + i] = wreg[r];
   // U = T (beta v), dP = (q e^gamma)^T do: column tiles c0 + 64 j of the dv columns
   f32x16 ureg[DV / 64], dpreg[DV / 64];
 #pragma unroll
@@ -179,8 +212,17 @@ __global__ void __launch_bounds__(256) gdn_bwd_prep_kernel(BwdPrepArgs a) {
     const int n0 = c0 + 64 * j;
     ureg[j] = f32x16{};
     dpreg[j] = f32x16{};
-    mm<C>(ureg[j], [&](int m, int k) { return sT[(r0 + m) * LD + k]; }, [&](int k, int n) { return sB[k] * sV[k * LV + n0 + n]; });
-    mm<C>(dpreg[j], [&](int m, int k) { return sQ[k * LD + r0 + m] * sE[k]; }, [&](int k, int n) { return sDo[k * LV + n0 + n]; });
+    auto ta = [&](int m, int k) { return sT[(r0 + m) * LD + k]; };
+    auto vb = [&](int k, int n) { return sB[k] * sV[k * LV + n0 + n]; };
+    auto qa = [&](int m, int k) { return sQ[k * LD + r0 + m] * sE[k]; };
+    auto db = [&](int k, int n) { return sDo[k * LV + n0 + n]; };
+    if (j == 0) {  // W with the first column tile's products
+      mm3<C>(wreg, ta, [&](int k, int n) { return sB[k] * sE[k] * sK[k * LD + c0 + n]; }, ureg[j], ta, vb, dpreg[j], qa, db);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) a.W[(cb * C + r0 + acc_row(r, h)) * DK + c0 + i] = wreg[r];
+    } else {
+      mm2<C>(ureg[j], ta, vb, dpreg[j], qa, db);
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int R = r0 + acc_row(r, h);
@@ -205,16 +247,23 @@ __global__ void __launch_bounds__(256) gdn_bwd_prep_kernel(BwdPrepArgs a) {
       sQ[rr * LD + cc] = sK[rr * LD + cc] * __expf(sGam[C - 1] - sGam[rr]);
     }
   }
-  // dX = Attn^T do
+  // dX = Attn^T do (both column tiles in one k loop when dv = 128)
   f32x16 dxreg[DV / 64];
-#pragma unroll
-  for (int j = 0; j < DV / 64; ++j) {
-    const int n0 = c0 + 64 * j;
-    dxreg[j] = f32x16{};
-    mm<C>(dxreg[j], [&](int m, int k) { return sA[k * LD + r0 + m]; }, [&](int k, int n) { return sDo[k * LV + n0 + n]; });
-#pragma unroll
-    for (int r = 0; r < 16; ++r) a.dX[(cb * C + r0 + acc_row(r, h)) * DV + n0 + i] = dxreg[j][r];
+  {
+    auto at = [&](int m, int k) { return sA[k * LD + r0 + m]; };
+    dxreg[0] = f32x16{};
+    if constexpr (DV == 128) {
+      dxreg[1] = f32x16{};
+      mm2<C>(dxreg[0], at, [&](int k, int n) { return sDo[k * LV + c0 + n]; },
+             dxreg[1], at, [&](int k, int n) { return sDo[k * LV + c0 + 64 + n]; });
+    } else {
+      mm<C>(dxreg[0], at, [&](int k, int n) { return sDo[k * LV + c0 + n]; });
+    }
   }
+#pragma unroll
+  for (int j = 0; j < DV / 64; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) a.dX[(cb * C + r0 + acc_row(r, h)) * DV + c0 + 64 * j + i] = dxreg[j][r];
   if (!ops) return;
   // The per-chunk operators of the operator-form scans (gdn_bwd.hip):
   //   A = e^{gamma_C} I - Kd^T W,  H = Kd^T U,  G = dP - W^T dX,  Kd = k e^{gamma_C - gamma}
@@ -225,22 +274,25 @@ __global__ void __launch_bounds__(256) gdn_bwd_prep_kernel(BwdPrepArgs a) {
     for (int r = 0; r < 16; ++r) sDo[(r0 + acc_row(r, h)) * LV + c0 + 64 * j + i] = dxreg[j][r];
   __syncthreads();  // dX over the do rows
   auto kdT = [&](int m, int k) { return sQ[k * LD + r0 + m]; };  // Kd^T
-  {
-    f32x16 acc = {};
-    mm<C>(acc, kdT, [&](int k, int n) { return sT[k * LD + c0 + n]; });
-    const float ec = sE[C - 1];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int R = r0 + acc_row(r, h), Nc = c0 + i;
-      a.A[(cb * DK + R) * DK + Nc] = (R == Nc ? ec : 0.f) - acc[r];
-    }
-  }
+  auto wT = [&](int m, int k) { return sT[k * LD + r0 + m]; };   // W^T
 #pragma unroll
   for (int j = 0; j < DV / 64; ++j) {
     const int n0 = c0 + 64 * j;
     f32x16 hacc = {}, gacc = {};
-    mm<C>(hacc, kdT, [&](int k, int n) { return sV[k * LV + n0 + n]; });
-    mm<C>(gacc, [&](int m, int k) { return sT[k * LD + r0 + m]; }, [&](int k, int n) { return sDo[k * LV + n0 + n]; });
+    auto ub = [&](int k, int n) { return sV[k * LV + n0 + n]; };
+    auto xb = [&](int k, int n) { return sDo[k * LV + n0 + n]; };
+    if (j == 0) {  // A with the first column tile's products
+      f32x16 acc = {};
+      mm3<C>(acc, kdT, [&](int k, int n) { return sT[k * LD + c0 + n]; }, hacc, kdT, ub, gacc, wT, xb);
+      const float ec = sE[C - 1];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int R = r0 + acc_row(r, h), Nc = c0 + i;
+        a.A[(cb * DK + R) * DK + Nc] = (R == Nc ? ec : 0.f) - acc[r];
+      }
+    } else {
+      mm2<C>(hacc, kdT, ub, gacc, wT, xb);
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int R = r0 + acc_row(r, h);
@@ -302,11 +354,12 @@ __global__ void __launch_bounds__(256) gdn_bwd_chunk_kernel(BwdChunkArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) dxo[r] = a.dX[(cb * C + r0 + acc_row(r, h)) * DV + e0 + c0 + i];
     __syncthreads();
-    mm<64>(T1, [&](int m, int k) { return b0[(r0 + m) * LD + k]; }, [&](int k, int n) { return b1[(c0 + n) * LD + k]; });
-    mm<64>(T2, [&](int m, int k) { return b0[(r0 + m) * LD + k]; }, [&](int k, int n) { return b2[(c0 + n) * LD + k]; });
-    mm<64>(T3, [&](int m, int k) { return b1[(r0 + m) * LD + k]; }, [&](int k, int n) { return b3[(c0 + n) * LD + k]; });
     f32x16 kds = {};  // k dSn
-    mm<DK>(kds, [&](int m, int k) { return sK[(r0 + m) * LD + k]; }, [&](int k, int n) { return b3[k * LD + c0 + n]; });
+    static_assert(DK == 64, "the four products below share one k loop");
+    mm4<64>(T1, [&](int m, int k) { return b0[(r0 + m) * LD + k]; }, [&](int k, int n) { return b1[(c0 + n) * LD + k]; },
+            T2, [&](int m, int k) { return b0[(r0 + m) * LD + k]; }, [&](int k, int n) { return b2[(c0 + n) * LD + k]; },
+            T3, [&](int m, int k) { return b1[(r0 + m) * LD + k]; }, [&](int k, int n) { return b3[(c0 + n) * LD + k]; },
+            kds, [&](int m, int k) { return sK[(r0 + m) * LD + k]; }, [&](int k, int n) { return b3[k * LD + c0 + n]; });
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int R = r0 + acc_row(r, h), Nc = c0 + i;
@@ -314,10 +367,10 @@ __global__ void __launch_bounds__(256) gdn_bwd_chunk_kernel(BwdChunkArgs a) {
       corr = fmaf(b3[R * LD + Nc], b2[R * LD + Nc], corr);
     }
     __syncthreads();
-    mm<64>(T4, [&](int m, int k) { return b5[(r0 + m) * LD + k]; }, [&](int k, int n) { return b2[(c0 + n) * LD + k]; });
-    mm<64>(T5, [&](int m, int k) { return b5[(r0 + m) * LD + k]; }, [&](int k, int n) { return b4[(c0 + n) * LD + k]; });
     f32x16 dvb = {};  // T^T dxt
-    mm<C>(dvb, [&](int m, int k) { return sT[k * LD + r0 + m]; }, [&](int k, int n) { return b5[k * LD + c0 + n]; });
+    mm3<64>(T4, [&](int m, int k) { return b5[(r0 + m) * LD + k]; }, [&](int k, int n) { return b2[(c0 + n) * LD + k]; },
+            T5, [&](int m, int k) { return b5[(r0 + m) * LD + k]; }, [&](int k, int n) { return b4[(c0 + n) * LD + k]; },
+            dvb, [&](int m, int k) { return sT[k * LD + r0 + m]; }, [&](int k, int n) { return b5[k * LD + c0 + n]; });
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int R = r0 + acc_row(r, h), Nc = c0 + i;
@@ -340,8 +393,8 @@ __global__ void __launch_bounds__(256) gdn_bwd_chunk_kernel(BwdChunkArgs a) {
   }
   __syncthreads();
   f32x16 qk = {}, kk = {};
-  mm<DK>(qk, [&](int m, int k) { return b0[(r0 + m) * LD + k]; }, [&](int k, int n) { return sK[(c0 + n) * LD + k]; });
-  mm<DK>(kk, [&](int m, int k) { return sK[(r0 + m) * LD + k]; }, [&](int k, int n) { return sK[(c0 + n) * LD + k]; });
+  mm2<DK>(qk, [&](int m, int k) { return b0[(r0 + m) * LD + k]; }, [&](int k, int n) { return sK[(c0 + n) * LD + k]; },
+          kk, [&](int m, int k) { return sK[(r0 + m) * LD + k]; }, [&](int k, int n) { return sK[(c0 + n) * LD + k]; });
   f32x16 ddec, G1;  // d/dD (times D) and beta k k^T
   float rowG[16], kdk = 0.f;
 #pragma unroll
@@ -349,50 +402,37 @@ __global__ void __launch_bounds__(256) gdn_bwd_chunk_kernel(BwdChunkArgs a) {
     ddec[r] = T1[r] * qk[r];
     G1[r] = sB[r0 + acc_row(r, h)] * kk[r];
   }
-  {  // dq = dqg e^gamma + dAttn k
-    f32x16 dq = {};
-    mm<C>(dq, [&](int m, int k) { return b1[(r0 + m) * LD + k]; }, [&](int k, int n) { return sK[k * LD + c0 + n]; });
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int R = r0 + acc_row(r, h), Nc = c0 + i;
-      a.dq[(cb * C + R) * DK + Nc] = fmaf(T2[r], sE[R], dq[r]);
-      rowG[r] = T2[r] * b0[R * LD + Nc] * sE[R];
-    }
-  }
-  f32x16 dk = {};  // dAttn^T q + dKd e^{gamma_C - gamma}
-  mm<C>(dk, [&](int m, int k) { return b1[k * LD + r0 + m]; }, [&](int k, int n) { return b0[k * LD + c0 + n]; });
+  // dq = dqg e^gamma + dAttn k;  dk = dAttn^T q + dKd e^{gamma_C - gamma};
+  // dT = dW Z^T + dxt (beta v)^T,  Z = beta e^gamma k  (three independent products)
+  f32x16 dq = {}, dk = {}, tdt = {};
+  mm3<C>(dq, [&](int m, int k) { return b1[(r0 + m) * LD + k]; }, [&](int k, int n) { return sK[k * LD + c0 + n]; },
+         dk, [&](int m, int k) { return b1[k * LD + r0 + m]; }, [&](int k, int n) { return b0[k * LD + c0 + n]; },
+         tdt, [&](int m, int k) { return b2[(r0 + m) * LD + k]; }, [&](int k, int n) { return sK[(c0 + n) * LD + k]; });
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int R = r0 + acc_row(r, h), Nc = c0 + i;
+    a.dq[(cb * C + R) * DK + Nc] = fmaf(T2[r], sE[R], dq[r]);
+    rowG[r] = T2[r] * b0[R * LD + Nc] * sE[R];
     const float t = T3[r] * sDec[R];
     dk[r] += t;
     const float kd = t * sK[R * LD + Nc];
     rowG[r] -= kd;
     kdk += kd;
-  }
-  {  // dT = dW Z^T + dxt (beta v)^T,  Z = beta e^gamma k
-    f32x16 t = {};
-    mm<DK>(t, [&](int m, int k) { return b2[(r0 + m) * LD + k]; }, [&](int k, int n) { return sK[(c0 + n) * LD + k]; });
-#pragma unroll
-    for (int r = 0; r < 16; ++r) b3[(r0 + acc_row(r, h)) * LD + c0 + i] = fmaf(t[r], bcol * ecol, T5[r]);
+    b3[R * LD + Nc] = fmaf(tdt[r], bcol * ecol, T5[r]);
   }
   __syncthreads();
   f32x16 dkb = {};
-  {  // dZ = T^T dW: dkb = dZ e^gamma, d gamma += dZ . Z
-    f32x16 dZ = {};
-    mm<C>(dZ, [&](int m, int k) { return sT[k * LD + r0 + m]; }, [&](int k, int n) { return b2[k * LD + c0 + n]; });
+  {  // dZ = T^T dW: dkb = dZ e^gamma, d gamma += dZ . Z;  Y = dT T^T
+    f32x16 dZ = {}, y = {};
+    mm2<C>(dZ, [&](int m, int k) { return sT[k * LD + r0 + m]; }, [&](int k, int n) { return b2[k * LD + c0 + n]; },
+           y, [&](int m, int k) { return b3[(r0 + m) * LD + k]; }, [&](int k, int n) { return sT[(c0 + n) * LD + k]; });
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int R = r0 + acc_row(r, h), Nc = c0 + i;
       dkb[r] = dZ[r] * sE[R];
       rowG[r] = fmaf(dkb[r] * sB[R], sK[R * LD + Nc], rowG[r]);
+      b4[R * LD + Nc] = y[r];
     }
-  }
-  {  // Y = dT T^T
-    f32x16 y = {};
-    mm<C>(y, [&](int m, int k) { return b3[(r0 + m) * LD + k]; }, [&](int k, int n) { return sT[(c0 + n) * LD + k]; });
-#pragma unroll
-    for (int r = 0; r < 16; ++r) b4[(r0 + acc_row(r, h)) * LD + c0 + i] = y[r];
   }
   __syncthreads();
   float colG = 0.f;
@@ -412,8 +452,8 @@ __global__ void __launch_bounds__(256) gdn_bwd_chunk_kernel(BwdChunkArgs a) {
   }
   __syncthreads();
   // dkb += dG1 k;  dk += dG1^T (beta k) + dkb beta;  dbeta += dkb . k
-  mm<C>(dkb, [&](int m, int k) { return b5[(r0 + m) * LD + k]; }, [&](int k, int n) { return sK[k * LD + c0 + n]; });
-  mm<C>(dk, [&](int m, int k) { return b5[k * LD + r0 + m] * sB[k]; }, [&](int k, int n) { return sK[k * LD + c0 + n]; });
+  mm2<C>(dkb, [&](int m, int k) { return b5[(r0 + m) * LD + k]; }, [&](int k, int n) { return sK[k * LD + c0 + n]; },
+         dk, [&](int m, int k) { return b5[k * LD + r0 + m] * sB[k]; }, [&](int k, int n) { return sK[k * LD + c0 + n]; });
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int R = r0 + acc_row(r, h), Nc = c0 + i;
