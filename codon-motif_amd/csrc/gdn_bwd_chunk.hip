@@ -156,7 +156,9 @@ __global__ void __launch_bounds__(256) gdn_bwd_prep_kernel(BwdPrepArgs a) {
   __syncthreads();
 
   // T = (I - A)^{-1}, unit lower triangular: the 16x16 diagonal blocks by substitution,
-  // then block diagonal d = 1, 2, 3: T_ij = T_ii (sum_{k = j}^{i-1} A_ik T_kj).
+  // the 32x32 diagonal blocks' off-diagonal pieces T_{2p+1,2p} = T_{2p+1,2p+1} A_{2p+1,2p}
+  // T_{2p,2p} (16-wide products per thread), then the lower left 32x32 block
+  // T[32:, :32] = T[32:, 32:] (A[32:, :32] T[:32, :32]) as two 32x32x32 MFMA products.
   if (tid < 64) {
     const int b = tid >> 4, c = tid & 15;
     float x[16];
@@ -175,23 +177,34 @@ __global__ void __launch_bounds__(256) gdn_bwd_prep_kernel(BwdPrepArgs a) {
     if ((c >> 4) > (r >> 4)) sT[r * LD + c] = 0.f;
   }
   __syncthreads();
-  for (int d = 1; d < 4; ++d) {
-    const int nb = 4 - d;
-    for (int e = tid; e < nb * 256; e += 256) {
-      const int bj = e >> 8, rr = (e >> 4) & 15, cc = e & 15, bi = bj + d;
-      float s = 0.f;
-      for (int k = 16 * bj; k < 16 * bi; ++k) s = fmaf(sA[(16 * bi + rr) * LD + k], sT[k * LD + 16 * bj + cc], s);
-      sXs[e] = s;
-    }
-    __syncthreads();
-    for (int e = tid; e < nb * 256; e += 256) {
-      const int bj = e >> 8, rr = (e >> 4) & 15, cc = e & 15, bi = bj + d;
-      float s = 0.f;
-      for (int k = 0; k <= rr; ++k) s = fmaf(sT[(16 * bi + rr) * LD + 16 * bi + k], sXs[(bj << 8) + (k << 4) + cc], s);
-      sT[(16 * bi + rr) * LD + 16 * bj + cc] = s;
-    }
-    __syncthreads();
+  for (int e = tid; e < 2 * 256; e += 256) {  // blocks (1, 0) and (3, 2)
+    const int bj = 2 * (e >> 8), rr = (e >> 4) & 15, cc = e & 15, bi = bj + 1;
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) s = fmaf(sA[(16 * bi + rr) * LD + 16 * bj + k], sT[(16 * bj + k) * LD + 16 * bj + cc], s);
+    sXs[e] = s;
   }
+  __syncthreads();
+  for (int e = tid; e < 2 * 256; e += 256) {
+    const int bj = 2 * (e >> 8), rr = (e >> 4) & 15, cc = e & 15, bi = bj + 1;
+    float s = 0.f;
+    for (int k = 0; k <= rr; ++k) s = fmaf(sT[(16 * bi + rr) * LD + 16 * bi + k], sXs[((e >> 8) << 8) + (k << 4) + cc], s);
+    sT[(16 * bi + rr) * LD + 16 * bj + cc] = s;
+  }
+  __syncthreads();
+  if (w == 0) {  // one wave: X = A[32:, :32] T[:32, :32] into A's (zero) upper right block
+    f32x16 x = {};
+    mm<32>(x, [&](int m, int k) { return sA[(32 + m) * LD + k]; }, [&](int k, int n) { return sT[k * LD + n]; });
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sA[acc_row(r, h) * LD + 32 + i] = x[r];
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // (lgkmcnt 0: the X rows are written before any read)
+    __builtin_amdgcn_wave_barrier();
+    f32x16 t = {};
+    mm<32>(t, [&](int m, int k) { return sT[(32 + m) * LD + 32 + k]; }, [&](int k, int n) { return sA[k * LD + 32 + n]; });
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sT[(32 + acc_row(r, h)) * LD + i] = t[r];
+  }
+  __syncthreads();
 
   // Attn = (q k^T) * D (lower, diagonal included) over the dead A
   {
