@@ -101,15 +101,23 @@ struct BwdChunkArgs {
   const float *W, *U;                       // with X NULL: the residuals X = U - W P formed here
 };
 
-// rows [C][cols] of a chunk (global, float4 loads) into LDS rows of stride ld
+// rows [C][cols] of a chunk (global, float4 loads) into LDS rows of stride ld: every load
+// of the call is issued before the first store, so a call costs one memory round trip
 template <int COLS>
 __device__ __forceinline__ void load_rows(float *dst, int ld, const float *src, int64_t src_ld, int col0) {
-  constexpr int q4 = COLS / 4;
-  for (int e = threadIdx.x; e < kC * q4; e += 256) {
-    const int r = e / q4, c = 4 * (e - r * q4);
-    const f32x4 x = *reinterpret_cast<const f32x4 *>(src + r * src_ld + col0 + c);
+  constexpr int q4 = COLS / 4, n = kC * q4 / 256;
+  static_assert(kC * q4 % 256 == 0, "whole float4 rounds per thread");
+  f32x4 x[n];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) dst[r * ld + c + t] = x[t];
+  for (int j = 0; j < n; ++j) {
+    const int e = threadIdx.x + 256 * j, r = e / q4, c = 4 * (e - r * q4);
+    x[j] = *reinterpret_cast<const f32x4 *>(src + r * src_ld + col0 + c);
+  }
+#pragma unroll
+  for (int j = 0; j < n; ++j) {
+    const int e = threadIdx.x + 256 * j, r = e / q4, c = 4 * (e - r * q4);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) dst[r * ld + c + t] = x[j][t];
   }
 }
 
