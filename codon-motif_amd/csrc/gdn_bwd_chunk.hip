@@ -101,24 +101,40 @@ struct BwdChunkArgs {
   const float *W, *U;                       // with X NULL: the residuals X = U - W P formed here
 };
 
-// rows [C][cols] of a chunk (global, float4 loads) into LDS rows of stride ld: every load
-// of the call is issued before the first store, so a call costs one memory round trip
+// rows [C][cols] of a chunk (global, float4 loads) into LDS rows of stride ld, in two
+// halves so that the loads of several matrices can all be in flight before the first
+// store: fetch_rows issues a matrix's loads, put_rows writes them (one memory round trip
+// for every matrix fetched together).
 template <int COLS>
-__device__ __forceinline__ void load_rows(float *dst, int ld, const float *src, int64_t src_ld, int col0) {
-  constexpr int q4 = COLS / 4, n = kC * q4 / 256;
+struct Rows {
+  static constexpr int q4 = COLS / 4, n = kC * q4 / 256;
   static_assert(kC * q4 % 256 == 0, "whole float4 rounds per thread");
   f32x4 x[n];
+};
+template <int COLS>
+__device__ __forceinline__ Rows<COLS> fetch_rows(const float *src, int64_t src_ld, int col0) {
+  using R = Rows<COLS>;
+  R rw;
 #pragma unroll
-  for (int j = 0; j < n; ++j) {
-    const int e = threadIdx.x + 256 * j, r = e / q4, c = 4 * (e - r * q4);
-    x[j] = *reinterpret_cast<const f32x4 *>(src + r * src_ld + col0 + c);
+  for (int j = 0; j < R::n; ++j) {
+    const int e = threadIdx.x + 256 * j, r = e / R::q4, c = 4 * (e - r * R::q4);
+    rw.x[j] = *reinterpret_cast<const f32x4 *>(src + r * src_ld + col0 + c);
   }
+  return rw;
+}
+template <int COLS>
+__device__ __forceinline__ void put_rows(float *dst, int ld, const Rows<COLS> &rw) {
+  using R = Rows<COLS>;
 #pragma unroll
-  for (int j = 0; j < n; ++j) {
-    const int e = threadIdx.x + 256 * j, r = e / q4, c = 4 * (e - r * q4);
+  for (int j = 0; j < R::n; ++j) {
+    const int e = threadIdx.x + 256 * j, r = e / R::q4, c = 4 * (e - r * R::q4);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) dst[r * ld + c + t] = x[j][t];
+    for (int t = 0; t < 4; ++t) dst[r * ld + c + t] = rw.x[j][t];
   }
+}
+template <int COLS>
+__device__ __forceinline__ void load_rows(float *dst, int ld, const float *src, int64_t src_ld, int col0) {
+  put_rows<COLS>(dst, ld, fetch_rows<COLS>(src, src_ld, col0));
 }
 
 template <int DV>
@@ -133,10 +149,14 @@ __global__ void __launch_bounds__(256) gdn_bwd_prep_kernel(BwdPrepArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, i = lane & 31, h = lane >> 5;
   const int r0 = 32 * (w >> 1), c0 = 32 * (w & 1);
 
-  load_rows<DK>(sK, LD, a.k + cb * C * DK, DK, 0);
-  load_rows<DK>(sQ, LD, a.q + cb * C * DK, DK, 0);
-  load_rows<DV>(sV, LV, a.v + cb * C * DV, DV, 0);
-  load_rows<DV>(sDo, LV, a.dout + cb * C * DV, DV, 0);
+  {  // the four matrices' loads in flight together
+    const Rows<DK> rk = fetch_rows<DK>(a.k + cb * C * DK, DK, 0), rq = fetch_rows<DK>(a.q + cb * C * DK, DK, 0);
+    const Rows<DV> rv = fetch_rows<DV>(a.v + cb * C * DV, DV, 0), rd = fetch_rows<DV>(a.dout + cb * C * DV, DV, 0);
+    put_rows<DK>(sK, LD, rk);
+    put_rows<DK>(sQ, LD, rq);
+    put_rows<DV>(sV, LV, rv);
+    put_rows<DV>(sDo, LV, rd);
+  }
   if (w == 0) {  // gamma = inclusive cumsum of g over the chunk
     float s = a.g[cb * C + lane];
 #pragma unroll
@@ -338,8 +358,12 @@ __global__ void __launch_bounds__(256) gdn_bwd_chunk_kernel(BwdChunkArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, i = lane & 31, h = lane >> 5;
   const int tr = w >> 1, tc = w & 1, r0 = 32 * tr, c0 = 32 * tc;
 
-  load_rows<DK>(sK, LD, a.k + cb * C * DK, DK, 0);
-  load_rows<C>(sT, LD, a.T + cb * C * C, C, 0);
+  {
+    const Rows<DK> rk = fetch_rows<DK>(a.k + cb * C * DK, DK, 0);
+    const Rows<C> rt = fetch_rows<C>(a.T + cb * C * C, C, 0);
+    put_rows<DK>(sK, LD, rk);
+    put_rows<C>(sT, LD, rt);
+  }
   if (tid < 64) {
     const float gm = a.gam[cb * C + tid];
     sGam[tid] = gm;
@@ -355,11 +379,18 @@ __global__ void __launch_bounds__(256) gdn_bwd_chunk_kernel(BwdChunkArgs a) {
   for (int r = 0; r < 16; ++r) rowB[r] = 0.f;
   for (int j = 0; j < DV / 64; ++j) {
     const int e0 = 64 * j;
-    load_rows<64>(b0, LD, a.dout + cb * C * DV, DV, e0);
-    load_rows<64>(b1, LD, (a.X ? a.X : a.U) + cb * C * DV, DV, e0);
-    load_rows<64>(b2, LD, a.P + cb * DK * DV, DV, e0);
-    load_rows<64>(b3, LD, a.dSn + cb * DK * DV, DV, e0);
-    load_rows<64>(b4, LD, a.v + cb * C * DV, DV, e0);
+    {  // the five matrices' loads in flight together
+      const Rows<64> r0_ = fetch_rows<64>(a.dout + cb * C * DV, DV, e0);
+      const Rows<64> r1_ = fetch_rows<64>((a.X ? a.X : a.U) + cb * C * DV, DV, e0);
+      const Rows<64> r2_ = fetch_rows<64>(a.P + cb * DK * DV, DV, e0);
+      const Rows<64> r3_ = fetch_rows<64>(a.dSn + cb * DK * DV, DV, e0);
+      const Rows<64> r4_ = fetch_rows<64>(a.v + cb * C * DV, DV, e0);
+      put_rows<64>(b0, LD, r0_);
+      put_rows<64>(b1, LD, r1_);
+      put_rows<64>(b2, LD, r2_);
+      put_rows<64>(b3, LD, r3_);
+      put_rows<64>(b4, LD, r4_);
+    }
     if (!a.X) {  // X = U - W P for these columns: W over b5 (free until dxt), U in b1
       load_rows<DK>(b5, LD, a.W + cb * C * DK, DK, 0);
       __syncthreads();
