@@ -28,9 +28,11 @@ FLAGS = [
     '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
     '-I', os.path.join(os.path.dirname(os.path.dirname(HERE)), 'include'),
 ]
-# Per-source extras.  chord.hip: MFMA accumulators in ordinary VGPRs, so the softmax
-# and rescale code reads them without accumulator-register copies (the GDN kernels
-# keep the default: their register budgets rely on the accumulator file).
+# Per-source extras.  chord.hip and gdn_chunk.hip: MFMA accumulators in ordinary VGPRs,
+# so the softmax / rescale code and the scan's per-chunk chain read them without
+# accumulator-register copies.  The backward kernels keep the default: their register
+# budgets rely on the accumulator file (the VGPR form made the per-chunk gradient
+# kernel 19% slower).
 EXTRA = {'chord.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form'], 'gdn_chunk.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form']}
 
 
