@@ -366,11 +366,58 @@ def config_rows(dev, model, with_cpu=True):
             round(dt * 1e3, 1), 'cpu_tok_s': round(Bd / dt, 1), 'cores': torch.get_num_threads(),
             'method': '1 warm-up step, median of 3 steps (the context grows by one per step)'}
     rows['config5_packed_prefill'] = {
-        'skipped': 'kept off the GPU this build: a packed 73364-token prefill exceeded its test time limit '
-                   'with the fused GatedDelta front end (now switched off for packed input); cause not established'}
+        'skipped': 'the packed route is kept off the GPU at this size: a packed 73364-token prefill exceeded its '
+                   'test time limit with the fused GatedDelta front end (now switched off for packed input); '
+                   'cause not established',
+        'gpu_per_sequence': config5_per_sequence(dev, model)}
     if with_cpu:
         rows['config5_packed_prefill']['cpu'] = config5_cpu_subset(model)
     return rows
+
+
+def config5_per_sequence(dev, model, reps=3):
+    '''Config 5's workload on the GPU through the unpacked route: each of the 16
+    sequences (lengths from presets.packed_lengths(), ids seeded as the packed test's) is
+    one B = 1 forward from empty state, logits included, captured as its own hipGraph;
+    a round replays the 16 graphs in order between HIP events; 1 warm-up round, median
+    of `reps`.  tok/s = 73364 tokens / round time.'''
+    import torch
+
+    from motif.model.presets import cu_seqlens_of, packed_lengths
+    lens = packed_lengths()
+    cu = cu_seqlens_of(lens).tolist()
+    ids = torch.randint(0, model.config.vocab_size, (1, cu[-1]), generator=torch.Generator().manual_seed(5))
+    seqs = [ids[:, a:b].to(dev) for a, b in zip(cu[:-1], cu[1:])]
+    graphs = []
+    side = torch.cuda.Stream()
+    for s in seqs:
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            model(s)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = model(s)
+        graphs.append((g, out))
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    times = []
+    for r in range(reps + 1):
+        torch.cuda.synchronize()
+        ev0.record()
+        for g, _ in graphs:
+            g.replay()
+        ev1.record()
+        torch.cuda.synchronize()
+        if r:
+            times.append(ev0.elapsed_time(ev1))
+    finite = all(bool(torch.isfinite(out.logits).all()) for _, out in graphs)
+    del graphs
+    ms = sorted(times)[len(times) // 2]
+    return {'route': 'each sequence as its own B=1 forward from empty state (unpacked kernels), one hipGraph per '
+                     'sequence, the 16 replayed in order; 1 warm-up round, median of '
+                     f'{reps}', 'tokens': cu[-1], 'ms': round(ms, 3), 'tok_s': round(cu[-1] / (ms * 1e-3), 1),
+            'logits_finite': finite}
 
 
 def config5_cpu_subset(model, n=2):
