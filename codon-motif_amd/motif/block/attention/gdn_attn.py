@@ -182,7 +182,7 @@ class GatedDeltaAttention(BasicAttention):
         o = self.o_norm(torch.cat([o, gate], dim=-1)).reshape(B, L, -1)
         return project(o, self.o_proj.weight, self.o_proj.bias)
 
-    def _prefill_fused(self, proj, tails, S0, cu_seqlens=None):
+    def _prefill_fused(self, proj, tails, S0, cu_seqlens=None, y=None):
         '''The whole prefill after the projections in three kernels, or None when the
         fused kernels do not serve this layer / these inputs.'''
         if self.o_norm.weight is None or self.conv_size != 4 or wants_grad(proj, self):
@@ -190,7 +190,41 @@ class GatedDeltaAttention(BasicAttention):
         return gdn_prefill_fused(proj, self._proj_offsets(), (self.q_conv.weight, self.k_conv.weight,
                                                              self.v_conv.weight), tails, self.A_log, self.dt_bias,
                                  self.dk ** -0.5, self.o_norm.weight, self.o_norm.eps, S0, self.num_heads, self.dk,
-                                 self.dv, cu_seqlens)
+                                 self.dv, cu_seqlens, y=y)
+
+    def prefill_core(self, hidden_states, past_key_value, out):
+        '''The prefill of forward() up to the o_proj input (no reference counterpart as
+        one call): the projections, conv, gates, chunk rule and GatedRMSNorm, written into
+        `out` (a bf16 [B, L, H dv] view with unit feature stride, e.g. the left columns of
+        a wider buffer that another projection's input fills), with `past_key_value`
+        (None, or a GatedDeltaAttentionLayerCache) updated as forward() updates it.
+        Returns False, before anything ran, when the fused prefill kernels do not serve
+        this call; the caller then runs forward().'''
+        B, L, _ = hidden_states.shape
+        if (L < 2 or self.o_norm.weight is None or self.conv_size != 4 or self.dk not in (32, 64)
+                or self.dv not in (64, 128) or hidden_states.dtype != torch.bfloat16 or not hidden_states.is_cuda
+                or wants_grad(hidden_states, self)):
+            return False
+        tails, S0 = (None, None, None), None
+        if past_key_value is not None:
+            if not isinstance(past_key_value, GatedDeltaAttentionLayerCache):
+                return False
+            if past_key_value.conv_state is not None:
+                tails = past_key_value.conv_state
+            S0 = past_key_value.state
+        if S0 is not None and (S0.dtype != torch.float32 or not S0.is_contiguous()
+                               or tuple(S0.shape) != (B, self.num_heads, self.dk, self.dv)):
+            return False
+        if any(t is None for t in tails) and any(t is not None for t in tails):
+            return False
+        proj, _ = self._project(hidden_states)
+        whole = self._prefill_fused(proj, tails, S0, y=out)
+        if whole is None:
+            return False
+        _, S, conv_tails = whole
+        if past_key_value is not None:
+            past_key_value.update(S, conv_tails, steps=L)
+        return True
 
     def _decode_fusable(self, hidden_states, cache):
         '''True when one decode step can run as the fused kernel: one token, a cache whose

@@ -13,7 +13,8 @@ from motif.model.cache import DecoderBlockCache, GatedDeltaAttentionLayerCache, 
 from motif.model.config import MotifChordConfig
 from motif.ops import RMSNorm
 from motif.ops.attn_res import apply_block_attn_res, attn_res_read_norms
-from motif.ops.linear_rows import linear_rows_dual, linear_rows_pair, rows_eligible
+from motif.ops.epilogue import swiglu, usable
+from motif.ops.linear_rows import linear_rows_dual, linear_rows_pair, rows_eligible, sum_weights
 
 
 @dataclass
@@ -74,6 +75,34 @@ def _split_step(decoder, x, m, layer_cache, mask, position, prev):
     return linear_rows_dual(o, w_out, act, w_down, gate=g_pre, aux2=prev)
 
 
+def _prefill_step(decoder, x, m, layer_cache, prev):
+    '''A GatedDelta decoder's prefill with its two output projections as one library GEMM:
+    the layer writes its o_proj input y and the MLP its SwiGLU output s side by side
+    into one [B, L, H dv + I] buffer, and f_h = [y | s] [W_o | W_down]^T (no reference
+    counterpart as one op: motif/block/decoder.py:205-210 computes o_proj(y) and
+    down_proj(s) as two GEMMs, rounds each to the activation dtype and adds them; here
+    the sum is accumulated in fp32 and rounded once).  partial = prev + f_h as the
+    reference adds it.  Returns (f_h, partial), or None (before anything ran) when the
+    step does not qualify: not a GatedDelta layer, decode-sized input, autograd, biases,
+    or inputs the fused prefill kernels do not serve.'''
+    attn, mlp = decoder.attn, decoder.mlp
+    if (not isinstance(attn, GatedDeltaAttention) or x.dim() != 3 or x.dtype != torch.bfloat16
+            or mlp.gate_up_proj.bias is not None or rows_eligible(m, mlp.gate_up_proj.weight)
+            or attn.o_proj.out_features != mlp.down_proj.out_features):
+        return None
+    w = sum_weights(decoder, '_out_sum', (attn.o_proj, mlp.down_proj))
+    if w is None:
+        return None
+    B, L, _ = x.shape
+    hv, inner = attn.o_proj.in_features, mlp.down_proj.in_features
+    buf = torch.empty(B, L, hv + inner, dtype=x.dtype, device=x.device)
+    if not usable(buf[..., hv:]) or not attn.prefill_core(x, layer_cache, buf[..., :hv]):
+        return None
+    swiglu(torch.nn.functional.linear(m, mlp.gate_up_proj.weight), out=buf[..., hv:])
+    f_h = torch.nn.functional.linear(buf, w)
+    return f_h, (None if prev is None else prev + f_h)
+
+
 class DecoderBlock(nn.Module):
     def __init__(self, config: MotifChordConfig):
         super().__init__()
@@ -122,10 +151,14 @@ class DecoderBlock(nn.Module):
         # workgroups waiting for CUs.)
         for i, decoder in enumerate(self.features):
             x, m = self._read(attn_res, i, decoder)
-            if use_attn_cache:
+            if cu_seqlens is None:
                 prev = attn_res.partial_block
-                done = _split_step(decoder, x, m, cache.attn[i], mask, position,
-                                   prev if prev is not None and prev.shape == m.shape else None)
+                prev = prev if prev is not None and prev.shape == m.shape else None
+                done = None
+                if use_attn_cache:
+                    done = _split_step(decoder, x, m, cache.attn[i], mask, position, prev)
+                if done is None:
+                    done = _prefill_step(decoder, x, m, cache.attn[i] if use_attn_cache else None, prev)
                 if done is not None:
                     attn_res.update_increment(*done)
                     continue

@@ -55,15 +55,26 @@ def gated_rms_norm_heads(o, gate, weight, eps):
     return y
 
 
-def swiglu(x):
-    '''x [..., 2I] -> x[..., :I] * SiLU(x[..., I:]).'''
+def swiglu(x, out=None):
+    '''x [..., 2I] -> x[..., :I] * SiLU(x[..., I:]); written into `out` (a [B, L, I]
+    view of x's dtype with unit feature stride and 16-byte aligned rows, e.g. the right
+    columns of a wider buffer) when given.'''
     if wants_grad(x):
-        out, gate = x.chunk(2, dim=-1)
-        return out * F.silu(gate)
+        if out is not None:
+            raise ValueError('swiglu: out= is forward-only')
+        val, gate = x.chunk(2, dim=-1)
+        return val * F.silu(gate)
     x2 = x.reshape(-1, x.shape[-1])
     M, I = x2.shape[0], x.shape[-1] // 2
-    y = torch.empty(*x.shape[:-1], I, dtype=x.dtype, device=x.device)
-    rc = _lib.lib().motif_swiglu(x2.data_ptr(), x2.stride(0), y.data_ptr(), I, M, I, _lib.dtype_code(x.dtype),
+    if out is None:
+        y = torch.empty(*x.shape[:-1], I, dtype=x.dtype, device=x.device)
+        y_rs = I
+    else:
+        if (out.dim() != 3 or tuple(out.shape) != (*x.shape[:-1], I) or out.dtype != x.dtype
+                or out.stride(-1) != 1 or out.stride(0) != out.shape[1] * out.stride(1) or not usable(out)):
+            raise ValueError(f'swiglu: out must be a {x.dtype} [..., {I}] view of rows with one stride')
+        y, y_rs = out, out.stride(1)
+    rc = _lib.lib().motif_swiglu(x2.data_ptr(), x2.stride(0), y.data_ptr(), y_rs, M, I, _lib.dtype_code(x.dtype),
                                  _lib.stream_ptr(x.device))
     _lib.check(rc, 'motif_swiglu')
     return y

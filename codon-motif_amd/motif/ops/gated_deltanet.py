@@ -315,7 +315,7 @@ PACKED_FRONT = False
 
 
 def gdn_prefill_fused(proj, offsets, conv_weights, tails, a_log, dt_bias, q_scale, norm_weight, norm_eps, S=None,
-                      heads=None, dk=None, dv=None, cu_seqlens=None):
+                      heads=None, dk=None, dv=None, cu_seqlens=None, y=None):
     '''A GatedDeltaAttention prefill from its input projections to the o_proj input, in
     three kernels (no reference counterpart as one call; replaces
     motif/block/attention/gdn_attn.py:183-209: the q / k / v short conv + SiLU, the q / k
@@ -324,9 +324,11 @@ def gdn_prefill_fused(proj, offsets, conv_weights, tails, a_log, dt_bias, q_scal
     proj [B, L, ncols] bf16 with columns (q, k, v, gate, a, b) at `offsets`;
     conv_weights (wq, wk, wv) nn.Conv1d weights [C, 1, 4]; tails (tq, tk, tv) incoming
     conv tails [B, C, 3] or Nones; S [B, H, dk, dv] fp32 or None; cu_seqlens (B == 1)
-    for packed sequences (zero tails and states).  Returns (y [B, L, H*dv],
-    S_out [B|nseq, H, dk, dv], (tq, tk, tv) outgoing tails), or None when the fused
-    kernels do not serve these inputs (the caller then runs the separate steps).
+    for packed sequences (zero tails and states); y (optional) a [B, L, H*dv] bf16 view
+    with unit feature stride to write the output into (e.g. the left columns of a wider
+    buffer).  Returns (y [B, L, H*dv], S_out [B|nseq, H, dk, dv], (tq, tk, tv) outgoing
+    tails), or None, before anything ran, when the fused kernels do not serve these
+    inputs (the caller then runs the separate steps).
     '''
     if cu_seqlens is not None and not PACKED_FRONT:
         return None
@@ -356,7 +358,11 @@ def gdn_prefill_fused(proj, offsets, conv_weights, tails, a_log, dt_bias, q_scal
         cu_dev = ps.cu
     if L == 0 or nseq == 0:
         return None
-    y = torch.empty(B, L, H * dv, dtype=torch.bfloat16, device=dev)
+    if y is None:
+        y = torch.empty(B, L, H * dv, dtype=torch.bfloat16, device=dev)
+    elif (tuple(y.shape) != (B, L, H * dv) or y.dtype != torch.bfloat16 or y.device != dev
+          or y.stride(-1) != 1):
+        raise ValueError(f'gdn_prefill_fused: y must be a bf16 [{B}, {L}, {H * dv}] view with unit feature stride')
     S_out = torch.empty(nseq, H, dk, dv, dtype=torch.float32, device=dev)
     tout = [torch.empty(nseq, c, 3, dtype=torch.bfloat16, device=dev) for c in C]
     nbytes = _lib.lib().motif_gdn_chunk_workspace_bytes(H, dk, dv, 64, max(total, 1))

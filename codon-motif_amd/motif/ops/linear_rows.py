@@ -208,3 +208,21 @@ def cat_weights(owner, name, linears):
         cached = (key, w, b)
         owner.__dict__[name] = cached
     return cached[1], cached[2]
+
+
+def sum_weights(owner, name, linears):
+    '''Column-concatenated weight [N, K1 + K2 + ...] of several bias-free nn.Linear of
+    one output width: x W^T over inputs laid side by side, [x1 | x2 | ...], is the sum
+    of their projections in one GEMM (accumulated in fp32 and rounded once).  Cached
+    like cat_weights; None under autograd or when a Linear has a bias.'''
+    params = [m.weight for m in linears]
+    if any(m.bias is not None for m in linears) or (
+            torch.is_grad_enabled() and any(p.requires_grad for p in params)):
+        return None
+    key = tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in params)
+    cached = owner.__dict__.get(name)
+    if cached is None or cached[0] != key:
+        with torch.no_grad():
+            cached = (key, torch.cat(params, dim=1))
+        owner.__dict__[name] = cached
+    return cached[1]

@@ -68,7 +68,9 @@ class _Tap:
     with a cache) the cache contents before the call, keeping batch rows `rows`.  While
     active, decode steps run layer by layer (the decoder's split step, which batches the
     layer's projections with the MLP's and equals the layer-by-layer step bit for bit,
-    calls no layer forward).'''
+    calls no layer forward), and so do GatedDelta prefills (the decoder's prefill step
+    applies o_proj inside the shared output GEMM, so no layer output exists to record;
+    tests/test_gpu_prefill_step.py compares the two forms).'''
 
     def __init__(self, model, rows=None):
         self.model, self.rows, self.records = model, rows, []
@@ -91,6 +93,7 @@ class _Tap:
     def __enter__(self):
         import motif.block.decoder as dec
         self._split, dec._split_step = dec._split_step, (lambda *a, **k: None)
+        self._prefill, dec._prefill_step = dec._prefill_step, (lambda *a, **k: None)
         self.layers = []
         for bi, block in enumerate(self.model.blocks):
             for li, dec in enumerate(block.features):
@@ -117,6 +120,7 @@ class _Tap:
     def __exit__(self, *exc):
         import motif.block.decoder as dec
         dec._split_step = self._split
+        dec._prefill_step = self._prefill
         for attn in self.layers:
             del attn.forward, attn.forward_varlen
 
