@@ -92,7 +92,7 @@ __device__ __forceinline__ float group_sum(float x) {
 // LPT lanes per token (64 / LPT tokens per wave), PPL 16-byte pieces per lane
 // (D <= LPT * PPL * Piece::N).  Every lane of a wave takes part in the group sums;
 // lanes of tokens past the end compute on zeros and store nothing.
-template <typename T, int LPT, int PPL>
+template <typename T, int LPT, int PPL, int NS>
 __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
   constexpr int E = Piece<T>::N;
   const int sub = threadIdx.x & (LPT - 1);
@@ -114,6 +114,20 @@ __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
     for (int e = 0; e < E; ++e) qw[i][e] = qv[e] * wv[e];
   }
 
+  // the norm weights of the outputs, requested first (read after the reductions they
+  // would add a memory round trip at the end); only the norms asked for
+  uint4 nwr[2][PPL];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+#pragma unroll
+    for (int i = 0; i < PPL; ++i) nwr[k][i] = uint4{0u, 0u, 0u, 0u};
+    if (k < a.nnorm) {
+      const buf_t nb = make_buf(a.nw[k], dbytes);
+#pragma unroll
+      for (int i = 0; i < PPL; ++i) nwr[k][i] = buf_ld16(nb, (sub + LPT * i) * 16);
+    }
+  }
+
   // every source row is loaded before any reduction, so the loads overlap.  Plain loads
   // from per-lane row addresses (a buffer resource per row would differ between the
   // tokens of a wave and turn each load into a loop over them); pieces past D load the
@@ -121,32 +135,32 @@ __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
   // would become a branch around the load, and a wait for it).  The unpacking runs for
   // every source slot after all loads (absent sources read as zeros): unpacked inside
   // each source's branch, the loads of a source would wait for the previous one.
-  uint4 raw[kMaxSrc][PPL];
+  uint4 raw[NS][PPL];
 #pragma unroll
-  for (int n = 0; n < kMaxSrc; ++n)
+  for (int n = 0; n < NS; ++n)
 #pragma unroll
     for (int i = 0; i < PPL; ++i) raw[n][i] = uint4{0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int n = 0; n < kMaxSrc; ++n) {
+  for (int n = 0; n < NS; ++n) {
     if (n >= a.nsrc) break;
     const T *row = static_cast<const T *>(a.src[n]) + b * a.sb[n] + int64_t(t) * a.st[n];
 #pragma unroll
     for (int i = 0; i < PPL; ++i) raw[n][i] = *reinterpret_cast<const uint4 *>(row + min(sub + LPT * i, np - 1) * E);
   }
-  float x[kMaxSrc][PPL][E];
+  float x[NS][PPL][E];
 #pragma unroll
   for (int i = 0; i < PPL; ++i) {
     const uint32_t keep = sub + LPT * i < np ? 0xffffffffu : 0u;
 #pragma unroll
-    for (int n = 0; n < kMaxSrc; ++n) {
+    for (int n = 0; n < NS; ++n) {
       const uint4 u = raw[n][i];
       Piece<T>::unpack(uint4{u.x & keep, u.y & keep, u.z & keep, u.w & keep}, x[n][i]);
     }
   }
-  float logit[kMaxSrc];
+  float logit[NS];
   float mx = -INFINITY;
 #pragma unroll
-  for (int n = 0; n < kMaxSrc; ++n) {
+  for (int n = 0; n < NS; ++n) {
     logit[n] = -INFINITY;
     if (n < a.nsrc) {
       float ss = 0.f, dot = 0.f;
@@ -163,9 +177,9 @@ __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
       mx = fmaxf(mx, logit[n]);
     }
   }
-  float alpha[kMaxSrc], den = 0.f;
+  float alpha[NS], den = 0.f;
 #pragma unroll
-  for (int n = 0; n < kMaxSrc; ++n) {
+  for (int n = 0; n < NS; ++n) {
     alpha[n] = n < a.nsrc ? exp_f(logit[n] - mx) : 0.f;
     den += alpha[n];
   }
@@ -176,7 +190,7 @@ __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
 #pragma unroll
     for (int e = 0; e < E; ++e) h[i][e] = 0.f;
 #pragma unroll
-    for (int n = 0; n < kMaxSrc; ++n)
+    for (int n = 0; n < NS; ++n)
       if (n < a.nsrc) {
 #pragma unroll
         for (int e = 0; e < E; ++e) h[i][e] = fmaf(alpha[n] * inv, x[n][i][e], h[i][e]);
@@ -213,7 +227,7 @@ __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
       const int p = sub + LPT * i;
       if (p >= np) continue;
       float w[E], y[E];
-      Piece<T>::unpack(buf_ld16(make_buf(a.nw[k], dbytes), p * 16), w);
+      Piece<T>::unpack(nwr[k][i], w);
 #pragma unroll
       for (int e = 0; e < E; ++e) y[e] = round_to<T>(h[i][e] * r) * w[e];
       Piece<T>::store(nrow + p * E, y);
@@ -224,15 +238,15 @@ __global__ void __launch_bounds__(256) attn_res_kernel(AttnResArgs a) {
 // Up to 256 tokens (decode batches) each token gets a one-wave workgroup, so the
 // launch spreads over as many CUs as there are tokens (64 decode rows: 5.6 us per read
 // against 8.2 us with four waves and eight tokens per workgroup).
-template <typename T, int LPT>
+template <typename T, int LPT, int NS>
 int launch_lpt(const AttnResArgs &a, int ppl, hipStream_t s) {
   const int bs = a.B * a.T <= 256 ? LPT : 256;
   const dim3 grid((a.B * a.T + bs / LPT - 1) / (bs / LPT)), block(bs);
   switch (ppl) {
-    case 1: attn_res_kernel<T, LPT, 1><<<grid, block, 0, s>>>(a); break;
-    case 2: attn_res_kernel<T, LPT, 2><<<grid, block, 0, s>>>(a); break;
-    case 3: attn_res_kernel<T, LPT, 3><<<grid, block, 0, s>>>(a); break;
-    case 4: attn_res_kernel<T, LPT, 4><<<grid, block, 0, s>>>(a); break;
+    case 1: attn_res_kernel<T, LPT, 1, NS><<<grid, block, 0, s>>>(a); break;
+    case 2: attn_res_kernel<T, LPT, 2, NS><<<grid, block, 0, s>>>(a); break;
+    case 3: attn_res_kernel<T, LPT, 3, NS><<<grid, block, 0, s>>>(a); break;
+    case 4: attn_res_kernel<T, LPT, 4, NS><<<grid, block, 0, s>>>(a); break;
     default: return set_error(MOTIF_ERR_UNSUPPORTED, "attn_res_read: D too large (at most 256 16-byte pieces)");
   }
   return check_launch("attn_res_kernel");
@@ -244,8 +258,11 @@ int launch(const AttnResArgs &a, hipStream_t s) {
   const int np = a.D / E;
   // two tokens a wave (32 lanes each) up to 128 pieces, else one; one token a wave
   // (and a workgroup) for up to 256 tokens
-  if (np <= 128 && a.B * a.T > 256) return launch_lpt<T, 32>(a, (np + 31) / 32, s);
-  return launch_lpt<T, 64>(a, (np + 63) / 64, s);
+  // source slots in registers: 4 (every read of a block of up to four decoders) or the
+  // most the kernel takes
+  if (np <= 128 && a.B * a.T > 256)
+    return a.nsrc <= 4 ? launch_lpt<T, 32, 4>(a, (np + 31) / 32, s) : launch_lpt<T, 32, kMaxSrc>(a, (np + 31) / 32, s);
+  return a.nsrc <= 4 ? launch_lpt<T, 64, 4>(a, (np + 63) / 64, s) : launch_lpt<T, 64, kMaxSrc>(a, (np + 63) / 64, s);
 }
 
 }  // namespace
