@@ -770,7 +770,61 @@ __global__ void __launch_bounds__(256) chord_decode_kernel(ChordArgs a, const fl
 constexpr int kMfmaRows = 16;
 constexpr int kVRow = 72;  // LDS V row stride (bf16): 144 bytes, conflict-free gathers
 
-__global__ void __launch_bounds__(256) chord_decode_mfma_kernel(ChordArgs a) {
+// The whole decode step of a Chord layer in one launch (motif_chord_decode_step): q, k
+// and v come from the layer's projection rows, q and k RMSNormed here exactly as
+// chord_prep_kernel does it; the workgroup whose split holds a new position appends
+// its key / value row to the cache before any of its loads; the last workgroup of
+// each (batch row, kv head) to finish merges the splits' partials (chord_merge_kernel's
+// arithmetic), and the last of those advances the cursor.  `cnt` holds B * Hkv + 1
+// arrival counters that are zero between launches (each launch leaves them zero).
+struct StepArgs {
+  const bf16_t *proj; int64_t p_sb, p_st;  // [B, L, ncols]
+  int q_off, k_off, v_off;
+  const bf16_t *qw, *kw;                    // RMSNorm weights [D]
+  float neps;
+  int *cnt;
+};
+
+// RMSNorm of 16 features per lane, the row's 64 features over lanes l, l ^ 16, l ^ 32,
+// l ^ 48 (16 g .. 16 g + 15 on lane group g): T(x * rsqrt(mean(x^2) + eps)) * w.  The
+// sum of squares is formed in chord_prep_kernel's order (an fma chain per 8-element
+// piece, then the pieces added pairwise as its 8-lane butterfly adds them), so both
+// kernels produce the same bits.
+__device__ __forceinline__ void rms_norm16(uint4 &u0, uint4 &u1, const uint4 w0, const uint4 w1, float eps) {
+  float x0[8], x1[8], wa[8], wb[8];
+  const uint32_t a0[4] = {u0.x, u0.y, u0.z, u0.w}, a1[4] = {u1.x, u1.y, u1.z, u1.w};
+  const uint32_t b0[4] = {w0.x, w0.y, w0.z, w0.w}, b1[4] = {w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x0[2 * i] = __uint_as_float(a0[i] << 16); x0[2 * i + 1] = __uint_as_float(a0[i] & 0xffff0000u);
+    x1[2 * i] = __uint_as_float(a1[i] << 16); x1[2 * i + 1] = __uint_as_float(a1[i] & 0xffff0000u);
+    wa[2 * i] = __uint_as_float(b0[i] << 16); wa[2 * i + 1] = __uint_as_float(b0[i] & 0xffff0000u);
+    wb[2 * i] = __uint_as_float(b1[i] << 16); wb[2 * i + 1] = __uint_as_float(b1[i] & 0xffff0000u);
+  }
+  float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    s0 = fmaf(x0[e], x0[e], s0);
+    s1 = fmaf(x1[e], x1[e], s1);
+  }
+  float ss = s0 + s1;
+  ss += __shfl_xor(ss, 16, 64);
+  ss += __shfl_xor(ss, 32, 64);
+  const float rs = rsqrtf(ss / kD + eps);
+  uint32_t o0[4], o1[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o0[i] = static_cast<uint32_t>(f32_to_bf16(bf16_to_f32(f32_to_bf16(x0[2 * i] * rs)) * wa[2 * i])) |
+            (static_cast<uint32_t>(f32_to_bf16(bf16_to_f32(f32_to_bf16(x0[2 * i + 1] * rs)) * wa[2 * i + 1])) << 16);
+    o1[i] = static_cast<uint32_t>(f32_to_bf16(bf16_to_f32(f32_to_bf16(x1[2 * i] * rs)) * wb[2 * i])) |
+            (static_cast<uint32_t>(f32_to_bf16(bf16_to_f32(f32_to_bf16(x1[2 * i + 1] * rs)) * wb[2 * i + 1])) << 16);
+  }
+  u0 = uint4{o0[0], o0[1], o0[2], o0[3]};
+  u1 = uint4{o1[0], o1[1], o1[2], o1[3]};
+}
+
+template <bool STEP>
+__global__ void __launch_bounds__(256) chord_decode_mfma_kernel(ChordArgs a, StepArgs sa) {
   // wave index in an SGPR: the key loop below is then scalar (MFMAs must not sit
   // under a lane-mask branch, as they ignore EXEC)
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -787,7 +841,16 @@ __global__ void __launch_bounds__(256) chord_decode_mfma_kernel(ChordArgs a) {
   const int head = kvh * group + (row_ok ? gr % group : 0);
   const int qi = row_ok ? gr / group : 0;
   bf16x8 qb[2];
-  {
+  if constexpr (STEP) {
+    // the raw q row of the projection, normalised here (every lane joins the sums)
+    const bf16_t *qr = sa.proj + b * sa.p_sb + int64_t(qi) * sa.p_st + sa.q_off + head * kD + 16 * g;
+    uint4 u0 = *reinterpret_cast<const uint4 *>(qr), u1 = *reinterpret_cast<const uint4 *>(qr + 8);
+    rms_norm16(u0, u1, *reinterpret_cast<const uint4 *>(sa.qw + 16 * g),
+               *reinterpret_cast<const uint4 *>(sa.qw + 16 * g + 8), sa.neps);
+    const uint4 z{0, 0, 0, 0};
+    qb[0] = __builtin_bit_cast(bf16x8, row_ok ? u0 : z);
+    qb[1] = __builtin_bit_cast(bf16x8, row_ok ? u1 : z);
+  } else {
     const bf16_t *qr = qg + b * a.q_sb + head * a.q_sh + int64_t(qi) * a.q_st + 16 * g;
     const uint4 u0 = *reinterpret_cast<const uint4 *>(qr), u1 = *reinterpret_cast<const uint4 *>(qr + 8);
     const uint4 z{0, 0, 0, 0};
@@ -846,6 +909,53 @@ __global__ void __launch_bounds__(256) chord_decode_mfma_kernel(ChordArgs a) {
   f32x4 o[4];
 #pragma unroll
   for (int ft = 0; ft < 4; ++ft) o[ft] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if constexpr (STEP) {
+    // The new positions [q_start, q_start + L) this split holds: wave 0 appends their key
+    // (RMSNormed, chord_prep_kernel's order: an fma chain per lane, then the 8-lane
+    // butterfly) and value rows, lane = 32 (value?) + 8 t + piece, before any load of
+    // this workgroup reads them; no other workgroup reads these positions.
+    if (w == 0) {
+      const int is_v = lane >> 5, t = (lane >> 3) & 3, piece = lane & 7;
+      const int pos = q_start + t;
+      const bool mine = t < a.L && pos >= k_lo && pos < k_lo + per && pos < a.S;
+      const bf16_t *src = sa.proj + b * sa.p_sb + int64_t(min(t, a.L - 1)) * sa.p_st + (is_v ? sa.v_off : sa.k_off) +
+                          kvh * kD + 8 * piece;
+      const uint4 u = *reinterpret_cast<const uint4 *>(src);
+      const uint4 wr = *reinterpret_cast<const uint4 *>(sa.kw + 8 * piece);
+      float x[8], wk[8];
+      const uint32_t ua[4] = {u.x, u.y, u.z, u.w}, wa[4] = {wr.x, wr.y, wr.z, wr.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[2 * i] = __uint_as_float(ua[i] << 16); x[2 * i + 1] = __uint_as_float(ua[i] & 0xffff0000u);
+        wk[2 * i] = __uint_as_float(wa[i] << 16); wk[2 * i + 1] = __uint_as_float(wa[i] & 0xffff0000u);
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
+#pragma unroll
+      for (int off = 1; off < 8; off <<= 1) ss += __shfl_xor(ss, off, 64);
+      uint4 o = u;
+      if (!is_v) {
+        const float rs = rsqrtf(ss / kD + sa.neps);
+        uint32_t ow[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          ow[i] = static_cast<uint32_t>(f32_to_bf16(bf16_to_f32(f32_to_bf16(x[2 * i] * rs)) * wk[2 * i])) |
+                  (static_cast<uint32_t>(f32_to_bf16(bf16_to_f32(f32_to_bf16(x[2 * i + 1] * rs)) * wk[2 * i + 1]))
+                   << 16);
+        o = uint4{ow[0], ow[1], ow[2], ow[3]};
+      }
+      if (mine) {
+        bf16_t *dst = is_v ? static_cast<bf16_t *>(const_cast<void *>(a.v)) + b * a.v_sb + kvh * a.v_sh + int64_t(pos) * a.v_st
+                           : static_cast<bf16_t *>(const_cast<void *>(a.k)) + b * a.k_sb + kvh * a.k_sh + int64_t(pos) * a.k_st;
+        *reinterpret_cast<uint4 *>(dst + 8 * piece) = o;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  }
 
   int n0 = k_lo + w * 32;
   Stage cur;
@@ -964,8 +1074,82 @@ __global__ void __launch_bounds__(256) chord_decode_mfma_kernel(ChordArgs a) {
       if (a.lse && d == 0) a.lse[(static_cast<size_t>(b) * a.H + hh) * a.L + ii] = M + fast_log2(Ls);
     } else {
       float *pp = a.part + ((((static_cast<size_t>(b) * a.Hkv + kvh) * a.splits + split) * total_rows + grr) * (kD + 2));
-      pp[d] = ov;
-      if (d == 0) { pp[kD] = M; pp[kD + 1] = Ls; }
+      if constexpr (STEP) {
+        // device-coherent stores (through to memory): the merging workgroup may run on
+        // another XCD, and a device-wide release fence would write back a whole L2
+        __hip_atomic_store(&pp[d], ov, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (d == 0) {
+          __hip_atomic_store(&pp[kD], M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(&pp[kD + 1], Ls, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      } else {
+        pp[d] = ov;
+        if (d == 0) { pp[kD] = M; pp[kD + 1] = Ls; }
+      }
+    }
+  }
+  if constexpr (STEP) {
+    // Arrival of this split once every thread's partial stores have completed; the
+    // last split of the (batch row, kv head) merges, as chord_merge_kernel does, row by
+    // row, reading the partials with device-coherent loads.
+    __shared__ int s_last;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    const int slot = b * a.Hkv + kvh;  // one row chunk per (batch row, kv head) on this path
+    if (tid == 0)
+      s_last = __hip_atomic_fetch_add(&sa.cnt[slot], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.splits - 1;
+    __syncthreads();
+    if (!s_last) return;
+    auto ldp = [](const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    // this (batch row, kv head)'s partials [splits][rows][D + 2] are one block: staged
+    // into LDS with every load in flight together when they fit (one memory round trip)
+    // (over the K tiles' LDS, dead since the loop: splits x rows x 66 floats at the
+    // model's shape is 1056 of its 4096)
+    constexpr int kMergeLds = static_cast<int>(sizeof(sKs) / sizeof(float));
+    float *s_part = reinterpret_cast<float *>(&sKs[0][0]);
+    const int nfl = a.splits * total_rows * (kD + 2);
+    const float *blk = a.part + (static_cast<size_t>(b) * a.Hkv + kvh) * a.splits * total_rows * (kD + 2);
+    const bool staged = nfl <= kMergeLds;
+    if (staged) {
+      float tmp[kMergeLds / 256];
+#pragma unroll
+      for (int j = 0; j < kMergeLds / 256; ++j) {
+        const int i = j * 256 + tid;
+        tmp[j] = i < nfl ? ldp(blk + i) : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < kMergeLds / 256; ++j) {
+        const int i = j * 256 + tid;
+        if (i < nfl) s_part[i] = tmp[j];
+      }
+      __syncthreads();
+    }
+    auto part_at = [&](int i) { return staged ? s_part[i] : ldp(blk + i); };
+    const int sstride = total_rows * (kD + 2);
+    for (int e = tid; e < total_rows * kD; e += 256) {
+      const int r = e / kD, d = e % kD;
+      const int pr = r * (kD + 2);
+      float M = -INFINITY;
+      for (int sp = 0; sp < a.splits; ++sp) M = fmaxf(M, part_at(sp * sstride + pr + kD));
+      const float Mu = M == -INFINITY ? 0.f : M;
+      float o = 0.f, Ls = 0.f;
+      for (int sp = 0; sp < a.splits; ++sp) {
+        const float f = fast_exp2(part_at(sp * sstride + pr + kD) - Mu);
+        o += part_at(sp * sstride + pr + d) * f;
+        Ls += part_at(sp * sstride + pr + kD + 1) * f;
+      }
+      const int hh = kvh * group + r % group, ii = r / group;
+      st(static_cast<bf16_t *>(a.out) + b * a.o_sb + hh * a.o_sh + int64_t(ii) * a.o_st + d, o / fmaxf(Ls, 1e-20f));
+    }
+    if (tid == 0) {
+      __hip_atomic_store(&sa.cnt[slot], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // every workgroup has read the cursor before it arrived: the last (batch row, kv
+      // head) to finish advances it
+      const int all = a.B * a.Hkv;
+      if (__hip_atomic_fetch_add(&sa.cnt[all], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == all - 1) {
+        __hip_atomic_store(&sa.cnt[all], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *a.len_dev = min(*a.len_dev + a.L, a.S);
+      }
     }
   }
 }
@@ -1160,7 +1344,7 @@ extern "C" int motif_chord_fwd(
       if (rc) return rc;
     }
     if (!mfma) return launch_vector_dt(dtype, a, R, D, tab, tn, s);
-    chord_decode_mfma_kernel<<<dim3(a.splits, Hkv, B * a.nqc), dim3(256), 0, s>>>(a);
+    chord_decode_mfma_kernel<false><<<dim3(a.splits, Hkv, B * a.nqc), dim3(256), 0, s>>>(a, StepArgs{});
     rc = check_launch("chord_decode_kernel");
     if (rc || a.splits == 1) return rc;
     chord_merge_kernel<bf16_t><<<dim3(rows, Hkv, B), dim3(64), 0, s>>>(a);
@@ -1267,7 +1451,7 @@ int motif::chord_decode_run(
     return launch_vector_dt(dtype, a, R, D, tab, tn, s);  // its merge advances the cursor
   }
   a.nqc = (rows + kMfmaRows - 1) / kMfmaRows;
-  chord_decode_mfma_kernel<<<dim3(splits, Hkv, B * a.nqc), dim3(256), 0, s>>>(a);
+  chord_decode_mfma_kernel<false><<<dim3(splits, Hkv, B * a.nqc), dim3(256), 0, s>>>(a, StepArgs{});
   if ((rc = check_launch("chord_decode_kernel"))) return rc;
   chord_merge_kernel<bf16_t><<<dim3(rows, Hkv, B), dim3(64), 0, s>>>(a);
   return check_launch("chord_merge_kernel");
@@ -1287,4 +1471,79 @@ extern "C" int motif_chord_decode(
                                  length_dev, capacity, alpha, beta, mu, ssmax, log_n, ln_sb, ln_st, log_table,
                                  log_table_len, out, o_sb, o_sh, o_st, B, H, Hkv, L, D, scale, eps, workspace,
                                  workspace_bytes, dtype, stream);
+}
+
+// ------------------------------------------------------------------ fused decode step
+
+namespace motif {
+
+static size_t step_ws_bytes(int B, int H, int Hkv, int L, int splits) {
+  const size_t part = static_cast<size_t>(B) * Hkv * splits * (static_cast<size_t>(H / Hkv) * L) * (kD + 2) * sizeof(float);
+  return part + (static_cast<size_t>(B) * Hkv + 1) * sizeof(int);
+}
+
+}  // namespace motif
+
+extern "C" size_t motif_chord_decode_step_workspace_bytes(int B, int H, int Hkv, int L, int capacity) {
+  if (B <= 0 || H <= 0 || Hkv <= 0 || H % Hkv || L <= 0 || capacity < L) return 0;
+  return motif::step_ws_bytes(B, H, Hkv, L, motif::decode_splits(B, Hkv, capacity));
+}
+
+extern "C" int motif_chord_decode_step(
+    const void *proj, int64_t p_sb, int64_t p_st, int q_off, int k_off, int v_off,
+    const void *q_norm_weight, const void *k_norm_weight, float norm_eps,
+    void *k_cache, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    void *v_cache, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    int *length_dev, int capacity,
+    const float *alpha, const float *beta, const float *mu, const float *ssmax,
+    const float *log_table, int log_table_len,
+    void *out, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    int B, int H, int Hkv, int L, int D, float scale, float eps,
+    void *workspace, size_t workspace_bytes, void *stream) {
+  using namespace motif;
+  if (B < 0 || H <= 0 || Hkv <= 0 || L < 0 || H % Hkv)
+    return set_error(MOTIF_ERR_INVALID, "chord_decode_step: bad size");
+  if (D != kD || (H / Hkv) * L > kMfmaRows)
+    return set_error(MOTIF_ERR_UNSUPPORTED, "chord_decode_step: head_dim 64 and at most 16 query rows per kv head");
+  if (B == 0 || L == 0) return MOTIF_OK;
+  if (capacity < L) return set_error(MOTIF_ERR_INVALID, "chord_decode_step: capacity below the query count");
+  if (!proj || !q_norm_weight || !k_norm_weight || !k_cache || !v_cache || !length_dev || !alpha || !beta || !mu ||
+      !ssmax || !log_table || !out)
+    return set_error(MOTIF_ERR_INVALID, "chord_decode_step: NULL pointer");
+  if (log_table_len < capacity)
+    return set_error(MOTIF_ERR_INVALID, "chord_decode_step: the log table is shorter than the capacity");
+  if (((p_sb | p_st | q_off | k_off | v_off | k_st | v_st | o_st | k_sh | v_sh | o_sh | k_sb | v_sb | o_sb) % 8) != 0 ||
+      ((reinterpret_cast<uintptr_t>(proj) | reinterpret_cast<uintptr_t>(q_norm_weight) |
+        reinterpret_cast<uintptr_t>(k_norm_weight) | reinterpret_cast<uintptr_t>(k_cache) |
+        reinterpret_cast<uintptr_t>(v_cache) | reinterpret_cast<uintptr_t>(out)) & 15) != 0)
+    return set_error(MOTIF_ERR_UNSUPPORTED, "chord_decode_step: rows must be 16-byte aligned");
+  const int splits = decode_splits(B, Hkv, capacity);
+  const size_t need = step_ws_bytes(B, H, Hkv, L, splits);
+  if (!workspace || workspace_bytes < need)
+    return set_error(MOTIF_ERR_INVALID, "chord_decode_step: workspace too small (need " + std::to_string(need) + " bytes)");
+
+  ChordArgs a;
+  a.q = nullptr; a.q_sb = a.q_sh = a.q_st = 0;
+  a.k = k_cache; a.k_sb = k_sb; a.k_sh = k_sh; a.k_st = k_st;
+  a.v = v_cache; a.v_sb = v_sb; a.v_sh = v_sh; a.v_st = v_st;
+  a.alpha = alpha; a.beta = beta; a.mu = mu; a.ssmax = ssmax;
+  a.log_n = nullptr; a.ln_sb = a.ln_st = 0;
+  a.out = out; a.o_sb = o_sb; a.o_sh = o_sh; a.o_st = o_st;
+  a.lse = nullptr;
+  a.B = B; a.H = H; a.Hkv = Hkv; a.L = L; a.S = capacity; a.q_start = 0;
+  a.scale = scale; a.eps = eps;
+  a.cu = nullptr;
+  a.part = static_cast<float *>(workspace);
+  a.splits = splits;
+  a.nqc = 1;
+  a.len_dev = length_dev; a.log_tab = log_table;
+  StepArgs sa;
+  sa.proj = static_cast<const bf16_t *>(proj); sa.p_sb = p_sb; sa.p_st = p_st;
+  sa.q_off = q_off; sa.k_off = k_off; sa.v_off = v_off;
+  sa.qw = static_cast<const bf16_t *>(q_norm_weight); sa.kw = static_cast<const bf16_t *>(k_norm_weight);
+  sa.neps = norm_eps;
+  sa.cnt = reinterpret_cast<int *>(static_cast<char *>(workspace) + (need - (static_cast<size_t>(B) * Hkv + 1) * sizeof(int)));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  chord_decode_mfma_kernel<true><<<dim3(splits, Hkv, B), dim3(256), 0, s>>>(a, sa);
+  return check_launch("chord_decode_step");
 }

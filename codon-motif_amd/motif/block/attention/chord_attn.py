@@ -29,7 +29,8 @@ from motif.ops import RMSNorm, apply_chord_attention, apply_chord_attention_varl
 from motif.ops.packed import PackedSeqs
 from motif.ops import _lib
 from motif.ops.autograd_path import wants_grad
-from motif.ops.chord_attention import HEAD_DIMS, chord_decode_cursor, chord_decode_workspace, serves_head_dim
+from motif.ops.chord_attention import (HEAD_DIMS, chord_decode_cursor, chord_decode_step, chord_decode_step_serves,
+                                       chord_decode_step_workspace, chord_decode_workspace, serves_head_dim)
 from motif.ops.epilogue import mul_sigmoid, usable
 from motif.ops.linear_rows import cat_weights, linear_rows, project, rows_eligible
 
@@ -37,6 +38,9 @@ GGD_EPS = 1e-5
 _KERNEL_DTYPES = (torch.bfloat16, torch.float32)  # the input kernel (norms, cache append)
 _ATTN_DTYPES = (torch.bfloat16, torch.float32, torch.float16)  # the attention kernels
 _DECODE_ROWS = 8  # (GQA group x L) up to this size is a decode-shaped call
+# Cursor decode steps in one launch (motif_chord_decode_step) where it serves; False keeps
+# the input kernel + decode kernels (the same bits, three launches).
+FUSED_STEP = True
 
 
 class LogPositions:
@@ -310,17 +314,29 @@ class ChordAttention(BasicAttention):
         '''The cursor step from the projected tokens proj [B, L, q|k|v|g]: (merged
         attention output [B, L, hidden], gate pre-activation [B, L, hidden]).'''
         B, L = proj.shape[0], proj.shape[1]
-        q = torch.empty(B, self.num_heads, L, self.head_dim, dtype=proj.dtype, device=proj.device)
         ks, vs = cache._slab
-        self._prep(proj, q, ks, vs, cache.length_dev, -1, cache.capacity)
         if cache.__dict__.get('log_table') is None or cache.log_table.numel() < cache.capacity:
             cache.log_table = LogPositions.get(cache.capacity, proj.device)  # held: a graph keeps its address
-        if cache.decode_workspace is None:
-            cache.decode_workspace = chord_decode_workspace(B, self.num_heads, self.num_kv_heads, L, cache.capacity,
-                                                            self.head_dim, proj.dtype, proj.device)
         alpha, beta, mu, ssmax = self.ggd_params()
-        out = chord_decode_cursor(q, ks, vs, cache.length_dev, alpha, beta, mu, ssmax, cache.log_table,
-                                  self.head_dim ** -0.5, GGD_EPS, workspace=cache.decode_workspace)
+        if FUSED_STEP and chord_decode_step_serves(proj, self.num_heads, self.num_kv_heads, self.head_dim):
+            # norms, append, attention, merge and cursor advance in one launch
+            if cache.step_workspace is None:
+                cache.step_workspace = chord_decode_step_workspace(B, self.num_heads, self.num_kv_heads, L,
+                                                                   cache.capacity, proj.device)
+            dt = proj.dtype
+            hs, kd = self.hidden_size, self.kv_dim
+            out = chord_decode_step(proj, (0, hs, hs + kd), self.q_norm.weight.to(dt).contiguous(),
+                                    self.k_norm.weight.to(dt).contiguous(), self.q_norm.eps, ks, vs, cache.length_dev,
+                                    alpha, beta, mu, ssmax, cache.log_table, self.num_heads, self.head_dim ** -0.5,
+                                    GGD_EPS, cache.step_workspace)
+        else:
+            q = torch.empty(B, self.num_heads, L, self.head_dim, dtype=proj.dtype, device=proj.device)
+            self._prep(proj, q, ks, vs, cache.length_dev, -1, cache.capacity)
+            if cache.decode_workspace is None:
+                cache.decode_workspace = chord_decode_workspace(B, self.num_heads, self.num_kv_heads, L, cache.capacity,
+                                                                self.head_dim, proj.dtype, proj.device)
+            out = chord_decode_cursor(q, ks, vs, cache.length_dev, alpha, beta, mu, ssmax, cache.log_table,
+                                      self.head_dim ** -0.5, GGD_EPS, workspace=cache.decode_workspace)
         cache.length += L
         cache.cursor_steps = getattr(cache, 'cursor_steps', 0) + 1
         return self._merge_heads(out), proj[..., self.hidden_size + 2 * self.kv_dim:]

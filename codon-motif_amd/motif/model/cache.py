@@ -235,6 +235,7 @@ class StaticKVLayerCache(KVLayerCache):
         super().__init__(num_heads)
         self.length_dev: Optional[torch.Tensor] = None
         self.decode_workspace: Optional[torch.Tensor] = None
+        self.step_workspace: Optional[torch.Tensor] = None  # the fused decode step's (zeroed once)
 
     def allocate(self, batch, kv_heads, capacity, head_dim, device, dtype):
         shape = (batch, kv_heads, capacity, head_dim)
@@ -242,6 +243,7 @@ class StaticKVLayerCache(KVLayerCache):
         self.length = 0
         self.length_dev = torch.zeros(1, dtype=torch.int32, device=device)
         self.decode_workspace = None
+        self.step_workspace = None
         return self
 
     def _room(self, like, n):

@@ -71,6 +71,10 @@ _SIGNATURES = {
     'motif_chord_decode': (
         _T4 * 3 + [_P, _I32] + [_P] * 4 + [_P, _I64, _I64, _P, _I32] + _T4 + [_I32] * 5 + [_F32, _F32]
         + [_P, _SZ, _I32, _P], _I32),
+    'motif_chord_decode_step_workspace_bytes': ([_I32] * 5, _SZ),
+    'motif_chord_decode_step': (
+        [_P, _I64, _I64, _I32, _I32, _I32, _P, _P, _F32] + [_P, _I64, _I64, _I64] * 2 + [_P, _I32] + [_P] * 4
+        + [_P, _I32] + _T4 + [_I32] * 5 + [_F32, _F32] + [_P, _SZ, _P], _I32),
     'motif_chord_decode_noalloc_scratch_bytes': ([], _SZ),
     'motif_chord_decode_noalloc': (
         _T4 * 3 + [_P, _I32] + [_P] * 4 + [_P, _I64, _I64, _P, _I32] + _T4 + [_I32] * 5 + [_F32, _F32]

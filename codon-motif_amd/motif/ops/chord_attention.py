@@ -292,6 +292,46 @@ def chord_decode_workspace(B, H, Hkv, L, capacity, D, dtype, device) -> torch.Te
     return torch.empty(max(int(n), 1), dtype=torch.uint8, device=device)
 
 
+def chord_decode_step_serves(proj, H, Hkv, D) -> bool:
+    '''Whether chord_decode_step serves a decode of these projection rows: bf16, head
+    dim 64, at most 16 query rows per kv head, 16-byte aligned rows.'''
+    return (proj.is_cuda and proj.dtype == torch.bfloat16 and proj.dim() == 3 and proj.stride(-1) == 1
+            and D == HEAD_DIM and H % Hkv == 0 and (H // Hkv) * proj.shape[1] <= 16
+            and proj.data_ptr() % 16 == 0 and proj.stride(0) % 8 == 0 and proj.stride(1) % 8 == 0
+            and _lib.available())
+
+
+def chord_decode_step_workspace(B, H, Hkv, L, capacity, device) -> torch.Tensor:
+    '''A zeroed workspace for chord_decode_step at these sizes (its arrival counters must
+    start at zero; every call leaves them zero).'''
+    n = int(_lib.lib().motif_chord_decode_step_workspace_bytes(B, H, Hkv, L, capacity))
+    return torch.zeros(max(n, 1), dtype=torch.uint8, device=device)
+
+
+def chord_decode_step(proj, offsets, q_norm_weight, k_norm_weight, norm_eps, k_cache, v_cache, length_dev, alpha,
+                      beta, mu, ssmax, log_table, num_heads, softmax_scale, eps, workspace):
+    '''A Chord decode step at the device cursor in one launch (new; the reference's
+    motif/block/attention/chord_attn.py:255-265 q / k norms and v, the cache append
+    motif/model/cache.py:170-215 and the decode call of apply_chord_attention): from the
+    projection rows proj [B, L, ncols] (q, k, v at column `offsets`), appends the
+    normalised keys and the values at length_dev, attends over length_dev + L keys with
+    q_start = length_dev and log_n = log_table[q_start + i], advances length_dev by L.
+    Returns out [B, H, L, 64], the same bits as chord_qkv_prep followed by
+    chord_decode_cursor.'''
+    B, L = proj.shape[0], proj.shape[1]
+    Hkv, cap, D = k_cache.shape[1], k_cache.shape[2], k_cache.shape[3]
+    out = torch.empty(B, num_heads, L, D, dtype=proj.dtype, device=proj.device)
+    rc = _lib.lib().motif_chord_decode_step(
+        proj.data_ptr(), proj.stride(0), proj.stride(1), *[int(o) for o in offsets],
+        q_norm_weight.data_ptr(), k_norm_weight.data_ptr(), float(norm_eps),
+        *_lib.t4(k_cache), *_lib.t4(v_cache), length_dev.data_ptr(), cap,
+        alpha.data_ptr(), beta.data_ptr(), mu.data_ptr(), ssmax.data_ptr(), log_table.data_ptr(), log_table.numel(),
+        *_lib.t4(out), B, num_heads, Hkv, L, D, float(softmax_scale), float(eps),
+        workspace.data_ptr(), workspace.numel(), _lib.stream_ptr(proj.device))
+    _lib.check(rc, 'motif_chord_decode_step')
+    return out
+
+
 def chord_decode_cursor(q, k_cache, v_cache, length_dev, alpha, beta, mu, ssmax, log_table, softmax_scale=None,
                         eps=1e-5, log_n=None, workspace=None, library_scratch=False):
     '''Chord attention of L new queries over a fixed-capacity cache (new).

@@ -390,6 +390,34 @@ int motif_chord_decode_noalloc(
     int B, int H, int Hkv, int L, int D, float scale, float eps, int dtype, void *stream);
 
 /*
+ * A ChordAttention decode step over a device cursor in one launch (bf16, head dim 64,
+ * (H / Hkv) * L <= 16 query rows per kv head): what motif_chord_qkv_prep (with its
+ * device cursor) followed by motif_chord_decode computes, with the same bits --
+ * q = RMSNorm(q_h; q_norm_weight) and the new keys / values k_cache[b, g, pos + t] =
+ * RMSNorm(k_g; k_norm_weight), v_cache[b, g, pos + t] = v_g from the projection rows
+ * proj [B, L, ncols] (strides p_sb, p_st; q, k, v of head h / kv head g at columns
+ * q_off + h*64, k_off + g*64, v_off + g*64), attention over *length_dev + L keys, out
+ * [B, H, L, 64], then *length_dev += L.  Replaces motif/block/attention/chord_attn.py:
+ * 255-265 (q / k norms, v), the cache append motif/model/cache.py:170-215 and the
+ * decode call of apply_chord_attention (motif/ops/chord_attention.py:1128-1229).
+ * workspace: motif_chord_decode_step_workspace_bytes(B, H, Hkv, L, capacity) bytes whose
+ * last (B * Hkv + 1) ints are arrival counters that must be zero before the first call
+ * (each call leaves them zero); calls that overlap in time on one workspace race.
+ */
+size_t motif_chord_decode_step_workspace_bytes(int B, int H, int Hkv, int L, int capacity);
+int motif_chord_decode_step(
+    const void *proj, int64_t p_sb, int64_t p_st, int q_off, int k_off, int v_off,
+    const void *q_norm_weight, const void *k_norm_weight, float norm_eps,
+    void *k_cache, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    void *v_cache, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    int *length_dev, int capacity,
+    const float *alpha, const float *beta, const float *mu, const float *ssmax,
+    const float *log_table, int log_table_len,
+    void *out, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    int B, int H, int Hkv, int L, int D, float scale, float eps,
+    void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * ChordAttention input stage for a preallocated KV cache: from the fused q | k | v
  * projection rows proj [B, L, ncols] (strides p_sb, p_st; head h of q at column
  * q_off + h*D, of k at k_off + g*D, of v at v_off + g*D), per head
