@@ -248,6 +248,13 @@ class ChordAttention(BasicAttention):
         B, H, L, D = out.shape
         return out.transpose(1, 2).reshape(B, L, H * D)
 
+    @staticmethod
+    def _heads_out(q):
+        '''An attention destination [B, H, L, D] laid out as [B, L, H, D], so that
+        _merge_heads of it is a view rather than a copy.'''
+        B, H, L, D = q.shape
+        return torch.empty((B, L, H, D), dtype=q.dtype, device=q.device).transpose(1, 2)
+
     # ------------------------------------------------------------------ forward
     def forward(
         self,
@@ -279,7 +286,8 @@ class ChordAttention(BasicAttention):
             alpha, beta, mu, ssmax = self.ggd_params()
             out = apply_chord_attention(q, k, v, alpha, beta, mu, ssmax,
                                         log_n if log_n.dim() == 2 else log_n.expand(B, L),
-                                        q_start=int(q_start), softmax_scale=self.head_dim ** -0.5, eps=GGD_EPS)
+                                        q_start=int(q_start), softmax_scale=self.head_dim ** -0.5, eps=GGD_EPS,
+                                        out=self._heads_out(q))
             return AttentionOutput(output=self._gated_output(self._merge_heads(out), g), past_key_value=cache)
         return self._materialised(q, k, v, g, q_start, log_n, attention_mask, output_attentions, cache)
 
@@ -356,7 +364,7 @@ class ChordAttention(BasicAttention):
         log_n = table[ps.positions()][None]
         alpha, beta, mu, ssmax = self.ggd_params()
         out = apply_chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, log_n, ps,
-                                           softmax_scale=self.head_dim ** -0.5, eps=GGD_EPS)
+                                           softmax_scale=self.head_dim ** -0.5, eps=GGD_EPS, out=self._heads_out(q))
         return AttentionOutput(output=self._gated_output(self._merge_heads(out), g), payload={'k': k, 'v': v})
 
     def _materialised(self, q, k, v, g, q_start, log_n, attention_mask, output_attentions, cache):

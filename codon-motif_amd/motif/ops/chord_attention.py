@@ -143,6 +143,25 @@ def _aligned(t):
     return t if ok else t.contiguous()
 
 
+def _check_out(out, shape, dtype, device):
+    '''A caller's destination: the output's shape, dtype and device, unit feature stride,
+    rows on 16-byte boundaries (the kernels' vector stores).'''
+    if tuple(out.shape) != tuple(shape) or out.dtype != dtype or out.device != device:
+        raise ValueError(f'out must be {tuple(shape)} {dtype} on {device}, got {tuple(out.shape)} {out.dtype} '
+                         f'on {out.device}')
+    per16 = 16 // out.element_size()
+    if out.stride(-1) != 1 or out.data_ptr() % 16 or any(s % per16 for s in out.stride()[:-1]):
+        raise ValueError('out must have unit feature stride and 16-byte aligned rows')
+    return out
+
+
+def _out_for(out, q):
+    '''The kernel's destination: the caller's `out` (checked) or a new [B, H, L, D].'''
+    if out is None:
+        return torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    return _check_out(out, q.shape, q.dtype, q.device)
+
+
 def _launch(q, k, v, alpha, beta, mu, ssmax, log_n, q_start, scale, eps, out, lse=None,
             cu_dev=None, nseq=None, max_seqlen=None, cu_host=None):
     B, H, L, D = q.shape
@@ -198,6 +217,7 @@ def apply_chord_attention(
     q_start: Optional[int] = None,
     softmax_scale: Optional[float] = None,
     eps: float = 1e-5,
+    out: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     '''Chord attention forward on the HIP kernels.
 
@@ -212,9 +232,12 @@ def apply_chord_attention(
         q_start: absolute position of the first query; defaults to S - L.
         softmax_scale: defaults to D ** -0.5.
         eps: GGD epsilon.
+        out: optional [B, H, L, D] destination in q's dtype with unit feature stride (a
+            strided view, e.g. the transpose of a [B, L, H, D] buffer, so the heads come
+            out already merged); not a reference argument.
 
     Returns:
-        [B, H, L, D] in q's dtype.
+        [B, H, L, D] in q's dtype (`out` when given).
 
     Raises:
         ValueError: on unsupported inputs or a negative q_start.
@@ -228,8 +251,10 @@ def apply_chord_attention(
         if _grad_kernels_serve(q, k, v, alpha, beta, mu, ssmax, log_n, q_start):
             scale = q.shape[-1] ** -0.5 if softmax_scale is None else float(softmax_scale)
             qs = k.shape[2] - q.shape[2] if q_start is None else int(q_start)
-            return ChordFunction.apply(q, k, v, alpha, beta, mu, ssmax, log_n, qs, scale, float(eps))
-        return chord_attention_torch(q, k, v, alpha, beta, mu, ssmax, log_n, q_start, softmax_scale, eps)
+            res = ChordFunction.apply(q, k, v, alpha, beta, mu, ssmax, log_n, qs, scale, float(eps))
+        else:
+            res = chord_attention_torch(q, k, v, alpha, beta, mu, ssmax, log_n, q_start, softmax_scale, eps)
+        return res if out is None else _check_out(out, res.shape, res.dtype, res.device).copy_(res)
     if not _lib.available():
         raise RuntimeError('there is no usable HIP backend in the current environment')
     B, H, L, D, Hkv, S = _check_tensors(q, k, v, log_n)
@@ -241,14 +266,14 @@ def apply_chord_attention(
     q_start = int(q_start)
     if q_start < 0:
         raise ValueError(f'q_start must not be negative, got {q_start}')
-    out = torch.empty((B, H, L, D), dtype=q.dtype, device=q.device)
+    out = _out_for(out, q)
     if L == 0:
         return out
     return _launch(q, k, v, alpha, beta, mu, ssmax, log_n, q_start, softmax_scale, eps, out)
 
 
 def apply_chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, log_n, cu_seqlens,
-                                 softmax_scale=None, eps=1e-5):
+                                 softmax_scale=None, eps=1e-5, out=None):
     '''Packed-sequence Chord attention (no reference counterpart).
 
     B == 1; q [1, H, T, D], k/v [1, H_kv, T, D] hold the sequences back to back,
@@ -259,6 +284,7 @@ def apply_chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, log_n, cu_seql
     metadata then spares the call every read back from the device).
     Calls that need gradients run the sequences separately: through the HIP forward /
     backward pair (`ChordFunction`) where it serves, else as differentiable torch runs.
+    `out` is an optional destination, as for apply_chord_attention.
     '''
     if wants_grad(q, k, v, alpha, beta, mu, ssmax, log_n):
         if (q.shape[0] == 1 and q.shape[2] > 0 and k.shape[2] == q.shape[2]
@@ -267,9 +293,11 @@ def apply_chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, log_n, cu_seql
             outs = [apply_chord_attention(q[:, :, a:b], k[:, :, a:b], v[:, :, a:b], alpha, beta, mu, ssmax,
                                           log_n[:, a:b], q_start=0, softmax_scale=softmax_scale, eps=eps)
                     for a, b in zip(cu[:-1], cu[1:]) if b > a]
-            return torch.cat(outs, dim=2)
-        cu_t = cu_seqlens.cu_host if isinstance(cu_seqlens, PackedSeqs) else cu_seqlens
-        return chord_attention_varlen_torch(q, k, v, alpha, beta, mu, ssmax, log_n, cu_t, softmax_scale, eps)
+            res = torch.cat(outs, dim=2)
+        else:
+            cu_t = cu_seqlens.cu_host if isinstance(cu_seqlens, PackedSeqs) else cu_seqlens
+            res = chord_attention_varlen_torch(q, k, v, alpha, beta, mu, ssmax, log_n, cu_t, softmax_scale, eps)
+        return res if out is None else _check_out(out, res.shape, res.dtype, res.device).copy_(res)
     if not _lib.available():
         raise RuntimeError('there is no usable HIP backend in the current environment')
     B, H, L, D, Hkv, S = _check_tensors(q, k, v, log_n)
@@ -279,7 +307,7 @@ def apply_chord_attention_varlen(q, k, v, alpha, beta, mu, ssmax, log_n, cu_seql
     ps = PackedSeqs.of(cu_seqlens, L, q.device)
     if softmax_scale is None:
         softmax_scale = D ** -0.5
-    out = torch.empty((B, H, L, D), dtype=q.dtype, device=q.device)
+    out = _out_for(out, q)
     if L == 0:
         return out
     return _launch(q, k, v, alpha, beta, mu, ssmax, log_n, 0, softmax_scale, eps, out,

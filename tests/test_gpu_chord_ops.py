@@ -246,3 +246,77 @@ def test_varlen_other_dtypes_and_head_dims(dtype, D):
             assert (out[:, :, a:b].double().cpu() - ref).abs().max().item() <= 1e-4
         else:
             assert_bf16_close(out[:, :, a:b], ref, what=f'{dtype} D={D} rows {a}:{b}')
+
+
+def _merged(q):
+    B, H, L, D = q.shape
+    return torch.empty((B, L, H, D), dtype=q.dtype, device=q.device).transpose(1, 2)
+
+
+@pytest.mark.parametrize('dtype,D,L,S', [
+    (torch.bfloat16, 64, 2048, 2048),   # the prefill kernel
+    (torch.bfloat16, 64, 1, 900),       # a decode-shaped call (split-K kernel)
+    (torch.float32, 64, 100, 300),
+    (torch.bfloat16, 48, 77, 77),       # a padded head dim (output copied back)
+])
+@torch.no_grad()
+def test_out_destination_equals_new_output(dtype, D, L, S):
+    '''`out=` a [B, L, H, D] buffer's transposed view: the same values bit for bit as a
+    new [B, H, L, D] output, written in place (the heads come out merged).'''
+    ops = _ops()
+    B, H, Hkv = 2, 12, 3
+    q, k, v, alpha, beta, mu, ssmax = chord_inputs(B, H, Hkv, L, S, seed=21, D=D)
+    q, k, v = (t.to(DEV, dtype) for t in (q, k, v))
+    params = [t.to(DEV) for t in (alpha, beta, mu, ssmax)]
+    log_n = _log_n(B, L, S - L).to(DEV)
+    ref = ops.apply_chord_attention(q, k, v, *params, log_n)
+    dst = _merged(q)
+    got = ops.apply_chord_attention(q, k, v, *params, log_n, out=dst)
+    assert got is dst and dst.transpose(1, 2).is_contiguous()
+    assert torch.equal(got, ref)
+
+
+@torch.no_grad()
+def test_varlen_out_destination_equals_new_output():
+    ops = _ops()
+    lens = [130, 1, 64, 0, 257]
+    cu = torch.tensor([0] + list(torch.cumsum(torch.tensor(lens), 0)), dtype=torch.int32).to(DEV)
+    T, H, Hkv = sum(lens), 12, 3
+    q, k, v, alpha, beta, mu, ssmax = chord_inputs(1, H, Hkv, T, T, seed=22)
+    args = [t.to(DEV) for t in (q, k, v, alpha, beta, mu, ssmax)]
+    log_n = torch.cat([ochord.log_n_table(0, n) for n in lens]).float()[None].to(DEV)
+    ref = ops.apply_chord_attention_varlen(*args, log_n, cu)
+    dst = _merged(args[0])
+    assert ops.apply_chord_attention_varlen(*args, log_n, cu, out=dst) is dst
+    assert torch.equal(dst, ref)
+
+
+def test_out_destination_under_autograd():
+    '''With gradients recorded the result is copied into `out`; the gradients through
+    `out` equal those of the call without it.'''
+    ops = _ops()
+    B, H, Hkv, L = 1, 4, 2, 200
+    base = chord_inputs(B, H, Hkv, L, L, seed=23)
+    log_n = _log_n(B, L, 0).to(DEV)
+    grads = []
+    for use_out in (False, True):
+        q, k, v = (t.to(DEV, torch.bfloat16).requires_grad_() for t in base[:3])
+        params = [t.to(DEV) for t in base[3:]]
+        dst = _merged(q.detach()) if use_out else None
+        o = ops.apply_chord_attention(q, k, v, *params, log_n, q_start=0, out=dst)
+        (o.float() * torch.linspace(-1, 1, 64, device=DEV)).sum().backward()
+        grads.append([o.detach().clone(), q.grad, k.grad, v.grad])
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
+
+
+def test_out_destination_rejects_wrong_buffers():
+    ops = _ops()
+    B, H, Hkv, L = 1, 4, 2, 16
+    q, k, v, alpha, beta, mu, ssmax = (t.to(DEV) for t in chord_inputs(B, H, Hkv, L, L, seed=24))
+    log_n = _log_n(B, L, 0).to(DEV)
+    for bad in (torch.empty((B, H, L, 32), dtype=q.dtype, device=DEV),           # shape
+                torch.empty((B, H, L, 64), dtype=torch.float32, device=DEV),     # dtype
+                torch.empty((B, H, 64, L), dtype=q.dtype, device=DEV).transpose(2, 3)):  # feature stride
+        with torch.no_grad(), pytest.raises(ValueError):
+            ops.apply_chord_attention(q, k, v, alpha, beta, mu, ssmax, log_n, q_start=0, out=bad)
