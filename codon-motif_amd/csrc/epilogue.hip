@@ -14,6 +14,13 @@
 //                          gdn_attn.py:193-195; softplus threshold 20)
 //   mul_sigmoid_kernel     y = T(x * T(sigmoid(g)))             (Chord output gate,
 //                          motif/block/attention/chord_attn.py:254, :313)
+//   residual_fold_kernel   f = T(T(a * T(sigmoid(g))) + b) (T(a + b) without a gate) and
+//                          p = T(..T(T(c_0 + c_1) + c_2) .. + f) over the block's running-sum
+//                          addends c_0 .. c_{n-1} not yet summed: a decoder's output and
+//                          every add of the block's running sum since the last one that was
+//                          stored, one add (and one rounding) each, in the reference's order
+//                          (motif/block/decoder.py:205-213); without a / b only the sum of
+//                          the c_j
 #include "capi_internal.h"
 #include "common.h"
 
@@ -207,6 +214,79 @@ __global__ void __launch_bounds__(256) mul_sigmoid_kernel(EwArgs a) {
   st16(static_cast<T *>(a.y) + m * a.y_rs + c, V16<T>::pack(x));
 }
 
+// ------------------------------------------------------------ residual fold
+constexpr int kMaxChain = 8;
+struct FoldArgs {
+  const void *a; int64_t a_rs;   // branch output (NULL: only the sum of the c_j)
+  const void *g; int64_t g_rs;   // gate pre-activation of a (may be NULL)
+  const void *b; int64_t b_rs;   // second branch
+  const void *c[kMaxChain]; int64_t c_rs[kMaxChain];
+  int nc;                        // addends c_j (0: no running sum)
+  void *f; int64_t f_rs;
+  void *p; int64_t p_rs;
+  int M, N;
+};
+
+// One 16-byte chunk of a row per thread; every load is issued before the arithmetic.
+template <typename T, bool BRANCH, bool GATE>
+__global__ void __launch_bounds__(256) residual_fold_kernel(FoldArgs a) {
+  constexpr int E = V16<T>::N;
+  const int cpr = a.N / E;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= static_cast<int64_t>(a.M) * cpr) return;
+  const int64_t m = i / cpr;
+  const int c = static_cast<int>(i - m * cpr) * E;
+  uint4 ra{}, rg{}, rb{};
+  if (BRANCH) {
+    ra = ld16(static_cast<const T *>(a.a) + m * a.a_rs + c);
+    if (GATE) rg = ld16(static_cast<const T *>(a.g) + m * a.g_rs + c);
+    rb = ld16(static_cast<const T *>(a.b) + m * a.b_rs + c);
+  }
+  uint4 rc[kMaxChain];
+#pragma unroll
+  for (int j = 0; j < kMaxChain; ++j)
+    rc[j] = j < a.nc ? ld16(static_cast<const T *>(a.c[j]) + m * a.c_rs[j] + c) : uint4{0u, 0u, 0u, 0u};
+  float f[E];
+  if (BRANCH) {
+    float x[E], y[E];
+    V16<T>::unpack(ra, x);
+    V16<T>::unpack(rb, y);
+    if (GATE) {
+      float g[E];
+      V16<T>::unpack(rg, g);
+#pragma unroll
+      for (int e = 0; e < E; ++e) x[e] = V16<T>::round(x[e] * V16<T>::round(1.f / (1.f + expf(-g[e]))));
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) f[e] = V16<T>::round(x[e] + y[e]);
+    st16(static_cast<T *>(a.f) + m * a.f_rs + c, V16<T>::pack(f));
+  }
+  if (a.nc == 0) return;
+  float p[E];
+  V16<T>::unpack(rc[0], p);
+#pragma unroll
+  for (int j = 1; j < kMaxChain; ++j) {
+    if (j >= a.nc) break;
+    float q[E];
+    V16<T>::unpack(rc[j], q);
+#pragma unroll
+    for (int e = 0; e < E; ++e) p[e] = V16<T>::round(p[e] + q[e]);
+  }
+  if (BRANCH) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) p[e] = p[e] + f[e];
+  }
+  st16(static_cast<T *>(a.p) + m * a.p_rs + c, V16<T>::pack(p));
+}
+
+template <typename T>
+int launch_fold(const FoldArgs &a, dim3 grid, hipStream_t s) {
+  if (!a.a) residual_fold_kernel<T, false, false><<<grid, 256, 0, s>>>(a);
+  else if (a.g) residual_fold_kernel<T, true, true><<<grid, 256, 0, s>>>(a);
+  else residual_fold_kernel<T, true, false><<<grid, 256, 0, s>>>(a);
+  return check_launch("residual_fold_kernel");
+}
+
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
@@ -306,4 +386,37 @@ extern "C" int motif_mul_sigmoid(const void *x, int64_t x_rs, const void *g, int
   if (dtype == MOTIF_BF16) mul_sigmoid_kernel<bf16_t><<<grid, block, 0, s>>>(a);
   else mul_sigmoid_kernel<float><<<grid, block, 0, s>>>(a);
   return check_launch("mul_sigmoid_kernel");
+}
+
+extern "C" int motif_residual_fold(const void *a_, int64_t a_rs, const void *g, int64_t g_rs, const void *b_,
+                                   int64_t b_rs, const void *const *chain, const int64_t *chain_rs, int nchain,
+                                   void *f, int64_t f_rs, void *p, int64_t p_rs, int M, int N, int dtype,
+                                   void *stream) {
+  using namespace motif;
+  if (M < 0 || N <= 0) return set_error(MOTIF_ERR_INVALID, "residual_fold: bad size");
+  if (nchain < 0 || nchain > kMaxChain) return set_error(MOTIF_ERR_UNSUPPORTED, "residual_fold: 0 to 8 addends");
+  if (a_ ? (!b_ || !f) : (nchain < 2 || g || b_ || f))
+    return set_error(MOTIF_ERR_INVALID, "residual_fold: a and b together (with f), or only two or more addends");
+  if (nchain > 0 && (!chain || !chain_rs || !p)) return set_error(MOTIF_ERR_INVALID, "residual_fold: NULL pointer");
+  if (dtype != MOTIF_F32 && dtype != MOTIF_BF16) return set_error(MOTIF_ERR_UNSUPPORTED, "residual_fold: dtype");
+  const int vec = dtype == MOTIF_BF16 ? 8 : 4;
+  FoldArgs a{};
+  a.a = a_; a.a_rs = a_rs; a.g = a_ ? g : nullptr; a.g_rs = g_rs; a.b = b_; a.b_rs = b_rs;
+  a.nc = nchain; a.f = f; a.f_rs = f_rs; a.p = nchain > 0 ? p : nullptr; a.p_rs = p_rs; a.M = M; a.N = N;
+  bool ok = N % vec == 0;
+  if (a_) ok = ok && aligned16(a_) && aligned16(b_) && aligned16(f) && (a_rs | b_rs | f_rs) % vec == 0 &&
+               (!a.g || (aligned16(g) && g_rs % vec == 0));
+  for (int j = 0; j < nchain; ++j) {
+    if (!chain[j]) return set_error(MOTIF_ERR_INVALID, "residual_fold: NULL addend");
+    a.c[j] = chain[j];
+    a.c_rs[j] = chain_rs[j];
+    ok = ok && aligned16(chain[j]) && chain_rs[j] % vec == 0;
+  }
+  if (nchain > 0) ok = ok && aligned16(p) && p_rs % vec == 0;
+  if (!ok) return set_error(MOTIF_ERR_UNSUPPORTED, "residual_fold: rows must be 16-byte aligned");
+  if (M == 0) return MOTIF_OK;
+  const int64_t n = static_cast<int64_t>(M) * (N / vec);
+  const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return dtype == MOTIF_BF16 ? launch_fold<bf16_t>(a, grid, s) : launch_fold<float>(a, grid, s);
 }

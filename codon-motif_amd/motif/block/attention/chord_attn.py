@@ -266,6 +266,29 @@ class ChordAttention(BasicAttention):
         past_key_value: Optional[KVLayerCache] = None,
         section_log_len: Optional[torch.Tensor] = None,
     ) -> AttentionOutput:
+        res = self._attend(hidden_states, kv_states, attention_mask, output_attentions, embedding_start,
+                           past_key_value, section_log_len)
+        if isinstance(res, AttentionOutput):
+            return res
+        merged, g, cache = res
+        return AttentionOutput(output=self._gated_output(merged, g), past_key_value=cache)
+
+    def prefill_parts(self, hidden_states: torch.Tensor, past_key_value: Optional[KVLayerCache] = None,
+                      embedding_start: Union[int, torch.Tensor] = 0):
+        '''A self-attention call on the prefill kernels, stopped before the output side:
+        (merged heads [B, L, H * D], the output gate's pre-activation g [B, L, H * D],
+        cache), so that the caller applies o_proj and the gate itself (the decoder folds
+        the gate into its residual pass).  None, before anything runs, for every call
+        that forward serves another way (decode at the cache cursor, the materialised
+        path).'''
+        return self._attend(hidden_states, None, None, False, embedding_start, past_key_value, None,
+                            parts_only=True)
+
+    def _attend(self, hidden_states, kv_states, attention_mask, output_attentions, embedding_start,
+                past_key_value, section_log_len, parts_only=False):
+        '''forward up to the output side: (merged heads, gate pre-activation, cache) on
+        the prefill kernels, or the finished AttentionOutput of the cursor / materialised
+        routes (None for those with `parts_only`).'''
         cache = past_key_value if isinstance(past_key_value, KVLayerCache) else None
         self_attn = kv_states is None or kv_states is hidden_states
         B, L, _ = hidden_states.shape
@@ -277,7 +300,9 @@ class ChordAttention(BasicAttention):
                   and self._kernel_serves(hidden_states))
 
         if kernel and self_attn and section_log_len is None and self._on_cursor(hidden_states, cache, q_start):
-            return self._cursor_step(hidden_states, cache)
+            return None if parts_only else self._cursor_step(hidden_states, cache)
+        if parts_only and not kernel:
+            return None
 
         fused = kernel and self_attn and self._prep_fusable(hidden_states, cache)
         q, k, v, g = self._inputs(hidden_states, None if self_attn else kv_states, cache, fused)
@@ -288,7 +313,7 @@ class ChordAttention(BasicAttention):
                                         log_n if log_n.dim() == 2 else log_n.expand(B, L),
                                         q_start=int(q_start), softmax_scale=self.head_dim ** -0.5, eps=GGD_EPS,
                                         out=self._heads_out(q))
-            return AttentionOutput(output=self._gated_output(self._merge_heads(out), g), past_key_value=cache)
+            return self._merge_heads(out), g, cache
         return self._materialised(q, k, v, g, q_start, log_n, attention_mask, output_attentions, cache)
 
     def _cursor_step(self, x, cache: StaticKVLayerCache) -> AttentionOutput:

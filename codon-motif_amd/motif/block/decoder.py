@@ -13,7 +13,8 @@ from motif.model.cache import DecoderBlockCache, GatedDeltaAttentionLayerCache, 
 from motif.model.config import MotifChordConfig
 from motif.ops import RMSNorm
 from motif.ops.attn_res import apply_block_attn_res, attn_res_read_norms
-from motif.ops.epilogue import swiglu, usable
+from motif.ops.autograd_path import wants_grad
+from motif.ops.epilogue import residual_fold, swiglu, usable
 from motif.ops.linear_rows import linear_rows_dual, linear_rows_pair, rows_eligible, sum_weights
 
 
@@ -75,14 +76,14 @@ def _split_step(decoder, x, m, layer_cache, mask, position, prev):
     return linear_rows_dual(o, w_out, act, w_down, gate=g_pre, aux2=prev)
 
 
-def _prefill_step(decoder, x, m, layer_cache, prev):
+def _prefill_step(decoder, x, m, layer_cache):
     '''A GatedDelta decoder's prefill with its two output projections as one library GEMM:
     the layer writes its o_proj input y and the MLP its SwiGLU output s side by side
     into one [B, L, H dv + I] buffer, and f_h = [y | s] [W_o | W_down]^T (no reference
     counterpart as one op: motif/block/decoder.py:205-210 computes o_proj(y) and
     down_proj(s) as two GEMMs, rounds each to the activation dtype and adds them; here
-    the sum is accumulated in fp32 and rounded once).  partial = prev + f_h as the
-    reference adds it.  Returns (f_h, partial), or None (before anything ran) when the
+    the sum is accumulated in fp32 and rounded once).  Returns f_h (the caller registers
+    it with the block's running-sum add put off), or None (before anything ran) when the
     step does not qualify: not a GatedDelta layer, decode-sized input, autograd, biases,
     or inputs the fused prefill kernels do not serve.'''
     attn, mlp = decoder.attn, decoder.mlp
@@ -99,8 +100,39 @@ def _prefill_step(decoder, x, m, layer_cache, prev):
     if not usable(buf[..., hv:]) or not attn.prefill_core(x, layer_cache, buf[..., :hv]):
         return None
     swiglu(torch.nn.functional.linear(m, mlp.gate_up_proj.weight), out=buf[..., hv:])
-    f_h = torch.nn.functional.linear(buf, w)
-    return f_h, (None if prev is None else prev + f_h)
+    return torch.nn.functional.linear(buf, w)
+
+
+def _chord_prefill_step(decoder, x, m, layer_cache, mask, position, attn_res):
+    '''A Chord decoder's prefill with its output side in one elementwise pass: the layer
+    stops before its output gate (o = o_proj(attention), g its pre-activation), the MLP
+    runs, and motif.ops.epilogue.residual_fold forms f_h = o * sigmoid(g) + mlp and the
+    block's running sum with every add put off since it was last stored -- the
+    reference's ops in its order, one rounding each (motif/block/attention/
+    chord_attn.py:254, motif/block/decoder.py:205-213).  Returns (f_h, partial, layer
+    cache), or None (before anything ran) when the call takes another route.'''
+    attn, mlp = decoder.attn, decoder.mlp
+    if (not isinstance(attn, ChordAttention) or x.dim() != 3 or x.dtype != torch.bfloat16 or mask is not None
+            or attn.o_proj.bias is not None or mlp._fused(m) or wants_grad(x, m, attn, mlp)):
+        return None
+    chain = attn_res.pending_sum()
+    if not chain:
+        p = attn_res.partial_block
+        chain = [] if p is None else [p]
+    if chain and tuple(chain[0].shape) != (*x.shape[:-1], attn.o_proj.out_features):
+        return None
+    parts = attn.prefill_parts(x, past_key_value=layer_cache, embedding_start=position)
+    if parts is None:
+        return None
+    merged, g_pre, layer_cache = parts
+    o = torch.nn.functional.linear(merged, attn.o_proj.weight)
+    f_h, partial = residual_fold(o, mlp(m), gate=g_pre, chain=chain)
+    return f_h, partial, layer_cache
+
+
+def _prev(attn_res, like):
+    p = attn_res.partial_block
+    return p if p is not None and p.shape == like.shape else None
 
 
 class DecoderBlock(nn.Module):
@@ -149,16 +181,26 @@ class DecoderBlock(nn.Module):
         # (The MLP on a second stream overlapped little, now and then let a prefill read
         # memory that the other stream had taken over, and kept whole-CU attention
         # workgroups waiting for CUs.)
+        # At prefill the GatedDelta decoders put the block's running-sum add off; the
+        # next Chord decoder (or the first read of partial_block) folds every put-off add
+        # into one pass.
         for i, decoder in enumerate(self.features):
             x, m = self._read(attn_res, i, decoder)
             if cu_seqlens is None:
-                prev = attn_res.partial_block
-                prev = prev if prev is not None and prev.shape == m.shape else None
+                layer_cache = cache.attn[i] if use_attn_cache else None
                 done = None
-                if use_attn_cache:
-                    done = _split_step(decoder, x, m, cache.attn[i], mask, position, prev)
+                if use_attn_cache and decoder.mlp._fused(m):
+                    done = _split_step(decoder, x, m, layer_cache, mask, position, _prev(attn_res, m))
                 if done is None:
-                    done = _prefill_step(decoder, x, m, cache.attn[i] if use_attn_cache else None, prev)
+                    f_h = _prefill_step(decoder, x, m, layer_cache)
+                    if f_h is not None:
+                        attn_res.update_increment(f_h, defer=True)
+                        continue
+                    tail = _chord_prefill_step(decoder, x, m, layer_cache, mask, position, attn_res)
+                    if tail is not None:
+                        if use_attn_cache:
+                            cache.attn[i] = tail[2]
+                        done = tail[:2]
                 if done is not None:
                     attn_res.update_increment(*done)
                     continue

@@ -35,6 +35,8 @@ from typing import Iterator, List, Optional, Sequence, Tuple
 
 import torch
 
+from motif.ops.epilogue import MAX_CHAIN, residual_fold
+
 PAGE = 256  # positions per allocation unit of a growing key / value slab
 
 
@@ -371,9 +373,32 @@ class AttnResCache:
     def __init__(self, blocks: Optional[List[torch.Tensor]] = None, partial_block: Optional[torch.Tensor] = None,
                  seq_len: int = 0, chunk_len: int = 0):
         self.blocks: List[torch.Tensor] = [] if blocks is None else list(blocks)
+        self._chain: List[torch.Tensor] = []  # addends of the running sum not yet summed
         self.partial_block = partial_block
         self.seq_len = seq_len
         self.chunk_len = chunk_len
+
+    @property
+    def partial_block(self) -> Optional[torch.Tensor]:
+        '''The running sum of the increments.  Increments registered with `defer=True`
+        are added here, on first access, in one pass: one add and one rounding each, in
+        registration order (motif.ops.epilogue.residual_fold), so the value equals the
+        add-per-increment one.'''
+        if self._chain:
+            chain, self._chain = self._chain, []
+            self._partial = chain[0] if len(chain) == 1 else residual_fold(None, None, chain=chain)[1]
+        return self._partial
+
+    @partial_block.setter
+    def partial_block(self, value: Optional[torch.Tensor]) -> None:
+        self._partial = value
+        self._chain = []
+
+    def pending_sum(self) -> List[torch.Tensor]:
+        '''The running sum's addends that are not summed yet, in order (the stored sum
+        first, when there is one); empty when no add is put off.  A caller that folds
+        them into its own pass registers its result with update_increment(f_h, partial).'''
+        return list(self._chain)
 
     def aligned_values(self) -> List[torch.Tensor]:
         '''Every source, each cut to the last `chunk_len` positions (the shortest entry's
@@ -396,10 +421,22 @@ class AttnResCache:
         self.blocks = [hidden_states]
         self.chunk_len = n
 
-    def update_increment(self, f_h: torch.Tensor, partial: Optional[torch.Tensor] = None) -> None:
+    def update_increment(self, f_h: torch.Tensor, partial: Optional[torch.Tensor] = None,
+                         defer: bool = False) -> None:
         '''Register decoder output f_h.  `partial` (new, optional) is partial_block + f_h
-        already computed by the caller (the decode projection kernel folds it in).'''
+        already computed by the caller (the decode projection kernel folds it in).
+        `defer` (new): put the add partial_block + f_h off until partial_block is read
+        or a caller folds pending_sum() into its own pass (same value; up to
+        MAX_CHAIN adds are summed in one pass).'''
         self.blocks.append(f_h)
+        if partial is None and defer and not self._chain and (
+                self._partial is None or self._partial.shape == f_h.shape):
+            self._chain = ([self._partial] if self._partial is not None else []) + [f_h]
+            return
+        if partial is None and defer and self._chain and len(self._chain) < MAX_CHAIN and \
+                self._chain[0].shape == f_h.shape:
+            self._chain.append(f_h)
+            return
         if partial is None:
             prev = self.partial_block
             if prev is None:

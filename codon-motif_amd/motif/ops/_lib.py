@@ -60,6 +60,7 @@ _SIGNATURES = {
     'motif_mul_sigmoid': ([_P, _I64, _P, _I64, _P, _I64, _I32, _I32, _I32, _P], _I32),
     'motif_swiglu': ([_P, _I64, _P, _I64, _I32, _I32, _I32, _P], _I32),
     'motif_add_fold': ([_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I32, _I32, _I32, _P], _I32),
+    'motif_residual_fold': ([_P, _I64] * 3 + [_P, _P, _I32, _P, _I64, _P, _I64, _I32, _I32, _I32, _P], _I32),
     'motif_attn_res_read_norms': (
         [_P, _P, _P, _I32, _P, _P, _F32, _P, _I64, _I64, _I32, _P, _P, _P, _P, _F32] + [_I32] * 4 + [_P], _I32),
     'motif_attn_res_read': (

@@ -7,12 +7,16 @@ over HBM, rounding to the activation dtype where the reference's separate ops ro
 - `swiglu`: out * SiLU(gate) of the fused gate/up projection (motif/ops/swiglu.py:252-253).
 - `add_fold`: f = a + b and p' = p + f, the decoder's f_h and the block's running sum
   (motif/block/decoder.py:208-213).
+- `residual_fold`: the same with the Chord output gate on a and the running sum's
+  put-off adds folded in: f = a * sigmoid(g) + b, p = ((c_0 + c_1) + ..) + f.
 
 `usable(*tensors)` says whether the kernels serve a call (ROCm, bf16/fp32, 16-byte
 aligned rows, no autograd); callers keep the torch formula otherwise.  Each wrapper
 also computes its torch formula itself when any input or weight needs a gradient
 (the kernels are forward-only), so no caller can drop a gradient by accident.
 '''
+import ctypes
+
 import torch
 import torch.nn.functional as F
 
@@ -101,6 +105,73 @@ def add_fold(a, b, p=None):
                                    _lib.stream_ptr(a.device))
     _lib.check(rc, 'motif_add_fold')
     return f, po
+
+
+MAX_CHAIN = 8
+
+
+def _fold_torch(a, g, b, chain):
+    '''residual_fold as torch ops: each op rounds to the dtype as the reference's do.'''
+    f = None
+    if a is not None:
+        f = (a if g is None else a * torch.sigmoid(g)) + b
+    if not chain:
+        return f, None
+    p = chain[0]
+    for c in list(chain[1:]) + ([f] if f is not None else []):
+        p = p + c
+    return f, p
+
+
+def _row_view(t):
+    '''[M, N] view of t's rows (unit feature stride), or None when there is none.'''
+    if t.stride(-1) != 1:
+        return None
+    try:
+        return t.view(-1, t.shape[-1])
+    except RuntimeError:
+        return None
+
+
+def residual_fold(a, b, gate=None, chain=()):
+    '''(f, p) with f = a * sigmoid(gate) + b (a + b without a gate) and
+    p = ((chain[0] + chain[1]) + ..) + f, one add and one rounding each in that order
+    (None without a chain); with a and b None, p sums the chain only.  Every operand
+    [..., N] of one shape and dtype (row views allowed); at most MAX_CHAIN addends.
+    Calls the kernel does not serve (autograd, other dtypes, unaligned rows) take the
+    same ops in torch.'''
+    chain = list(chain)
+    ops = [t for t in (a, gate, b) if t is not None] + chain
+    if not ops:
+        raise ValueError('residual_fold: nothing to sum')
+    if a is None and (gate is not None or b is not None or len(chain) < 2):
+        raise ValueError('residual_fold: a and b together, or a chain of two or more addends')
+    if (a is None) != (b is None):
+        raise ValueError('residual_fold: a and b together')
+    shape = ops[0].shape
+    N = shape[-1]
+    rows = [_row_view(t) for t in ops]
+    if (len(chain) > MAX_CHAIN or wants_grad(*ops) or any(t.shape != shape for t in ops)
+            or any(r is None for r in rows) or not usable(*rows)):
+        return _fold_torch(a, gate, b, chain)
+    M = rows[0].shape[0]
+    dev, dt = ops[0].device, ops[0].dtype
+    it = iter(rows)
+    a2 = next(it) if a is not None else None
+    g2 = next(it) if gate is not None else None
+    b2 = next(it) if b is not None else None
+    c2 = list(it)
+    f = torch.empty(shape, dtype=dt, device=dev) if a is not None else None
+    p = torch.empty(shape, dtype=dt, device=dev) if chain else None
+    n = len(c2)
+    ptrs = (ctypes.c_void_p * max(n, 1))(*[t.data_ptr() for t in c2])
+    rs = (ctypes.c_int64 * max(n, 1))(*[t.stride(0) for t in c2])
+    rc = _lib.lib().motif_residual_fold(
+        _lib.ptr(a2), 0 if a2 is None else a2.stride(0), _lib.ptr(g2), 0 if g2 is None else g2.stride(0),
+        _lib.ptr(b2), 0 if b2 is None else b2.stride(0), ptrs, rs, n,
+        _lib.ptr(f), N, _lib.ptr(p), N, M, N, _lib.dtype_code(dt), _lib.stream_ptr(dev))
+    _lib.check(rc, 'motif_residual_fold')
+    return f, p
 
 
 def gdn_gates(a, b, a_log, dt_bias):

@@ -588,6 +588,21 @@ int motif_add_fold(const void *a, int64_t a_rs, const void *b, int64_t b_rs, con
                    void *f, int64_t f_rs, void *p_out, int64_t po_rs, int M, int N, int dtype, void *stream);
 
 /*
+ * A decoder's output and the block's running sum in one pass, with the adds of the
+ * running sum that were put off since it was last stored:
+ *   f = T(T(a * T(sigmoid(g))) + b)        (f = T(a + b) when g is NULL)
+ *   p = T(..T(T(c_0 + c_1) + c_2) .. + f)  over the addends chain[0 .. nchain)
+ * one add and one rounding to T each, in the order of the reference's adds
+ * (motif/block/decoder.py:205-213: f_h = attn + mlp, then partial_block + f_h per
+ * decoder; motif/block/attention/chord_attn.py:254: the Chord output gate).  nchain = 0:
+ * no p.  With a, g, b and f NULL: p = the sum of the nchain >= 2 addends only.  All
+ * [M, N] row-major with their row strides, 16-byte aligned; at most 8 addends.
+ */
+int motif_residual_fold(const void *a, int64_t a_rs, const void *g, int64_t g_rs, const void *b, int64_t b_rs,
+                        const void *const *chain, const int64_t *chain_rs, int nchain, void *f, int64_t f_rs,
+                        void *p, int64_t p_rs, int M, int N, int dtype, void *stream);
+
+/*
  * GDN gates in one pass: beta = sigmoid(b), g = -exp(A_log) * softplus(a + dt_bias)
  * (softplus threshold 20), each step rounded to T as the reference's separate ops
  * round (motif/block/attention/gdn_attn.py:193-195).  a, b [B, L, H] (strides a_sb,

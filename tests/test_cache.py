@@ -121,6 +121,39 @@ def test_attn_res_history_alignment_and_partial_sum():
     assert c.is_empty and c.current_seq_len == 0
 
 
+def test_attn_res_deferred_adds_equal_eager_adds():
+    """update_increment(defer=True) puts the running-sum adds off; partial_block then
+    sums them in registration order with one rounding per add (bf16 here), equal bit
+    for bit to the add-per-increment sums, and pending_sum lists what is put off."""
+    g = torch.Generator().manual_seed(3)
+    fs = [(torch.randn(2, 5, 8, generator=g) * 10 ** (i % 3)).to(torch.bfloat16) for i in range(11)]
+    eager, lazy = AttnResCache(), AttnResCache()
+    for c in (eager, lazy):
+        c.init_embedding(torch.zeros(2, 5, 8, dtype=torch.bfloat16))
+    for i, f in enumerate(fs):
+        eager.update_increment(f)
+        lazy.update_increment(f, defer=True)
+        if i == 0:
+            assert lazy.pending_sum() == [f]  # the first increment is the sum itself
+        if i == 2:
+            assert len(lazy.pending_sum()) == 3 and torch.equal(lazy.partial_block, eager.partial_block)
+            assert lazy.pending_sum() == []   # read: summed and stored
+    assert len(lazy.pending_sum()) <= 8       # at most eight addends wait
+    assert torch.equal(lazy.partial_block, eager.partial_block)
+    assert lazy.num_sources() == eager.num_sources() == 12
+    # a stored sum heads the pending list; a caller's own result replaces the list
+    c = AttnResCache(partial_block=fs[0])
+    c.update_increment(fs[1], defer=True)
+    assert c.pending_sum() == [fs[0], fs[1]]
+    c.update_increment(fs[2], partial=fs[3])
+    assert c.pending_sum() == [] and c.partial_block is fs[3]
+    # an increment of another shape is added at once (the stored sum first)
+    c = AttnResCache(partial_block=fs[0])
+    c.update_increment(fs[1], defer=True)
+    c.update_increment(torch.ones(2, 1, 8, dtype=torch.bfloat16), defer=True)
+    assert c.pending_sum() == [] and c.partial_block.shape == (2, 6, 8)
+
+
 class _Dec:
     def __init__(self, ctype, heads=4):
         self.cache_type = ctype

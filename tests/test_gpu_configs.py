@@ -68,9 +68,10 @@ class _Tap:
     with a cache) the cache contents before the call, keeping batch rows `rows`.  While
     active, decode steps run layer by layer (the decoder's split step, which batches the
     layer's projections with the MLP's and equals the layer-by-layer step bit for bit,
-    calls no layer forward), and so do GatedDelta prefills (the decoder's prefill step
-    applies o_proj inside the shared output GEMM, so no layer output exists to record;
-    tests/test_gpu_prefill_step.py compares the two forms).'''
+    calls no layer forward), and so do GatedDelta and Chord prefills (the decoder's
+    prefill steps apply o_proj inside the shared output GEMM or the output gate inside
+    the residual pass, so no layer output exists to record; tests/test_gpu_prefill_step.py
+    and tests/test_gpu_residual_fold.py compare the forms).'''
 
     def __init__(self, model, rows=None):
         self.model, self.rows, self.records = model, rows, []
@@ -94,6 +95,7 @@ class _Tap:
         import motif.block.decoder as dec
         self._split, dec._split_step = dec._split_step, (lambda *a, **k: None)
         self._prefill, dec._prefill_step = dec._prefill_step, (lambda *a, **k: None)
+        self._chord, dec._chord_prefill_step = dec._chord_prefill_step, (lambda *a, **k: None)
         self.layers = []
         for bi, block in enumerate(self.model.blocks):
             for li, dec in enumerate(block.features):
@@ -121,6 +123,7 @@ class _Tap:
         import motif.block.decoder as dec
         dec._split_step = self._split
         dec._prefill_step = self._prefill
+        dec._chord_prefill_step = self._chord
         for attn in self.layers:
             del attn.forward, attn.forward_varlen
 

@@ -4,7 +4,7 @@ fp32 and rounded once, against the reference's form (two GEMMs, each rounded, th
 added; the layer forward followed by SwiGLU.forward_residual) at the 172M model's shapes.
 
 - f_h is within one bf16 rounding of the float64 sum of the same two products (the
-  reference's form is three roundings away), partial is prev + f_h as torch adds it;
+  reference's form is three roundings away);
 - the layer cache the step updates (state and conv tails, from zero and carried on
   from a first chunk) equals the layer forward's bit for bit;
 - inside a whole model prefill (config-3 model, T = 1024) every GatedDelta decoder's
@@ -37,7 +37,7 @@ def _exact(decoder, x, m):
     return (y.double() @ attn.o_proj.weight.double().t()) + (s.double() @ mlp.down_proj.weight.double().t())
 
 
-def _check_one(decoder, x, m, prev, f, p, what):
+def _check_one(decoder, x, m, f, what):
     f64 = _exact(decoder, x, m)
     d = (f.double() - f64).abs()
     bound = 2.0 ** -8 * f64.abs() + 1e-5 * f64.abs().max()
@@ -47,10 +47,6 @@ def _check_one(decoder, x, m, prev, f, p, what):
     e_fused, e_ref = d.mean().item(), (f_ref.double() - f64).abs().mean().item()
     print(f'{what}: mean |f_h - exact| fused {e_fused:.3e}, two roundings then add {e_ref:.3e}', flush=True)
     assert e_fused <= e_ref, what
-    if prev is None:
-        assert p is None
-    else:
-        assert torch.equal(p, prev + f), what
 
 
 @torch.no_grad()
@@ -62,9 +58,8 @@ def test_prefill_step_one_decoder(L):
     g = gen(3)
     x = torch.randn(1, L, 768, generator=g).to(DEV, torch.bfloat16)
     m = torch.randn(1, L, 768, generator=g).to(DEV, torch.bfloat16)
-    prev = (torch.randn(1, L, 768, generator=g) * 0.1).to(DEV, torch.bfloat16)
-    f, p = _prefill_step(dec, x, m, None, prev)
-    _check_one(dec, x, m, prev, f, p, f'one decoder, L={L}')
+    f = _prefill_step(dec, x, m, None)
+    _check_one(dec, x, m, f, f'one decoder, L={L}')
 
 
 @torch.no_grad()
@@ -78,7 +73,7 @@ def test_prefill_step_cache_equals_layer_forward():
     ms = [torch.randn(1, n, 768, generator=g).to(DEV, torch.bfloat16) for n in (700, 333)]
     c_step, c_layer = GatedDeltaAttentionLayerCache(), GatedDeltaAttentionLayerCache()
     for i, (x, m) in enumerate(zip(xs, ms)):
-        assert _prefill_step(dec, x, m, c_step, None) is not None
+        assert _prefill_step(dec, x, m, c_step) is not None
         dec.attn(hidden_states=x, past_key_value=c_layer)
         assert torch.equal(c_step.state, c_layer.state), f'chunk {i}: state'
         assert all(torch.equal(a, b) for a, b in zip(c_step.conv_state, c_layer.conv_state)), f'chunk {i}: tails'
@@ -92,10 +87,10 @@ def test_prefill_step_inside_a_model_prefill():
     calls = []
     real = decmod._prefill_step
 
-    def record(decoder, x, m, layer_cache, prev):
-        out = real(decoder, x, m, layer_cache, prev)
+    def record(decoder, x, m, layer_cache):
+        out = real(decoder, x, m, layer_cache)
         if out is not None:
-            calls.append((decoder, x.clone(), m.clone(), None if prev is None else prev.clone(), *out))
+            calls.append((decoder, x.clone(), m.clone(), out))
         return out
     decmod._prefill_step = record
     try:
@@ -103,5 +98,5 @@ def test_prefill_step_inside_a_model_prefill():
     finally:
         decmod._prefill_step = real
     assert len(calls) == 12, 'every GatedDelta decoder prefills through the step'
-    for i, (decoder, x, m, prev, f, p) in enumerate(calls):
-        _check_one(decoder, x, m, prev, f, p, f'model prefill, GatedDelta decoder {i}')
+    for i, (decoder, x, m, f) in enumerate(calls):
+        _check_one(decoder, x, m, f, f'model prefill, GatedDelta decoder {i}')
