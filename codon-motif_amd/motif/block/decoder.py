@@ -92,14 +92,23 @@ def _prefill_step(decoder, x, m, layer_cache):
             or attn.o_proj.out_features != mlp.down_proj.out_features):
         return None
     w = sum_weights(decoder, '_out_sum', (attn.o_proj, mlp.down_proj))
-    if w is None:
+    m2 = _rows(m)
+    if w is None or m2 is None:
         return None
     B, L, _ = x.shape
     hv, inner = attn.o_proj.in_features, mlp.down_proj.in_features
+    # everything the side branch writes is allocated before the fork (see _Fork)
     buf = torch.empty(B, L, hv + inner, dtype=x.dtype, device=x.device)
-    if not usable(buf[..., hv:]) or not attn.prefill_core(x, layer_cache, buf[..., :hv]):
+    h1 = torch.empty(B * L, 2 * inner, dtype=x.dtype, device=x.device)
+    if not usable(buf[..., hv:]):
         return None
-    swiglu(torch.nn.functional.linear(m, mlp.gate_up_proj.weight), out=buf[..., hv:])
+    fork = _Fork(x.device)
+    if not attn.prefill_core(x, layer_cache, buf[..., :hv]):
+        return None
+    with fork.side():
+        torch.mm(m2, mlp.gate_up_proj.weight.t(), out=h1)
+        swiglu(h1.view(B, L, 2 * inner), out=buf[..., hv:])
+    fork.join()
     return torch.nn.functional.linear(buf, w)
 
 
@@ -121,13 +130,70 @@ def _chord_prefill_step(decoder, x, m, layer_cache, mask, position, attn_res):
         chain = [] if p is None else [p]
     if chain and tuple(chain[0].shape) != (*x.shape[:-1], attn.o_proj.out_features):
         return None
+    m2 = _rows(m)
+    if m2 is None or mlp.gate_up_proj.bias is not None or mlp.down_proj.bias is not None:
+        return None
+    B, L, _ = x.shape
+    inner = mlp.down_proj.in_features
+    # everything the side branch writes is allocated before the fork (see _Fork)
+    h1 = torch.empty(B * L, 2 * inner, dtype=x.dtype, device=x.device)
+    s = torch.empty(B, L, inner, dtype=x.dtype, device=x.device)
+    d = torch.empty(B, L, mlp.down_proj.out_features, dtype=x.dtype, device=x.device)
+    fork = _Fork(x.device)
     parts = attn.prefill_parts(x, past_key_value=layer_cache, embedding_start=position)
     if parts is None:
         return None
     merged, g_pre, layer_cache = parts
+    with fork.side():
+        torch.mm(m2, mlp.gate_up_proj.weight.t(), out=h1)
+        swiglu(h1.view(B, L, 2 * inner), out=s)
+        torch.mm(s.view(B * L, inner), mlp.down_proj.weight.t(), out=d.view(B * L, -1))
     o = torch.nn.functional.linear(merged, attn.o_proj.weight)
-    f_h, partial = residual_fold(o, mlp(m), gate=g_pre, chain=chain)
+    fork.join()
+    f_h, partial = residual_fold(o, d, gate=g_pre, chain=chain)
     return f_h, partial, layer_cache
+
+
+_SIDE_STREAMS = {}
+
+
+class _Fork:
+    '''The MLP branch of a prefill on a second stream of the device while the attention
+    layer runs on the current one (the branches only meet at the output side).
+
+    The fork point is recorded when the _Fork is made, before the layer's kernels are
+    enqueued; the MLP's launches are enqueued after them (so the layer's whole-CU
+    workgroups are dispatched first and the MLP fills the CUs they leave, e.g. during
+    the GatedDelta state scan), and join() makes the current stream wait for them.
+    The side branch allocates nothing and touches only tensors that existed before the
+    fork (the MLP input, the weights, and outputs allocated before it): a block that
+    the current stream frees after the fork could still be in use by its own pending
+    kernels, so it must never reach the side branch.  Both streams keep the default
+    priority.'''
+
+    def __init__(self, device):
+        self.main = torch.cuda.current_stream(device)
+        stream = _SIDE_STREAMS.get(device)
+        if stream is None:
+            stream = _SIDE_STREAMS[device] = torch.cuda.Stream(device=device)
+        self.stream = stream
+        stream.wait_stream(self.main)
+
+    def side(self):
+        return torch.cuda.stream(self.stream)
+
+    def join(self):
+        self.main.wait_stream(self.stream)
+
+
+def _rows(t):
+    '''[M, K] view of t's rows, or None when there is none.'''
+    if t.stride(-1) != 1:
+        return None
+    try:
+        return t.view(-1, t.shape[-1])
+    except RuntimeError:
+        return None
 
 
 def _prev(attn_res, like):
@@ -177,13 +243,11 @@ class DecoderBlock(nn.Module):
                                  f'{len(self.features)} layers')
         use_attn_cache = cu_seqlens is None and len(cache.attn) == len(self.features)
 
-        # The attention and MLP branches of a layer run in sequence on the current stream.
-        # (The MLP on a second stream overlapped little, now and then let a prefill read
-        # memory that the other stream had taken over, and kept whole-CU attention
-        # workgroups waiting for CUs.)
-        # At prefill the GatedDelta decoders put the block's running-sum add off; the
-        # next Chord decoder (or the first read of partial_block) folds every put-off add
-        # into one pass.
+        # At prefill (the steps below) each decoder's MLP branch runs on a second stream
+        # while its attention layer runs on this one (_Fork); other calls run the
+        # branches in sequence.  The GatedDelta decoders put the block's running-sum add
+        # off; the next Chord decoder (or the first read of partial_block) folds every
+        # put-off add into one pass.
         for i, decoder in enumerate(self.features):
             x, m = self._read(attn_res, i, decoder)
             if cu_seqlens is None:
