@@ -1,6 +1,7 @@
 '''Decoder / DecoderBlock with the reference interface (motif/block/decoder.py:44-222):
 pre-norm attention in parallel with a pre-norm SwiGLU MLP, and the intra-block
 attention-residual read in front of every decoder.'''
+import contextlib
 from dataclasses import dataclass
 from typing import List, Literal, Optional, Union
 
@@ -169,9 +170,16 @@ class _Fork:
     fork (the MLP input, the weights, and outputs allocated before it): a block that
     the current stream frees after the fork could still be in use by its own pending
     kernels, so it must never reach the side branch.  Both streams keep the default
-    priority.'''
+    priority.
+
+    Only while a graph is being captured: launched one by one from the host, the
+    forked prefill measured 6.3 ms against 4.3 in sequence (config 3, B = 1, T = 4096);
+    replayed from a graph, 3.0 ms against 3.2.  Both forms give the same bits.'''
 
     def __init__(self, device):
+        self.on = torch.cuda.is_current_stream_capturing()
+        if not self.on:
+            return
         self.main = torch.cuda.current_stream(device)
         stream = _SIDE_STREAMS.get(device)
         if stream is None:
@@ -180,10 +188,11 @@ class _Fork:
         stream.wait_stream(self.main)
 
     def side(self):
-        return torch.cuda.stream(self.stream)
+        return torch.cuda.stream(self.stream) if self.on else contextlib.nullcontext()
 
     def join(self):
-        self.main.wait_stream(self.stream)
+        if self.on:
+            self.main.wait_stream(self.stream)
 
 
 def _rows(t):
@@ -244,8 +253,8 @@ class DecoderBlock(nn.Module):
         use_attn_cache = cu_seqlens is None and len(cache.attn) == len(self.features)
 
         # At prefill (the steps below) each decoder's MLP branch runs on a second stream
-        # while its attention layer runs on this one (_Fork); other calls run the
-        # branches in sequence.  The GatedDelta decoders put the block's running-sum add
+        # while its attention layer runs on this one when a graph is being captured
+        # (_Fork); other calls run the branches in sequence.  The GatedDelta decoders put the block's running-sum add
         # off; the next Chord decoder (or the first read of partial_block) folds every
         # put-off add into one pass.
         for i, decoder in enumerate(self.features):
