@@ -105,6 +105,7 @@ def _prefill_step(decoder, x, m, layer_cache):
         return None
     fork = _Fork(x.device)
     if not attn.prefill_core(x, layer_cache, buf[..., :hv]):
+        fork.join()  # (a capture may not end with the side stream forked)
         return None
     with fork.side():
         torch.mm(m2, mlp.gate_up_proj.weight.t(), out=h1)
@@ -143,6 +144,7 @@ def _chord_prefill_step(decoder, x, m, layer_cache, mask, position, attn_res):
     fork = _Fork(x.device)
     parts = attn.prefill_parts(x, past_key_value=layer_cache, embedding_start=position)
     if parts is None:
+        fork.join()
         return None
     merged, g_pre, layer_cache = parts
     with fork.side():

@@ -52,3 +52,30 @@ def test_captured_prefill_with_fork_equals_eager(B, T):
         assert torch.equal(out.logits, eager), f'replay {i}'
         assert torch.equal(model(ids).logits, eager), f'eager after replay {i}'
         torch.cuda.synchronize()
+
+
+@torch.no_grad()
+def test_fork_is_joined_when_a_step_bails_out():
+    '''A prefill step that forks and then finds its layer route unserved joins the side
+    stream before returning None: the capture around it ends cleanly.'''
+    import motif.block.decoder as decmod
+    from motif.model.cache import AttnResCache
+    from motif.model.motif import MotifChordModel
+    from motif.model.presets import config_172m, init_random
+    model = init_random(MotifChordModel(config_172m()), seed=3).to(DEV, torch.bfloat16).eval()
+    gdn, chord = model.blocks[0].features[0], model.blocks[0].features[3]
+    g = gen(13)
+    x = torch.randn(1, 256, 768, generator=g).to(DEV, torch.bfloat16)
+    m = torch.randn(1, 256, 768, generator=g).to(DEV, torch.bfloat16)
+    gdn.attn.prefill_core = lambda *a, **k: False
+    chord.attn.prefill_parts = lambda *a, **k: None
+    try:
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            assert decmod._prefill_step(gdn, x, m, None) is None
+            assert decmod._chord_prefill_step(chord, x, m, None, None, 0, AttnResCache()) is None
+        graph.replay()
+        torch.cuda.synchronize()
+    finally:
+        del gdn.attn.prefill_core, chord.attn.prefill_parts
