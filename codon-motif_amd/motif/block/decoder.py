@@ -123,7 +123,8 @@ def _chord_prefill_step(decoder, x, m, layer_cache, mask, position, attn_res):
     chord_attn.py:254, motif/block/decoder.py:205-213).  Returns (f_h, partial, layer
     cache), or None (before anything ran) when the call takes another route.'''
     attn, mlp = decoder.attn, decoder.mlp
-    if (not isinstance(attn, ChordAttention) or x.dim() != 3 or x.dtype != torch.bfloat16 or mask is not None
+    if (not isinstance(attn, ChordAttention) or x.dim() != 3 or x.dtype != torch.bfloat16 or not x.is_cuda
+            or mask is not None
             or attn.o_proj.bias is not None or mlp._fused(m) or wants_grad(x, m, attn, mlp)):
         return None
     chain = attn_res.pending_sum()
@@ -179,7 +180,7 @@ class _Fork:
     replayed from a graph, 3.0 ms against 3.2.  Both forms give the same bits.'''
 
     def __init__(self, device):
-        self.on = torch.cuda.is_current_stream_capturing()
+        self.on = torch.device(device).type == 'cuda' and torch.cuda.is_current_stream_capturing()
         if not self.on:
             return
         self.main = torch.cuda.current_stream(device)

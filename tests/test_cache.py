@@ -180,3 +180,18 @@ def test_build_cache_structure_and_flags():
     assert all(b.attn == [] for b in t)
     c.reset()
     assert all(b.is_empty() for b in c) and c.seq_len == 0
+
+
+def test_chord_only_model_prefills_on_the_cpu():
+    '''A decoder block of Chord layers runs on CPU tensors (the materialised attention
+    path): the ROCm-only prefill steps and the second-stream fork stand aside.'''
+    from motif.model.config import MotifChordConfig
+    from motif.model.motif import MotifChordModel
+    import motif.block.decoder as decmod
+    cfg = MotifChordConfig(vocab_size=50, model_dim=64, num_heads=2, num_kv_heads=1, head_k_dim=32,
+                           block=('chord', 'chord'), block_n=1)
+    model = MotifChordModel(cfg).eval().to(torch.bfloat16)
+    with torch.no_grad():
+        out = model(torch.randint(0, 50, (1, 9), generator=torch.Generator().manual_seed(0)))
+    assert out.logits.shape == (1, 9, 50) and bool(torch.isfinite(out.logits.float()).all())
+    assert decmod._Fork(torch.device('cpu')).on is False
