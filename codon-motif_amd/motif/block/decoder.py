@@ -121,7 +121,8 @@ def _chord_prefill_step(decoder, x, m, layer_cache, mask, position, attn_res):
     block's running sum with every add put off since it was last stored -- the
     reference's ops in its order, one rounding each (motif/block/attention/
     chord_attn.py:254, motif/block/decoder.py:205-213).  Returns (f_h, partial, layer
-    cache), or None (before anything ran) when the call takes another route.'''
+    cache), or None when the call takes another route (having run at most the sum of the
+    put-off adds, which partial_block then holds).'''
     attn, mlp = decoder.attn, decoder.mlp
     if (not isinstance(attn, ChordAttention) or x.dim() != 3 or x.dtype != torch.bfloat16 or not x.is_cuda
             or mask is not None
