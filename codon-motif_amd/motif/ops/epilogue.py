@@ -51,6 +51,8 @@ def gated_rms_norm_heads(o, gate, weight, eps):
         return (y.transpose(1, 2) * F.silu(gate.reshape(B, L, H, dv))).reshape(B, L, H * dv)
     w = weight.detach().to(dt).contiguous()
     y = torch.empty(B, L, H * dv, dtype=dt, device=o.device)
+    if y.numel() == 0:
+        return y
     rc = _lib.lib().motif_gated_rms_norm(
         o.data_ptr(), o.stride(0), o.stride(1), o.stride(2), gate.data_ptr(), gate.stride(0), gate.stride(1),
         w.data_ptr(), float(eps), y.data_ptr(), y.stride(0), y.stride(1), B, L, H, dv,
@@ -78,6 +80,8 @@ def swiglu(x, out=None):
                 or out.stride(-1) != 1 or out.stride(0) != out.shape[1] * out.stride(1) or not usable(out)):
             raise ValueError(f'swiglu: out must be a {x.dtype} [..., {I}] view of rows with one stride')
         y, y_rs = out, out.stride(1)
+    if M == 0:
+        return y
     rc = _lib.lib().motif_swiglu(x2.data_ptr(), x2.stride(0), y.data_ptr(), y_rs, M, I, _lib.dtype_code(x.dtype),
                                  _lib.stream_ptr(x.device))
     _lib.check(rc, 'motif_swiglu')
@@ -99,6 +103,8 @@ def add_fold(a, b, p=None):
         p2 = p.reshape(-1, N)
         po = torch.empty_like(f)
         po2 = po.view(-1, N)
+    if f.numel() == 0:
+        return f, po
     rc = _lib.lib().motif_add_fold(a2.data_ptr(), a2.stride(0), b2.data_ptr(), b2.stride(0), _lib.ptr(p2),
                                    0 if p2 is None else p2.stride(0), f2.data_ptr(), N, _lib.ptr(po2),
                                    0 if po2 is None else N, a2.shape[0], N, _lib.dtype_code(a.dtype),
@@ -163,6 +169,8 @@ def residual_fold(a, b, gate=None, chain=()):
     c2 = list(it)
     f = torch.empty(shape, dtype=dt, device=dev) if a is not None else None
     p = torch.empty(shape, dtype=dt, device=dev) if chain else None
+    if M == 0:
+        return f, p
     n = len(c2)
     ptrs = (ctypes.c_void_p * max(n, 1))(*[t.data_ptr() for t in c2])
     rs = (ctypes.c_int64 * max(n, 1))(*[t.stride(0) for t in c2])
@@ -187,6 +195,8 @@ def gdn_gates(a, b, a_log, dt_bias):
     db = dt_bias.detach().to(dt).contiguous()
     beta = torch.empty(B, H, L, dtype=dt, device=a.device)
     g = torch.empty(B, H, L, dtype=dt, device=a.device)
+    if beta.numel() == 0:
+        return beta, g
     rc = _lib.lib().motif_gdn_gates(a.data_ptr(), a.stride(0), a.stride(1), b.data_ptr(), b.stride(0), b.stride(1),
                                     al.data_ptr(), db.data_ptr(), beta.data_ptr(), g.data_ptr(),
                                     beta.stride(0), beta.stride(1), beta.stride(2), B, L, H,
@@ -202,6 +212,8 @@ def mul_sigmoid(x, g):
     N = x.shape[-1]
     x2, g2 = x.reshape(-1, N), g.reshape(-1, N)
     y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    if y.numel() == 0:
+        return y
     rc = _lib.lib().motif_mul_sigmoid(x2.data_ptr(), x2.stride(0), g2.data_ptr(), g2.stride(0), y.data_ptr(), N,
                                       x2.shape[0], N, _lib.dtype_code(x.dtype), _lib.stream_ptr(x.device))
     _lib.check(rc, 'motif_mul_sigmoid')

@@ -132,3 +132,28 @@ def test_block_ending_in_gated_delta_sums_put_off_adds():
     for i, (a, b) in enumerate(zip(lz_blocks, eg_blocks)):
         assert torch.equal(a, b), f'block {i}'
     assert torch.equal(lz, eg)
+
+
+@torch.no_grad()
+def test_fold_edge_shapes():
+    '''Empty rows, rows the kernel does not serve (a width that is not a multiple of 16
+    bytes: the torch ops run), and nine addends (past the kernel's eight: torch ops) all
+    give the separate ops' values.'''
+    from motif.ops.epilogue import residual_fold
+    g = gen(50)
+    for M, N, n in ((0, 768, 3), (37, 100, 2), (64, 768, 9)):
+        a, b, gt = ((torch.randn(M, N, generator=g) * 2).to(DEV, torch.bfloat16) for _ in range(3))
+        chain = [torch.randn(M, N, generator=g).to(DEV, torch.bfloat16) for _ in range(n)]
+        f, p = residual_fold(a, b, gate=gt, chain=chain)
+        f_ref, p_ref = _ref(a, gt, b, chain)
+        assert torch.equal(f, f_ref) and torch.equal(p, p_ref), (M, N, n)
+
+
+@torch.no_grad()
+def test_elementwise_stages_take_empty_rows():
+    from motif.ops.epilogue import add_fold, mul_sigmoid, swiglu
+    e = torch.empty(1, 0, 768, dtype=torch.bfloat16, device=DEV)
+    assert swiglu(torch.empty(1, 0, 1536, dtype=torch.bfloat16, device=DEV)).shape == (1, 0, 768)
+    assert mul_sigmoid(e, e).shape == e.shape
+    f, p = add_fold(e, e, e)
+    assert f.shape == p.shape == e.shape
