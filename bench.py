@@ -703,7 +703,8 @@ def main():
         'config': {'workload': 'config 3: MotifChordModel forward, d=768, 4x(3 GDN + 1 Chord), H=12, '
                                'GDN dk=64 dv=128, Chord D=64 Hkv=3, vocab 32000, B=1, T=4096, bf16',
                    'global_batch': 1, 'seq_len': T, 'parallelism': 'single GPU',
-                   'execution': 'forward captured once as a hipGraph, replayed per step'},
+                   'execution': 'forward captured once as a hipGraph, replayed per step (inside the graph '
+                                'each decoder\'s MLP branch runs on a second stream beside its attention layer)'},
         'prefill_eager': {'tok_s': round(T / (ms_eager * 1e-3), 1), 'ms_per_step': round(ms_eager, 4),
                           'note': 'the same forward launched from Python each step'},
         'prefill_graph_matches_eager': graph_ok,
